@@ -1,0 +1,406 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Parrot inference MoE path (one GPU).
+
+Workload (the headline metric): the full default
+Parrot model -- 16 layers, E=16 experts, top-2 + shared expert, Block
+AttnRes, 32768-vocab tied head -- random-init with seed 2, bf16, router
+statistics off, forward over batch 1 x 512 token ids drawn uniformly from
+[0, 32768) (synthetic data).  MoE, RMSNorm and depth mixing run on the HIP
+kernels (moe_backend="grouped_hip", depth_backend="hip"); attention, the
+embedding and the vocabulary head are PyTorch-ROCm.
+
+A step is one full forward.  The timed loop replays the forward captured in
+a HIP graph (each replay recomputes everything from the static input ids);
+the eager rate is reported beside it.  Per-kernel durations of the hot path
+are measured with HIP events on the stream the kernels are launched on, at
+the in-model shapes, and the dominant kernel's roofline fraction is
+reported.  The CPU baseline is the fp32 CPU oracle of the reference's
+``moe_backend="pytorch"`` forward on a bounded sample.
+
+Prints one JSON line on stdout.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "parrot-h200-worker_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_HBM_GBPS = 8000.0        # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+REFERENCE_TOK_S = 5250.0      # reference grouped_mps, same workload, Apple M4 Pro (README.md:43)
+TOKENS = 512
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--kernel-iters", type=int, default=200)
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="approximate CPU time spent on the cpu_baseline sample")
+    p.add_argument("--skip-cpu-baseline", action="store_true")
+    p.add_argument("--skip-kernels", action="store_true")
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# per-kernel timing through the C ABI (no allocation inside the timed loop)
+# ---------------------------------------------------------------------------
+
+class StageBench:
+    """Preallocated buffers for timing each C-ABI stage of one MoE layer."""
+
+    def __init__(self, moe, x, logit_bias=None):
+        import torch
+        from parrot import _abi, hip_moe
+        from parrot._abi import ptr
+        self.torch, self.lib, self.ptr = torch, _abi.load(), ptr
+        cfg = moe.cfg
+        self.moe, self.x = moe, x.contiguous()
+        self.T, self.dim = x.shape
+        self.E, self.H, self.Hs = cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim
+        self.C = hip_moe.capacity(self.T, self.E)
+        self.bias = None if logit_bias is None else logit_bias.to(x.device, torch.float32)
+        dev = x.device
+        with torch.no_grad():
+            self.routed = hip_moe.route(moe, self.x, False, logit_bias=self.bias)
+            self.packed = hip_moe.pack_expert_weights(moe)
+        g = self.routed.grouping
+        self.g = g
+        self.rws_bytes = self.lib.parrot_route_workspace_bytes(self.T, self.E)
+        self.rws = torch.empty(max(self.rws_bytes, 256), dtype=torch.uint8, device=dev)
+        self.ews_bytes = self.lib.parrot_experts_workspace_bytes(self.T, self.dim, self.H, self.Hs)
+        self.ews = torch.empty(self.ews_bytes, dtype=torch.uint8, device=dev)
+        self.out = torch.empty_like(self.x)
+        self.stream = torch.cuda.current_stream(dev)
+        self.s = self.stream.cuda_stream
+        counts = g.counts.cpu()
+        self.hit = int((counts > 0).sum())
+        self.overflow = int(g.offsets[-1].item())
+
+    def route(self):
+        p, r, g = self.ptr, self.routed, self.g
+        return self.lib.parrot_route_bf16(
+            p(self.x), p(self.moe.router.weight), p(self.bias), self.T, self.dim, self.E, self.C,
+            None, None, p(r.weights), p(r.indices), p(g.positions), p(g.counts), p(g.offsets),
+            p(g.perm), p(g.overflow), p(self.rws), self.rws_bytes, self.s)
+
+    def gate_up(self):
+        p, g = self.ptr, self.g
+        return self.lib.parrot_experts_gate_up_bf16(
+            p(self.x), self.T, self.dim, self.E, self.H, self.Hs, self.C, p(g.counts),
+            p(g.offsets), p(g.perm), p(g.overflow), p(self.packed[0]), p(self.packed[2]),
+            p(self.ews), self.ews_bytes, self.s)
+
+    def down(self):
+        p, g = self.ptr, self.g
+        return self.lib.parrot_experts_down_bf16(
+            self.T, self.dim, self.E, self.H, self.Hs, self.C, p(g.counts), p(g.offsets),
+            p(g.perm), p(g.overflow), p(self.routed.weights), p(self.packed[1]),
+            p(self.packed[3]), p(self.ews), self.ews_bytes, self.s)
+
+    def combine(self):
+        p = self.ptr
+        return self.lib.parrot_experts_combine_bf16(self.T, self.dim, self.H, self.Hs, None,
+                                                    p(self.out), p(self.ews), self.ews_bytes,
+                                                    self.s)
+
+    # algorithmic bytes / flops per launch
+    def bytes_route(self):
+        T, d, E = self.T, self.dim, self.E
+        return T * d * 2 + E * d * 2 + 2 * T * (8 + 4 + 4) + E * 4 + E * self.C * 4 + self.overflow * 4
+
+    def bytes_gate_up(self):
+        T, d, H, Hs = self.T, self.dim, self.H, self.Hs
+        return (self.hit * 2 * H * d + 2 * Hs * d + T * d + 2 * T * H + T * Hs) * 2
+
+    def bytes_down(self):
+        T, d, H, Hs = self.T, self.dim, self.H, self.Hs
+        return (self.hit * d * H + d * Hs + 2 * T * H + T * Hs) * 2 + 3 * T * d * 4 + 2 * T * 4
+
+    def bytes_combine(self):
+        return 3 * self.T * self.dim * 4 + self.T * self.dim * 2
+
+    def flops_gate_up(self):
+        return 2 * (2 * self.T) * 2 * self.H * self.dim + 2 * self.T * 2 * self.Hs * self.dim
+
+    def flops_down(self):
+        return 2 * (2 * self.T) * self.H * self.dim + 2 * self.T * self.Hs * self.dim
+
+
+def event_time_us(fn, iters: int, stream) -> float:
+    """Average duration of `fn`'s launches, HIP events on `stream`."""
+    import torch
+    for _ in range(5):
+        rc = fn()
+        if rc:
+            raise RuntimeError(f"stage returned status {rc}")
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) * 1000.0 / iters
+
+
+def entry(us: float, nbytes: int, flops: int | None = None) -> dict:
+    gbps = nbytes / (us * 1e-6) / 1e9
+    out = {"us": round(us, 3), "bytes": int(nbytes), "gbps": round(gbps, 1),
+           "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4)}
+    if flops is not None:
+        tf = flops / (us * 1e-6) / 1e12
+        out.update(flops=int(flops), tflops=round(tf, 2), mfma_frac=round(tf / PEAK_BF16_TFLOPS, 4))
+    return out
+
+
+def layer_kernels(moe, x, iters, logit_bias=None) -> tuple[dict, "StageBench"]:
+    sb = StageBench(moe, x, logit_bias)
+    res = {
+        "route_group": entry(event_time_us(sb.route, iters, sb.stream), sb.bytes_route()),
+        "gate_up": entry(event_time_us(sb.gate_up, iters, sb.stream), sb.bytes_gate_up(),
+                         sb.flops_gate_up()),
+        "down": entry(event_time_us(sb.down, iters, sb.stream), sb.bytes_down(), sb.flops_down()),
+        "combine": entry(event_time_us(sb.combine, iters, sb.stream), sb.bytes_combine()),
+        "experts_hit": sb.hit,
+        "overflow_assignments": sb.overflow,
+        "capacity": sb.C,
+    }
+    return res, sb
+
+
+def norm_kernels(model, iters) -> dict:
+    import ctypes
+
+    import torch
+    from parrot import _abi
+    from parrot._abi import ptr
+    lib = _abi.load()
+    dev = torch.device("cuda:0")
+    d = model.config.dim
+    x = torch.randn(TOKENS, d, device=dev).bfloat16()
+    out = torch.empty_like(x)
+    norm = model.blocks[0].attention_norm
+    s = torch.cuda.current_stream(dev)
+    rms_us = event_time_us(lambda: lib.parrot_rms_norm_bf16(ptr(x), ptr(norm.weight), ptr(out),
+                                                            TOKENS, d, 1e-6, s.cuda_stream),
+                           iters, s)
+    srcs = [torch.randn(TOKENS, d, device=dev).bfloat16() for _ in range(9)]
+    arr = (ctypes.c_void_p * 9)(*[t.data_ptr() for t in srcs])
+    mix = model.depth_mix[-1]
+    depth_us = event_time_us(
+        lambda: lib.parrot_depth_mix_bf16(ctypes.cast(arr, ctypes.c_void_p), 9, ptr(mix.query),
+                                          ptr(mix.norm.weight), 1e-6, ptr(norm.weight), 1e-6,
+                                          TOKENS, d, None, ptr(out), s.cuda_stream), iters, s)
+    return {
+        "rms_norm": entry(rms_us, 2 * TOKENS * d * 2 + d * 2),
+        "depth_mix_norm_s9": entry(depth_us, 9 * TOKENS * d * 2 + 3 * d * 2 + TOKENS * d * 2),
+    }
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the fp32 CPU oracle of the reference pytorch forward
+# ---------------------------------------------------------------------------
+
+def cpu_baseline(model, ids, seconds: float) -> dict:
+    import torch
+
+    from oracle import parrot_fp32
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(threads)
+    oracle = parrot_fp32.ParrotFP32(model.config, model.state_dict())
+    cpu_ids = ids.cpu()
+    with torch.no_grad():
+        oracle.forward(cpu_ids)  # warmup
+        samples = []
+        t_start = time.perf_counter()
+        while len(samples) < 3 or (time.perf_counter() - t_start < seconds and len(samples) < 20):
+            t0 = time.perf_counter()
+            oracle.forward(cpu_ids)
+            samples.append(time.perf_counter() - t0)
+    med = statistics.median(samples)
+    cpu_model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(TOKENS / med, 2), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{len(samples)} fp32 CPU forwards of the same 1x512 workload "
+                      f"(oracle/parrot_fp32.py, the reference pytorch path), median "
+                      f"{med * 1e3:.1f} ms; cpu_count={os.cpu_count()}; {cpu_model}"}
+
+
+# ---------------------------------------------------------------------------
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the MoE hot path has no multi-GPU implementation and "
+              "every GPU box here has a single MI355X.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from parrot import ModelConfig, Parrot, _abi
+    _abi.load()  # fail loudly without the HIP library
+    dev = torch.device("cuda:0")
+
+    log("building model (seed 2)")
+    torch.manual_seed(2)
+    model = Parrot(ModelConfig(moe_backend="grouped_hip", depth_backend="hip",
+                               collect_router_stats=False)).to(device=dev, dtype=torch.bfloat16)
+    model.eval()
+    ids = torch.randint(0, 32768, (1, TOKENS), generator=torch.Generator().manual_seed(2)).to(dev)
+
+    # capture the first layer's MoE input for the per-kernel measurements
+    captured = {}
+    moe0 = model.blocks[0].moe
+    original = moe0.inference
+
+    def spy(x, **kw):
+        captured["x"] = x.detach().reshape(-1, x.shape[-1]).clone()
+        return original(x, **kw)
+
+    moe0.inference = spy
+    with torch.no_grad():
+        model(ids)
+    del moe0.inference
+
+    log("eager forward")
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            model(ids)
+        torch.cuda.synchronize()
+        eager = []
+        for _ in range(max(3, args.steps // 4)):
+            t0 = time.perf_counter()
+            model(ids)
+            torch.cuda.synchronize()
+            eager.append(time.perf_counter() - t0)
+    eager_ms = statistics.median(eager) * 1e3
+
+    log("graph capture")
+    static_ids = ids.clone()
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                model(static_ids)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_logits = model(static_ids).logits
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        reference_logits = model(ids).logits
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(static_logits, reference_logits):
+            raise RuntimeError("graph replay differs from the eager forward")
+
+        log(f"timed: {args.steps} graph replays")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = TOKENS * args.steps / elapsed
+
+    kernels = {}
+    roofline = None
+    if not args.skip_kernels:
+        log("per-kernel timing")
+        c4, _ = layer_kernels(moe0, captured["x"], args.kernel_iters)
+        kernels["C4_in_model_T512_E16"] = c4
+        kernels.update(norm_kernels(model, args.kernel_iters))
+        for name, tokens, skew in (("C2_T256_E32", 256, False), ("C3_T4096_E32_skew", 4096, True)):
+            moe, x, bias = _layer_case(tokens, skew)
+            kernels[name], _ = layer_kernels(moe, x, max(20, args.kernel_iters // 4), bias)
+            del moe
+        gu = c4["gate_up"]
+        roofline = {"kernel": "grouped_gemm_kernel<64,128,1> (experts gate_up + SwiGLU), "
+                              "C4 in-model shape T=512 E=16",
+                    "bound": "hbm", "achieved": gu["gbps"], "peak": PEAK_HBM_GBPS,
+                    "unit": "GB/s", "frac": gu["hbm_frac"], "traffic": None}
+
+    result = {
+        "metric": "tokens/sec Parrot bf16 fwd bs1x512 on 1 MI355X",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / REFERENCE_TOK_S, 2),
+        "baseline": "5,250 tokens/s: reference grouped_mps+metal on Apple M4 Pro, same workload "
+                    "(README.md:42-44); no MI355X number is published",
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "Parrot default (16 layers, E=16 top-2 + shared, AttnRes, "
+                               "vocab 32768) bf16 forward, batch 1 x 512, router stats off, "
+                               "seed 2, HIP-graph replay",
+                   "tokens": TOKENS, "moe_backend": "grouped_hip", "depth_backend": "hip"},
+        "eager_ms_per_step": round(eager_ms, 3),
+        "eager_tokens_per_s": round(TOKENS / (eager_ms / 1e3), 1),
+        "roofline": roofline,
+        "kernels": kernels,
+        "cpu_baseline": None,
+    }
+    if not args.skip_cpu_baseline:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(model, ids, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+def _layer_case(tokens: int, skewed: bool):
+    """MoE layer of BASELINE configs 2/3: E=32, weights N(0, 0.02), x N(0, 1)."""
+    import torch
+
+    from parrot.model import ModelConfig, MoE
+    cfg = ModelConfig(n_experts=32, moe_backend="grouped_hip", depth_backend="hip",
+                      collect_router_stats=False)
+    gen = torch.Generator().manual_seed(1)
+    moe = MoE(cfg)
+    with torch.no_grad():
+        for p in moe.parameters():
+            p.copy_(torch.randn(p.shape, generator=gen) * 0.02)
+    moe = moe.to(device="cuda", dtype=torch.bfloat16).eval()
+    x = torch.randn(tokens, cfg.dim, generator=torch.Generator().manual_seed(1)).to(
+        device="cuda", dtype=torch.bfloat16)
+    bias = None
+    if skewed:
+        bias = torch.zeros(32)
+        bias[0], bias[1] = 4.0, 2.0
+    return moe, x, bias
+
+
+if __name__ == "__main__":
+    main()

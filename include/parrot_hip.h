@@ -1,0 +1,185 @@
+/*
+ * parrot_hip.h -- C ABI of the MI355X (gfx950) Parrot inference MoE path.
+ *
+ * Shared library: parrot-h200-worker_amd/parrot/_lib/libparrot_hip.so
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless stated; tensors are dense and
+ *     row-major.  bf16 tensors are 16-byte aligned.
+ *   - `stream` is a hipStream_t (PyTorch-ROCm: torch.cuda.current_stream().cuda_stream).
+ *     Every entry point only enqueues work on that stream: no host
+ *     synchronisation, no allocation, no global mutable state.
+ *   - The return value is a status: 0 on success, a negative PARROT_ERR_*
+ *     code when an argument is rejected before anything is launched, or a
+ *     positive hipError_t from the launch.
+ *   - The caller owns every buffer, including the workspaces whose sizes the
+ *     *_workspace_bytes functions report.
+ *
+ * Each entry point names the reference interface it replaces
+ * (paths relative to the jkpdino/parrot-h200-worker checkout).
+ */
+#ifndef PARROT_HIP_H
+#define PARROT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PARROT_ABI_VERSION 1
+
+#define PARROT_OK 0
+#define PARROT_ERR_NULL_POINTER (-1)
+#define PARROT_ERR_BAD_SHAPE (-2)
+#define PARROT_ERR_UNSUPPORTED (-3)
+#define PARROT_ERR_WORKSPACE (-4)
+#define PARROT_ERR_ALIGNMENT (-5)
+
+/* ABI version (PARROT_ABI_VERSION) of the loaded library. */
+int parrot_abi_version(void);
+
+/* Text for a status returned by any entry point (static storage). */
+const char* parrot_status_string(int status);
+
+/* Fixed expert capacity C = max(8, roundup8(ceil(2 * 2T / E))), top-2.
+ * Replaces the capacity expression of grouped_mps_experts,
+ * parrot/metal_moe.py:388-391. */
+int32_t parrot_capacity(int64_t tokens, int32_t experts);
+
+/* y = bf16(x * rsqrt(mean(x^2) + eps) * weight) per row; x, weight, out bf16.
+ * dim % 4 == 0, dim <= 4096.
+ * Replaces metal_rms_norm (parrot/metal_moe.py:37-55) with its kernels
+ * rms_norm_bf16 / rms_norm_decode_bf16 (parrot/kernels/moe_bf16.metal:4-65). */
+int parrot_rms_norm_bf16(const void* x, const void* weight, void* out, int64_t rows,
+                         int32_t dim, float eps, void* stream);
+
+/* Block AttnRes depth mix over 1..9 bf16 sources [tokens, dim]:
+ *   score_s = <rmsnorm(v_s; score_norm_weight, score_eps), query>,
+ *   mix = bf16(sum_s softmax(score)_s v_s).
+ * Writes mix to out_mix when non-NULL, and rmsnorm(mix; out_norm_weight,
+ * out_eps) to out_norm when non-NULL (at least one of them).
+ * dim % 4 == 0, dim <= 2048.
+ * Replaces metal_depth_mix (parrot/metal_moe.py:419-452; kernels
+ * depth_scores_bf16, depth_mix_bf16, depth_mix_decode_bf16) and
+ * metal_depth_mix_norm (parrot/metal_moe.py:455-477; kernel
+ * depth_mix_norm_decode_bf16), for every token count. */
+int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const void* query,
+                          const void* score_norm_weight, float score_eps,
+                          const void* out_norm_weight, float out_eps, int64_t tokens,
+                          int32_t dim, void* out_mix, void* out_norm, void* stream);
+
+/* Workspace bytes for the routing / grouping entry points. */
+size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts);
+
+/* Router + top-2 + deterministic grouping.
+ *   logits = x . router_weight^T (fp32) [+ logit_bias[e]], softmax top-2 with
+ *   ties to the lower expert index, route weights renormalised over the pair.
+ * Outputs (all required unless marked optional):
+ *   out_logits  fp32 [T, E]   optional, the logits after the bias
+ *   out_probs   fp32 [T, E]   optional, softmax probabilities (router stats)
+ *   out_weights fp32 [T, 2], out_indices int64 [T, 2]
+ *   out_positions int32 [2T]  stable slot of assignment a = 2t + k among the
+ *                             expert's assignments (ascending a)
+ *   out_counts  int32 [E]
+ *   out_offsets int32 [2E + 2] exclusive prefix of counts (E + 1 entries),
+ *                             then of max(0, counts - C) (E + 1 entries)
+ *   out_perm    int32 [E, C]  assignment id in slot (e, s), -1 when empty
+ *   out_overflow int32 [2T]   assignments with slot >= C, grouped by expert
+ *                             then ascending a; valid entries:
+ *                             out_offsets[2E + 1]
+ * x, router_weight bf16; 2 <= E <= 32; dim % 32 == 0.
+ * Replaces metal_route (parrot/metal_moe.py:58-81; kernel moe_route_bf16,
+ * parrot/kernels/moe_bf16.metal:67-134) and the slot/scatter bookkeeping of
+ * grouped_mps_experts (parrot/metal_moe.py:384-399). */
+int parrot_route_bf16(const void* x, const void* router_weight, const float* logit_bias,
+                      int64_t tokens, int32_t dim, int32_t experts, int32_t capacity,
+                      float* out_logits, float* out_probs, float* out_weights,
+                      int64_t* out_indices, int32_t* out_positions, int32_t* out_counts,
+                      int32_t* out_offsets, int32_t* out_perm, int32_t* out_overflow,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* As parrot_route_bf16, starting from given fp32 logits [T, E] (the
+ * "identical router logits" entry of the parity contract). */
+int parrot_route_from_logits_f32(const float* logits, const float* logit_bias, int64_t tokens,
+                                 int32_t experts, int32_t capacity, float* out_probs,
+                                 float* out_weights, int64_t* out_indices,
+                                 int32_t* out_positions, int32_t* out_counts,
+                                 int32_t* out_offsets, int32_t* out_perm,
+                                 int32_t* out_overflow, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* Grouping for caller-supplied top-2 indices int64 [T, 2], values in [0, E).
+ * Outputs as parrot_route_bf16.
+ * Replaces moe_count_assignments (parrot/kernels/moe_bf16.metal:650-660,
+ * called from parrot/metal_moe.py:384-387). */
+int parrot_group_indices(const int64_t* indices, int64_t tokens, int32_t experts,
+                         int32_t capacity, int32_t* out_positions, int32_t* out_counts,
+                         int32_t* out_offsets, int32_t* out_perm, int32_t* out_overflow,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes for parrot_grouped_experts_bf16. */
+size_t parrot_experts_workspace_bytes(int64_t tokens, int32_t dim, int32_t hidden_dim,
+                                      int32_t shared_dim);
+
+/* The three stages of parrot_grouped_experts_bf16, for callers that schedule
+ * them separately.  They share one workspace of
+ * parrot_experts_workspace_bytes() bytes that carries the intermediate
+ * results from stage to stage (hidden rows, then fp32 expert outputs), so
+ * the same workspace must be passed to all three, in order, on one stream.
+ *   gate_up: h = bf16(silu(x Wg^T) * (x Wu^T)) for every routed assignment
+ *            (in-capacity slots and overflow list alike) and every token of
+ *            the shared expert, one grouped MFMA launch;
+ *   down:    y = w[a] * (h Wd^T) per routed assignment, h Ws^T per token;
+ *   combine: out[t] = bf16(y_shared[t] + y[2t] + y[2t+1]) (+ addend).
+ * Replace the torch.bmm / swiglu_from_gate_up_bf16 / moe_overflow_hidden_bf16
+ * (gate_up), torch.bmm + overflow dot (down) and moe_gather_grouped_bf16
+ * (combine) steps of grouped_mps_experts, parrot/metal_moe.py:400-415. */
+int parrot_experts_gate_up_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,
+                                int32_t hidden_dim, int32_t shared_dim, int32_t capacity,
+                                const int32_t* counts, const int32_t* offsets,
+                                const int32_t* perm, const int32_t* overflow,
+                                const void* packed_gate_up, const void* shared_gate_up,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+int parrot_experts_down_bf16(int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
+                             int32_t shared_dim, int32_t capacity, const int32_t* counts,
+                             const int32_t* offsets, const int32_t* perm,
+                             const int32_t* overflow, const float* route_weights,
+                             const void* down, const void* shared_down, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+int parrot_experts_combine_bf16(int64_t tokens, int32_t dim, int32_t hidden_dim,
+                                int32_t shared_dim, const void* addend, void* out,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Routed + shared SwiGLU experts and the weighted combine:
+ *   out[t] = bf16(shared(x_t) + sum_k w[t,k] * expert_{i[t,k]}(x_t))
+ *   (then bf16(addend[t] + out[t]) when addend is non-NULL).
+ * counts/offsets/perm/overflow/route_weights come from the routing entry
+ * points above.  Weights (bf16):
+ *   packed_gate_up [E, 2H, dim]  rows 32g..32g+15 = gate rows 16g..16g+15,
+ *                                rows 32g+16..32g+31 = up rows 16g..16g+15
+ *   down           [E, dim, H]
+ *   shared_gate_up [2Hs, dim]    interleaved the same way
+ *   shared_down    [dim, Hs]
+ * dim, H and Hs multiples of 64; E <= 32.
+ * Replaces grouped_mps_experts (parrot/metal_moe.py:372-416): the zero-fill
+ * and scatter into [E, C, dim], moe_overflow_hidden_bf16, the two torch.bmm,
+ * swiglu_from_gate_up_bf16, the shared expert (_fused_shared, :145-148) and
+ * moe_gather_grouped_bf16 (parrot/kernels/moe_bf16.metal:662-777). */
+int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,
+                                int32_t hidden_dim, int32_t shared_dim, int32_t capacity,
+                                const int32_t* counts, const int32_t* offsets,
+                                const int32_t* perm, const int32_t* overflow,
+                                const float* route_weights, const void* packed_gate_up,
+                                const void* down, const void* shared_gate_up,
+                                const void* shared_down, const void* addend, void* out,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PARROT_HIP_H */

@@ -1,0 +1,351 @@
+"""PyTorch-ROCm host side of the MI355X inference MoE path.
+
+Drop-in counterpart of the reference's Metal bridge (parrot/metal_moe.py):
+the same operator contract -- route, grouped experts, RMSNorm, depth mix and
+depth mix + RMSNorm -- backed by the gfx950 HIP kernels in
+``parrot/kernels/*.hip`` through the C ABI of ``include/parrot_hip.h``.
+
+Every function runs on PyTorch's current HIP stream, allocates its outputs
+and workspaces with torch on the input's device, never synchronises with the
+host and never falls back to another backend: unsupported inputs raise.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import TYPE_CHECKING
+
+import torch
+from torch import Tensor
+
+from . import _abi
+from ._abi import ptr
+
+if TYPE_CHECKING:
+    from .model import MoE
+
+MAX_EXPERTS = 32
+MAX_DEPTH_SOURCES = 9
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require(x: Tensor, what: str, dtypes=(torch.bfloat16,)) -> None:
+    """Preconditions shared by every HIP operator (cf. parrot/metal_moe.py:154-157)."""
+    if x.device.type != "cuda":
+        raise RuntimeError(f"{what} requires a ROCm (cuda) tensor, got {x.device}")
+    if x.dtype not in dtypes:
+        raise RuntimeError(f"{what} requires {', '.join(map(str, dtypes))}, got {x.dtype}")
+    if torch.is_grad_enabled():
+        raise RuntimeError(f"{what} is inference-only; disable gradients")
+
+
+def _scratch(owner, name: str, nbytes: int, device: torch.device) -> Tensor:
+    """Reusable byte workspace kept outside the module's state_dict
+    (cf. parrot/metal_moe.py:15-23)."""
+    cached = owner.__dict__.get(name)
+    if cached is None or cached.numel() < nbytes or cached.device != device:
+        cached = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        owner.__dict__[name] = cached
+    return cached
+
+
+def capacity(tokens: int, experts: int) -> int:
+    """C = max(8, roundup8(ceil(2 * assignments / E))) (parrot/metal_moe.py:388-391)."""
+    assignments = 2 * tokens
+    return max(8, ((2 * assignments + experts - 1) // experts + 7) // 8 * 8)
+
+
+@dataclass
+class Grouping:
+    """Deterministic expert grouping of the 2T assignments a = 2t + k.
+
+    positions[a]: stable slot of a among its expert's assignments;
+    counts[e]; offsets[: E + 1] exclusive prefix of counts and
+    offsets[E + 1 :] of max(0, counts - C); perm[e, s] = assignment in
+    slot s < C (-1 if empty); overflow[: offsets[2E + 1]] = assignments with
+    slot >= C, expert-contiguous, ascending a within an expert.
+    """
+    positions: Tensor
+    counts: Tensor
+    offsets: Tensor
+    perm: Tensor
+    overflow: Tensor
+    capacity: int
+
+    @property
+    def overflow_count(self) -> Tensor:
+        return self.offsets[-1]
+
+
+@dataclass
+class RouteResult:
+    probabilities: Tensor | None
+    weights: Tensor
+    indices: Tensor
+    grouping: Grouping
+    logits: Tensor | None = None
+
+
+def _alloc_grouping(tokens: int, experts: int, cap: int, device) -> Grouping:
+    i32 = dict(dtype=torch.int32, device=device)
+    return Grouping(
+        positions=torch.empty(2 * tokens, **i32),
+        counts=torch.empty(experts, **i32),
+        offsets=torch.empty(2 * experts + 2, **i32),
+        perm=torch.empty((experts, cap), **i32),
+        overflow=torch.empty(max(2 * tokens, 1), **i32),
+        capacity=cap,
+    )
+
+
+def _route_workspace(owner, tokens: int, experts: int, device) -> tuple[Tensor, int]:
+    nbytes = _abi.load().parrot_route_workspace_bytes(tokens, experts)
+    return _scratch(owner, "_hip_route_workspace", nbytes, device), nbytes
+
+
+# ---------------------------------------------------------------------------
+# routing (cf. metal_route, parrot/metal_moe.py:58-81)
+# ---------------------------------------------------------------------------
+
+def route(module: "MoE", flat: Tensor, collect_stats: bool,
+          logit_bias: Tensor | None = None, return_logits: bool = False) -> RouteResult:
+    """Router projection + softmax top-2 + deterministic grouping."""
+    _require(flat, "HIP routing")
+    tokens, dim = flat.shape
+    experts = module.cfg.n_experts
+    if experts > MAX_EXPERTS or module.cfg.top_k != 2:
+        raise RuntimeError(f"HIP routing supports top-2 of at most {MAX_EXPERTS} experts")
+    flat = flat.contiguous()
+    router_w = module.router.weight
+    if router_w.dtype != flat.dtype or not router_w.is_contiguous():
+        raise RuntimeError("router weight must be contiguous and match the input dtype")
+    dev = flat.device
+    cap = capacity(tokens, experts)
+    f32 = dict(dtype=torch.float32, device=dev)
+    probs = torch.empty((tokens, experts), **f32) if collect_stats else None
+    logits = torch.empty((tokens, experts), **f32) if return_logits else None
+    weights = torch.empty((tokens, 2), **f32)
+    indices = torch.empty((tokens, 2), dtype=torch.int64, device=dev)
+    g = _alloc_grouping(tokens, experts, cap, dev)
+    if logit_bias is not None:
+        logit_bias = logit_bias.to(device=dev, dtype=torch.float32).contiguous()
+    ws, nbytes = _route_workspace(module, tokens, experts, dev)
+    lib = _abi.load()
+    _abi.check(lib.parrot_route_bf16(
+        ptr(flat), ptr(router_w), ptr(logit_bias), tokens, dim, experts, cap,
+        ptr(logits), ptr(probs), ptr(weights), ptr(indices), ptr(g.positions), ptr(g.counts),
+        ptr(g.offsets), ptr(g.perm), ptr(g.overflow), ptr(ws), nbytes, _stream(dev)),
+        "parrot_route_bf16")
+    module.__dict__["_hip_grouping"] = g
+    return RouteResult(probs, weights, indices, g, logits)
+
+
+def route_from_logits(logits: Tensor, logit_bias: Tensor | None = None,
+                      collect_stats: bool = False) -> RouteResult:
+    """Top-2 + grouping from given fp32 router logits [T, E] (parity entry)."""
+    if logits.device.type != "cuda" or logits.dtype != torch.float32 or logits.ndim != 2:
+        raise RuntimeError("route_from_logits requires fp32 [tokens, experts] ROCm logits")
+    tokens, experts = logits.shape
+    logits = logits.contiguous()
+    dev = logits.device
+    cap = capacity(tokens, experts)
+    f32 = dict(dtype=torch.float32, device=dev)
+    probs = torch.empty((tokens, experts), **f32) if collect_stats else None
+    weights = torch.empty((tokens, 2), **f32)
+    indices = torch.empty((tokens, 2), dtype=torch.int64, device=dev)
+    g = _alloc_grouping(tokens, experts, cap, dev)
+    if logit_bias is not None:
+        logit_bias = logit_bias.to(device=dev, dtype=torch.float32).contiguous()
+    lib = _abi.load()
+    nbytes = lib.parrot_route_workspace_bytes(tokens, experts)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+    _abi.check(lib.parrot_route_from_logits_f32(
+        ptr(logits), ptr(logit_bias), tokens, experts, cap, ptr(probs), ptr(weights),
+        ptr(indices), ptr(g.positions), ptr(g.counts), ptr(g.offsets), ptr(g.perm),
+        ptr(g.overflow), ptr(ws), nbytes, _stream(dev)), "parrot_route_from_logits_f32")
+    return RouteResult(probs, weights, indices, g)
+
+
+def group_indices(indices: Tensor, experts: int, cap: int | None = None) -> Grouping:
+    """Deterministic grouping of caller-supplied top-2 indices
+    (cf. moe_count_assignments, parrot/kernels/moe_bf16.metal:650-660)."""
+    if indices.device.type != "cuda" or indices.dtype != torch.int64 or indices.shape[-1] != 2:
+        raise RuntimeError("group_indices requires int64 [tokens, 2] ROCm indices")
+    indices = indices.reshape(-1, 2).contiguous()
+    tokens = indices.shape[0]
+    dev = indices.device
+    cap = capacity(tokens, experts) if cap is None else cap
+    g = _alloc_grouping(tokens, experts, cap, dev)
+    lib = _abi.load()
+    nbytes = lib.parrot_route_workspace_bytes(tokens, experts)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+    _abi.check(lib.parrot_group_indices(
+        ptr(indices), tokens, experts, cap, ptr(g.positions), ptr(g.counts), ptr(g.offsets),
+        ptr(g.perm), ptr(g.overflow), ptr(ws), nbytes, _stream(dev)), "parrot_group_indices")
+    return g
+
+
+# ---------------------------------------------------------------------------
+# packed expert weights (cf. pack_combined_weights, parrot/metal_moe.py:105-131)
+# ---------------------------------------------------------------------------
+
+def _interleave_gate_up(gate: Tensor, up: Tensor) -> Tensor:
+    """[..., H, dim] x 2 -> [..., 2H, dim] alternating 16 gate and 16 up rows."""
+    *lead, hidden, dim = gate.shape
+    g = gate.reshape(*lead, hidden // 16, 16, dim)
+    u = up.reshape(*lead, hidden // 16, 16, dim)
+    return torch.stack((g, u), dim=-3).reshape(*lead, 2 * hidden, dim).contiguous()
+
+
+def _expert_parameters(module: "MoE") -> list[Tensor]:
+    params = [p for expert in module.experts
+              for p in (expert.gate.weight, expert.up.weight, expert.down.weight)]
+    return params + [module.shared.gate.weight, module.shared.up.weight,
+                     module.shared.down.weight]
+
+
+def pack_expert_weights(module: "MoE") -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(gate_up [E, 2H, dim], down [E, dim, H], shared_gate_up [2Hs, dim],
+    shared_down [dim, Hs]), cached until a parameter changes.  As in the
+    reference, an eval-mode module under no-grad reuses the cache without
+    re-checking versions; call ``invalidate_packed_weights`` after editing
+    weights in place in that mode."""
+    cached = module.__dict__.get("_hip_packed")
+    if cached is not None and not torch.is_grad_enabled() and not module.training:
+        return cached[1]
+    params = _expert_parameters(module)
+    version = tuple((p._version, p.device, p.dtype, p.data_ptr()) for p in params)
+    if cached is not None and cached[0] == version:
+        return cached[1]
+    with torch.no_grad():
+        gate = torch.stack([e.gate.weight.detach() for e in module.experts])
+        up = torch.stack([e.up.weight.detach() for e in module.experts])
+        packed = (
+            _interleave_gate_up(gate, up),
+            torch.stack([e.down.weight.detach() for e in module.experts]).contiguous(),
+            _interleave_gate_up(module.shared.gate.weight.detach(),
+                                module.shared.up.weight.detach()),
+            module.shared.down.weight.detach().contiguous(),
+        )
+    module.__dict__["_hip_packed"] = (version, packed)
+    return packed
+
+
+def invalidate_packed_weights(module: "MoE") -> None:
+    module.__dict__.pop("_hip_packed", None)
+
+
+# ---------------------------------------------------------------------------
+# grouped experts (cf. grouped_mps_experts, parrot/metal_moe.py:372-416)
+# ---------------------------------------------------------------------------
+
+def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: Tensor,
+                        positions: Tensor | None = None, counts: Tensor | None = None,
+                        addend: Tensor | None = None,
+                        grouping: Grouping | None = None) -> Tensor:
+    """Routed + shared SwiGLU experts and weighted combine; returns
+    ``addend + delta`` (each rounded to the input dtype) when ``addend`` is
+    given, else the MoE delta."""
+    _require(flat, "The grouped HIP backend")
+    cfg = module.cfg
+    tokens, dim = flat.shape
+    experts = cfg.n_experts
+    if cfg.top_k != 2 or experts > MAX_EXPERTS:
+        raise RuntimeError(f"grouped HIP experts support top-2 of at most {MAX_EXPERTS} experts")
+    flat = flat.contiguous()
+    if grouping is None:
+        cached = module.__dict__.get("_hip_grouping")
+        if positions is not None and cached is not None and cached.positions is positions:
+            grouping = cached
+        else:
+            # Slots are recomputed from the indices in the deterministic stable
+            # order; the expert outputs do not depend on the slot order.
+            grouping = group_indices(indices, experts)
+    gate_up, down, shared_gate_up, shared_down = pack_expert_weights(module)
+    if gate_up.dtype != flat.dtype:
+        raise RuntimeError("expert weights must match the input dtype")
+    if addend is not None:
+        _require(addend, "MoE addend")
+        addend = addend.reshape(tokens, dim).contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    lib = _abi.load()
+    nbytes = lib.parrot_experts_workspace_bytes(tokens, dim, cfg.expert_dim,
+                                                cfg.shared_expert_dim)
+    ws = _scratch(module, "_hip_experts_workspace", nbytes, flat.device)
+    out = torch.empty_like(flat)
+    _abi.check(lib.parrot_grouped_experts_bf16(
+        ptr(flat), tokens, dim, experts, cfg.expert_dim, cfg.shared_expert_dim,
+        grouping.capacity, ptr(grouping.counts), ptr(grouping.offsets), ptr(grouping.perm),
+        ptr(grouping.overflow), ptr(weights), ptr(gate_up), ptr(down), ptr(shared_gate_up),
+        ptr(shared_down), ptr(addend), ptr(out), ptr(ws), nbytes, _stream(flat.device)),
+        "parrot_grouped_experts_bf16")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm and Block AttnRes (cf. parrot/metal_moe.py:37-55, 419-477)
+# ---------------------------------------------------------------------------
+
+def rms_norm(module, x: Tensor) -> Tensor:
+    """Inference RMSNorm for ROCm bf16 tensors."""
+    _require(x, "HIP RMSNorm")
+    x = x.contiguous()
+    dim = x.shape[-1]
+    rows = x.numel() // dim
+    out = torch.empty_like(x)
+    weight = module.weight
+    if weight.dtype != x.dtype:
+        raise RuntimeError("RMSNorm weight must match the input dtype")
+    _abi.check(_abi.load().parrot_rms_norm_bf16(
+        ptr(x), ptr(weight), ptr(out), rows, dim, float(module.eps), _stream(x.device)),
+        "parrot_rms_norm_bf16")
+    return out
+
+
+_SourceArray = ctypes.c_void_p * MAX_DEPTH_SOURCES
+
+
+def _depth(module, sources: list[Tensor], output_norm) -> Tensor:
+    if not 1 <= len(sources) <= MAX_DEPTH_SOURCES:
+        raise RuntimeError(f"HIP depth mixing supports one to {MAX_DEPTH_SOURCES} sources")
+    first = sources[0]
+    _require(first, "The HIP depth backend")
+    dim = first.shape[-1]
+    tokens = first.numel() // dim
+    flat = []
+    for s in sources:
+        if s.shape != first.shape or s.dtype != first.dtype or s.device != first.device:
+            raise RuntimeError("depth sources must share shape, dtype and device")
+        flat.append(s.contiguous())
+    array = _SourceArray(*([t.data_ptr() for t in flat] +
+                           [flat[0].data_ptr()] * (MAX_DEPTH_SOURCES - len(flat))))
+    out = torch.empty_like(flat[0])
+    norm_w = None if output_norm is None else output_norm.weight
+    _abi.check(_abi.load().parrot_depth_mix_bf16(
+        ctypes.cast(array, ctypes.c_void_p), len(flat), ptr(module.query),
+        ptr(module.norm.weight), float(module.norm.eps), ptr(norm_w),
+        0.0 if output_norm is None else float(output_norm.eps), tokens, dim,
+        ptr(out) if output_norm is None else None,
+        None if output_norm is None else ptr(out), _stream(first.device)),
+        "parrot_depth_mix_bf16")
+    # Keep the source tensors alive until the kernel is enqueued (it is).
+    del flat
+    return out
+
+
+def depth_mix(module, sources: list[Tensor]) -> Tensor:
+    """Block AttnRes mix of 1..9 sources (cf. metal_depth_mix)."""
+    return _depth(module, sources, None)
+
+
+def depth_mix_norm(module, sources: list[Tensor], output_norm) -> Tensor:
+    """Depth mix rounded to bf16, then the consumer RMSNorm, in one kernel
+    (cf. metal_depth_mix_norm, for every token count)."""
+    return _depth(module, sources, output_norm)

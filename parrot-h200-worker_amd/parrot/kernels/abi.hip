@@ -1,0 +1,334 @@
+// extern "C" entry points declared in include/parrot_hip.h.
+//
+// Every entry point validates its arguments on the host and returns a
+// negative PARROT_ERR_* code before launching anything, or the hipError_t
+// of its launches.  Nothing here allocates, synchronises or keeps state.
+#include "../../../include/parrot_hip.h"
+
+#include "common.h"
+
+namespace {
+
+using parrot::kMaxDepthSources;
+using parrot::kMaxExperts;
+
+constexpr size_t kAlign = 256;
+
+size_t round_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int status(hipError_t e) { return e == hipSuccess ? PARROT_OK : static_cast<int>(e); }
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+size_t route_ws_bytes(int64_t tokens, int32_t experts) {
+  return round_up(static_cast<size_t>(parrot::route_blocks(tokens)) * experts * sizeof(int32_t));
+}
+
+struct ExpertsWorkspace {
+  uint16_t* hidden;
+  float* y_routed;
+  float* y_shared;
+  size_t bytes;
+};
+
+ExpertsWorkspace experts_ws(void* base, int64_t tokens, int32_t dim, int32_t hidden_dim,
+                            int32_t shared_dim) {
+  const size_t hstride = static_cast<size_t>(hidden_dim > shared_dim ? hidden_dim : shared_dim);
+  const size_t h_bytes = round_up(3 * static_cast<size_t>(tokens) * hstride * sizeof(uint16_t));
+  const size_t yr_bytes = round_up(2 * static_cast<size_t>(tokens) * dim * sizeof(float));
+  const size_t ys_bytes = round_up(static_cast<size_t>(tokens) * dim * sizeof(float));
+  char* p = static_cast<char*>(base);
+  ExpertsWorkspace ws;
+  ws.hidden = reinterpret_cast<uint16_t*>(p);
+  ws.y_routed = reinterpret_cast<float*>(p + h_bytes);
+  ws.y_shared = reinterpret_cast<float*>(p + h_bytes + yr_bytes);
+  ws.bytes = h_bytes + yr_bytes + ys_bytes;
+  return ws;
+}
+
+int check_group_outputs(int32_t* positions, int32_t* counts, int32_t* offsets, int32_t* perm,
+                        int32_t* overflow) {
+  if (!positions || !counts || !offsets || !perm || !overflow) return PARROT_ERR_NULL_POINTER;
+  return PARROT_OK;
+}
+
+int check_route_shape(int64_t tokens, int32_t experts, int32_t capacity) {
+  if (tokens < 0 || tokens > (int64_t{1} << 29)) return PARROT_ERR_BAD_SHAPE;
+  if (experts < 2 || experts > kMaxExperts) return PARROT_ERR_UNSUPPORTED;
+  if (capacity < 1) return PARROT_ERR_BAD_SHAPE;
+  if (static_cast<int64_t>(experts) * capacity > (int64_t{1} << 30)) return PARROT_ERR_BAD_SHAPE;
+  return PARROT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int parrot_abi_version(void) { return PARROT_ABI_VERSION; }
+
+const char* parrot_status_string(int s) {
+  switch (s) {
+    case PARROT_OK: return "ok";
+    case PARROT_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case PARROT_ERR_BAD_SHAPE: return "invalid shape or size";
+    case PARROT_ERR_UNSUPPORTED: return "shape outside the supported range of the HIP kernels";
+    case PARROT_ERR_WORKSPACE: return "workspace missing or too small";
+    case PARROT_ERR_ALIGNMENT: return "tensor pointer is not 16-byte aligned";
+    default: break;
+  }
+  if (s > 0) return hipGetErrorString(static_cast<hipError_t>(s));
+  return "unknown status";
+}
+
+int32_t parrot_capacity(int64_t tokens, int32_t experts) {
+  if (experts <= 0 || tokens < 0) return 0;
+  const int64_t assignments = 2 * tokens;
+  const int64_t per = (2 * assignments + experts - 1) / experts;
+  const int64_t c = (per + 7) / 8 * 8;
+  return static_cast<int32_t>(c < 8 ? 8 : c);
+}
+
+int parrot_rms_norm_bf16(const void* x, const void* weight, void* out, int64_t rows,
+                         int32_t dim, float eps, void* stream) {
+  if (!x || !weight || !out) return PARROT_ERR_NULL_POINTER;
+  if (rows < 0 || dim <= 0 || dim % 4) return PARROT_ERR_BAD_SHAPE;
+  if (dim > 4096) return PARROT_ERR_UNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+       reinterpret_cast<uintptr_t>(out)) & 7u)
+    return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_rms_norm(static_cast<const uint16_t*>(x),
+                                        static_cast<const uint16_t*>(weight),
+                                        static_cast<uint16_t*>(out), rows, dim, eps,
+                                        as_stream(stream)));
+}
+
+int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const void* query,
+                          const void* score_norm_weight, float score_eps,
+                          const void* out_norm_weight, float out_eps, int64_t tokens,
+                          int32_t dim, void* out_mix, void* out_norm, void* stream) {
+  if (!sources || !query || !score_norm_weight) return PARROT_ERR_NULL_POINTER;
+  if (!out_mix && !out_norm) return PARROT_ERR_NULL_POINTER;
+  if (out_norm && !out_norm_weight) return PARROT_ERR_NULL_POINTER;
+  if (n_sources < 1 || n_sources > kMaxDepthSources) return PARROT_ERR_UNSUPPORTED;
+  if (tokens < 0 || dim <= 0 || dim % 4) return PARROT_ERR_BAD_SHAPE;
+  if (dim > 2048) return PARROT_ERR_UNSUPPORTED;
+  parrot::DepthSources srcs{};
+  uintptr_t bits = reinterpret_cast<uintptr_t>(query) |
+                   reinterpret_cast<uintptr_t>(score_norm_weight) |
+                   reinterpret_cast<uintptr_t>(out_norm_weight) |
+                   reinterpret_cast<uintptr_t>(out_mix) | reinterpret_cast<uintptr_t>(out_norm);
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    const void* p = sources[s < n_sources ? s : 0];
+    if (!p) return PARROT_ERR_NULL_POINTER;
+    bits |= reinterpret_cast<uintptr_t>(p);
+    srcs.src[s] = static_cast<const uint16_t*>(p);
+  }
+  if (bits & 7u) return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_depth_mix(
+      srcs, n_sources, static_cast<const uint16_t*>(query),
+      static_cast<const uint16_t*>(score_norm_weight), score_eps,
+      static_cast<const uint16_t*>(out_norm_weight), out_eps, tokens, dim,
+      static_cast<uint16_t*>(out_mix), static_cast<uint16_t*>(out_norm), as_stream(stream)));
+}
+
+size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts) {
+  if (tokens < 0 || experts <= 0) return 0;
+  return route_ws_bytes(tokens, experts);
+}
+
+static int route_common(const void* x, const void* router_weight, const float* logits,
+                        const float* logit_bias, int64_t tokens, int32_t dim, int32_t experts,
+                        int32_t capacity, float* out_logits, float* out_probs,
+                        float* out_weights, int64_t* out_indices, int32_t* out_positions,
+                        int32_t* out_counts, int32_t* out_offsets, int32_t* out_perm,
+                        int32_t* out_overflow, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  if (int rc = check_route_shape(tokens, experts, capacity)) return rc;
+  if (!out_weights || !out_indices) return PARROT_ERR_NULL_POINTER;
+  if (int rc = check_group_outputs(out_positions, out_counts, out_offsets, out_perm, out_overflow))
+    return rc;
+  if (!workspace || workspace_bytes < route_ws_bytes(tokens, experts)) return PARROT_ERR_WORKSPACE;
+  int32_t* block_counts = static_cast<int32_t*>(workspace);
+  const hipStream_t s = as_stream(stream);
+  hipError_t e = parrot::launch_route(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(router_weight), logits,
+      logit_bias, tokens, dim, experts, out_logits, out_probs, out_weights, out_indices,
+      out_positions, block_counts, s);
+  if (e != hipSuccess) return status(e);
+  return status(parrot::launch_group(out_indices, tokens, experts, capacity, block_counts,
+                                     out_positions, out_counts, out_offsets, out_perm,
+                                     out_overflow, s));
+}
+
+int parrot_route_bf16(const void* x, const void* router_weight, const float* logit_bias,
+                      int64_t tokens, int32_t dim, int32_t experts, int32_t capacity,
+                      float* out_logits, float* out_probs, float* out_weights,
+                      int64_t* out_indices, int32_t* out_positions, int32_t* out_counts,
+                      int32_t* out_offsets, int32_t* out_perm, int32_t* out_overflow,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  if (!x || !router_weight) return PARROT_ERR_NULL_POINTER;
+  if (dim <= 0 || dim % 32) return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(router_weight)) return PARROT_ERR_ALIGNMENT;
+  return route_common(x, router_weight, nullptr, logit_bias, tokens, dim, experts, capacity,
+                      out_logits, out_probs, out_weights, out_indices, out_positions,
+                      out_counts, out_offsets, out_perm, out_overflow, workspace,
+                      workspace_bytes, stream);
+}
+
+int parrot_route_from_logits_f32(const float* logits, const float* logit_bias, int64_t tokens,
+                                 int32_t experts, int32_t capacity, float* out_probs,
+                                 float* out_weights, int64_t* out_indices,
+                                 int32_t* out_positions, int32_t* out_counts,
+                                 int32_t* out_offsets, int32_t* out_perm,
+                                 int32_t* out_overflow, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  if (!logits) return PARROT_ERR_NULL_POINTER;
+  return route_common(nullptr, nullptr, logits, logit_bias, tokens, 0, experts, capacity,
+                      nullptr, out_probs, out_weights, out_indices, out_positions, out_counts,
+                      out_offsets, out_perm, out_overflow, workspace, workspace_bytes, stream);
+}
+
+int parrot_group_indices(const int64_t* indices, int64_t tokens, int32_t experts,
+                         int32_t capacity, int32_t* out_positions, int32_t* out_counts,
+                         int32_t* out_offsets, int32_t* out_perm, int32_t* out_overflow,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (!indices) return PARROT_ERR_NULL_POINTER;
+  if (int rc = check_route_shape(tokens, experts, capacity)) return rc;
+  if (int rc = check_group_outputs(out_positions, out_counts, out_offsets, out_perm, out_overflow))
+    return rc;
+  if (!workspace || workspace_bytes < route_ws_bytes(tokens, experts)) return PARROT_ERR_WORKSPACE;
+  int32_t* block_counts = static_cast<int32_t*>(workspace);
+  const hipStream_t s = as_stream(stream);
+  hipError_t e = parrot::launch_rank_indices(indices, tokens, experts, out_positions,
+                                             block_counts, s);
+  if (e != hipSuccess) return status(e);
+  return status(parrot::launch_group(indices, tokens, experts, capacity, block_counts,
+                                     out_positions, out_counts, out_offsets, out_perm,
+                                     out_overflow, s));
+}
+
+size_t parrot_experts_workspace_bytes(int64_t tokens, int32_t dim, int32_t hidden_dim,
+                                      int32_t shared_dim) {
+  if (tokens < 0 || dim <= 0 || hidden_dim <= 0 || shared_dim <= 0) return 0;
+  return experts_ws(nullptr, tokens, dim, hidden_dim, shared_dim).bytes;
+}
+
+}  // extern "C"
+
+namespace {
+
+struct ExpertsCall {
+  parrot::GroupMap map;
+  parrot::ExpertWeights w;
+  ExpertsWorkspace ws;
+};
+
+// Validation shared by the expert entry points; weights / map pointers a
+// stage does not read may be NULL (need_* = false).
+int check_experts(int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
+                  int32_t shared_dim, int32_t capacity, const int32_t* counts,
+                  const int32_t* offsets, const int32_t* perm, const int32_t* overflow,
+                  void* workspace, size_t workspace_bytes, ExpertsWorkspace* ws) {
+  if (!counts || !offsets || !perm || !overflow) return PARROT_ERR_NULL_POINTER;
+  if (int rc = check_route_shape(tokens, experts, capacity)) return rc;
+  if (dim <= 0 || hidden_dim <= 0 || shared_dim <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (dim % 64 || hidden_dim % 64 || shared_dim % 64) return PARROT_ERR_UNSUPPORTED;
+  *ws = experts_ws(workspace, tokens, dim, hidden_dim, shared_dim);
+  if (!workspace || workspace_bytes < ws->bytes) return PARROT_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return PARROT_ERR_ALIGNMENT;
+  return PARROT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int parrot_experts_gate_up_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,
+                                int32_t hidden_dim, int32_t shared_dim, int32_t capacity,
+                                const int32_t* counts, const int32_t* offsets,
+                                const int32_t* perm, const int32_t* overflow,
+                                const void* packed_gate_up, const void* shared_gate_up,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (!x || !packed_gate_up || !shared_gate_up) return PARROT_ERR_NULL_POINTER;
+  ExpertsWorkspace ws;
+  if (int rc = check_experts(tokens, dim, experts, hidden_dim, shared_dim, capacity, counts,
+                             offsets, perm, overflow, workspace, workspace_bytes, &ws))
+    return rc;
+  if (!aligned16(x) || !aligned16(packed_gate_up) || !aligned16(shared_gate_up))
+    return PARROT_ERR_ALIGNMENT;
+  parrot::GroupMap map{counts, offsets, perm, overflow, nullptr};
+  parrot::ExpertWeights w{static_cast<const uint16_t*>(packed_gate_up), nullptr,
+                          static_cast<const uint16_t*>(shared_gate_up), nullptr};
+  return status(parrot::launch_expert_gemm(1, static_cast<const uint16_t*>(x), tokens, dim,
+                                           experts, hidden_dim, shared_dim, capacity, map, w,
+                                           ws.hidden, ws.y_routed, ws.y_shared,
+                                           as_stream(stream)));
+}
+
+int parrot_experts_down_bf16(int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
+                             int32_t shared_dim, int32_t capacity, const int32_t* counts,
+                             const int32_t* offsets, const int32_t* perm,
+                             const int32_t* overflow, const float* route_weights,
+                             const void* down, const void* shared_down, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  if (!route_weights || !down || !shared_down) return PARROT_ERR_NULL_POINTER;
+  ExpertsWorkspace ws;
+  if (int rc = check_experts(tokens, dim, experts, hidden_dim, shared_dim, capacity, counts,
+                             offsets, perm, overflow, workspace, workspace_bytes, &ws))
+    return rc;
+  if (!aligned16(down) || !aligned16(shared_down)) return PARROT_ERR_ALIGNMENT;
+  parrot::GroupMap map{counts, offsets, perm, overflow, route_weights};
+  parrot::ExpertWeights w{nullptr, static_cast<const uint16_t*>(down), nullptr,
+                          static_cast<const uint16_t*>(shared_down)};
+  return status(parrot::launch_expert_gemm(2, nullptr, tokens, dim, experts, hidden_dim,
+                                           shared_dim, capacity, map, w, ws.hidden, ws.y_routed,
+                                           ws.y_shared, as_stream(stream)));
+}
+
+int parrot_experts_combine_bf16(int64_t tokens, int32_t dim, int32_t hidden_dim,
+                                int32_t shared_dim, const void* addend, void* out,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (!out) return PARROT_ERR_NULL_POINTER;
+  if (tokens < 0 || dim <= 0 || dim % 4 || hidden_dim <= 0 || shared_dim <= 0)
+    return PARROT_ERR_BAD_SHAPE;
+  const ExpertsWorkspace ws = experts_ws(workspace, tokens, dim, hidden_dim, shared_dim);
+  if (!workspace || workspace_bytes < ws.bytes) return PARROT_ERR_WORKSPACE;
+  if (!aligned16(workspace) || !aligned16(out) || (addend && !aligned16(addend)))
+    return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_combine(ws.y_routed, ws.y_shared,
+                                       static_cast<const uint16_t*>(addend), tokens, dim,
+                                       static_cast<uint16_t*>(out), as_stream(stream)));
+}
+
+int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,
+                                int32_t hidden_dim, int32_t shared_dim, int32_t capacity,
+                                const int32_t* counts, const int32_t* offsets,
+                                const int32_t* perm, const int32_t* overflow,
+                                const float* route_weights, const void* packed_gate_up,
+                                const void* down, const void* shared_gate_up,
+                                const void* shared_down, const void* addend, void* out,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (!out || !route_weights || !down || !shared_down) return PARROT_ERR_NULL_POINTER;
+  ExpertsWorkspace ws;
+  if (int rc = check_experts(tokens, dim, experts, hidden_dim, shared_dim, capacity, counts,
+                             offsets, perm, overflow, workspace, workspace_bytes, &ws))
+    return rc;
+  if (!aligned16(down) || !aligned16(shared_down) || !aligned16(out) ||
+      (addend && !aligned16(addend)))
+    return PARROT_ERR_ALIGNMENT;
+  int rc = parrot_experts_gate_up_bf16(x, tokens, dim, experts, hidden_dim, shared_dim,
+                                       capacity, counts, offsets, perm, overflow,
+                                       packed_gate_up, shared_gate_up, workspace,
+                                       workspace_bytes, stream);
+  if (rc != PARROT_OK) return rc;
+  rc = parrot_experts_down_bf16(tokens, dim, experts, hidden_dim, shared_dim, capacity, counts,
+                                offsets, perm, overflow, route_weights, down, shared_down,
+                                workspace, workspace_bytes, stream);
+  if (rc != PARROT_OK) return rc;
+  return parrot_experts_combine_bf16(tokens, dim, hidden_dim, shared_dim, addend, out,
+                                     workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,130 @@
+// Shared device helpers and the internal launcher API of the Parrot HIP
+// inference path (gfx950 / CDNA4, 64-wide wavefronts).
+//
+// Storage type for bf16 is uint16_t; conversions are bit-exact
+// round-to-nearest-even, so every rounding point is explicit in the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace parrot {
+
+constexpr int kWave = 64;
+constexpr int kMaxExperts = 32;
+constexpr int kMaxDepthSources = 9;
+// Assignments (token, k) handled by one route workgroup: 64 tokens x top-2.
+constexpr int kRouteTokensPerBlock = 64;
+constexpr int kRouteAssignPerBlock = 2 * kRouteTokensPerBlock;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// IEEE round-to-nearest-even fp32 -> bf16; NaN stays NaN (quietened).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) |
+         (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+__device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Butterfly sum over the 64 lanes of a wavefront; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// silu(g) * u with silu(g) = g / (1 + e^-g), evaluated in fp32.
+__device__ __forceinline__ float swiglu(float g, float u) {
+  return (g / (1.0f + __expf(-g))) * u;
+}
+
+// ---------------------------------------------------------------------------
+// Launchers (host side, defined next to their kernels).  All return a
+// hipError_t; shapes are validated by the C-ABI layer before these run.
+// ---------------------------------------------------------------------------
+
+hipError_t launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out,
+                           int64_t rows, int dim, float eps, hipStream_t s);
+
+struct DepthSources {
+  const uint16_t* src[kMaxDepthSources];
+};
+
+hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
+                            const uint16_t* query, const uint16_t* score_w,
+                            float score_eps, const uint16_t* out_norm_w,
+                            float out_eps, int64_t tokens, int dim,
+                            uint16_t* out_mix, uint16_t* out_norm, hipStream_t s);
+
+// Routing: router projection (or given fp32 logits) + top-2 + per-block
+// stable ranks.  Writes block-local ranks into `positions` and per-block
+// expert histograms into `block_counts` [n_blocks, experts].
+hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
+                        const float* given_logits, const float* bias,
+                        int64_t tokens, int dim, int experts, float* out_logits,
+                        float* probs, float* weights, int64_t* indices,
+                        int32_t* positions, int32_t* block_counts, hipStream_t s);
+
+// Number of route workgroups (= rows of block_counts) for `tokens`.
+int route_blocks(int64_t tokens);
+
+// Block-local ranks for externally supplied top-2 indices.
+hipError_t launch_rank_indices(const int64_t* indices, int64_t tokens, int experts,
+                               int32_t* positions, int32_t* block_counts,
+                               hipStream_t s);
+
+// Turns block-local ranks into global stable positions and writes the
+// fixed-capacity map, the expert-contiguous overflow list and the offsets
+// table: offsets[0..E] = exclusive prefix of counts, offsets[E+1..2E+1] =
+// exclusive prefix of per-expert overflow counts.
+hipError_t launch_group(const int64_t* indices, int64_t tokens, int experts,
+                        int capacity, const int32_t* block_counts,
+                        int32_t* positions, int32_t* counts, int32_t* offsets,
+                        int32_t* perm, int32_t* overflow, hipStream_t s);
+
+struct ExpertWeights {
+  const uint16_t* gate_up;         // [E, 2H, dim], gate/up interleaved per 16 rows
+  const uint16_t* down;            // [E, dim, H]
+  const uint16_t* shared_gate_up;  // [2Hs, dim], interleaved the same way
+  const uint16_t* shared_down;     // [dim, Hs]
+};
+
+struct GroupMap {
+  const int32_t* counts;    // [E]
+  const int32_t* offsets;   // [2E+2]
+  const int32_t* perm;      // [E, C]
+  const int32_t* overflow;  // [2T]
+  const float* weights;     // [2T] route weights
+};
+
+// M tile chosen for a token count (16, 32, 64 or 128 rows).
+int experts_tile_m(int64_t tokens, int experts);
+
+// Grouped SwiGLU expert GEMM over every routed assignment plus the shared
+// expert.  Phase 1 (gate/up + SwiGLU) reads x and writes hidden
+// [3T, max(H, Hs)] bf16; phase 2 (down) reads hidden and writes y_routed
+// [2T, dim] fp32 (route-weighted, assignment order) and y_shared [T, dim].
+hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int dim,
+                              int experts, int hidden_dim, int shared_dim, int capacity,
+                              const GroupMap& map, const ExpertWeights& w, uint16_t* hidden,
+                              float* y_routed, float* y_shared, hipStream_t s);
+
+hipError_t launch_combine(const float* y_routed, const float* y_shared,
+                          const uint16_t* addend, int64_t tokens, int dim,
+                          uint16_t* out, hipStream_t s);
+
+}  // namespace parrot

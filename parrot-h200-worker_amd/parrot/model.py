@@ -1,0 +1,754 @@
+"""Parrot XL decoder: PyTorch reference backend plus the MI355X HIP backend.
+
+Public API mirrors the reference package (parrot/__init__.py, parrot/model.py):
+``ModelConfig``, ``Parrot`` (``forward``, ``prefill``, ``decode_step``,
+``decode_next``, ``parameter_counts``), ``ModelOutput``, ``GenerationState``.
+
+Backends
+  * ``moe_backend="pytorch"`` / ``depth_backend="pytorch"``: plain PyTorch on
+    any device (training and inference), the semantics of the reference's
+    pytorch path (parrot/model.py:109-164, 435-569, 658-931).
+  * ``moe_backend="grouped_hip"`` / ``depth_backend="hip"``: the inference
+    hot path on MI355X -- router/top-2, deterministic fixed-capacity grouping
+    with exact overflow, grouped MFMA SwiGLU experts, combine, RMSNorm and
+    Block AttnRes run as HIP kernels (``parrot.hip_moe``).  It takes the place
+    of the reference's Apple-Metal ``grouped_mps`` / ``metal`` pair and, like
+    it, is inference-only and raises on unsupported inputs instead of falling
+    back.
+
+The module tree, parameter names and initialisation order are those of the
+reference, so state_dicts are interchangeable and ``torch.manual_seed(s);
+Parrot(cfg)`` draws the same weights.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Literal
+
+import torch
+from torch import Tensor, nn
+from torch.nn import functional as F
+from torch.utils.checkpoint import checkpoint
+
+_ROPE_TABLES: dict[tuple, tuple[Tensor, Tensor]] = {}
+_WINDOW_MASKS: dict[tuple, list[Tensor]] = {}
+
+MOE_BACKENDS = ("pytorch", "grouped_hip")
+DEPTH_BACKENDS = ("pytorch", "hip")
+_FOREIGN_BACKENDS = {
+    "metal": "Apple-Metal", "dense_mps": "Apple-Metal", "grouped_mps": "Apple-Metal",
+    "training_mps": "Apple-Metal training", "training_cuda": "CUDA training",
+}
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    vocab_size: int = 32768
+    dim: int = 768
+    n_layers: int = 16
+    n_heads: int = 8
+    n_kv_heads: int = 2
+    head_dim: int = 96
+    kv_latent_dim: int = 128
+    global_every: int = 4
+    window_size: int = 2048  # includes the current position
+    max_seq_len: int = 4096
+    n_experts: int = 16
+    top_k: int = 2
+    expert_dim: int = 512
+    shared_expert_dim: int = 256
+    moe_backend: Literal["pytorch", "grouped_hip"] = "pytorch"
+    depth_backend: Literal["pytorch", "hip"] = "pytorch"
+    residual: Literal["attnres", "standard"] = "attnres"
+    depth_block_size: int = 4  # attention and MoE each count as one module
+    rope_theta: float = 10000.0
+    norm_eps: float = 1e-6
+    aux_loss_weight: float = 0.01
+    collect_router_stats: bool = True
+    checkpoint_modules: bool = False
+    local_query_chunk: int = 256
+
+    @property
+    def depth_sources(self) -> int:
+        """Sources of the final depth mix: the embedding plus every block sum."""
+        modules = 2 * self.n_layers
+        return 1 + (modules + self.depth_block_size - 1) // self.depth_block_size
+
+    @property
+    def uses_hip(self) -> bool:
+        return self.moe_backend == "grouped_hip" or self.depth_backend == "hip"
+
+    def __post_init__(self):
+        # Same checks as the reference (parrot/model.py:45-82), with the HIP
+        # backend's limits in place of the Metal ones.
+        positive = ("vocab_size", "dim", "n_layers", "n_heads", "n_kv_heads", "head_dim",
+                    "kv_latent_dim", "global_every", "window_size", "max_seq_len",
+                    "n_experts", "top_k", "expert_dim", "shared_expert_dim",
+                    "depth_block_size", "local_query_chunk")
+        for name in positive:
+            if getattr(self, name) <= 0:
+                raise ValueError(f"{name} must be positive")
+        if self.n_heads % self.n_kv_heads or self.head_dim % 2:
+            raise ValueError("n_heads must divide by n_kv_heads; head_dim must be even")
+        if self.top_k > self.n_experts:
+            raise ValueError("top_k cannot exceed n_experts")
+        if self.residual not in ("attnres", "standard"):
+            raise ValueError("residual must be attnres or standard")
+        if self.moe_backend in _FOREIGN_BACKENDS:
+            raise ValueError(
+                f"moe_backend {self.moe_backend!r} is the reference's "
+                f"{_FOREIGN_BACKENDS[self.moe_backend]} backend; on MI355X use "
+                "'grouped_hip' (inference) or 'pytorch'")
+        if self.moe_backend not in MOE_BACKENDS:
+            raise ValueError("invalid moe_backend")
+        if self.depth_backend == "metal":
+            raise ValueError("depth_backend 'metal' is Apple-only; on MI355X use 'hip'")
+        if self.depth_backend not in DEPTH_BACKENDS:
+            raise ValueError("depth_backend must be pytorch or hip")
+        if self.moe_backend == "grouped_hip":
+            if self.top_k != 2:
+                raise ValueError("grouped_hip requires top_k=2")
+            if self.n_experts > 32:
+                raise ValueError("grouped_hip supports at most 32 routed experts")
+            if any(w % 64 for w in (self.dim, self.expert_dim, self.shared_expert_dim)):
+                raise ValueError("grouped_hip requires dim, expert_dim and "
+                                 "shared_expert_dim divisible by 64")
+        if self.uses_hip and (self.dim % 4 or self.dim > 2048):
+            raise ValueError("the HIP norm kernels require dim divisible by four and <= 2048")
+        if self.depth_backend == "hip" and self.depth_sources > 9:
+            raise ValueError("hip depth mixing supports at most nine sources")
+        if self.norm_eps <= 0 or self.rope_theta <= 0 or self.aux_loss_weight < 0:
+            raise ValueError("Invalid norm_eps, rope_theta, or aux_loss_weight")
+
+
+@dataclass
+class LocalKVCache:
+    key: Tensor    # [batch, kv heads, max positions, head width], RoPE applied
+    value: Tensor
+
+
+@dataclass
+class MLALatentCache:
+    latent: Tensor  # [batch, max positions, latent width]
+
+
+@dataclass
+class GenerationState:
+    layers: list[LocalKVCache | MLALatentCache]
+    position: int
+    batch_size: int
+
+
+@dataclass
+class ModelOutput:
+    logits: Tensor               # [batch, model positions, vocab]
+    loss: Tensor | None
+    lm_loss: Tensor | None
+    aux_loss: Tensor             # unweighted mean over layers
+    expert_utilization: Tensor   # [layers, experts], fraction of assignments
+
+
+def _hip_inference(x: Tensor) -> bool:
+    """True where the HIP kernels apply: ROCm bf16 tensors without autograd."""
+    return x.device.type == "cuda" and x.dtype == torch.bfloat16 and not torch.is_grad_enabled()
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float, use_hip: bool = False):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+        self.use_hip = use_hip
+
+    def forward(self, x: Tensor) -> Tensor:
+        if self.use_hip and _hip_inference(x):
+            from . import hip_moe
+            return hip_moe.rms_norm(self, x)
+        # fp32 statistics, one rounding back (reference parrot/model.py:125-127)
+        y = x.float()
+        y = y * torch.rsqrt(y.square().mean(-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+class DepthMix(nn.Module):
+    """Block AttnRes: attend over earlier block sums with a learned query.
+
+    Keys are RMS-normalised, values are the raw block sums
+    (reference parrot/model.py:130-164)."""
+
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.query = nn.Parameter(torch.zeros(cfg.dim))
+        self.norm = RMSNorm(cfg.dim, cfg.norm_eps, use_hip=cfg.depth_backend == "hip")
+
+    def forward(self, sources: list[Tensor]) -> Tensor:
+        if self.cfg.depth_backend == "hip":
+            from . import hip_moe
+            return hip_moe.depth_mix(self, sources)
+        values = torch.stack(sources, dim=0)
+        keys = F.rms_norm(values, (self.cfg.dim,), self.norm.weight, self.norm.eps)
+        scores = (keys.float() * self.query.float()).sum(-1)
+        alpha = scores.softmax(dim=0).to(values.dtype)
+        return (alpha.unsqueeze(-1) * values).sum(0)
+
+    def normalized(self, sources: list[Tensor], output_norm: RMSNorm) -> Tensor:
+        """``output_norm(self(sources))``; one fused kernel on the HIP backend."""
+        if self.cfg.depth_backend == "hip" and _hip_inference(sources[0]):
+            from . import hip_moe
+            return hip_moe.depth_mix_norm(self, sources, output_norm)
+        return output_norm(self(sources))
+
+
+def _rope_tables(cfg: ModelConfig, like: Tensor) -> tuple[Tensor, Tensor]:
+    """cos/sin of position * theta^(-2i/d), computed in fp32 then cast."""
+    key = (like.device.type, like.device.index, like.dtype, cfg.max_seq_len, cfg.head_dim,
+           cfg.rope_theta)
+    tables = _ROPE_TABLES.get(key)
+    if tables is None:
+        with torch.inference_mode(False):
+            inv = cfg.rope_theta ** (
+                -torch.arange(0, cfg.head_dim, 2, device=like.device).float() / cfg.head_dim)
+            angle = torch.arange(cfg.max_seq_len, device=like.device).float()[:, None] * inv
+            tables = (angle.cos().to(like.dtype), angle.sin().to(like.dtype))
+        _ROPE_TABLES[key] = tables
+    return tables
+
+
+def _apply_rope(cfg: ModelConfig, x: Tensor, start: int) -> Tensor:
+    """Rotate interleaved (even, odd) pairs of the head width."""
+    end = start + x.shape[-2]
+    if end > cfg.max_seq_len:
+        raise ValueError("RoPE position exceeds max_seq_len")
+    cos_t, sin_t = _rope_tables(cfg, x)
+    cos, sin = cos_t[start:end], sin_t[start:end]
+    even, odd = x[..., 0::2], x[..., 1::2]
+    return torch.stack((even * cos - odd * sin, even * sin + odd * cos), -1).flatten(-2)
+
+
+def _window_masks(cfg: ModelConfig, t: int, device) -> list[Tensor]:
+    """Boolean masks of the query chunks of a sliding-window prefill."""
+    key = (device.type, device.index, t, cfg.window_size, cfg.local_query_chunk)
+    masks = _WINDOW_MASKS.get(key)
+    if masks is None:
+        masks = []
+        for start in range(0, t, cfg.local_query_chunk):
+            end = min(t, start + cfg.local_query_chunk)
+            lo = max(0, start - cfg.window_size + 1)
+            q = torch.arange(start, end, device=device)[:, None]
+            k = torch.arange(lo, end, device=device)[None, :]
+            masks.append((k <= q) & (k > q - cfg.window_size))
+        _WINDOW_MASKS[key] = masks
+    return masks
+
+
+class LocalGQA(nn.Module):
+    """Sliding-window grouped-query attention with RoPE
+    (reference parrot/model.py:167-328)."""
+
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.q = nn.Linear(cfg.dim, cfg.n_heads * cfg.head_dim, bias=False)
+        self.k = nn.Linear(cfg.dim, cfg.n_kv_heads * cfg.head_dim, bias=False)
+        self.v = nn.Linear(cfg.dim, cfg.n_kv_heads * cfg.head_dim, bias=False)
+        self.out = nn.Linear(cfg.n_heads * cfg.head_dim, cfg.dim, bias=False)
+
+    def _heads(self, y: Tensor, heads: int) -> Tensor:
+        b, t, _ = y.shape
+        return y.view(b, t, heads, self.cfg.head_dim).transpose(1, 2)
+
+    def _qkv(self, x: Tensor, start: int = 0):
+        c = self.cfg
+        q = _apply_rope(c, self._heads(self.q(x), c.n_heads), start)
+        k = _apply_rope(c, self._heads(self.k(x), c.n_kv_heads), start)
+        v = self._heads(self.v(x), c.n_kv_heads)
+        return q, k, v
+
+    def prefill(self, x: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+        b, t, _ = x.shape
+        c = self.cfg
+        q, k, v = self._qkv(x)
+        if t <= c.window_size and t <= c.local_query_chunk:
+            y = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+        else:
+            parts = []
+            for mask, start in zip(_window_masks(c, t, x.device),
+                                   range(0, t, c.local_query_chunk)):
+                end = min(t, start + c.local_query_chunk)
+                lo = max(0, start - c.window_size + 1)
+                parts.append(F.scaled_dot_product_attention(
+                    q[:, :, start:end], k[:, :, lo:end], v[:, :, lo:end],
+                    attn_mask=mask, enable_gqa=True))
+            y = torch.cat(parts, dim=2)
+        return self.out(y.transpose(1, 2).reshape(b, t, -1)), k, v
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.prefill(x)[0]
+
+    def _packed_qkv(self) -> Tensor:
+        cached = self.__dict__.get("_qkv_weight")
+        if cached is not None and not torch.is_grad_enabled() and not self.training:
+            return cached[1]
+        params = (self.q.weight, self.k.weight, self.v.weight)
+        version = tuple((p._version, p.device, p.dtype, p.data_ptr()) for p in params)
+        if cached is None or cached[0] != version:
+            cached = (version, torch.cat([p.detach() for p in params], 0).contiguous())
+            self.__dict__["_qkv_weight"] = cached
+        return cached[1]
+
+    def decode(self, x: Tensor, cache: LocalKVCache, position: int,
+               addend: Tensor | None = None, defer_sum: bool = False) -> Tensor:
+        if x.shape[1] != 1:
+            raise ValueError("decode expects one model position")
+        if defer_sum:
+            raise RuntimeError("deferred attention reduction is not supported on this backend")
+        c = self.cfg
+        b = x.shape[0]
+        qw, kw = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+        q, k, v = F.linear(x, self._packed_qkv()).split((qw, kw, kw), dim=-1)
+        q = _apply_rope(c, q.view(b, 1, c.n_heads, c.head_dim).transpose(1, 2), position)
+        k = _apply_rope(c, k.view(b, 1, c.n_kv_heads, c.head_dim).transpose(1, 2), position)
+        v = v.view(b, 1, c.n_kv_heads, c.head_dim).transpose(1, 2)
+        cache.key[:, :, position:position + 1].copy_(k)
+        cache.value[:, :, position:position + 1].copy_(v)
+        lo = max(0, position - c.window_size + 1)
+        y = F.scaled_dot_product_attention(
+            q, cache.key[:, :, lo:position + 1], cache.value[:, :, lo:position + 1],
+            enable_gqa=True)
+        result = self.out(y.transpose(1, 2).reshape(b, 1, -1))
+        return result if addend is None else addend + result
+
+
+class GlobalMLA(nn.Module):
+    """NoPE attention over a joint KV latent (reference parrot/model.py:331-432).
+
+    Prefill expands the latent into heads; decode keeps only the latent and
+    absorbs the key/value up-projections into the query and output maps."""
+
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.cfg = cfg
+        width = cfg.n_heads * cfg.head_dim
+        self.q = nn.Linear(cfg.dim, width, bias=False)
+        self.kv_down = nn.Linear(cfg.dim, cfg.kv_latent_dim, bias=False)
+        self.k_up = nn.Linear(cfg.kv_latent_dim, width, bias=False)
+        self.v_up = nn.Linear(cfg.kv_latent_dim, width, bias=False)
+        self.out = nn.Linear(width, cfg.dim, bias=False)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.prefill(x)[0]
+
+    def prefill(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        b, t, _ = x.shape
+        c = self.cfg
+
+        def heads(y):
+            return y.view(b, t, c.n_heads, c.head_dim).transpose(1, 2)
+
+        latent = self.kv_down(x)
+        y = F.scaled_dot_product_attention(
+            heads(self.q(x)), heads(self.k_up(latent)), heads(self.v_up(latent)),
+            is_causal=True)
+        return self.out(y.transpose(1, 2).reshape(b, t, -1)), latent
+
+    def _absorbed(self) -> tuple[Tensor, Tensor]:
+        """(W_q absorbed with k_up [H*L, dim], v_up absorbed with out [dim, H*L])."""
+        cached = self.__dict__.get("_absorbed_weights")
+        if cached is not None and not torch.is_grad_enabled() and not self.training:
+            return cached[1]
+        c = self.cfg
+        params = (self.q.weight, self.k_up.weight, self.v_up.weight, self.out.weight)
+        version = tuple((p._version, p.device, p.dtype, p.data_ptr()) for p in params)
+        if cached is None or cached[0] != version:
+            with torch.no_grad():
+                wq = self.q.weight.detach().float().view(c.n_heads, c.head_dim, c.dim)
+                wk = self.k_up.weight.detach().float().view(c.n_heads, c.head_dim, c.kv_latent_dim)
+                wv = self.v_up.weight.detach().float().view(c.n_heads, c.head_dim, c.kv_latent_dim)
+                wo = self.out.weight.detach().float().view(c.dim, c.n_heads, c.head_dim)
+                # q_latent[h, l] = sum_d k_up[h, d, l] q[h, d]
+                absorbed_q = torch.matmul(wk.transpose(1, 2), wq).reshape(
+                    c.n_heads * c.kv_latent_dim, c.dim)
+                # out[m] = sum_{h, l} (sum_d out[m, h, d] v_up[h, d, l]) ctx[h, l]
+                absorbed_o = torch.matmul(wo.permute(1, 0, 2), wv).permute(1, 0, 2).reshape(
+                    c.dim, c.n_heads * c.kv_latent_dim)
+                dtype = self.q.weight.dtype
+                cached = (version, (absorbed_q.to(dtype).contiguous(),
+                                    absorbed_o.to(dtype).contiguous()))
+            self.__dict__["_absorbed_weights"] = cached
+        return cached[1]
+
+    def decode(self, x: Tensor, cache: MLALatentCache, position: int,
+               addend: Tensor | None = None, defer_sum: bool = False) -> Tensor:
+        if x.shape[1] != 1:
+            raise ValueError("decode expects one model position")
+        if defer_sum:
+            raise RuntimeError("deferred attention reduction is not supported on this backend")
+        c = self.cfg
+        b = x.shape[0]
+        absorbed_q, absorbed_o = self._absorbed()
+        cache.latent[:, position:position + 1].copy_(self.kv_down(x))
+        latent = cache.latent[:, :position + 1].float()
+        q_latent = F.linear(x.float(), absorbed_q.float()).view(
+            b, 1, c.n_heads, c.kv_latent_dim).transpose(1, 2)
+        per_head = latent[:, None].expand(-1, c.n_heads, -1, -1)
+        context = F.scaled_dot_product_attention(q_latent, per_head, per_head,
+                                                 scale=c.head_dim ** -0.5)
+        context = context.transpose(1, 2).reshape(b, 1, c.n_heads * c.kv_latent_dim)
+        result = F.linear(context, absorbed_o.float()).to(x.dtype)
+        return result if addend is None else addend + result
+
+
+class SwiGLU(nn.Module):
+    def __init__(self, dim: int, intermediate: int):
+        super().__init__()
+        self.gate = nn.Linear(dim, intermediate, bias=False)
+        self.up = nn.Linear(dim, intermediate, bias=False)
+        self.down = nn.Linear(intermediate, dim, bias=False)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.down(F.silu(self.gate(x)) * self.up(x))
+
+
+class MoE(nn.Module):
+    """Top-k routed SwiGLU experts plus one shared expert
+    (reference parrot/model.py:463-607)."""
+
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.router = nn.Linear(cfg.dim, cfg.n_experts, bias=False)
+        self.experts = nn.ModuleList(
+            [SwiGLU(cfg.dim, cfg.expert_dim) for _ in range(cfg.n_experts)])
+        self.shared = SwiGLU(cfg.dim, cfg.shared_expert_dim)
+
+    def _hip_route_applies(self, x: Tensor) -> bool:
+        return (self.cfg.moe_backend == "grouped_hip" and _hip_inference(x) and
+                self.cfg.top_k == 2 and self.cfg.n_experts <= 32)
+
+    def _torch_route(self, flat: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+        # Router projection and softmax in fp32 with autocast off.
+        with torch.autocast(device_type=flat.device.type, enabled=False):
+            probs = F.linear(flat.float(), self.router.weight.float()).softmax(-1)
+        weights, indices = probs.topk(self.cfg.top_k, dim=-1)
+        return probs, weights / weights.sum(-1, keepdim=True), indices
+
+    def _torch_experts(self, flat: Tensor, weights: Tensor, indices: Tensor) -> Tensor:
+        result = self.shared(flat)
+        for e, expert in enumerate(self.experts):
+            rows, slots = torch.where(indices == e)
+            if rows.numel():
+                contribution = expert(flat[rows]) * weights[rows, slots, None].to(result.dtype)
+                result = result.index_add(0, rows, contribution)
+        return result
+
+    def forward(self, x: Tensor) -> tuple[Tensor, Tensor | None, Tensor | None]:
+        flat = x.reshape(-1, x.shape[-1])
+        route_counts = None
+        grouping = None
+        if self._hip_route_applies(x):
+            from . import hip_moe
+            routed = hip_moe.route(self, flat, self.cfg.collect_router_stats)
+            probs, weights, indices = routed.probabilities, routed.weights, routed.indices
+            grouping = routed.grouping
+            route_counts = grouping.counts
+        else:
+            probs, weights, indices = self._torch_route(flat)
+        if self.cfg.moe_backend == "grouped_hip":
+            from . import hip_moe
+            result = hip_moe.grouped_hip_experts(self, flat, indices, weights,
+                                                 grouping=grouping)
+        else:
+            result = self._torch_experts(flat, weights, indices)
+        if not self.cfg.collect_router_stats:
+            return result.view_as(x), None, None
+        if route_counts is not None:
+            counts = route_counts.float()
+        else:
+            flat_idx = indices.flatten()
+            counts = torch.zeros(self.cfg.n_experts, device=indices.device,
+                                 dtype=torch.float32).scatter_add_(
+                0, flat_idx, torch.ones(flat_idx.shape, device=indices.device,
+                                        dtype=torch.float32))
+        utilization = counts / indices.numel()
+        aux = self.cfg.n_experts * (utilization * probs.mean(0)).sum()
+        return result.view_as(x), aux, utilization.detach()
+
+    def inference(self, x: Tensor, *, direct: bool, addend: Tensor | None = None,
+                  defer_sum: bool = False) -> Tensor:
+        """Inference without router statistics.  On the HIP backend the
+        addend (an open AttnRes partial sum) is folded into the combine
+        kernel; ``direct`` (decode) selects small-M GEMM tiles automatically."""
+        if defer_sum:
+            raise ValueError("deferred MoE reduction is not supported on this backend")
+        if not self._hip_route_applies(x):
+            result = self.forward(x)[0]
+            return result if addend is None else addend + result
+        from . import hip_moe
+        flat = x.reshape(-1, x.shape[-1])
+        routed = hip_moe.route(self, flat, collect_stats=False)
+        result = hip_moe.grouped_hip_experts(self, flat, routed.indices, routed.weights,
+                                             addend=addend, grouping=routed.grouping)
+        return result.view_as(x)
+
+
+class Block(nn.Module):
+    def __init__(self, cfg: ModelConfig, index: int):
+        super().__init__()
+        is_global = (index + 1) % cfg.global_every == 0
+        self.attention = GlobalMLA(cfg) if is_global else LocalGQA(cfg)
+        self.moe = MoE(cfg)
+        self.attention_norm = RMSNorm(cfg.dim, cfg.norm_eps, cfg.uses_hip)
+        self.moe_norm = RMSNorm(cfg.dim, cfg.norm_eps, cfg.uses_hip)
+
+    def attend(self, x: Tensor) -> Tensor:
+        return self.attention(self.attention_norm(x))
+
+    def feedforward(self, x: Tensor):
+        return self.moe(self.moe_norm(x))
+
+    def feedforward_inference(self, x: Tensor, *, direct: bool) -> Tensor:
+        return self.moe.inference(self.moe_norm(x), direct=direct)
+
+
+class _AttnRes:
+    """Block AttnRes residual stream: completed block sums plus the open
+    partial sum of the current block (reference parrot/model.py:680-710)."""
+
+    def __init__(self, embedded: Tensor, block_size: int):
+        self.completed = [embedded]
+        self.partial: Tensor | None = None
+        self.block_size = block_size
+        self.modules = 0
+
+    def sources(self) -> list[Tensor]:
+        return self.completed if self.partial is None else self.completed + [self.partial]
+
+    def close(self, summed: Tensor) -> None:
+        """Record ``partial + delta`` (already summed) for the next module."""
+        self.partial = summed
+        self.modules += 1
+        if self.modules % self.block_size == 0:
+            self.completed.append(summed)
+            self.partial = None
+
+    def push(self, delta: Tensor) -> None:
+        self.close(delta if self.partial is None else self.partial + delta)
+
+
+class Parrot(nn.Module):
+    def __init__(self, cfg: ModelConfig = ModelConfig()):
+        super().__init__()
+        self.config = cfg
+        self.embedding = nn.Embedding(cfg.vocab_size, cfg.dim)
+        self.blocks = nn.ModuleList([Block(cfg, i) for i in range(cfg.n_layers)])
+        self.depth_mix = nn.ModuleList(
+            [DepthMix(cfg) for _ in range(2 * cfg.n_layers + 1)]
+            if cfg.residual == "attnres" else [])
+        self.final_norm = RMSNorm(cfg.dim, cfg.norm_eps, cfg.uses_hip)
+        # The vocabulary head is tied to embedding.weight.
+        self.apply(self._init_weights)
+
+    @staticmethod
+    def _init_weights(module):
+        if isinstance(module, (nn.Linear, nn.Embedding)):
+            nn.init.normal_(module.weight, std=0.02)
+
+    # -- helpers -------------------------------------------------------------
+
+    def _mixed_input(self, stream: _AttnRes | None, x: Tensor, index: int,
+                     norm: RMSNorm) -> Tensor:
+        """Normalised input of module ``index``: RMSNorm of the depth mix
+        (AttnRes) or of the running residual (standard)."""
+        if stream is None:
+            return norm(x)
+        return self.depth_mix[index].normalized(stream.sources(), norm)
+
+    def _fuse_moe_addend(self, block: Block, h: Tensor, stream: _AttnRes | None) -> bool:
+        """Fold ``partial + delta`` into the MoE combine kernel (HIP only)."""
+        return (stream is not None and stream.partial is not None and
+                not self.config.collect_router_stats and block.moe._hip_route_applies(h))
+
+    # -- training / full-sequence forward ------------------------------------
+
+    def forward(self, input_ids: Tensor, labels: Tensor | None = None, *,
+                bag_size: int = 1, supervised_logits_only: bool = False) -> ModelOutput:
+        """Unpadded streams; labels are UNSHIFTED source-token ids or -100.
+
+        bag_size=1: position i predicts token i+1.  bag_size>1: the mean
+        embedding of bag i predicts every token of bag i+1."""
+        cfg = self.config
+        if input_ids.ndim != 2 or input_ids.numel() == 0:
+            raise ValueError("input_ids must be a nonempty [batch, source_tokens] tensor")
+        if not isinstance(bag_size, int) or bag_size < 1 or input_ids.shape[1] % bag_size:
+            raise ValueError("source_tokens must be divisible by positive integer bag_size")
+        b, source_len = input_ids.shape
+        t = source_len // bag_size
+        if t > cfg.max_seq_len:
+            raise ValueError("Input exceeds max_seq_len model positions")
+        if labels is not None and (labels.shape != input_ids.shape or t < 2):
+            raise ValueError("labels must match input_ids and contain at least two model positions")
+        if supervised_logits_only and labels is None:
+            raise ValueError("supervised_logits_only requires labels")
+
+        x = self.embedding(input_ids).reshape(b, t, bag_size, -1).mean(2)
+        stream = _AttnRes(x, cfg.depth_block_size) if cfg.residual == "attnres" else None
+        aux_losses, utilization = [], []
+        remat = cfg.checkpoint_modules and self.training and torch.is_grad_enabled()
+        index = 0
+        for block in self.blocks:
+            h = self._mixed_input(stream, x, index, block.attention_norm)
+            delta = (checkpoint(block.attention, h, use_reentrant=False) if remat
+                     else block.attention(h))
+            if stream is None:
+                x = x + delta
+            else:
+                stream.push(delta)
+            index += 1
+
+            h = self._mixed_input(stream, x, index, block.moe_norm)
+            if self._fuse_moe_addend(block, h, stream):
+                stream.close(block.moe.inference(h, direct=False, addend=stream.partial))
+            else:
+                delta, aux, usage = (checkpoint(block.moe, h, use_reentrant=False) if remat
+                                     else block.moe(h))
+                if cfg.collect_router_stats:
+                    aux_losses.append(aux)
+                    utilization.append(usage)
+                if stream is None:
+                    x = x + delta
+                else:
+                    stream.push(delta)
+            index += 1
+        if stream is not None:
+            x = self.depth_mix[-1](stream.sources())
+        # Loss-only callers can skip the last position's projection exactly.
+        head_input = x[:, :-1] if supervised_logits_only else x
+        logits = F.linear(self.final_norm(head_input), self.embedding.weight)
+
+        if cfg.collect_router_stats:
+            aux_loss = torch.stack(aux_losses).mean()
+            expert_utilization = torch.stack(utilization)
+        else:
+            aux_loss = x.new_zeros((), dtype=torch.float32)
+            expert_utilization = x.new_zeros((cfg.n_layers, cfg.n_experts), dtype=torch.float32)
+        lm_loss = loss = None
+        if labels is not None:
+            targets = labels.reshape(b, t, bag_size)[:, 1:]
+            loss_logits = (logits if supervised_logits_only else logits[:, :-1]).float()
+            valid = targets != -100
+            picked = loss_logits.gather(-1, targets.masked_fill(~valid, 0))
+            lse = torch.logsumexp(loss_logits, dim=-1)
+            total = (lse * valid.sum(-1) - (picked * valid).sum(-1)).sum()
+            lm_loss = total / valid.sum().clamp_min(1)
+            loss = lm_loss + cfg.aux_loss_weight * aux_loss
+        return ModelOutput(logits, loss, lm_loss, aux_loss, expert_utilization)
+
+    # -- incremental generation ----------------------------------------------
+
+    @torch.inference_mode()
+    def prefill(self, input_ids: Tensor) -> tuple[Tensor, GenerationState]:
+        """Run the prompt once; return next-token logits and the KV state."""
+        cfg = self.config
+        if self.training:
+            raise RuntimeError("prefill requires model.eval()")
+        if input_ids.ndim != 2 or input_ids.shape[1] < 1:
+            raise ValueError("input_ids must be nonempty [batch, positions]")
+        b, t = input_ids.shape
+        if t > cfg.max_seq_len:
+            raise ValueError("Prompt exceeds max_seq_len")
+        x = self.embedding(input_ids)
+        stream = _AttnRes(x, cfg.depth_block_size) if cfg.residual == "attnres" else None
+        caches: list[LocalKVCache | MLALatentCache] = []
+        index = 0
+        for block in self.blocks:
+            h = self._mixed_input(stream, x, index, block.attention_norm)
+            if isinstance(block.attention, LocalGQA):
+                delta, key, value = block.attention.prefill(h)
+                shape = (b, cfg.n_kv_heads, cfg.max_seq_len, cfg.head_dim)
+                cache = LocalKVCache(key.new_empty(shape), value.new_empty(shape))
+                cache.key[:, :, :t].copy_(key)
+                cache.value[:, :, :t].copy_(value)
+            else:
+                delta, latent = block.attention.prefill(h)
+                cache = MLALatentCache(latent.new_empty((b, cfg.max_seq_len, cfg.kv_latent_dim)))
+                cache.latent[:, :t].copy_(latent)
+            caches.append(cache)
+            if stream is None:
+                x = x + delta
+            else:
+                stream.push(delta)
+            index += 1
+
+            h = self._mixed_input(stream, x, index, block.moe_norm)
+            if stream is not None and stream.partial is not None and \
+                    block.moe._hip_route_applies(h):
+                stream.close(block.moe.inference(h, direct=False, addend=stream.partial))
+            else:
+                delta = block.moe.inference(h, direct=False)
+                if stream is None:
+                    x = x + delta
+                else:
+                    stream.push(delta)
+            index += 1
+        if stream is not None:
+            x = self.depth_mix[-1](stream.sources())
+        logits = F.linear(self.final_norm(x[:, -1:]), self.embedding.weight)
+        return logits, GenerationState(caches, t, b)
+
+    @torch.inference_mode()
+    def decode_step(self, input_ids: Tensor, state: GenerationState, *,
+                    _next_token_only: bool = False) -> tuple[Tensor, GenerationState]:
+        """Append one token per sequence to an existing generation state."""
+        cfg = self.config
+        if self.training:
+            raise RuntimeError("decode_step requires model.eval()")
+        if input_ids.shape != (state.batch_size, 1):
+            raise ValueError("decode_step input must be [cached batch, 1]")
+        if state.position >= cfg.max_seq_len:
+            raise ValueError("Generation state has reached max_seq_len")
+        if len(state.layers) != cfg.n_layers:
+            raise ValueError("Generation state does not match model depth")
+        x = self.embedding(input_ids)
+        stream = _AttnRes(x, cfg.depth_block_size) if cfg.residual == "attnres" else None
+        index = 0
+        for block, cache in zip(self.blocks, state.layers):
+            h = self._mixed_input(stream, x, index, block.attention_norm)
+            addend = stream.partial if stream is not None else None
+            if isinstance(block.attention, LocalGQA):
+                if not isinstance(cache, LocalKVCache):
+                    raise ValueError("Local attention received an MLA cache")
+            elif not isinstance(cache, MLALatentCache):
+                raise ValueError("MLA attention received a local cache")
+            out = block.attention.decode(h, cache, state.position, addend=addend)
+            if stream is None:
+                x = x + out
+            else:
+                stream.close(out)  # out = partial + delta
+            index += 1
+
+            if stream is not None:
+                h = self._mixed_input(stream, x, index, block.moe_norm)
+                stream.close(block.moe.inference(h, direct=True, addend=stream.partial))
+            else:
+                x = x + block.feedforward_inference(x, direct=True)
+            index += 1
+        if stream is not None:
+            h = self.depth_mix[-1].normalized(stream.sources(), self.final_norm)
+        else:
+            h = self.final_norm(x)
+        logits = F.linear(h, self.embedding.weight)
+        state.position += 1
+        return (logits.argmax(-1) if _next_token_only else logits), state
+
+    @torch.inference_mode()
+    def decode_next(self, input_ids: Tensor,
+                    state: GenerationState) -> tuple[Tensor, GenerationState]:
+        """Append one token and return the next greedy token without logits."""
+        return self.decode_step(input_ids, state, _next_token_only=True)
+
+    def parameter_counts(self) -> dict[str, int]:
+        total = sum(p.numel() for p in self.parameters())
+        cfg = self.config
+        inactive = cfg.n_layers * (cfg.n_experts - cfg.top_k) * 3 * cfg.dim * cfg.expert_dim
+        return {"total": total, "active_per_token": total - inactive}

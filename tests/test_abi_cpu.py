@@ -1,0 +1,91 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+declared in include/parrot_hip.h, and rejects bad arguments with the
+documented negative status before any HIP call is made."""
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "parrot_hip.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(parrot_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from parrot import _abi
+    if not _abi.LIBRARY.exists():
+        pytest.fail("libparrot_hip.so is not built; run __graft_entry__.build()")
+    return _abi.load()
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared_functions()
+    assert "parrot_route_bf16" in names and "parrot_grouped_experts_bf16" in names
+    from parrot import _abi
+    assert names == sorted(_abi.SIGNATURES)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    from parrot import _abi
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _abi.SIGNATURES, f"{name} missing from the ctypes binding"
+
+
+def test_version_and_status_strings(lib):
+    assert lib.parrot_abi_version() == 1
+    assert lib.parrot_status_string(0) == b"ok"
+    for code in (-1, -2, -3, -4, -5):
+        assert lib.parrot_status_string(code) != b"unknown status"
+
+
+def test_capacity_matches_oracle(lib):
+    from oracle import routing
+    for tokens in (0, 1, 8, 64, 255, 256, 512, 4096, 10007):
+        for experts in (2, 8, 16, 32):
+            assert lib.parrot_capacity(tokens, experts) == routing.capacity(tokens, experts)
+
+
+def test_workspace_sizes(lib):
+    assert lib.parrot_route_workspace_bytes(512, 16) >= 8 * 16 * 4
+    small = lib.parrot_experts_workspace_bytes(8, 768, 512, 256)
+    big = lib.parrot_experts_workspace_bytes(512, 768, 512, 256)
+    assert big > small > 0
+    assert big >= 3 * 512 * 512 * 2 + 3 * 512 * 768 * 4
+
+
+def test_argument_validation_without_gpu(lib):
+    """Rejected before launch: no device is touched."""
+    from parrot import _abi
+    for name, (_, argtypes) in _abi.SIGNATURES.items():
+        assert len(argtypes) == len(getattr(lib, name).argtypes)
+    fake = 0x10000  # 16-byte aligned, never dereferenced on these paths
+    null = None
+    assert lib.parrot_rms_norm_bf16(null, fake, fake, 4, 64, 1e-6, null) == -1
+    assert lib.parrot_rms_norm_bf16(fake, fake, fake, 4, 66, 1e-6, null) == -2
+    assert lib.parrot_rms_norm_bf16(fake, fake, fake, 4, 8192, 1e-6, null) == -3
+    assert lib.parrot_rms_norm_bf16(fake + 2, fake, fake, 4, 64, 1e-6, null) == -5
+    srcs = (ctypes.c_void_p * 9)(*([fake] * 9))
+    assert lib.parrot_depth_mix_bf16(ctypes.cast(srcs, ctypes.c_void_p), 10, fake, fake, 1e-6,
+                                     fake, 1e-6, 4, 64, fake, null, null) == -3
+    assert lib.parrot_depth_mix_bf16(ctypes.cast(srcs, ctypes.c_void_p), 2, fake, fake, 1e-6,
+                                     null, 1e-6, 4, 64, null, null, null) == -1
+    ws = lib.parrot_route_workspace_bytes(64, 8)
+    args = [fake] * 9  # out_logits .. out_overflow
+    # experts outside 2..32
+    assert lib.parrot_route_bf16(fake, fake, null, 64, 64, 33, 32, *args, fake, ws, null) == -3
+    # dim not a multiple of 32
+    assert lib.parrot_route_bf16(fake, fake, null, 64, 48, 8, 32, *args, fake, ws, null) == -3
+    # workspace too small
+    assert lib.parrot_route_bf16(fake, fake, null, 64, 64, 8, 32, *args, fake, 0, null) == -4
+    # grouped experts: widths must be multiples of 64
+    assert lib.parrot_grouped_experts_bf16(
+        fake, 64, 96, 8, 128, 64, 32, *([fake] * 9), null, fake, fake, 1 << 30, null) == -3
+    assert lib.parrot_grouped_experts_bf16(
+        fake, 64, 64, 8, 128, 64, 32, *([fake] * 9), null, fake, fake, 16, null) == -4

@@ -1,0 +1,153 @@
+"""GPU parity of the bandwidth kernels and the grouped MoE layer.
+
+Tolerance: bf16 outputs within max-abs 2e-2 and
+mean-abs 2e-3 of the fp32 oracle evaluated on the same (bf16-valued)
+inputs and weights.  The RMSNorm / depth-mix kernels round once, so they are
+also held to one bf16 ulp of the oracle's value.
+"""
+import numpy as np
+import pytest
+import torch
+
+from moe_cases import error_stats, inputs, moe_module, oracle_moe, skew_bias
+from oracle import layers
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _ulp_ok(got: torch.Tensor, ref: torch.Tensor):
+    """|got - ref| <= 1 bf16 ulp of ref (+ tiny absolute slack)."""
+    ref = ref.float().cpu()
+    got = got.float().cpu()
+    ulp = torch.ldexp(torch.ones_like(ref), torch.frexp(ref)[1] - 8)
+    assert ((got - ref).abs() <= ulp + 1e-6).all(), float(((got - ref).abs() - ulp).max())
+
+
+class _Norm(torch.nn.Module):
+    def __init__(self, dim, eps=1e-6):
+        super().__init__()
+        self.weight = torch.nn.Parameter((torch.rand(dim) + 0.5))
+        self.eps = eps
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 768), (7, 768), (512, 768), (4097, 768), (33, 64),
+                                      (16, 2048), (5, 4096)])
+def test_rms_norm(rows, dim):
+    from parrot import hip_moe
+    _say(f"rms_norm rows={rows} dim={dim}")
+    norm = _Norm(dim).cuda().bfloat16()
+    x = (torch.randn(rows, dim) * 3).cuda().bfloat16()
+    with torch.no_grad():
+        got = hip_moe.rms_norm(norm, x)
+    ref = layers.rms_norm(x.float().cpu(), norm.weight.float().cpu(), 1e-6)
+    _ulp_ok(got, ref)
+
+
+class _Depth(torch.nn.Module):
+    def __init__(self, dim):
+        super().__init__()
+        self.query = torch.nn.Parameter(torch.randn(dim) * 0.5)
+        self.norm = _Norm(dim)
+
+
+@pytest.mark.parametrize("sources", [1, 2, 5, 9])
+@pytest.mark.parametrize("tokens,dim", [(1, 768), (16, 768), (512, 768), (100, 64), (3, 2048)])
+def test_depth_mix_and_norm(sources, tokens, dim):
+    from parrot import hip_moe
+    _say(f"depth_mix S={sources} T={tokens} dim={dim}")
+    torch.manual_seed(sources * 100 + tokens)
+    depth = _Depth(dim).cuda().bfloat16()
+    out_norm = _Norm(dim).cuda().bfloat16()
+    src = [(torch.randn(tokens, dim) * (1 + s)).cuda().bfloat16() for s in range(sources)]
+    with torch.no_grad():
+        mix = hip_moe.depth_mix(depth, src)
+        fused = hip_moe.depth_mix_norm(depth, src, out_norm)
+    cpu = [s.float().cpu() for s in src]
+    ref = layers.depth_mix(cpu, depth.query.float().cpu(), depth.norm.weight.float().cpu(), 1e-6)
+    _ulp_ok(mix, ref)
+    # fused: the norm consumes the bf16-rounded mix, exactly as unfused
+    ref_norm = layers.rms_norm(mix.float().cpu(), out_norm.weight.float().cpu(), 1e-6)
+    _ulp_ok(fused, ref_norm)
+
+
+MOE_CASES = [
+    ("C2", 256, 32, False),
+    ("C3", 4096, 32, True),
+    ("C4", 512, 16, False),
+    ("C5_b1", 1, 16, False),
+    ("C5_b2", 2, 16, False),
+    ("C5_b8", 8, 16, False),
+    ("odd", 130, 16, False),
+    ("large", 16384, 16, False),
+]
+
+
+@pytest.mark.parametrize("name,tokens,experts,skewed", MOE_CASES)
+def test_moe_layer(name, tokens, experts, skewed):
+    from parrot import hip_moe
+    _say(f"moe layer {name}: T={tokens} E={experts} skew={skewed}")
+    module = moe_module(experts, seed=1)
+    x = inputs(tokens, seed=1 + tokens)
+    bias = skew_bias(experts) if skewed else None
+    with torch.no_grad():
+        routed = hip_moe.route(module, x, False, logit_bias=bias)
+        out = hip_moe.grouped_hip_experts(module, x, routed.indices, routed.weights,
+                                          grouping=routed.grouping)
+    idx = routed.indices.cpu().numpy()
+    ref, ref_idx, _, _ = oracle_moe(module, x, logit_bias=None if bias is None else bias.numpy())
+    same = (ref_idx == idx).all(-1)
+    _say(f"  routing agreement {same.mean():.5f}; overflow "
+         f"{int(routed.grouping.offsets[-1])} of {2 * tokens}")
+    assert same.mean() >= 0.995
+    # Compare every token with the oracle evaluated on the HIP's routing.
+    ref_same, _, _, _ = oracle_moe(module, x, indices=idx, weights=routed.weights.cpu().numpy())
+    mx, mean = error_stats(out, ref_same)
+    _say(f"  max-abs {mx:.3e} mean-abs {mean:.3e}")
+    assert mx <= MAX_ABS and mean <= MEAN_ABS
+    mx2, mean2 = error_stats(out[torch.from_numpy(same).cuda()], ref[torch.from_numpy(same)])
+    assert mx2 <= MAX_ABS and mean2 <= MEAN_ABS
+
+
+def test_moe_addend_and_tiny_shapes():
+    from parrot import hip_moe
+    _say("moe addend + tiny widths")
+    module = moe_module(8, seed=4, dim=64, hidden=128, shared=64)
+    x = inputs(64, seed=4, dim=64)
+    addend = inputs(64, seed=5, dim=64)
+    with torch.no_grad():
+        routed = hip_moe.route(module, x, False)
+        out = hip_moe.grouped_hip_experts(module, x, routed.indices, routed.weights,
+                                          addend=addend, grouping=routed.grouping)
+        delta = hip_moe.grouped_hip_experts(module, x, routed.indices, routed.weights,
+                                            grouping=routed.grouping)
+    # identical rounding sequence to `addend + delta` in bf16
+    assert torch.equal(out, addend + delta)
+    ref, _, _, _ = oracle_moe(module, x, indices=routed.indices.cpu().numpy(),
+                              weights=routed.weights.cpu().numpy())
+    mx, mean = error_stats(delta, ref)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS
+
+
+def test_experts_from_external_indices():
+    """grouped_hip_experts without a HIP route (positions recomputed)."""
+    from parrot import hip_moe
+    _say("experts from external indices")
+    module = moe_module(16, seed=6)
+    x = inputs(300, seed=6)
+    rng = np.random.default_rng(6)
+    idx = np.stack([rng.choice(16, 2, replace=False) for _ in range(300)]).astype(np.int64)
+    idx[:200, 0] = 3  # heavy skew onto expert 3 -> overflow
+    idx[:200, 1] = np.where(idx[:200, 1] == 3, 4, idx[:200, 1])
+    w = rng.random((300, 2)).astype(np.float32)
+    with torch.no_grad():
+        out = hip_moe.grouped_hip_experts(module, x, torch.from_numpy(idx).cuda(),
+                                          torch.from_numpy(w).cuda())
+    ref, _, _, _ = oracle_moe(module, x, indices=idx, weights=w)
+    mx, mean = error_stats(out, ref)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS

@@ -1,0 +1,108 @@
+"""GPU parity: routing and grouping are bit-exact with the C oracle.
+
+Contract: given identical fp32 router logits, the top-2 indices, every
+per-expert slot permutation and the overflow assignment are bit-exact
+(route weights / probabilities within 1e-6).  The HIP projection's own
+logits are checked against fp32 and then run through the oracle's top-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+from moe_cases import inputs, moe_module, skew_bias
+from oracle import routing
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _assert_grouping_equal(g, ref):
+    np.testing.assert_array_equal(g.positions.cpu().numpy(), ref["positions"])
+    np.testing.assert_array_equal(g.counts.cpu().numpy(), ref["counts"])
+    np.testing.assert_array_equal(g.offsets.cpu().numpy(), ref["offsets"])
+    np.testing.assert_array_equal(g.perm.cpu().numpy(), ref["perm"])
+    n = int(ref["offsets"][-1])
+    np.testing.assert_array_equal(g.overflow.cpu().numpy()[:n], ref["overflow"])
+
+
+CASES = [(256, 32, False), (4096, 32, True), (512, 16, False), (1, 16, False), (3, 16, False),
+         (8, 16, False), (64, 8, False), (1000, 2, False), (130, 3, False), (777, 32, True),
+         (16384, 16, False)]
+
+
+@pytest.mark.parametrize("tokens,experts,skewed", CASES)
+def test_route_from_logits_bit_exact(tokens, experts, skewed):
+    from parrot import hip_moe
+    _say(f"route_from_logits T={tokens} E={experts} skew={skewed}")
+    rng = np.random.default_rng(tokens * 31 + experts)
+    logits = (rng.normal(size=(tokens, experts)) * 0.55).astype(np.float32)
+    logits[::13, 1] = logits[::13, 0]  # exact ties
+    bias = skew_bias(experts).numpy() if skewed else None
+    res = hip_moe.route_from_logits(torch.from_numpy(logits).cuda(),
+                                    None if bias is None else torch.from_numpy(bias),
+                                    collect_stats=True)
+    idx, w, probs = routing.top2(logits, bias, want_probs=True)
+    np.testing.assert_array_equal(res.indices.cpu().numpy(), idx)
+    np.testing.assert_allclose(res.weights.cpu().numpy(), w, atol=1e-6, rtol=0)
+    np.testing.assert_allclose(res.probabilities.cpu().numpy(), probs, atol=1e-6, rtol=0)
+    ref = routing.group(idx, experts)
+    assert res.grouping.capacity == ref["capacity"]
+    _assert_grouping_equal(res.grouping, ref)
+    if skewed:
+        _say(f"  overflow assignments: {int(ref['offsets'][-1])} of {2 * tokens}")
+
+
+@pytest.mark.parametrize("tokens,experts,skewed", [(256, 32, False), (4096, 32, True),
+                                                   (512, 16, False), (5, 16, False)])
+def test_route_projection(tokens, experts, skewed):
+    """HIP logits ~ fp32 logits; HIP top-2 == oracle top-2 of the HIP logits."""
+    from parrot import hip_moe
+    _say(f"route projection T={tokens} E={experts} skew={skewed}")
+    module = moe_module(experts, seed=1)
+    x = inputs(tokens, seed=1)
+    bias = skew_bias(experts) if skewed else None
+    with torch.no_grad():
+        res = hip_moe.route(module, x, collect_stats=True, logit_bias=bias, return_logits=True)
+    got_logits = res.logits.cpu().numpy()
+    ref_logits = (x.float().cpu() @ module.router.weight.float().cpu().T).numpy()
+    if bias is not None:
+        ref_logits = ref_logits + bias.numpy()
+    assert np.abs(got_logits - ref_logits).max() < 1e-4
+    idx, w, _ = routing.top2(got_logits)
+    np.testing.assert_array_equal(res.indices.cpu().numpy(), idx)
+    np.testing.assert_allclose(res.weights.cpu().numpy(), w, atol=1e-6)
+    _assert_grouping_equal(res.grouping, routing.group(idx, experts))
+    # With the fp32 oracle's own logits, routing agrees except at near-ties.
+    ref_idx, _, _ = routing.top2(ref_logits)
+    mismatch = (ref_idx != idx).any(-1).mean()
+    assert mismatch <= 0.002, mismatch
+
+
+def test_group_indices_adversarial():
+    from parrot import hip_moe
+    cases = {
+        "one_expert": np.stack([np.zeros(3000), np.arange(3000) % 15 + 1], 1),
+        "round_robin": np.stack([np.arange(512) % 16, (np.arange(512) + 1) % 16], 1),
+        "two_experts": np.stack([np.zeros(700), np.ones(700)], 1),
+    }
+    for name, idx in cases.items():
+        _say(f"group_indices {name}")
+        idx = idx.astype(np.int64)
+        g = hip_moe.group_indices(torch.from_numpy(idx).cuda(), 16)
+        _assert_grouping_equal(g, routing.group(idx, 16))
+
+
+def test_routing_is_deterministic():
+    from parrot import hip_moe
+    _say("routing determinism")
+    module = moe_module(32, seed=1)
+    x = inputs(4096, seed=3)
+    with torch.no_grad():
+        a = hip_moe.route(module, x, False, logit_bias=skew_bias(32))
+        b = hip_moe.route(module, x, False, logit_bias=skew_bias(32))
+    for name in ("positions", "counts", "offsets", "perm", "overflow"):
+        assert torch.equal(getattr(a.grouping, name), getattr(b.grouping, name)), name
+    assert torch.equal(a.indices, b.indices) and torch.equal(a.weights, b.weights)

@@ -1,0 +1,117 @@
+"""Host-side behaviour of the model API: configuration validation, loud
+failure of the HIP backend off-GPU, and the reference's error paths."""
+import pytest
+import torch
+
+from conftest import tiny_model_config
+
+
+def test_defaults_match_reference_config():
+    from parrot import ModelConfig
+    c = ModelConfig()
+    assert (c.dim, c.n_layers, c.n_experts, c.expert_dim, c.shared_expert_dim) == (768, 16, 16, 512, 256)
+    assert (c.window_size, c.max_seq_len, c.kv_latent_dim, c.head_dim) == (2048, 4096, 128, 96)
+    assert c.depth_sources == 9
+
+
+@pytest.mark.parametrize("backend", ["grouped_mps", "metal", "dense_mps", "training_mps",
+                                     "training_cuda", "bogus"])
+def test_foreign_moe_backends_rejected(backend):
+    from parrot import ModelConfig
+    with pytest.raises(ValueError):
+        ModelConfig(moe_backend=backend)
+
+
+def test_hip_config_constraints():
+    from parrot import ModelConfig
+    ModelConfig(moe_backend="grouped_hip", depth_backend="hip", n_experts=32)
+    with pytest.raises(ValueError):
+        ModelConfig(moe_backend="grouped_hip", n_experts=33)
+    with pytest.raises(ValueError):
+        ModelConfig(moe_backend="grouped_hip", top_k=3)
+    with pytest.raises(ValueError):
+        ModelConfig(moe_backend="grouped_hip", expert_dim=500)
+    with pytest.raises(ValueError):
+        ModelConfig(depth_backend="hip", n_layers=20)  # 11 depth sources
+    with pytest.raises(ValueError):
+        ModelConfig(depth_backend="metal")
+
+
+def test_parameter_counts_match_reference_numbers():
+    """README.md:174-175 and benchmark_cuda_h200_32experts_results.json:28."""
+    from parrot import ModelConfig, Parrot
+    with torch.device("meta"):
+        m16 = Parrot(ModelConfig())
+        m32 = Parrot(ModelConfig(n_experts=32))
+    assert m16.parameter_counts() == {"total": 360458496, "active_per_token": 96217344}
+    assert m32.parameter_counts() == {"total": 662644992, "active_per_token": 96413952}
+
+
+def test_hip_backend_fails_loudly_on_cpu():
+    """No silent CPU fallback: the HIP backends raise for CPU tensors."""
+    from parrot import Parrot
+    torch.manual_seed(0)
+    model = Parrot(tiny_model_config(moe_backend="grouped_hip", depth_backend="hip",
+                                     collect_router_stats=False)).eval()
+    ids = torch.randint(0, 32768, (1, 16))
+    with torch.no_grad(), pytest.raises(RuntimeError):
+        model(ids)
+    moe_only = Parrot(tiny_model_config(moe_backend="grouped_hip")).eval()
+    with torch.no_grad(), pytest.raises(RuntimeError):
+        moe_only(ids)
+
+
+def test_generation_error_paths():
+    from parrot import Parrot
+    torch.manual_seed(0)
+    model = Parrot(tiny_model_config())
+    ids = torch.randint(0, 32768, (1, 8))
+    with pytest.raises(RuntimeError):
+        model.prefill(ids)  # training mode
+    model.eval()
+    with pytest.raises(ValueError):
+        model.prefill(torch.randint(0, 32768, (1, 200)))  # > max_seq_len
+    logits, state = model.prefill(ids)
+    with pytest.raises(ValueError):
+        model.decode_step(torch.zeros(2, 1, dtype=torch.long), state)
+    state.layers[0], state.layers[3] = state.layers[3], state.layers[0]
+    with pytest.raises(ValueError):
+        model.decode_step(torch.zeros(1, 1, dtype=torch.long), state)
+    state.position = 128
+    with pytest.raises(ValueError):
+        model.decode_step(torch.zeros(1, 1, dtype=torch.long), state)
+
+
+def test_forward_input_validation():
+    from parrot import Parrot
+    model = Parrot(tiny_model_config()).eval()
+    with pytest.raises(ValueError):
+        model(torch.zeros(4, dtype=torch.long))
+    with pytest.raises(ValueError):
+        model(torch.zeros(1, 9, dtype=torch.long), bag_size=2)
+    with pytest.raises(ValueError):
+        model(torch.zeros(1, 8, dtype=torch.long), supervised_logits_only=True)
+
+
+def test_bag_and_supervised_loss_path():
+    """bag_size > 1 and supervised_logits_only run on the pytorch backend."""
+    from parrot import Parrot
+    torch.manual_seed(3)
+    model = Parrot(tiny_model_config())
+    ids = torch.randint(0, 32768, (2, 16))
+    out = model(ids, labels=ids, bag_size=4, supervised_logits_only=True)
+    assert out.logits.shape == (2, 3, 32768)
+    out.loss.backward()
+    assert model.blocks[0].moe.router.weight.grad is not None
+
+
+def test_checkpoint_modules_same_loss():
+    from parrot import Parrot
+    torch.manual_seed(4)
+    a = Parrot(tiny_model_config())
+    b = Parrot(tiny_model_config(checkpoint_modules=True))
+    b.load_state_dict(a.state_dict())
+    ids = torch.randint(0, 32768, (1, 16))
+    la = a(ids, labels=ids).loss
+    lb = b(ids, labels=ids).loss
+    torch.testing.assert_close(la, lb)
