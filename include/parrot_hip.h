@@ -70,6 +70,22 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
                           const void* out_norm_weight, float out_eps, int64_t tokens,
                           int32_t dim, void* out_mix, void* out_norm, void* stream);
 
+/* Rotary embedding of the local-attention heads fused with the head-major
+ * split of one packed projection qkv [batch * seq, (H + 2 Hk) * head_dim]
+ * (bf16, row-major, columns q | k | v):
+ *   q [batch, H, seq, head_dim]; k, v [batch, Hk, seq, head_dim], or
+ *   [batch, H, seq, head_dim] with every kv head repeated H / Hk times when
+ *   expand_kv != 0.
+ * Pairs (2i, 2i+1) of q and k rotate by angle (start + s) * theta^(-2i/d)
+ * read from fp32 tables cos_table / sin_table [max_positions, head_dim / 2];
+ * v is copied.  head_dim % 4 == 0, H % Hk == 0, start + seq <= max_positions.
+ * Replaces LocalGQA._project / _project_decode / _rope
+ * (parrot/model.py:206-262), which run RoPE as strided bf16 elementwise ops. */
+int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* sin_table,
+                         int64_t batch, int32_t seq, int32_t start, int32_t max_positions,
+                         int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t expand_kv,
+                         void* q, void* k, void* v, void* stream);
+
 /* Workspace bytes for the routing / grouping entry points. */
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts);
 

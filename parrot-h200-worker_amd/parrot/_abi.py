@@ -29,6 +29,9 @@ SIGNATURES: dict[str, tuple] = {
     "parrot_rms_norm_bf16": (ctypes.c_int, [_p, _p, _p, _i64, _i32, _f32, _p]),
     "parrot_depth_mix_bf16": (
         ctypes.c_int, [_p, _i32, _p, _p, _f32, _p, _f32, _i64, _i32, _p, _p, _p]),
+    "parrot_rope_qkv_bf16": (
+        ctypes.c_int,
+        [_p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),
     "parrot_route_workspace_bytes": (_sz, [_i64, _i32]),
     "parrot_route_bf16": (
         ctypes.c_int,

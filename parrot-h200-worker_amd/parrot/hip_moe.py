@@ -290,6 +290,32 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
 
 
 # ---------------------------------------------------------------------------
+# RoPE for the local attention layers
+# ---------------------------------------------------------------------------
+
+def rope_qkv(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, kv_heads: int, head_dim: int,
+             start: int, expand_kv: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """Split a packed q|k|v projection [b, t, (H + 2 Hk) d] into head-major
+    q [b, H, t, d], k, v [b, Hk or H, t, d] and rotate q and k by RoPE at
+    positions start .. start + t - 1 (fp32 tables [max_positions, d / 2])."""
+    _require(qkv, "HIP RoPE")
+    b, t, width = qkv.shape
+    if width != (heads + 2 * kv_heads) * head_dim:
+        raise RuntimeError("packed q|k|v width does not match the head layout")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise RuntimeError("RoPE tables must be fp32")
+    qkv = qkv.contiguous()
+    kv_out = heads if expand_kv else kv_heads
+    q = qkv.new_empty((b, heads, t, head_dim))
+    k = qkv.new_empty((b, kv_out, t, head_dim))
+    v = qkv.new_empty((b, kv_out, t, head_dim))
+    _abi.check(_abi.load().parrot_rope_qkv_bf16(
+        ptr(qkv), ptr(cos), ptr(sin), b, t, start, cos.shape[0], heads, kv_heads, head_dim,
+        int(expand_kv), ptr(q), ptr(k), ptr(v), _stream(qkv.device)), "parrot_rope_qkv_bf16")
+    return q, k, v
+
+
+# ---------------------------------------------------------------------------
 # RMSNorm and Block AttnRes (cf. parrot/metal_moe.py:37-55, 419-477)
 # ---------------------------------------------------------------------------
 

@@ -133,6 +133,24 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
       static_cast<uint16_t*>(out_mix), static_cast<uint16_t*>(out_norm), as_stream(stream)));
 }
 
+int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* sin_table,
+                         int64_t batch, int32_t seq, int32_t start, int32_t max_positions,
+                         int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t expand_kv,
+                         void* q, void* k, void* v, void* stream) {
+  if (!qkv || !cos_table || !sin_table || !q || !k || !v) return PARROT_ERR_NULL_POINTER;
+  if (batch < 0 || seq < 0 || start < 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0)
+    return PARROT_ERR_BAD_SHAPE;
+  if (heads % kv_heads || head_dim % 4) return PARROT_ERR_UNSUPPORTED;
+  if (static_cast<int64_t>(start) + seq > max_positions) return PARROT_ERR_BAD_SHAPE;
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(q) |
+                         reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v);
+  if (bits & 7u) return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_rope_qkv(
+      static_cast<const uint16_t*>(qkv), cos_table, sin_table, batch, seq, start, heads,
+      kv_heads, head_dim, expand_kv, static_cast<uint16_t*>(q), static_cast<uint16_t*>(k),
+      static_cast<uint16_t*>(v), as_stream(stream)));
+}
+
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts) {
   if (tokens < 0 || experts <= 0) return 0;
   return route_ws_bytes(tokens, experts);

@@ -13,8 +13,8 @@ namespace parrot {
 constexpr int kWave = 64;
 constexpr int kMaxExperts = 32;
 constexpr int kMaxDepthSources = 9;
-// Assignments (token, k) handled by one route workgroup: 64 tokens x top-2.
-constexpr int kRouteTokensPerBlock = 64;
+// Assignments (token, k) handled by one route workgroup: 16 tokens x top-2.
+constexpr int kRouteTokensPerBlock = 16;
 constexpr int kRouteAssignPerBlock = 2 * kRouteTokensPerBlock;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -40,11 +40,26 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Butterfly sum over the 64 lanes of a wavefront; every lane gets the total.
+// DPP lane exchange inside rows of 16 lanes (VALU latency, no LDS trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wavefront, returned to every lane.  Within each
+// row of 16 lanes: quad_perm [1,0,3,2] and [2,3,0,1] (xor 1, xor 2), then
+// row_half_mirror and row_mirror fold the quads and half-rows; the four row
+// totals are then read from lanes 0, 16, 32, 48 and added in that order.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+  v += dpp<0xb1>(v);
+  v += dpp<0x4e>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return ((r0 + r1) + r2) + r3;
 }
 
 // silu(g) * u with silu(g) = g / (1 + e^-g), evaluated in fp32.
@@ -122,6 +137,12 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
                               int experts, int hidden_dim, int shared_dim, int capacity,
                               const GroupMap& map, const ExpertWeights& w, uint16_t* hidden,
                               float* y_routed, float* y_shared, hipStream_t s);
+
+// RoPE + head-major split of a packed q|k|v projection (see rope.hip).
+hipError_t launch_rope_qkv(const uint16_t* qkv, const float* cos_t, const float* sin_t,
+                           int64_t batch, int seq, int start, int heads, int kv_heads,
+                           int head_dim, int expand_kv, uint16_t* q, uint16_t* k,
+                           uint16_t* v, hipStream_t s);
 
 hipError_t launch_combine(const float* y_routed, const float* y_shared,
                           const uint16_t* addend, int64_t tokens, int dim,

@@ -49,14 +49,31 @@ struct GemmArgs {
   float* y_shared;            // phase 2 output [T, dim]
 };
 
+// Raw buffer loads: the per-lane byte offset is fixed for the whole k loop
+// and the stage offset travels in an SGPR, so the loop carries no 64-bit
+// address arithmetic; reads past `bytes` return zero instead of faulting.
+constexpr int kBufferWord3 = 0x00020000;  // gfx9-family buffer resource word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferWord3);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
+                                               uint32_t soffset) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+}
+
 template <int BM>
 struct WaveLayout {
   static constexpr int kWavesM = BM >= 64 ? 2 : 1;
   static constexpr int kWavesN = 4 / kWavesM;
 };
 
+// Occupancy is bounded by LDS (two workgroups per CU), so let each wave
+// use up to 256 VGPRs rather than squeezing registers for occupancy.
 template <int BM, int BN, int PHASE>
-__global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void grouped_gemm_kernel(GemmArgs p) {
   constexpr int kWavesM = WaveLayout<BM>::kWavesM;
   constexpr int kWavesN = WaveLayout<BM>::kWavesN;
   constexpr int kWaveM = BM / kWavesM;
@@ -133,49 +150,57 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
 
   // Thread -> 16-byte vector of a stage: vector v = tid + 256 i covers row
   // v / 8, k-columns 8 (v % 8) .. +8, so 8 neighbouring threads read one
-  // 128-byte row segment.
+  // 128-byte row segment.  Threads beyond the A stage (BM = 16) load a
+  // duplicate vector so every load is unconditional; only the owning threads
+  // store it to LDS.
   const int a_ld = PHASE == 1 ? p.dim : p.hstride;
+  const int64_t a_rows = PHASE == 1 ? p.tokens : 3 * p.tokens;
+  const __amdgpu_buffer_rsrc_t a_rsrc =
+      make_rsrc(p.a_src, static_cast<uint32_t>(a_rows * a_ld * 2));
   const uint16_t* wbase = shared ? p.w_shared
                                  : p.w_routed + static_cast<int64_t>(seg) * N * K;
-  const uint16_t* a_ptr0 = p.a_src + static_cast<int64_t>(row_src[(tid < kAVec ? tid : 0) >> 3]) * a_ld + (tid & 7) * 8;
-  const uint16_t* a_ptr1 = p.a_src + static_cast<int64_t>(row_src[((tid + 256) < kAVec ? tid + 256 : 0) >> 3]) * a_ld + (tid & 7) * 8;
-  const uint16_t* a_ptr2 = p.a_src + static_cast<int64_t>(row_src[((tid + 512) < kAVec ? tid + 512 : 0) >> 3]) * a_ld + (tid & 7) * 8;
-  const uint16_t* a_ptr3 = p.a_src + static_cast<int64_t>(row_src[((tid + 768) < kAVec ? tid + 768 : 0) >> 3]) * a_ld + (tid & 7) * 8;
-  const int64_t b_step = static_cast<int64_t>(32) * K;  // 32 rows further per extra vector
-  const uint16_t* b_ptr = wbase + static_cast<int64_t>(min(n0 + (tid >> 3), N - 1)) * K + (tid & 7) * 8;
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_rsrc(wbase, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
+  const uint32_t col_bytes = (tid & 7) * 16;
+  const uint32_t a_off0 = row_src[(tid % kAVec) >> 3] * a_ld * 2 + col_bytes;
+  const uint32_t a_off1 = row_src[((tid + 256) % kAVec) >> 3] * a_ld * 2 + col_bytes;
+  const uint32_t a_off2 = row_src[((tid + 512) % kAVec) >> 3] * a_ld * 2 + col_bytes;
+  const uint32_t a_off3 = row_src[((tid + 768) % kAVec) >> 3] * a_ld * 2 + col_bytes;
+  // B rows past N (a partial N tile) lie past the buffer end and read zero.
+  const uint32_t b_off0 = static_cast<uint32_t>(n0 + (tid >> 3)) * K * 2 + col_bytes;
+  const uint32_t b_step = 32u * K * 2;  // 32 rows further per extra vector
   const int b_row0 = tid >> 3;
   const int col8 = (tid & 7) * 8;
 
   static_assert(kBPer <= 4, "B stage holds at most 4 vectors per thread");
-  uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
-#define PARROT_LOAD_STAGE(kt)                                                              \
-  do {                                                                                     \
-    const int ko = (kt) * kBK;                                                             \
-    if (tid < kAVec) ra0 = *reinterpret_cast<const uint4*>(a_ptr0 + ko);                   \
-    if (kAPer > 1 && tid + 256 < kAVec) ra1 = *reinterpret_cast<const uint4*>(a_ptr1 + ko);\
-    if (kAPer > 2 && tid + 512 < kAVec) ra2 = *reinterpret_cast<const uint4*>(a_ptr2 + ko);\
-    if (kAPer > 3 && tid + 768 < kAVec) ra3 = *reinterpret_cast<const uint4*>(a_ptr3 + ko);\
-    rb0 = *reinterpret_cast<const uint4*>(b_ptr + ko);                                     \
-    if (kBPer > 1) rb1 = *reinterpret_cast<const uint4*>(                                  \
-        (n0 + b_row0 + 32 < N ? b_ptr + b_step : b_ptr) + ko);                             \
-    if (kBPer > 2) rb2 = *reinterpret_cast<const uint4*>(                                  \
-        (n0 + b_row0 + 64 < N ? b_ptr + 2 * b_step : b_ptr) + ko);                         \
-    if (kBPer > 3) rb3 = *reinterpret_cast<const uint4*>(                                  \
-        (n0 + b_row0 + 96 < N ? b_ptr + 3 * b_step : b_ptr) + ko);                         \
+  // Two register stages (P, Q) of global loads are in flight while the
+  // MFMAs consume the current LDS stage; LDS is double-buffered, one
+  // barrier per 64-wide k step.
+  uint4 pa0, pa1, pa2, pa3, pb0, pb1, pb2, pb3;
+  uint4 qa0, qa1, qa2, qa3, qb0, qb1, qb2, qb3;
+#define PARROT_LOAD_STAGE(R, kt)                                                            \
+  do {                                                                                      \
+    const uint32_t ko = static_cast<uint32_t>(kt) * (kBK * 2);                              \
+    R##a0 = buffer_load16(a_rsrc, a_off0, ko);                                              \
+    if (kAPer > 1) R##a1 = buffer_load16(a_rsrc, a_off1, ko);                               \
+    if (kAPer > 2) R##a2 = buffer_load16(a_rsrc, a_off2, ko);                               \
+    if (kAPer > 3) R##a3 = buffer_load16(a_rsrc, a_off3, ko);                               \
+    R##b0 = buffer_load16(b_rsrc, b_off0, ko);                                              \
+    if (kBPer > 1) R##b1 = buffer_load16(b_rsrc, b_off0 + b_step, ko);                      \
+    if (kBPer > 2) R##b2 = buffer_load16(b_rsrc, b_off0 + 2 * b_step, ko);                  \
+    if (kBPer > 3) R##b3 = buffer_load16(b_rsrc, b_off0 + 3 * b_step, ko);                  \
   } while (0)
-#define PARROT_STORE_STAGE(buf)                                                            \
-  do {                                                                                     \
-    if (tid < kAVec) *reinterpret_cast<uint4*>(&a_lds[buf][tid >> 3][col8]) = ra0;         \
-    if (kAPer > 1 && tid + 256 < kAVec)                                                    \
-      *reinterpret_cast<uint4*>(&a_lds[buf][(tid + 256) >> 3][col8]) = ra1;                \
-    if (kAPer > 2 && tid + 512 < kAVec)                                                    \
-      *reinterpret_cast<uint4*>(&a_lds[buf][(tid + 512) >> 3][col8]) = ra2;                \
-    if (kAPer > 3 && tid + 768 < kAVec)                                                    \
-      *reinterpret_cast<uint4*>(&a_lds[buf][(tid + 768) >> 3][col8]) = ra3;                \
-    *reinterpret_cast<uint4*>(&b_lds[buf][b_row0][col8]) = rb0;                            \
-    if (kBPer > 1) *reinterpret_cast<uint4*>(&b_lds[buf][b_row0 + 32][col8]) = rb1;        \
-    if (kBPer > 2) *reinterpret_cast<uint4*>(&b_lds[buf][b_row0 + 64][col8]) = rb2;        \
-    if (kBPer > 3) *reinterpret_cast<uint4*>(&b_lds[buf][b_row0 + 96][col8]) = rb3;        \
+#define PARROT_STORE_STAGE(R, buf)                                                          \
+  do {                                                                                      \
+    if (kAVec >= 256 || tid < kAVec)                                                        \
+      *reinterpret_cast<uint4*>(&a_lds[buf][(tid % kAVec) >> 3][col8]) = R##a0;             \
+    if (kAPer > 1) *reinterpret_cast<uint4*>(&a_lds[buf][(tid + 256) >> 3][col8]) = R##a1;  \
+    if (kAPer > 2) *reinterpret_cast<uint4*>(&a_lds[buf][(tid + 512) >> 3][col8]) = R##a2;  \
+    if (kAPer > 3) *reinterpret_cast<uint4*>(&a_lds[buf][(tid + 768) >> 3][col8]) = R##a3;  \
+    *reinterpret_cast<uint4*>(&b_lds[buf][b_row0][col8]) = R##b0;                           \
+    if (kBPer > 1) *reinterpret_cast<uint4*>(&b_lds[buf][b_row0 + 32][col8]) = R##b1;       \
+    if (kBPer > 2) *reinterpret_cast<uint4*>(&b_lds[buf][b_row0 + 64][col8]) = R##b2;       \
+    if (kBPer > 3) *reinterpret_cast<uint4*>(&b_lds[buf][b_row0 + 96][col8]) = R##b3;       \
   } while (0)
 
   const int wm0 = (wave / kWavesN) * kWaveM;
@@ -186,35 +211,48 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < kTilesN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+#define PARROT_COMPUTE(buf)                                                                 \
+  do {                                                                                      \
+    _Pragma("unroll") for (int kk = 0; kk < kBK / 32; ++kk) {                               \
+      bf16x8 af[kTilesM], bfr[kTilesN];                                                     \
+      _Pragma("unroll") for (int i = 0; i < kTilesM; ++i)                                   \
+        af[i] = *reinterpret_cast<const bf16x8*>(                                           \
+            &a_lds[buf][wm0 + i * 16 + (lane & 15)][kk * 32 + (lane >> 4) * 8]);            \
+      _Pragma("unroll") for (int j = 0; j < kTilesN; ++j)                                   \
+        bfr[j] = *reinterpret_cast<const bf16x8*>(                                          \
+            &b_lds[buf][wn0 + j * 16 + (lane & 15)][kk * 32 + (lane >> 4) * 8]);            \
+      _Pragma("unroll") for (int i = 0; i < kTilesM; ++i)                                   \
+        _Pragma("unroll") for (int j = 0; j < kTilesN; ++j)                                 \
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0); \
+    }                                                                                       \
+  } while (0)
+
+  // Every load is issued unconditionally (stage index clamped to the last
+  // stage) so the compiler can wait for exactly the stage being stored
+  // while the next one stays in flight.
   const int KT = K / kBK;
-  PARROT_LOAD_STAGE(0);
-  PARROT_STORE_STAGE(0);
+  PARROT_LOAD_STAGE(p, 0);
+  PARROT_LOAD_STAGE(q, min(1, KT - 1));
+  PARROT_STORE_STAGE(p, 0);
   __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) PARROT_LOAD_STAGE(kt + 1);
-#pragma unroll
-    for (int kk = 0; kk < kBK / 32; ++kk) {
-      bf16x8 af[kTilesM], bfr[kTilesN];
-#pragma unroll
-      for (int i = 0; i < kTilesM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(
-            &a_lds[buf][wm0 + i * 16 + (lane & 15)][kk * 32 + (lane >> 4) * 8]);
-#pragma unroll
-      for (int j = 0; j < kTilesN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8*>(
-            &b_lds[buf][wn0 + j * 16 + (lane & 15)][kk * 32 + (lane >> 4) * 8]);
-#pragma unroll
-      for (int i = 0; i < kTilesM; ++i)
-#pragma unroll
-        for (int j = 0; j < kTilesN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < KT) PARROT_STORE_STAGE(buf ^ 1);
+  for (int kt = 0; kt < KT; kt += 2) {
+    // even step: LDS buffer 0 holds stage kt, registers q hold stage kt + 1
+    PARROT_LOAD_STAGE(p, min(kt + 2, KT - 1));
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+    PARROT_COMPUTE(0);
+    PARROT_STORE_STAGE(q, 1);
+    __syncthreads();
+    if (kt + 1 >= KT) break;
+    // odd step: LDS buffer 1 holds stage kt + 1, registers p hold stage kt + 2
+    PARROT_LOAD_STAGE(q, min(kt + 3, KT - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    PARROT_COMPUTE(1);
+    PARROT_STORE_STAGE(p, 0);
     __syncthreads();
   }
 #undef PARROT_LOAD_STAGE
 #undef PARROT_STORE_STAGE
+#undef PARROT_COMPUTE
 
   // ---- epilogue --------------------------------------------------------------
   // C fragment: lane holds column (lane & 15) of rows 4 * (lane >> 4) + r.

@@ -1,7 +1,9 @@
 // RMSNorm and Block AttnRes depth mixing: HBM-bound row kernels.
 //
-// One 64-lane wavefront owns one row; lanes stride over 4-element (8-byte)
-// chunks so a wavefront instruction moves 512 contiguous bytes.  Sums are
+// One 64-lane wavefront (one workgroup) owns one row, so small token counts
+// still spread over every CU; lanes stride over 4-element (8-byte) chunks so
+// a wavefront instruction moves 512 contiguous bytes, and every load of a
+// row is issued before the first reduction.  Sums are
 // fp32 butterfly reductions; every output is rounded to bf16 exactly once,
 // at the same point as the reference (parrot/model.py:125-127 for RMSNorm,
 // :149-155 for the depth mix, parrot/kernels/moe_bf16.metal:414-433 for the
@@ -12,11 +14,11 @@ namespace parrot {
 
 namespace {
 
-constexpr int kRowsPerBlock = 4;  // one row per wavefront, 256 threads
+constexpr int kRowsPerBlock = 1;  // one row per 64-lane workgroup
 
 // y = bf16((x * rsqrt(mean(x^2) + eps)) * w)        (parrot/model.py:125-127)
 template <int MAXC>
-__global__ __launch_bounds__(256) void rms_norm_kernel(
+__global__ __launch_bounds__(64) void rms_norm_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     uint16_t* __restrict__ out, int64_t rows, int dim, float eps) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -53,15 +55,19 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(
 
 // Block AttnRes: score_s = <rmsnorm_w(v_s), q>, alpha = softmax_s(score),
 // mix = bf16(sum_s alpha_s v_s); optionally y = rmsnorm_out(mix).
+// Every source row is loaded up front (all loads in flight together), parked
+// in LDS, and the per-source work then runs as compact runtime loops.
 template <int MAXC>
-__global__ __launch_bounds__(256) void depth_mix_kernel(
+__global__ __launch_bounds__(64) void depth_mix_kernel(
     DepthSources srcs, int n_sources, const uint16_t* __restrict__ query,
     const uint16_t* __restrict__ score_w, float score_eps,
     const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
     uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm) {
+  __shared__ uint2 stage[kMaxDepthSources][MAXC][kWave];
+  __shared__ float score_s[kMaxDepthSources];
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t tok = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (tok >= tokens) return;  // uniform per wavefront
+  const int64_t tok = blockIdx.x;
+  if (tok >= tokens) return;
   const int chunks = dim >> 2;
   const int64_t base = tok * (dim >> 2);
 
@@ -82,58 +88,74 @@ __global__ __launch_bounds__(256) void depth_mix_kernel(
     }
   }
 
-  uint2 v[kMaxDepthSources][MAXC];
-  float score[kMaxDepthSources];
+  // Per-lane partial sums of every source, then all 2S wavefront reductions
+  // back to back so their latencies overlap.
+  float ss[kMaxDepthSources], dq[kMaxDepthSources];
+  {
+    uint2 v[kMaxDepthSources][MAXC];
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) {
-    score[s] = -INFINITY;
-    if (s < n_sources) {
-      const uint2* src = reinterpret_cast<const uint2*>(srcs.src[s]) + base;
-      float ss = 0.0f, dq = 0.0f;
+    for (int s = 0; s < kMaxDepthSources; ++s) {
+      if (s < n_sources) {
+        const uint2* src = reinterpret_cast<const uint2*>(srcs.src[s]) + base;
 #pragma unroll
-      for (int c = 0; c < MAXC; ++c) {
-        const int i = lane + c * kWave;
-        v[s][c] = i < chunks ? src[i] : make_uint2(0u, 0u);
-        const float e0 = lo_bf16(v[s][c].x), e1 = hi_bf16(v[s][c].x);
-        const float e2 = lo_bf16(v[s][c].y), e3 = hi_bf16(v[s][c].y);
-        ss += e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3;
-        dq += e0 * wq[c][0] + e1 * wq[c][1] + e2 * wq[c][2] + e3 * wq[c][3];
+        for (int c = 0; c < MAXC; ++c) {
+          const int i = lane + c * kWave;
+          v[s][c] = i < chunks ? src[i] : make_uint2(0u, 0u);
+        }
       }
-      ss = wave_sum(ss);
-      dq = wave_sum(dq);
-      score[s] = dq * rsqrtf(ss / static_cast<float>(dim) + score_eps);
+    }
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s) {
+      ss[s] = 0.0f;
+      dq[s] = 0.0f;
+      if (s < n_sources) {
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+          stage[s][c][lane] = v[s][c];
+          const float e0 = lo_bf16(v[s][c].x), e1 = hi_bf16(v[s][c].x);
+          const float e2 = lo_bf16(v[s][c].y), e3 = hi_bf16(v[s][c].y);
+          ss[s] += e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3;
+          dq[s] += e0 * wq[c][0] + e1 * wq[c][1] + e2 * wq[c][2] + e3 * wq[c][3];
+        }
+      }
     }
   }
-  float mx = score[0];
-#pragma unroll
-  for (int s = 1; s < kMaxDepthSources; ++s)
-    if (s < n_sources) mx = fmaxf(mx, score[s]);
-  float alpha[kMaxDepthSources];
-  float denom = 0.0f;
+  float mx = -INFINITY;
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) {
-    alpha[s] = s < n_sources ? __expf(score[s] - mx) : 0.0f;
-    denom += alpha[s];
+    if (s < n_sources) {
+      const float score = wave_sum(dq[s]) * rsqrtf(wave_sum(ss[s]) / static_cast<float>(dim) + score_eps);
+      if (lane == 0) score_s[s] = score;
+      mx = fmaxf(mx, score);
+    }
   }
+  __syncthreads();
+  float denom = 0.0f;
+#pragma unroll 1
+  for (int s = 0; s < n_sources; ++s) denom += __expf(score_s[s] - mx);
   const float inv = 1.0f / denom;
 
+  float acc[MAXC][4];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) acc[c][0] = acc[c][1] = acc[c][2] = acc[c][3] = 0.0f;
+#pragma unroll 1
+  for (int s = 0; s < n_sources; ++s) {
+    const float a = __expf(score_s[s] - mx) * inv;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const uint2 x = stage[s][c][lane];
+      acc[c][0] += a * lo_bf16(x.x);
+      acc[c][1] += a * hi_bf16(x.x);
+      acc[c][2] += a * lo_bf16(x.y);
+      acc[c][3] += a * hi_bf16(x.y);
+    }
+  }
   uint2 mixed[MAXC];
   float ss_out = 0.0f;
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
-    float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
-#pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s) {
-      if (s < n_sources) {
-        const float a = alpha[s] * inv;
-        m0 += a * lo_bf16(v[s][c].x);
-        m1 += a * hi_bf16(v[s][c].x);
-        m2 += a * lo_bf16(v[s][c].y);
-        m3 += a * hi_bf16(v[s][c].y);
-      }
-    }
-    mixed[c].x = pack_bf16x2(m0, m1);
-    mixed[c].y = pack_bf16x2(m2, m3);
+    mixed[c].x = pack_bf16x2(acc[c][0], acc[c][1]);
+    mixed[c].y = pack_bf16x2(acc[c][2], acc[c][3]);
     const float r0 = lo_bf16(mixed[c].x), r1 = hi_bf16(mixed[c].x);
     const float r2 = lo_bf16(mixed[c].y), r3 = hi_bf16(mixed[c].y);
     ss_out += r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3;
@@ -185,12 +207,12 @@ hipError_t launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out,
   if (rows == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
   switch (chunk_bucket(dim)) {
-    case 1: rms_norm_kernel<1><<<grid, 256, 0, s>>>(x, w, out, rows, dim, eps); break;
-    case 2: rms_norm_kernel<2><<<grid, 256, 0, s>>>(x, w, out, rows, dim, eps); break;
-    case 3: rms_norm_kernel<3><<<grid, 256, 0, s>>>(x, w, out, rows, dim, eps); break;
-    case 4: rms_norm_kernel<4><<<grid, 256, 0, s>>>(x, w, out, rows, dim, eps); break;
-    case 8: rms_norm_kernel<8><<<grid, 256, 0, s>>>(x, w, out, rows, dim, eps); break;
-    default: rms_norm_kernel<16><<<grid, 256, 0, s>>>(x, w, out, rows, dim, eps); break;
+    case 1: rms_norm_kernel<1><<<grid, 64, 0, s>>>(x, w, out, rows, dim, eps); break;
+    case 2: rms_norm_kernel<2><<<grid, 64, 0, s>>>(x, w, out, rows, dim, eps); break;
+    case 3: rms_norm_kernel<3><<<grid, 64, 0, s>>>(x, w, out, rows, dim, eps); break;
+    case 4: rms_norm_kernel<4><<<grid, 64, 0, s>>>(x, w, out, rows, dim, eps); break;
+    case 8: rms_norm_kernel<8><<<grid, 64, 0, s>>>(x, w, out, rows, dim, eps); break;
+    default: rms_norm_kernel<16><<<grid, 64, 0, s>>>(x, w, out, rows, dim, eps); break;
   }
   return hipGetLastError();
 }
@@ -203,7 +225,7 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
   if (tokens == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((tokens + kRowsPerBlock - 1) / kRowsPerBlock));
 #define PARROT_DEPTH(C)                                                          \
-  depth_mix_kernel<C><<<grid, 256, 0, s>>>(srcs, n_sources, query, score_w,     \
+  depth_mix_kernel<C><<<grid, 64, 0, s>>>(srcs, n_sources, query, score_w,     \
                                            score_eps, out_norm_w, out_eps,      \
                                            tokens, dim, out_mix, out_norm)
   switch (chunk_bucket(dim)) {

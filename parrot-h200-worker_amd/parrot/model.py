@@ -258,8 +258,17 @@ class LocalGQA(nn.Module):
         b, t, _ = y.shape
         return y.view(b, t, heads, self.cfg.head_dim).transpose(1, 2)
 
-    def _qkv(self, x: Tensor, start: int = 0):
+    def _hip(self, x: Tensor) -> bool:
+        return self.cfg.uses_hip and _hip_inference(x)
+
+    def _qkv(self, x: Tensor, start: int = 0, expand_kv: bool = False):
         c = self.cfg
+        if self._hip(x):
+            # One packed projection, then RoPE + head split in one HIP kernel.
+            from . import hip_moe
+            cos, sin = _rope_tables(c, x.new_empty(0, dtype=torch.float32))
+            return hip_moe.rope_qkv(F.linear(x, self._packed_qkv()), cos, sin, c.n_heads,
+                                    c.n_kv_heads, c.head_dim, start, expand_kv)
         q = _apply_rope(c, self._heads(self.q(x), c.n_heads), start)
         k = _apply_rope(c, self._heads(self.k(x), c.n_kv_heads), start)
         v = self._heads(self.v(x), c.n_kv_heads)
@@ -268,6 +277,14 @@ class LocalGQA(nn.Module):
     def prefill(self, x: Tensor) -> tuple[Tensor, Tensor, Tensor]:
         b, t, _ = x.shape
         c = self.cfg
+        if self._hip(x) and t <= c.window_size:
+            # Every key of a sequence that fits the window is visible to all
+            # later queries, so the banded mask is plain causal: one flash
+            # attention call over kv heads expanded by the RoPE kernel.
+            q, k, v = self._qkv(x, expand_kv=True)
+            y = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            rep = c.n_heads // c.n_kv_heads
+            return self.out(y.transpose(1, 2).reshape(b, t, -1)), k[:, ::rep], v[:, ::rep]
         q, k, v = self._qkv(x)
         if t <= c.window_size and t <= c.local_query_chunk:
             y = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
@@ -305,11 +322,14 @@ class LocalGQA(nn.Module):
             raise RuntimeError("deferred attention reduction is not supported on this backend")
         c = self.cfg
         b = x.shape[0]
-        qw, kw = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
-        q, k, v = F.linear(x, self._packed_qkv()).split((qw, kw, kw), dim=-1)
-        q = _apply_rope(c, q.view(b, 1, c.n_heads, c.head_dim).transpose(1, 2), position)
-        k = _apply_rope(c, k.view(b, 1, c.n_kv_heads, c.head_dim).transpose(1, 2), position)
-        v = v.view(b, 1, c.n_kv_heads, c.head_dim).transpose(1, 2)
+        if self._hip(x):
+            q, k, v = self._qkv(x, start=position)
+        else:
+            qw, kw = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+            q, k, v = F.linear(x, self._packed_qkv()).split((qw, kw, kw), dim=-1)
+            q = _apply_rope(c, q.view(b, 1, c.n_heads, c.head_dim).transpose(1, 2), position)
+            k = _apply_rope(c, k.view(b, 1, c.n_kv_heads, c.head_dim).transpose(1, 2), position)
+            v = v.view(b, 1, c.n_kv_heads, c.head_dim).transpose(1, 2)
         cache.key[:, :, position:position + 1].copy_(k)
         cache.value[:, :, position:position + 1].copy_(v)
         lo = max(0, position - c.window_size + 1)
@@ -591,7 +611,9 @@ class Parrot(nn.Module):
         if supervised_logits_only and labels is None:
             raise ValueError("supervised_logits_only requires labels")
 
-        x = self.embedding(input_ids).reshape(b, t, bag_size, -1).mean(2)
+        x = self.embedding(input_ids)
+        if bag_size > 1:
+            x = x.reshape(b, t, bag_size, -1).mean(2)
         stream = _AttnRes(x, cfg.depth_block_size) if cfg.residual == "attnres" else None
         aux_losses, utilization = [], []
         remat = cfg.checkpoint_modules and self.training and torch.is_grad_enabled()

@@ -61,17 +61,32 @@ def test_tiny_router_stats():
 
 
 def test_default_forward_512():
-    """default model (E=16), seed 2, batch 1 x 512."""
-    from parrot import ModelConfig
+    """default model (E=16), seed 2, batch 1 x 512.
+
+    The HIP path must agree with the fp32 oracle at least as well as the
+    plain PyTorch bf16 execution of the same model and weights (the
+    reference's pytorch backend in bf16), which bounds what bf16 can reach
+    on this random-init model: ~14% of positions have an fp32 top-1/top-2
+    logit gap below 0.02, while 16 layers of bf16 activations move the
+    logits by ~0.013 on average."""
+    from parrot import ModelConfig, Parrot
     _say("default forward 1x512 (seed 2)")
     model = _hip_model(ModelConfig(moe_backend="grouped_hip", depth_backend="hip",
                                    collect_router_stats=False), 2)
+    control = Parrot(ModelConfig(collect_router_stats=False))
+    control.load_state_dict(model.state_dict())
+    control = control.to(device="cuda", dtype=torch.bfloat16).eval()
     ids = torch.randint(0, 32768, (1, 512), generator=torch.Generator().manual_seed(2))
     with torch.no_grad():
         got = model(ids.cuda()).logits
+        base = control(ids.cuda()).logits
     ref = _oracle(model).forward(ids)
-    agree = _compare(got, ref, 0.98)
-    _say(f"  argmax agreement at 512 positions: {agree:.4f}")
+    agree = _compare(got, ref, 0.9)
+    control_agree = _compare(base, ref, 0.9)
+    _say(f"  argmax agreement: HIP {agree:.4f}, PyTorch bf16 control {control_agree:.4f}")
+    assert agree >= control_agree - 0.01
+    d = (got.float().cpu() - ref.float()).abs()
+    assert d.mean() < 0.02
 
 
 def test_prefill_and_decode():
