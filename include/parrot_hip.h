@@ -174,9 +174,13 @@ int parrot_experts_combine_bf16(int64_t tokens, int32_t dim, int32_t hidden_dim,
  *   out[t] = bf16(shared(x_t) + sum_k w[t,k] * expert_{i[t,k]}(x_t))
  *   (then bf16(addend[t] + out[t]) when addend is non-NULL).
  * counts/offsets/perm/overflow/route_weights come from the routing entry
- * points above.  Weights (bf16):
+ * points above.  Weights (bf16), each matrix [N, K] stored in MFMA fragment
+ * order: 1 KB blocks of 16 rows x 32 k, block (g, s) at byte
+ * (g * K/32 + s) * 1024, holding row 16 g + r, k = 32 s + 8 c .. + 7 at byte
+ * 16 (16 c + r) of the block:
  *   packed_gate_up [E, 2H, dim]  rows 32g..32g+15 = gate rows 16g..16g+15,
  *                                rows 32g+16..32g+31 = up rows 16g..16g+15
+ *                                (before the fragment ordering)
  *   down           [E, dim, H]
  *   shared_gate_up [2Hs, dim]    interleaved the same way
  *   shared_down    [dim, Hs]

@@ -201,7 +201,21 @@ def _interleave_gate_up(gate: Tensor, up: Tensor) -> Tensor:
     *lead, hidden, dim = gate.shape
     g = gate.reshape(*lead, hidden // 16, 16, dim)
     u = up.reshape(*lead, hidden // 16, 16, dim)
-    return torch.stack((g, u), dim=-3).reshape(*lead, 2 * hidden, dim).contiguous()
+    return torch.stack((g, u), dim=-3).reshape(*lead, 2 * hidden, dim)
+
+
+def _fragment_order(w: Tensor) -> Tensor:
+    """[..., N, K] row-major -> MFMA fragment order, same shape and size.
+
+    Blocks of 16 rows x 32 k (1 KB) are laid out row-group-major, k-step
+    minor; inside a block, lane l = 16 g + r of a wavefront holds row r,
+    k = 8 g .. 8 g + 7 at bytes 16 l .. 16 l + 15 -- the operand layout of
+    v_mfma_f32_16x16x32_bf16, so one wavefront load is 1 KB contiguous."""
+    *lead, n, k = w.shape
+    nd = len(lead)
+    v = w.reshape(*lead, n // 16, 16, k // 32, 4, 8)
+    order = list(range(nd)) + [nd, nd + 2, nd + 3, nd + 1, nd + 4]
+    return v.permute(*order).contiguous().reshape(*lead, n, k)
 
 
 def _expert_parameters(module: "MoE") -> list[Tensor]:
@@ -213,10 +227,11 @@ def _expert_parameters(module: "MoE") -> list[Tensor]:
 
 def pack_expert_weights(module: "MoE") -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """(gate_up [E, 2H, dim], down [E, dim, H], shared_gate_up [2Hs, dim],
-    shared_down [dim, Hs]), cached until a parameter changes.  As in the
-    reference, an eval-mode module under no-grad reuses the cache without
-    re-checking versions; call ``invalidate_packed_weights`` after editing
-    weights in place in that mode."""
+    shared_down [dim, Hs]) in MFMA fragment order (``_fragment_order``), the
+    gate/up matrices with 16 gate rows then 16 up rows per 32-row group;
+    cached until a parameter changes.  As in the reference, an eval-mode
+    module under no-grad reuses the cache without re-checking versions; call
+    ``invalidate_packed_weights`` after editing weights in place in that mode."""
     cached = module.__dict__.get("_hip_packed")
     if cached is not None and not torch.is_grad_enabled() and not module.training:
         return cached[1]
@@ -228,11 +243,11 @@ def pack_expert_weights(module: "MoE") -> tuple[Tensor, Tensor, Tensor, Tensor]:
         gate = torch.stack([e.gate.weight.detach() for e in module.experts])
         up = torch.stack([e.up.weight.detach() for e in module.experts])
         packed = (
-            _interleave_gate_up(gate, up),
-            torch.stack([e.down.weight.detach() for e in module.experts]).contiguous(),
-            _interleave_gate_up(module.shared.gate.weight.detach(),
-                                module.shared.up.weight.detach()),
-            module.shared.down.weight.detach().contiguous(),
+            _fragment_order(_interleave_gate_up(gate, up)),
+            _fragment_order(torch.stack([e.down.weight.detach() for e in module.experts])),
+            _fragment_order(_interleave_gate_up(module.shared.gate.weight.detach(),
+                                                module.shared.up.weight.detach())),
+            _fragment_order(module.shared.down.weight.detach()),
         )
     module.__dict__["_hip_packed"] = (version, packed)
     return packed

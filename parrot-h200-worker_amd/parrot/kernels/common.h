@@ -126,9 +126,6 @@ struct GroupMap {
   const float* weights;     // [2T] route weights
 };
 
-// M tile chosen for a token count (16, 32, 64 or 128 rows).
-int experts_tile_m(int64_t tokens, int experts);
-
 // Grouped SwiGLU expert GEMM over every routed assignment plus the shared
 // expert.  Phase 1 (gate/up + SwiGLU) reads x and writes hidden
 // [3T, max(H, Hs)] bf16; phase 2 (down) reads hidden and writes y_routed

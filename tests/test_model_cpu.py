@@ -115,3 +115,24 @@ def test_checkpoint_modules_same_loss():
     la = a(ids, labels=ids).loss
     lb = b(ids, labels=ids).loss
     torch.testing.assert_close(la, lb)
+
+
+def test_packed_weight_fragment_order():
+    """Packed expert matrices use the MFMA operand layout documented in
+    include/parrot_hip.h: block (g, s) holds row 16 g + r, k = 32 s + 8 c .. +7
+    at element offset 8 (16 c + r) of the 512-element block."""
+    from parrot.hip_moe import _fragment_order, _interleave_gate_up
+    n, k = 48, 96
+    w = torch.arange(n * k, dtype=torch.float32).reshape(n, k)
+    f = _fragment_order(w).reshape(-1)
+    for g in range(n // 16):
+        for s in range(k // 32):
+            block = f[(g * (k // 32) + s) * 512:(g * (k // 32) + s + 1) * 512].reshape(64, 8)
+            for c in range(4):
+                for r in range(16):
+                    assert torch.equal(block[16 * c + r], w[16 * g + r, 32 * s + 8 * c:32 * s + 8 * c + 8])
+    gate = torch.arange(32 * 8, dtype=torch.float32).reshape(32, 8)
+    up = -gate
+    gu = _interleave_gate_up(gate, up)
+    assert torch.equal(gu[:16], gate[:16]) and torch.equal(gu[16:32], up[:16])
+    assert torch.equal(gu[32:48], gate[16:]) and torch.equal(gu[48:], up[16:])
