@@ -54,6 +54,15 @@ def parse_args():
                    help="approximate CPU time spent on the cpu_baseline sample")
     p.add_argument("--skip-cpu-baseline", action="store_true")
     p.add_argument("--skip-kernels", action="store_true")
+    p.add_argument("--skip-sweep", action="store_true",
+                   help="skip the token-count sweep of the per-kernel timings")
+    p.add_argument("--skip-decode", action="store_true")
+    p.add_argument("--traffic-workload", action="store_true",
+                   help="only launch the dispatches the two rocprofv3 --pmc passes count: the "
+                        "dominant kernel at the in-model shape and a calibration copy")
+    p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                   help="(no GPU) turn the counter CSVs of the FETCH_SIZE and WRITE_SIZE "
+                        "passes into the traffic summary under profiles/")
     return p.parse_args()
 
 
@@ -251,22 +260,221 @@ def cpu_baseline(model, ids, seconds: float) -> dict:
 
 
 # ---------------------------------------------------------------------------
+# token-count sweep, decode, CPU layer baselines
+# ---------------------------------------------------------------------------
 
-def main():
-    args = parse_args()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
-              f"WORLD_SIZE={world}); the MoE hot path has no multi-GPU implementation and "
-              "every GPU box here has a single MI355X.", file=sys.stderr)
-        sys.exit(2)
+SWEEP_TOKENS = (512, 4096, 16384, 65536)
 
+
+def sweep_kernels(moe, iters: int) -> dict:
+    """Every hot-path kernel of one E=16 MoE layer (block 0's weights) plus
+    RMSNorm and the 9-source depth mix, at growing token counts: where the
+    per-launch fixed cost stops dominating, the bandwidth kernels approach
+    their HBM asymptote and the expert GEMMs become MFMA-bound."""
+    import ctypes
+
+    import torch
+    from parrot import _abi
+    from parrot._abi import ptr
+    lib = _abi.load()
+    dev = torch.device("cuda:0")
+    d = moe.cfg.dim
+    gen = torch.Generator(device=dev).manual_seed(7)
+    out = {}
+    for T in SWEEP_TOKENS:
+        n = max(10, iters if T <= 4096 else iters // 4)
+        x = torch.randn(T, d, device=dev, generator=gen).bfloat16()
+        res, sb = layer_kernels(moe, x, n)
+        y = torch.empty_like(x)
+        s = torch.cuda.current_stream(dev)
+        w = torch.ones(d, device=dev, dtype=torch.bfloat16)
+        res["rms_norm"] = entry(event_time_us(
+            lambda: lib.parrot_rms_norm_bf16(ptr(x), ptr(w), ptr(y), T, d, 1e-6, s.cuda_stream),
+            n, s), 2 * T * d * 2 + d * 2)
+        srcs = [torch.randn(T, d, device=dev, generator=gen).bfloat16() for _ in range(9)]
+        arr = (ctypes.c_void_p * 9)(*[t.data_ptr() for t in srcs])
+        q = torch.randn(d, device=dev, generator=gen).bfloat16()
+        res["depth_mix_norm_s9"] = entry(event_time_us(
+            lambda: lib.parrot_depth_mix_bf16(ctypes.cast(arr, ctypes.c_void_p), 9, ptr(q),
+                                              ptr(w), 1e-6, ptr(w), 1e-6, T, d, None, ptr(y),
+                                              s.cuda_stream), n, s),
+            9 * T * d * 2 + 3 * d * 2 + T * d * 2)
+        out[f"T{T}"] = res
+        del sb, srcs, x, y
+        torch.cuda.empty_cache()
+    return out
+
+
+def decode_bench(model, steps: int = 16) -> dict:
+    """prefill a 128-token prompt (seed 3), then `steps`
+    greedy decode steps, at batch 1, 2, 4 and 8 (eager; 4096-position caches)."""
+    import torch
+    dev = torch.device("cuda:0")
+    out = {}
+    for b in (1, 2, 4, 8):
+        prompt = torch.randint(0, 32768, (b, 128),
+                               generator=torch.Generator().manual_seed(3)).to(dev)
+        with torch.inference_mode():
+            for _ in range(2):  # warm the allocator and kernels
+                logits, state = model.prefill(prompt)
+                nxt = logits[:, -1].argmax(-1, keepdim=True)
+                for _ in range(2):
+                    nxt, state = model.decode_next(nxt, state)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            logits, state = model.prefill(prompt)
+            nxt = logits[:, -1].argmax(-1, keepdim=True)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for _ in range(steps):
+                nxt, state = model.decode_next(nxt, state)
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+        out[f"b{b}"] = {"prefill_ms": round((t1 - t0) * 1e3, 3),
+                        "decode_ms_per_step": round((t2 - t1) * 1e3 / steps, 3),
+                        "decode_tokens_per_s": round(b * steps / (t2 - t1), 1),
+                        "generation_tokens_per_s": round(b * steps / (t2 - t0), 1)}
+    return out
+
+
+def cpu_layer_baselines(seconds: float) -> dict:
+    """The fp32 CPU oracle of one MoE layer (the reference's pytorch loop) at
+    BASELINE configs 2 and 3, tokens/s."""
+    import torch
+
+    from oracle import layers
+    out = {}
+    for name, tokens, skew in (("C2_T256_E32", 256, False), ("C3_T4096_E32_skew", 4096, True)):
+        moe, x, bias = _layer_case(tokens, skew, device="cpu", dtype=torch.float32)
+        sd = {k: v.detach() for k, v in moe.state_dict().items()}
+        experts = [(sd[f"experts.{e}.gate.weight"], sd[f"experts.{e}.up.weight"],
+                    sd[f"experts.{e}.down.weight"]) for e in range(32)]
+        shared = (sd["shared.gate.weight"], sd["shared.up.weight"], sd["shared.down.weight"])
+        bias_np = None if bias is None else bias.numpy()
+        with torch.no_grad():
+            layers.moe_layer(x, sd["router.weight"], experts, shared, bias_np)
+            samples = []
+            t_start = time.perf_counter()
+            while len(samples) < 3 or (time.perf_counter() - t_start < seconds / 2
+                                       and len(samples) < 20):
+                t0 = time.perf_counter()
+                layers.moe_layer(x, sd["router.weight"], experts, shared, bias_np)
+                samples.append(time.perf_counter() - t0)
+        med = statistics.median(samples)
+        out[name] = {"tokens_per_s": round(tokens / med, 1), "median_ms": round(med * 1e3, 3),
+                     "runs": len(samples), "threads": torch.get_num_threads()}
+    return out
+
+
+# ---------------------------------------------------------------------------
+# HBM traffic of the dominant kernel (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)
+# ---------------------------------------------------------------------------
+
+TRAFFIC_FILE = ROOT / "profiles" / "experts_gate_up_C4_traffic.json"
+TRAFFIC_KERNEL = "grouped_gemm_kernel<64, 128, 1>"
+TRAFFIC_LAUNCHES = 20
+CALIBRATION_ELEMS = 1 << 27       # bf16: 256 MiB read + 256 MiB written per launch
+CALIBRATION_LAUNCHES = 5
+TRAFFIC_COMMANDS = [
+    "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc_fetch -o traffic "
+    "-- python3 bench.py --traffic-workload",
+    "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc_write -o traffic "
+    "-- python3 bench.py --traffic-workload",
+    "python3 bench.py --summarize-traffic gpurun_out/pmc_fetch gpurun_out/pmc_write",
+]
+
+
+def traffic_workload() -> None:
+    """The dispatches the two --pmc passes count: the model forward that
+    captures block 0's MoE input, then TRAFFIC_LAUNCHES launches of the
+    experts gate/up kernel on it (the last TRAFFIC_LAUNCHES dispatches named
+    TRAFFIC_KERNEL), then CALIBRATION_LAUNCHES of torch's `neg` over a bf16
+    tensor of CALIBRATION_ELEMS elements: a plain streaming kernel whose HBM
+    bytes are known exactly."""
+    import torch
+    model, ids, captured = build_model()
+    sb = StageBench(model.blocks[0].moe, captured["x"])
+    torch.cuda.synchronize()
+    for _ in range(TRAFFIC_LAUNCHES):
+        rc = sb.gate_up()
+        if rc:
+            raise RuntimeError(f"gate_up returned status {rc}")
+    torch.cuda.synchronize()
+    src = torch.ones(CALIBRATION_ELEMS, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(CALIBRATION_LAUNCHES):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"traffic_workload": "done", "kernel": TRAFFIC_KERNEL,
+                      "launches": TRAFFIC_LAUNCHES, "calibration_launches": CALIBRATION_LAUNCHES,
+                      "experts_hit": sb.hit, "algorithmic_bytes": sb.bytes_gate_up()}), flush=True)
+
+
+def _counter_rows(directory: str, counter: str) -> list[tuple[str, float]]:
+    """(kernel name, value) per dispatch, in dispatch order, from the
+    counter_collection CSVs rocprofv3 wrote under `directory`."""
+    import csv
+    rows = []
+    for path in sorted(Path(directory).rglob("*counter_collection.csv")):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if r.get("Counter_Name") != counter:
+                    continue
+                key = int(r.get("Dispatch_Id") or r.get("Correlation_Id") or len(rows))
+                rows.append((key, r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return [(name, value) for _, name, value in rows]
+
+
+def summarize_traffic(fetch_dir: str, write_dir: str) -> dict:
+    def per_launch(directory, counter):
+        rows = _counter_rows(directory, counter)
+        gemm = [v for n, v in rows if TRAFFIC_KERNEL in n][-TRAFFIC_LAUNCHES:]
+        copy = [v for n, v in rows if "neg" in n][-CALIBRATION_LAUNCHES:]
+        if len(gemm) < TRAFFIC_LAUNCHES or len(copy) < CALIBRATION_LAUNCHES:
+            raise SystemExit(f"{directory}: found {len(gemm)} {TRAFFIC_KERNEL} and {len(copy)} "
+                             f"calibration dispatches of {counter}")
+        return statistics.median(gemm), statistics.median(copy)
+
+    copy_kib = CALIBRATION_ELEMS * 2 / 1024
+    fetch_gemm, fetch_copy = per_launch(fetch_dir, "FETCH_SIZE")
+    write_gemm, write_copy = per_launch(write_dir, "WRITE_SIZE")
+    fetch_scale, write_scale = copy_kib / fetch_copy, copy_kib / write_copy
+    summary = {
+        "kernel": TRAFFIC_KERNEL,
+        "workload": "experts gate/up + SwiGLU, block 0's MoE input of the bs1x512 forward "
+                    "(seed 2), T=512 E=16",
+        "unit": "KiB per dispatch (median)",
+        "fetch_kib": round(fetch_gemm, 1), "write_kib": round(write_gemm, 1),
+        "calibration": {"kernel": "torch.neg, bf16, %d elements" % CALIBRATION_ELEMS,
+                        "bytes_each_way_kib": copy_kib, "fetch_kib": round(fetch_copy, 1),
+                        "write_kib": round(write_copy, 1)},
+        "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
+        "traffic_bytes": int(round((fetch_gemm * fetch_scale + write_gemm * write_scale) * 1024)),
+        "commands": TRAFFIC_COMMANDS,
+    }
+    TRAFFIC_FILE.write_text(json.dumps(summary, indent=1) + "\n")
+    return summary
+
+
+def load_traffic() -> int | None:
+    try:
+        summary = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    return summary.get("traffic_bytes") if summary.get("kernel") == TRAFFIC_KERNEL else None
+
+
+# ---------------------------------------------------------------------------
+
+def build_model():
+    """The default model (seed 2, bf16, HIP backends), the bs1x512 ids, and
+    block 0's MoE input captured from one forward."""
     import torch
 
     from parrot import ModelConfig, Parrot, _abi
     _abi.load()  # fail loudly without the HIP library
     dev = torch.device("cuda:0")
-
     log("building model (seed 2)")
     torch.manual_seed(2)
     model = Parrot(ModelConfig(moe_backend="grouped_hip", depth_backend="hip",
@@ -274,7 +482,6 @@ def main():
     model.eval()
     ids = torch.randint(0, 32768, (1, TOKENS), generator=torch.Generator().manual_seed(2)).to(dev)
 
-    # capture the first layer's MoE input for the per-kernel measurements
     captured = {}
     moe0 = model.blocks[0].moe
     original = moe0.inference
@@ -287,6 +494,28 @@ def main():
     with torch.no_grad():
         model(ids)
     del moe0.inference
+    return model, ids, captured
+
+
+def main():
+    args = parse_args()
+    if args.summarize_traffic:
+        print(json.dumps(summarize_traffic(*args.summarize_traffic)))
+        return
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the MoE hot path has no multi-GPU implementation and "
+              "every GPU box here has a single MI355X.", file=sys.stderr)
+        sys.exit(2)
+    if args.traffic_workload:
+        traffic_workload()
+        return
+
+    import torch
+
+    model, ids, captured = build_model()
+    moe0 = model.blocks[0].moe
 
     log("eager forward")
     with torch.no_grad():
@@ -331,6 +560,7 @@ def main():
         elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
     value = TOKENS * args.steps / elapsed
+    del graph, static_logits, reference_logits
 
     kernels = {}
     roofline = None
@@ -343,11 +573,22 @@ def main():
             moe, x, bias = _layer_case(tokens, skew)
             kernels[name], _ = layer_kernels(moe, x, max(20, args.kernel_iters // 4), bias)
             del moe
+        if not args.skip_sweep:
+            log("token sweep")
+            kernels["sweep_E16"] = sweep_kernels(moe0, max(20, args.kernel_iters // 4))
         gu = c4["gate_up"]
-        roofline = {"kernel": "grouped_gemm_kernel<64,128,1> (experts gate_up + SwiGLU), "
+        traffic = load_traffic()
+        roofline = {"kernel": f"{TRAFFIC_KERNEL} (experts gate_up + SwiGLU), "
                               "C4 in-model shape T=512 E=16",
                     "bound": "hbm", "achieved": gu["gbps"], "peak": PEAK_HBM_GBPS,
-                    "unit": "GB/s", "frac": gu["hbm_frac"], "traffic": None}
+                    "unit": "GB/s", "frac": gu["hbm_frac"], "traffic": traffic,
+                    "algorithmic_bytes": gu["bytes"],
+                    "traffic_source": str(TRAFFIC_FILE.relative_to(ROOT)) if traffic else None}
+
+    decode = None
+    if not args.skip_decode:
+        log("decode (config 5)")
+        decode = decode_bench(model)
 
     result = {
         "metric": "tokens/sec Parrot bf16 fwd bs1x512 on 1 MI355X",
@@ -372,17 +613,20 @@ def main():
         "eager_tokens_per_s": round(TOKENS / (eager_ms / 1e3), 1),
         "roofline": roofline,
         "kernels": kernels,
+        "decode": decode,
         "cpu_baseline": None,
     }
     if not args.skip_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(model, ids, args.cpu_seconds)
+        result["cpu_baseline"]["moe_layers"] = cpu_layer_baselines(args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 
-def _layer_case(tokens: int, skewed: bool):
+def _layer_case(tokens: int, skewed: bool, device="cuda", dtype=None):
     """MoE layer of BASELINE configs 2/3: E=32, weights N(0, 0.02), x N(0, 1)."""
     import torch
+    dtype = torch.bfloat16 if dtype is None else dtype
 
     from parrot.model import ModelConfig, MoE
     cfg = ModelConfig(n_experts=32, moe_backend="grouped_hip", depth_backend="hip",
@@ -392,9 +636,9 @@ def _layer_case(tokens: int, skewed: bool):
     with torch.no_grad():
         for p in moe.parameters():
             p.copy_(torch.randn(p.shape, generator=gen) * 0.02)
-    moe = moe.to(device="cuda", dtype=torch.bfloat16).eval()
+    moe = moe.to(device=device, dtype=dtype).eval()
     x = torch.randn(tokens, cfg.dim, generator=torch.Generator().manual_seed(1)).to(
-        device="cuda", dtype=torch.bfloat16)
+        device=device, dtype=dtype)
     bias = None
     if skewed:
         bias = torch.zeros(32)

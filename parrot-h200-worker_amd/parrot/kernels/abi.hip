@@ -22,8 +22,20 @@ int status(hipError_t e) { return e == hipSuccess ? PARROT_OK : static_cast<int>
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-size_t route_ws_bytes(int64_t tokens, int32_t experts) {
+// Route workspace: block histograms [route_blocks, E], then chunk totals
+// [route_chunks, E] for the two-level scan of long inputs.
+size_t route_hist_bytes(int64_t tokens, int32_t experts) {
   return round_up(static_cast<size_t>(parrot::route_blocks(tokens)) * experts * sizeof(int32_t));
+}
+
+size_t route_ws_bytes(int64_t tokens, int32_t experts) {
+  return route_hist_bytes(tokens, experts) +
+         round_up(static_cast<size_t>(parrot::route_chunks(tokens)) * experts * sizeof(int32_t));
+}
+
+int32_t* route_chunk_totals(void* workspace, int64_t tokens, int32_t experts) {
+  return reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
+                                    route_hist_bytes(tokens, experts));
 }
 
 struct ExpertsWorkspace {
@@ -176,6 +188,7 @@ static int route_common(const void* x, const void* router_weight, const float* l
       out_positions, block_counts, s);
   if (e != hipSuccess) return status(e);
   return status(parrot::launch_group(out_indices, tokens, experts, capacity, block_counts,
+                                     route_chunk_totals(workspace, tokens, experts),
                                      out_positions, out_counts, out_offsets, out_perm,
                                      out_overflow, s));
 }
@@ -223,6 +236,7 @@ int parrot_group_indices(const int64_t* indices, int64_t tokens, int32_t experts
                                              block_counts, s);
   if (e != hipSuccess) return status(e);
   return status(parrot::launch_group(indices, tokens, experts, capacity, block_counts,
+                                     route_chunk_totals(workspace, tokens, experts),
                                      out_positions, out_counts, out_offsets, out_perm,
                                      out_overflow, s));
 }

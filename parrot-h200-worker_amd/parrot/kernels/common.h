@@ -16,6 +16,7 @@ constexpr int kMaxDepthSources = 9;
 // Assignments (token, k) handled by one route workgroup: 16 tokens x top-2.
 constexpr int kRouteTokensPerBlock = 16;
 constexpr int kRouteAssignPerBlock = 2 * kRouteTokensPerBlock;
+constexpr int kScanChunk = 256;  // route blocks per chunk of the two-level histogram scan
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -94,8 +95,12 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
                         float* probs, float* weights, int64_t* indices,
                         int32_t* positions, int32_t* block_counts, hipStream_t s);
 
-// Number of route workgroups (= rows of block_counts) for `tokens`.
+// Number of 16-token route blocks (= rows of block_counts) for `tokens`.
 int route_blocks(int64_t tokens);
+
+// Rows of the chunk-total table the group step needs beside block_counts
+// (0 when one chunk holds every route block).
+int route_chunks(int64_t tokens);
 
 // Block-local ranks for externally supplied top-2 indices.
 hipError_t launch_rank_indices(const int64_t* indices, int64_t tokens, int experts,
@@ -106,8 +111,10 @@ hipError_t launch_rank_indices(const int64_t* indices, int64_t tokens, int exper
 // fixed-capacity map, the expert-contiguous overflow list and the offsets
 // table: offsets[0..E] = exclusive prefix of counts, offsets[E+1..2E+1] =
 // exclusive prefix of per-expert overflow counts.
+// `chunk_totals` [route_chunks(tokens), experts] is scratch (unused when
+// route_chunks is 0).
 hipError_t launch_group(const int64_t* indices, int64_t tokens, int experts,
-                        int capacity, const int32_t* block_counts,
+                        int capacity, const int32_t* block_counts, int32_t* chunk_totals,
                         int32_t* positions, int32_t* counts, int32_t* offsets,
                         int32_t* perm, int32_t* overflow, hipStream_t s);
 

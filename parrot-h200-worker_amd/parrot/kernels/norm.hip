@@ -55,16 +55,14 @@ __global__ __launch_bounds__(64) void rms_norm_kernel(
 
 // Block AttnRes: score_s = <rmsnorm_w(v_s), q>, alpha = softmax_s(score),
 // mix = bf16(sum_s alpha_s v_s); optionally y = rmsnorm_out(mix).
-// Every source row is loaded up front (all loads in flight together), parked
-// in LDS, and the per-source work then runs as compact runtime loops.
+// One wavefront per token.  Every source row is loaded up front (all loads in
+// flight together) and kept in registers through the scores and the mix.
 template <int MAXC>
 __global__ __launch_bounds__(64) void depth_mix_kernel(
     DepthSources srcs, int n_sources, const uint16_t* __restrict__ query,
     const uint16_t* __restrict__ score_w, float score_eps,
     const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
     uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm) {
-  __shared__ uint2 stage[kMaxDepthSources][MAXC][kWave];
-  __shared__ float score_s[kMaxDepthSources];
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t tok = blockIdx.x;
   if (tok >= tokens) return;
@@ -88,66 +86,77 @@ __global__ __launch_bounds__(64) void depth_mix_kernel(
     }
   }
 
-  // Per-lane partial sums of every source, then all 2S wavefront reductions
-  // back to back so their latencies overlap.
-  float ss[kMaxDepthSources], dq[kMaxDepthSources];
-  {
-    uint2 v[kMaxDepthSources][MAXC];
-#pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s) {
-      if (s < n_sources) {
-        const uint2* src = reinterpret_cast<const uint2*>(srcs.src[s]) + base;
-#pragma unroll
-        for (int c = 0; c < MAXC; ++c) {
-          const int i = lane + c * kWave;
-          v[s][c] = i < chunks ? src[i] : make_uint2(0u, 0u);
-        }
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s) {
-      ss[s] = 0.0f;
-      dq[s] = 0.0f;
-      if (s < n_sources) {
-#pragma unroll
-        for (int c = 0; c < MAXC; ++c) {
-          stage[s][c][lane] = v[s][c];
-          const float e0 = lo_bf16(v[s][c].x), e1 = hi_bf16(v[s][c].x);
-          const float e2 = lo_bf16(v[s][c].y), e3 = hi_bf16(v[s][c].y);
-          ss[s] += e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3;
-          dq[s] += e0 * wq[c][0] + e1 * wq[c][1] + e2 * wq[c][2] + e3 * wq[c][3];
-        }
-      }
-    }
-  }
-  float mx = -INFINITY;
+  // Every source row stays in registers from its load to the mix (the
+  // source loop is unrolled over the maximum count, guarded by n_sources),
+  // so a token needs no LDS and no barrier and occupancy is set by VGPRs.
+  uint2 v[kMaxDepthSources][MAXC];
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) {
     if (s < n_sources) {
-      const float score = wave_sum(dq[s]) * rsqrtf(wave_sum(ss[s]) / static_cast<float>(dim) + score_eps);
-      if (lane == 0) score_s[s] = score;
-      mx = fmaxf(mx, score);
+      const uint2* src = reinterpret_cast<const uint2*>(srcs.src[s]) + base;
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) {
+        const int i = lane + c * kWave;
+        v[s][c] = i < chunks ? src[i] : make_uint2(0u, 0u);
+      }
     }
   }
-  __syncthreads();
+  // Per-lane partial sums of every source, then all 2S wavefront reductions
+  // back to back so their latencies overlap.  The reductions leave every
+  // lane with the same totals, so the scores are wavefront-uniform.
+  float ss[kMaxDepthSources], dq[kMaxDepthSources];
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    ss[s] = 0.0f;
+    dq[s] = 0.0f;
+    if (s < n_sources) {
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) {
+        const float e0 = lo_bf16(v[s][c].x), e1 = hi_bf16(v[s][c].x);
+        const float e2 = lo_bf16(v[s][c].y), e3 = hi_bf16(v[s][c].y);
+        ss[s] += e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3;
+        dq[s] += e0 * wq[c][0] + e1 * wq[c][1] + e2 * wq[c][2] + e3 * wq[c][3];
+      }
+    }
+  }
+  float score[kMaxDepthSources];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    score[s] = -INFINITY;
+    if (s < n_sources) {
+      score[s] = wave_sum(dq[s]) * rsqrtf(wave_sum(ss[s]) / static_cast<float>(dim) + score_eps);
+      mx = fmaxf(mx, score[s]);
+    }
+  }
   float denom = 0.0f;
-#pragma unroll 1
-  for (int s = 0; s < n_sources; ++s) denom += __expf(score_s[s] - mx);
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s)
+    if (s < n_sources) denom += __expf(score[s] - mx);
   const float inv = 1.0f / denom;
+
+  // Keep only the packed bf16 rows live across the reductions: without this
+  // the compiler holds the unpacked fp32 copies (twice the registers, half
+  // the occupancy) to reuse them in the mix.
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s)
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) asm volatile("" : "+v"(v[s][c].x), "+v"(v[s][c].y));
 
   float acc[MAXC][4];
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) acc[c][0] = acc[c][1] = acc[c][2] = acc[c][3] = 0.0f;
-#pragma unroll 1
-  for (int s = 0; s < n_sources; ++s) {
-    const float a = __expf(score_s[s] - mx) * inv;
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      const uint2 x = stage[s][c][lane];
-      acc[c][0] += a * lo_bf16(x.x);
-      acc[c][1] += a * hi_bf16(x.x);
-      acc[c][2] += a * lo_bf16(x.y);
-      acc[c][3] += a * hi_bf16(x.y);
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    if (s < n_sources) {
+      const float a = __expf(score[s] - mx) * inv;
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) {
+        acc[c][0] += a * lo_bf16(v[s][c].x);
+        acc[c][1] += a * hi_bf16(v[s][c].x);
+        acc[c][2] += a * lo_bf16(v[s][c].y);
+        acc[c][3] += a * hi_bf16(v[s][c].y);
+      }
     }
   }
   uint2 mixed[MAXC];

@@ -28,35 +28,142 @@ __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
-// Block-local stable rank of each of the block's assignments and the
-// block's per-expert histogram.  `ids` holds expert ids (-1 = padding or an
-// id outside [0, experts)).
-__device__ __forceinline__ void block_rank(const int* ids, int64_t a0, int64_t n_assign,
-                                           int experts, int32_t* positions,
-                                           int32_t* block_counts) {
-  const int j = threadIdx.x;
-  if (j < kRouteAssignPerBlock) {
-    const int e = ids[j];
-    if (e >= 0 && a0 + j < n_assign) {
-      int rank = 0;
-      for (int i = 0; i < j; ++i) rank += ids[i] == e;
-      positions[a0 + j] = rank;
+// ---- top-2 across a row of 16 lanes ----------------------------------------
+// A token's logits are spread over one DPP row: lane j holds experts j and
+// j + 16.  Selection is a max-reduction of 64-bit keys (order-preserving
+// float bits, then the complemented expert index), so equal logits go to
+// the lower expert index: the strict '>' scan in expert order of the
+// reference.
+
+// Order-preserving map of a float to uint32 (-0 canonicalised to +0, so it
+// ties with +0 as it does under '>').
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t u = __float_as_uint(v + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t expert_key(float v, int e) {
+  return (static_cast<uint64_t>(order_key(v)) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
+}
+
+// Inverse of order_key on the high word of a key.
+__device__ __forceinline__ float key_value(uint64_t k) {
+  const uint32_t o = static_cast<uint32_t>(k >> 32);
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+__device__ __forceinline__ int key_expert(uint64_t k) {
+  return static_cast<int>(0xffffffffu - static_cast<uint32_t>(k));
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_max_key(uint64_t k) {
+  const int lo = static_cast<int>(static_cast<uint32_t>(k));
+  const int hi = static_cast<int>(static_cast<uint32_t>(k >> 32));
+  const uint32_t olo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xf, 0xf, false));
+  const uint32_t ohi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xf, 0xf, false));
+  const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;
+  return o > k ? o : k;
+}
+
+// Max over the 16 lanes of a DPP row, returned to every lane of the row
+// (xor 1, xor 2 inside quads, then half-row and row mirrors).
+__device__ __forceinline__ uint64_t row_max_key(uint64_t k) {
+  k = dpp_max_key<0xb1>(k);
+  k = dpp_max_key<0x4e>(k);
+  k = dpp_max_key<0x141>(k);
+  return dpp_max_key<0x140>(k);
+}
+
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp<0xb1>(v);
+  v += dpp<0x4e>(v);
+  v += dpp<0x141>(v);
+  return v + dpp<0x140>(v);
+}
+
+// Top-2 of the token whose logits lane j of this DPP row holds for experts
+// j (l0) and j + 16 (l1; ignored unless experts > 16), route weights
+// renormalised over the two selected exponentials, and the optional logits
+// and probabilities.  Every lane of the row calls it; lane 0 of the row
+// writes the per-token outputs and returns the two ids in `ids`.
+__device__ __forceinline__ void select_top2(float l0, float l1, int experts, int64_t t,
+                                            bool valid, float* out_logits, float* probs,
+                                            float* weights, int64_t* indices, int* ids) {
+  const int j = threadIdx.x & 15;
+  const bool has0 = j < experts, has1 = j + 16 < experts;
+  constexpr uint64_t kNone = 0;  // below every real key
+  const uint64_t k0 = has0 ? expert_key(l0, j) : kNone;
+  const uint64_t k1 = has1 ? expert_key(l1, j + 16) : kNone;
+  const uint64_t mine = k1 > k0 ? k1 : k0;    // k0 wins ties: lower index
+  const uint64_t other = k1 > k0 ? k0 : k1;
+  const uint64_t best = row_max_key(mine);
+  const uint64_t runner = row_max_key(mine == best ? other : mine);
+  const int first = key_expert(best), second = key_expert(runner);
+  // The selected logits, decoded from their keys.
+  const float vb = key_value(best), vr = key_value(runner);
+  if (valid) {
+    if (out_logits != nullptr) {
+      if (has0) out_logits[t * experts + j] = l0;
+      if (has1) out_logits[t * experts + j + 16] = l1;
     }
-  } else if (j >= 64 && j - 64 < experts) {
-    const int e = j - 64;
-    int count = 0;
-    for (int i = 0; i < kRouteAssignPerBlock; ++i) count += ids[i] == e;
-    block_counts[static_cast<int64_t>(blockIdx.x) * experts + e] = count;
+    if (probs != nullptr) {
+      const float p0 = has0 ? __expf(l0 - vb) : 0.0f;
+      const float p1 = has1 ? __expf(l1 - vb) : 0.0f;
+      const float inv = 1.0f / row_sum(p0 + p1);
+      if (has0) probs[t * experts + j] = p0 * inv;
+      if (has1) probs[t * experts + j + 16] = p1 * inv;
+    }
+  }
+  if (j == 0) {
+    if (valid) {
+      const float e2 = __expf(vr - vb);
+      const float sel = 1.0f + e2;
+      indices[2 * t] = first;
+      indices[2 * t + 1] = second;
+      weights[2 * t] = 1.0f / sel;
+      weights[2 * t + 1] = e2 / sel;
+    }
+    ids[0] = valid ? first : -1;
+    ids[1] = valid ? second : -1;
   }
 }
 
-// One workgroup routes 16 tokens.  The router projection [16 x dim] .
-// [dim x E] runs on v_mfma_f32_16x16x32_bf16 with the 32-wide k steps split
-// round-robin over the 4 wavefronts; each wavefront issues the loads of up
-// to 8 steps before its MFMAs, and the partial logits are summed in a fixed
-// order through LDS.  Fragments: lane l holds row/col (l & 15) and the 8 k
-// values at (l >> 4) * 8 of a step; C holds column (l & 15), rows
-// 4 (l >> 4) + r.  With GIVEN_LOGITS the fp32 logits are read instead.
+// ---- block-local ranks and histograms from wavefront ballots ---------------
+// Each half-wavefront owns one route block of 32 assignments; lane l holds
+// assignment id `id` (-1 = padding or an id outside [0, experts)).  For every
+// expert, a ballot of the lanes holding it gives the stable rank (set bits
+// below the lane, v_mbcnt) and the block's count (popcount).  Writes
+// positions[a] for valid ids and block_counts[block, e] for blocks below
+// n_blocks.
+__device__ __forceinline__ void rank_half_waves(int id, int64_t block, int64_t n_blocks,
+                                                int64_t n_assign, int experts,
+                                                int32_t* positions, int32_t* block_counts) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint64_t half = lane < 32 ? 0x00000000ffffffffull : 0xffffffff00000000ull;
+  int rank = 0, count = 0;
+#pragma unroll 1
+  for (int e = 0; e < experts; ++e) {
+    const uint64_t m = __ballot(id == e) & half;
+    const int below = static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+        static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+    if (id == e) rank = below;
+    if ((lane & 31) == e) count = __popcll(m);
+  }
+  const int64_t a = block * kRouteAssignPerBlock + (lane & 31);
+  if (id >= 0 && a < n_assign) positions[a] = rank;
+  if ((lane & 31) < experts && block < n_blocks) block_counts[block * experts + (lane & 31)] = count;
+}
+
+// One workgroup routes one 16-token route block.  The router projection
+// [16 x dim] . [dim x E] runs on v_mfma_f32_16x16x32_bf16 with the 32-wide
+// k steps split round-robin over the 4 wavefronts; each wavefront issues the
+// loads of up to 8 steps before its MFMAs, and the partial logits are summed
+// in a fixed order through LDS.  Fragments: lane l holds row/col (l & 15)
+// and the 8 k values at (l >> 4) * 8 of a step; C holds column (l & 15),
+// rows 4 (l >> 4) + r.  With GIVEN_LOGITS the fp32 logits are read instead.
+// This split-K shape keeps short inputs (prefill, decode) latency-bound at
+// the minimum.
 template <bool GIVEN_LOGITS>
 __global__ __launch_bounds__(256) void route_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
@@ -117,81 +224,164 @@ __global__ __launch_bounds__(256) void route_kernel(
   }
   __syncthreads();
 
-  if (threadIdx.x < kRouteTokensPerBlock) {
-    // Runtime loops over the experts keep this code small: it runs once per
-    // workgroup, so its instruction fetch is not amortised.
-    const int tl = threadIdx.x;
-    const int64_t t = t0 + tl;
+  {
+    // Token tl = tid / 16 on DPP row tid / 16; lane j holds experts j, j + 16.
+    const int tl = threadIdx.x >> 4;
+    const int j = threadIdx.x & 15;
     auto logit = [&](int e) -> float {
       float v = part_s[0][tl][e];
       if constexpr (!GIVEN_LOGITS) v = ((v + part_s[1][tl][e]) + part_s[2][tl][e]) + part_s[3][tl][e];
       return v + (bias != nullptr ? bias[e] : 0.0f);
     };
-    float best = logit(0), runner = logit(1);
-    int first = 0, second = 1;
-    if (runner > best) {
-      const float tmp = best;
-      best = runner;
-      runner = tmp;
-      first = 1;
-      second = 0;
-    }
-#pragma unroll 1
-    for (int e = 2; e < experts; ++e) {
-      const float v = logit(e);
-      if (v > best) {
-        runner = best;
-        second = first;
-        best = v;
-        first = e;
-      } else if (v > runner) {
-        runner = v;
-        second = e;
-      }
-    }
-    if (t < tokens) {
-      const float e2 = __expf(runner - best);
-      const float sel = 1.0f + e2;
-      indices[2 * t] = first;
-      indices[2 * t + 1] = second;
-      weights[2 * t] = 1.0f / sel;
-      weights[2 * t + 1] = e2 / sel;
-      if (out_logits != nullptr) {
-#pragma unroll 1
-        for (int e = 0; e < experts; ++e) out_logits[t * experts + e] = logit(e);
-      }
-      if (probs != nullptr) {
-        float denom = 0.0f;
-#pragma unroll 1
-        for (int e = 0; e < experts; ++e) denom += __expf(logit(e) - best);
-        const float inv = 1.0f / denom;
-#pragma unroll 1
-        for (int e = 0; e < experts; ++e) probs[t * experts + e] = __expf(logit(e) - best) * inv;
-      }
-    }
-    ids_s[2 * tl] = t < tokens ? first : -1;
-    ids_s[2 * tl + 1] = t < tokens ? second : -1;
+    const float l0 = j < experts ? logit(j) : 0.0f;
+    const float l1 = j + 16 < experts ? logit(j + 16) : 0.0f;
+    select_top2(l0, l1, experts, t0 + tl, t0 + tl < tokens, out_logits, probs, weights, indices,
+                &ids_s[2 * tl]);
   }
   __syncthreads();
-  block_rank(ids_s, static_cast<int64_t>(blockIdx.x) * kRouteAssignPerBlock, 2 * tokens, experts,
-             positions, block_counts);
+  // Wavefront 0 ranks the block in lanes 0-31; lanes 32-63 carry no
+  // assignments and name no block (index gridDim.x is past the last).
+  if (threadIdx.x < kWave) {
+    const bool mine = threadIdx.x < kRouteAssignPerBlock;
+    rank_half_waves(mine ? ids_s[threadIdx.x] : -1, mine ? blockIdx.x : gridDim.x, gridDim.x,
+                    2 * tokens, experts, positions, block_counts);
+  }
+}
+
+// Long inputs: one workgroup routes 4 route blocks (64 tokens); wavefront w
+// computes the logits of route block 4 blockIdx.x + w over the full K, 8
+// k steps of loads in flight at a time.  Same block-local ranks and
+// histograms as route_kernel, so the group step is shared.
+__global__ __launch_bounds__(256) void route_wide_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
+    const float* __restrict__ bias, int64_t tokens, int dim, int experts,
+    float* __restrict__ out_logits, float* __restrict__ probs, float* __restrict__ weights,
+    int64_t* __restrict__ indices, int32_t* __restrict__ positions,
+    int32_t* __restrict__ block_counts, int n_blocks) {
+  constexpr int kTokens = 4 * kRouteTokensPerBlock;
+  __shared__ float logit_s[kTokens][kMaxExperts + 1];
+  __shared__ int ids_s[4 * kRouteAssignPerBlock];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTokens;
+  {
+    const int64_t r = t0 + wave * 16 + (lane & 15);
+    const int64_t row = r < tokens ? r : tokens - 1;
+    const int e0 = min(lane & 15, experts - 1);
+    const int e1 = min(16 + (lane & 15), experts - 1);
+    const int koff = (lane >> 4) * 8;
+    const uint16_t* pa = x + row * dim + koff;
+    const uint16_t* pb0 = wr + static_cast<int64_t>(e0) * dim + koff;
+    const uint16_t* pb1 = wr + static_cast<int64_t>(e1) * dim + koff;
+    const bool two = experts > 16;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc1 = {0.f, 0.f, 0.f, 0.f};
+    const int steps = dim / 32;
+    for (int c0 = 0; c0 < steps; c0 += kStepsPerChunk) {
+      bf16x8 a[kStepsPerChunk], b0[kStepsPerChunk], b1[kStepsPerChunk];
+#pragma unroll
+      for (int i = 0; i < kStepsPerChunk; ++i) {
+        const int st = min(c0 + i, steps - 1);  // unconditional loads, clamped
+        a[i] = load_bf16x8(pa + st * 32);
+        b0[i] = load_bf16x8(pb0 + st * 32);
+        b1[i] = load_bf16x8(pb1 + st * 32);
+      }
+#pragma unroll
+      for (int i = 0; i < kStepsPerChunk; ++i) {
+        if (c0 + i < steps) {
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b0[i], acc0, 0, 0, 0);
+          if (two) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b1[i], acc1, 0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      logit_s[wave * 16 + 4 * (lane >> 4) + r][lane & 15] = acc0[r];
+      logit_s[wave * 16 + 4 * (lane >> 4) + r][16 + (lane & 15)] = acc1[r];
+    }
+  }
+  __syncthreads();
+  // Four passes of 16 tokens, one per DPP row.
+#pragma unroll 1
+  for (int pass = 0; pass < 4; ++pass) {
+    const int tl = pass * 16 + (threadIdx.x >> 4);
+    const int j = threadIdx.x & 15;
+    const float b0 = bias != nullptr && j < experts ? bias[j] : 0.0f;
+    const float b1 = bias != nullptr && j + 16 < experts ? bias[j + 16] : 0.0f;
+    select_top2(logit_s[tl][j] + b0, logit_s[tl][16 + j] + b1, experts, t0 + tl,
+                t0 + tl < tokens, out_logits, probs, weights, indices, &ids_s[2 * tl]);
+  }
+  __syncthreads();
+  // Wavefronts 0 and 1 rank route blocks 4 bx + 2 w (lanes 0-31) and
+  // 4 bx + 2 w + 1 (lanes 32-63).
+  if (threadIdx.x < 2 * kWave)
+    rank_half_waves(ids_s[threadIdx.x], static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 5),
+                    n_blocks, 2 * tokens, experts, positions, block_counts);
 }
 
 // Block-local ranks for top-2 indices supplied by the caller.
-__global__ __launch_bounds__(256) void rank_indices_kernel(
+__global__ __launch_bounds__(64) void rank_indices_kernel(
     const int64_t* __restrict__ indices, int64_t tokens, int experts,
-    int32_t* __restrict__ positions, int32_t* __restrict__ block_counts) {
-  __shared__ int ids_s[kRouteAssignPerBlock];
-  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * kRouteAssignPerBlock;
-  if (threadIdx.x < kRouteAssignPerBlock) {
-    const int64_t a = a0 + threadIdx.x;
-    const int64_t e = a < 2 * tokens ? indices[a] : -1;
-    // Ids outside [0, experts) are excluded from the grouping (slot -1).
-    ids_s[threadIdx.x] = (e >= 0 && e < experts) ? static_cast<int>(e) : -1;
-    if (a < 2 * tokens && ids_s[threadIdx.x] < 0) positions[a] = -1;
+    int32_t* __restrict__ positions, int32_t* __restrict__ block_counts, int n_blocks) {
+  // Lanes 0-31 hold route block 2 bx, lanes 32-63 route block 2 bx + 1.
+  const int64_t a = static_cast<int64_t>(blockIdx.x) * 2 * kRouteAssignPerBlock + threadIdx.x;
+  const int64_t e = a < 2 * tokens ? indices[a] : -1;
+  // Ids outside [0, experts) are excluded from the grouping (slot -1).
+  const int id = (e >= 0 && e < experts) ? static_cast<int>(e) : -1;
+  if (a < 2 * tokens && id < 0) positions[a] = -1;
+  rank_half_waves(id, static_cast<int64_t>(blockIdx.x) * 2 + (threadIdx.x >> 5), n_blocks,
+                  2 * tokens, experts, positions, block_counts);
+}
+
+// Adds rows lo + g, lo + g + n_groups, ... below `hi` of column e of the
+// int32 table [rows, experts] to `all`, and those below `split` also to
+// `below`; four independent loads per round trip (g = this thread's lane
+// group).
+__device__ __forceinline__ void sum_column(const int32_t* table, int experts, int e, int g,
+                                           int n_groups, int lo, int hi, int split, int& below,
+                                           int& all) {
+  for (int i0 = lo + g; i0 < hi; i0 += 4 * n_groups) {
+    int v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      v[k] = table[static_cast<int64_t>(min(i0 + k * n_groups, hi - 1)) * experts + e];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = i0 + k * n_groups;
+      if (i < hi) {
+        all += v[k];
+        below += i < split ? v[k] : 0;
+      }
+    }
   }
+}
+
+// Lane groups of a 256-thread workgroup for per-expert column sums: 16
+// groups of 16 experts (E <= 16) or 8 groups of 32.
+__device__ __forceinline__ int lane_groups(int experts) { return experts <= 16 ? 16 : 8; }
+
+// First level of the histogram scan for long inputs: chunk c's per-expert
+// totals over route blocks [256 c, 256 c + 256), summed by lane groups in a
+// fixed order.
+__global__ __launch_bounds__(256) void chunk_sum_kernel(const int32_t* __restrict__ block_counts,
+                                                        int n_blocks, int experts,
+                                                        int32_t* __restrict__ chunk_totals) {
+  __shared__ int part_s[16][kMaxExperts];
+  const int n_groups = lane_groups(experts);
+  const int e_stride = 256 / n_groups;
+  const int g = threadIdx.x / e_stride;
+  const int e = threadIdx.x - g * e_stride;
+  const int first = blockIdx.x * kScanChunk;
+  const int last = min(first + kScanChunk, n_blocks);
+  int sum = 0, unused = 0;
+  if (e < experts) sum_column(block_counts, experts, e, g, n_groups, first, last, last, unused, sum);
+  part_s[g][e] = sum;
   __syncthreads();
-  block_rank(ids_s, a0, 2 * tokens, experts, positions, block_counts);
+  if (threadIdx.x < experts) {
+    int total = 0;
+    for (int k = 0; k < n_groups; ++k) total += part_s[k][threadIdx.x];
+    chunk_totals[static_cast<int64_t>(blockIdx.x) * experts + threadIdx.x] = total;
+  }
 }
 
 constexpr int kGroupAssign = 256;                                  // assignments per group WG
@@ -201,15 +391,18 @@ constexpr int kBlocksPerGroup = kGroupAssign / kRouteAssignPerBlock;  // route b
 // expert-contiguous overflow list.  Workgroup g finalises assignments
 // [256 g, 256 g + 256) (route blocks 8 g .. 8 g + 7) and fills the empty map
 // slots [256 g, 256 g + 256).  Per-expert bases are exclusive sums of the
-// route blocks' histograms, summed by 8 thread groups in a fixed order.
+// route blocks' histograms, summed by lane groups in a fixed order --
+// directly over every route block for short inputs, or over chunk totals
+// plus at most one chunk of route blocks when `chunk_totals` is given.
 __global__ __launch_bounds__(256) void group_kernel(
     const int64_t* __restrict__ indices, int64_t tokens, int experts, int capacity,
     int n_route_blocks, const int32_t* __restrict__ block_counts,
+    const int32_t* __restrict__ chunk_totals, int n_chunks,
     int32_t* __restrict__ positions, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
     int32_t* __restrict__ overflow) {
-  __shared__ int before_s[8][kMaxExperts];
-  __shared__ int total_s[8][kMaxExperts];
+  __shared__ int before_s[16][kMaxExperts];
+  __shared__ int total_s[16][kMaxExperts];
   __shared__ int base_s[kBlocksPerGroup][kMaxExperts];
   __shared__ int cnt_s[kMaxExperts];
   __shared__ int off_s[kMaxExperts + 1];
@@ -217,15 +410,25 @@ __global__ __launch_bounds__(256) void group_kernel(
   const int gb = blockIdx.x;
   const int tid = threadIdx.x;
   const int first_block = gb * kBlocksPerGroup;
+  const int n_groups = lane_groups(experts);
+  const int e_stride = 256 / n_groups;
+  const int lane_group = tid / e_stride;
   {
-    const int e = tid & 31;
-    const int lane_group = tid >> 5;
+    const int e = tid - lane_group * e_stride;
     int before = 0, total = 0;
     if (e < experts) {
-      for (int i = lane_group; i < n_route_blocks; i += 8) {
-        const int c = block_counts[static_cast<int64_t>(i) * experts + e];
-        before += i < first_block ? c : 0;
-        total += c;
+      if (chunk_totals == nullptr) {
+        sum_column(block_counts, experts, e, lane_group, n_groups, 0, n_route_blocks, first_block,
+                   before, total);
+      } else {
+        // Two levels: whole chunks before this workgroup's chunk, then the
+        // route blocks of its own chunk before `first_block`.
+        const int c0 = first_block / kScanChunk;
+        sum_column(chunk_totals, experts, e, lane_group, n_groups, 0, n_chunks, c0, before, total);
+        const int hi = min(first_block, n_route_blocks);
+        int in_chunk = 0;
+        sum_column(block_counts, experts, e, lane_group, n_groups, c0 * kScanChunk, hi, hi, before,
+                   in_chunk);
       }
     }
     before_s[lane_group][e] = before;
@@ -234,28 +437,36 @@ __global__ __launch_bounds__(256) void group_kernel(
   __syncthreads();
   if (tid < experts) {
     int before = 0, total = 0;
-    for (int g = 0; g < 8; ++g) {
+    for (int g = 0; g < n_groups; ++g) {
       before += before_s[g][tid];
       total += total_s[g][tid];
     }
     cnt_s[tid] = total;
-    for (int j = 0; j < kBlocksPerGroup; ++j) {
-      base_s[j][tid] = before;
-      const int rb = first_block + j;
-      before += rb < n_route_blocks ? block_counts[static_cast<int64_t>(rb) * experts + tid] : 0;
+    if (n_route_blocks > 0) {
+      int bc[kBlocksPerGroup];
+#pragma unroll
+      for (int j = 0; j < kBlocksPerGroup; ++j)
+        bc[j] = block_counts[static_cast<int64_t>(min(first_block + j, n_route_blocks - 1)) * experts + tid];
+#pragma unroll
+      for (int j = 0; j < kBlocksPerGroup; ++j) {
+        base_s[j][tid] = before;
+        before += first_block + j < n_route_blocks ? bc[j] : 0;
+      }
     }
   }
   __syncthreads();
-  if (tid == 0) {
+  // Exclusive prefixes of the counts and of the overflow counts: thread e
+  // sums entries [0, e) itself (independent LDS reads, no serial chain).
+  if (tid <= experts) {
     int o = 0, v = 0;
-    for (int e = 0; e < experts; ++e) {
-      off_s[e] = o;
-      ovf_s[e] = v;
-      o += cnt_s[e];
-      v += max(0, cnt_s[e] - capacity);
+#pragma unroll
+    for (int e = 0; e < kMaxExperts; ++e) {
+      const int c = e < tid ? cnt_s[e] : 0;
+      o += c;
+      v += max(0, c - capacity);
     }
-    off_s[experts] = o;
-    ovf_s[experts] = v;
+    off_s[tid] = o;
+    ovf_s[tid] = v;
   }
   __syncthreads();
   const int64_t slot = static_cast<int64_t>(gb) * kGroupAssign + tid;
@@ -284,21 +495,29 @@ __global__ __launch_bounds__(256) void group_kernel(
 
 }  // namespace
 
+// The wide (64-token) route kernel takes over once its workgroups alone
+// cover every CU; below that the split-K kernel's shorter chain wins.
+constexpr int64_t kWideRouteTokens = 16384;
+
 hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
                         const float* given_logits, const float* bias,
                         int64_t tokens, int dim, int experts, float* out_logits,
                         float* probs, float* weights, int64_t* indices,
                         int32_t* positions, int32_t* block_counts, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((tokens + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock));
+  const int nrb = route_blocks(tokens);
   if (given_logits != nullptr) {
-    route_kernel<true><<<grid, 256, 0, s>>>(x, router_w, given_logits, bias, tokens, dim, experts,
-                                            out_logits, probs, weights, indices, positions,
-                                            block_counts);
+    route_kernel<true><<<nrb, 256, 0, s>>>(x, router_w, given_logits, bias, tokens, dim, experts,
+                                           out_logits, probs, weights, indices, positions,
+                                           block_counts);
+  } else if (tokens >= kWideRouteTokens) {
+    route_wide_kernel<<<(nrb + 3) / 4, 256, 0, s>>>(x, router_w, bias, tokens, dim, experts,
+                                                    out_logits, probs, weights, indices,
+                                                    positions, block_counts, nrb);
   } else {
-    route_kernel<false><<<grid, 256, 0, s>>>(x, router_w, given_logits, bias, tokens, dim,
-                                             experts, out_logits, probs, weights, indices,
-                                             positions, block_counts);
+    route_kernel<false><<<nrb, 256, 0, s>>>(x, router_w, given_logits, bias, tokens, dim,
+                                            experts, out_logits, probs, weights, indices,
+                                            positions, block_counts);
   }
   return hipGetLastError();
 }
@@ -306,8 +525,9 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
 hipError_t launch_rank_indices(const int64_t* indices, int64_t tokens, int experts,
                                int32_t* positions, int32_t* block_counts, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>(route_blocks(tokens)));
-  rank_indices_kernel<<<grid, 256, 0, s>>>(indices, tokens, experts, positions, block_counts);
+  const int nrb = route_blocks(tokens);
+  rank_indices_kernel<<<(nrb + 1) / 2, 64, 0, s>>>(indices, tokens, experts, positions,
+                                                   block_counts, nrb);
   return hipGetLastError();
 }
 
@@ -315,15 +535,26 @@ int route_blocks(int64_t tokens) {
   return static_cast<int>((tokens + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock);
 }
 
+int route_chunks(int64_t tokens) {
+  const int nrb = route_blocks(tokens);
+  return nrb > kScanChunk ? (nrb + kScanChunk - 1) / kScanChunk : 0;
+}
+
 hipError_t launch_group(const int64_t* indices, int64_t tokens, int experts,
-                        int capacity, const int32_t* block_counts,
+                        int capacity, const int32_t* block_counts, int32_t* chunk_totals,
                         int32_t* positions, int32_t* counts, int32_t* offsets,
                         int32_t* perm, int32_t* overflow, hipStream_t s) {
   const int nrb = route_blocks(tokens);
+  const int n_chunks = route_chunks(tokens);
+  if (n_chunks > 0) {
+    chunk_sum_kernel<<<n_chunks, 256, 0, s>>>(block_counts, nrb, experts, chunk_totals);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  }
   const int64_t assign_blocks = (2 * tokens + kGroupAssign - 1) / kGroupAssign;
   const int64_t fill_blocks = (static_cast<int64_t>(experts) * capacity + kGroupAssign - 1) / kGroupAssign;
   const int grid = static_cast<int>(max(max(assign_blocks, fill_blocks), int64_t{1}));
   group_kernel<<<grid, 256, 0, s>>>(indices, tokens, experts, capacity, nrb, block_counts,
+                                    n_chunks > 0 ? chunk_totals : nullptr, n_chunks,
                                     positions, counts, offsets, perm, overflow);
   return hipGetLastError();
 }

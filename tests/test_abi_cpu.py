@@ -53,7 +53,12 @@ def test_capacity_matches_oracle(lib):
 
 
 def test_workspace_sizes(lib):
-    assert lib.parrot_route_workspace_bytes(512, 16) >= 8 * 16 * 4
+    # one int32 histogram row of E counts per 16-token route block ...
+    assert lib.parrot_route_workspace_bytes(512, 16) >= 32 * 16 * 4
+    assert lib.parrot_route_workspace_bytes(4096, 16) >= 256 * 16 * 4
+    # ... plus one row per 256 route blocks once there is more than one chunk
+    assert lib.parrot_route_workspace_bytes(65536, 16) >= (4096 + 16) * 16 * 4
+    assert lib.parrot_route_workspace_bytes(4097, 32) >= (257 + 2) * 32 * 4
     small = lib.parrot_experts_workspace_bytes(8, 768, 512, 256)
     big = lib.parrot_experts_workspace_bytes(512, 768, 512, 256)
     assert big > small > 0

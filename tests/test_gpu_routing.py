@@ -56,7 +56,8 @@ def test_route_from_logits_bit_exact(tokens, experts, skewed):
 
 
 @pytest.mark.parametrize("tokens,experts,skewed", [(256, 32, False), (4096, 32, True),
-                                                   (512, 16, False), (5, 16, False)])
+                                                   (512, 16, False), (5, 16, False),
+                                                   (16421, 16, False), (20000, 32, True)])
 def test_route_projection(tokens, experts, skewed):
     """HIP logits ~ fp32 logits; HIP top-2 == oracle top-2 of the HIP logits."""
     from parrot import hip_moe
@@ -87,6 +88,9 @@ def test_group_indices_adversarial():
         "one_expert": np.stack([np.zeros(3000), np.arange(3000) % 15 + 1], 1),
         "round_robin": np.stack([np.arange(512) % 16, (np.arange(512) + 1) % 16], 1),
         "two_experts": np.stack([np.zeros(700), np.ones(700)], 1),
+        # long enough for the two-level histogram scan (> 256 route blocks)
+        "long_skewed": np.stack([np.zeros(40001), np.arange(40001) % 7 + 1], 1),
+        "long_uniform": np.stack([np.arange(9000) % 16, (np.arange(9000) * 5 + 3) % 16], 1),
     }
     for name, idx in cases.items():
         _say(f"group_indices {name}")
