@@ -29,10 +29,6 @@ namespace parrot {
 
 namespace {
 
-constexpr int kBK = 64;        // k per pipeline stage
-constexpr int kLdsPad = 8;     // bf16 padding per LDS row (keeps b128 reads conflict-free)
-constexpr int kLdsStride = kBK + kLdsPad;
-
 struct GemmArgs {
   const uint16_t* a_src;      // phase 1: x [T, dim]; phase 2: hidden [3T, hstride]
   int64_t tokens;
@@ -97,9 +93,67 @@ struct WaveLayout {
   static constexpr int kWavesN = 4 / kWavesM;
 };
 
-// Occupancy is bounded by LDS (two workgroups per CU), so let each wave
-// use up to 256 VGPRs rather than squeezing registers for occupancy.
-template <int BM, int BN, int PHASE>
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Waits until at most N vector-memory loads of this wavefront are
+// outstanding, then joins the workgroup barrier.  Written out because
+// __syncthreads() would also wait for every in-flight direct-to-LDS load
+// (vmcnt(0)), which drains the stage ring on every k step.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(N) : "memory");
+}
+
+// 16 bytes per lane from a buffer straight into LDS: lane l's bytes land at
+// lds + 16 l (buffer_load_dwordx4 ... lds).  Reads past the buffer end
+// return zero.
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* lds,
+                                                uint32_t voffset, uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voffset, soffset, 0, 0);
+}
+
+// One 16-byte MFMA fragment from LDS, read with inline asm so the compiler
+// does not treat it as an LDS access: otherwise it cannot tell the ring slot
+// being read from the slots the in-flight direct-to-LDS loads fill, and
+// waits for all of them (vmcnt(0)), draining the pipeline every step.  The
+// ring's ordering is explicit instead (wait_vm_barrier), and the caller waits
+// for the reads with lds_wait before using the fragments.
+__device__ __forceinline__ bf16x8 lds_read_frag(const uint16_t* p) {
+  const uint32_t addr = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)p));
+  bf16x8 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Waits for every outstanding LDS read of this wavefront, then ties the
+// fragments to the wait so no use of them is scheduled before it.
+template <int NA, int NB>
+__device__ __forceinline__ void lds_wait(bf16x8 (&a)[NA], bf16x8 (&b)[NB]) {
+  asm volatile("s_waitcnt lgkmcnt(0)");
+#pragma unroll
+  for (int i = 0; i < NA; ++i) asm volatile("" : "+v"(a[i]));
+#pragma unroll
+  for (int i = 0; i < NB; ++i) asm volatile("" : "+v"(b[i]));
+}
+
+// ---------------------------------------------------------------------------
+// LDS-pipelined grouped GEMM: a ring of S k-stages (BK = 64) in LDS, filled
+// by direct-to-LDS buffer loads with S - 1 stages in flight while the MFMAs
+// consume the oldest; one barrier per k step.
+//
+// Every operand tile is stored in LDS in MFMA fragment order: 1 KB blocks of
+// 16 rows x 32 k where lane l's 16 bytes (row l % 16, k 8 (l / 16) .. +8) sit
+// at byte 16 l.  A direct-to-LDS load writes lane l's 16 bytes at 16 l, so
+// one wavefront load fills one block, and one ds_read_b128 per lane reads a
+// whole fragment without bank conflicts.  The packed weights are already in
+// this order in HBM (each block is 1 KB contiguous); A blocks are gathered
+// row by row through the index map.
+//
+// Stage layout: A blocks (m-tile i, k half h) at block 2 i + h, then B
+// blocks (16-column group g, k half h) at block BM / 8 + 2 g + h.  Wavefront w
+// loads blocks [w P, w P + P) of every stage, P = (BM + BN) / 32.
+template <int BM, int BN, int S, int PHASE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void grouped_gemm_kernel(GemmArgs p) {
   constexpr int kWavesM = WaveLayout<BM>::kWavesM;
@@ -108,22 +162,23 @@ void grouped_gemm_kernel(GemmArgs p) {
   constexpr int kWaveN = BN / kWavesN;
   constexpr int kTilesM = kWaveM / 16;
   constexpr int kTilesN = kWaveN / 16;
-  constexpr int kAVec = BM * (kBK / 8);  // 16-byte vectors per A stage
-  constexpr int kBVec = BN * (kBK / 8);
-  constexpr int kAPer = (kAVec + 255) / 256;
-  constexpr int kBPer = kBVec / 256;
+  constexpr int kABlocks = BM / 8;                      // 16-row tiles x 2 k halves
+  constexpr int kBlocks = (BM + BN) / 8;
+  constexpr int P = kBlocks / 4;                        // loads per wavefront per stage
+  constexpr int kStageElems = kBlocks * 512;
+  static_assert(kBlocks % 4 == 0, "stage blocks must split evenly over 4 wavefronts");
   static_assert(PHASE != 1 || kWaveN % 32 == 0, "gate/up pairs need 32-column wave tiles");
-  static_assert(kBVec % 256 == 0, "B stage must split evenly over 256 threads");
-  static_assert(kAPer <= 4, "A stage holds at most 4 vectors per thread");
+  static_assert(S >= 2, "the ring needs at least two stages");
 
-  __shared__ __attribute__((aligned(16))) uint16_t a_lds[2][BM][kLdsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t b_lds[2][BN][kLdsStride];
+  __shared__ __attribute__((aligned(16))) uint16_t ring[S][kStageElems];
   __shared__ int row_src[BM];
   __shared__ int row_dst[BM];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid >> 6;
+  // Uniform by construction; readfirstlane lets the compiler keep the
+  // per-wavefront load choice (A or B buffer, LDS block) in SGPRs.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = static_cast<int>(p.tokens);
 
   int seg = -1, mt = 0, rows = 0;
@@ -133,48 +188,7 @@ void grouped_gemm_kernel(GemmArgs p) {
   const int K = PHASE == 1 ? p.dim : (shared ? p.shared_dim : p.hidden_dim);
   const int n0 = static_cast<int>(blockIdx.x) * BN;
   if (n0 >= N) return;
-
-  // ---- weights: the first two stages go out before the row lookups --------
-  const uint16_t* wbase = shared ? p.w_shared
-                                 : p.w_routed + static_cast<int64_t>(seg) * N * K;
-  const __amdgpu_buffer_rsrc_t b_rsrc =
-      make_rsrc(wbase, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
-  // B arrives in MFMA fragment order (1 KB blocks of 16 rows x 32 k, lane l's
-  // 16 bytes at 16 l).  Vector v = tid + 256 i of a stage is lane v % 64 of
-  // block v / 64 = (16-row group (v / 64) / 2, 32-k half (v / 64) % 2); it
-  // lands in LDS row 16 group + lane % 16, k chunk 4 half + lane / 16.
-  // Rows past N lie past the buffer end and read zero.
-  const int ksteps32 = K / 32;
-  uint32_t b_off[4];
-  int b_lrow[4], b_lcol[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int v = tid + 256 * i;
-    const int blk = v >> 6, l = v & 63;
-    const int grp = blk >> 1, half = blk & 1;
-    b_off[i] = static_cast<uint32_t>(((n0 / 16 + grp) * ksteps32 + half) * 64 + l) * 16;
-    b_lrow[i] = grp * 16 + (l & 15);
-    b_lcol[i] = (half * 4 + (l >> 4)) * 8;
-  }
-  static_assert(kBPer == 4, "B stage is 1024 vectors: 4 per thread");
-  // Two register stages (P, Q) of global loads are in flight while the
-  // MFMAs consume the current LDS stage; LDS is double-buffered, one
-  // barrier per 64-wide k step.  Every load is issued unconditionally (stage
-  // index clamped to the last stage) so the compiler can wait for exactly
-  // the stage being stored while the next one stays in flight.
-  uint4 pa0, pa1, pa2, pa3, pb0, pb1, pb2, pb3;
-  uint4 qa0, qa1, qa2, qa3, qb0, qb1, qb2, qb3;
-#define PARROT_LOAD_B(R, kt)                                                                \
-  do {                                                                                      \
-    const uint32_t kb = static_cast<uint32_t>(kt) * 2048;  /* two 1 KB blocks per stage */ \
-    R##b0 = buffer_load16(b_rsrc, b_off[0], kb);                                            \
-    R##b1 = buffer_load16(b_rsrc, b_off[1], kb);                                            \
-    R##b2 = buffer_load16(b_rsrc, b_off[2], kb);                                            \
-    R##b3 = buffer_load16(b_rsrc, b_off[3], kb);                                            \
-  } while (0)
-  const int KT = K / kBK;
-  PARROT_LOAD_B(p, 0);
-  PARROT_LOAD_B(q, min(1, KT - 1));
+  const int KT = K / 64;
 
   // ---- per-row source / destination ---------------------------------------
   if (tid < BM) {
@@ -202,98 +216,100 @@ void grouped_gemm_kernel(GemmArgs p) {
   }
   __syncthreads();
 
-  // Thread -> 16-byte vector of an A stage: vector v = tid + 256 i covers
-  // row v / 8, k-columns 8 (v % 8) .. +8, so 8 neighbouring threads read one
-  // 128-byte row segment.  Threads beyond the A stage (BM = 16) load a
-  // duplicate vector so every load is unconditional; only the owning threads
-  // store it to LDS.
+  // ---- this lane's loads: one 16-byte piece of each of its P blocks -------
   const int a_ld = PHASE == 1 ? p.dim : p.hstride;
   const int64_t a_rows = PHASE == 1 ? p.tokens : 3 * p.tokens;
   const __amdgpu_buffer_rsrc_t a_rsrc =
       make_rsrc(p.a_src, static_cast<uint32_t>(a_rows * a_ld * 2));
-  const uint32_t col_bytes = (tid & 7) * 16;
-  const uint32_t a_off0 = row_src[(tid % kAVec) >> 3] * a_ld * 2 + col_bytes;
-  const uint32_t a_off1 = row_src[((tid + 256) % kAVec) >> 3] * a_ld * 2 + col_bytes;
-  const uint32_t a_off2 = row_src[((tid + 512) % kAVec) >> 3] * a_ld * 2 + col_bytes;
-  const uint32_t a_off3 = row_src[((tid + 768) % kAVec) >> 3] * a_ld * 2 + col_bytes;
-  const int col8 = (tid & 7) * 8;
-#define PARROT_LOAD_A(R, kt)                                                                \
-  do {                                                                                      \
-    const uint32_t ko = static_cast<uint32_t>(kt) * (kBK * 2);                              \
-    R##a0 = buffer_load16(a_rsrc, a_off0, ko);                                              \
-    if (kAPer > 1) R##a1 = buffer_load16(a_rsrc, a_off1, ko);                               \
-    if (kAPer > 2) R##a2 = buffer_load16(a_rsrc, a_off2, ko);                               \
-    if (kAPer > 3) R##a3 = buffer_load16(a_rsrc, a_off3, ko);                               \
-  } while (0)
-#define PARROT_STORE_STAGE(R, buf)                                                          \
-  do {                                                                                      \
-    if (kAVec >= 256 || tid < kAVec)                                                        \
-      *reinterpret_cast<uint4*>(&a_lds[buf][(tid % kAVec) >> 3][col8]) = R##a0;             \
-    if (kAPer > 1) *reinterpret_cast<uint4*>(&a_lds[buf][(tid + 256) >> 3][col8]) = R##a1;  \
-    if (kAPer > 2) *reinterpret_cast<uint4*>(&a_lds[buf][(tid + 512) >> 3][col8]) = R##a2;  \
-    if (kAPer > 3) *reinterpret_cast<uint4*>(&a_lds[buf][(tid + 768) >> 3][col8]) = R##a3;  \
-    *reinterpret_cast<uint4*>(&b_lds[buf][b_lrow[0]][b_lcol[0]]) = R##b0;                   \
-    *reinterpret_cast<uint4*>(&b_lds[buf][b_lrow[1]][b_lcol[1]]) = R##b1;                   \
-    *reinterpret_cast<uint4*>(&b_lds[buf][b_lrow[2]][b_lcol[2]]) = R##b2;                   \
-    *reinterpret_cast<uint4*>(&b_lds[buf][b_lrow[3]][b_lcol[3]]) = R##b3;                   \
-  } while (0)
-#define PARROT_LOAD_STAGE(R, kt)                                                            \
-  do {                                                                                      \
-    PARROT_LOAD_A(R, kt);                                                                   \
-    PARROT_LOAD_B(R, kt);                                                                   \
-  } while (0)
+  const uint16_t* wbase = shared ? p.w_shared
+                                 : p.w_routed + static_cast<int64_t>(seg) * N * K;
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_rsrc(wbase, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
+  const int ksteps32 = K / 32;
+  uint32_t voff[P];
+  bool is_a[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int b = wave * P + i;
+    is_a[i] = b < kABlocks;
+    if (b < kABlocks) {
+      // A block (m-tile b / 2, k half b % 2): row 16 (b / 2) + l % 16,
+      // k 32 (b % 2) + 8 (l / 16); the stage adds 128 bytes of k.
+      const int r = row_src[(b >> 1) * 16 + (lane & 15)];
+      voff[i] = static_cast<uint32_t>(r * a_ld + (b & 1) * 32 + (lane >> 4) * 8) * 2;
+    } else {
+      // B block (group g, k half h) = packed block (n0 / 16 + g, 2 kt + h);
+      // the stage adds two blocks (2 KB).  Groups past N read zero.
+      const int g = (b - kABlocks) >> 1, h = (b - kABlocks) & 1;
+      voff[i] = static_cast<uint32_t>(((n0 / 16 + g) * ksteps32 + h) * 1024 + lane * 16);
+    }
+  }
+  auto issue = [&](uint16_t* stage, int kt) {
+    const int ks = min(kt, KT - 1);
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      uint16_t* dst = stage + (wave * P + i) * 512;
+      if (is_a[i]) buffer_to_lds16(a_rsrc, dst, voff[i], static_cast<uint32_t>(ks) * 128);
+      else buffer_to_lds16(b_rsrc, dst, voff[i], static_cast<uint32_t>(ks) * 2048);
+    }
+  };
 
-  const int wm0 = (wave / kWavesN) * kWaveM;
-  const int wn0 = (wave % kWavesN) * kWaveN;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
   f32x4 acc[kTilesM][kTilesN];
 #pragma unroll
   for (int i = 0; i < kTilesM; ++i)
 #pragma unroll
     for (int j = 0; j < kTilesN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-#define PARROT_COMPUTE(buf)                                                                 \
-  do {                                                                                      \
-    _Pragma("unroll") for (int kk = 0; kk < kBK / 32; ++kk) {                               \
-      bf16x8 af[kTilesM], bfr[kTilesN];                                                     \
-      _Pragma("unroll") for (int i = 0; i < kTilesM; ++i)                                   \
-        af[i] = *reinterpret_cast<const bf16x8*>(                                           \
-            &a_lds[buf][wm0 + i * 16 + (lane & 15)][kk * 32 + (lane >> 4) * 8]);            \
-      _Pragma("unroll") for (int j = 0; j < kTilesN; ++j)                                   \
-        bfr[j] = *reinterpret_cast<const bf16x8*>(                                          \
-            &b_lds[buf][wn0 + j * 16 + (lane & 15)][kk * 32 + (lane >> 4) * 8]);            \
-      _Pragma("unroll") for (int i = 0; i < kTilesM; ++i)                                   \
-        _Pragma("unroll") for (int j = 0; j < kTilesN; ++j)                                 \
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0); \
-    }                                                                                       \
-  } while (0)
-
-  PARROT_LOAD_A(p, 0);
-  PARROT_LOAD_A(q, min(1, KT - 1));
-  PARROT_STORE_STAGE(p, 0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; kt += 2) {
-    // even step: LDS buffer 0 holds stage kt, registers q hold stage kt + 1
-    PARROT_LOAD_STAGE(p, min(kt + 2, KT - 1));
-    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
-    PARROT_COMPUTE(0);
-    PARROT_STORE_STAGE(q, 1);
-    __syncthreads();
-    if (kt + 1 >= KT) break;
-    // odd step: LDS buffer 1 holds stage kt + 1, registers p hold stage kt + 2
-    PARROT_LOAD_STAGE(q, min(kt + 3, KT - 1));
+  // Fragment reads go through lds_read_frag (see there); the k half h = 1
+  // reads are in flight while the h = 0 MFMAs run.
+  auto compute = [&](const uint16_t* stage) {
+    bf16x8 a0[kTilesM], b0[kTilesN], a1[kTilesM], b1[kTilesN];
+#pragma unroll
+    for (int i = 0; i < kTilesM; ++i)
+      a0[i] = lds_read_frag(stage + ((wm * kTilesM + i) * 2) * 512 + lane * 8);
+#pragma unroll
+    for (int j = 0; j < kTilesN; ++j)
+      b0[j] = lds_read_frag(stage + (kABlocks + (wn * kTilesN + j) * 2) * 512 + lane * 8);
+    lds_wait(a0, b0);
+#pragma unroll
+    for (int i = 0; i < kTilesM; ++i)
+      a1[i] = lds_read_frag(stage + ((wm * kTilesM + i) * 2 + 1) * 512 + lane * 8);
+#pragma unroll
+    for (int j = 0; j < kTilesN; ++j)
+      b1[j] = lds_read_frag(stage + (kABlocks + (wn * kTilesN + j) * 2 + 1) * 512 + lane * 8);
+#pragma unroll
+    for (int i = 0; i < kTilesM; ++i)
+#pragma unroll
+      for (int j = 0; j < kTilesN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[i], b0[j], acc[i][j], 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    PARROT_COMPUTE(1);
-    PARROT_STORE_STAGE(p, 0);
-    __syncthreads();
+    lds_wait(a1, b1);
+#pragma unroll
+    for (int i = 0; i < kTilesM; ++i)
+#pragma unroll
+      for (int j = 0; j < kTilesN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+  };
+
+  // k step kt computes slot kt % S and refills slot (kt - 1) % S with stage
+  // kt + S - 1.  Stages past the last are reloads of the last one into
+  // slots that are never read again, so every step issues the same P loads
+  // and waits for the same count: stage kt has landed for every wavefront,
+  // and every wavefront is done reading stage kt - 1, whose slot gets
+  // refilled.
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st) issue(ring[st], st);
+  for (int kt = 0; kt < KT; ++kt) {
+    wait_vm_barrier<P * (S - 2)>();
+    issue(ring[(kt + S - 1) % S], kt + S - 1);
+    compute(ring[kt % S]);
   }
-#undef PARROT_LOAD_A
-#undef PARROT_LOAD_B
-#undef PARROT_LOAD_STAGE
-#undef PARROT_STORE_STAGE
-#undef PARROT_COMPUTE
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue --------------------------------------------------------------
   // C fragment: lane holds column (lane & 15) of rows 4 * (lane >> 4) + r.
+  const int wm0 = wm * kWaveM, wn0 = wn * kWaveN;
   if (PHASE == 1) {
 #pragma unroll
     for (int jp = 0; jp < kTilesN / 2; ++jp) {
@@ -333,7 +349,7 @@ void grouped_gemm_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Streaming variant for small row tiles (BM <= 64, K <= kStreamKCap): the
+// Streaming variant for small row tiles (BM <= 32, K <= kStreamKCap): the
 // weight-streaming regime of prefill and decode.
 //
 // The workgroup's whole A tile (BM gathered rows x K) is copied into LDS once
@@ -346,8 +362,6 @@ void grouped_gemm_kernel(GemmArgs p) {
 // as its MFMAs have consumed it.  The k loop has no barrier.
 // Wavefront w owns output columns [w WN, w WN + WN) of the 4 WN-wide tile.
 constexpr int kStreamKCap = 768;  // largest K whose A tile fits the LDS budget
-
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 template <int BM, int WN, int PF, int PHASE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
@@ -505,13 +519,13 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int S>
 hipError_t launch_phase(int phase, const GemmArgs& args, int n_max, hipStream_t s) {
   const int T = static_cast<int>(args.tokens);
   const int m_tiles = (T + BM - 1) / BM + (2 * T) / BM + args.experts;
   const dim3 grid((n_max + BN - 1) / BN, m_tiles);
-  if (phase == 1) grouped_gemm_kernel<BM, BN, 1><<<grid, 256, 0, s>>>(args);
-  else grouped_gemm_kernel<BM, BN, 2><<<grid, 256, 0, s>>>(args);
+  if (phase == 1) grouped_gemm_kernel<BM, BN, S, 1><<<grid, 256, 0, s>>>(args);
+  else grouped_gemm_kernel<BM, BN, S, 2><<<grid, 256, 0, s>>>(args);
   return hipGetLastError();
 }
 
@@ -551,10 +565,14 @@ hipError_t run_stream(int phase, GemmArgs args, int n_max, hipStream_t s) {
   }
 }
 
-template <int BM, bool STREAM>
+// Tile plans.  kStreamBM: the streaming kernel with BM-row tiles when every
+// K fits its LDS budget (else the pipelined kernel with 32- or 64-row
+// tiles); kTiled64: the pipelined kernel with 64-row tiles.
+enum class TilePlan { kStream16, kStream32, kTiled64 };
+
+template <TilePlan PLAN>
 hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t* hidden,
                      hipStream_t s) {
-  constexpr int BN = 128;
   int n_max;
   if (phase == 1) {
     args.w_routed = w.gate_up;
@@ -568,23 +586,26 @@ hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t*
     n_max = args.dim;
   }
   const int k_max = phase == 1 ? args.dim : max(args.hidden_dim, args.shared_dim);
-  if (STREAM && k_max <= kStreamKCap) return run_stream<BM>(phase, args, n_max, s);
-  return launch_phase<BM, BN>(phase, args, n_max, s);
+  if constexpr (PLAN != TilePlan::kTiled64) {
+    constexpr int BM = PLAN == TilePlan::kStream16 ? 16 : 32;
+    if (k_max <= kStreamKCap) return run_stream<BM>(phase, args, n_max, s);
+    return launch_phase<32, 128, 3>(phase, args, n_max, s);
+  } else {
+    return launch_phase<64, 128, 3>(phase, args, n_max, s);
+  }
 }
 
 // Kernel and row tile per launch, chosen from T and E only (the per-expert
-// counts stay on the device).  While an expert's rows fit one small tile the
-// launch is weight-streaming bound and the streaming kernel wins (every extra
-// row tile re-streams that expert's weights); with more rows per expert the
-// LDS-tiled kernel with 64-row tiles, which shares each staged weight tile
-// across four wavefronts, is faster.
-enum class TilePlan { kStream16, kStream32, kStream64, kTiled64 };
-
+// counts stay on the device).  Measured on MI355X: while an expert holds up
+// to ~3 x 32 rows the launch is weight-streaming bound and the streaming
+// kernel with 32-row tiles is fastest (more, smaller workgroups keep more
+// weight loads in flight, and the re-streamed tiles of one expert mostly hit
+// L2); with more rows per expert the pipelined kernel with 64-row tiles and a
+// 3-stage ring (two workgroups per CU) is.
 TilePlan experts_tile_plan(int64_t tokens, int experts) {
   const int64_t per_expert = (2 * tokens + experts - 1) / experts;
   if (tokens <= 16) return TilePlan::kStream16;
-  if (per_expert <= 24) return TilePlan::kStream32;
-  if (per_expert <= 48) return TilePlan::kStream64;
+  if (per_expert <= 96) return TilePlan::kStream32;
   return TilePlan::kTiled64;
 }
 
@@ -612,10 +633,9 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
   args.y_routed = y_routed;
   args.y_shared = y_shared;
   switch (experts_tile_plan(tokens, experts)) {
-    case TilePlan::kStream16: return run_phase<16, true>(phase, args, w, hidden, s);
-    case TilePlan::kStream32: return run_phase<32, true>(phase, args, w, hidden, s);
-    case TilePlan::kStream64: return run_phase<64, true>(phase, args, w, hidden, s);
-    default: return run_phase<64, false>(phase, args, w, hidden, s);
+    case TilePlan::kStream16: return run_phase<TilePlan::kStream16>(phase, args, w, hidden, s);
+    case TilePlan::kStream32: return run_phase<TilePlan::kStream32>(phase, args, w, hidden, s);
+    default: return run_phase<TilePlan::kTiled64>(phase, args, w, hidden, s);
   }
 }
 

@@ -118,6 +118,27 @@ def test_moe_layer(name, tokens, experts, skewed):
     assert mx2 <= MAX_ABS and mean2 <= MEAN_ABS
 
 
+@pytest.mark.parametrize("tokens,experts,dim,hidden,shared", [
+    (40, 8, 1024, 1280, 256),     # small-T plan with K > 768: pipelined 32-row tiles
+    (1200, 8, 1024, 1280, 256),   # many rows per expert: pipelined 64-row tiles
+    (300, 4, 2048, 512, 192),     # widest supported dim
+])
+def test_moe_layer_other_widths(tokens, experts, dim, hidden, shared):
+    from parrot import hip_moe
+    _say(f"moe layer T={tokens} E={experts} dim={dim} H={hidden} Hs={shared}")
+    module = moe_module(experts, seed=7, dim=dim, hidden=hidden, shared=shared)
+    x = inputs(tokens, seed=7, dim=dim)
+    with torch.no_grad():
+        routed = hip_moe.route(module, x, False)
+        out = hip_moe.grouped_hip_experts(module, x, routed.indices, routed.weights,
+                                          grouping=routed.grouping)
+    ref, _, _, _ = oracle_moe(module, x, indices=routed.indices.cpu().numpy(),
+                              weights=routed.weights.cpu().numpy())
+    mx, mean = error_stats(out, ref)
+    _say(f"  max-abs {mx:.3e} mean-abs {mean:.3e}")
+    assert mx <= MAX_ABS and mean <= MEAN_ABS
+
+
 def test_moe_addend_and_tiny_shapes():
     from parrot import hip_moe
     _say("moe addend + tiny widths")
