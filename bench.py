@@ -307,8 +307,12 @@ def sweep_kernels(moe, iters: int) -> dict:
 
 def decode_bench(model, steps: int = 16) -> dict:
     """prefill a 128-token prompt (seed 3), then `steps`
-    greedy decode steps, at batch 1, 2, 4 and 8 (eager; 4096-position caches)."""
+    greedy decode steps, at batch 1, 2, 4 and 8 (4096-position caches):
+    eager `decode_next` steps, and the same steps replayed from one captured
+    HIP graph (`parrot.decode_graph.DecodeGraph`; its one-time capture is
+    reported separately)."""
     import torch
+    from parrot.decode_graph import DecodeGraph
     dev = torch.device("cuda:0")
     out = {}
     for b in (1, 2, 4, 8):
@@ -323,17 +327,39 @@ def decode_bench(model, steps: int = 16) -> dict:
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             logits, state = model.prefill(prompt)
-            nxt = logits[:, -1].argmax(-1, keepdim=True)
+            first = logits[:, -1].argmax(-1, keepdim=True)
             torch.cuda.synchronize()
             t1 = time.perf_counter()
+            nxt = first
             for _ in range(steps):
                 nxt, state = model.decode_next(nxt, state)
             torch.cuda.synchronize()
             t2 = time.perf_counter()
+            eager_tokens = nxt.clone()
+
+            logits, state = model.prefill(prompt)
+            torch.cuda.synchronize()
+            t3 = time.perf_counter()
+            graph = DecodeGraph(model, state)
+            torch.cuda.synchronize()
+            t4 = time.perf_counter()
+            nxt = first
+            for _ in range(steps):
+                nxt = graph.step(nxt)
+            torch.cuda.synchronize()
+            t5 = time.perf_counter()
+            if not torch.equal(nxt, eager_tokens):
+                raise RuntimeError("graph-replayed decoding differs from eager decoding")
+            del graph
         out[f"b{b}"] = {"prefill_ms": round((t1 - t0) * 1e3, 3),
-                        "decode_ms_per_step": round((t2 - t1) * 1e3 / steps, 3),
-                        "decode_tokens_per_s": round(b * steps / (t2 - t1), 1),
-                        "generation_tokens_per_s": round(b * steps / (t2 - t0), 1)}
+                        "eager_decode_ms_per_step": round((t2 - t1) * 1e3 / steps, 3),
+                        "eager_decode_tokens_per_s": round(b * steps / (t2 - t1), 1),
+                        "eager_generation_tokens_per_s": round(b * steps / (t2 - t0), 1),
+                        "graph_capture_ms": round((t4 - t3) * 1e3, 1),
+                        "graph_decode_ms_per_step": round((t5 - t4) * 1e3 / steps, 3),
+                        "graph_decode_tokens_per_s": round(b * steps / (t5 - t4), 1),
+                        "graph_generation_tokens_per_s": round(
+                            b * steps / ((t1 - t0) + (t5 - t4)), 1)}
     return out
 
 

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 1
+#define PARROT_ABI_VERSION 2
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -76,15 +76,55 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
  *   q [batch, H, seq, head_dim]; k, v [batch, Hk, seq, head_dim], or
  *   [batch, H, seq, head_dim] with every kv head repeated H / Hk times when
  *   expand_kv != 0.
- * Pairs (2i, 2i+1) of q and k rotate by angle (start + s) * theta^(-2i/d)
- * read from fp32 tables cos_table / sin_table [max_positions, head_dim / 2];
- * v is copied.  head_dim % 4 == 0, H % Hk == 0, start + seq <= max_positions.
+ * Pairs (2i, 2i+1) of q and k rotate by angle p * theta^(-2i/d) at position
+ * p = start + s, plus *start_device when start_device (a device int32) is
+ * non-NULL, read from fp32 tables cos_table / sin_table
+ * [max_positions, head_dim / 2]; positions past the table are clamped to its
+ * last row (a device position cannot be checked here).  v is copied.
+ * head_dim % 4 == 0, H % Hk == 0, start + seq <= max_positions.
  * Replaces LocalGQA._project / _project_decode / _rope
  * (parrot/model.py:206-262), which run RoPE as strided bf16 elementwise ops. */
 int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* sin_table,
-                         int64_t batch, int32_t seq, int32_t start, int32_t max_positions,
-                         int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t expand_kv,
-                         void* q, void* k, void* v, void* stream);
+                         int64_t batch, int32_t seq, int32_t start, const int32_t* start_device,
+                         int32_t max_positions, int32_t heads, int32_t kv_heads,
+                         int32_t head_dim, int32_t expand_kv, void* q, void* k, void* v,
+                         void* stream);
+
+/* Decode-step attention of the sliding-window GQA layers.  q [batch, H,
+ * head_dim] and the new key / value rows k_new, v_new [batch, Hk, head_dim]
+ * (RoPE applied, bf16); caches [batch, Hk, max_positions, head_dim] bf16.
+ * With p = *position (device int32): stores k_new / v_new at cache position
+ * p and writes out [batch, H, head_dim] (bf16) =
+ * softmax(q . K^T * scale) V over positions max(0, p - window + 1) .. p of
+ * each query head's kv head (head h uses kv head h / (H / Hk)); fp32 scores,
+ * softmax and accumulation.  Nothing is written when p is outside
+ * [0, max_positions).  head_dim % 8 == 0, head_dim <= 256,
+ * (min(window, max_positions) + 5 head_dim + 4) * 4 <= 65536; caches and new
+ * rows 16-byte aligned.  Reading p from device memory keeps the shapes
+ * static, so a decode step can be captured in a HIP graph.
+ * Replaces the cache update + scaled_dot_product_attention of
+ * LocalGQA.decode (parrot/model.py:239-262) and the Metal kernel
+ * local_attention_decode_bf16 (parrot/kernels/moe_bf16.metal:1203-1362). */
+int parrot_decode_attention_bf16(const void* q, const void* k_new, const void* v_new,
+                                 void* key_cache, void* value_cache, const int32_t* position,
+                                 int32_t batch, int32_t heads, int32_t kv_heads,
+                                 int32_t head_dim, int32_t max_positions, int32_t window,
+                                 float scale, void* out, void* stream);
+
+/* Decode-step attention of the MLA layers over the joint latent cache.
+ * q [batch, H, latent_dim] fp32 (the query through the absorbed key
+ * up-projection), latent_new [batch, latent_dim] bf16, latent_cache
+ * [batch, max_positions, latent_dim] bf16.  With p = *position: stores
+ * latent_new at position p and writes out [batch, H, latent_dim] (fp32) =
+ * softmax(q . Lat^T * scale) Lat over positions 0 .. p, the latents serving
+ * as both keys and values.  Limits as parrot_decode_attention_bf16 with
+ * window = max_positions.  Replaces the cache update + attention of
+ * GlobalMLA.decode (parrot/model.py:399-432) and the Metal kernel
+ * mla_attention_decode_bf16 (parrot/kernels/moe_bf16.metal:1391-1518). */
+int parrot_decode_attention_latent_f32(const float* q, const void* latent_new, void* latent_cache,
+                                       const int32_t* position, int32_t batch, int32_t heads,
+                                       int32_t latent_dim, int32_t max_positions, float scale,
+                                       float* out, void* stream);
 
 /* Workspace bytes for the routing / grouping entry points. */
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts);

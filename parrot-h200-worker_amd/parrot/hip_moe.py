@@ -309,25 +309,88 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
 # ---------------------------------------------------------------------------
 
 def rope_qkv(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, kv_heads: int, head_dim: int,
-             start: int, expand_kv: bool) -> tuple[Tensor, Tensor, Tensor]:
+             start: int, expand_kv: bool,
+             start_device: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """Split a packed q|k|v projection [b, t, (H + 2 Hk) d] into head-major
     q [b, H, t, d], k, v [b, Hk or H, t, d] and rotate q and k by RoPE at
-    positions start .. start + t - 1 (fp32 tables [max_positions, d / 2])."""
+    positions start .. start + t - 1 (fp32 tables [max_positions, d / 2]),
+    shifted by the device int32 ``start_device`` when given."""
     _require(qkv, "HIP RoPE")
     b, t, width = qkv.shape
     if width != (heads + 2 * kv_heads) * head_dim:
         raise RuntimeError("packed q|k|v width does not match the head layout")
     if cos.dtype != torch.float32 or sin.dtype != torch.float32:
         raise RuntimeError("RoPE tables must be fp32")
+    if start_device is not None and (start_device.dtype != torch.int32 or
+                                     start_device.device != qkv.device):
+        raise RuntimeError("start_device must be an int32 tensor on the projection's device")
     qkv = qkv.contiguous()
     kv_out = heads if expand_kv else kv_heads
     q = qkv.new_empty((b, heads, t, head_dim))
     k = qkv.new_empty((b, kv_out, t, head_dim))
     v = qkv.new_empty((b, kv_out, t, head_dim))
     _abi.check(_abi.load().parrot_rope_qkv_bf16(
-        ptr(qkv), ptr(cos), ptr(sin), b, t, start, cos.shape[0], heads, kv_heads, head_dim,
-        int(expand_kv), ptr(q), ptr(k), ptr(v), _stream(qkv.device)), "parrot_rope_qkv_bf16")
+        ptr(qkv), ptr(cos), ptr(sin), b, t, start, ptr(start_device), cos.shape[0], heads,
+        kv_heads, head_dim, int(expand_kv), ptr(q), ptr(k), ptr(v), _stream(qkv.device)),
+        "parrot_rope_qkv_bf16")
     return q, k, v
+
+
+# ---------------------------------------------------------------------------
+# Decode-step attention over the generation caches (cf. parrot/model.py:239-262,
+# 399-432; parrot/kernels/moe_bf16.metal:1203-1518)
+# ---------------------------------------------------------------------------
+
+def _check_position(position: Tensor, device: torch.device) -> None:
+    if position.dtype != torch.int32 or position.device != device or position.numel() != 1:
+        raise RuntimeError("position must be a one-element int32 tensor on the cache's device")
+
+
+def decode_attention(q: Tensor, k_new: Tensor, v_new: Tensor, key_cache: Tensor,
+                     value_cache: Tensor, position: Tensor, window: int,
+                     scale: float) -> Tensor:
+    """One decode step of sliding-window GQA: store k_new / v_new [b, Hk, 1, d]
+    at cache position p = position (device int32) and attend q [b, H, 1, d]
+    over positions max(0, p - window + 1) .. p.  Returns [b, H * d] bf16."""
+    _require(q, "HIP decode attention")
+    b, heads, t, d = q.shape
+    _, kv_heads, max_pos, _ = key_cache.shape
+    if t != 1 or k_new.shape != (b, kv_heads, 1, d) or v_new.shape != k_new.shape:
+        raise RuntimeError("decode attention takes one new position per sequence")
+    if key_cache.shape != (b, kv_heads, max_pos, d) or value_cache.shape != key_cache.shape:
+        raise RuntimeError("cache shapes do not match the heads")
+    if not (key_cache.is_contiguous() and value_cache.is_contiguous()):
+        raise RuntimeError("caches must be contiguous")
+    _check_position(position, q.device)
+    q, k_new, v_new = q.contiguous(), k_new.contiguous(), v_new.contiguous()
+    out = q.new_empty((b, heads * d))
+    _abi.check(_abi.load().parrot_decode_attention_bf16(
+        ptr(q), ptr(k_new), ptr(v_new), ptr(key_cache), ptr(value_cache), ptr(position),
+        b, heads, kv_heads, d, max_pos, window, scale, ptr(out), _stream(q.device)),
+        "parrot_decode_attention_bf16")
+    return out
+
+
+def decode_attention_latent(q: Tensor, latent_new: Tensor, latent_cache: Tensor,
+                            position: Tensor, heads: int, scale: float) -> Tensor:
+    """One MLA decode step over the latent cache: store latent_new [b, 1, r]
+    at position p and attend the fp32 absorbed queries q [b, 1, H * r] over
+    latents 0 .. p (keys = values).  Returns the fp32 context [b, H * r]."""
+    b, max_pos, r = latent_cache.shape
+    if q.dtype != torch.float32 or q.device.type != "cuda" or torch.is_grad_enabled():
+        raise RuntimeError("HIP latent decode attention takes fp32 ROCm queries without grad")
+    _require(latent_new, "HIP latent decode attention")
+    if q.numel() != b * heads * r or latent_new.shape != (b, 1, r):
+        raise RuntimeError("latent decode shapes do not match the cache")
+    if not latent_cache.is_contiguous():
+        raise RuntimeError("latent cache must be contiguous")
+    _check_position(position, q.device)
+    q, latent_new = q.contiguous(), latent_new.contiguous()
+    out = q.new_empty((b, heads * r))
+    _abi.check(_abi.load().parrot_decode_attention_latent_f32(
+        ptr(q), ptr(latent_new), ptr(latent_cache), ptr(position), b, heads, r, max_pos, scale,
+        ptr(out), _stream(q.device)), "parrot_decode_attention_latent_f32")
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -146,11 +146,13 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
 }
 
 int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* sin_table,
-                         int64_t batch, int32_t seq, int32_t start, int32_t max_positions,
-                         int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t expand_kv,
-                         void* q, void* k, void* v, void* stream) {
+                         int64_t batch, int32_t seq, int32_t start, const int32_t* start_device,
+                         int32_t max_positions, int32_t heads, int32_t kv_heads,
+                         int32_t head_dim, int32_t expand_kv, void* q, void* k, void* v,
+                         void* stream) {
   if (!qkv || !cos_table || !sin_table || !q || !k || !v) return PARROT_ERR_NULL_POINTER;
-  if (batch < 0 || seq < 0 || start < 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0)
+  if (batch < 0 || seq < 0 || start < 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
+      max_positions <= 0)
     return PARROT_ERR_BAD_SHAPE;
   if (heads % kv_heads || head_dim % 4) return PARROT_ERR_UNSUPPORTED;
   if (static_cast<int64_t>(start) + seq > max_positions) return PARROT_ERR_BAD_SHAPE;
@@ -158,9 +160,52 @@ int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* s
                          reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v);
   if (bits & 7u) return PARROT_ERR_ALIGNMENT;
   return status(parrot::launch_rope_qkv(
-      static_cast<const uint16_t*>(qkv), cos_table, sin_table, batch, seq, start, heads,
-      kv_heads, head_dim, expand_kv, static_cast<uint16_t*>(q), static_cast<uint16_t*>(k),
-      static_cast<uint16_t*>(v), as_stream(stream)));
+      static_cast<const uint16_t*>(qkv), cos_table, sin_table, batch, seq, start, start_device,
+      max_positions, heads, kv_heads, head_dim, expand_kv, static_cast<uint16_t*>(q),
+      static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), as_stream(stream)));
+}
+
+static int check_decode_shape(int32_t batch, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                              int32_t max_positions, int32_t window) {
+  if (batch < 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 || max_positions <= 0 ||
+      window <= 0)
+    return PARROT_ERR_BAD_SHAPE;
+  if (heads % kv_heads || head_dim % 8 || head_dim > parrot::kMaxDecodeHeadDim)
+    return PARROT_ERR_UNSUPPORTED;
+  if (parrot::decode_attention_lds_bytes(window, max_positions, head_dim) > parrot::kMaxDecodeLds)
+    return PARROT_ERR_UNSUPPORTED;
+  return PARROT_OK;
+}
+
+int parrot_decode_attention_bf16(const void* q, const void* k_new, const void* v_new,
+                                 void* key_cache, void* value_cache, const int32_t* position,
+                                 int32_t batch, int32_t heads, int32_t kv_heads,
+                                 int32_t head_dim, int32_t max_positions, int32_t window,
+                                 float scale, void* out, void* stream) {
+  if (!q || !k_new || !v_new || !key_cache || !value_cache || !position || !out)
+    return PARROT_ERR_NULL_POINTER;
+  if (int rc = check_decode_shape(batch, heads, kv_heads, head_dim, max_positions, window))
+    return rc;
+  if (!aligned16(k_new) || !aligned16(v_new) || !aligned16(key_cache) || !aligned16(value_cache))
+    return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_decode_attention(
+      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new),
+      static_cast<const uint16_t*>(v_new), static_cast<uint16_t*>(key_cache),
+      static_cast<uint16_t*>(value_cache), position, batch, heads, kv_heads, head_dim,
+      max_positions, window, scale, static_cast<uint16_t*>(out), as_stream(stream)));
+}
+
+int parrot_decode_attention_latent_f32(const float* q, const void* latent_new, void* latent_cache,
+                                       const int32_t* position, int32_t batch, int32_t heads,
+                                       int32_t latent_dim, int32_t max_positions, float scale,
+                                       float* out, void* stream) {
+  if (!q || !latent_new || !latent_cache || !position || !out) return PARROT_ERR_NULL_POINTER;
+  if (int rc = check_decode_shape(batch, heads, 1, latent_dim, max_positions, max_positions))
+    return rc;
+  if (!aligned16(latent_new) || !aligned16(latent_cache)) return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_decode_attention_latent(
+      q, static_cast<const uint16_t*>(latent_new), static_cast<uint16_t*>(latent_cache),
+      position, batch, heads, latent_dim, max_positions, scale, out, as_stream(stream)));
 }
 
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts) {

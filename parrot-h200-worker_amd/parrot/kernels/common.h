@@ -143,10 +143,27 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
                               float* y_routed, float* y_shared, hipStream_t s);
 
 // RoPE + head-major split of a packed q|k|v projection (see rope.hip).
+// The first position is start (+ *start_device when non-null); positions
+// past the table are clamped to its last row.
 hipError_t launch_rope_qkv(const uint16_t* qkv, const float* cos_t, const float* sin_t,
-                           int64_t batch, int seq, int start, int heads, int kv_heads,
-                           int head_dim, int expand_kv, uint16_t* q, uint16_t* k,
-                           uint16_t* v, hipStream_t s);
+                           int64_t batch, int seq, int start, const int32_t* start_device,
+                           int max_positions, int heads, int kv_heads, int head_dim,
+                           int expand_kv, uint16_t* q, uint16_t* k, uint16_t* v, hipStream_t s);
+
+// Decode-step attention over the generation caches (see decode.hip); the
+// position is read from device memory.
+constexpr int kMaxDecodeHeadDim = 256;
+constexpr size_t kMaxDecodeLds = 64 * 1024;  // dynamic LDS without an opt-in
+size_t decode_attention_lds_bytes(int window, int max_pos, int head_dim);
+hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_new,
+                                   const uint16_t* v_new, uint16_t* k_cache, uint16_t* v_cache,
+                                   const int32_t* position, int batch, int heads, int kv_heads,
+                                   int head_dim, int max_pos, int window, float scale,
+                                   uint16_t* out, hipStream_t s);
+hipError_t launch_decode_attention_latent(const float* q, const uint16_t* latent_new,
+                                          uint16_t* latent_cache, const int32_t* position,
+                                          int batch, int heads, int latent_dim, int max_pos,
+                                          float scale, float* out, hipStream_t s);
 
 hipError_t launch_combine(const float* y_routed, const float* y_shared,
                           const uint16_t* addend, int64_t tokens, int dim,

@@ -5,7 +5,8 @@
 // pair i of the head width rotates as
 //   out[2i] = x[2i] cos(p w_i) - x[2i+1] sin(p w_i)
 //   out[2i+1] = x[2i] sin(p w_i) + x[2i+1] cos(p w_i),   w_i = theta^(-2i/d),
-// at model position p = start + row; values are not rotated.  The angle
+// at model position p = start + row (+ a position read from device memory,
+// for graph-captured decode steps); values are not rotated.  The angle
 // tables are fp32 here and each output is rounded to bf16 once.
 // Input: qkv [rows = batch * seq, (H + 2 Hk) * d] (one packed projection).
 // Output: q [batch, H, seq, d], k and v [batch, Hk or H, seq, d]; with
@@ -19,9 +20,10 @@ namespace {
 
 __global__ __launch_bounds__(256) void rope_qkv_kernel(
     const uint2* __restrict__ qkv, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, int64_t rows, int seq, int start, int heads,
-    int kv_heads, int head_dim, int expand, uint16_t* __restrict__ q,
-    uint16_t* __restrict__ k, uint16_t* __restrict__ v) {
+    const float* __restrict__ sin_t, int64_t rows, int seq, int start,
+    const int32_t* __restrict__ start_device, int max_positions, int heads, int kv_heads,
+    int head_dim, int expand, uint16_t* __restrict__ q, uint16_t* __restrict__ k,
+    uint16_t* __restrict__ v) {
   const int quads = (heads + 2 * kv_heads) * head_dim / 4;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= rows * quads) return;
@@ -34,7 +36,9 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(
   uint2 x = qkv[i];
   if (head < heads + kv_heads) {
     const int half = head_dim / 2;
-    const int64_t pos = static_cast<int64_t>(start + tp) * half + w / 2;
+    int p = start + tp + (start_device != nullptr ? *start_device : 0);
+    p = min(max(p, 0), max_positions - 1);  // a device position is not validated on the host
+    const int64_t pos = static_cast<int64_t>(p) * half + w / 2;
     const float c0 = cos_t[pos], s0 = sin_t[pos];
     const float c1 = cos_t[pos + 1], s1 = sin_t[pos + 1];
     const float e0 = lo_bf16(x.x), o0 = hi_bf16(x.x);
@@ -64,15 +68,16 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(
 }  // namespace
 
 hipError_t launch_rope_qkv(const uint16_t* qkv, const float* cos_t, const float* sin_t,
-                           int64_t batch, int seq, int start, int heads, int kv_heads,
-                           int head_dim, int expand_kv, uint16_t* q, uint16_t* k,
-                           uint16_t* v, hipStream_t s) {
+                           int64_t batch, int seq, int start, const int32_t* start_device,
+                           int max_positions, int heads, int kv_heads, int head_dim,
+                           int expand_kv, uint16_t* q, uint16_t* k, uint16_t* v, hipStream_t s) {
   const int64_t rows = batch * seq;
   const int64_t total = rows * (heads + 2 * kv_heads) * head_dim / 4;
   if (total == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((total + 255) / 256));
   rope_qkv_kernel<<<grid, 256, 0, s>>>(reinterpret_cast<const uint2*>(qkv), cos_t, sin_t, rows,
-                                       seq, start, heads, kv_heads, head_dim, expand_kv, q, k, v);
+                                       seq, start, start_device, max_positions, heads, kv_heads,
+                                       head_dim, expand_kv, q, k, v);
   return hipGetLastError();
 }
 

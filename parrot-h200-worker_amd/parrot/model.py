@@ -137,6 +137,10 @@ class GenerationState:
     layers: list[LocalKVCache | MLALatentCache]
     position: int
     batch_size: int
+    # The same position as a one-element int32 tensor on the cache device,
+    # advanced on the device each step; set by prefill on the HIP backend,
+    # whose decode kernels read it, so a decode step has static shapes.
+    position_device: Tensor | None = None
 
 
 @dataclass
@@ -315,13 +319,26 @@ class LocalGQA(nn.Module):
         return cached[1]
 
     def decode(self, x: Tensor, cache: LocalKVCache, position: int,
-               addend: Tensor | None = None, defer_sum: bool = False) -> Tensor:
+               addend: Tensor | None = None, defer_sum: bool = False,
+               position_device: Tensor | None = None) -> Tensor:
         if x.shape[1] != 1:
             raise ValueError("decode expects one model position")
         if defer_sum:
             raise RuntimeError("deferred attention reduction is not supported on this backend")
         c = self.cfg
         b = x.shape[0]
+        if self._hip(x) and position_device is not None:
+            # RoPE at the device position, then one kernel stores the new key
+            # and value and attends over the window (parrot/model.py:239-262).
+            from . import hip_moe
+            cos, sin = _rope_tables(c, x.new_empty(0, dtype=torch.float32))
+            q, k, v = hip_moe.rope_qkv(F.linear(x, self._packed_qkv()), cos, sin, c.n_heads,
+                                       c.n_kv_heads, c.head_dim, 0, False,
+                                       start_device=position_device)
+            y = hip_moe.decode_attention(q, k, v, cache.key, cache.value, position_device,
+                                         c.window_size, c.head_dim ** -0.5)
+            result = self.out(y.view(b, 1, -1))
+            return result if addend is None else addend + result
         if self._hip(x):
             q, k, v = self._qkv(x, start=position)
         else:
@@ -398,14 +415,34 @@ class GlobalMLA(nn.Module):
             self.__dict__["_absorbed_weights"] = cached
         return cached[1]
 
+    def _absorbed_f32(self) -> tuple[Tensor, Tensor]:
+        """fp32 copies of the absorbed maps, cached with them."""
+        pair = self._absorbed()
+        cached = self.__dict__.get("_absorbed_f32_weights")
+        if cached is None or cached[0] is not pair:
+            cached = (pair, (pair[0].float(), pair[1].float()))
+            self.__dict__["_absorbed_f32_weights"] = cached
+        return cached[1]
+
     def decode(self, x: Tensor, cache: MLALatentCache, position: int,
-               addend: Tensor | None = None, defer_sum: bool = False) -> Tensor:
+               addend: Tensor | None = None, defer_sum: bool = False,
+               position_device: Tensor | None = None) -> Tensor:
         if x.shape[1] != 1:
             raise ValueError("decode expects one model position")
         if defer_sum:
             raise RuntimeError("deferred attention reduction is not supported on this backend")
         c = self.cfg
         b = x.shape[0]
+        if c.uses_hip and _hip_inference(x) and position_device is not None:
+            # One kernel stores the new latent and attends over the latent
+            # cache at the device position (parrot/model.py:399-432).
+            from . import hip_moe
+            absorbed_q, absorbed_o = self._absorbed_f32()
+            context = hip_moe.decode_attention_latent(
+                F.linear(x.float(), absorbed_q), self.kv_down(x), cache.latent, position_device,
+                c.n_heads, c.head_dim ** -0.5)
+            result = F.linear(context.view(b, 1, -1), absorbed_o).to(x.dtype)
+            return result if addend is None else addend + result
         absorbed_q, absorbed_o = self._absorbed()
         cache.latent[:, position:position + 1].copy_(self.kv_down(x))
         latent = cache.latent[:, :position + 1].float()
@@ -716,7 +753,10 @@ class Parrot(nn.Module):
         if stream is not None:
             x = self.depth_mix[-1](stream.sources())
         logits = F.linear(self.final_norm(x[:, -1:]), self.embedding.weight)
-        return logits, GenerationState(caches, t, b)
+        position_device = None
+        if cfg.uses_hip and _hip_inference(logits):
+            position_device = torch.full((1,), t, dtype=torch.int32, device=logits.device)
+        return logits, GenerationState(caches, t, b, position_device)
 
     @torch.inference_mode()
     def decode_step(self, input_ids: Tensor, state: GenerationState, *,
@@ -742,7 +782,8 @@ class Parrot(nn.Module):
                     raise ValueError("Local attention received an MLA cache")
             elif not isinstance(cache, MLALatentCache):
                 raise ValueError("MLA attention received a local cache")
-            out = block.attention.decode(h, cache, state.position, addend=addend)
+            out = block.attention.decode(h, cache, state.position, addend=addend,
+                                         position_device=state.position_device)
             if stream is None:
                 x = x + out
             else:
@@ -761,6 +802,8 @@ class Parrot(nn.Module):
             h = self.final_norm(x)
         logits = F.linear(h, self.embedding.weight)
         state.position += 1
+        if state.position_device is not None:
+            state.position_device.add_(1)
         return (logits.argmax(-1) if _next_token_only else logits), state
 
     @torch.inference_mode()

@@ -39,7 +39,10 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_version_and_status_strings(lib):
-    assert lib.parrot_abi_version() == 1
+    from parrot import _abi
+    header = (ROOT / "include" / "parrot_hip.h").read_text()
+    assert f"#define PARROT_ABI_VERSION {_abi.ABI_VERSION}" in header
+    assert lib.parrot_abi_version() == _abi.ABI_VERSION
     assert lib.parrot_status_string(0) == b"ok"
     for code in (-1, -2, -3, -4, -5):
         assert lib.parrot_status_string(code) != b"unknown status"
@@ -94,3 +97,25 @@ def test_argument_validation_without_gpu(lib):
         fake, 64, 96, 8, 128, 64, 32, *([fake] * 9), null, fake, fake, 1 << 30, null) == -3
     assert lib.parrot_grouped_experts_bf16(
         fake, 64, 64, 8, 128, 64, 32, *([fake] * 9), null, fake, fake, 16, null) == -4
+    # RoPE: start + seq past the table
+    assert lib.parrot_rope_qkv_bf16(fake, fake, fake, 1, 4, 126, null, 128, 8, 2, 96, 0,
+                                    fake, fake, fake, null) == -2
+    # decode attention: null position, head_dim % 8, heads % kv_heads, LDS budget, alignment
+    dec = dict(batch=2, heads=8, kv_heads=2, head_dim=96, max_positions=4096, window=2048)
+
+    def local(position=fake, k_new=fake, **kw):
+        a = {**dec, **kw}
+        return lib.parrot_decode_attention_bf16(
+            fake, k_new, fake, fake, fake, position, a["batch"], a["heads"], a["kv_heads"],
+            a["head_dim"], a["max_positions"], a["window"], 0.1, fake, null)
+    assert local(position=null) == -1
+    assert local(head_dim=100) == -3
+    assert local(head_dim=264) == -3
+    assert local(heads=6, kv_heads=4) == -3
+    assert local(window=0) == -2
+    assert local(window=1 << 20, max_positions=1 << 20) == -3
+    assert local(k_new=fake + 8) == -5
+    assert lib.parrot_decode_attention_latent_f32(fake, fake, fake, null, 2, 8, 128, 4096, 0.1,
+                                                  fake, null) == -1
+    assert lib.parrot_decode_attention_latent_f32(fake, fake, fake, fake, 2, 8, 128, 1 << 16,
+                                                  0.1, fake, null) == -3
