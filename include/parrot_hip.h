@@ -98,9 +98,9 @@ int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* s
  * softmax(q . K^T * scale) V over positions max(0, p - window + 1) .. p of
  * each query head's kv head (head h uses kv head h / (H / Hk)); fp32 scores,
  * softmax and accumulation.  Nothing is written when p is outside
- * [0, max_positions).  head_dim % 8 == 0, head_dim <= 256,
- * (min(window, max_positions) + 5 head_dim + 4) * 4 <= 65536; caches and new
- * rows 16-byte aligned.  Reading p from device memory keeps the shapes
+ * [0, max_positions).  head_dim in {8, 16, 32, 64, 96, 128, 192, 256},
+ * (min(window, max_positions) + head_dim + 2048 + 4) * 4 <= 65536; caches
+ * and new rows 16-byte aligned.  Reading p from device memory keeps the shapes
  * static, so a decode step can be captured in a HIP graph.
  * Replaces the cache update + scaled_dot_product_attention of
  * LocalGQA.decode (parrot/model.py:239-262) and the Metal kernel
@@ -125,6 +125,33 @@ int parrot_decode_attention_latent_f32(const float* q, const void* latent_new, v
                                        const int32_t* position, int32_t batch, int32_t heads,
                                        int32_t latent_dim, int32_t max_positions, float scale,
                                        float* out, void* stream);
+
+/* Workspace bytes of parrot_decode_moe_bf16: hidden rows [3T, max(H, Hs)]
+ * bf16. */
+size_t parrot_decode_moe_workspace_bytes(int64_t tokens, int32_t hidden_dim,
+                                         int32_t shared_dim);
+
+/* Whole MoE layer for a decode step of tokens <= 16 rows x [tokens, dim]
+ * (bf16) in two launches: router logits (fp32, + logit_bias when non-NULL),
+ * top-2 with ties to the lower expert index and weights renormalised over
+ * the two (written to out_indices [tokens, 2] int64 / out_weights
+ * [tokens, 2] fp32); SwiGLU of both routed experts and the shared expert
+ * (hidden rounded to bf16); out = bf16(shared + w0 y0 + w1 y1), or
+ * bf16(addend + bf16(...)) with an addend.  Packed weights as for
+ * parrot_grouped_experts_bf16.  Every assignment is computed (capacity and
+ * overflow do not apply at these sizes).  2 <= experts <= 32; dim, H, Hs
+ * multiples of 64.  Replaces metal_experts_decode (parrot/metal_moe.py:
+ * 182-221; kernels moe_decode_lanes_bf16 / moe_sum_decode_lanes_bf16,
+ * parrot/kernels/moe_bf16.metal:894-1024, 1185-1201) and, for these sizes,
+ * the route + grouped-experts path of MoE.inference (parrot/model.py:
+ * 571-607). */
+int parrot_decode_moe_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,
+                           int32_t hidden_dim, int32_t shared_dim, const void* router_weight,
+                           const float* logit_bias, const void* packed_gate_up,
+                           const void* packed_down, const void* shared_gate_up,
+                           const void* shared_down, const void* addend, void* out,
+                           int64_t* out_indices, float* out_weights, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /* Workspace bytes for the routing / grouping entry points. */
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts);

@@ -48,9 +48,13 @@ def _require(x: Tensor, what: str, dtypes=(torch.bfloat16,)) -> None:
 
 def _scratch(owner, name: str, nbytes: int, device: torch.device) -> Tensor:
     """Reusable byte workspace kept outside the module's state_dict
-    (cf. parrot/metal_moe.py:15-23)."""
+    (cf. parrot/metal_moe.py:15-23).  A buffer that is outgrown stays
+    referenced (never freed): a HIP graph captured earlier may still read
+    and write it on replay."""
     cached = owner.__dict__.get(name)
     if cached is None or cached.numel() < nbytes or cached.device != device:
+        if cached is not None:
+            owner.__dict__.setdefault("_hip_retired_scratch", []).append(cached)
         cached = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
         owner.__dict__[name] = cached
     return cached
@@ -302,6 +306,46 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
         ptr(shared_down), ptr(addend), ptr(out), ptr(ws), nbytes, _stream(flat.device)),
         "parrot_grouped_experts_bf16")
     return out
+
+
+DECODE_MAX_TOKENS = 16  # rows the fused decode MoE takes
+
+
+def decode_experts(module: "MoE", flat: Tensor, addend: Tensor | None = None,
+                   logit_bias: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+    """The whole MoE layer for at most DECODE_MAX_TOKENS rows in two launches
+    (route + gate/up + SwiGLU, then down + weighted combine): returns
+    ``(out, indices [T, 2] int64, weights [T, 2] fp32)`` with ``out`` =
+    ``addend + delta`` when an addend is given (cf. metal_experts_decode,
+    parrot/metal_moe.py:182-221)."""
+    _require(flat, "The fused HIP decode MoE")
+    cfg = module.cfg
+    tokens, dim = flat.shape
+    if tokens > DECODE_MAX_TOKENS:
+        raise RuntimeError(f"the fused decode MoE takes at most {DECODE_MAX_TOKENS} rows")
+    if cfg.top_k != 2 or cfg.n_experts > MAX_EXPERTS:
+        raise RuntimeError(f"HIP experts support top-2 of at most {MAX_EXPERTS} experts")
+    flat = flat.contiguous()
+    gate_up, down, shared_gate_up, shared_down = pack_expert_weights(module)
+    if addend is not None:
+        _require(addend, "MoE addend")
+        addend = addend.reshape(tokens, dim).contiguous()
+    bias = None
+    if logit_bias is not None:
+        bias = logit_bias.to(device=flat.device, dtype=torch.float32).contiguous()
+    lib = _abi.load()
+    nbytes = lib.parrot_decode_moe_workspace_bytes(DECODE_MAX_TOKENS, cfg.expert_dim,
+                                                   cfg.shared_expert_dim)
+    ws = _scratch(module, "_hip_decode_workspace", nbytes, flat.device)
+    out = torch.empty_like(flat)
+    indices = torch.empty((tokens, 2), dtype=torch.int64, device=flat.device)
+    weights = torch.empty((tokens, 2), dtype=torch.float32, device=flat.device)
+    _abi.check(lib.parrot_decode_moe_bf16(
+        ptr(flat), tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim,
+        ptr(module.router.weight), ptr(bias), ptr(gate_up), ptr(down), ptr(shared_gate_up),
+        ptr(shared_down), ptr(addend), ptr(out), ptr(indices), ptr(weights), ptr(ws), nbytes,
+        _stream(flat.device)), "parrot_decode_moe_bf16")
+    return out, indices, weights
 
 
 # ---------------------------------------------------------------------------

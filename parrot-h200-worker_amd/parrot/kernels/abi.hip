@@ -170,7 +170,7 @@ static int check_decode_shape(int32_t batch, int32_t heads, int32_t kv_heads, in
   if (batch < 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 || max_positions <= 0 ||
       window <= 0)
     return PARROT_ERR_BAD_SHAPE;
-  if (heads % kv_heads || head_dim % 8 || head_dim > parrot::kMaxDecodeHeadDim)
+  if (heads % kv_heads || !parrot::decode_head_dim_supported(head_dim))
     return PARROT_ERR_UNSUPPORTED;
   if (parrot::decode_attention_lds_bytes(window, max_positions, head_dim) > parrot::kMaxDecodeLds)
     return PARROT_ERR_UNSUPPORTED;
@@ -377,6 +377,45 @@ int parrot_experts_combine_bf16(int64_t tokens, int32_t dim, int32_t hidden_dim,
   return status(parrot::launch_combine(ws.y_routed, ws.y_shared,
                                        static_cast<const uint16_t*>(addend), tokens, dim,
                                        static_cast<uint16_t*>(out), as_stream(stream)));
+}
+
+size_t parrot_decode_moe_workspace_bytes(int64_t tokens, int32_t hidden_dim,
+                                         int32_t shared_dim) {
+  if (tokens < 0 || hidden_dim <= 0 || shared_dim <= 0) return 0;
+  const size_t hstride = static_cast<size_t>(hidden_dim > shared_dim ? hidden_dim : shared_dim);
+  return round_up(3 * static_cast<size_t>(tokens) * hstride * sizeof(uint16_t));
+}
+
+int parrot_decode_moe_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,
+                           int32_t hidden_dim, int32_t shared_dim, const void* router_weight,
+                           const float* logit_bias, const void* packed_gate_up,
+                           const void* packed_down, const void* shared_gate_up,
+                           const void* shared_down, const void* addend, void* out,
+                           int64_t* out_indices, float* out_weights, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (!x || !router_weight || !packed_gate_up || !packed_down || !shared_gate_up ||
+      !shared_down || !out || !out_indices || !out_weights)
+    return PARROT_ERR_NULL_POINTER;
+  if (tokens < 0 || dim <= 0 || hidden_dim <= 0 || shared_dim <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (tokens > parrot::decode_moe_max_tokens() || experts < 2 || experts > parrot::kMaxExperts ||
+      dim % 64 || hidden_dim % 64 || shared_dim % 64)
+    return PARROT_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < parrot_decode_moe_workspace_bytes(tokens, hidden_dim,
+                                                                        shared_dim))
+    return PARROT_ERR_WORKSPACE;
+  if (!aligned16(x) || !aligned16(router_weight) || !aligned16(packed_gate_up) ||
+      !aligned16(packed_down) || !aligned16(shared_gate_up) || !aligned16(shared_down) ||
+      !aligned16(workspace))
+    return PARROT_ERR_ALIGNMENT;
+  parrot::ExpertWeights w{static_cast<const uint16_t*>(packed_gate_up),
+                          static_cast<const uint16_t*>(packed_down),
+                          static_cast<const uint16_t*>(shared_gate_up),
+                          static_cast<const uint16_t*>(shared_down)};
+  return status(parrot::launch_decode_moe(
+      static_cast<const uint16_t*>(x), static_cast<int>(tokens), dim, experts, hidden_dim,
+      shared_dim, static_cast<const uint16_t*>(router_weight), logit_bias, w,
+      static_cast<const uint16_t*>(addend), static_cast<uint16_t*>(out), out_indices,
+      out_weights, static_cast<uint16_t*>(workspace), as_stream(stream)));
 }
 
 int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,

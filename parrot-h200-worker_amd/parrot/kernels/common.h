@@ -63,6 +63,81 @@ __device__ __forceinline__ float wave_sum(float v) {
   return ((r0 + r1) + r2) + r3;
 }
 
+// ---------------------------------------------------------------------------
+// Top-2 across a row of 16 lanes (route.hip, decode_moe.hip)
+// ---------------------------------------------------------------------------
+// A token's logits are spread over one DPP row: lane j holds experts j and
+// j + 16.  Selection is a max-reduction of 64-bit keys (order-preserving
+// float bits, then the complemented expert index), so equal logits go to
+// the lower expert index: the strict '>' scan in expert order of the
+// reference.
+
+// Order-preserving map of a float to uint32 (-0 canonicalised to +0, so it
+// ties with +0 as it does under '>').
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t u = __float_as_uint(v + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t expert_key(float v, int e) {
+  return (static_cast<uint64_t>(order_key(v)) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
+}
+
+// Inverse of order_key on the high word of a key.
+__device__ __forceinline__ float key_value(uint64_t k) {
+  const uint32_t o = static_cast<uint32_t>(k >> 32);
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+__device__ __forceinline__ int key_expert(uint64_t k) {
+  return static_cast<int>(0xffffffffu - static_cast<uint32_t>(k));
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_max_key(uint64_t k) {
+  const int lo = static_cast<int>(static_cast<uint32_t>(k));
+  const int hi = static_cast<int>(static_cast<uint32_t>(k >> 32));
+  const uint32_t olo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xf, 0xf, false));
+  const uint32_t ohi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xf, 0xf, false));
+  const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;
+  return o > k ? o : k;
+}
+
+// Max over the 16 lanes of a DPP row, returned to every lane of the row
+// (xor 1, xor 2 inside quads, then half-row and row mirrors).
+__device__ __forceinline__ uint64_t row_max_key(uint64_t k) {
+  k = dpp_max_key<0xb1>(k);
+  k = dpp_max_key<0x4e>(k);
+  k = dpp_max_key<0x141>(k);
+  return dpp_max_key<0x140>(k);
+}
+
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp<0xb1>(v);
+  v += dpp<0x4e>(v);
+  v += dpp<0x141>(v);
+  return v + dpp<0x140>(v);
+}
+
+// Top-2 of the logits a DPP row holds (lane j: experts j -> l0 and j + 16 ->
+// l1, the latter ignored unless experts > 16): the two expert ids and their
+// logits, returned to every lane of the row.
+__device__ __forceinline__ void row_top2(float l0, float l1, int experts, int& first,
+                                         int& second, float& best_logit, float& runner_logit) {
+  const int j = threadIdx.x & 15;
+  constexpr uint64_t kNone = 0;  // below every real key
+  const uint64_t k0 = j < experts ? expert_key(l0, j) : kNone;
+  const uint64_t k1 = j + 16 < experts ? expert_key(l1, j + 16) : kNone;
+  const uint64_t mine = k1 > k0 ? k1 : k0;  // k0 wins ties: lower index
+  const uint64_t other = k1 > k0 ? k0 : k1;
+  const uint64_t best = row_max_key(mine);
+  const uint64_t runner = row_max_key(mine == best ? other : mine);
+  first = key_expert(best);
+  second = key_expert(runner);
+  best_logit = key_value(best);
+  runner_logit = key_value(runner);
+}
+
 // silu(g) * u with silu(g) = g / (1 + e^-g), evaluated in fp32.
 __device__ __forceinline__ float swiglu(float g, float u) {
   return (g / (1.0f + __expf(-g))) * u;
@@ -152,8 +227,8 @@ hipError_t launch_rope_qkv(const uint16_t* qkv, const float* cos_t, const float*
 
 // Decode-step attention over the generation caches (see decode.hip); the
 // position is read from device memory.
-constexpr int kMaxDecodeHeadDim = 256;
 constexpr size_t kMaxDecodeLds = 64 * 1024;  // dynamic LDS without an opt-in
+bool decode_head_dim_supported(int head_dim);  // 8, 16, 32, 64, 96, 128, 192, 256
 size_t decode_attention_lds_bytes(int window, int max_pos, int head_dim);
 hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_new,
                                    const uint16_t* v_new, uint16_t* k_cache, uint16_t* v_cache,
@@ -164,6 +239,15 @@ hipError_t launch_decode_attention_latent(const float* q, const uint16_t* latent
                                           uint16_t* latent_cache, const int32_t* position,
                                           int batch, int heads, int latent_dim, int max_pos,
                                           float scale, float* out, hipStream_t s);
+
+// Fused MoE layer for T <= decode_moe_max_tokens() tokens (see
+// decode_moe.hip): route + gate/up + SwiGLU, then down + weighted combine
+// (+ addend).  `hidden` is scratch [3T, max(H, Hs)] bf16.
+int decode_moe_max_tokens();
+hipError_t launch_decode_moe(const uint16_t* x, int tokens, int dim, int experts, int hidden_dim,
+                             int shared_dim, const uint16_t* router_w, const float* bias,
+                             const ExpertWeights& w, const uint16_t* addend, uint16_t* out,
+                             int64_t* indices, float* weights, uint16_t* hidden, hipStream_t s);
 
 hipError_t launch_combine(const float* y_routed, const float* y_shared,
                           const uint16_t* addend, int64_t tokens, int dim,

@@ -12,10 +12,10 @@
 // p is read from device memory, so a decode step has static shapes and can
 // be captured once in a HIP graph and replayed as the position advances.
 //
-// One workgroup per (query head, sequence).  Scores: one key per thread
-// (16-byte loads of the key row, fp32 dot with the query in LDS); softmax in
-// fp32 over the scores kept in LDS; values: wavefront w takes keys w, w + 4,
-// ... and lane u accumulates dims 2u, 2u + 1; the four wavefront partials are
+// One workgroup per (query head, sequence).  Scores: one key per thread,
+// all 16-byte chunks of its row loaded at once, fp32 dot with the query in
+// LDS; softmax in fp32 over the scores kept in LDS; values: each thread owns
+// one 16-byte chunk of the rows of a key slot, and the slot partials are
 // added in a fixed order.  The key and value at p are read from the new rows
 // (not from the cache being written), so no workgroup waits for another.
 #include "common.h"
@@ -60,26 +60,26 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return r;
 }
 
-template <typename QT, typename OT>
+// CH = head_dim / 8 16-byte chunks per key / value row.
+template <typename QT, typename OT, int CH>
 __global__ __launch_bounds__(256) void decode_attention_kernel(
     const QT* __restrict__ q, const uint16_t* __restrict__ k_new,
     const uint16_t* __restrict__ v_new, uint16_t* __restrict__ k_cache,
     uint16_t* __restrict__ v_cache, const int32_t* __restrict__ position, int heads,
-    int kv_heads, int head_dim, int max_pos, int window, float scale, OT* __restrict__ out) {
+    int kv_heads, int max_pos, int window, float scale, OT* __restrict__ out) {
+  constexpr int D = CH * 8;
+  constexpr int kSlots = 256 / CH;  // value pass: key slots x chunks
   extern __shared__ float smem[];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid >> 6;
-  const int D = head_dim;
   const int rep = heads / kv_heads;
   const int kvh = h / rep;
   const int lcap = min(window, max_pos);
-  float* s = smem;           // [lcap] scores, then probabilities
-  float* qs = s + lcap;      // [D]
-  float* part = qs + D;      // [4][D]
-  float* red = part + 4 * D; // [4]
+  float* s = smem;                 // [lcap] scores, then probabilities
+  float* qs = s + lcap;            // [D]
+  float* part = qs + D;            // [kSlots][D]
+  float* red = part + kSlots * D;  // [4]
 
   const int pos = *position;
   if (pos < 0 || pos >= max_pos) return;  // uniform: nothing to attend to
@@ -101,17 +101,22 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   for (int i = tid; i < D; i += 256) qs[i] = to_f32(q[(static_cast<int64_t>(b) * heads + h) * D + i]);
   __syncthreads();
 
-  // Scores, one key per thread.
+  // Scores: one key per thread per pass, every chunk of its row in flight.
   float mx = -INFINITY;
   for (int j = tid; j < L; j += 256) {
     const int key = lo + j;
-    const uint16_t* row = key == pos ? kn : kc + static_cast<int64_t>(key) * D;
+    const uint4* row = reinterpret_cast<const uint4*>(
+        key == pos ? kn : kc + static_cast<int64_t>(key) * D);
+    uint4 kr[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) kr[c] = row[c];
     float acc = 0.0f;
-    for (int c = 0; c < D; c += 8) {
-      const uint4 v = *reinterpret_cast<const uint4*>(row + c);
-      acc += lo_bf16(v.x) * qs[c] + hi_bf16(v.x) * qs[c + 1] + lo_bf16(v.y) * qs[c + 2] +
-             hi_bf16(v.y) * qs[c + 3] + lo_bf16(v.z) * qs[c + 4] + hi_bf16(v.z) * qs[c + 5] +
-             lo_bf16(v.w) * qs[c + 6] + hi_bf16(v.w) * qs[c + 7];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const float* qc = qs + c * 8;
+      acc += lo_bf16(kr[c].x) * qc[0] + hi_bf16(kr[c].x) * qc[1] + lo_bf16(kr[c].y) * qc[2] +
+             hi_bf16(kr[c].y) * qc[3] + lo_bf16(kr[c].z) * qc[4] + hi_bf16(kr[c].z) * qc[5] +
+             lo_bf16(kr[c].w) * qc[6] + hi_bf16(kr[c].w) * qc[7];
     }
     acc *= scale;
     s[j] = acc;
@@ -126,47 +131,88 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   }
   sum = block_sum(sum, red);  // also orders the probability writes before the reads below
 
-  // Values: wavefront w takes keys w, w + 4, ...; lane u dims 2u, 2u + 1
-  // (and 2u + 128, 2u + 129 when D > 128; D <= kMaxDecodeHeadDim).
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  const int pairs = D / 2;
-  for (int j = wave; j < L; j += 4) {
-    const int key = lo + j;
-    const uint32_t* row = reinterpret_cast<const uint32_t*>(
-        key == pos ? vn : vc + static_cast<int64_t>(key) * D);
-    const float p = s[j];
-    if (lane < pairs) {
-      const uint32_t w = row[lane];
-      a0 += p * lo_bf16(w);
-      a1 += p * hi_bf16(w);
+  // Values: thread = (key slot, 16-byte chunk); slot k takes keys k,
+  // k + kSlots, ..., four rows in flight at a time.  Partials per slot are
+  // added in slot order below.
+  const int chunk = tid % CH;
+  const int slot = tid / CH;
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (slot < kSlots) {
+    for (int j0 = slot; j0 < L; j0 += 4 * kSlots) {
+      uint4 vr[4];
+      float p[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = min(j0 + u * kSlots, L - 1);
+        const int key = lo + j;
+        vr[u] = reinterpret_cast<const uint4*>(
+            key == pos ? vn : vc + static_cast<int64_t>(key) * D)[chunk];
+        p[u] = j0 + u * kSlots < L ? s[j] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a[0] += p[u] * lo_bf16(vr[u].x);
+        a[1] += p[u] * hi_bf16(vr[u].x);
+        a[2] += p[u] * lo_bf16(vr[u].y);
+        a[3] += p[u] * hi_bf16(vr[u].y);
+        a[4] += p[u] * lo_bf16(vr[u].z);
+        a[5] += p[u] * hi_bf16(vr[u].z);
+        a[6] += p[u] * lo_bf16(vr[u].w);
+        a[7] += p[u] * hi_bf16(vr[u].w);
+      }
     }
-    if (lane + kWave < pairs) {
-      const uint32_t w = row[lane + kWave];
-      a2 += p * lo_bf16(w);
-      a3 += p * hi_bf16(w);
-    }
-  }
-  if (lane < pairs) {
-    part[wave * D + 2 * lane] = a0;
-    part[wave * D + 2 * lane + 1] = a1;
-  }
-  if (lane + kWave < pairs) {
-    part[wave * D + 2 * (lane + kWave)] = a2;
-    part[wave * D + 2 * (lane + kWave) + 1] = a3;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[slot * D + chunk * 8 + i] = a[i];
   }
   __syncthreads();
   const float inv = 1.0f / sum;
   for (int i = tid; i < D; i += 256) {
-    const float o = ((part[i] + part[D + i]) + part[2 * D + i]) + part[3 * D + i];
+    float o = 0.0f;
+    for (int k = 0; k < kSlots; ++k) o += part[k * D + i];
     store_out(out + (static_cast<int64_t>(b) * heads + h) * D + i, o * inv);
   }
 }
 
+template <typename QT, typename OT>
+hipError_t launch_decode(const QT* q, const uint16_t* k_new, const uint16_t* v_new,
+                         uint16_t* k_cache, uint16_t* v_cache, const int32_t* position, int batch,
+                         int heads, int kv_heads, int head_dim, int max_pos, int window,
+                         float scale, OT* out, hipStream_t s) {
+  const size_t lds = decode_attention_lds_bytes(window, max_pos, head_dim);
+  const dim3 grid(heads, batch);
+#define PARROT_DECODE(CH)                                                                      \
+  decode_attention_kernel<QT, OT, CH><<<grid, 256, lds, s>>>(q, k_new, v_new, k_cache, v_cache, \
+                                                              position, heads, kv_heads,       \
+                                                              max_pos, window, scale, out)
+  switch (head_dim / 8) {
+    case 1: PARROT_DECODE(1); break;
+    case 2: PARROT_DECODE(2); break;
+    case 4: PARROT_DECODE(4); break;
+    case 8: PARROT_DECODE(8); break;
+    case 12: PARROT_DECODE(12); break;
+    case 16: PARROT_DECODE(16); break;
+    case 24: PARROT_DECODE(24); break;
+    case 32: PARROT_DECODE(32); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef PARROT_DECODE
+  return hipGetLastError();
+}
+
 }  // namespace
+
+bool decode_head_dim_supported(int head_dim) {
+  switch (head_dim) {
+    case 8: case 16: case 32: case 64: case 96: case 128: case 192: case 256: return true;
+    default: return false;
+  }
+}
 
 size_t decode_attention_lds_bytes(int window, int max_pos, int head_dim) {
   const int lcap = window < max_pos ? window : max_pos;
-  return (static_cast<size_t>(lcap) + 5 * head_dim + 4) * sizeof(float);
+  const int slots = 256 / (head_dim / 8 > 0 ? head_dim / 8 : 1);
+  return (static_cast<size_t>(lcap) + head_dim + static_cast<size_t>(slots) * head_dim + 4) *
+         sizeof(float);
 }
 
 hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_new,
@@ -175,11 +221,8 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_new,
                                    int head_dim, int max_pos, int window, float scale,
                                    uint16_t* out, hipStream_t s) {
   if (batch == 0) return hipSuccess;
-  const size_t lds = decode_attention_lds_bytes(window, max_pos, head_dim);
-  decode_attention_kernel<uint16_t, uint16_t><<<dim3(heads, batch), 256, lds, s>>>(
-      q, k_new, v_new, k_cache, v_cache, position, heads, kv_heads, head_dim, max_pos, window,
-      scale, out);
-  return hipGetLastError();
+  return launch_decode(q, k_new, v_new, k_cache, v_cache, position, batch, heads, kv_heads,
+                       head_dim, max_pos, window, scale, out, s);
 }
 
 hipError_t launch_decode_attention_latent(const float* q, const uint16_t* latent_new,
@@ -187,11 +230,8 @@ hipError_t launch_decode_attention_latent(const float* q, const uint16_t* latent
                                           int batch, int heads, int latent_dim, int max_pos,
                                           float scale, float* out, hipStream_t s) {
   if (batch == 0) return hipSuccess;
-  const size_t lds = decode_attention_lds_bytes(max_pos, max_pos, latent_dim);
-  decode_attention_kernel<float, float><<<dim3(heads, batch), 256, lds, s>>>(
-      q, latent_new, latent_new, latent_cache, latent_cache, position, heads, 1, latent_dim,
-      max_pos, max_pos, scale, out);
-  return hipGetLastError();
+  return launch_decode(q, latent_new, latent_new, latent_cache, latent_cache, position, batch,
+                       heads, 1, latent_dim, max_pos, max_pos, scale, out, s);
 }
 
 }  // namespace parrot

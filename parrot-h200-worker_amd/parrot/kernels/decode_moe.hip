@@ -1,0 +1,232 @@
+// Fused MoE layer for decode steps: T <= 16 tokens in two kernels.
+//
+// Reference semantics are those of the grouped path (route_kernel, the
+// grouped SwiGLU GEMMs, combine_kernel): parrot/model.py:520-551 and
+// 571-607 -- logits = x Wr^T (+ bias) in fp32, top-2 with ties to the lower
+// expert index, weights renormalised over the two, h = bf16(silu(x Wg^T) *
+// (x Wu^T)) per routed assignment and for the shared expert, out =
+// bf16(shared + w0 y0 + w1 y1) (+ addend with a second rounding).  Every
+// assignment is computed, so capacity and overflow change nothing here.  The
+// reference's Apple decode fusion is moe_decode_lanes_bf16 /
+// moe_sum_decode_lanes_bf16 (parrot/kernels/moe_bf16.metal:894-1024,
+// 1185-1201, driven by parrot/metal_moe.py:182-221).
+//
+// At decode sizes the layer is a weight stream of ~2 x 2.4 MB per token plus
+// the shared expert, and launch latency dominates; the grouped path spends 5
+// launches (route, group, gate/up, down, combine).  Here:
+//   decode_up_kernel   grid (max(H, Hs) / 16 slices, 2T + 1 slots): slot
+//       2t + k is token t's k-th routed expert, slot 2T the shared expert for
+//       all tokens.  A routed workgroup recomputes its token's router logits
+//       and top-2 (every workgroup of a token does the same arithmetic in the
+//       same order, so they agree), then one 16-column slice of SwiGLU.
+//   decode_down_kernel grid (dim / 16 slices, T): 16 output columns of one
+//       token: both weighted routed rows and the shared row, summed in the
+//       combine kernel's order, with the addend folded in.
+// Weights are the packed fragment-ordered matrices of the grouped path (1 KB
+// blocks of 16 rows x 32 k; lane l's 16 bytes are row l % 16, k 8 (l / 16)
+// .. +8), so lane l of wavefront w reads 16 contiguous bytes of k step
+// s = w, w + 4, ...; partial sums over (k chunk, wavefront) are added in a
+// fixed order through LDS.
+#include "common.h"
+
+namespace parrot {
+
+namespace {
+
+constexpr int kDecodeMaxTokens = 16;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
+
+__device__ __forceinline__ float dot8(uint4 a, uint4 b) {
+  return lo_bf16(a.x) * lo_bf16(b.x) + hi_bf16(a.x) * hi_bf16(b.x) +
+         lo_bf16(a.y) * lo_bf16(b.y) + hi_bf16(a.y) * hi_bf16(b.y) +
+         lo_bf16(a.z) * lo_bf16(b.z) + hi_bf16(a.z) * hi_bf16(b.z) +
+         lo_bf16(a.w) * lo_bf16(b.w) + hi_bf16(a.w) * hi_bf16(b.w);
+}
+
+// Router logits of token t for all experts into lg[0..E), then top-2.
+// Thread (e = tid / 8, part = tid % 8) sums the dim / 8 columns of its part;
+// the 8 parts of an expert are added in a fixed order by DPP (xor 1, xor 2,
+// half-row mirror) inside 8-lane groups.
+__device__ __forceinline__ void route_token(const uint16_t* x_row, const uint16_t* wr,
+                                            const float* bias, int dim, int experts, float* lg,
+                                            int* sel, float* sel_w) {
+  const int tid = threadIdx.x;
+  const int e = tid >> 3, part = tid & 7;
+  float acc = 0.0f;
+  if (e < experts) {
+    const int span = dim / 8;  // multiple of 8 (dim % 64 == 0)
+    const uint4* xa = reinterpret_cast<const uint4*>(x_row + part * span);
+    const uint4* wa = reinterpret_cast<const uint4*>(wr + static_cast<int64_t>(e) * dim + part * span);
+    for (int c = 0; c < span / 8; ++c) acc += dot8(xa[c], wa[c]);
+  }
+  acc += dpp<0xb1>(acc);
+  acc += dpp<0x4e>(acc);
+  acc += dpp<0x141>(acc);
+  if (part == 0 && e < experts) lg[e] = acc + (bias != nullptr ? bias[e] : 0.0f);
+  __syncthreads();
+  if (tid < 16) {
+    int first, second;
+    float vb, vr;
+    row_top2(tid < experts ? lg[tid] : 0.0f, tid + 16 < experts ? lg[tid + 16] : 0.0f, experts,
+             first, second, vb, vr);
+    if (tid == 0) {
+      const float e2 = __expf(vr - vb);
+      const float den = 1.0f + e2;
+      sel[0] = first;
+      sel[1] = second;
+      sel_w[0] = 1.0f / den;
+      sel_w[1] = e2 / den;
+    }
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void decode_up_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
+    const float* __restrict__ bias, int tokens, int dim, int experts, int hidden_dim,
+    int shared_dim, int hstride, const uint16_t* __restrict__ gate_up,
+    const uint16_t* __restrict__ shared_gate_up, uint16_t* __restrict__ hidden,
+    int64_t* __restrict__ indices, float* __restrict__ weights) {
+  __shared__ float lg[kMaxExperts];
+  __shared__ int sel[2];
+  __shared__ float sel_w[2];
+  __shared__ float part[4][4][kDecodeMaxTokens][32];  // [wave][k chunk][token][gate 16 | up 16]
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int slot = blockIdx.y;
+  const int slice = blockIdx.x;
+  const bool shared = slot == 2 * tokens;
+  const int H = shared ? shared_dim : hidden_dim;
+  if (slice * 16 >= H) return;  // uniform
+  const int t0 = shared ? 0 : slot >> 1;
+  const int nt = shared ? tokens : 1;
+  const uint16_t* w;
+  if (shared) {
+    w = shared_gate_up;
+  } else {
+    route_token(x + static_cast<int64_t>(t0) * dim, wr, bias, dim, experts, lg, sel, sel_w);
+    const int k = slot & 1;
+    if (slice == 0 && k == 0 && tid < 2) {
+      indices[2 * t0 + tid] = sel[tid];
+      weights[2 * t0 + tid] = sel_w[tid];
+    }
+    w = gate_up + static_cast<int64_t>(sel[k]) * 2 * hidden_dim * dim;
+  }
+  // Packed rows [32 slice, 32 slice + 32): gate group 2 slice, up group
+  // 2 slice + 1; block (g, s) at ((g * ksteps) + s) KB.
+  const int ksteps = dim / 32;
+  const uint4* wg = reinterpret_cast<const uint4*>(w) + (2 * slice) * ksteps * 64 + lane;
+  const uint4* wu = wg + ksteps * 64;
+  const int c = lane >> 4;
+  float ag[kDecodeMaxTokens], au[kDecodeMaxTokens];
+#pragma unroll
+  for (int t = 0; t < kDecodeMaxTokens; ++t) ag[t] = au[t] = 0.0f;
+  for (int s = wave; s < ksteps; s += 4) {
+    const uint4 g = wg[s * 64];
+    const uint4 u = wu[s * 64];
+#pragma unroll
+    for (int t = 0; t < kDecodeMaxTokens; ++t) {
+      if (t < nt) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(
+            x + static_cast<int64_t>(t0 + t) * dim + s * 32 + c * 8);
+        ag[t] += dot8(g, xv);
+        au[t] += dot8(u, xv);
+      }
+    }
+  }
+  const int r = lane & 15;
+#pragma unroll
+  for (int t = 0; t < kDecodeMaxTokens; ++t) {
+    if (t < nt) {
+      part[wave][c][t][r] = ag[t];
+      part[wave][c][t][16 + r] = au[t];
+    }
+  }
+  __syncthreads();
+  if (tid < nt * 16) {
+    const int t = tid >> 4, rr = tid & 15;
+    float gs = 0.0f, us = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < 4; ++wv)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        gs += part[wv][cc][t][rr];
+        us += part[wv][cc][t][16 + rr];
+      }
+    const int64_t row = shared ? 2 * tokens + t : slot;
+    hidden[row * hstride + slice * 16 + rr] = f32_to_bf16(swiglu(gs, us));
+  }
+}
+
+__global__ __launch_bounds__(256) void decode_down_kernel(
+    const uint16_t* __restrict__ hidden, int tokens, int dim, int hidden_dim, int shared_dim,
+    int hstride, const int64_t* __restrict__ indices, const float* __restrict__ weights,
+    const uint16_t* __restrict__ down, const uint16_t* __restrict__ shared_down,
+    const uint16_t* __restrict__ addend, uint16_t* __restrict__ out) {
+  __shared__ float part[3][4][4][16];  // [contribution][wave][k chunk][column]
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int slice = blockIdx.x;  // output columns [16 slice, 16 slice + 16)
+  const int t = blockIdx.y;
+  const int c = lane >> 4;
+  // Contribution 0 / 1: routed slot 2t + k (expert indices[2t + k], K = H);
+  // contribution 2: the shared expert (K = Hs).
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const bool sh = q == 2;
+    const int K = sh ? shared_dim : hidden_dim;
+    const int ksteps = K / 32;
+    const uint16_t* w = sh ? shared_down
+                           : down + indices[2 * t + q] * static_cast<int64_t>(dim) * hidden_dim;
+    const uint4* wb = reinterpret_cast<const uint4*>(w) + slice * ksteps * 64 + lane;
+    const uint16_t* hrow = hidden + (sh ? 2 * tokens + t : 2 * t + q) * static_cast<int64_t>(hstride);
+    float acc = 0.0f;
+    for (int s = wave; s < ksteps; s += 4)
+      acc += dot8(wb[s * 64], *reinterpret_cast<const uint4*>(hrow + s * 32 + c * 8));
+    part[q][wave][c][lane & 15] = acc;
+  }
+  __syncthreads();
+  if (tid < 16) {
+    float y[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      float v = 0.0f;
+#pragma unroll
+      for (int wv = 0; wv < 4; ++wv)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) v += part[q][wv][cc][tid];
+      y[q] = v;
+    }
+    // combine_kernel's order: shared, then the two weighted routed rows.
+    const float v = (y[2] + weights[2 * t] * y[0]) + weights[2 * t + 1] * y[1];
+    const int64_t o = static_cast<int64_t>(t) * dim + slice * 16 + tid;
+    uint16_t r = f32_to_bf16(v);
+    if (addend != nullptr) r = f32_to_bf16(bf16_to_f32(addend[o]) + bf16_to_f32(r));
+    out[o] = r;
+  }
+}
+
+}  // namespace
+
+int decode_moe_max_tokens() { return kDecodeMaxTokens; }
+
+hipError_t launch_decode_moe(const uint16_t* x, int tokens, int dim, int experts, int hidden_dim,
+                             int shared_dim, const uint16_t* router_w, const float* bias,
+                             const ExpertWeights& w, const uint16_t* addend, uint16_t* out,
+                             int64_t* indices, float* weights, uint16_t* hidden, hipStream_t s) {
+  if (tokens == 0) return hipSuccess;
+  const int hstride = hidden_dim > shared_dim ? hidden_dim : shared_dim;
+  decode_up_kernel<<<dim3(hstride / 16, 2 * tokens + 1), 256, 0, s>>>(
+      x, router_w, bias, tokens, dim, experts, hidden_dim, shared_dim, hstride, w.gate_up,
+      w.shared_gate_up, hidden, indices, weights);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  decode_down_kernel<<<dim3(dim / 16, tokens), 256, 0, s>>>(
+      hidden, tokens, dim, hidden_dim, shared_dim, hstride, indices, weights, w.down,
+      w.shared_down, addend, out);
+  return hipGetLastError();
+}
+
+}  // namespace parrot

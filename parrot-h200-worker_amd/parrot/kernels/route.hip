@@ -28,60 +28,6 @@ __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
-// ---- top-2 across a row of 16 lanes ----------------------------------------
-// A token's logits are spread over one DPP row: lane j holds experts j and
-// j + 16.  Selection is a max-reduction of 64-bit keys (order-preserving
-// float bits, then the complemented expert index), so equal logits go to
-// the lower expert index: the strict '>' scan in expert order of the
-// reference.
-
-// Order-preserving map of a float to uint32 (-0 canonicalised to +0, so it
-// ties with +0 as it does under '>').
-__device__ __forceinline__ uint32_t order_key(float v) {
-  const uint32_t u = __float_as_uint(v + 0.0f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ uint64_t expert_key(float v, int e) {
-  return (static_cast<uint64_t>(order_key(v)) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
-}
-
-// Inverse of order_key on the high word of a key.
-__device__ __forceinline__ float key_value(uint64_t k) {
-  const uint32_t o = static_cast<uint32_t>(k >> 32);
-  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
-}
-
-__device__ __forceinline__ int key_expert(uint64_t k) {
-  return static_cast<int>(0xffffffffu - static_cast<uint32_t>(k));
-}
-
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_max_key(uint64_t k) {
-  const int lo = static_cast<int>(static_cast<uint32_t>(k));
-  const int hi = static_cast<int>(static_cast<uint32_t>(k >> 32));
-  const uint32_t olo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xf, 0xf, false));
-  const uint32_t ohi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xf, 0xf, false));
-  const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;
-  return o > k ? o : k;
-}
-
-// Max over the 16 lanes of a DPP row, returned to every lane of the row
-// (xor 1, xor 2 inside quads, then half-row and row mirrors).
-__device__ __forceinline__ uint64_t row_max_key(uint64_t k) {
-  k = dpp_max_key<0xb1>(k);
-  k = dpp_max_key<0x4e>(k);
-  k = dpp_max_key<0x141>(k);
-  return dpp_max_key<0x140>(k);
-}
-
-__device__ __forceinline__ float row_sum(float v) {
-  v += dpp<0xb1>(v);
-  v += dpp<0x4e>(v);
-  v += dpp<0x141>(v);
-  return v + dpp<0x140>(v);
-}
-
 // Top-2 of the token whose logits lane j of this DPP row holds for experts
 // j (l0) and j + 16 (l1; ignored unless experts > 16), route weights
 // renormalised over the two selected exponentials, and the optional logits
@@ -92,16 +38,9 @@ __device__ __forceinline__ void select_top2(float l0, float l1, int experts, int
                                             float* weights, int64_t* indices, int* ids) {
   const int j = threadIdx.x & 15;
   const bool has0 = j < experts, has1 = j + 16 < experts;
-  constexpr uint64_t kNone = 0;  // below every real key
-  const uint64_t k0 = has0 ? expert_key(l0, j) : kNone;
-  const uint64_t k1 = has1 ? expert_key(l1, j + 16) : kNone;
-  const uint64_t mine = k1 > k0 ? k1 : k0;    // k0 wins ties: lower index
-  const uint64_t other = k1 > k0 ? k0 : k1;
-  const uint64_t best = row_max_key(mine);
-  const uint64_t runner = row_max_key(mine == best ? other : mine);
-  const int first = key_expert(best), second = key_expert(runner);
-  // The selected logits, decoded from their keys.
-  const float vb = key_value(best), vr = key_value(runner);
+  int first, second;
+  float vb, vr;
+  row_top2(l0, l1, experts, first, second, vb, vr);
   if (valid) {
     if (out_logits != nullptr) {
       if (has0) out_logits[t * experts + j] = l0;

@@ -535,7 +535,9 @@ class MoE(nn.Module):
                   defer_sum: bool = False) -> Tensor:
         """Inference without router statistics.  On the HIP backend the
         addend (an open AttnRes partial sum) is folded into the combine
-        kernel; ``direct`` (decode) selects small-M GEMM tiles automatically."""
+        kernel; inputs of at most 16 rows (decode steps) run the fused
+        two-launch decode MoE, larger ones route + grouped experts with tiles
+        chosen by size (so ``direct`` needs no separate handling)."""
         if defer_sum:
             raise ValueError("deferred MoE reduction is not supported on this backend")
         if not self._hip_route_applies(x):
@@ -543,6 +545,9 @@ class MoE(nn.Module):
             return result if addend is None else addend + result
         from . import hip_moe
         flat = x.reshape(-1, x.shape[-1])
+        if flat.shape[0] <= hip_moe.DECODE_MAX_TOKENS:
+            # Decode-sized inputs: the whole layer in two launches.
+            return hip_moe.decode_experts(self, flat, addend=addend)[0].view_as(x)
         routed = hip_moe.route(self, flat, collect_stats=False)
         result = hip_moe.grouped_hip_experts(self, flat, routed.indices, routed.weights,
                                              addend=addend, grouping=routed.grouping)

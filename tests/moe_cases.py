@@ -14,6 +14,7 @@ import torch
 from oracle import layers
 
 DIM, HIDDEN, SHARED = 768, 512, 256
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3  # bf16 MoE output vs fp32
 
 
 def moe_module(experts: int, seed: int, dim=DIM, hidden=HIDDEN, shared=SHARED,

@@ -122,3 +122,40 @@ def test_decode_graph_matches_eager():
                                        getattr(mine, name)[:, :, :48],
                                        getattr(theirs, name)[:, :48] if name == "latent" else
                                        getattr(theirs, name)[:, :, :48])
+
+
+@pytest.mark.parametrize("tokens,experts,skewed,with_addend", [
+    (1, 16, False, False), (2, 16, False, True), (5, 32, True, False), (8, 16, False, True),
+    (16, 3, False, True), (16, 32, False, False)])
+def test_decode_moe_fused(tokens, experts, skewed, with_addend):
+    """The two-launch decode MoE against the fp32 oracle (parrot/model.py:
+    520-551) on its own routing, and its routing against the oracle's top-2
+    of fp32 logits."""
+    import numpy as np
+    from moe_cases import MAX_ABS, MEAN_ABS, error_stats, inputs, moe_module, oracle_moe, skew_bias
+    from parrot import hip_moe
+    _say(f"decode moe T={tokens} E={experts} skew={skewed} addend={with_addend}")
+    module = moe_module(experts, seed=11)
+    x = inputs(tokens, seed=11 + tokens)
+    bias = skew_bias(experts) if skewed else None
+    addend = inputs(tokens, seed=12) if with_addend else None
+    with torch.no_grad():
+        out, idx, w = hip_moe.decode_experts(module, x, addend=addend, logit_bias=bias)
+        delta, idx2, w2 = hip_moe.decode_experts(module, x, logit_bias=bias)
+    assert torch.equal(idx, idx2) and torch.equal(w, w2)
+    if with_addend:  # the same two roundings as `addend + delta`
+        assert torch.equal(out, addend + delta)
+    idx_np = idx.cpu().numpy()
+    ref_routed, ref_idx, ref_w, logits = oracle_moe(
+        module, x, logit_bias=None if bias is None else bias.numpy())
+    # routing: identical wherever the fp32 logits leave a visible margin
+    biased = logits.numpy() + (0 if bias is None else bias.numpy())
+    top = np.sort(biased, axis=-1)[:, ::-1]
+    clear = (top[:, 0] - top[:, 1] > 1e-4) & (top[:, 1] - top[:, 2] > 1e-4) if experts > 2 else \
+        np.ones(tokens, bool)
+    assert (idx_np[clear] == ref_idx[clear]).all()
+    np.testing.assert_allclose(w.cpu().numpy()[clear], ref_w[clear], atol=2e-6)
+    ref, _, _, _ = oracle_moe(module, x, indices=idx_np, weights=w.cpu().numpy())
+    mx, mean = error_stats(delta, ref)
+    _say(f"  max-abs {mx:.3e} mean-abs {mean:.3e}")
+    assert mx <= MAX_ABS and mean <= MEAN_ABS

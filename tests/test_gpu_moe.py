@@ -9,12 +9,11 @@ import numpy as np
 import pytest
 import torch
 
-from moe_cases import error_stats, inputs, moe_module, oracle_moe, skew_bias
+from moe_cases import MAX_ABS, MEAN_ABS, error_stats, inputs, moe_module, oracle_moe, skew_bias
 from oracle import layers
 
 pytestmark = pytest.mark.gpu
 
-MAX_ABS, MEAN_ABS = 2e-2, 2e-3
 
 
 def _say(msg):
