@@ -140,7 +140,7 @@ size_t parrot_decode_moe_workspace_bytes(int64_t tokens, int32_t hidden_dim,
  * bf16(addend + bf16(...)) with an addend.  Packed weights as for
  * parrot_grouped_experts_bf16.  Every assignment is computed (capacity and
  * overflow do not apply at these sizes).  2 <= experts <= 32; dim, H, Hs
- * multiples of 64.  Replaces metal_experts_decode (parrot/metal_moe.py:
+ * multiples of 64, dim <= 2048.  Replaces metal_experts_decode (parrot/metal_moe.py:
  * 182-221; kernels moe_decode_lanes_bf16 / moe_sum_decode_lanes_bf16,
  * parrot/kernels/moe_bf16.metal:894-1024, 1185-1201) and, for these sizes,
  * the route + grouped-experts path of MoE.inference (parrot/model.py:

@@ -398,7 +398,7 @@ int parrot_decode_moe_bf16(const void* x, int64_t tokens, int32_t dim, int32_t e
     return PARROT_ERR_NULL_POINTER;
   if (tokens < 0 || dim <= 0 || hidden_dim <= 0 || shared_dim <= 0) return PARROT_ERR_BAD_SHAPE;
   if (tokens > parrot::decode_moe_max_tokens() || experts < 2 || experts > parrot::kMaxExperts ||
-      dim % 64 || hidden_dim % 64 || shared_dim % 64)
+      dim % 64 || dim > 2048 || hidden_dim % 64 || shared_dim % 64)
     return PARROT_ERR_UNSUPPORTED;
   if (!workspace || workspace_bytes < parrot_decode_moe_workspace_bytes(tokens, hidden_dim,
                                                                         shared_dim))

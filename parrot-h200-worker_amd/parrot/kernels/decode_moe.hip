@@ -55,10 +55,21 @@ __device__ __forceinline__ void route_token(const uint16_t* x_row, const uint16_
   const int e = tid >> 3, part = tid & 7;
   float acc = 0.0f;
   if (e < experts) {
-    const int span = dim / 8;  // multiple of 8 (dim % 64 == 0)
-    const uint4* xa = reinterpret_cast<const uint4*>(x_row + part * span);
-    const uint4* wa = reinterpret_cast<const uint4*>(wr + static_cast<int64_t>(e) * dim + part * span);
-    for (int c = 0; c < span / 8; ++c) acc += dot8(xa[c], wa[c]);
+    const int n = dim / 64;  // 16-byte chunks per part (dim % 64 == 0)
+    const uint4* xa = reinterpret_cast<const uint4*>(x_row) + part * n;
+    const uint4* wa = reinterpret_cast<const uint4*>(wr + static_cast<int64_t>(e) * dim) + part * n;
+    for (int c0 = 0; c0 < n; c0 += 12) {  // 12 chunks (dim 768) in flight at once
+      uint4 xv[12], wv[12];
+#pragma unroll
+      for (int u = 0; u < 12; ++u) {
+        const int c = min(c0 + u, n - 1);
+        xv[u] = xa[c];
+        wv[u] = wa[c];
+      }
+#pragma unroll
+      for (int u = 0; u < 12; ++u)
+        if (c0 + u < n) acc += dot8(xv[u], wv[u]);
+    }
   }
   acc += dpp<0xb1>(acc);
   acc += dpp<0x4e>(acc);
@@ -92,6 +103,7 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   __shared__ int sel[2];
   __shared__ float sel_w[2];
   __shared__ float part[4][4][kDecodeMaxTokens][32];  // [wave][k chunk][token][gate 16 | up 16]
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [rows of this slot][dim]
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -102,8 +114,15 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   if (slice * 16 >= H) return;  // uniform
   const int t0 = shared ? 0 : slot >> 1;
   const int nt = shared ? tokens : 1;
+  // The slot's activation rows, staged in LDS as bf16; these loads are in
+  // flight together with the router's (the barrier in route_token, or the
+  // one below, orders them before use).
+  for (int i = tid; i < nt * dim / 8; i += 256)
+    reinterpret_cast<uint4*>(xs)[i] =
+        reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t0) * dim)[i];
   const uint16_t* w;
   if (shared) {
+    __syncthreads();
     w = shared_gate_up;
   } else {
     route_token(x + static_cast<int64_t>(t0) * dim, wr, bias, dim, experts, lg, sel, sel_w);
@@ -115,7 +134,9 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
     w = gate_up + static_cast<int64_t>(sel[k]) * 2 * hidden_dim * dim;
   }
   // Packed rows [32 slice, 32 slice + 32): gate group 2 slice, up group
-  // 2 slice + 1; block (g, s) at ((g * ksteps) + s) KB.
+  // 2 slice + 1; block (g, s) at ((g * ksteps) + s) KB.  Wavefront w takes
+  // k steps w, w + 4, ..., the weight fragments of up to 8 of them in
+  // flight at once.
   const int ksteps = dim / 32;
   const uint4* wg = reinterpret_cast<const uint4*>(w) + (2 * slice) * ksteps * 64 + lane;
   const uint4* wu = wg + ksteps * 64;
@@ -123,16 +144,26 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   float ag[kDecodeMaxTokens], au[kDecodeMaxTokens];
 #pragma unroll
   for (int t = 0; t < kDecodeMaxTokens; ++t) ag[t] = au[t] = 0.0f;
-  for (int s = wave; s < ksteps; s += 4) {
-    const uint4 g = wg[s * 64];
-    const uint4 u = wu[s * 64];
+  for (int s0 = wave; s0 < ksteps; s0 += 32) {
+    uint4 g[8], u[8];
 #pragma unroll
-    for (int t = 0; t < kDecodeMaxTokens; ++t) {
-      if (t < nt) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(
-            x + static_cast<int64_t>(t0 + t) * dim + s * 32 + c * 8);
-        ag[t] += dot8(g, xv);
-        au[t] += dot8(u, xv);
+    for (int i = 0; i < 8; ++i) {
+      const int st = min(s0 + 4 * i, ksteps - 1);
+      g[i] = wg[st * 64];
+      u[i] = wu[st * 64];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int st = s0 + 4 * i;
+      if (st < ksteps) {
+#pragma unroll
+        for (int t = 0; t < kDecodeMaxTokens; ++t) {
+          if (t < nt) {
+            const uint4 xv = *reinterpret_cast<const uint4*>(xs + t * dim + st * 32 + c * 8);
+            ag[t] += dot8(g[i], xv);
+            au[t] += dot8(u[i], xv);
+          }
+        }
       }
     }
   }
@@ -173,21 +204,41 @@ __global__ __launch_bounds__(256) void decode_down_kernel(
   const int t = blockIdx.y;
   const int c = lane >> 4;
   // Contribution 0 / 1: routed slot 2t + k (expert indices[2t + k], K = H);
-  // contribution 2: the shared expert (K = Hs).
+  // contribution 2: the shared expert (K = Hs).  Wavefront w takes k steps
+  // w, w + 4, ...; the loads of up to 4 steps of all three are issued
+  // before any arithmetic.
+  const uint4* wb[3];
+  const uint16_t* hrow[3];
+  int ks[3];
 #pragma unroll
   for (int q = 0; q < 3; ++q) {
     const bool sh = q == 2;
-    const int K = sh ? shared_dim : hidden_dim;
-    const int ksteps = K / 32;
+    ks[q] = (sh ? shared_dim : hidden_dim) / 32;
     const uint16_t* w = sh ? shared_down
                            : down + indices[2 * t + q] * static_cast<int64_t>(dim) * hidden_dim;
-    const uint4* wb = reinterpret_cast<const uint4*>(w) + slice * ksteps * 64 + lane;
-    const uint16_t* hrow = hidden + (sh ? 2 * tokens + t : 2 * t + q) * static_cast<int64_t>(hstride);
-    float acc = 0.0f;
-    for (int s = wave; s < ksteps; s += 4)
-      acc += dot8(wb[s * 64], *reinterpret_cast<const uint4*>(hrow + s * 32 + c * 8));
-    part[q][wave][c][lane & 15] = acc;
+    wb[q] = reinterpret_cast<const uint4*>(w) + slice * ks[q] * 64 + lane;
+    hrow[q] = hidden + (sh ? 2 * tokens + t : 2 * t + q) * static_cast<int64_t>(hstride) + c * 8;
   }
+  float acc[3] = {0.0f, 0.0f, 0.0f};
+  const int kmax = max(ks[0], ks[2]);
+  for (int s0 = wave; s0 < kmax; s0 += 16) {
+    uint4 wv[3][4], hv[3][4];
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int st = min(s0 + 4 * i, ks[q] - 1);
+        wv[q][i] = wb[q][st * 64];
+        hv[q][i] = *reinterpret_cast<const uint4*>(hrow[q] + st * 32);
+      }
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (s0 + 4 * i < ks[q]) acc[q] += dot8(wv[q][i], hv[q][i]);
+  }
+#pragma unroll
+  for (int q = 0; q < 3; ++q) part[q][wave][c][lane & 15] = acc[q];
   __syncthreads();
   if (tid < 16) {
     float y[3];
@@ -219,7 +270,8 @@ hipError_t launch_decode_moe(const uint16_t* x, int tokens, int dim, int experts
                              int64_t* indices, float* weights, uint16_t* hidden, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
   const int hstride = hidden_dim > shared_dim ? hidden_dim : shared_dim;
-  decode_up_kernel<<<dim3(hstride / 16, 2 * tokens + 1), 256, 0, s>>>(
+  const size_t x_lds = static_cast<size_t>(tokens) * dim * sizeof(uint16_t);
+  decode_up_kernel<<<dim3(hstride / 16, 2 * tokens + 1), 256, x_lds, s>>>(
       x, router_w, bias, tokens, dim, experts, hidden_dim, shared_dim, hstride, w.gate_up,
       w.shared_gate_up, hidden, indices, weights);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
