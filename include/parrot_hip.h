@@ -153,6 +153,21 @@ int parrot_decode_moe_bf16(const void* x, int64_t tokens, int32_t dim, int32_t e
                            int64_t* out_indices, float* out_weights, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* Workspace bytes of parrot_vocab_argmax_bf16. */
+size_t parrot_vocab_argmax_workspace_bytes(int64_t rows, int32_t vocab);
+
+/* Greedy next token per row without materialising the logits:
+ * out_tokens[r] = argmax_v sum_d hidden[r, d] * weight[v, d] for hidden
+ * [rows, dim] and the tied head weight [vocab, dim] (bf16, row-major), fp32
+ * logits, ties to the lower index.  rows <= 16, dim % 8 == 0, dim <= 2048.
+ * Replaces argmax(F.linear(h, embedding.weight)) of decode_next
+ * (parrot/model.py:714-715, 922, 927-931) and the Metal kernels
+ * vocab_argmax_partials_bf16 / vocab_argmax_reduce_bf16
+ * (parrot/kernels/moe_bf16.metal:1541-1621). */
+int parrot_vocab_argmax_bf16(const void* hidden, int64_t rows, int32_t dim, const void* weight,
+                             int32_t vocab, int64_t* out_tokens, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 /* Workspace bytes for the routing / grouping entry points. */
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts);
 

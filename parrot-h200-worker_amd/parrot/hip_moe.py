@@ -348,6 +348,27 @@ def decode_experts(module: "MoE", flat: Tensor, addend: Tensor | None = None,
     return out, indices, weights
 
 
+def vocab_argmax(h: Tensor, weight: Tensor) -> Tensor:
+    """Greedy tokens argmax(h @ weight^T) over fp32 logits for h [..., dim]
+    (at most 16 rows) and the head weight [vocab, dim]; returns int64 ids of
+    shape h.shape[:-1] (cf. vocab_argmax_partials/reduce_bf16,
+    parrot/kernels/moe_bf16.metal:1541-1621)."""
+    _require(h, "HIP vocabulary argmax")
+    flat = h.reshape(-1, h.shape[-1]).contiguous()
+    rows, dim = flat.shape
+    vocab = weight.shape[0]
+    if weight.dtype != h.dtype or weight.shape[1] != dim or not weight.is_contiguous():
+        raise RuntimeError("head weight must be a contiguous [vocab, dim] tensor of h's dtype")
+    lib = _abi.load()
+    nbytes = lib.parrot_vocab_argmax_workspace_bytes(16, vocab)
+    ws = _scratch(weight, "_hip_vocab_workspace", nbytes, h.device)
+    out = torch.empty(rows, dtype=torch.int64, device=h.device)
+    _abi.check(lib.parrot_vocab_argmax_bf16(ptr(flat), rows, dim, ptr(weight), vocab, ptr(out),
+                                            ptr(ws), nbytes, _stream(h.device)),
+               "parrot_vocab_argmax_bf16")
+    return out.view(h.shape[:-1])
+
+
 # ---------------------------------------------------------------------------
 # RoPE for the local attention layers
 # ---------------------------------------------------------------------------

@@ -418,6 +418,33 @@ int parrot_decode_moe_bf16(const void* x, int64_t tokens, int32_t dim, int32_t e
       out_weights, static_cast<uint16_t*>(workspace), as_stream(stream)));
 }
 
+size_t parrot_vocab_argmax_workspace_bytes(int64_t rows, int32_t vocab) {
+  if (rows < 0 || vocab <= 0) return 0;
+  const size_t n = static_cast<size_t>(rows) * parrot::vocab_argmax_groups(vocab);
+  return round_up(n * sizeof(float)) + round_up(n * sizeof(int32_t));
+}
+
+int parrot_vocab_argmax_bf16(const void* hidden, int64_t rows, int32_t dim, const void* weight,
+                             int32_t vocab, int64_t* out_tokens, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  if (!hidden || !weight || !out_tokens) return PARROT_ERR_NULL_POINTER;
+  if (rows < 0 || dim <= 0 || vocab <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (rows > parrot::vocab_argmax_max_rows() || dim % 8 || dim > 2048)
+    return PARROT_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < parrot_vocab_argmax_workspace_bytes(rows, vocab))
+    return PARROT_ERR_WORKSPACE;
+  if (!aligned16(hidden) || !aligned16(weight) || !aligned16(workspace))
+    return PARROT_ERR_ALIGNMENT;
+  const size_t n = static_cast<size_t>(rows) * parrot::vocab_argmax_groups(vocab);
+  float* part_v = static_cast<float*>(workspace);
+  int32_t* part_i = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
+                                               round_up(n * sizeof(float)));
+  return status(parrot::launch_vocab_argmax(
+      static_cast<const uint16_t*>(hidden), static_cast<int>(rows), dim,
+      static_cast<const uint16_t*>(weight), vocab, part_v, part_i, out_tokens,
+      as_stream(stream)));
+}
+
 int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,
                                 int32_t hidden_dim, int32_t shared_dim, int32_t capacity,
                                 const int32_t* counts, const int32_t* offsets,

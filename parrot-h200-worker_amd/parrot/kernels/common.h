@@ -249,6 +249,14 @@ hipError_t launch_decode_moe(const uint16_t* x, int tokens, int dim, int experts
                              const ExpertWeights& w, const uint16_t* addend, uint16_t* out,
                              int64_t* indices, float* weights, uint16_t* hidden, hipStream_t s);
 
+// Greedy token per row of h [rows <= vocab_argmax_max_rows(), dim] over a
+// [vocab, dim] head, fp32 logits (see vocab.hip); part_v / part_i hold
+// rows x vocab_argmax_groups(vocab) partials.
+int vocab_argmax_max_rows();
+int vocab_argmax_groups(int vocab);
+hipError_t launch_vocab_argmax(const uint16_t* h, int rows, int dim, const uint16_t* w, int vocab,
+                               float* part_v, int32_t* part_i, int64_t* out, hipStream_t s);
+
 hipError_t launch_combine(const float* y_routed, const float* y_shared,
                           const uint16_t* addend, int64_t tokens, int dim,
                           uint16_t* out, hipStream_t s);

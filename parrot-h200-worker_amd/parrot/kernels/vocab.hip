@@ -1,0 +1,175 @@
+// Greedy next token without materialising the logits: argmax over the
+// vocabulary of fp32 logits h . W[v] for each row of h.
+//
+// Reference semantics: decode_next = argmax(F.linear(h, embedding.weight))
+// (parrot/model.py:714-715, 922, 927-931), and the reference's Apple kernels
+// vocab_argmax_partials_bf16 / vocab_argmax_reduce_bf16
+// (parrot/kernels/moe_bf16.metal:1541-1621): fp32 accumulation of bf16
+// products, ties to the lower vocabulary index.  Keeping the logits in fp32
+// (the bf16 head of the eager path rounds them first) makes the pick follow
+// the fp32 model more closely.
+//
+// vocab_argmax_partials_kernel: wavefront w of workgroup g scans vocabulary
+// rows 16 g + 4 w .. + 3 for every row of h.  A whole wavefront reads one
+// vocabulary row (lane l takes 16-byte chunks l, l + 64, ..., so one load
+// instruction reads 1 KB contiguous), the loads of all 4 rows issued before
+// any arithmetic; the rows of h come from LDS and each dot is a wavefront
+// sum.  Measured on MI355X: 5.6 TB/s over the 50 MB head at one row of h.
+// vocab_argmax_reduce_kernel picks the best of the per-wavefront partials.
+#include "common.h"
+
+namespace parrot {
+
+namespace {
+
+constexpr int kVocabRowsPerWave = 4;
+constexpr int kVocabRowsPerGroup = 4 * kVocabRowsPerWave;
+constexpr int kVocabMaxRows = 16;  // rows of h per launch
+
+__device__ __forceinline__ float dot8v(uint4 a, uint4 b) {
+  return lo_bf16(a.x) * lo_bf16(b.x) + hi_bf16(a.x) * hi_bf16(b.x) +
+         lo_bf16(a.y) * lo_bf16(b.y) + hi_bf16(a.y) * hi_bf16(b.y) +
+         lo_bf16(a.z) * lo_bf16(b.z) + hi_bf16(a.z) * hi_bf16(b.z) +
+         lo_bf16(a.w) * lo_bf16(b.w) + hi_bf16(a.w) * hi_bf16(b.w);
+}
+
+// (value, index) keys: larger value wins, then the lower index.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// NCH = ceil(dim / 8 / 64) chunks per lane per vocabulary row; RB >= rows.
+template <int NCH, int RB>
+__global__ __launch_bounds__(256) void vocab_argmax_partials_kernel(
+    const uint16_t* __restrict__ h, int rows, int dim, const uint16_t* __restrict__ w, int vocab,
+    float* __restrict__ part_v, int32_t* __restrict__ part_i) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t hs[];  // [rows][dim]
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int chunks = dim / 8;
+  const int v0 = blockIdx.x * kVocabRowsPerGroup + wave * kVocabRowsPerWave;
+  uint4 wr[kVocabRowsPerWave][NCH];
+#pragma unroll
+  for (int r = 0; r < kVocabRowsPerWave; ++r) {
+    const uint4* row = reinterpret_cast<const uint4*>(
+        w + static_cast<int64_t>(min(v0 + r, vocab - 1)) * dim);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) wr[r][c] = row[min(lane + 64 * c, chunks - 1)];
+  }
+  for (int i = tid; i < rows * chunks; i += 256)
+    reinterpret_cast<uint4*>(hs)[i] = reinterpret_cast<const uint4*>(h)[i];
+  __syncthreads();
+
+  float bv[RB];
+  int bi[RB];
+#pragma unroll
+  for (int b = 0; b < RB; ++b) {
+    bv[b] = -INFINITY;
+    bi[b] = 0x7fffffff;
+  }
+#pragma unroll
+  for (int b = 0; b < RB; ++b) {
+    if (b < rows) {
+      uint4 hv[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        hv[c] = reinterpret_cast<const uint4*>(hs + b * dim)[min(lane + 64 * c, chunks - 1)];
+#pragma unroll
+      for (int r = 0; r < kVocabRowsPerWave; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+          if (lane + 64 * c < chunks) acc += dot8v(wr[r][c], hv[c]);
+        acc = wave_sum(acc);  // uniform across the wavefront
+        if (v0 + r < vocab && better(acc, v0 + r, bv[b], bi[b])) {
+          bv[b] = acc;
+          bi[b] = v0 + r;
+        }
+      }
+    }
+  }
+  // rows ascend with the wavefront index, so a later wavefront only wins
+  // with a strictly larger logit: the per-wavefront partials keep the order.
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+  if (lane == 0) {
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+      if (b < rows) {
+        part_v[b * waves + blockIdx.x * 4 + wave] = bv[b];
+        part_i[b * waves + blockIdx.x * 4 + wave] = bi[b];
+      }
+  }
+}
+
+__global__ __launch_bounds__(256) void vocab_argmax_reduce_kernel(
+    const float* __restrict__ part_v, const int32_t* __restrict__ part_i, int groups,
+    int64_t* __restrict__ out) {
+  __shared__ float vs[256];
+  __shared__ int is[256];
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x;
+  float v = -INFINITY;
+  int i = 0x7fffffff;
+  for (int g = tid; g < groups; g += 256) {
+    const float pv = part_v[static_cast<int64_t>(r) * groups + g];
+    const int pi = part_i[static_cast<int64_t>(r) * groups + g];
+    if (better(pv, pi, v, i)) {
+      v = pv;
+      i = pi;
+    }
+  }
+  vs[tid] = v;
+  is[tid] = i;
+  __syncthreads();
+  for (int stride = 128; stride > 0; stride >>= 1) {
+    if (tid < stride && better(vs[tid + stride], is[tid + stride], vs[tid], is[tid])) {
+      vs[tid] = vs[tid + stride];
+      is[tid] = is[tid + stride];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) out[r] = is[0];
+}
+
+}  // namespace
+
+int vocab_argmax_max_rows() { return kVocabMaxRows; }
+
+// Partials per row of h: one per wavefront.
+int vocab_argmax_groups(int vocab) {
+  return 4 * ((vocab + kVocabRowsPerGroup - 1) / kVocabRowsPerGroup);
+}
+
+hipError_t launch_vocab_argmax(const uint16_t* h, int rows, int dim, const uint16_t* w, int vocab,
+                               float* part_v, int32_t* part_i, int64_t* out, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  const int blocks = (vocab + kVocabRowsPerGroup - 1) / kVocabRowsPerGroup;
+  const size_t lds = static_cast<size_t>(rows) * dim * sizeof(uint16_t);
+  const int nch = (dim / 8 + 63) / 64;
+  const int rb = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
+#define PARROT_VOCAB(NCH, RB)                                                             \
+  vocab_argmax_partials_kernel<NCH, RB><<<blocks, 256, lds, s>>>(h, rows, dim, w, vocab, \
+                                                                 part_v, part_i)
+#define PARROT_VOCAB_RB(NCH)          \
+  switch (rb) {                       \
+    case 1: PARROT_VOCAB(NCH, 1); break; \
+    case 2: PARROT_VOCAB(NCH, 2); break; \
+    case 4: PARROT_VOCAB(NCH, 4); break; \
+    case 8: PARROT_VOCAB(NCH, 8); break; \
+    default: PARROT_VOCAB(NCH, 16); break; \
+  }
+  switch (nch) {
+    case 1: PARROT_VOCAB_RB(1); break;
+    case 2: PARROT_VOCAB_RB(2); break;
+    case 3: PARROT_VOCAB_RB(3); break;
+    default: PARROT_VOCAB_RB(4); break;
+  }
+#undef PARROT_VOCAB_RB
+#undef PARROT_VOCAB
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  vocab_argmax_reduce_kernel<<<rows, 256, 0, s>>>(part_v, part_i, vocab_argmax_groups(vocab), out);
+  return hipGetLastError();
+}
+
+}  // namespace parrot

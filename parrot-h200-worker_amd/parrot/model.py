@@ -805,11 +805,18 @@ class Parrot(nn.Module):
             h = self.depth_mix[-1].normalized(stream.sources(), self.final_norm)
         else:
             h = self.final_norm(x)
-        logits = F.linear(h, self.embedding.weight)
+        if _next_token_only and state.position_device is not None and h.shape[0] <= 16:
+            # Greedy token straight from fp32 logits, never materialised
+            # (cf. vocab_argmax_partials/reduce_bf16, moe_bf16.metal:1541-1621).
+            from . import hip_moe
+            output = hip_moe.vocab_argmax(h, self.embedding.weight)
+        else:
+            logits = F.linear(h, self.embedding.weight)
+            output = logits.argmax(-1) if _next_token_only else logits
         state.position += 1
         if state.position_device is not None:
             state.position_device.add_(1)
-        return (logits.argmax(-1) if _next_token_only else logits), state
+        return output, state
 
     @torch.inference_mode()
     def decode_next(self, input_ids: Tensor,

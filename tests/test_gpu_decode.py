@@ -159,3 +159,28 @@ def test_decode_moe_fused(tokens, experts, skewed, with_addend):
     mx, mean = error_stats(delta, ref)
     _say(f"  max-abs {mx:.3e} mean-abs {mean:.3e}")
     assert mx <= MAX_ABS and mean <= MEAN_ABS
+
+
+@pytest.mark.parametrize("rows,vocab,dim", [(1, 32768, 768), (3, 32768, 768), (16, 32768, 768),
+                                            (5, 1000, 64), (2, 777, 2048)])
+def test_vocab_argmax(rows, vocab, dim):
+    """Greedy tokens from fp32 logits equal the fp32 argmax wherever the top
+    two logits are not within fp32 reassociation of each other, and exact
+    ties go to the lower index."""
+    from parrot import hip_moe
+    _say(f"vocab argmax rows={rows} vocab={vocab} dim={dim}")
+    g = torch.Generator().manual_seed(rows * 7 + dim)
+    w = (torch.randn(vocab, dim, generator=g) * 0.02).bfloat16()
+    h = torch.randn(rows, dim, generator=g).bfloat16()
+    # planted exact tie: rows 11 and 900 % vocab of the head are identical
+    # and made the best match of h[0]
+    w[11] = h[0] * 0.05
+    w[(900 % (vocab - 12)) + 12] = w[11]
+    with torch.no_grad():
+        got = hip_moe.vocab_argmax(h.cuda(), w.cuda()).cpu()
+    logits = h.double() @ w.double().T
+    top2 = logits.topk(2, dim=-1)
+    ref = logits.argmax(-1)
+    assert got[0].item() == 11
+    clear = (top2.values[:, 0] - top2.values[:, 1]) > 1e-4
+    assert torch.equal(got[clear], ref[clear])
