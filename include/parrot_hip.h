@@ -81,14 +81,17 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
  * non-NULL, read from fp32 tables cos_table / sin_table
  * [max_positions, head_dim / 2]; positions past the table are clamped to its
  * last row (a device position cannot be checked here).  v is copied.
+ * With vt_keys > 0, v is written transposed instead: v [batch, Hk,
+ * head_dim, vt_keys] (vt_keys >= seq; the layout parrot_causal_attention_bf16
+ * reads; entries past seq are left untouched).
  * head_dim % 4 == 0, H % Hk == 0, start + seq <= max_positions.
  * Replaces LocalGQA._project / _project_decode / _rope
  * (parrot/model.py:206-262), which run RoPE as strided bf16 elementwise ops. */
 int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* sin_table,
                          int64_t batch, int32_t seq, int32_t start, const int32_t* start_device,
                          int32_t max_positions, int32_t heads, int32_t kv_heads,
-                         int32_t head_dim, int32_t expand_kv, void* q, void* k, void* v,
-                         void* stream);
+                         int32_t head_dim, int32_t expand_kv, int32_t vt_keys, void* q,
+                         void* k, void* v, void* stream);
 
 /* Decode-step attention of the sliding-window GQA layers.  q [batch, H,
  * head_dim] and the new key / value rows k_new, v_new [batch, Hk, head_dim]
@@ -167,6 +170,27 @@ size_t parrot_vocab_argmax_workspace_bytes(int64_t rows, int32_t vocab);
 int parrot_vocab_argmax_bf16(const void* hidden, int64_t rows, int32_t dim, const void* weight,
                              int32_t vocab, int64_t* out_tokens, void* workspace,
                              size_t workspace_bytes, void* stream);
+
+/* Causal attention with an optional sliding window, for prefill and full
+ * forwards: out[b, i, h, :] = softmax_j(q[b,h,i] . k[b,h',j] * scale)
+ * v[b,h',j] over keys i - window < j <= i (window >= seq: plain causal),
+ * h' = h / (heads / kv_heads); fp32 scores, softmax and accumulation, P
+ * rounded to bf16 for its product with V, one bf16 rounding of the output.
+ * q [batch, heads, seq, head_dim] and k [batch, kv_heads, seq, head_dim]
+ * given by element strides {batch, head, row} with unit stride along
+ * head_dim; the values are given transposed, vt [batch, kv_heads, head_dim,
+ * >= roundup(seq, 32)] by strides {batch, head, dim row} with unit stride
+ * along the keys (entries past seq may hold anything).  Strides multiples of
+ * 8, bases 16-byte aligned; out [batch, seq, heads, head_dim] contiguous.
+ * head_dim in {64, 96, 128}.  Replaces scaled_dot_product_attention(...,
+ * is_causal=True) and the masked chunk loop of LocalGQA.prefill
+ * (parrot/model.py:264-295) and the causal SDPA of GlobalMLA.prefill
+ * (parrot/model.py:350-360). */
+int parrot_causal_attention_bf16(const void* q, const void* k, const void* vt,
+                                 const int64_t* q_strides, const int64_t* k_strides,
+                                 const int64_t* vt_strides, int64_t batch, int32_t seq,
+                                 int32_t heads, int32_t kv_heads, int32_t head_dim,
+                                 int32_t window, float scale, void* out, void* stream);
 
 /* Workspace bytes for the routing / grouping entry points. */
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts);

@@ -31,12 +31,14 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int, [_p, _i32, _p, _p, _f32, _p, _f32, _i64, _i32, _p, _p, _p]),
     "parrot_rope_qkv_bf16": (
         ctypes.c_int,
-        [_p, _p, _p, _i64, _i32, _i32, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),
+        [_p, _p, _p, _i64, _i32, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),
     "parrot_decode_attention_bf16": (
         ctypes.c_int,
         [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p]),
     "parrot_decode_moe_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "parrot_vocab_argmax_workspace_bytes": (_sz, [_i64, _i32]),
+    "parrot_causal_attention_bf16": (
+        ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p]),
     "parrot_vocab_argmax_bf16": (ctypes.c_int, [_p, _i64, _i32, _p, _i32, _p, _p, _sz, _p]),
     "parrot_decode_moe_bf16": (
         ctypes.c_int,

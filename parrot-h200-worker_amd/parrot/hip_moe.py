@@ -374,12 +374,14 @@ def vocab_argmax(h: Tensor, weight: Tensor) -> Tensor:
 # ---------------------------------------------------------------------------
 
 def rope_qkv(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, kv_heads: int, head_dim: int,
-             start: int, expand_kv: bool,
-             start_device: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+             start: int, expand_kv: bool, start_device: Tensor | None = None,
+             vt_keys: int = 0) -> tuple[Tensor, Tensor, Tensor]:
     """Split a packed q|k|v projection [b, t, (H + 2 Hk) d] into head-major
     q [b, H, t, d], k, v [b, Hk or H, t, d] and rotate q and k by RoPE at
     positions start .. start + t - 1 (fp32 tables [max_positions, d / 2]),
-    shifted by the device int32 ``start_device`` when given."""
+    shifted by the device int32 ``start_device`` when given.  With
+    ``vt_keys`` > 0 the values come back transposed, [b, Hk, d, vt_keys]
+    (columns past t unwritten), the layout ``causal_attention`` reads."""
     _require(qkv, "HIP RoPE")
     b, t, width = qkv.shape
     if width != (heads + 2 * kv_heads) * head_dim:
@@ -393,12 +395,67 @@ def rope_qkv(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, kv_heads: int, h
     kv_out = heads if expand_kv else kv_heads
     q = qkv.new_empty((b, heads, t, head_dim))
     k = qkv.new_empty((b, kv_out, t, head_dim))
-    v = qkv.new_empty((b, kv_out, t, head_dim))
+    if vt_keys:
+        v = qkv.new_empty((b, kv_heads, head_dim, vt_keys))
+    else:
+        v = qkv.new_empty((b, kv_out, t, head_dim))
     _abi.check(_abi.load().parrot_rope_qkv_bf16(
         ptr(qkv), ptr(cos), ptr(sin), b, t, start, ptr(start_device), cos.shape[0], heads,
-        kv_heads, head_dim, int(expand_kv), ptr(q), ptr(k), ptr(v), _stream(qkv.device)),
-        "parrot_rope_qkv_bf16")
+        kv_heads, head_dim, int(expand_kv), vt_keys, ptr(q), ptr(k), ptr(v),
+        _stream(qkv.device)), "parrot_rope_qkv_bf16")
     return q, k, v
+
+
+# ---------------------------------------------------------------------------
+# Causal attention for prefill / forward (cf. parrot/model.py:264-295, 350-360)
+# ---------------------------------------------------------------------------
+
+ATTENTION_HEAD_DIMS = (64, 96, 128)
+
+
+def padded_keys(t: int) -> int:
+    """Key capacity of a transposed value tensor for ``causal_attention``."""
+    return (t + 31) // 32 * 32
+
+
+def causal_attention(q: Tensor, k: Tensor, v: Tensor | None = None, *, scale: float,
+                     window: int | None = None, vt: Tensor | None = None) -> Tensor:
+    """softmax(q k^T * scale) v with key j visible to query i iff
+    i - window < j <= i, for q [b, H, t, d] and k [b, Hk, t, d] (any strides
+    with a unit last stride; Hk divides H), and the values either as v
+    [b, Hk, t, d] or already transposed as vt [b, Hk, d, >= padded_keys(t)]
+    (unit stride along the keys).  Returns [b, t, H * d] bf16, the layout of
+    the output projection's input."""
+    _require(q, "HIP causal attention")
+    b, heads, t, d = q.shape
+    kv_heads = k.shape[1]
+    if k.shape != (b, kv_heads, t, d) or heads % kv_heads:
+        raise RuntimeError("attention shapes do not match")
+    if d not in ATTENTION_HEAD_DIMS:
+        raise RuntimeError(f"HIP attention supports head widths {ATTENTION_HEAD_DIMS}")
+    if (v is None) == (vt is None):
+        raise RuntimeError("pass exactly one of v and vt")
+    if vt is None:
+        if v.shape != k.shape:
+            raise RuntimeError("attention shapes do not match")
+        vt = v.new_empty((b, kv_heads, d, padded_keys(t)))
+        vt[..., :t].copy_(v.transpose(-1, -2))
+    elif vt.shape[:3] != (b, kv_heads, d) or vt.shape[3] < padded_keys(t):
+        raise RuntimeError("transposed values must be [b, Hk, d, >= padded_keys(t)]")
+    tensors = []
+    for x in (q, k, vt):
+        if x.stride(-1) != 1 or any(st % 8 for st in x.stride()[:3]) or x.data_ptr() % 16:
+            x = x.contiguous()
+        tensors.append(x)
+    q, k, vt = tensors
+    out = q.new_empty((b, t, heads * d))
+    strides = [(ctypes.c_int64 * 3)(*x.stride()[:3]) for x in (q, k, vt)]
+    _abi.check(_abi.load().parrot_causal_attention_bf16(
+        ptr(q), ptr(k), ptr(vt), ctypes.cast(strides[0], ctypes.c_void_p),
+        ctypes.cast(strides[1], ctypes.c_void_p), ctypes.cast(strides[2], ctypes.c_void_p),
+        b, t, heads, kv_heads, d, t if window is None else window, scale, ptr(out),
+        _stream(q.device)), "parrot_causal_attention_bf16")
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -148,20 +148,21 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
 int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* sin_table,
                          int64_t batch, int32_t seq, int32_t start, const int32_t* start_device,
                          int32_t max_positions, int32_t heads, int32_t kv_heads,
-                         int32_t head_dim, int32_t expand_kv, void* q, void* k, void* v,
-                         void* stream) {
+                         int32_t head_dim, int32_t expand_kv, int32_t vt_keys, void* q,
+                         void* k, void* v, void* stream) {
   if (!qkv || !cos_table || !sin_table || !q || !k || !v) return PARROT_ERR_NULL_POINTER;
   if (batch < 0 || seq < 0 || start < 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
-      max_positions <= 0)
+      max_positions <= 0 || vt_keys < 0)
     return PARROT_ERR_BAD_SHAPE;
   if (heads % kv_heads || head_dim % 4) return PARROT_ERR_UNSUPPORTED;
   if (static_cast<int64_t>(start) + seq > max_positions) return PARROT_ERR_BAD_SHAPE;
+  if (vt_keys > 0 && (vt_keys < seq || expand_kv)) return PARROT_ERR_BAD_SHAPE;
   const uintptr_t bits = reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(q) |
                          reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v);
   if (bits & 7u) return PARROT_ERR_ALIGNMENT;
   return status(parrot::launch_rope_qkv(
       static_cast<const uint16_t*>(qkv), cos_table, sin_table, batch, seq, start, start_device,
-      max_positions, heads, kv_heads, head_dim, expand_kv, static_cast<uint16_t*>(q),
+      max_positions, heads, kv_heads, head_dim, expand_kv, vt_keys, static_cast<uint16_t*>(q),
       static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), as_stream(stream)));
 }
 
@@ -443,6 +444,34 @@ int parrot_vocab_argmax_bf16(const void* hidden, int64_t rows, int32_t dim, cons
       static_cast<const uint16_t*>(hidden), static_cast<int>(rows), dim,
       static_cast<const uint16_t*>(weight), vocab, part_v, part_i, out_tokens,
       as_stream(stream)));
+}
+
+int parrot_causal_attention_bf16(const void* q, const void* k, const void* vt,
+                                 const int64_t* q_strides, const int64_t* k_strides,
+                                 const int64_t* vt_strides, int64_t batch, int32_t seq,
+                                 int32_t heads, int32_t kv_heads, int32_t head_dim,
+                                 int32_t window, float scale, void* out, void* stream) {
+  if (!q || !k || !vt || !q_strides || !k_strides || !vt_strides || !out)
+    return PARROT_ERR_NULL_POINTER;
+  if (batch < 0 || seq < 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 || window <= 0)
+    return PARROT_ERR_BAD_SHAPE;
+  if (heads % kv_heads || !parrot::attention_head_dim_supported(head_dim) ||
+      batch > 65535 || heads > 65535)
+    return PARROT_ERR_UNSUPPORTED;
+  // V^T rows must hold roundup(seq, 32) keys (the kernel reads whole blocks).
+  const int64_t padded = (static_cast<int64_t>(seq) + 31) / 32 * 32;
+  if (vt_strides[2] < padded || vt_strides[1] < head_dim * vt_strides[2])
+    return PARROT_ERR_BAD_SHAPE;
+  for (int i = 0; i < 3; ++i)
+    if (q_strides[i] % 8 || k_strides[i] % 8 || vt_strides[i] % 8 || q_strides[i] < 0 ||
+        k_strides[i] < 0 || vt_strides[i] < 0)
+      return PARROT_ERR_ALIGNMENT;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(vt)) return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_causal_attention(
+      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+      static_cast<const uint16_t*>(vt), q_strides, k_strides, vt_strides,
+      static_cast<int>(batch), seq, heads, kv_heads, head_dim, window, scale,
+      static_cast<uint16_t*>(out), as_stream(stream)));
 }
 
 int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,

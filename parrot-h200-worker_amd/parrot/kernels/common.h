@@ -220,10 +220,12 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
 // RoPE + head-major split of a packed q|k|v projection (see rope.hip).
 // The first position is start (+ *start_device when non-null); positions
 // past the table are clamped to its last row.
+// With vt_keys > 0, v is written transposed: [batch, Hk, head_dim, vt_keys].
 hipError_t launch_rope_qkv(const uint16_t* qkv, const float* cos_t, const float* sin_t,
                            int64_t batch, int seq, int start, const int32_t* start_device,
                            int max_positions, int heads, int kv_heads, int head_dim,
-                           int expand_kv, uint16_t* q, uint16_t* k, uint16_t* v, hipStream_t s);
+                           int expand_kv, int vt_keys, uint16_t* q, uint16_t* k, uint16_t* v,
+                           hipStream_t s);
 
 // Decode-step attention over the generation caches (see decode.hip); the
 // position is read from device memory.
@@ -256,6 +258,18 @@ int vocab_argmax_max_rows();
 int vocab_argmax_groups(int vocab);
 hipError_t launch_vocab_argmax(const uint16_t* h, int rows, int dim, const uint16_t* w, int vocab,
                                float* part_v, int32_t* part_i, int64_t* out, hipStream_t s);
+
+// Causal / sliding-window attention (see attention.hip).  Strides are in
+// elements: [batch, head, row] for q and k (unit stride along head_dim),
+// [batch, head, dim row] for the transposed values vt (unit stride along the
+// keys, rows of at least roundup(seq, 32) keys); out [batch, seq, heads,
+// head_dim].
+bool attention_head_dim_supported(int head_dim);  // 64, 96, 128
+hipError_t launch_causal_attention(const uint16_t* q, const uint16_t* k, const uint16_t* vt,
+                                   const int64_t* q_strides, const int64_t* k_strides,
+                                   const int64_t* vt_strides, int batch, int seq, int heads,
+                                   int kv_heads, int head_dim, int window, float scale,
+                                   uint16_t* out, hipStream_t s);
 
 hipError_t launch_combine(const float* y_routed, const float* y_shared,
                           const uint16_t* addend, int64_t tokens, int dim,

@@ -11,7 +11,8 @@
 // Input: qkv [rows = batch * seq, (H + 2 Hk) * d] (one packed projection).
 // Output: q [batch, H, seq, d], k and v [batch, Hk or H, seq, d]; with
 // expand_kv each key/value head is written once for each of the H / Hk
-// query heads that share it.
+// query heads that share it; with vt_keys > 0 v is written transposed,
+// [batch, Hk, d, vt_keys], the value layout the attention kernel reads.
 #include "common.h"
 
 namespace parrot {
@@ -22,7 +23,7 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(
     const uint2* __restrict__ qkv, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, int64_t rows, int seq, int start,
     const int32_t* __restrict__ start_device, int max_positions, int heads, int kv_heads,
-    int head_dim, int expand, uint16_t* __restrict__ q, uint16_t* __restrict__ k,
+    int head_dim, int expand, int vt_keys, uint16_t* __restrict__ q, uint16_t* __restrict__ k,
     uint16_t* __restrict__ v) {
   const int quads = (heads + 2 * kv_heads) * head_dim / 4;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -54,6 +55,14 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(
   }
   const bool is_k = head < heads + kv_heads;
   const int kvh = head - heads - (is_k ? 0 : kv_heads);
+  if (!is_k && vt_keys > 0) {  // transposed values: [b, Hk, d, vt_keys]
+    uint16_t* col = v + ((b * kv_heads + kvh) * head_dim + w) * vt_keys + tp;
+    col[0] = static_cast<uint16_t>(x.x & 0xffffu);
+    col[vt_keys] = static_cast<uint16_t>(x.x >> 16);
+    col[2 * vt_keys] = static_cast<uint16_t>(x.y & 0xffffu);
+    col[3 * vt_keys] = static_cast<uint16_t>(x.y >> 16);
+    return;
+  }
   uint16_t* dst = is_k ? k : v;
   if (!expand) {
     *reinterpret_cast<uint2*>(dst + ((b * kv_out + kvh) * seq + tp) * head_dim + w) = x;
@@ -70,14 +79,15 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(
 hipError_t launch_rope_qkv(const uint16_t* qkv, const float* cos_t, const float* sin_t,
                            int64_t batch, int seq, int start, const int32_t* start_device,
                            int max_positions, int heads, int kv_heads, int head_dim,
-                           int expand_kv, uint16_t* q, uint16_t* k, uint16_t* v, hipStream_t s) {
+                           int expand_kv, int vt_keys, uint16_t* q, uint16_t* k, uint16_t* v,
+                           hipStream_t s) {
   const int64_t rows = batch * seq;
   const int64_t total = rows * (heads + 2 * kv_heads) * head_dim / 4;
   if (total == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((total + 255) / 256));
   rope_qkv_kernel<<<grid, 256, 0, s>>>(reinterpret_cast<const uint2*>(qkv), cos_t, sin_t, rows,
                                        seq, start, start_device, max_positions, heads, kv_heads,
-                                       head_dim, expand_kv, q, k, v);
+                                       head_dim, expand_kv, vt_keys, q, k, v);
   return hipGetLastError();
 }
 

@@ -281,6 +281,19 @@ class LocalGQA(nn.Module):
     def prefill(self, x: Tensor) -> tuple[Tensor, Tensor, Tensor]:
         b, t, _ = x.shape
         c = self.cfg
+        if self._hip(x):
+            from . import hip_moe
+            if c.head_dim in hip_moe.ATTENTION_HEAD_DIMS:
+                # One HIP kernel for the whole sliding-window causal
+                # attention, reading the grouped kv heads in place; the RoPE
+                # kernel writes the values transposed for it.
+                cos, sin = _rope_tables(c, x.new_empty(0, dtype=torch.float32))
+                q, k, vt = hip_moe.rope_qkv(F.linear(x, self._packed_qkv()), cos, sin,
+                                            c.n_heads, c.n_kv_heads, c.head_dim, 0, False,
+                                            vt_keys=hip_moe.padded_keys(t))
+                y = hip_moe.causal_attention(q, k, vt=vt, scale=c.head_dim ** -0.5,
+                                             window=c.window_size)
+                return self.out(y), k, vt[..., :t].transpose(-1, -2)
         if self._hip(x) and t <= c.window_size:
             # Every key of a sequence that fits the window is visible to all
             # later queries, so the banded mask is plain causal: one flash
@@ -384,6 +397,16 @@ class GlobalMLA(nn.Module):
             return y.view(b, t, c.n_heads, c.head_dim).transpose(1, 2)
 
         latent = self.kv_down(x)
+        if c.uses_hip and _hip_inference(x):
+            from . import hip_moe
+            if c.head_dim in hip_moe.ATTENTION_HEAD_DIMS:
+                # Values produced transposed, [b, H * d, keys], by one GEMM.
+                latent_t = F.pad(latent.transpose(1, 2), (0, hip_moe.padded_keys(t) - t))
+                vt = torch.matmul(self.v_up.weight, latent_t).view(
+                    b, c.n_heads, c.head_dim, -1)
+                y = hip_moe.causal_attention(heads(self.q(x)), heads(self.k_up(latent)), vt=vt,
+                                             scale=c.head_dim ** -0.5)
+                return self.out(y), latent
         y = F.scaled_dot_product_attention(
             heads(self.q(x)), heads(self.k_up(latent)), heads(self.v_up(latent)),
             is_causal=True)

@@ -98,8 +98,26 @@ def test_argument_validation_without_gpu(lib):
     assert lib.parrot_grouped_experts_bf16(
         fake, 64, 64, 8, 128, 64, 32, *([fake] * 9), null, fake, fake, 16, null) == -4
     # RoPE: start + seq past the table
-    assert lib.parrot_rope_qkv_bf16(fake, fake, fake, 1, 4, 126, null, 128, 8, 2, 96, 0,
+    assert lib.parrot_rope_qkv_bf16(fake, fake, fake, 1, 4, 126, null, 128, 8, 2, 96, 0, 0,
                                     fake, fake, fake, null) == -2
+    # RoPE: transposed values need room for every key and no kv expansion
+    assert lib.parrot_rope_qkv_bf16(fake, fake, fake, 1, 40, 0, null, 128, 8, 2, 96, 0, 32,
+                                    fake, fake, fake, null) == -2
+    assert lib.parrot_rope_qkv_bf16(fake, fake, fake, 1, 4, 0, null, 128, 8, 2, 96, 1, 32,
+                                    fake, fake, fake, null) == -2
+    # causal attention: unsupported head width, short V^T rows, odd strides
+    st = (ctypes.c_int64 * 3)(8 * 512 * 96, 512 * 96, 96)
+    vt_ok = (ctypes.c_int64 * 3)(2 * 96 * 512, 96 * 512, 512)
+    vt_short = (ctypes.c_int64 * 3)(2 * 96 * 496, 96 * 496, 496)
+    odd = (ctypes.c_int64 * 3)(8 * 512 * 96, 512 * 96, 100)
+
+    def attn(q_st=st, vt_st=vt_ok, d=96, seq=512):
+        return lib.parrot_causal_attention_bf16(
+            fake, fake, fake, ctypes.cast(q_st, ctypes.c_void_p), ctypes.cast(st, ctypes.c_void_p),
+            ctypes.cast(vt_st, ctypes.c_void_p), 1, seq, 8, 2, d, 2048, 0.1, fake, null)
+    assert attn(d=80) == -3
+    assert attn(vt_st=vt_short) == -2
+    assert attn(q_st=odd) == -5
     # decode attention: null position, head_dim % 8, heads % kv_heads, LDS budget, alignment
     dec = dict(batch=2, heads=8, kv_heads=2, head_dim=96, max_positions=4096, window=2048)
 

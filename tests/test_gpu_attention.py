@@ -1,0 +1,74 @@
+"""GPU parity of the causal / sliding-window attention kernel against an
+fp32 CPU restatement of scaled_dot_product_attention with the reference's
+masks (parrot/model.py:264-295 band mask, 350-360 causal), with PyTorch's
+own bf16 flash attention on the GPU as a control for the error bf16
+operands allow."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _reference(q, k, v, scale, window):
+    b, H, t, d = q.shape
+    rep = H // k.shape[1]
+    k = k.float().repeat_interleave(rep, dim=1)
+    v = v.float().repeat_interleave(rep, dim=1)
+    i = torch.arange(t)[:, None]
+    j = torch.arange(t)[None, :]
+    mask = (j <= i) & (j > i - window)
+    s = (q.float() @ k.transpose(-1, -2)) * scale
+    s = s.masked_fill(~mask, float("-inf"))
+    return (torch.softmax(s, dim=-1) @ v).transpose(1, 2).reshape(b, t, H * d)
+
+
+@pytest.mark.parametrize("b,H,Hk,t,d,window,strided", [
+    (1, 8, 2, 512, 96, 2048, False),   # local layer of the bs1x512 forward
+    (2, 8, 8, 77, 96, 4096, True),     # MLA layer: heads view of [b, t, H*d]
+    (1, 4, 1, 300, 64, 100, False),    # band narrower than the sequence
+    (2, 2, 2, 33, 128, 33, False),
+    (3, 8, 2, 1, 96, 2048, False),
+    (1, 8, 2, 17, 96, 5, True),
+])
+def test_causal_attention(b, H, Hk, t, d, window, strided):
+    from parrot import hip_moe
+    _say(f"attention b={b} H={H} Hk={Hk} t={t} d={d} window={window} strided={strided}")
+    g = torch.Generator().manual_seed(t * 31 + d)
+    if strided:
+        q = torch.randn(b, t, H * d, generator=g).bfloat16().view(b, t, H, d).transpose(1, 2)
+        k = torch.randn(b, t, Hk * d, generator=g).bfloat16().view(b, t, Hk, d).transpose(1, 2)
+        v = torch.randn(b, t, Hk * d, generator=g).bfloat16().view(b, t, Hk, d).transpose(1, 2)
+    else:
+        q = torch.randn(b, H, t, d, generator=g).bfloat16()
+        k = torch.randn(b, Hk, t, d, generator=g).bfloat16()
+        v = torch.randn(b, Hk, t, d, generator=g).bfloat16()
+    scale = d ** -0.5
+    with torch.no_grad():
+        got = hip_moe.causal_attention(q.cuda(), k.cuda(), v.cuda(), scale=scale,
+                                       window=window).float().cpu()
+        # the same through transposed values whose padding holds non-finite bytes
+        vt = torch.full((b, Hk, d, hip_moe.padded_keys(t) + 8), float("nan"),
+                        dtype=torch.bfloat16, device="cuda")
+        vt[..., :t] = v.cuda().transpose(-1, -2)
+        got_t = hip_moe.causal_attention(q.cuda(), k.cuda(), vt=vt, scale=scale,
+                                         window=window).float().cpu()
+    assert torch.equal(got, got_t)
+    ref = _reference(q, k, v, scale, window)
+    err = (got - ref).abs()
+    _say(f"  max-abs {err.max():.3e} mean-abs {err.mean():.3e}")
+    assert err.max() <= 1e-2 and err.mean() <= 1e-3
+    if window >= t:  # PyTorch's bf16 attention as the control
+        rep = H // Hk
+        with torch.no_grad():
+            ctl = F.scaled_dot_product_attention(
+                q.cuda(), k.cuda().repeat_interleave(rep, 1).contiguous(),
+                v.cuda().repeat_interleave(rep, 1).contiguous(), is_causal=True)
+        ctl = ctl.float().cpu().transpose(1, 2).reshape(b, t, H * d)
+        ctl_err = (ctl - ref).abs()
+        _say(f"  control max-abs {ctl_err.max():.3e} mean-abs {ctl_err.mean():.3e}")
+        assert err.mean() <= 2 * ctl_err.mean() + 1e-5

@@ -218,3 +218,10 @@ def test_rope_qkv(b, t, start, expand):
     _ulp_ok(q, ref_q)
     _ulp_ok(k, ref_k.repeat_interleave(rep, dim=1))
     assert torch.equal(v.float().cpu(), ref_v.repeat_interleave(rep, dim=1))
+    if not expand:  # transposed values for the attention kernel, same q and k
+        with torch.no_grad():
+            q2, k2, vt = hip_moe.rope_qkv(qkv, cos, sin, H, Hk, d, start, False,
+                                          vt_keys=hip_moe.padded_keys(t))
+        assert torch.equal(q2, q) and torch.equal(k2, k)
+        assert vt.shape == (b, Hk, d, hip_moe.padded_keys(t))
+        assert torch.equal(vt[..., :t].transpose(-1, -2), v)
