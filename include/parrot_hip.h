@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 2
+#define PARROT_ABI_VERSION 3
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -191,6 +191,47 @@ int parrot_causal_attention_bf16(const void* q, const void* k, const void* vt,
                                  const int64_t* vt_strides, int64_t batch, int32_t seq,
                                  int32_t heads, int32_t kv_heads, int32_t head_dim,
                                  int32_t window, float scale, void* out, void* stream);
+
+/* Dense projection y = x . W^T (bf16 in and out, fp32 accumulation) for the
+ * attention layers' linear maps, with the weight pre-packed in MFMA fragment
+ * order: w_packed holds W [n, k] as blocks of 16 rows x 32 k (1 KB), row
+ * group major and k step minor; inside a block lane l = 16 g + r holds row r,
+ * k = 8 g .. 8 g + 7 (16 bytes at 16 l).  x [rows, k] with row stride lda;
+ * out [rows, n] with row stride ldo; when addend [rows, n] (row stride
+ * ld_addend) is non-NULL, out = bf16(addend + bf16(x W^T)) (addend may be
+ * out itself).  k % 64 == 0, k <= 2048, n % 16 == 0, lda % 8 == 0, x
+ * 16-byte aligned.
+ * Replaces the bias-free nn.Linear maps of LocalGQA / GlobalMLA
+ * (parrot/model.py:167-230, 331-432) with the residual add of the
+ * attention output as in attention_output_decode_bf16
+ * (parrot/kernels/moe_bf16.metal:1364-1389). */
+int parrot_proj_bf16(const void* x, int64_t rows, int32_t k, int64_t lda, const void* w_packed,
+                     int32_t n, const void* addend, int64_t ld_addend, void* out, int64_t ldo,
+                     void* stream);
+
+/* As parrot_proj_bf16 for x [batch * seq, k] (contiguous) without addend,
+ * stored transposed per sequence: out[(b * n + j) * ld_keys + t] =
+ * bf16(x W^T)[b * seq + t, j], ld_keys >= seq, ld_keys % 4 == 0, out 8-byte
+ * aligned; entries t >= seq are not written.  Produces the transposed values
+ * parrot_causal_attention_bf16 reads (v_up of GlobalMLA.prefill,
+ * parrot/model.py:350-360). */
+int parrot_proj_transposed_bf16(const void* x, int64_t batch, int32_t seq, int32_t k,
+                                const void* w_packed, int32_t n, int32_t ld_keys, void* out,
+                                void* stream);
+
+/* The packed q|k|v projection of a local-attention layer fused with RoPE and
+ * the head split: x [batch * seq, dim] (contiguous) times the packed
+ * [(H + 2 Hk) * head_dim, dim] weight (as parrot_proj_bf16), each output
+ * rounded to bf16, then exactly the transform of parrot_rope_qkv_bf16 with
+ * expand_kv = 0 (q, k and v, or v transposed when vt_keys > 0).  Replaces
+ * F.linear + parrot_rope_qkv_bf16, i.e. the projections, _apply_rope and
+ * the head split of LocalGQA (parrot/model.py:176-230). */
+int parrot_proj_rope_qkv_bf16(const void* x, int64_t batch, int32_t seq, int32_t dim,
+                              const void* w_packed, const float* cos_table,
+                              const float* sin_table, int32_t start,
+                              const int32_t* start_device, int32_t max_positions, int32_t heads,
+                              int32_t kv_heads, int32_t head_dim, int32_t vt_keys, void* q,
+                              void* k, void* v, void* stream);
 
 /* Workspace bytes for the routing / grouping entry points. */
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts);

@@ -257,8 +257,16 @@ def pack_expert_weights(module: "MoE") -> tuple[Tensor, Tensor, Tensor, Tensor]:
     return packed
 
 
-def invalidate_packed_weights(module: "MoE") -> None:
-    module.__dict__.pop("_hip_packed", None)
+_PACKED_CACHES = ("_hip_packed", "_qkv_weight", "_absorbed_weights", "_absorbed_f32_weights")
+
+
+def invalidate_packed_weights(module: torch.nn.Module) -> None:
+    """Drop every packed / derived weight cached on ``module`` and its
+    submodules (expert packs, packed projections, absorbed MLA maps)."""
+    for sub in module.modules():
+        for key in [k for k in sub.__dict__
+                    if k in _PACKED_CACHES or k.startswith("_packed_linear_")]:
+            del sub.__dict__[key]
 
 
 # ---------------------------------------------------------------------------
@@ -403,6 +411,107 @@ def rope_qkv(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, kv_heads: int, h
         ptr(qkv), ptr(cos), ptr(sin), b, t, start, ptr(start_device), cos.shape[0], heads,
         kv_heads, head_dim, int(expand_kv), vt_keys, ptr(q), ptr(k), ptr(v),
         _stream(qkv.device)), "parrot_rope_qkv_bf16")
+    return q, k, v
+
+
+# ---------------------------------------------------------------------------
+# Dense projections of the attention layers (cf. parrot/model.py:167-230,
+# 331-432; parrot/kernels/moe_bf16.metal:1364-1389 for the residual add)
+# ---------------------------------------------------------------------------
+
+def proj_supported(k: int, n: int) -> bool:
+    """Shapes the projection kernels take: k % 64 == 0, k <= 2048, n % 16 == 0."""
+    return 0 < k <= 2048 and k % 64 == 0 and n > 0 and n % 16 == 0
+
+
+def pack_linear(owner, name: str, weights: tuple[Tensor, ...]) -> Tensor:
+    """The row concatenation of ``weights`` ([n_i, k] each) in MFMA fragment
+    order (``_fragment_order``), cached on ``owner`` (attribute
+    ``_packed_linear_<name>``, so no method is shadowed) until a weight
+    changes.  As for the expert weights, an eval-mode owner under no-grad
+    reuses the cache without re-checking versions."""
+    name = "_packed_linear_" + name
+    cached = owner.__dict__.get(name)
+    if cached is not None and not torch.is_grad_enabled() and not owner.training:
+        return cached[1]
+    version = tuple((p._version, p.device, p.dtype, p.data_ptr()) for p in weights)
+    if cached is None or cached[0] != version:
+        with torch.no_grad():
+            w = torch.cat([p.detach() for p in weights], 0)
+            cached = (version, _fragment_order(w.contiguous()))
+        owner.__dict__[name] = cached
+    return cached[1]
+
+
+def _rows(x: Tensor) -> Tensor:
+    """x as a [rows, k] matrix the projection kernels can read in place."""
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    return x2
+
+
+def proj(x: Tensor, packed: Tensor, n: int, addend: Tensor | None = None) -> Tensor:
+    """y = x W^T for x [..., k] and W [n, k] packed by ``pack_linear``; with
+    ``addend`` [..., n], bf16(addend + bf16(x W^T)) (the residual add of the
+    attention output)."""
+    _require(x, "HIP projection")
+    x2 = _rows(x)
+    rows, k = x2.shape
+    if packed.numel() != n * k:
+        raise RuntimeError("packed projection weight does not match the input width")
+    out = x.new_empty((*x.shape[:-1], n))
+    add = None
+    if addend is not None:
+        if addend.shape != out.shape or addend.dtype != x.dtype:
+            raise RuntimeError("projection addend must match the output")
+        add = addend.reshape(rows, n).contiguous()
+    _abi.check(_abi.load().parrot_proj_bf16(
+        ptr(x2), rows, k, x2.stride(0), ptr(packed), n, ptr(add), n, ptr(out), n,
+        _stream(x.device)), "parrot_proj_bf16")
+    return out
+
+
+def proj_transposed(x: Tensor, packed: Tensor, n: int, keys: int) -> Tensor:
+    """(x W^T) transposed per sequence: x [b, t, k] -> [b, n, keys] with
+    columns past t unwritten (``causal_attention``'s value layout)."""
+    _require(x, "HIP projection")
+    b, t, k = x.shape
+    if packed.numel() != n * k:
+        raise RuntimeError("packed projection weight does not match the input width")
+    x = x.contiguous()
+    out = x.new_empty((b, n, keys))
+    _abi.check(_abi.load().parrot_proj_transposed_bf16(
+        ptr(x), b, t, k, ptr(packed), n, keys, ptr(out), _stream(x.device)),
+        "parrot_proj_transposed_bf16")
+    return out
+
+
+def proj_rope_qkv(x: Tensor, packed: Tensor, cos: Tensor, sin: Tensor, heads: int,
+                  kv_heads: int, head_dim: int, start: int = 0,
+                  start_device: Tensor | None = None,
+                  vt_keys: int = 0) -> tuple[Tensor, Tensor, Tensor]:
+    """The packed q|k|v projection of x [b, t, dim] fused with ``rope_qkv``
+    (expand_kv off): the same q, k and v (or v transposed with ``vt_keys``),
+    bit for bit, as ``rope_qkv(F.linear(x, W), ...)`` with W unpacked."""
+    _require(x, "HIP projection")
+    b, t, dim = x.shape
+    n = (heads + 2 * kv_heads) * head_dim
+    if packed.numel() != n * dim:
+        raise RuntimeError("packed q|k|v weight does not match the head layout")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise RuntimeError("RoPE tables must be fp32")
+    if start_device is not None and (start_device.dtype != torch.int32 or
+                                     start_device.device != x.device):
+        raise RuntimeError("start_device must be an int32 tensor on the input's device")
+    x = x.contiguous()
+    q = x.new_empty((b, heads, t, head_dim))
+    k = x.new_empty((b, kv_heads, t, head_dim))
+    v = x.new_empty((b, kv_heads, head_dim, vt_keys) if vt_keys else (b, kv_heads, t, head_dim))
+    _abi.check(_abi.load().parrot_proj_rope_qkv_bf16(
+        ptr(x), b, t, dim, ptr(packed), ptr(cos), ptr(sin), start, ptr(start_device),
+        cos.shape[0], heads, kv_heads, head_dim, vt_keys, ptr(q), ptr(k), ptr(v),
+        _stream(x.device)), "parrot_proj_rope_qkv_bf16")
     return q, k, v
 
 

@@ -474,6 +474,67 @@ int parrot_causal_attention_bf16(const void* q, const void* k, const void* vt,
       static_cast<uint16_t*>(out), as_stream(stream)));
 }
 
+int parrot_proj_bf16(const void* x, int64_t rows, int32_t k, int64_t lda, const void* w_packed,
+                     int32_t n, const void* addend, int64_t ld_addend, void* out, int64_t ldo,
+                     void* stream) {
+  if (!x || !w_packed || !out) return PARROT_ERR_NULL_POINTER;
+  if (rows < 0 || k <= 0 || n <= 0 || lda < k || ldo < n || (addend && ld_addend < n))
+    return PARROT_ERR_BAD_SHAPE;
+  if (!parrot::proj_shape_supported(k, n) || rows > INT32_MAX) return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w_packed) || lda % 8) return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_proj_store(
+      static_cast<const uint16_t*>(x), static_cast<int>(rows), k, lda,
+      static_cast<const uint16_t*>(w_packed), n, static_cast<const uint16_t*>(addend), ld_addend,
+      static_cast<uint16_t*>(out), ldo, as_stream(stream)));
+}
+
+int parrot_proj_transposed_bf16(const void* x, int64_t batch, int32_t seq, int32_t k,
+                                const void* w_packed, int32_t n, int32_t ld_keys, void* out,
+                                void* stream) {
+  if (!x || !w_packed || !out) return PARROT_ERR_NULL_POINTER;
+  if (batch < 0 || seq < 0 || k <= 0 || n <= 0 || ld_keys < seq) return PARROT_ERR_BAD_SHAPE;
+  if (!parrot::proj_shape_supported(k, n) || batch * seq > INT32_MAX)
+    return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w_packed) || (reinterpret_cast<uintptr_t>(out) & 7u) ||
+      ld_keys % 4)
+    return PARROT_ERR_ALIGNMENT;
+  if (batch == 0 || seq == 0) return PARROT_OK;
+  return status(parrot::launch_proj_transposed(
+      static_cast<const uint16_t*>(x), static_cast<int>(batch * seq), seq, k,
+      static_cast<const uint16_t*>(w_packed), n, ld_keys, static_cast<uint16_t*>(out),
+      as_stream(stream)));
+}
+
+int parrot_proj_rope_qkv_bf16(const void* x, int64_t batch, int32_t seq, int32_t dim,
+                              const void* w_packed, const float* cos_table,
+                              const float* sin_table, int32_t start,
+                              const int32_t* start_device, int32_t max_positions, int32_t heads,
+                              int32_t kv_heads, int32_t head_dim, int32_t vt_keys, void* q,
+                              void* k, void* v, void* stream) {
+  if (!x || !w_packed || !cos_table || !sin_table || !q || !k || !v)
+    return PARROT_ERR_NULL_POINTER;
+  // The same shape rules as parrot_rope_qkv_bf16 (a device start on top of
+  // `start` is clamped by the kernel).
+  if (batch < 0 || seq < 0 || start < 0 || dim <= 0 || heads <= 0 || kv_heads <= 0 ||
+      head_dim <= 0 || max_positions <= 0 || vt_keys < 0 || (vt_keys > 0 && vt_keys < seq) ||
+      static_cast<int64_t>(start) + seq > max_positions)
+    return PARROT_ERR_BAD_SHAPE;
+  if (heads % kv_heads || head_dim % 4) return PARROT_ERR_UNSUPPORTED;
+  const int64_t n = static_cast<int64_t>(heads + 2 * kv_heads) * head_dim;
+  if (n > INT32_MAX || !parrot::proj_shape_supported(dim, static_cast<int>(n)) ||
+      batch * seq > INT32_MAX)
+    return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w_packed) ||
+      (vt_keys > 0 && ((reinterpret_cast<uintptr_t>(v) & 7u) || vt_keys % 4)))
+    return PARROT_ERR_ALIGNMENT;
+  if (batch == 0 || seq == 0) return PARROT_OK;
+  return status(parrot::launch_proj_rope_qkv(
+      static_cast<const uint16_t*>(x), static_cast<int>(batch * seq), seq, dim,
+      static_cast<const uint16_t*>(w_packed), cos_table, sin_table, start, start_device,
+      max_positions, heads, kv_heads, head_dim, vt_keys, static_cast<uint16_t*>(q),
+      static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), as_stream(stream)));
+}
+
 int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,
                                 int32_t hidden_dim, int32_t shared_dim, int32_t capacity,
                                 const int32_t* counts, const int32_t* offsets,

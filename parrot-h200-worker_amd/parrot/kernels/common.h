@@ -41,6 +41,32 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Raw buffer loads: the per-lane byte offset stays fixed over a k loop and
+// the step offset travels in an SGPR, so the loop carries no 64-bit address
+// arithmetic; reads past `bytes` return zero instead of faulting.
+constexpr int kBufferWord3 = 0x00020000;  // gfx9-family buffer resource word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferWord3);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
+                                               uint32_t soffset) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// One RoPE rotation pair (x[2i], x[2i+1]) by angle (c, s), in fp32 with the
+// products contracted the same way wherever it is applied, so the fused and
+// the stand-alone RoPE paths round identically.
+__device__ __forceinline__ float rope_even(float e, float o, float c, float s) {
+  return __builtin_fmaf(e, c, -(o * s));
+}
+__device__ __forceinline__ float rope_odd(float e, float o, float c, float s) {
+  return __builtin_fmaf(e, s, o * c);
+}
+
 // DPP lane exchange inside rows of 16 lanes (VALU latency, no LDS trip).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
@@ -274,5 +300,18 @@ hipError_t launch_causal_attention(const uint16_t* q, const uint16_t* k, const u
 hipError_t launch_combine(const float* y_routed, const float* y_shared,
                           const uint16_t* addend, int64_t tokens, int dim,
                           uint16_t* out, hipStream_t s);
+
+// Dense projections y = x W^T, W packed in MFMA fragment order (proj.hip).
+bool proj_shape_supported(int k, int n);  // k % 64 == 0, k <= 2048, n % 16 == 0
+hipError_t launch_proj_store(const uint16_t* x, int rows, int k, int64_t lda, const uint16_t* w,
+                             int n, const uint16_t* addend, int64_t ld_addend, uint16_t* out,
+                             int64_t ldo, hipStream_t s);
+hipError_t launch_proj_transposed(const uint16_t* x, int rows, int seq, int k, const uint16_t* w,
+                                  int n, int ld_keys, uint16_t* out, hipStream_t s);
+hipError_t launch_proj_rope_qkv(const uint16_t* x, int rows, int seq, int dim, const uint16_t* w,
+                                const float* cos_t, const float* sin_t, int start,
+                                const int32_t* start_device, int max_positions, int heads,
+                                int kv_heads, int head_dim, int vt_keys, uint16_t* q,
+                                uint16_t* k, uint16_t* v, hipStream_t s);
 
 }  // namespace parrot

@@ -45,20 +45,6 @@ struct GemmArgs {
   float* y_shared;            // phase 2 output [T, dim]
 };
 
-// Raw buffer loads: the per-lane byte offset is fixed for the whole k loop
-// and the stage offset travels in an SGPR, so the loop carries no 64-bit
-// address arithmetic; reads past `bytes` return zero instead of faulting.
-constexpr int kBufferWord3 = 0x00020000;  // gfx9-family buffer resource word 3
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferWord3);
-}
-
-__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
-                                               uint32_t soffset) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
-}
-
 // Which row segment and M-tile does this workgroup own?  One vector load of
 // the expert counts (lane e holds counts[e]), then a uniform scan over the
 // lanes' tile counts with readlane -- no chain of dependent memory loads.
@@ -92,8 +78,6 @@ struct WaveLayout {
   static constexpr int kWavesM = BM >= 64 ? 2 : 1;
   static constexpr int kWavesN = 4 / kWavesM;
 };
-
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Waits until at most N vector-memory loads of this wavefront are
 // outstanding, then joins the workgroup barrier.  Written out because

@@ -44,8 +44,8 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(
     const float c1 = cos_t[pos + 1], s1 = sin_t[pos + 1];
     const float e0 = lo_bf16(x.x), o0 = hi_bf16(x.x);
     const float e1 = lo_bf16(x.y), o1 = hi_bf16(x.y);
-    x.x = pack_bf16x2(e0 * c0 - o0 * s0, e0 * s0 + o0 * c0);
-    x.y = pack_bf16x2(e1 * c1 - o1 * s1, e1 * s1 + o1 * c1);
+    x.x = pack_bf16x2(rope_even(e0, o0, c0, s0), rope_odd(e0, o0, c0, s0));
+    x.y = pack_bf16x2(rope_even(e1, o1, c1, s1), rope_odd(e1, o1, c1, s1));
   }
   const int kv_out = expand ? heads : kv_heads;
   const int rep = heads / kv_heads;

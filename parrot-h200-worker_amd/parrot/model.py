@@ -278,22 +278,61 @@ class LocalGQA(nn.Module):
         v = self._heads(self.v(x), c.n_kv_heads)
         return q, k, v
 
-    def prefill(self, x: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    def fuses_addend(self, x: Tensor) -> bool:
+        """True when ``prefill(x, addend)`` folds the residual add into the
+        output projection kernel."""
+        return self._hip(x) and self._fused_projections()
+
+    def _fused_projections(self) -> bool:
+        from . import hip_moe
+        c = self.cfg
+        width = c.n_heads * c.head_dim
+        return (c.head_dim % 4 == 0 and
+                hip_moe.proj_supported(c.dim, width + 2 * c.n_kv_heads * c.head_dim) and
+                hip_moe.proj_supported(width, c.dim))
+
+    def _project_out(self, y: Tensor, addend: Tensor | None) -> Tensor:
+        """out(y) (+ addend, rounded as bf16(addend + bf16(out(y))))."""
+        if self._hip(y) and self._fused_projections():
+            from . import hip_moe
+            packed = hip_moe.pack_linear(self, "out", (self.out.weight,))
+            return hip_moe.proj(y, packed, self.cfg.dim, addend=addend)
+        result = self.out(y)
+        return result if addend is None else addend + result
+
+    def _qkv_fragments(self) -> Tensor:
+        from . import hip_moe
+        return hip_moe.pack_linear(self, "qkv", (self.q.weight, self.k.weight, self.v.weight))
+
+    def prefill(self, x: Tensor, addend: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+        """(out(attention(x)) [+ addend], keys, values) over the whole sequence."""
         b, t, _ = x.shape
         c = self.cfg
         if self._hip(x):
             from . import hip_moe
             if c.head_dim in hip_moe.ATTENTION_HEAD_DIMS:
                 # One HIP kernel for the whole sliding-window causal
-                # attention, reading the grouped kv heads in place; the RoPE
-                # kernel writes the values transposed for it.
+                # attention, reading the grouped kv heads in place; the
+                # projection (+ RoPE) kernel writes the values transposed.
                 cos, sin = _rope_tables(c, x.new_empty(0, dtype=torch.float32))
-                q, k, vt = hip_moe.rope_qkv(F.linear(x, self._packed_qkv()), cos, sin,
-                                            c.n_heads, c.n_kv_heads, c.head_dim, 0, False,
-                                            vt_keys=hip_moe.padded_keys(t))
+                keys = hip_moe.padded_keys(t)
+                if self._fused_projections():
+                    q, k, vt = hip_moe.proj_rope_qkv(x, self._qkv_fragments(), cos, sin,
+                                                     c.n_heads, c.n_kv_heads, c.head_dim,
+                                                     vt_keys=keys)
+                else:
+                    q, k, vt = hip_moe.rope_qkv(F.linear(x, self._packed_qkv()), cos, sin,
+                                                c.n_heads, c.n_kv_heads, c.head_dim, 0, False,
+                                                vt_keys=keys)
                 y = hip_moe.causal_attention(q, k, vt=vt, scale=c.head_dim ** -0.5,
                                              window=c.window_size)
-                return self.out(y), k, vt[..., :t].transpose(-1, -2)
+                return self._project_out(y, addend), k, vt[..., :t].transpose(-1, -2)
+        result, k, v = self._prefill_torch(x)
+        return (result if addend is None else addend + result), k, v
+
+    def _prefill_torch(self, x: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+        b, t, _ = x.shape
+        c = self.cfg
         if self._hip(x) and t <= c.window_size:
             # Every key of a sequence that fits the window is visible to all
             # later queries, so the banded mask is plain causal: one flash
@@ -317,8 +356,8 @@ class LocalGQA(nn.Module):
             y = torch.cat(parts, dim=2)
         return self.out(y.transpose(1, 2).reshape(b, t, -1)), k, v
 
-    def forward(self, x: Tensor) -> Tensor:
-        return self.prefill(x)[0]
+    def forward(self, x: Tensor, addend: Tensor | None = None) -> Tensor:
+        return self.prefill(x, addend)[0]
 
     def _packed_qkv(self) -> Tensor:
         cached = self.__dict__.get("_qkv_weight")
@@ -345,13 +384,17 @@ class LocalGQA(nn.Module):
             # and value and attends over the window (parrot/model.py:239-262).
             from . import hip_moe
             cos, sin = _rope_tables(c, x.new_empty(0, dtype=torch.float32))
-            q, k, v = hip_moe.rope_qkv(F.linear(x, self._packed_qkv()), cos, sin, c.n_heads,
-                                       c.n_kv_heads, c.head_dim, 0, False,
-                                       start_device=position_device)
+            if self._fused_projections():
+                q, k, v = hip_moe.proj_rope_qkv(x, self._qkv_fragments(), cos, sin, c.n_heads,
+                                                c.n_kv_heads, c.head_dim,
+                                                start_device=position_device)
+            else:
+                q, k, v = hip_moe.rope_qkv(F.linear(x, self._packed_qkv()), cos, sin, c.n_heads,
+                                           c.n_kv_heads, c.head_dim, 0, False,
+                                           start_device=position_device)
             y = hip_moe.decode_attention(q, k, v, cache.key, cache.value, position_device,
                                          c.window_size, c.head_dim ** -0.5)
-            result = self.out(y.view(b, 1, -1))
-            return result if addend is None else addend + result
+            return self._project_out(y.view(b, 1, -1), addend)
         if self._hip(x):
             q, k, v = self._qkv(x, start=position)
         else:
@@ -386,16 +429,46 @@ class GlobalMLA(nn.Module):
         self.v_up = nn.Linear(cfg.kv_latent_dim, width, bias=False)
         self.out = nn.Linear(width, cfg.dim, bias=False)
 
-    def forward(self, x: Tensor) -> Tensor:
-        return self.prefill(x)[0]
+    def forward(self, x: Tensor, addend: Tensor | None = None) -> Tensor:
+        return self.prefill(x, addend)[0]
 
-    def prefill(self, x: Tensor) -> tuple[Tensor, Tensor]:
+    def fuses_addend(self, x: Tensor) -> bool:
+        """True when ``prefill(x, addend)`` folds the residual add into the
+        output projection kernel."""
+        return self.cfg.uses_hip and _hip_inference(x) and self._fused_projections()
+
+    def _fused_projections(self) -> bool:
+        from . import hip_moe
+        c = self.cfg
+        width, r = c.n_heads * c.head_dim, c.kv_latent_dim
+        return (c.head_dim in hip_moe.ATTENTION_HEAD_DIMS and
+                hip_moe.proj_supported(c.dim, width) and hip_moe.proj_supported(c.dim, r) and
+                hip_moe.proj_supported(r, width) and hip_moe.proj_supported(width, c.dim))
+
+    def _fragments(self, name: str) -> Tensor:
+        from . import hip_moe
+        return hip_moe.pack_linear(self, name, (getattr(self, name).weight,))
+
+    def prefill(self, x: Tensor, addend: Tensor | None = None) -> tuple[Tensor, Tensor]:
+        """(out(attention(x)) [+ addend], latent) over the whole sequence."""
         b, t, _ = x.shape
         c = self.cfg
+        width = c.n_heads * c.head_dim
 
         def heads(y):
             return y.view(b, t, c.n_heads, c.head_dim).transpose(1, 2)
 
+        if c.uses_hip and _hip_inference(x) and self._fused_projections():
+            # Five projection kernels around one attention kernel; v_up
+            # writes the values transposed, [b, H * d, keys].
+            from . import hip_moe
+            latent = hip_moe.proj(x, self._fragments("kv_down"), c.kv_latent_dim)
+            q = hip_moe.proj(x, self._fragments("q"), width)
+            k = hip_moe.proj(latent, self._fragments("k_up"), width)
+            vt = hip_moe.proj_transposed(latent, self._fragments("v_up"), width,
+                                         hip_moe.padded_keys(t)).view(b, c.n_heads, c.head_dim, -1)
+            y = hip_moe.causal_attention(heads(q), heads(k), vt=vt, scale=c.head_dim ** -0.5)
+            return hip_moe.proj(y, self._fragments("out"), c.dim, addend=addend), latent
         latent = self.kv_down(x)
         if c.uses_hip and _hip_inference(x):
             from . import hip_moe
@@ -406,11 +479,13 @@ class GlobalMLA(nn.Module):
                     b, c.n_heads, c.head_dim, -1)
                 y = hip_moe.causal_attention(heads(self.q(x)), heads(self.k_up(latent)), vt=vt,
                                              scale=c.head_dim ** -0.5)
-                return self.out(y), latent
+                result = self.out(y)
+                return (result if addend is None else addend + result), latent
         y = F.scaled_dot_product_attention(
             heads(self.q(x)), heads(self.k_up(latent)), heads(self.v_up(latent)),
             is_causal=True)
-        return self.out(y.transpose(1, 2).reshape(b, t, -1)), latent
+        result = self.out(y.transpose(1, 2).reshape(b, t, -1))
+        return (result if addend is None else addend + result), latent
 
     def _absorbed(self) -> tuple[Tensor, Tensor]:
         """(W_q absorbed with k_up [H*L, dim], v_up absorbed with out [dim, H*L])."""
@@ -649,6 +724,12 @@ class Parrot(nn.Module):
             return norm(x)
         return self.depth_mix[index].normalized(stream.sources(), norm)
 
+    @staticmethod
+    def _fuse_attention_addend(block: Block, h: Tensor, stream: _AttnRes | None) -> bool:
+        """Fold ``partial + delta`` into the attention output projection (HIP only)."""
+        return stream is not None and stream.partial is not None and \
+            block.attention.fuses_addend(h)
+
     def _fuse_moe_addend(self, block: Block, h: Tensor, stream: _AttnRes | None) -> bool:
         """Fold ``partial + delta`` into the MoE combine kernel (HIP only)."""
         return (stream is not None and stream.partial is not None and
@@ -685,12 +766,15 @@ class Parrot(nn.Module):
         index = 0
         for block in self.blocks:
             h = self._mixed_input(stream, x, index, block.attention_norm)
-            delta = (checkpoint(block.attention, h, use_reentrant=False) if remat
-                     else block.attention(h))
-            if stream is None:
-                x = x + delta
+            if not remat and self._fuse_attention_addend(block, h, stream):
+                stream.close(block.attention(h, addend=stream.partial))
             else:
-                stream.push(delta)
+                delta = (checkpoint(block.attention, h, use_reentrant=False) if remat
+                         else block.attention(h))
+                if stream is None:
+                    x = x + delta
+                else:
+                    stream.push(delta)
             index += 1
 
             h = self._mixed_input(stream, x, index, block.moe_norm)
@@ -750,18 +834,22 @@ class Parrot(nn.Module):
         index = 0
         for block in self.blocks:
             h = self._mixed_input(stream, x, index, block.attention_norm)
+            fuse = self._fuse_attention_addend(block, h, stream)
+            addend = stream.partial if fuse else None
             if isinstance(block.attention, LocalGQA):
-                delta, key, value = block.attention.prefill(h)
+                delta, key, value = block.attention.prefill(h, addend)
                 shape = (b, cfg.n_kv_heads, cfg.max_seq_len, cfg.head_dim)
                 cache = LocalKVCache(key.new_empty(shape), value.new_empty(shape))
                 cache.key[:, :, :t].copy_(key)
                 cache.value[:, :, :t].copy_(value)
             else:
-                delta, latent = block.attention.prefill(h)
+                delta, latent = block.attention.prefill(h, addend)
                 cache = MLALatentCache(latent.new_empty((b, cfg.max_seq_len, cfg.kv_latent_dim)))
                 cache.latent[:, :t].copy_(latent)
             caches.append(cache)
-            if stream is None:
+            if fuse:
+                stream.close(delta)
+            elif stream is None:
                 x = x + delta
             else:
                 stream.push(delta)

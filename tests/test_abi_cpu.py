@@ -137,3 +137,28 @@ def test_argument_validation_without_gpu(lib):
                                                   fake, null) == -1
     assert lib.parrot_decode_attention_latent_f32(fake, fake, fake, fake, 2, 8, 128, 1 << 16,
                                                   0.1, fake, null) == -3
+    # dense projections: k % 64, k <= 2048, n % 16, strides and alignment
+    assert lib.parrot_proj_bf16(null, 4, 768, 768, fake, 768, null, 0, fake, 768, null) == -1
+    assert lib.parrot_proj_bf16(fake, 4, 96, 96, fake, 768, null, 0, fake, 768, null) == -3
+    assert lib.parrot_proj_bf16(fake, 4, 4096, 4096, fake, 768, null, 0, fake, 768, null) == -3
+    assert lib.parrot_proj_bf16(fake, 4, 768, 768, fake, 24, null, 0, fake, 24, null) == -3
+    assert lib.parrot_proj_bf16(fake, 4, 768, 700, fake, 768, null, 0, fake, 768, null) == -2
+    assert lib.parrot_proj_bf16(fake, 4, 768, 768, fake, 768, fake, 700, fake, 768, null) == -2
+    assert lib.parrot_proj_bf16(fake, 4, 768, 772, fake, 768, null, 0, fake, 768, null) == -5
+    assert lib.parrot_proj_bf16(fake + 8, 4, 768, 768, fake, 768, null, 0, fake, 768, null) == -5
+    # transposed: room for every key, 4-key rows, 8-byte aligned output
+    assert lib.parrot_proj_transposed_bf16(fake, 2, 40, 128, fake, 768, 32, fake, null) == -2
+    assert lib.parrot_proj_transposed_bf16(fake, 2, 40, 128, fake, 768, 42, fake, null) == -5
+    assert lib.parrot_proj_transposed_bf16(fake, 2, 40, 128, fake, 768, 64, fake + 2,
+                                           null) == -5
+    # fused q|k|v + RoPE: the RoPE shape rules, the projection shape rules
+    assert lib.parrot_proj_rope_qkv_bf16(fake, 1, 4, 768, fake, fake, fake, 126, null, 128, 8,
+                                         2, 96, 0, fake, fake, fake, null) == -2
+    assert lib.parrot_proj_rope_qkv_bf16(fake, 1, 40, 768, fake, fake, fake, 0, null, 128, 8,
+                                         2, 96, 32, fake, fake, fake, null) == -2
+    assert lib.parrot_proj_rope_qkv_bf16(fake, 1, 4, 768, fake, fake, fake, 0, null, 128, 8,
+                                         2, 98, 0, fake, fake, fake, null) == -3
+    assert lib.parrot_proj_rope_qkv_bf16(fake, 1, 4, 800, fake, fake, fake, 0, null, 128, 8,
+                                         2, 96, 0, fake, fake, fake, null) == -3
+    assert lib.parrot_proj_rope_qkv_bf16(fake, 1, 4, 768, fake, fake, fake, 0, null, 128, 8,
+                                         2, 96, 32, fake, fake, fake + 2, null) == -5
