@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 3
+#define PARROT_ABI_VERSION 4
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -182,7 +182,8 @@ int parrot_vocab_argmax_bf16(const void* hidden, int64_t rows, int32_t dim, cons
  * >= roundup(seq, 32)] by strides {batch, head, dim row} with unit stride
  * along the keys (entries past seq may hold anything).  Strides multiples of
  * 8, bases 16-byte aligned; out [batch, seq, heads, head_dim] contiguous.
- * head_dim in {64, 96, 128}.  Replaces scaled_dot_product_attention(...,
+ * head_dim in {64, 96, 128}; seq * k row stride and head_dim * vt row stride
+ * below 2^30 elements.  Replaces scaled_dot_product_attention(...,
  * is_causal=True) and the masked chunk loop of LocalGQA.prefill
  * (parrot/model.py:264-295) and the causal SDPA of GlobalMLA.prefill
  * (parrot/model.py:350-360). */
@@ -191,6 +192,24 @@ int parrot_causal_attention_bf16(const void* q, const void* k, const void* vt,
                                  const int64_t* vt_strides, int64_t batch, int32_t seq,
                                  int32_t heads, int32_t kv_heads, int32_t head_dim,
                                  int32_t window, float scale, void* out, void* stream);
+
+/* As parrot_causal_attention_bf16 with K and V given in MFMA fragment order,
+ * the layout parrot_proj_rope_qkv_frag_bf16 and parrot_proj_frag_bf16 write:
+ * per (batch, kv head), nblk = ceil(seq / 32) blocks of 32 keys, each block
+ * a sequence of 1 KB wavefront fragments of 64 lanes x 8 bf16, lane
+ * l = 16 g + c:
+ *   k_frag [batch, kv_heads, nblk, 2 (n), head_dim / 32 (s), 64, 8]: key
+ *     32 blk + 16 n + c, dims 32 s + 8 g .. 32 s + 8 g + 7;
+ *   v_frag [batch, kv_heads, nblk, head_dim / 16 (t), 64, 8]: dim 16 t + c,
+ *     keys 32 blk + 4 g .. + 3, then 32 blk + 16 + 4 g .. + 3.
+ * Keys past seq in the last block may hold anything.  Every fragment of a
+ * key block is then one contiguous 1 KB load (row-major K and V^T loads
+ * touch 16 rows per instruction, which bounds the strided entry point at
+ * prefill sizes).  Same results as parrot_causal_attention_bf16. */
+int parrot_causal_attention_frag_bf16(const void* q, const int64_t* q_strides, const void* k_frag,
+                                      const void* v_frag, int64_t batch, int32_t seq,
+                                      int32_t heads, int32_t kv_heads, int32_t head_dim,
+                                      int32_t window, float scale, void* out, void* stream);
 
 /* Dense projection y = x . W^T (bf16 in and out, fp32 accumulation) for the
  * attention layers' linear maps, with the weight pre-packed in MFMA fragment
@@ -232,6 +251,27 @@ int parrot_proj_rope_qkv_bf16(const void* x, int64_t batch, int32_t seq, int32_t
                               const int32_t* start_device, int32_t max_positions, int32_t heads,
                               int32_t kv_heads, int32_t head_dim, int32_t vt_keys, void* q,
                               void* k, void* v, void* stream);
+
+/* parrot_proj_rope_qkv_bf16 (vt_keys = 0) writing the attention operands in
+ * fragment order as well: q [batch, H, seq, head_dim]; k, v [batch, Hk, seq,
+ * head_dim] only when non-NULL (the KV cache of a prefill); k_frag, v_frag in
+ * the layout of parrot_causal_attention_frag_bf16.  head_dim in
+ * {64, 96, 128}. */
+int parrot_proj_rope_qkv_frag_bf16(const void* x, int64_t batch, int32_t seq, int32_t dim,
+                                   const void* w_packed, const float* cos_table,
+                                   const float* sin_table, int32_t start,
+                                   const int32_t* start_device, int32_t max_positions,
+                                   int32_t heads, int32_t kv_heads, int32_t head_dim, void* q,
+                                   void* k, void* v, void* k_frag, void* v_frag, void* stream);
+
+/* The projection x W^T of x [batch * seq, k] (as parrot_proj_bf16) stored as
+ * attention K (values = 0) or V (values = 1) in fragment order for
+ * n / head_dim heads (the layout of parrot_causal_attention_frag_bf16 with
+ * kv_heads = n / head_dim).  head_dim in {64, 96, 128}.  Replaces k_up /
+ * v_up of GlobalMLA.prefill (parrot/model.py:350-360). */
+int parrot_proj_frag_bf16(const void* x, int64_t batch, int32_t seq, int32_t k,
+                          const void* w_packed, int32_t n, int32_t head_dim, int32_t values,
+                          void* out, void* stream);
 
 /* Workspace bytes for the routing / grouping entry points. */
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts);

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (maps PyTorch's HIP runtime before the library)
 
 LIBRARY = Path(__file__).resolve().parent / "_lib" / "libparrot_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -39,6 +39,13 @@ SIGNATURES: dict[str, tuple] = {
     "parrot_vocab_argmax_workspace_bytes": (_sz, [_i64, _i32]),
     "parrot_causal_attention_bf16": (
         ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p]),
+    "parrot_causal_attention_frag_bf16": (
+        ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p]),
+    "parrot_proj_rope_qkv_frag_bf16": (
+        ctypes.c_int,
+        [_p, _i64, _i32, _i32, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,
+         _p]),
+    "parrot_proj_frag_bf16": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _i32, _i32, _i32, _p, _p]),
     "parrot_proj_bf16": (ctypes.c_int, [_p, _i64, _i32, _i64, _p, _i32, _p, _i64, _p, _i64, _p]),
     "parrot_proj_transposed_bf16": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _i32, _i32, _p, _p]),
     "parrot_proj_rope_qkv_bf16": (

@@ -16,6 +16,7 @@ from dataclasses import dataclass
 from typing import TYPE_CHECKING
 
 import torch
+import torch.nn.functional as F
 from torch import Tensor
 
 from . import _abi
@@ -515,6 +516,48 @@ def proj_rope_qkv(x: Tensor, packed: Tensor, cos: Tensor, sin: Tensor, heads: in
     return q, k, v
 
 
+def proj_rope_qkv_frag(x: Tensor, packed: Tensor, cos: Tensor, sin: Tensor, heads: int,
+                       kv_heads: int, head_dim: int, cache_kv: bool = True):
+    """``proj_rope_qkv`` writing K and V for ``causal_attention_frag``:
+    returns (q [b, H, t, d], k_frag, v_frag, k, v) with row-major k, v
+    [b, Hk, t, d] only when ``cache_kv`` (else None); k, v and the valid keys
+    of k_frag, v_frag equal ``proj_rope_qkv``'s bit for bit."""
+    _require(x, "HIP projection")
+    b, t, dim = x.shape
+    n = (heads + 2 * kv_heads) * head_dim
+    if packed.numel() != n * dim:
+        raise RuntimeError("packed q|k|v weight does not match the head layout")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise RuntimeError("RoPE tables must be fp32")
+    x = x.contiguous()
+    q = x.new_empty((b, heads, t, head_dim))
+    frag = b * kv_heads * key_blocks(t) * 32 * head_dim
+    kf = x.new_empty((b, kv_heads, frag // (b * kv_heads)))
+    vf = torch.empty_like(kf)
+    k = x.new_empty((b, kv_heads, t, head_dim)) if cache_kv else None
+    v = x.new_empty((b, kv_heads, t, head_dim)) if cache_kv else None
+    _abi.check(_abi.load().parrot_proj_rope_qkv_frag_bf16(
+        ptr(x), b, t, dim, ptr(packed), ptr(cos), ptr(sin), 0, None, cos.shape[0], heads,
+        kv_heads, head_dim, ptr(q), ptr(k), ptr(v), ptr(kf), ptr(vf), _stream(x.device)),
+        "parrot_proj_rope_qkv_frag_bf16")
+    return q, kf, vf, k, v
+
+
+def proj_frag(x: Tensor, packed: Tensor, n: int, head_dim: int, values: bool) -> Tensor:
+    """x [b, t, k] W^T stored as attention K (or V, ``values``) in fragment
+    order for n / head_dim heads: [b, n / head_dim, ceil(t / 32) * 32 * d]."""
+    _require(x, "HIP projection")
+    b, t, k = x.shape
+    if packed.numel() != n * k:
+        raise RuntimeError("packed projection weight does not match the input width")
+    x = x.contiguous()
+    out = x.new_empty((b, n // head_dim, key_blocks(t) * 32 * head_dim))
+    _abi.check(_abi.load().parrot_proj_frag_bf16(
+        ptr(x), b, t, k, ptr(packed), n, head_dim, int(values), ptr(out), _stream(x.device)),
+        "parrot_proj_frag_bf16")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Causal attention for prefill / forward (cf. parrot/model.py:264-295, 350-360)
 # ---------------------------------------------------------------------------
@@ -571,6 +614,51 @@ def causal_attention(q: Tensor, k: Tensor, v: Tensor | None = None, *, scale: fl
 # Decode-step attention over the generation caches (cf. parrot/model.py:239-262,
 # 399-432; parrot/kernels/moe_bf16.metal:1203-1518)
 # ---------------------------------------------------------------------------
+
+def key_blocks(t: int) -> int:
+    """Blocks of 32 keys in the fragment-order K / V of ``t`` positions."""
+    return (t + 31) // 32
+
+
+def pack_kv_fragments(k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
+    """Row-major K, V [b, Hk, t, d] -> the fragment order that
+    ``causal_attention_frag`` reads ([b, Hk, ceil(t / 32) * 32 * d] each):
+    per block of 32 keys, K fragments (n, s) with lane 16 g + c holding key
+    32 blk + 16 n + c, dims 32 s + 8 g .. + 7; V fragments t with lane
+    16 g + c holding dim 16 t + c, keys 32 blk + {4 g .. + 3, 16 + 4 g .. + 3}.
+    Padding keys are zero."""
+    b, hk, t, d = k.shape
+    nblk = key_blocks(t)
+    pad = nblk * 32 - t
+    kp = F.pad(k, (0, 0, 0, pad))
+    vp = F.pad(v, (0, 0, 0, pad))
+    kf = kp.reshape(b, hk, nblk, 2, 16, d // 32, 4, 8).permute(0, 1, 2, 3, 5, 6, 4, 7)
+    vf = vp.reshape(b, hk, nblk, 2, 4, 4, d // 16, 16).permute(0, 1, 2, 6, 4, 7, 3, 5)
+    return kf.contiguous().reshape(b, hk, -1), vf.contiguous().reshape(b, hk, -1)
+
+
+def causal_attention_frag(q: Tensor, k_frag: Tensor, v_frag: Tensor, *, kv_heads: int,
+                          scale: float, window: int | None = None) -> Tensor:
+    """``causal_attention`` with K and V in fragment order (``pack_kv_fragments``
+    or the fragment outputs of the projection kernels); q [b, H, t, d] with
+    any strides that are multiples of 8.  Returns [b, t, H * d] bf16."""
+    _require(q, "HIP causal attention")
+    b, heads, t, d = q.shape
+    if d not in ATTENTION_HEAD_DIMS:
+        raise RuntimeError(f"head_dim {d} is not supported (64, 96, 128)")
+    need = b * kv_heads * key_blocks(t) * 32 * d
+    if k_frag.numel() != need or v_frag.numel() != need:
+        raise RuntimeError("fragment-order K / V do not match the query shape")
+    if q.stride(-1) != 1 or any(st % 8 for st in q.stride()[:3]) or q.data_ptr() % 16:
+        q = q.contiguous()
+    out = q.new_empty((b, t, heads * d))
+    st = (ctypes.c_int64 * 3)(*q.stride()[:3])
+    _abi.check(_abi.load().parrot_causal_attention_frag_bf16(
+        ptr(q), ctypes.cast(st, ctypes.c_void_p), ptr(k_frag), ptr(v_frag), b, t, heads, kv_heads, d,
+        t if window is None else window, scale, ptr(out), _stream(q.device)),
+        "parrot_causal_attention_frag_bf16")
+    return out
+
 
 def _check_position(position: Tensor, device: torch.device) -> None:
     if position.dtype != torch.int32 or position.device != device or position.numel() != 1:

@@ -462,6 +462,11 @@ int parrot_causal_attention_bf16(const void* q, const void* k, const void* vt,
   const int64_t padded = (static_cast<int64_t>(seq) + 31) / 32 * 32;
   if (vt_strides[2] < padded || vt_strides[1] < head_dim * vt_strides[2])
     return PARROT_ERR_BAD_SHAPE;
+  // One kv head of K (seq rows) and of V^T (head_dim rows) is addressed with
+  // 32-bit byte offsets.
+  if (static_cast<int64_t>(seq) * k_strides[2] * 2 >= (int64_t{1} << 31) ||
+      static_cast<int64_t>(head_dim) * vt_strides[2] * 2 >= (int64_t{1} << 31))
+    return PARROT_ERR_UNSUPPORTED;
   for (int i = 0; i < 3; ++i)
     if (q_strides[i] % 8 || k_strides[i] % 8 || vt_strides[i] % 8 || q_strides[i] < 0 ||
         k_strides[i] < 0 || vt_strides[i] < 0)
@@ -470,6 +475,29 @@ int parrot_causal_attention_bf16(const void* q, const void* k, const void* vt,
   return status(parrot::launch_causal_attention(
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
       static_cast<const uint16_t*>(vt), q_strides, k_strides, vt_strides,
+      static_cast<int>(batch), seq, heads, kv_heads, head_dim, window, scale,
+      static_cast<uint16_t*>(out), as_stream(stream)));
+}
+
+int parrot_causal_attention_frag_bf16(const void* q, const int64_t* q_strides, const void* k_frag,
+                                      const void* v_frag, int64_t batch, int32_t seq,
+                                      int32_t heads, int32_t kv_heads, int32_t head_dim,
+                                      int32_t window, float scale, void* out, void* stream) {
+  if (!q || !q_strides || !k_frag || !v_frag || !out) return PARROT_ERR_NULL_POINTER;
+  if (batch < 0 || seq < 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 || window <= 0)
+    return PARROT_ERR_BAD_SHAPE;
+  if (heads % kv_heads || !parrot::attention_head_dim_supported(head_dim) ||
+      batch > 65535 || heads > 65535)
+    return PARROT_ERR_UNSUPPORTED;
+  // One kv head's fragments are addressed with 32-bit byte offsets.
+  const int64_t padded = (static_cast<int64_t>(seq) + 31) / 32 * 32;
+  if (padded * head_dim * 2 >= (int64_t{1} << 31)) return PARROT_ERR_UNSUPPORTED;
+  for (int i = 0; i < 3; ++i)
+    if (q_strides[i] % 8 || q_strides[i] < 0) return PARROT_ERR_ALIGNMENT;
+  if (!aligned16(q) || !aligned16(k_frag) || !aligned16(v_frag)) return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_causal_attention(
+      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_frag),
+      static_cast<const uint16_t*>(v_frag), q_strides, nullptr, nullptr,
       static_cast<int>(batch), seq, heads, kv_heads, head_dim, window, scale,
       static_cast<uint16_t*>(out), as_stream(stream)));
 }
@@ -532,7 +560,53 @@ int parrot_proj_rope_qkv_bf16(const void* x, int64_t batch, int32_t seq, int32_t
       static_cast<const uint16_t*>(x), static_cast<int>(batch * seq), seq, dim,
       static_cast<const uint16_t*>(w_packed), cos_table, sin_table, start, start_device,
       max_positions, heads, kv_heads, head_dim, vt_keys, static_cast<uint16_t*>(q),
-      static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), as_stream(stream)));
+      static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), nullptr, nullptr, as_stream(stream)));
+}
+
+int parrot_proj_rope_qkv_frag_bf16(const void* x, int64_t batch, int32_t seq, int32_t dim,
+                                   const void* w_packed, const float* cos_table,
+                                   const float* sin_table, int32_t start,
+                                   const int32_t* start_device, int32_t max_positions,
+                                   int32_t heads, int32_t kv_heads, int32_t head_dim, void* q,
+                                   void* k, void* v, void* k_frag, void* v_frag, void* stream) {
+  if (!x || !w_packed || !cos_table || !sin_table || !q || !k_frag || !v_frag)
+    return PARROT_ERR_NULL_POINTER;
+  if (batch < 0 || seq < 0 || start < 0 || dim <= 0 || heads <= 0 || kv_heads <= 0 ||
+      head_dim <= 0 || max_positions <= 0 || static_cast<int64_t>(start) + seq > max_positions)
+    return PARROT_ERR_BAD_SHAPE;
+  if (heads % kv_heads || !parrot::attention_head_dim_supported(head_dim))
+    return PARROT_ERR_UNSUPPORTED;
+  const int64_t n = static_cast<int64_t>(heads + 2 * kv_heads) * head_dim;
+  if (n > INT32_MAX || !parrot::proj_shape_supported(dim, static_cast<int>(n)) ||
+      batch * seq > INT32_MAX)
+    return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w_packed) || !aligned16(k_frag) || !aligned16(v_frag))
+    return PARROT_ERR_ALIGNMENT;
+  if (batch == 0 || seq == 0) return PARROT_OK;
+  return status(parrot::launch_proj_rope_qkv(
+      static_cast<const uint16_t*>(x), static_cast<int>(batch * seq), seq, dim,
+      static_cast<const uint16_t*>(w_packed), cos_table, sin_table, start, start_device,
+      max_positions, heads, kv_heads, head_dim, 0, static_cast<uint16_t*>(q),
+      static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), static_cast<uint16_t*>(k_frag),
+      static_cast<uint16_t*>(v_frag), as_stream(stream)));
+}
+
+int parrot_proj_frag_bf16(const void* x, int64_t batch, int32_t seq, int32_t k,
+                          const void* w_packed, int32_t n, int32_t head_dim, int32_t values,
+                          void* out, void* stream) {
+  if (!x || !w_packed || !out) return PARROT_ERR_NULL_POINTER;
+  if (batch < 0 || seq < 0 || k <= 0 || n <= 0 || head_dim <= 0 || n % head_dim ||
+      (values != 0 && values != 1))
+    return PARROT_ERR_BAD_SHAPE;
+  if (!parrot::proj_shape_supported(k, n) || !parrot::attention_head_dim_supported(head_dim) ||
+      batch * seq > INT32_MAX)
+    return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w_packed) || !aligned16(out)) return PARROT_ERR_ALIGNMENT;
+  if (batch == 0 || seq == 0) return PARROT_OK;
+  return status(parrot::launch_proj_frag(
+      static_cast<const uint16_t*>(x), static_cast<int>(batch * seq), seq, k,
+      static_cast<const uint16_t*>(w_packed), n, head_dim, values != 0,
+      static_cast<uint16_t*>(out), as_stream(stream)));
 }
 
 int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,

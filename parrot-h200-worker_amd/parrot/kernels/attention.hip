@@ -43,8 +43,8 @@ constexpr int kAttnWaves = 8;  // wavefronts per workgroup, splitting the key bl
 
 struct AttnArgs {
   const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* vt;
+  const uint16_t* k;            // FRAG: K in fragment order (kfrag_index)
+  const uint16_t* vt;           // FRAG: V in fragment order (vfrag_index)
   int64_t qs[3], ks[3], vs[3];  // element strides: batch, head, row (vt: dim row)
   int seq, heads, kv_heads, window;
   float scale_log2;             // scale * log2(e)
@@ -66,16 +66,21 @@ __device__ __forceinline__ float query_sum(float v) {
   return v + __shfl_xor(v, 32);
 }
 
-template <int D>
+// FRAG: K and V in fragment order [batch, kv heads, ceil(seq / 32), ...]:
+// every fragment of a key block is one 1 KB contiguous wavefront load (a
+// row-major K or V^T load touches 16 rows per instruction, and at prefill
+// sizes the per-CU memory pipeline, not the MFMAs, then sets the time).
+template <int D, bool FRAG>
 __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnArgs a) {
   constexpr int KS = D / 32;   // k steps of the score product
   constexpr int NT = D / 16;   // output dim tiles
   __shared__ float m_s[kAttnWaves][kAttnRows];
   __shared__ float l_s[kAttnWaves][kAttnRows];
+  __shared__ float f_s[kAttnWaves][kAttnRows];
   __shared__ float o_s[kAttnWaves][D][kAttnRows + 1];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4;
   const int c = lane & 15;       // this lane's query (column of S^T and O^T)
   const int q0 = blockIdx.x * kAttnRows;
@@ -85,9 +90,23 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
   const int W = a.window;
   const int kvh = h / (a.heads / a.kv_heads);
   const uint16_t* qb = a.q + b * a.qs[0] + h * a.qs[1];
-  const uint16_t* kb = a.k + b * a.ks[0] + kvh * a.ks[1];
-  const uint16_t* vb = a.vt + b * a.vs[0] + kvh * a.vs[1];
   const int query = q0 + c;
+
+  // K and V^T of this kv head through buffer resources: the per-lane byte
+  // offset is fixed, the block's key offset is uniform (an SGPR), and K rows
+  // past the sequence read as zero.
+  const int ks2 = static_cast<int>(a.ks[2]), vs2 = static_cast<int>(a.vs[2]);
+  const int nblk = (T + kAttnKeys - 1) / kAttnKeys;
+  const int64_t bh = static_cast<int64_t>(b) * a.kv_heads + kvh;
+  const __amdgpu_buffer_rsrc_t k_rsrc =
+      FRAG ? make_rsrc(a.k + bh * nblk * (kAttnKeys * D), static_cast<uint32_t>(nblk) * kAttnKeys * D * 2)
+           : make_rsrc(a.k + b * a.ks[0] + kvh * a.ks[1], static_cast<uint32_t>(T) * ks2 * 2);
+  const __amdgpu_buffer_rsrc_t v_rsrc =
+      FRAG ? make_rsrc(a.vt + bh * nblk * (kAttnKeys * D), static_cast<uint32_t>(nblk) * kAttnKeys * D * 2)
+           : make_rsrc(a.vt + b * a.vs[0] + kvh * a.vs[1], static_cast<uint32_t>(D) * vs2 * 2);
+  const uint32_t k_off0 = FRAG ? lane * 16 : static_cast<uint32_t>(c * ks2 + 8 * g) * 2;
+  const uint32_t k_off1 = FRAG ? k_off0 + KS * 1024 : k_off0 + static_cast<uint32_t>(16 * ks2) * 2;
+  const uint32_t v_off = FRAG ? lane * 16 : static_cast<uint32_t>(c * vs2 + 4 * g) * 2;
 
   // Q^T as the B operand: lane holds query q0 + c, dims 32 s + 8 g .. +8.
   bf16x8 qf[KS];
@@ -112,42 +131,45 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
 
   // One block's operands: K rows k0 + 16 n + c (A operand), V^T rows
   // 16 t + c at keys k0 + 4 g and k0 + 16 + 4 g (4 keys each).
-  bf16x8 kf[2][KS];
-  uint2 vf[NT][2];
-  auto load_block = [&](int k0) {
+  struct Block {
+    bf16x8 k[2][KS];
+    uint2 v[NT][2];
+  };
+  auto load_block = [&](Block& x, int k0) {
+    if constexpr (FRAG) {
+      // block k0 / 32: K fragments (n, s) at (n KS + s) KB, V fragments t at t KB
+      const uint32_t blk = static_cast<uint32_t>(k0 / kAttnKeys) * (kAttnKeys * D * 2);
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const uint16_t* row = kb + static_cast<int64_t>(min(k0 + 16 * n + c, T - 1)) * a.ks[2] + 8 * g;
+      for (int s = 0; s < KS; ++s) {
+        x.k[0][s] = __builtin_bit_cast(bf16x8, buffer_load16(k_rsrc, k_off0 + 1024 * s, blk));
+        x.k[1][s] = __builtin_bit_cast(bf16x8, buffer_load16(k_rsrc, k_off1 + 1024 * s, blk));
+      }
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kf[n][s] = load8(row + 32 * s);
+      for (int t = 0; t < NT; ++t) {
+        const uint4 v = buffer_load16(v_rsrc, v_off + 1024 * t, blk);
+        x.v[t][0] = make_uint2(v.x, v.y);
+        x.v[t][1] = make_uint2(v.z, v.w);
+      }
+      return;
     }
+    const uint32_t ko = static_cast<uint32_t>(k0) * ks2 * 2;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      x.k[0][s] = __builtin_bit_cast(bf16x8, buffer_load16(k_rsrc, k_off0 + 64 * s, ko));
+      x.k[1][s] = __builtin_bit_cast(bf16x8, buffer_load16(k_rsrc, k_off1 + 64 * s, ko));
+    }
+    // V^T rows hold at least roundup(T, 32) keys, so every block is in
+    // range; keys past T are zeroed in `step`.
+    const uint32_t vo = static_cast<uint32_t>(k0) * 2;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      // V^T rows hold at least roundup(T, 32) keys, so every block is in
-      // bounds; keys past T are zeroed below.
-      const uint16_t* row = vb + static_cast<int64_t>(16 * t + c) * a.vs[2] + k0 + 4 * g;
-      vf[t][0] = *reinterpret_cast<const uint2*>(row);
-      vf[t][1] = *reinterpret_cast<const uint2*>(row + 16);
+      const uint32_t off = v_off + static_cast<uint32_t>(16 * t * vs2) * 2;
+      x.v[t][0] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(v_rsrc, off, vo, 0));
+      x.v[t][1] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(v_rsrc, off + 32, vo, 0));
     }
   };
 
-  int k0 = k_first + kAttnKeys * wave;
-  if (k0 <= q_last) load_block(k0);
-  for (; k0 <= q_last; k0 += kAttnWaves * kAttnKeys) {
-    bf16x8 kc[2][KS];
-    uint2 vc[NT][2];
-#pragma unroll
-    for (int n = 0; n < 2; ++n)
-#pragma unroll
-      for (int s = 0; s < KS; ++s) kc[n][s] = kf[n][s];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      vc[t][0] = vf[t][0];
-      vc[t][1] = vf[t][1];
-    }
-    const int k_next = k0 + kAttnWaves * kAttnKeys;
-    if (k_next <= q_last) load_block(k_next);
-
+  auto step = [&](const Block& x, int k0) {
     // Scores S^T: lane holds query c, keys k0 + 16 n + 4 g + r, in log2
     // units.  A block every query of the workgroup sees whole (below the
     // diagonal, inside the window, inside the sequence) needs no mask.
@@ -157,35 +179,49 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
       sc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s)
-        sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc[n][s], qf[s], sc[n], 0, 0, 0);
+        sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.k[n][s], qf[s], sc[n], 0, 0, 0);
     }
     const bool whole = k0 + kAttnKeys - 1 <= q0 && k0 > q_last - W && k0 + kAttnKeys <= T;
     float p[2][4];
     float mx = -INFINITY;
+    if (whole) {
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
+      for (int n = 0; n < 2; ++n)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 16 * n + 4 * g + r;
-        const bool ok = whole || (key <= query && key > query - W && key < T);
-        p[n][r] = ok ? sc[n][r] * a.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, p[n][r]);
-      }
+        for (int r = 0; r < 4; ++r) {
+          p[n][r] = sc[n][r] * a.scale_log2;
+          mx = fmaxf(mx, p[n][r]);
+        }
+    } else {
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + 16 * n + 4 * g + r;
+          const bool ok = key <= query && key > query - W && key < T;
+          p[n][r] = ok ? sc[n][r] * a.scale_log2 : -INFINITY;
+          mx = fmaxf(mx, p[n][r]);
+        }
+    }
     // Raise the shared max only when some lane of the wavefront needs it.
     if (__ballot(mx > m + kLazy) != 0) {
       const float mn = fmaxf(m, query_max(mx));
-      const float alpha = m == -INFINITY ? 0.0f : exp2f(m - mn);
+      const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
       l *= alpha;
 #pragma unroll
       for (int t = 0; t < NT; ++t) o[t] = o[t] * alpha;
       m = mn;
     }
+    // exp2(-inf - m) is 0 for a masked key (m is finite once a key is seen,
+    // and a lane whose query has seen none keeps p == -inf, m == -inf: its
+    // probabilities are forced to 0 below).
+    const bool live = m != -INFINITY;
     bf16x8 pf;
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float e = p[n][r] == -INFINITY ? 0.0f : exp2f(p[n][r] - m);
+        const float e = live ? __builtin_amdgcn_exp2f(p[n][r] - m) : 0.0f;
         l += e;
         pf[4 * n + r] = static_cast<__bf16>(e);
       }
@@ -194,7 +230,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
     const bool in_seq = k0 + kAttnKeys <= T;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      uint2 lo = vc[t][0], hi = vc[t][1];
+      uint2 lo = x.v[t][0], hi = x.v[t][1];
       if (!in_seq) {
         const int ka = k0 + 4 * g, kb2 = k0 + 16 + 4 * g;
         lo.x = (ka + 1 < T ? 0xffffffffu : ka < T ? 0x0000ffffu : 0u) & lo.x;
@@ -205,10 +241,29 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
       const bf16x8 vfrag = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
       o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfrag, pf, o[t], 0, 0, 0);
     }
+  };
+
+  // Key blocks k0, k0 + 8 x 32, ... of this wavefront, two register sets in
+  // ping-pong: the next block's loads are in flight during each step.
+  constexpr int kStride = kAttnWaves * kAttnKeys;
+  Block x0, x1;
+  int k0 = k_first + kAttnKeys * wave;
+  if (k0 <= q_last) load_block(x0, k0);
+  while (k0 <= q_last) {
+    const int k1 = k0 + kStride;
+    if (k1 <= q_last) load_block(x1, k1);
+    step(x0, k0);
+    if (k1 > q_last) break;
+    const int k2 = k1 + kStride;
+    if (k2 <= q_last) load_block(x0, k2);
+    step(x1, k1);
+    k0 = k2;
   }
   l = query_sum(l);
 
-  // Merge the wavefronts' states in wavefront order.
+  // Merge the wavefronts' states in wavefront order: one scale factor
+  // exp2(m_w - max_w m_w) / sum_w (l_w ...) per (wavefront, query), then
+  // each output element is a D-independent weighted sum over wavefronts.
   if (g == 0) {
     m_s[wave][c] = m;
     l_s[wave][c] = l;
@@ -218,21 +273,31 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
 #pragma unroll
     for (int r = 0; r < 4; ++r) o_s[wave][16 * t + 4 * g + r][c] = o[t][r];
   __syncthreads();
+  if (threadIdx.x < kAttnRows) {
+    const int qq = threadIdx.x;
+    float mt = m_s[0][qq];
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; ++w) mt = fmaxf(mt, m_s[w][qq]);
+    float f[kAttnWaves];
+    float lt = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      f[w] = m_s[w][qq] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_s[w][qq] - mt);
+      lt += l_s[w][qq] * f[w];
+    }
+    const float inv = 1.0f / lt;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) f_s[w][qq] = f[w] * inv;
+  }
+  __syncthreads();
   for (int i = threadIdx.x; i < kAttnRows * D; i += 64 * kAttnWaves) {
     const int qq = i / D, d = i - qq * D;
     const int row = q0 + qq;
     if (row >= T) continue;
-    float mt = m_s[0][qq];
+    float ot = 0.0f;
 #pragma unroll
-    for (int w = 1; w < kAttnWaves; ++w) mt = fmaxf(mt, m_s[w][qq]);
-    float lt = 0.0f, ot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
-      const float f = m_s[w][qq] == -INFINITY ? 0.0f : exp2f(m_s[w][qq] - mt);
-      lt += l_s[w][qq] * f;
-      ot += o_s[w][d][qq] * f;
-    }
-    a.out[((static_cast<int64_t>(b) * T + row) * a.heads + h) * D + d] = f32_to_bf16(ot / lt);
+    for (int w = 0; w < kAttnWaves; ++w) ot += o_s[w][d][qq] * f_s[w][qq];
+    a.out[((static_cast<int64_t>(b) * T + row) * a.heads + h) * D + d] = f32_to_bf16(ot);
   }
 }
 
@@ -252,10 +317,11 @@ hipError_t launch_causal_attention(const uint16_t* q, const uint16_t* k, const u
   a.q = q;
   a.k = k;
   a.vt = vt;
+  const bool frag = k_strides == nullptr;  // fragment-order K and V
   for (int i = 0; i < 3; ++i) {
     a.qs[i] = q_strides[i];
-    a.ks[i] = k_strides[i];
-    a.vs[i] = vt_strides[i];
+    a.ks[i] = frag ? 0 : k_strides[i];
+    a.vs[i] = frag ? 0 : vt_strides[i];
   }
   a.seq = seq;
   a.heads = heads;
@@ -264,12 +330,16 @@ hipError_t launch_causal_attention(const uint16_t* q, const uint16_t* k, const u
   a.scale_log2 = scale * 1.4426950408889634f;
   a.out = out;
   const dim3 grid((seq + kAttnRows - 1) / kAttnRows, heads, batch);
+#define PARROT_ATTN(D)                                                                 \
+  (frag ? causal_attention_kernel<D, true><<<grid, 64 * kAttnWaves, 0, s>>>(a)         \
+        : causal_attention_kernel<D, false><<<grid, 64 * kAttnWaves, 0, s>>>(a))
   switch (head_dim) {
-    case 64: causal_attention_kernel<64><<<grid, 64 * kAttnWaves, 0, s>>>(a); break;
-    case 96: causal_attention_kernel<96><<<grid, 64 * kAttnWaves, 0, s>>>(a); break;
-    case 128: causal_attention_kernel<128><<<grid, 64 * kAttnWaves, 0, s>>>(a); break;
+    case 64: PARROT_ATTN(64); break;
+    case 96: PARROT_ATTN(96); break;
+    case 128: PARROT_ATTN(128); break;
     default: return hipErrorInvalidValue;
   }
+#undef PARROT_ATTN
   return hipGetLastError();
 }
 

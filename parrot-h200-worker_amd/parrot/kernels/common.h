@@ -67,6 +67,26 @@ __device__ __forceinline__ float rope_odd(float e, float o, float c, float s) {
   return __builtin_fmaf(e, s, o * c);
 }
 
+// Attention K and V in MFMA fragment order, per (batch, kv head), in blocks
+// of 32 keys, so that every fragment of a key block is one 1 KB contiguous
+// wavefront load:
+//   K: [blocks][n = 2][s = d / 32][lane = 16 g + c][8]: key 32 blk + 16 n + c,
+//      dims 32 s + 8 g .. + 7 (the A operand of S^T = K Q^T);
+//   V: [blocks][t = d / 16][lane = 16 g + c][8]: dim 16 t + c, keys
+//      32 blk + {4 g .. 4 g + 3, 16 + 4 g .. 16 + 4 g + 3} (the A operand of
+//      O^T += V^T P^T with P^T's k order).
+// bh = batch * kv_heads + kv head; nblk = ceil(seq / 32); element indices.
+__device__ __forceinline__ int64_t kfrag_index(int64_t bh, int nblk, int key, int w, int ks) {
+  const int blk = key >> 5, n = (key >> 4) & 1, c = key & 15;
+  const int s = w >> 5, g = (w >> 3) & 3, e = w & 7;
+  return ((((bh * nblk + blk) * 2 + n) * ks + s) * 64 + 16 * g + c) * 8 + e;
+}
+__device__ __forceinline__ int64_t vfrag_index(int64_t bh, int nblk, int key, int w, int nt) {
+  const int blk = key >> 5, half = (key >> 4) & 1, g = (key >> 2) & 3, j = key & 3;
+  const int t = w >> 4, c = w & 15;
+  return (((bh * nblk + blk) * nt + t) * 64 + 16 * g + c) * 8 + 4 * half + j;
+}
+
 // DPP lane exchange inside rows of 16 lanes (VALU latency, no LDS trip).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
@@ -291,6 +311,8 @@ hipError_t launch_vocab_argmax(const uint16_t* h, int rows, int dim, const uint1
 // keys, rows of at least roundup(seq, 32) keys); out [batch, seq, heads,
 // head_dim].
 bool attention_head_dim_supported(int head_dim);  // 64, 96, 128
+// k_strides == vt_strides == nullptr: k and vt are K and V in fragment order
+// (kfrag_index / vfrag_index).
 hipError_t launch_causal_attention(const uint16_t* q, const uint16_t* k, const uint16_t* vt,
                                    const int64_t* q_strides, const int64_t* k_strides,
                                    const int64_t* vt_strides, int batch, int seq, int heads,
@@ -312,6 +334,9 @@ hipError_t launch_proj_rope_qkv(const uint16_t* x, int rows, int seq, int dim, c
                                 const float* cos_t, const float* sin_t, int start,
                                 const int32_t* start_device, int max_positions, int heads,
                                 int kv_heads, int head_dim, int vt_keys, uint16_t* q,
-                                uint16_t* k, uint16_t* v, hipStream_t s);
+                                uint16_t* k, uint16_t* v, uint16_t* kf, uint16_t* vf,
+                                hipStream_t s);
+hipError_t launch_proj_frag(const uint16_t* x, int rows, int seq, int k, const uint16_t* w,
+                            int n, int head_dim, bool values, uint16_t* out, hipStream_t s);
 
 }  // namespace parrot

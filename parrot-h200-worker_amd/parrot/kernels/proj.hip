@@ -36,8 +36,12 @@
 //             layout the attention kernel reads (MLA values);
 //   kRopeQkv  columns [0, H d) -> q [b, H, seq, d], [H d, (H + Hk) d) ->
 //             k [b, Hk, seq, d], both rotated; the rest -> v, [b, Hk, seq, d]
-//             or transposed [b, Hk, d, vt_keys].  Rotation partners (2i,
-//             2i + 1) sit in adjacent lanes: one DPP quad_perm swap.
+//             or transposed [b, Hk, d, vt_keys]; and/or k and v in the
+//             attention kernel's fragment order (kfrag_index, vfrag_index).
+//             Rotation partners (2i, 2i + 1) sit in adjacent lanes: one DPP
+//             quad_perm swap.
+//   kFrag     the output as attention K or V in fragment order, columns
+//             grouped into heads of head_dim (the MLA up-projections).
 #include "common.h"
 
 namespace parrot {
@@ -48,7 +52,7 @@ constexpr int kProjRows = 16;        // rows per workgroup
 constexpr int kProjCols = 64;        // columns per workgroup: 4 wavefronts x 16
 constexpr int kProjMaxK = 2048;      // A tile at most 64 KB of LDS
 
-enum ProjEpilogue { kStore = 0, kStoreT = 1, kRopeQkv = 2 };
+enum ProjEpilogue { kStore = 0, kStoreT = 1, kRopeQkv = 2, kFrag = 3 };
 
 struct ProjArgs {
   const uint16_t* x;
@@ -69,8 +73,12 @@ struct ProjArgs {
   const int32_t* start_device;
   int heads, kv_heads, head_dim;
   uint16_t* q;
-  uint16_t* k;
-  uint16_t* v;
+  uint16_t* k;              // optional with kRopeQkv
+  uint16_t* v;              // optional with kRopeQkv
+  // fragment-order attention operands (kRopeQkv: optional; kFrag: one of them)
+  uint16_t* kf;
+  uint16_t* vf;
+  int nblk;                 // ceil(seq / 32)
 };
 
 __device__ __forceinline__ float swap_pair(float v) {  // lanes 2i <-> 2i + 1
@@ -87,6 +95,49 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint16_t* p) {
   bf16x8 v;
   asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
   return v;
+}
+
+// Stores one lane's 4 values (rows row0 .. row0 + 3, one column w of kv
+// head kvh of kv_heads) as attention values: row-major p.v [b, kv_heads,
+// seq, d] or transposed [b, kv_heads, d, ld_keys] when p.v is set, and in
+// fragment order when p.vf is set.  When seq % 4 == 0 the 4 rows are
+// consecutive positions of one sequence and the transposed and fragment
+// stores take them in one 8-byte store.
+__device__ __forceinline__ void store_values(const ProjArgs& p, const uint16_t (&bits)[4],
+                                             int row0, int kvh, int kv_heads, int w) {
+  const int d = p.head_dim;
+  if ((p.seq & 3) == 0) {
+    const int b = row0 / p.seq;
+    const int t0 = row0 - b * p.seq;
+    const int64_t bh = static_cast<int64_t>(b) * kv_heads + kvh;
+    uint2 u;
+    u.x = static_cast<uint32_t>(bits[0]) | (static_cast<uint32_t>(bits[1]) << 16);
+    u.y = static_cast<uint32_t>(bits[2]) | (static_cast<uint32_t>(bits[3]) << 16);
+    if (p.v != nullptr) {
+      if (p.ld_keys > 0) {
+        *reinterpret_cast<uint2*>(p.v + (bh * d + w) * p.ld_keys + t0) = u;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p.v[(bh * p.seq + t0 + r) * d + w] = bits[r];
+      }
+    }
+    if (p.vf != nullptr)
+      *reinterpret_cast<uint2*>(p.vf + vfrag_index(bh, p.nblk, t0, w, d / 16)) = u;
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = row0 + r;
+    if (row >= p.rows) break;
+    const int b = row / p.seq;
+    const int tp = row - b * p.seq;
+    const int64_t bh = static_cast<int64_t>(b) * kv_heads + kvh;
+    if (p.v != nullptr) {
+      if (p.ld_keys > 0) p.v[(bh * d + w) * p.ld_keys + tp] = bits[r];
+      else p.v[(bh * p.seq + tp) * d + w] = bits[r];
+    }
+    if (p.vf != nullptr) p.vf[vfrag_index(bh, p.nblk, tp, w, d / 16)] = bits[r];
+  }
 }
 
 // KST > 0: K == 32 KST and PF == KST (every k step loaded up front);
@@ -222,6 +273,34 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
     return;
   }
 
+  if (EPI == kFrag) {
+    const int d = p.head_dim;
+    const int head = col / d;
+    const int w = col - head * d;
+    const int heads = p.N / d;
+#pragma unroll
+    for (int mi = 0; mi < kTilesM; ++mi) {
+      const int row0 = m0 + mi * 16 + 4 * (lane >> 4);
+      if (row0 >= p.rows) continue;
+      uint16_t bits[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bits[r] = f32_to_bf16(acc[mi][r]);
+      if (p.kf != nullptr) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = row0 + r;
+          if (row >= p.rows) break;
+          const int b = row / p.seq;
+          p.kf[kfrag_index(static_cast<int64_t>(b) * heads + head, p.nblk, row - b * p.seq, w,
+                           d / 32)] = bits[r];
+        }
+      } else {
+        store_values(p, bits, row0, head, heads, w);
+      }
+    }
+    return;
+  }
+
   // kRopeQkv
   const int d = p.head_dim;
   const int head = col / d;  // per lane; a rotation pair never straddles heads (d even)
@@ -250,32 +329,33 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
       }
     }
     const int row0 = m0 + mi * 16 + 4 * (lane >> 4);
-    if (head < H + Hk || p.ld_keys == 0 || (p.seq & 3) != 0) {
+    if (row0 >= p.rows) continue;
+    uint16_t bits[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bits[r] = f32_to_bf16(val[r]);
+    if (head < H) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = row0 + r;
         if (row >= p.rows) break;
         const int b = row / p.seq;
         const int tp = row - b * p.seq;
-        const uint16_t bits = f32_to_bf16(val[r]);
-        if (head < H) {
-          p.q[((static_cast<int64_t>(b) * H + head) * p.seq + tp) * d + w] = bits;
-        } else if (head < H + Hk) {
-          p.k[((static_cast<int64_t>(b) * Hk + head - H) * p.seq + tp) * d + w] = bits;
-        } else if (p.ld_keys == 0) {
-          p.v[((static_cast<int64_t>(b) * Hk + head - H - Hk) * p.seq + tp) * d + w] = bits;
-        } else {
-          p.v[((static_cast<int64_t>(b) * Hk + head - H - Hk) * d + w) * p.ld_keys + tp] = bits;
-        }
+        p.q[((static_cast<int64_t>(b) * H + head) * p.seq + tp) * d + w] = bits[r];
       }
-    } else if (row0 < p.rows) {  // transposed values, 4 consecutive keys
-      const int b = row0 / p.seq;
-      const int t0 = row0 - b * p.seq;
-      uint2 u;
-      u.x = pack_bf16x2(val[0], val[1]);
-      u.y = pack_bf16x2(val[2], val[3]);
-      *reinterpret_cast<uint2*>(
-          p.v + ((static_cast<int64_t>(b) * Hk + head - H - Hk) * d + w) * p.ld_keys + t0) = u;
+    } else if (head < H + Hk) {
+      const int kvh = head - H;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = row0 + r;
+        if (row >= p.rows) break;
+        const int b = row / p.seq;
+        const int tp = row - b * p.seq;
+        if (p.k != nullptr) p.k[((static_cast<int64_t>(b) * Hk + kvh) * p.seq + tp) * d + w] = bits[r];
+        if (p.kf != nullptr)
+          p.kf[kfrag_index(static_cast<int64_t>(b) * Hk + kvh, p.nblk, tp, w, d / 32)] = bits[r];
+      }
+    } else {
+      store_values(p, bits, row0, head - H - Hk, Hk, w);
     }
   }
 }
@@ -334,8 +414,10 @@ hipError_t launch_proj_rope_qkv(const uint16_t* x, int rows, int seq, int dim, c
                                 const float* cos_t, const float* sin_t, int start,
                                 const int32_t* start_device, int max_positions, int heads,
                                 int kv_heads, int head_dim, int vt_keys, uint16_t* q,
-                                uint16_t* k, uint16_t* v, hipStream_t s) {
+                                uint16_t* k, uint16_t* v, uint16_t* kf, uint16_t* vf,
+                                hipStream_t s) {
   ProjArgs a{};
+  a.kf = kf; a.vf = vf; a.nblk = (seq + 31) / 32;
   a.x = x; a.lda = dim; a.rows = rows; a.K = dim; a.N = (heads + 2 * kv_heads) * head_dim;
   a.w = w; a.seq = seq; a.ld_keys = vt_keys;
   a.cos_t = cos_t; a.sin_t = sin_t; a.start = start; a.start_device = start_device;
@@ -343,6 +425,15 @@ hipError_t launch_proj_rope_qkv(const uint16_t* x, int rows, int seq, int dim, c
   a.heads = heads; a.kv_heads = kv_heads; a.head_dim = head_dim;
   a.q = q; a.k = k; a.v = v;
   return launch_proj<kRopeQkv>(a, s);
+}
+
+hipError_t launch_proj_frag(const uint16_t* x, int rows, int seq, int k, const uint16_t* w,
+                            int n, int head_dim, bool values, uint16_t* out, hipStream_t s) {
+  ProjArgs a{};
+  a.x = x; a.lda = k; a.rows = rows; a.K = k; a.N = n; a.w = w;
+  a.seq = seq; a.head_dim = head_dim; a.nblk = (seq + 31) / 32;
+  (values ? a.vf : a.kf) = out;
+  return launch_proj<kFrag>(a, s);
 }
 
 }  // namespace parrot

@@ -304,8 +304,11 @@ class LocalGQA(nn.Module):
         from . import hip_moe
         return hip_moe.pack_linear(self, "qkv", (self.q.weight, self.k.weight, self.v.weight))
 
-    def prefill(self, x: Tensor, addend: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
-        """(out(attention(x)) [+ addend], keys, values) over the whole sequence."""
+    def prefill(self, x: Tensor, addend: Tensor | None = None,
+                need_kv: bool = True) -> tuple[Tensor, Tensor | None, Tensor | None]:
+        """(out(attention(x)) [+ addend], keys, values) over the whole
+        sequence; the HIP path may return None for the keys and values
+        unless ``need_kv`` (a KV cache is being filled)."""
         b, t, _ = x.shape
         c = self.cfg
         if self._hip(x):
@@ -313,19 +316,21 @@ class LocalGQA(nn.Module):
             if c.head_dim in hip_moe.ATTENTION_HEAD_DIMS:
                 # One HIP kernel for the whole sliding-window causal
                 # attention, reading the grouped kv heads in place; the
-                # projection (+ RoPE) kernel writes the values transposed.
+                # projection (+ RoPE) kernel writes K and V in the attention
+                # kernel's fragment order (plus row-major for a cache).
                 cos, sin = _rope_tables(c, x.new_empty(0, dtype=torch.float32))
-                keys = hip_moe.padded_keys(t)
+                scale = c.head_dim ** -0.5
                 if self._fused_projections():
-                    q, k, vt = hip_moe.proj_rope_qkv(x, self._qkv_fragments(), cos, sin,
-                                                     c.n_heads, c.n_kv_heads, c.head_dim,
-                                                     vt_keys=keys)
-                else:
-                    q, k, vt = hip_moe.rope_qkv(F.linear(x, self._packed_qkv()), cos, sin,
-                                                c.n_heads, c.n_kv_heads, c.head_dim, 0, False,
-                                                vt_keys=keys)
-                y = hip_moe.causal_attention(q, k, vt=vt, scale=c.head_dim ** -0.5,
-                                             window=c.window_size)
+                    q, kf, vf, k, v = hip_moe.proj_rope_qkv_frag(
+                        x, self._qkv_fragments(), cos, sin, c.n_heads, c.n_kv_heads, c.head_dim,
+                        cache_kv=need_kv)
+                    y = hip_moe.causal_attention_frag(q, kf, vf, kv_heads=c.n_kv_heads,
+                                                      scale=scale, window=c.window_size)
+                    return self._project_out(y, addend), k, v
+                q, k, vt = hip_moe.rope_qkv(F.linear(x, self._packed_qkv()), cos, sin,
+                                            c.n_heads, c.n_kv_heads, c.head_dim, 0, False,
+                                            vt_keys=hip_moe.padded_keys(t))
+                y = hip_moe.causal_attention(q, k, vt=vt, scale=scale, window=c.window_size)
                 return self._project_out(y, addend), k, vt[..., :t].transpose(-1, -2)
         result, k, v = self._prefill_torch(x)
         return (result if addend is None else addend + result), k, v
@@ -357,7 +362,7 @@ class LocalGQA(nn.Module):
         return self.out(y.transpose(1, 2).reshape(b, t, -1)), k, v
 
     def forward(self, x: Tensor, addend: Tensor | None = None) -> Tensor:
-        return self.prefill(x, addend)[0]
+        return self.prefill(x, addend, need_kv=False)[0]
 
     def _packed_qkv(self) -> Tensor:
         cached = self.__dict__.get("_qkv_weight")
@@ -459,15 +464,15 @@ class GlobalMLA(nn.Module):
             return y.view(b, t, c.n_heads, c.head_dim).transpose(1, 2)
 
         if c.uses_hip and _hip_inference(x) and self._fused_projections():
-            # Five projection kernels around one attention kernel; v_up
-            # writes the values transposed, [b, H * d, keys].
+            # Five projection kernels around one attention kernel; k_up and
+            # v_up write K and V in the attention kernel's fragment order.
             from . import hip_moe
             latent = hip_moe.proj(x, self._fragments("kv_down"), c.kv_latent_dim)
             q = hip_moe.proj(x, self._fragments("q"), width)
-            k = hip_moe.proj(latent, self._fragments("k_up"), width)
-            vt = hip_moe.proj_transposed(latent, self._fragments("v_up"), width,
-                                         hip_moe.padded_keys(t)).view(b, c.n_heads, c.head_dim, -1)
-            y = hip_moe.causal_attention(heads(q), heads(k), vt=vt, scale=c.head_dim ** -0.5)
+            kf = hip_moe.proj_frag(latent, self._fragments("k_up"), width, c.head_dim, False)
+            vf = hip_moe.proj_frag(latent, self._fragments("v_up"), width, c.head_dim, True)
+            y = hip_moe.causal_attention_frag(heads(q), kf, vf, kv_heads=c.n_heads,
+                                              scale=c.head_dim ** -0.5)
             return hip_moe.proj(y, self._fragments("out"), c.dim, addend=addend), latent
         latent = self.kv_down(x)
         if c.uses_hip and _hip_inference(x):

@@ -162,3 +162,26 @@ def test_argument_validation_without_gpu(lib):
                                          2, 96, 0, fake, fake, fake, null) == -3
     assert lib.parrot_proj_rope_qkv_bf16(fake, 1, 4, 768, fake, fake, fake, 0, null, 128, 8,
                                          2, 96, 32, fake, fake, fake + 2, null) == -5
+    # fragment-order attention and the projections that write it
+    st8 = (ctypes.c_int64 * 3)(8 * 512 * 96, 512 * 96, 96)
+    st_odd = (ctypes.c_int64 * 3)(8 * 512 * 96, 512 * 96, 100)
+
+    def attn_frag(q_st=st8, d=96, kf=fake, window=2048):
+        return lib.parrot_causal_attention_frag_bf16(
+            fake, ctypes.cast(q_st, ctypes.c_void_p), kf, fake, 1, 512, 8, 2, d, window, 0.1,
+            fake, null)
+    assert attn_frag(kf=null) == -1
+    assert attn_frag(d=80) == -3
+    assert attn_frag(window=0) == -2
+    assert attn_frag(q_st=st_odd) == -5
+    assert attn_frag(kf=fake + 8) == -5
+    assert lib.parrot_proj_rope_qkv_frag_bf16(fake, 1, 4, 768, fake, fake, fake, 0, null, 128, 8,
+                                              2, 96, fake, null, null, null, fake, null) == -1
+    assert lib.parrot_proj_rope_qkv_frag_bf16(fake, 1, 4, 768, fake, fake, fake, 126, null, 128,
+                                              8, 2, 96, fake, null, null, fake, fake, null) == -2
+    assert lib.parrot_proj_rope_qkv_frag_bf16(fake, 1, 4, 768, fake, fake, fake, 0, null, 128, 8,
+                                              2, 80, fake, null, null, fake, fake, null) == -3
+    assert lib.parrot_proj_frag_bf16(fake, 1, 4, 128, fake, 768, 96, 2, fake, null) == -2
+    assert lib.parrot_proj_frag_bf16(fake, 1, 4, 128, fake, 770, 96, 0, fake, null) == -2
+    assert lib.parrot_proj_frag_bf16(fake, 1, 4, 128, fake, 640, 80, 0, fake, null) == -3
+    assert lib.parrot_proj_frag_bf16(fake, 1, 4, 128, fake, 768, 96, 1, fake + 8, null) == -5

@@ -72,3 +72,39 @@ def test_causal_attention(b, H, Hk, t, d, window, strided):
         ctl_err = (ctl - ref).abs()
         _say(f"  control max-abs {ctl_err.max():.3e} mean-abs {ctl_err.mean():.3e}")
         assert err.mean() <= 2 * ctl_err.mean() + 1e-5
+
+
+def _padded_nan(x, t):
+    """[b, h, t, d] -> [b, h, ceil(t / 32) * 32, d] with non-finite padding keys."""
+    from parrot import hip_moe
+    b, h, _, d = x.shape
+    out = torch.full((b, h, hip_moe.key_blocks(t) * 32, d), float("nan"), dtype=x.dtype)
+    out[:, :, :t] = x
+    return out
+
+
+@pytest.mark.parametrize("b,H,Hk,t,d,window", [
+    (1, 8, 2, 512, 96, 2048), (2, 8, 8, 77, 96, 4096), (1, 4, 1, 300, 64, 100),
+    (2, 2, 2, 33, 128, 33), (3, 8, 2, 1, 96, 2048), (1, 8, 2, 1000, 96, 256)])
+def test_causal_attention_fragments(b, H, Hk, t, d, window):
+    """K and V in fragment order (padding keys non-finite) give exactly the
+    strided kernel's output; the torch packer and the kernel agree on the
+    layout because the results match."""
+    from parrot import hip_moe
+    _say(f"attention fragments b={b} H={H} Hk={Hk} t={t} d={d} window={window}")
+    g = torch.Generator().manual_seed(t * 7 + d)
+    q = torch.randn(b, H, t, d, generator=g).bfloat16()
+    k = torch.randn(b, Hk, t, d, generator=g).bfloat16()
+    v = torch.randn(b, Hk, t, d, generator=g).bfloat16()
+    kf, vf = hip_moe.pack_kv_fragments(_padded_nan(k, t).cuda(), _padded_nan(v, t).cuda())
+    with torch.no_grad():
+        strided = hip_moe.causal_attention(q.cuda(), k.cuda(), v.cuda(), scale=d ** -0.5,
+                                           window=window)
+        frag = hip_moe.causal_attention_frag(q.cuda(), kf, vf, kv_heads=Hk, scale=d ** -0.5,
+                                             window=window)
+    assert torch.equal(frag, strided)
+    if t >= 300:
+        ref = _reference(q, k, v, d ** -0.5, window)
+        err = (frag.float().cpu() - ref).abs()
+        _say(f"  max-abs {err.max():.3e} mean-abs {err.mean():.3e}")
+        assert err.max() <= 1e-2 and err.mean() <= 1e-3

@@ -111,3 +111,56 @@ def test_proj_rope_qkv(batch, seq, start, device_start, vt):
         q2, k2, v2 = hip_moe.rope_qkv(qkv, cos, sin, H, Hk, d, start, False, pos, keys)
     assert torch.equal(q, q2) and torch.equal(k, k2)
     assert torch.equal(v[..., :seq] if vt else v, v2[..., :seq] if vt else v2)
+
+
+def _valid_fragments(b, h, t, d):
+    """Masks of the key positions a fragment-order K / V holds for t keys."""
+    from parrot import hip_moe
+    ones = torch.ones(b, h, t, d, dtype=torch.bfloat16, device="cuda")
+    km, vm = hip_moe.pack_kv_fragments(ones, ones)
+    return km != 0, vm != 0
+
+
+@pytest.mark.parametrize("batch,seq", [(1, 512), (2, 37), (3, 1), (1, 96)])
+def test_proj_rope_qkv_fragments(batch, seq):
+    """The fragment outputs hold exactly the row-major q|k|v path's k and v."""
+    from parrot import hip_moe
+    from parrot.model import ModelConfig, _rope_tables
+    cfg = ModelConfig()
+    H, Hk, d = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    n = (H + 2 * Hk) * d
+    _say(f"proj rope qkv fragments b={batch} t={seq}")
+    x, w = _operands(batch * seq, cfg.dim, n, 5 * seq)
+    packed = _packed(w)
+    cos, sin = _rope_tables(cfg, torch.empty(0, device="cuda"))
+    xc = x.cuda().view(batch, seq, cfg.dim)
+    with torch.no_grad():
+        q, kf, vf, k, v = hip_moe.proj_rope_qkv_frag(xc, packed, cos, sin, H, Hk, d)
+        q1, kf1, vf1, k1, v1 = hip_moe.proj_rope_qkv_frag(xc, packed, cos, sin, H, Hk, d,
+                                                          cache_kv=False)
+        q2, k2, v2 = hip_moe.proj_rope_qkv(xc, packed, cos, sin, H, Hk, d)
+    assert k1 is None and v1 is None
+    assert torch.equal(q, q2) and torch.equal(k, k2) and torch.equal(v, v2)
+    assert torch.equal(q1, q2)
+    kr, vr = hip_moe.pack_kv_fragments(k2, v2)
+    km, vm = _valid_fragments(batch, Hk, seq, d)
+    assert torch.equal(kf[km], kr[km]) and torch.equal(vf[vm], vr[vm])
+    assert torch.equal(kf1[km], kr[km]) and torch.equal(vf1[vm], vr[vm])
+
+
+@pytest.mark.parametrize("batch,seq,values", [(1, 512, False), (1, 512, True), (2, 45, True),
+                                              (2, 45, False), (1, 3, True)])
+def test_proj_fragments(batch, seq, values):
+    """The MLA up-projections stored as fragment-order K / V."""
+    from parrot import hip_moe
+    _say(f"proj fragments b={batch} t={seq} values={values}")
+    heads, d, r = 8, 96, 128
+    x, w = _operands(batch * seq, r, heads * d, seq + int(values))
+    packed = _packed(w)
+    xc = x.cuda().view(batch, seq, r)
+    with torch.no_grad():
+        got = hip_moe.proj_frag(xc, packed, heads * d, d, values)
+        plain = hip_moe.proj(xc, packed, heads * d).view(batch, seq, heads, d).transpose(1, 2)
+    ref = hip_moe.pack_kv_fragments(plain, plain)[1 if values else 0]
+    mask = _valid_fragments(batch, heads, seq, d)[1 if values else 0]
+    assert torch.equal(got[mask], ref[mask])
