@@ -273,6 +273,16 @@ int parrot_proj_frag_bf16(const void* x, int64_t batch, int32_t seq, int32_t k,
                           const void* w_packed, int32_t n, int32_t head_dim, int32_t values,
                           void* out, void* stream);
 
+/* Both MLA up-projections in one launch: w_packed is [Wk; Wv] ([2n, k],
+ * packed as parrot_proj_bf16), x [batch * seq, k] with row stride lda; the
+ * first n output columns are stored as k_frag and the last n as v_frag
+ * (n / head_dim heads each, the layout of parrot_causal_attention_frag_bf16).
+ * Replaces k_up(latent) and v_up(latent) of GlobalMLA.prefill
+ * (parrot/model.py:350-360). */
+int parrot_proj_kv_frag_bf16(const void* x, int64_t batch, int32_t seq, int32_t k, int64_t lda,
+                             const void* w_packed, int32_t n, int32_t head_dim, void* k_frag,
+                             void* v_frag, void* stream);
+
 /* Workspace bytes for the routing / grouping entry points. */
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts);
 

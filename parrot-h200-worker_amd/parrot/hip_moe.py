@@ -558,6 +558,23 @@ def proj_frag(x: Tensor, packed: Tensor, n: int, head_dim: int, values: bool) ->
     return out
 
 
+def proj_kv_frag(x: Tensor, packed: Tensor, n: int, head_dim: int) -> tuple[Tensor, Tensor]:
+    """Both MLA up-projections in one launch: ``packed`` holds [Wk; Wv]
+    ([2n, k], ``pack_linear``), x [b, t, k] may be a row-strided view; returns
+    (k_frag, v_frag) for n / head_dim heads, as two ``proj_frag`` calls would."""
+    _require(x, "HIP projection")
+    b, t, k = x.shape
+    if packed.numel() != 2 * n * k:
+        raise RuntimeError("packed [Wk; Wv] weight does not match the input width")
+    x2 = _rows(x)
+    kf = x.new_empty((b, n // head_dim, key_blocks(t) * 32 * head_dim))
+    vf = torch.empty_like(kf)
+    _abi.check(_abi.load().parrot_proj_kv_frag_bf16(
+        ptr(x2), b, t, k, x2.stride(0), ptr(packed), n, head_dim, ptr(kf), ptr(vf),
+        _stream(x.device)), "parrot_proj_kv_frag_bf16")
+    return kf, vf
+
+
 # ---------------------------------------------------------------------------
 # Causal attention for prefill / forward (cf. parrot/model.py:264-295, 350-360)
 # ---------------------------------------------------------------------------

@@ -604,9 +604,29 @@ int parrot_proj_frag_bf16(const void* x, int64_t batch, int32_t seq, int32_t k,
   if (!aligned16(x) || !aligned16(w_packed) || !aligned16(out)) return PARROT_ERR_ALIGNMENT;
   if (batch == 0 || seq == 0) return PARROT_OK;
   return status(parrot::launch_proj_frag(
-      static_cast<const uint16_t*>(x), static_cast<int>(batch * seq), seq, k,
-      static_cast<const uint16_t*>(w_packed), n, head_dim, values != 0,
-      static_cast<uint16_t*>(out), as_stream(stream)));
+      static_cast<const uint16_t*>(x), static_cast<int>(batch * seq), seq, k, k,
+      static_cast<const uint16_t*>(w_packed), n, head_dim,
+      values ? nullptr : static_cast<uint16_t*>(out), values ? static_cast<uint16_t*>(out) : nullptr,
+      as_stream(stream)));
+}
+
+int parrot_proj_kv_frag_bf16(const void* x, int64_t batch, int32_t seq, int32_t k, int64_t lda,
+                             const void* w_packed, int32_t n, int32_t head_dim, void* k_frag,
+                             void* v_frag, void* stream) {
+  if (!x || !w_packed || !k_frag || !v_frag) return PARROT_ERR_NULL_POINTER;
+  if (batch < 0 || seq < 0 || k <= 0 || n <= 0 || head_dim <= 0 || n % head_dim || lda < k)
+    return PARROT_ERR_BAD_SHAPE;
+  if (n > INT32_MAX / 2 || !parrot::proj_shape_supported(k, 2 * n) ||
+      !parrot::attention_head_dim_supported(head_dim) || batch * seq > INT32_MAX)
+    return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || lda % 8 || !aligned16(w_packed) || !aligned16(k_frag) ||
+      !aligned16(v_frag))
+    return PARROT_ERR_ALIGNMENT;
+  if (batch == 0 || seq == 0) return PARROT_OK;
+  return status(parrot::launch_proj_frag(
+      static_cast<const uint16_t*>(x), static_cast<int>(batch * seq), seq, k, lda,
+      static_cast<const uint16_t*>(w_packed), 2 * n, head_dim, static_cast<uint16_t*>(k_frag),
+      static_cast<uint16_t*>(v_frag), as_stream(stream)));
 }
 
 int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,

@@ -336,7 +336,9 @@ hipError_t launch_proj_rope_qkv(const uint16_t* x, int rows, int seq, int dim, c
                                 int kv_heads, int head_dim, int vt_keys, uint16_t* q,
                                 uint16_t* k, uint16_t* v, uint16_t* kf, uint16_t* vf,
                                 hipStream_t s);
-hipError_t launch_proj_frag(const uint16_t* x, int rows, int seq, int k, const uint16_t* w,
-                            int n, int head_dim, bool values, uint16_t* out, hipStream_t s);
+// kf and/or vf; with both, w is [Wk; Wv] and n counts both halves.
+hipError_t launch_proj_frag(const uint16_t* x, int rows, int seq, int k, int64_t lda,
+                            const uint16_t* w, int n, int head_dim, uint16_t* kf, uint16_t* vf,
+                            hipStream_t s);
 
 }  // namespace parrot

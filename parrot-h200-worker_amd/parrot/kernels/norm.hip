@@ -55,77 +55,90 @@ __global__ __launch_bounds__(64) void rms_norm_kernel(
 
 // Block AttnRes: score_s = <rmsnorm_w(v_s), q>, alpha = softmax_s(score),
 // mix = bf16(sum_s alpha_s v_s); optionally y = rmsnorm_out(mix).
-// One wavefront per token.  Every source row is loaded up front (all loads in
-// flight together) and kept in registers through the scores and the mix.
-template <int MAXC>
-__global__ __launch_bounds__(64) void depth_mix_kernel(
+// One workgroup per token and one wavefront per 256 dims: a lane owns 4
+// consecutive dims of every source, all of whose loads are issued up front.
+// The per-source sums (squares and query dot) are wavefront sums combined
+// across the wavefronts through LDS in wavefront order, so every wavefront
+// derives the same scores; the output norm's sum of squares likewise.
+// (A single wavefront per token serialises ~1500 VALU instructions of
+// unpacking and summing at dim 768 and leaves most SIMDs idle.)
+constexpr int kDepthDimsPerWave = 256;
+constexpr int kDepthMaxWaves = 8;  // dim <= 2048
+
+__global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     DepthSources srcs, int n_sources, const uint16_t* __restrict__ query,
     const uint16_t* __restrict__ score_w, float score_eps,
     const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
     uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm) {
+  __shared__ float part[kDepthMaxWaves][2 * kMaxDepthSources];
+  __shared__ float part_out[kDepthMaxWaves];
   const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int waves = blockDim.x >> 6;
   const int64_t tok = blockIdx.x;
-  if (tok >= tokens) return;
   const int chunks = dim >> 2;
-  const int64_t base = tok * (dim >> 2);
+  const int i = wave * kWave + lane;  // this lane's 4-dim chunk
+  const bool has = i < chunks;
+  const int64_t base = tok * chunks;
 
-  // Combined score weight w_d * q_d for this lane's elements.
-  float wq[MAXC][4];
-  {
-    const uint2* q2 = reinterpret_cast<const uint2*>(query);
-    const uint2* w2 = reinterpret_cast<const uint2*>(score_w);
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      const int i = lane + c * kWave;
-      uint2 q = i < chunks ? q2[i] : make_uint2(0u, 0u);
-      uint2 g = i < chunks ? w2[i] : make_uint2(0u, 0u);
-      wq[c][0] = lo_bf16(q.x) * lo_bf16(g.x);
-      wq[c][1] = hi_bf16(q.x) * hi_bf16(g.x);
-      wq[c][2] = lo_bf16(q.y) * lo_bf16(g.y);
-      wq[c][3] = hi_bf16(q.y) * hi_bf16(g.y);
-    }
-  }
-
-  // Every source row stays in registers from its load to the mix (the
-  // source loop is unrolled over the maximum count, guarded by n_sources),
-  // so a token needs no LDS and no barrier and occupancy is set by VGPRs.
-  uint2 v[kMaxDepthSources][MAXC];
+  // Every source chunk, then the score weights (w_d * q_d) of the lane's dims.
+  uint2 v[kMaxDepthSources];
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) {
-    if (s < n_sources) {
-      const uint2* src = reinterpret_cast<const uint2*>(srcs.src[s]) + base;
-#pragma unroll
-      for (int c = 0; c < MAXC; ++c) {
-        const int i = lane + c * kWave;
-        v[s][c] = i < chunks ? src[i] : make_uint2(0u, 0u);
-      }
-    }
+    v[s] = make_uint2(0u, 0u);
+    if (s < n_sources && has) v[s] = reinterpret_cast<const uint2*>(srcs.src[s])[base + i];
   }
-  // Per-lane partial sums of every source, then all 2S wavefront reductions
-  // back to back so their latencies overlap.  The reductions leave every
-  // lane with the same totals, so the scores are wavefront-uniform.
+  float wq[4] = {0.f, 0.f, 0.f, 0.f};
+  uint2 g_out = make_uint2(0u, 0u);
+  if (has) {
+    const uint2 q = reinterpret_cast<const uint2*>(query)[i];
+    const uint2 g = reinterpret_cast<const uint2*>(score_w)[i];
+    wq[0] = lo_bf16(q.x) * lo_bf16(g.x);
+    wq[1] = hi_bf16(q.x) * hi_bf16(g.x);
+    wq[2] = lo_bf16(q.y) * lo_bf16(g.y);
+    wq[3] = hi_bf16(q.y) * hi_bf16(g.y);
+    if (out_norm != nullptr) g_out = reinterpret_cast<const uint2*>(out_w)[i];
+  }
+
+  // Per-source partial sums, all wavefront reductions back to back.
   float ss[kMaxDepthSources], dq[kMaxDepthSources];
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) {
-    ss[s] = 0.0f;
-    dq[s] = 0.0f;
-    if (s < n_sources) {
+    const float e0 = lo_bf16(v[s].x), e1 = hi_bf16(v[s].x);
+    const float e2 = lo_bf16(v[s].y), e3 = hi_bf16(v[s].y);
+    ss[s] = e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3;
+    dq[s] = e0 * wq[0] + e1 * wq[1] + e2 * wq[2] + e3 * wq[3];
+  }
 #pragma unroll
-      for (int c = 0; c < MAXC; ++c) {
-        const float e0 = lo_bf16(v[s][c].x), e1 = hi_bf16(v[s][c].x);
-        const float e2 = lo_bf16(v[s][c].y), e3 = hi_bf16(v[s][c].y);
-        ss[s] += e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3;
-        dq[s] += e0 * wq[c][0] + e1 * wq[c][1] + e2 * wq[c][2] + e3 * wq[c][3];
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    if (s < n_sources) {
+      ss[s] = wave_sum(ss[s]);
+      dq[s] = wave_sum(dq[s]);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s) {
+      if (s < n_sources) {
+        part[wave][2 * s] = ss[s];
+        part[wave][2 * s + 1] = dq[s];
       }
     }
   }
+  __syncthreads();
+
   float score[kMaxDepthSources];
   float mx = -INFINITY;
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) {
     score[s] = -INFINITY;
     if (s < n_sources) {
-      score[s] = wave_sum(dq[s]) * rsqrtf(wave_sum(ss[s]) / static_cast<float>(dim) + score_eps);
+      float sst = part[0][2 * s], dqt = part[0][2 * s + 1];
+      for (int w = 1; w < waves; ++w) {
+        sst += part[w][2 * s];
+        dqt += part[w][2 * s + 1];
+      }
+      score[s] = dqt * rsqrtf(sst / static_cast<float>(dim) + score_eps);
       mx = fmaxf(mx, score[s]);
     }
   }
@@ -135,66 +148,36 @@ __global__ __launch_bounds__(64) void depth_mix_kernel(
     if (s < n_sources) denom += __expf(score[s] - mx);
   const float inv = 1.0f / denom;
 
-  // Keep only the packed bf16 rows live across the reductions: without this
-  // the compiler holds the unpacked fp32 copies (twice the registers, half
-  // the occupancy) to reuse them in the mix.
-#pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s)
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) asm volatile("" : "+v"(v[s][c].x), "+v"(v[s][c].y));
-
-  float acc[MAXC][4];
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c) acc[c][0] = acc[c][1] = acc[c][2] = acc[c][3] = 0.0f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) {
     if (s < n_sources) {
       const float a = __expf(score[s] - mx) * inv;
-#pragma unroll
-      for (int c = 0; c < MAXC; ++c) {
-        acc[c][0] += a * lo_bf16(v[s][c].x);
-        acc[c][1] += a * hi_bf16(v[s][c].x);
-        acc[c][2] += a * lo_bf16(v[s][c].y);
-        acc[c][3] += a * hi_bf16(v[s][c].y);
-      }
+      acc[0] += a * lo_bf16(v[s].x);
+      acc[1] += a * hi_bf16(v[s].x);
+      acc[2] += a * lo_bf16(v[s].y);
+      acc[3] += a * hi_bf16(v[s].y);
     }
   }
-  uint2 mixed[MAXC];
-  float ss_out = 0.0f;
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    mixed[c].x = pack_bf16x2(acc[c][0], acc[c][1]);
-    mixed[c].y = pack_bf16x2(acc[c][2], acc[c][3]);
-    const float r0 = lo_bf16(mixed[c].x), r1 = hi_bf16(mixed[c].x);
-    const float r2 = lo_bf16(mixed[c].y), r3 = hi_bf16(mixed[c].y);
-    ss_out += r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3;
-  }
-  if (out_mix != nullptr) {
-    uint2* dst = reinterpret_cast<uint2*>(out_mix) + base;
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      const int i = lane + c * kWave;
-      if (i < chunks) dst[i] = mixed[c];
-    }
-  }
-  if (out_norm != nullptr) {
-    ss_out = wave_sum(ss_out);
-    const float r = rsqrtf(ss_out / static_cast<float>(dim) + out_eps);
-    const uint2* w2 = reinterpret_cast<const uint2*>(out_w);
-    uint2* dst = reinterpret_cast<uint2*>(out_norm) + base;
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      const int i = lane + c * kWave;
-      if (i < chunks) {
-        const uint2 g = w2[i];
-        uint2 o;
-        o.x = pack_bf16x2(lo_bf16(mixed[c].x) * r * lo_bf16(g.x),
-                          hi_bf16(mixed[c].x) * r * hi_bf16(g.x));
-        o.y = pack_bf16x2(lo_bf16(mixed[c].y) * r * lo_bf16(g.y),
-                          hi_bf16(mixed[c].y) * r * hi_bf16(g.y));
-        dst[i] = o;
-      }
-    }
+  uint2 mixed;
+  mixed.x = pack_bf16x2(acc[0], acc[1]);
+  mixed.y = pack_bf16x2(acc[2], acc[3]);
+  if (out_mix != nullptr && has) reinterpret_cast<uint2*>(out_mix)[base + i] = mixed;
+  if (out_norm == nullptr) return;  // uniform over the workgroup
+
+  const float r0 = lo_bf16(mixed.x), r1 = hi_bf16(mixed.x);
+  const float r2 = lo_bf16(mixed.y), r3 = hi_bf16(mixed.y);
+  const float sso = wave_sum(has ? r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3 : 0.0f);
+  if (lane == 0) part_out[wave] = sso;
+  __syncthreads();
+  float total = part_out[0];
+  for (int w = 1; w < waves; ++w) total += part_out[w];
+  const float r = rsqrtf(total / static_cast<float>(dim) + out_eps);
+  if (has) {
+    uint2 o;
+    o.x = pack_bf16x2(r0 * r * lo_bf16(g_out.x), r1 * r * hi_bf16(g_out.x));
+    o.y = pack_bf16x2(r2 * r * lo_bf16(g_out.y), r3 * r * hi_bf16(g_out.y));
+    reinterpret_cast<uint2*>(out_norm)[base + i] = o;
   }
 }
 
@@ -232,19 +215,11 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
                             float out_eps, int64_t tokens, int dim,
                             uint16_t* out_mix, uint16_t* out_norm, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((tokens + kRowsPerBlock - 1) / kRowsPerBlock));
-#define PARROT_DEPTH(C)                                                          \
-  depth_mix_kernel<C><<<grid, 64, 0, s>>>(srcs, n_sources, query, score_w,     \
-                                           score_eps, out_norm_w, out_eps,      \
-                                           tokens, dim, out_mix, out_norm)
-  switch (chunk_bucket(dim)) {
-    case 1: PARROT_DEPTH(1); break;
-    case 2: PARROT_DEPTH(2); break;
-    case 3: PARROT_DEPTH(3); break;
-    case 4: PARROT_DEPTH(4); break;
-    default: PARROT_DEPTH(8); break;
-  }
-#undef PARROT_DEPTH
+  const int waves = (dim + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
+  if (waves > kDepthMaxWaves) return hipErrorInvalidValue;
+  depth_mix_kernel<<<static_cast<unsigned>(tokens), kWave * waves, 0, s>>>(
+      srcs, n_sources, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
+      out_norm);
   return hipGetLastError();
 }
 

@@ -41,7 +41,8 @@
 //             Rotation partners (2i, 2i + 1) sit in adjacent lanes: one DPP
 //             quad_perm swap.
 //   kFrag     the output as attention K or V in fragment order, columns
-//             grouped into heads of head_dim (the MLA up-projections).
+//             grouped into heads of head_dim, or both from one [Wk; Wv]
+//             weight (the MLA up-projections).
 #include "common.h"
 
 namespace parrot {
@@ -274,10 +275,16 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
   }
 
   if (EPI == kFrag) {
+    // With both outputs, columns [0, N / 2) are K and [N / 2, N) are V
+    // (N / 2 is a multiple of 16: one side per wavefront).
     const int d = p.head_dim;
-    const int head = col / d;
-    const int w = col - head * d;
-    const int heads = p.N / d;
+    const bool both = p.kf != nullptr && p.vf != nullptr;
+    const int half = both ? p.N / 2 : p.N;
+    const bool to_v = p.kf == nullptr || (both && nw >= half);
+    const int c2 = both && to_v ? col - half : col;
+    const int head = c2 / d;
+    const int w = c2 - head * d;
+    const int heads = half / d;
 #pragma unroll
     for (int mi = 0; mi < kTilesM; ++mi) {
       const int row0 = m0 + mi * 16 + 4 * (lane >> 4);
@@ -285,7 +292,7 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
       uint16_t bits[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) bits[r] = f32_to_bf16(acc[mi][r]);
-      if (p.kf != nullptr) {
+      if (!to_v) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = row0 + r;
@@ -427,12 +434,13 @@ hipError_t launch_proj_rope_qkv(const uint16_t* x, int rows, int seq, int dim, c
   return launch_proj<kRopeQkv>(a, s);
 }
 
-hipError_t launch_proj_frag(const uint16_t* x, int rows, int seq, int k, const uint16_t* w,
-                            int n, int head_dim, bool values, uint16_t* out, hipStream_t s) {
+hipError_t launch_proj_frag(const uint16_t* x, int rows, int seq, int k, int64_t lda,
+                            const uint16_t* w, int n, int head_dim, uint16_t* kf, uint16_t* vf,
+                            hipStream_t s) {
   ProjArgs a{};
-  a.x = x; a.lda = k; a.rows = rows; a.K = k; a.N = n; a.w = w;
+  a.x = x; a.lda = lda; a.rows = rows; a.K = k; a.N = n; a.w = w;
   a.seq = seq; a.head_dim = head_dim; a.nblk = (seq + 31) / 32;
-  (values ? a.vf : a.kf) = out;
+  a.kf = kf; a.vf = vf;
   return launch_proj<kFrag>(a, s);
 }
 

@@ -446,13 +446,15 @@ class GlobalMLA(nn.Module):
         from . import hip_moe
         c = self.cfg
         width, r = c.n_heads * c.head_dim, c.kv_latent_dim
-        return (c.head_dim in hip_moe.ATTENTION_HEAD_DIMS and
-                hip_moe.proj_supported(c.dim, width) and hip_moe.proj_supported(c.dim, r) and
-                hip_moe.proj_supported(r, width) and hip_moe.proj_supported(width, c.dim))
+        return (c.head_dim in hip_moe.ATTENTION_HEAD_DIMS and r % 8 == 0 and
+                hip_moe.proj_supported(c.dim, width + r) and
+                hip_moe.proj_supported(r, 2 * width) and hip_moe.proj_supported(width, c.dim))
 
-    def _fragments(self, name: str) -> Tensor:
+    def _fragments(self, *names: str) -> Tensor:
+        """The named linears' weights, row-concatenated and packed."""
         from . import hip_moe
-        return hip_moe.pack_linear(self, name, (getattr(self, name).weight,))
+        return hip_moe.pack_linear(self, "_".join(names),
+                                   tuple(getattr(self, n).weight for n in names))
 
     def prefill(self, x: Tensor, addend: Tensor | None = None) -> tuple[Tensor, Tensor]:
         """(out(attention(x)) [+ addend], latent) over the whole sequence."""
@@ -464,13 +466,14 @@ class GlobalMLA(nn.Module):
             return y.view(b, t, c.n_heads, c.head_dim).transpose(1, 2)
 
         if c.uses_hip and _hip_inference(x) and self._fused_projections():
-            # Five projection kernels around one attention kernel; k_up and
-            # v_up write K and V in the attention kernel's fragment order.
+            # Three projection kernels around one attention kernel: q with
+            # kv_down, then k_up with v_up writing K and V in the attention
+            # kernel's fragment order, then the output projection.
             from . import hip_moe
-            latent = hip_moe.proj(x, self._fragments("kv_down"), c.kv_latent_dim)
-            q = hip_moe.proj(x, self._fragments("q"), width)
-            kf = hip_moe.proj_frag(latent, self._fragments("k_up"), width, c.head_dim, False)
-            vf = hip_moe.proj_frag(latent, self._fragments("v_up"), width, c.head_dim, True)
+            qkv = hip_moe.proj(x, self._fragments("q", "kv_down"), width + c.kv_latent_dim)
+            q, latent = qkv[..., :width], qkv[..., width:]
+            kf, vf = hip_moe.proj_kv_frag(latent, self._fragments("k_up", "v_up"), width,
+                                          c.head_dim)
             y = hip_moe.causal_attention_frag(heads(q), kf, vf, kv_heads=c.n_heads,
                                               scale=c.head_dim ** -0.5)
             return hip_moe.proj(y, self._fragments("out"), c.dim, addend=addend), latent

@@ -185,3 +185,11 @@ def test_argument_validation_without_gpu(lib):
     assert lib.parrot_proj_frag_bf16(fake, 1, 4, 128, fake, 770, 96, 0, fake, null) == -2
     assert lib.parrot_proj_frag_bf16(fake, 1, 4, 128, fake, 640, 80, 0, fake, null) == -3
     assert lib.parrot_proj_frag_bf16(fake, 1, 4, 128, fake, 768, 96, 1, fake + 8, null) == -5
+    assert lib.parrot_proj_kv_frag_bf16(fake, 1, 4, 128, 896, fake, 768, 96, fake, null,
+                                        null) == -1
+    assert lib.parrot_proj_kv_frag_bf16(fake, 1, 4, 128, 100, fake, 768, 96, fake, fake,
+                                        null) == -2
+    assert lib.parrot_proj_kv_frag_bf16(fake, 1, 4, 128, 900, fake, 768, 96, fake, fake,
+                                        null) == -5
+    assert lib.parrot_proj_kv_frag_bf16(fake, 1, 4, 128, 896, fake, 768, 80, fake, fake,
+                                        null) == -2

@@ -164,3 +164,23 @@ def test_proj_fragments(batch, seq, values):
     ref = hip_moe.pack_kv_fragments(plain, plain)[1 if values else 0]
     mask = _valid_fragments(batch, heads, seq, d)[1 if values else 0]
     assert torch.equal(got[mask], ref[mask])
+
+
+@pytest.mark.parametrize("batch,seq", [(1, 512), (2, 45), (1, 3)])
+def test_proj_kv_fragments(batch, seq):
+    """[Wk; Wv] in one launch from a row-strided latent == two single launches."""
+    from parrot import hip_moe
+    _say(f"proj kv fragments b={batch} t={seq}")
+    heads, d, r = 8, 96, 128
+    x, w = _operands(batch * seq, r, 2 * heads * d, seq + 11)
+    wide = torch.zeros(batch * seq, 896, dtype=torch.bfloat16)
+    wide[:, 768:] = x
+    latent = wide.cuda().view(batch, seq, 896)[..., 768:]
+    with torch.no_grad():
+        kf, vf = hip_moe.proj_kv_frag(latent, _packed(w), heads * d, d)
+        k1 = hip_moe.proj_frag(x.cuda().view(batch, seq, r), _packed(w[:heads * d]), heads * d,
+                               d, False)
+        v1 = hip_moe.proj_frag(x.cuda().view(batch, seq, r), _packed(w[heads * d:]), heads * d,
+                               d, True)
+    km, vm = _valid_fragments(batch, heads, seq, d)
+    assert torch.equal(kf[km], k1[km]) and torch.equal(vf[vm], v1[vm])
