@@ -510,16 +510,22 @@ def build_model():
 
     captured = {}
     moe0 = model.blocks[0].moe
-    original = moe0.inference
+    originals = {name: getattr(moe0, name) for name in ("inference", "inference_then_mix")}
 
-    def spy(x, **kw):
-        captured["x"] = x.detach().reshape(-1, x.shape[-1]).clone()
-        return original(x, **kw)
+    def spying(name):
+        def spy(x, **kw):
+            captured.setdefault("x", x.detach().reshape(-1, x.shape[-1]).clone())
+            return originals[name](x, **kw)
+        return spy
 
-    moe0.inference = spy
+    for name in originals:
+        setattr(moe0, name, spying(name))
     with torch.no_grad():
         model(ids)
-    del moe0.inference
+    for name in originals:
+        delattr(moe0, name)
+    if "x" not in captured:
+        raise RuntimeError("block 0's MoE input was not captured")
     return model, ids, captured
 
 

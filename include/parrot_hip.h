@@ -70,6 +70,22 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
                           const void* out_norm_weight, float out_eps, int64_t tokens,
                           int32_t dim, void* out_mix, void* out_norm, void* stream);
 
+/* parrot_experts_combine_bf16 folded into the next module's depth mix: the
+ * combined MoE row out (bf16(addend + bf16(shared + routed rows)), exactly
+ * as parrot_experts_combine_bf16, written to out) is the last of n_sources
+ * depth sources; sources holds the other n_sources - 1 ([tokens, dim] bf16,
+ * in stream order), and the mix / normalised mix are written as by
+ * parrot_depth_mix_bf16.  workspace is the one filled by
+ * parrot_experts_down_bf16.  Replaces, for a layer whose MoE output feeds the
+ * next attention layer, the combine of grouped_mps_experts
+ * (parrot/metal_moe.py:372-416) followed by metal_depth_mix_norm
+ * (parrot/metal_moe.py:455-477). */
+int parrot_experts_combine_depth_mix_bf16(
+    int64_t tokens, int32_t dim, int32_t hidden_dim, int32_t shared_dim, const void* addend,
+    void* out, void* workspace, size_t workspace_bytes, const void* const* sources,
+    int32_t n_sources, const void* query, const void* score_norm_weight, float score_eps,
+    const void* out_norm_weight, float out_eps, void* out_mix, void* out_norm, void* stream);
+
 /* Rotary embedding of the local-attention heads fused with the head-major
  * split of one packed projection qkv [batch * seq, (H + 2 Hk) * head_dim]
  * (bf16, row-major, columns q | k | v):

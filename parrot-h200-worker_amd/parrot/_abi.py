@@ -46,6 +46,9 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _i32, _i32, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,
          _p]),
     "parrot_proj_frag_bf16": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _i32, _i32, _i32, _p, _p]),
+    "parrot_experts_combine_depth_mix_bf16": (
+        ctypes.c_int,
+        [_i64, _i32, _i32, _i32, _p, _p, _p, _sz, _p, _i32, _p, _p, _f32, _p, _f32, _p, _p, _p]),
     "parrot_proj_kv_frag_bf16": (
         ctypes.c_int, [_p, _i64, _i32, _i32, _i64, _p, _i32, _i32, _p, _p, _p]),
     "parrot_proj_bf16": (ctypes.c_int, [_p, _i64, _i32, _i64, _p, _i32, _p, _i64, _p, _i64, _p]),

@@ -276,11 +276,16 @@ def invalidate_packed_weights(module: torch.nn.Module) -> None:
 
 def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: Tensor,
                         positions: Tensor | None = None, counts: Tensor | None = None,
-                        addend: Tensor | None = None,
-                        grouping: Grouping | None = None) -> Tensor:
+                        addend: Tensor | None = None, grouping: Grouping | None = None,
+                        then_mix: tuple | None = None):
     """Routed + shared SwiGLU experts and weighted combine; returns
     ``addend + delta`` (each rounded to the input dtype) when ``addend`` is
-    given, else the MoE delta."""
+    given, else the MoE delta.
+
+    ``then_mix = (depth_module, sources, output_norm)``: the combine also runs
+    the next module's depth mix over ``sources + [result]`` (the kernel's
+    result row is the last source) and returns ``(result, normalised mix)``;
+    ``sources`` are [tokens, dim] views in stream order."""
     _require(flat, "The grouped HIP backend")
     cfg = module.cfg
     tokens, dim = flat.shape
@@ -308,13 +313,42 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
                                                 cfg.shared_expert_dim)
     ws = _scratch(module, "_hip_experts_workspace", nbytes, flat.device)
     out = torch.empty_like(flat)
-    _abi.check(lib.parrot_grouped_experts_bf16(
-        ptr(flat), tokens, dim, experts, cfg.expert_dim, cfg.shared_expert_dim,
-        grouping.capacity, ptr(grouping.counts), ptr(grouping.offsets), ptr(grouping.perm),
-        ptr(grouping.overflow), ptr(weights), ptr(gate_up), ptr(down), ptr(shared_gate_up),
-        ptr(shared_down), ptr(addend), ptr(out), ptr(ws), nbytes, _stream(flat.device)),
-        "parrot_grouped_experts_bf16")
-    return out
+    stream = _stream(flat.device)
+    if then_mix is None:
+        _abi.check(lib.parrot_grouped_experts_bf16(
+            ptr(flat), tokens, dim, experts, cfg.expert_dim, cfg.shared_expert_dim,
+            grouping.capacity, ptr(grouping.counts), ptr(grouping.offsets), ptr(grouping.perm),
+            ptr(grouping.overflow), ptr(weights), ptr(gate_up), ptr(down), ptr(shared_gate_up),
+            ptr(shared_down), ptr(addend), ptr(out), ptr(ws), nbytes, stream),
+            "parrot_grouped_experts_bf16")
+        return out
+    group_args = (experts, cfg.expert_dim, cfg.shared_expert_dim, grouping.capacity,
+                  ptr(grouping.counts), ptr(grouping.offsets), ptr(grouping.perm),
+                  ptr(grouping.overflow))
+    _abi.check(lib.parrot_experts_gate_up_bf16(
+        ptr(flat), tokens, dim, *group_args, ptr(gate_up), ptr(shared_gate_up), ptr(ws), nbytes,
+        stream), "parrot_experts_gate_up_bf16")
+    _abi.check(lib.parrot_experts_down_bf16(
+        tokens, dim, *group_args, ptr(weights), ptr(down), ptr(shared_down), ptr(ws), nbytes,
+        stream), "parrot_experts_down_bf16")
+    depth, sources, output_norm = then_mix
+    if len(sources) + 1 > MAX_DEPTH_SOURCES:
+        raise RuntimeError(f"HIP depth mixing supports one to {MAX_DEPTH_SOURCES} sources")
+    rows = []
+    for src in sources:
+        if src.shape[-1] != dim or src.numel() != flat.numel() or src.dtype != flat.dtype:
+            raise RuntimeError("depth sources must match the MoE input")
+        rows.append(src.reshape(tokens, dim).contiguous())
+    array = _SourceArray(*([t.data_ptr() for t in rows] +
+                           [out.data_ptr()] * (MAX_DEPTH_SOURCES - len(rows))))
+    mixed = torch.empty_like(flat)
+    _abi.check(lib.parrot_experts_combine_depth_mix_bf16(
+        tokens, dim, cfg.expert_dim, cfg.shared_expert_dim, ptr(addend), ptr(out), ptr(ws),
+        nbytes, ctypes.cast(array, ctypes.c_void_p), len(rows) + 1, ptr(depth.query),
+        ptr(depth.norm.weight), float(depth.norm.eps), ptr(output_norm.weight),
+        float(output_norm.eps), None, ptr(mixed), stream), "parrot_experts_combine_depth_mix_bf16")
+    del rows
+    return out, mixed
 
 
 DECODE_MAX_TOKENS = 16  # rows the fused decode MoE takes

@@ -142,7 +142,8 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
       srcs, n_sources, static_cast<const uint16_t*>(query),
       static_cast<const uint16_t*>(score_norm_weight), score_eps,
       static_cast<const uint16_t*>(out_norm_weight), out_eps, tokens, dim,
-      static_cast<uint16_t*>(out_mix), static_cast<uint16_t*>(out_norm), as_stream(stream)));
+      static_cast<uint16_t*>(out_mix), static_cast<uint16_t*>(out_norm), nullptr,
+      as_stream(stream)));
 }
 
 int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* sin_table,
@@ -378,6 +379,46 @@ int parrot_experts_combine_bf16(int64_t tokens, int32_t dim, int32_t hidden_dim,
   return status(parrot::launch_combine(ws.y_routed, ws.y_shared,
                                        static_cast<const uint16_t*>(addend), tokens, dim,
                                        static_cast<uint16_t*>(out), as_stream(stream)));
+}
+
+int parrot_experts_combine_depth_mix_bf16(
+    int64_t tokens, int32_t dim, int32_t hidden_dim, int32_t shared_dim, const void* addend,
+    void* out, void* workspace, size_t workspace_bytes, const void* const* sources,
+    int32_t n_sources, const void* query, const void* score_norm_weight, float score_eps,
+    const void* out_norm_weight, float out_eps, void* out_mix, void* out_norm, void* stream) {
+  if (!out || !query || !score_norm_weight) return PARROT_ERR_NULL_POINTER;
+  if (!out_mix && !out_norm) return PARROT_ERR_NULL_POINTER;
+  if (out_norm && !out_norm_weight) return PARROT_ERR_NULL_POINTER;
+  if (n_sources < 1 || n_sources > kMaxDepthSources) return PARROT_ERR_UNSUPPORTED;
+  if (n_sources > 1 && !sources) return PARROT_ERR_NULL_POINTER;
+  if (tokens < 0 || dim <= 0 || dim % 4 || hidden_dim <= 0 || shared_dim <= 0)
+    return PARROT_ERR_BAD_SHAPE;
+  if (dim > 2048) return PARROT_ERR_UNSUPPORTED;
+  const ExpertsWorkspace ws = experts_ws(workspace, tokens, dim, hidden_dim, shared_dim);
+  if (!workspace || workspace_bytes < ws.bytes) return PARROT_ERR_WORKSPACE;
+  parrot::DepthSources srcs{};
+  uintptr_t bits = reinterpret_cast<uintptr_t>(query) |
+                   reinterpret_cast<uintptr_t>(score_norm_weight) |
+                   reinterpret_cast<uintptr_t>(out_norm_weight) |
+                   reinterpret_cast<uintptr_t>(out_mix) | reinterpret_cast<uintptr_t>(out_norm);
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    const void* p = s < n_sources - 1 ? sources[s] : out;  // unread slots: any valid row
+    if (!p) return PARROT_ERR_NULL_POINTER;
+    bits |= reinterpret_cast<uintptr_t>(p);
+    srcs.src[s] = static_cast<const uint16_t*>(p);
+  }
+  if (bits & 7u) return PARROT_ERR_ALIGNMENT;
+  if (!aligned16(workspace) || !aligned16(out) || (addend && !aligned16(addend)))
+    return PARROT_ERR_ALIGNMENT;
+  const parrot::CombineSource comb{ws.y_routed, ws.y_shared,
+                                   static_cast<const uint16_t*>(addend),
+                                   static_cast<uint16_t*>(out)};
+  return status(parrot::launch_depth_mix(
+      srcs, n_sources, static_cast<const uint16_t*>(query),
+      static_cast<const uint16_t*>(score_norm_weight), score_eps,
+      static_cast<const uint16_t*>(out_norm_weight), out_eps, tokens, dim,
+      static_cast<uint16_t*>(out_mix), static_cast<uint16_t*>(out_norm), &comb,
+      as_stream(stream)));
 }
 
 size_t parrot_decode_moe_workspace_bytes(int64_t tokens, int32_t hidden_dim,

@@ -201,11 +201,23 @@ struct DepthSources {
   const uint16_t* src[kMaxDepthSources];
 };
 
+// The MoE combine folded into a depth mix: the combined row (as
+// launch_combine computes it) is produced in the kernel, written to `out`
+// and used as the last of the n_sources depth sources.
+struct CombineSource {
+  const float* y_routed;   // [2 T, dim], route weights applied
+  const float* y_shared;   // [T, dim]
+  const uint16_t* addend;  // optional [T, dim]
+  uint16_t* out;           // [T, dim]
+};
+
+// comb: optional (nullptr: every source is read from srcs).
 hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
                             const uint16_t* query, const uint16_t* score_w,
                             float score_eps, const uint16_t* out_norm_w,
                             float out_eps, int64_t tokens, int dim,
-                            uint16_t* out_mix, uint16_t* out_norm, hipStream_t s);
+                            uint16_t* out_mix, uint16_t* out_norm, const CombineSource* comb,
+                            hipStream_t s);
 
 // Routing: router projection (or given fp32 logits) + top-2 + per-block
 // stable ranks.  Writes block-local ranks into `positions` and per-block

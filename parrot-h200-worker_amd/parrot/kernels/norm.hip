@@ -69,7 +69,7 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     DepthSources srcs, int n_sources, const uint16_t* __restrict__ query,
     const uint16_t* __restrict__ score_w, float score_eps,
     const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
-    uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm) {
+    uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm, CombineSource comb) {
   __shared__ float part[kDepthMaxWaves][2 * kMaxDepthSources];
   __shared__ float part_out[kDepthMaxWaves];
   const int lane = threadIdx.x & (kWave - 1);
@@ -82,11 +82,35 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   const int64_t base = tok * chunks;
 
   // Every source chunk, then the score weights (w_d * q_d) of the lane's dims.
+  const bool combine = comb.y_shared != nullptr;
+  const int n_read = combine ? n_sources - 1 : n_sources;
   uint2 v[kMaxDepthSources];
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) {
     v[s] = make_uint2(0u, 0u);
-    if (s < n_sources && has) v[s] = reinterpret_cast<const uint2*>(srcs.src[s])[base + i];
+    if (s < n_read && has) v[s] = reinterpret_cast<const uint2*>(srcs.src[s])[base + i];
+  }
+  if (combine) {
+    // The MoE output row: bf16(shared + routed 0 + routed 1), then
+    // bf16(addend + that), exactly as the combine kernel; it is the new
+    // residual source and the last depth source.
+    uint2 o = make_uint2(0u, 0u);
+    if (has) {
+      const float4 sh = reinterpret_cast<const float4*>(comb.y_shared)[base + i];
+      const float4 r0 = reinterpret_cast<const float4*>(comb.y_routed)[(2 * tok) * chunks + i];
+      const float4 r1 = reinterpret_cast<const float4*>(comb.y_routed)[(2 * tok + 1) * chunks + i];
+      o.x = pack_bf16x2(sh.x + r0.x + r1.x, sh.y + r0.y + r1.y);
+      o.y = pack_bf16x2(sh.z + r0.z + r1.z, sh.w + r0.w + r1.w);
+      if (comb.addend != nullptr) {
+        const uint2 p = reinterpret_cast<const uint2*>(comb.addend)[base + i];
+        o.x = pack_bf16x2(lo_bf16(p.x) + lo_bf16(o.x), hi_bf16(p.x) + hi_bf16(o.x));
+        o.y = pack_bf16x2(lo_bf16(p.y) + lo_bf16(o.y), hi_bf16(p.y) + hi_bf16(o.y));
+      }
+      reinterpret_cast<uint2*>(comb.out)[base + i] = o;
+    }
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s)
+      if (s == n_sources - 1) v[s] = o;
   }
   float wq[4] = {0.f, 0.f, 0.f, 0.f};
   uint2 g_out = make_uint2(0u, 0u);
@@ -213,13 +237,15 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
                             const uint16_t* query, const uint16_t* score_w,
                             float score_eps, const uint16_t* out_norm_w,
                             float out_eps, int64_t tokens, int dim,
-                            uint16_t* out_mix, uint16_t* out_norm, hipStream_t s) {
+                            uint16_t* out_mix, uint16_t* out_norm, const CombineSource* comb,
+                            hipStream_t s) {
   if (tokens == 0) return hipSuccess;
   const int waves = (dim + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
   if (waves > kDepthMaxWaves) return hipErrorInvalidValue;
+  const CombineSource none{};
   depth_mix_kernel<<<static_cast<unsigned>(tokens), kWave * waves, 0, s>>>(
       srcs, n_sources, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
-      out_norm);
+      out_norm, comb != nullptr ? *comb : none);
   return hipGetLastError();
 }
 

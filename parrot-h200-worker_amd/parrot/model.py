@@ -660,6 +660,25 @@ class MoE(nn.Module):
         return result.view_as(x)
 
 
+    def inference_then_mix(self, x: Tensor, *, addend: Tensor | None, depth: "DepthMix",
+                           sources: list[Tensor], output_norm: "RMSNorm") -> tuple[Tensor, Tensor]:
+        """``inference(x, addend=addend)`` and the next module's input,
+        ``depth.normalized(sources + [result], output_norm)``; on the grouped
+        HIP path the combine and that depth mix are one kernel."""
+        from . import hip_moe
+        flat = x.reshape(-1, x.shape[-1])
+        if (self._hip_route_applies(x) and flat.shape[0] > hip_moe.DECODE_MAX_TOKENS and
+                depth.cfg.depth_backend == "hip" and
+                len(sources) < hip_moe.MAX_DEPTH_SOURCES):
+            routed = hip_moe.route(self, flat, collect_stats=False)
+            result, mixed = hip_moe.grouped_hip_experts(
+                self, flat, routed.indices, routed.weights, addend=addend,
+                grouping=routed.grouping, then_mix=(depth, sources, output_norm))
+            return result.view_as(x), mixed.view_as(x)
+        result = self.inference(x, direct=False, addend=addend)
+        return result, depth.normalized(sources + [result], output_norm)
+
+
 class Block(nn.Module):
     def __init__(self, cfg: ModelConfig, index: int):
         super().__init__()
@@ -732,6 +751,18 @@ class Parrot(nn.Module):
             return norm(x)
         return self.depth_mix[index].normalized(stream.sources(), norm)
 
+    def _moe_closing(self, block: Block, h: Tensor, stream: _AttnRes, index: int,
+                     next_norm: RMSNorm) -> Tensor:
+        """Close MoE module ``index`` (fused addend) and return the input of
+        module ``index + 1``: its depth mix normalised by ``next_norm``, made
+        by the MoE's combine kernel on the HIP path."""
+        older = list(stream.completed)  # the sources after closing: older + [result]
+        result, mixed = block.moe.inference_then_mix(
+            h, addend=stream.partial, depth=self.depth_mix[index + 1], sources=older,
+            output_norm=next_norm)
+        stream.close(result)
+        return mixed
+
     @staticmethod
     def _fuse_attention_addend(block: Block, h: Tensor, stream: _AttnRes | None) -> bool:
         """Fold ``partial + delta`` into the attention output projection (HIP only)."""
@@ -772,8 +803,11 @@ class Parrot(nn.Module):
         aux_losses, utilization = [], []
         remat = cfg.checkpoint_modules and self.training and torch.is_grad_enabled()
         index = 0
-        for block in self.blocks:
-            h = self._mixed_input(stream, x, index, block.attention_norm)
+        pending = None  # the next module's input, made by the previous MoE's combine
+        for bi, block in enumerate(self.blocks):
+            h = pending if pending is not None else \
+                self._mixed_input(stream, x, index, block.attention_norm)
+            pending = None
             if not remat and self._fuse_attention_addend(block, h, stream):
                 stream.close(block.attention(h, addend=stream.partial))
             else:
@@ -787,7 +821,10 @@ class Parrot(nn.Module):
 
             h = self._mixed_input(stream, x, index, block.moe_norm)
             if self._fuse_moe_addend(block, h, stream):
-                stream.close(block.moe.inference(h, direct=False, addend=stream.partial))
+                last = bi + 1 == len(self.blocks)
+                pending = self._moe_closing(
+                    block, h, stream, index,
+                    self.final_norm if last else self.blocks[bi + 1].attention_norm)
             else:
                 delta, aux, usage = (checkpoint(block.moe, h, use_reentrant=False) if remat
                                      else block.moe(h))
@@ -799,11 +836,15 @@ class Parrot(nn.Module):
                 else:
                     stream.push(delta)
             index += 1
-        if stream is not None:
-            x = self.depth_mix[-1](stream.sources())
-        # Loss-only callers can skip the last position's projection exactly.
-        head_input = x[:, :-1] if supervised_logits_only else x
-        logits = F.linear(self.final_norm(head_input), self.embedding.weight)
+        if pending is not None:
+            # The last MoE's combine produced final_norm(depth_mix[-1](...)).
+            normed = pending[:, :-1] if supervised_logits_only else pending
+        else:
+            if stream is not None:
+                x = self.depth_mix[-1](stream.sources())
+            # Loss-only callers can skip the last position's projection exactly.
+            normed = self.final_norm(x[:, :-1] if supervised_logits_only else x)
+        logits = F.linear(normed, self.embedding.weight)
 
         if cfg.collect_router_stats:
             aux_loss = torch.stack(aux_losses).mean()
@@ -840,8 +881,11 @@ class Parrot(nn.Module):
         stream = _AttnRes(x, cfg.depth_block_size) if cfg.residual == "attnres" else None
         caches: list[LocalKVCache | MLALatentCache] = []
         index = 0
-        for block in self.blocks:
-            h = self._mixed_input(stream, x, index, block.attention_norm)
+        pending = None  # the next module's input, made by the previous MoE's combine
+        for bi, block in enumerate(self.blocks):
+            h = pending if pending is not None else \
+                self._mixed_input(stream, x, index, block.attention_norm)
+            pending = None
             fuse = self._fuse_attention_addend(block, h, stream)
             addend = stream.partial if fuse else None
             if isinstance(block.attention, LocalGQA):
@@ -866,7 +910,10 @@ class Parrot(nn.Module):
             h = self._mixed_input(stream, x, index, block.moe_norm)
             if stream is not None and stream.partial is not None and \
                     block.moe._hip_route_applies(h):
-                stream.close(block.moe.inference(h, direct=False, addend=stream.partial))
+                last = bi + 1 == len(self.blocks)
+                pending = self._moe_closing(
+                    block, h, stream, index,
+                    self.final_norm if last else self.blocks[bi + 1].attention_norm)
             else:
                 delta = block.moe.inference(h, direct=False)
                 if stream is None:
@@ -874,9 +921,13 @@ class Parrot(nn.Module):
                 else:
                     stream.push(delta)
             index += 1
-        if stream is not None:
-            x = self.depth_mix[-1](stream.sources())
-        logits = F.linear(self.final_norm(x[:, -1:]), self.embedding.weight)
+        if pending is not None:
+            normed = pending[:, -1:]  # final_norm(depth_mix[-1](...)) from the last combine
+        else:
+            if stream is not None:
+                x = self.depth_mix[-1](stream.sources())
+            normed = self.final_norm(x[:, -1:])
+        logits = F.linear(normed, self.embedding.weight)
         position_device = None
         if cfg.uses_hip and _hip_inference(logits):
             position_device = torch.full((1,), t, dtype=torch.int32, device=logits.device)

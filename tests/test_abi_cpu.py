@@ -193,3 +193,14 @@ def test_argument_validation_without_gpu(lib):
                                         null) == -5
     assert lib.parrot_proj_kv_frag_bf16(fake, 1, 4, 128, 896, fake, 768, 80, fake, fake,
                                         null) == -2
+    # combine folded into a depth mix: sources, counts, workspace
+    ews = lib.parrot_experts_workspace_bytes(64, 64, 128, 64)
+    assert lib.parrot_experts_combine_depth_mix_bf16(
+        64, 64, 128, 64, null, fake, fake, ews, null, 2, fake, fake, 1e-6, fake, 1e-6, null, fake,
+        null) == -1
+    assert lib.parrot_experts_combine_depth_mix_bf16(
+        64, 64, 128, 64, null, fake, fake, ews, fake, 10, fake, fake, 1e-6, fake, 1e-6, null,
+        fake, null) == -3
+    assert lib.parrot_experts_combine_depth_mix_bf16(
+        64, 64, 128, 64, null, fake, fake, 16, null, 1, fake, fake, 1e-6, fake, 1e-6, null, fake,
+        null) == -4

@@ -225,3 +225,29 @@ def test_rope_qkv(b, t, start, expand):
         assert torch.equal(q2, q) and torch.equal(k2, k)
         assert vt.shape == (b, Hk, d, hip_moe.padded_keys(t))
         assert torch.equal(vt[..., :t].transpose(-1, -2), v)
+
+
+@pytest.mark.parametrize("tokens,n_older", [(512, 3), (130, 0), (64, 8), (17, 1)])
+def test_combine_then_depth_mix(tokens, n_older):
+    """The combine folded into the next module's depth mix writes exactly the
+    combine's output and exactly the depth mix + norm of it with the older
+    sources (the same kernel arithmetic, the new row taken from registers)."""
+    from moe_cases import inputs, moe_module
+    from parrot import hip_moe
+    _say(f"combine + depth mix T={tokens} older={n_older}")
+    module = moe_module(16, seed=3)
+    x = inputs(tokens, seed=4)
+    addend = inputs(tokens, seed=5)
+    depth = _Depth(x.shape[1]).cuda().bfloat16()
+    norm = _Norm(x.shape[1]).cuda().bfloat16()
+    older = [inputs(tokens, seed=10 + i) * (1 + i) for i in range(n_older)]
+    with torch.no_grad():
+        routed = hip_moe.route(module, x, False)
+        plain = hip_moe.grouped_hip_experts(module, x, routed.indices, routed.weights,
+                                            addend=addend, grouping=routed.grouping)
+        fused, mixed = hip_moe.grouped_hip_experts(module, x, routed.indices, routed.weights,
+                                                   addend=addend, grouping=routed.grouping,
+                                                   then_mix=(depth, older, norm))
+        ref = hip_moe.depth_mix_norm(depth, older + [plain], norm)
+    assert torch.equal(fused, plain)
+    assert torch.equal(mixed, ref)
