@@ -850,8 +850,10 @@ class Parrot(nn.Module):
             aux_loss = torch.stack(aux_losses).mean()
             expert_utilization = torch.stack(utilization)
         else:
-            aux_loss = x.new_zeros((), dtype=torch.float32)
-            expert_utilization = x.new_zeros((cfg.n_layers, cfg.n_experts), dtype=torch.float32)
+            # one zero fill for both (views of one buffer)
+            zeros = x.new_zeros((1 + cfg.n_layers * cfg.n_experts,), dtype=torch.float32)
+            aux_loss = zeros[0]
+            expert_utilization = zeros[1:].view(cfg.n_layers, cfg.n_experts)
         lm_loss = loss = None
         if labels is not None:
             targets = labels.reshape(b, t, bag_size)[:, 1:]
