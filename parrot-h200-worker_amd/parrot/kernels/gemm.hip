@@ -524,11 +524,13 @@ hipError_t launch_stream(int phase, const GemmArgs& args, int n_max, hipStream_t
 }
 
 // Register-ring depth: the largest of 8 / 4 / 2 / 1 dividing every segment's
-// number of 32-wide k steps in this phase.
+// number of 32-wide k steps in this phase, at most 4 for gate/up (its two
+// fragments per step double the registers per stage; measured on MI355X in
+// the bs1 x 512 forward, 4 stages beat 8 for gate/up and 8 beat 4 for down).
 int stream_depth(int phase, const GemmArgs& a) {
   const int k0 = phase == 1 ? a.dim : a.hidden_dim;
   const int k1 = phase == 1 ? a.dim : a.shared_dim;
-  for (int pf = 8; pf > 1; pf >>= 1)
+  for (int pf = phase == 1 ? 4 : 8; pf > 1; pf >>= 1)
     if ((k0 / 32) % pf == 0 && (k1 / 32) % pf == 0) return pf;
   return 1;
 }
