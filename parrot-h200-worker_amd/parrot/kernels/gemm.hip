@@ -45,32 +45,57 @@ struct GemmArgs {
   float* y_shared;            // phase 2 output [T, dim]
 };
 
-// Which row segment and M-tile does this workgroup own?  One vector load of
-// the expert counts (lane e holds counts[e]), then a uniform scan over the
-// lanes' tile counts with readlane -- no chain of dependent memory loads.
-// Segment E (the shared expert, all T tokens) comes first.
+// The row tile a workgroup owns: segment `seg` (E = the shared expert),
+// M-tile `mt` of its `rows` rows; the segment's hidden rows start at `hbase`
+// and its part of the overflow list at `obase`.
+struct Tile {
+  int seg, mt, rows, hbase, obase;
+};
+
+// Which tile does this workgroup own?  The shared expert's tiles come first
+// and need no load.  For routed tiles one batch of vector loads fetches the
+// expert counts and both offset tables (lane e holds expert e's entries),
+// then a uniform scan over the lanes' tile counts with readlane picks the
+// segment -- one memory hop, no chain of dependent loads.
 template <int BM>
-__device__ __forceinline__ bool find_tile(const GemmArgs& p, int T, int& seg, int& mt,
-                                          int& rows) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int count = lane < p.experts ? p.counts[lane] : 0;
-  const int tiles = (count + BM - 1) / BM;
+__device__ __forceinline__ bool find_tile(const GemmArgs& p, int T, Tile& t) {
   const int shared_tiles = (T + BM - 1) / BM;
   int m = static_cast<int>(blockIdx.y);
   if (m < shared_tiles) {
-    seg = p.experts; mt = m; rows = T;
+    t = Tile{p.experts, m, T, 2 * T, 0};
     return true;
   }
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool mine = lane < p.experts;  // experts <= kMaxExperts < kWave
+  const int count = mine ? p.counts[lane] : 0;
+  const int hoff = mine ? p.offsets[lane] : 0;
+  const int ooff = mine ? p.offsets[p.experts + 1 + lane] : 0;
+  const int tiles = (count + BM - 1) / BM;
   m -= shared_tiles;
   for (int e = 0; e < p.experts; ++e) {
     const int te = __builtin_amdgcn_readlane(tiles, e);
     if (m < te) {
-      seg = e; mt = m; rows = __builtin_amdgcn_readlane(count, e);
+      t = Tile{e, m, __builtin_amdgcn_readlane(count, e), __builtin_amdgcn_readlane(hoff, e),
+               __builtin_amdgcn_readlane(ooff, e)};
       return true;
     }
     m -= te;
   }
   return false;
+}
+
+// Segment row of tile row r; padding rows past the segment's end clamp onto
+// the tile's first row (they are computed but never stored).
+__device__ __forceinline__ int segment_row(const Tile& t, int BM, int r) {
+  const int s = t.mt * BM + r;
+  return s < t.rows ? s : t.mt * BM;
+}
+
+// Assignment id of routed segment row s: in-capacity rows from the slot
+// map, the rest from the expert's part of the overflow list.
+__device__ __forceinline__ int assignment_of(const GemmArgs& p, const Tile& t, int s) {
+  return s < p.capacity ? p.perm[static_cast<int64_t>(t.seg) * p.capacity + s]
+                        : p.overflow[t.obase + s - p.capacity];
 }
 
 template <int BM>
@@ -165,9 +190,9 @@ void grouped_gemm_kernel(GemmArgs p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = static_cast<int>(p.tokens);
 
-  int seg = -1, mt = 0, rows = 0;
-  if (!find_tile<BM>(p, T, seg, mt, rows)) return;
-  const bool shared = seg == p.experts;
+  Tile t;
+  if (!find_tile<BM>(p, T, t)) return;
+  const bool shared = t.seg == p.experts;
   const int N = PHASE == 1 ? 2 * (shared ? p.shared_dim : p.hidden_dim) : p.dim;
   const int K = PHASE == 1 ? p.dim : (shared ? p.shared_dim : p.hidden_dim);
   const int n0 = static_cast<int>(blockIdx.x) * BN;
@@ -175,30 +200,20 @@ void grouped_gemm_kernel(GemmArgs p) {
   const int KT = K / 64;
 
   // ---- per-row source / destination ---------------------------------------
-  if (tid < BM) {
-    const int s = mt * BM + tid;
-    const bool valid = s < rows;
-    const int sc = valid ? s : mt * BM;  // clamp padding rows onto a real row
-    int tok, hrow, asg = -1;
-    if (shared) {
-      tok = sc;
-      hrow = 2 * T + sc;
-    } else {
-      asg = sc < p.capacity
-                ? p.perm[static_cast<int64_t>(seg) * p.capacity + sc]
-                : p.overflow[p.offsets[p.experts + 1 + seg] + sc - p.capacity];
-      tok = asg >> 1;
-      hrow = p.offsets[seg] + sc;
+  // Phase 1 gathers x rows by token (through the slot map) and writes hidden
+  // row hbase + s.  Phase 2 reads hidden row hbase + s, known without a load,
+  // so its A loads start at once; the assignment ids it scatters to are
+  // needed only by the epilogue.
+  const int sc = segment_row(t, BM, tid);
+  const int asg = tid < BM && !shared ? assignment_of(p, t, sc) : 0;
+  if (PHASE == 1) {
+    if (tid < BM) {
+      row_src[tid] = shared ? sc : asg >> 1;
+      row_dst[tid] = t.mt * BM + tid < t.rows ? t.hbase + sc : -1;
     }
-    if (PHASE == 1) {
-      row_src[tid] = tok;
-      row_dst[tid] = valid ? hrow : -1;
-    } else {
-      row_src[tid] = hrow;
-      row_dst[tid] = valid ? (shared ? tok : asg) : -1;
-    }
+    __syncthreads();
   }
-  __syncthreads();
+  asm volatile("" ::: "memory");  // issue the id loads before the A loads
 
   // ---- this lane's loads: one 16-byte piece of each of its P blocks -------
   const int a_ld = PHASE == 1 ? p.dim : p.hstride;
@@ -206,7 +221,7 @@ void grouped_gemm_kernel(GemmArgs p) {
   const __amdgpu_buffer_rsrc_t a_rsrc =
       make_rsrc(p.a_src, static_cast<uint32_t>(a_rows * a_ld * 2));
   const uint16_t* wbase = shared ? p.w_shared
-                                 : p.w_routed + static_cast<int64_t>(seg) * N * K;
+                                 : p.w_routed + static_cast<int64_t>(t.seg) * N * K;
   const __amdgpu_buffer_rsrc_t b_rsrc =
       make_rsrc(wbase, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
   const int ksteps32 = K / 32;
@@ -219,7 +234,8 @@ void grouped_gemm_kernel(GemmArgs p) {
     if (b < kABlocks) {
       // A block (m-tile b / 2, k half b % 2): row 16 (b / 2) + l % 16,
       // k 32 (b % 2) + 8 (l / 16); the stage adds 128 bytes of k.
-      const int r = row_src[(b >> 1) * 16 + (lane & 15)];
+      const int ar = (b >> 1) * 16 + (lane & 15);
+      const int r = PHASE == 1 ? row_src[ar] : t.hbase + segment_row(t, BM, ar);
       voff[i] = static_cast<uint32_t>(r * a_ld + (b & 1) * 32 + (lane >> 4) * 8) * 2;
     } else {
       // B block (group g, k half h) = packed block (n0 / 16 + g, 2 kt + h);
@@ -284,6 +300,12 @@ void grouped_gemm_kernel(GemmArgs p) {
   // refilled.
 #pragma unroll
   for (int st = 0; st < S - 1; ++st) issue(ring[st], st);
+  if (PHASE == 2) {
+    // The k loop's first barrier publishes these; wait for the LDS writes
+    // first, as that barrier is written out without one.
+    if (tid < BM) row_dst[tid] = t.mt * BM + tid < t.rows ? (shared ? sc : asg) : -1;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
   for (int kt = 0; kt < KT; ++kt) {
     wait_vm_barrier<P * (S - 2)>();
     issue(ring[(kt + S - 1) % S], kt + S - 1);
@@ -364,9 +386,9 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
   const int wave = tid >> 6;
   const int T = static_cast<int>(p.tokens);
 
-  int seg = -1, mt = 0, rows = 0;
-  if (!find_tile<BM>(p, T, seg, mt, rows)) return;
-  const bool shared = seg == p.experts;
+  Tile t;
+  if (!find_tile<BM>(p, T, t)) return;
+  const bool shared = t.seg == p.experts;
   const int N = PHASE == 1 ? 2 * (shared ? p.shared_dim : p.hidden_dim) : p.dim;
   const int K = PHASE == 1 ? p.dim : (shared ? p.shared_dim : p.hidden_dim);
   const int n0 = static_cast<int>(blockIdx.x) * BN;
@@ -378,7 +400,7 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
 
   // ---- B: first PF k steps of this lane's fragments -------------------------
   const uint16_t* wbase = shared ? p.w_shared
-                                 : p.w_routed + static_cast<int64_t>(seg) * N * K;
+                                 : p.w_routed + static_cast<int64_t>(t.seg) * N * K;
   const __amdgpu_buffer_rsrc_t b_rsrc =
       make_rsrc(wbase, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
   // Fragment order: the 1 KB block of (16-row group g, 32-k step) starts at
@@ -395,30 +417,21 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
     for (int j = 0; j < kTilesN; ++j)
       bq[i][j] = buffer_load16(b_rsrc, b_off[j], static_cast<uint32_t>(min(i, ksteps - 1)) * 1024);
 
-  if (tid < BM) {
-    const int s = mt * BM + tid;
-    const bool valid = s < rows;
-    const int sc = valid ? s : mt * BM;  // padding rows read a real row
-    int tok, hrow, asg = -1;
-    if (shared) {
-      tok = sc;
-      hrow = 2 * T + sc;
-    } else {
-      asg = sc < p.capacity
-                ? p.perm[static_cast<int64_t>(seg) * p.capacity + sc]
-                : p.overflow[p.offsets[p.experts + 1 + seg] + sc - p.capacity];
-      tok = asg >> 1;
-      hrow = p.offsets[seg] + sc;
+  // ---- per-row source / destination ---------------------------------------
+  // Phase 1 gathers x rows by token (through the slot map) and writes hidden
+  // row hbase + s.  Phase 2 reads hidden row hbase + s, known without a load,
+  // so its A gather starts at once; the assignment ids it scatters to are
+  // needed only by the epilogue and arrive meanwhile.
+  const int sc = segment_row(t, BM, tid);
+  const int asg = tid < BM && !shared ? assignment_of(p, t, sc) : 0;
+  if (PHASE == 1) {
+    if (tid < BM) {
+      row_src[tid] = shared ? sc : asg >> 1;
+      row_dst[tid] = t.mt * BM + tid < t.rows ? t.hbase + sc : -1;
     }
-    if (PHASE == 1) {
-      row_src[tid] = tok;
-      row_dst[tid] = valid ? hrow : -1;
-    } else {
-      row_src[tid] = hrow;
-      row_dst[tid] = valid ? (shared ? tok : asg) : -1;
-    }
+    __syncthreads();
   }
-  __syncthreads();
+  asm volatile("" ::: "memory");  // issue the id loads before the A gather
 
   // ---- A: the whole tile, direct to LDS ------------------------------------
   {
@@ -429,12 +442,39 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
       const int r = slot / chunks;
       const int pc = slot - r * chunks;
       const int c = (pc & ~swz) | ((pc ^ r) & swz);
-      const uint16_t* g = p.a_src + static_cast<int64_t>(row_src[r]) * a_ld + c * 8;
+      const int src = PHASE == 1 ? row_src[r] : t.hbase + segment_row(t, BM, r);
+      const uint16_t* g = p.a_src + static_cast<int64_t>(src) * a_ld + c * 8;
       __builtin_amdgcn_global_load_lds(g, (lds_void_t*)(a_lds + i * kWave * 8), 16, 0, 0);
     }
   }
+  if (PHASE == 2 && tid < BM) row_dst[tid] = t.mt * BM + tid < t.rows ? (shared ? sc : asg) : -1;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+
+  // This lane's output rows (C fragment rows 4 (lane / 16) + r of each
+  // 16-row tile), read once so the epilogue waits for no LDS read.
+  int dst_row[kTilesM][4];
+#pragma unroll
+  for (int mi = 0; mi < kTilesM; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst_row[mi][r] = row_dst[mi * 16 + 4 * (lane >> 4) + r];
+  // Phase 2, routed rows: their route weights, loaded inside the first k
+  // step, right after its weight refill.  Loads retire in order, so issued
+  // before the loop they would hold up its first MFMAs; issued there, the
+  // first wait that covers them comes PF steps later.
+  float route_w[kTilesM][4];
+#pragma unroll
+  for (int mi = 0; mi < kTilesM; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) route_w[mi][r] = 0.f;
+  auto load_route_weights = [&]() {
+    if (PHASE == 2 && !shared) {
+#pragma unroll
+      for (int mi = 0; mi < kTilesM; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) route_w[mi][r] = p.weights[max(dst_row[mi][r], 0)];
+    }
+  };
 
   f32x4 acc[kTilesM][kTilesN];
 #pragma unroll
@@ -463,6 +503,13 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
       const uint32_t next = static_cast<uint32_t>(min(step + PF, ksteps - 1)) * 1024;
 #pragma unroll
       for (int j = 0; j < kTilesN; ++j) bq[i][j] = buffer_load16(b_rsrc, b_off[j], next);
+      if (i == 0 && s0 == 0) load_route_weights();
+      // Keep the refill in its own step: left free, the scheduler sinks
+      // every refill to the end of the loop body, and the next pass's first
+      // MFMAs then wait on loads issued a few instructions earlier.  LDS
+      // reads and SALU work may still cross (mask 0x104), so the next
+      // step's A fragments are read while this step's MFMAs run.
+      __builtin_amdgcn_sched_barrier(0x104);
     }
   }
 
@@ -475,8 +522,7 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
       for (int mi = 0; mi < kTilesM; ++mi) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = mi * 16 + 4 * (lane >> 4) + r;
-          const int dst = row_dst[row];
+          const int dst = dst_row[mi][r];
           if (dst >= 0)
             p.hidden_out[static_cast<int64_t>(dst) * p.hstride + h] =
                 f32_to_bf16(swiglu(acc[mi][0][r], acc[mi][1][r]));
@@ -492,11 +538,10 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
       for (int mi = 0; mi < kTilesM; ++mi) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = mi * 16 + 4 * (lane >> 4) + r;
-          const int dst = row_dst[row];
+          const int dst = dst_row[mi][r];
           if (dst < 0) continue;
           if (shared) p.y_shared[static_cast<int64_t>(dst) * p.dim + n] = acc[mi][j][r];
-          else p.y_routed[static_cast<int64_t>(dst) * p.dim + n] = p.weights[dst] * acc[mi][j][r];
+          else p.y_routed[static_cast<int64_t>(dst) * p.dim + n] = route_w[mi][r] * acc[mi][j][r];
         }
       }
     }
