@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 4
+#define PARROT_ABI_VERSION 5
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -69,6 +69,27 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
                           const void* score_norm_weight, float score_eps,
                           const void* out_norm_weight, float out_eps, int64_t tokens,
                           int32_t dim, void* out_mix, void* out_norm, void* stream);
+
+/* parrot_depth_mix_bf16 (out_norm required) followed by the router of
+ * parrot_route_bf16 on the normalised rows, in one launch: writes
+ * out_weights fp32 [T, 2] and out_indices int64 [T, 2] exactly as
+ * parrot_route_bf16 does for x = out_norm below 16384 tokens (the same
+ * split-K logit arithmetic to the bit, the same top-2 and renormalised
+ * weights; from 16384 tokens parrot_route_bf16 sums each logit in one chain,
+ * so its logits may differ in the last bits).  No grouping outputs, no
+ * router stats.
+ * router_weight bf16 [E, dim], 16-byte aligned; logit_bias optional fp32 [E];
+ * 2 <= E <= 32; dim % 32 == 0, dim <= 2048.
+ * Replaces, for a MoE layer's input, metal_depth_mix_norm
+ * (parrot/metal_moe.py:455-477) followed by the router projection and top-2
+ * of metal_route (parrot/metal_moe.py:58-81; parrot/model.py:520-527). */
+int parrot_depth_mix_route_bf16(const void* const* sources, int32_t n_sources,
+                                const void* query, const void* score_norm_weight,
+                                float score_eps, const void* out_norm_weight, float out_eps,
+                                int64_t tokens, int32_t dim, void* out_mix, void* out_norm,
+                                const void* router_weight, const float* logit_bias,
+                                int32_t experts, float* out_weights, int64_t* out_indices,
+                                void* stream);
 
 /* parrot_experts_combine_bf16 folded into the next module's depth mix: the
  * combined MoE row out (bf16(addend + bf16(shared + routed rows)), exactly
@@ -382,6 +403,44 @@ int parrot_experts_down_bf16(int64_t tokens, int32_t dim, int32_t experts, int32
 int parrot_experts_combine_bf16(int64_t tokens, int32_t dim, int32_t hidden_dim,
                                 int32_t shared_dim, const void* addend, void* out,
                                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* 1 when parrot_experts_gate_up_grouping_bf16 supports this shape (the
+ * streaming kernel's shapes: 2T <= 2048 assignments, at most 96 rows per
+ * expert on average, dim, H, Hs <= 768), else 0. */
+int parrot_experts_group_in_kernel(int64_t tokens, int32_t dim, int32_t experts,
+                                   int32_t hidden_dim, int32_t shared_dim);
+
+/* parrot_group_indices and parrot_experts_gate_up_bf16 in one launch: the
+ * gate/up stage groups the top-2 indices int64 [T, 2] itself (stable slot
+ * order, as parrot_group_indices) and writes
+ *   out_counts  int32 [E], out_offsets int32 [2E + 2] (as parrot_route_bf16),
+ *   out_sorted  int32 [2T]  assignment id of each routed hidden row: the
+ *               expert-contiguous slot order, in-capacity slots then
+ *               overflow (out_sorted[offsets[e] + s] = slot s of expert e);
+ * positions / perm / overflow are not materialised.  Follow it with
+ * parrot_experts_down_sorted_bf16 and parrot_experts_combine_bf16 (or its
+ * depth-mix form) on the same workspace.  PARROT_ERR_UNSUPPORTED outside
+ * parrot_experts_group_in_kernel's shapes.
+ * Replaces moe_count_assignments (parrot/kernels/moe_bf16.metal:650-660) and
+ * the gate/up steps of grouped_mps_experts (parrot/metal_moe.py:384-408). */
+int parrot_experts_gate_up_grouping_bf16(const void* x, int64_t tokens, int32_t dim,
+                                         int32_t experts, int32_t hidden_dim,
+                                         int32_t shared_dim, int32_t capacity,
+                                         const int64_t* indices, int32_t* out_counts,
+                                         int32_t* out_offsets, int32_t* out_sorted,
+                                         const void* packed_gate_up, const void* shared_gate_up,
+                                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* parrot_experts_down_bf16 with the grouping written by
+ * parrot_experts_gate_up_grouping_bf16 (counts, offsets, sorted).
+ * Replaces the down steps of grouped_mps_experts
+ * (parrot/metal_moe.py:409-415). */
+int parrot_experts_down_sorted_bf16(int64_t tokens, int32_t dim, int32_t experts,
+                                    int32_t hidden_dim, int32_t shared_dim, int32_t capacity,
+                                    const int32_t* counts, const int32_t* offsets,
+                                    const int32_t* sorted, const float* route_weights,
+                                    const void* down, const void* shared_down, void* workspace,
+                                    size_t workspace_bytes, void* stream);
 
 /* Routed + shared SwiGLU experts and the weighted combine:
  *   out[t] = bf16(shared(x_t) + sum_k w[t,k] * expert_{i[t,k]}(x_t))

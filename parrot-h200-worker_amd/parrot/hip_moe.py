@@ -293,10 +293,14 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
     if cfg.top_k != 2 or experts > MAX_EXPERTS:
         raise RuntimeError(f"grouped HIP experts support top-2 of at most {MAX_EXPERTS} experts")
     flat = flat.contiguous()
+    self_group = False
     if grouping is None:
         cached = module.__dict__.get("_hip_grouping")
         if positions is not None and cached is not None and cached.positions is positions:
             grouping = cached
+        elif groups_in_kernel(module, tokens, dim):
+            # The gate/up launch groups the indices itself.
+            self_group = True
         else:
             # Slots are recomputed from the indices in the deterministic stable
             # order; the expert outputs do not depend on the slot order.
@@ -314,7 +318,7 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
     ws = _scratch(module, "_hip_experts_workspace", nbytes, flat.device)
     out = torch.empty_like(flat)
     stream = _stream(flat.device)
-    if then_mix is None:
+    if then_mix is None and not self_group:
         _abi.check(lib.parrot_grouped_experts_bf16(
             ptr(flat), tokens, dim, experts, cfg.expert_dim, cfg.shared_expert_dim,
             grouping.capacity, ptr(grouping.counts), ptr(grouping.offsets), ptr(grouping.perm),
@@ -322,15 +326,39 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
             ptr(shared_down), ptr(addend), ptr(out), ptr(ws), nbytes, stream),
             "parrot_grouped_experts_bf16")
         return out
-    group_args = (experts, cfg.expert_dim, cfg.shared_expert_dim, grouping.capacity,
-                  ptr(grouping.counts), ptr(grouping.offsets), ptr(grouping.perm),
-                  ptr(grouping.overflow))
-    _abi.check(lib.parrot_experts_gate_up_bf16(
-        ptr(flat), tokens, dim, *group_args, ptr(gate_up), ptr(shared_gate_up), ptr(ws), nbytes,
-        stream), "parrot_experts_gate_up_bf16")
-    _abi.check(lib.parrot_experts_down_bf16(
-        tokens, dim, *group_args, ptr(weights), ptr(down), ptr(shared_down), ptr(ws), nbytes,
-        stream), "parrot_experts_down_bf16")
+    if self_group:
+        if indices.dtype != torch.int64 or indices.numel() != 2 * tokens:
+            raise RuntimeError("top-2 indices must be int64 [tokens, 2]")
+        indices = indices.reshape(-1).contiguous()
+        cap = capacity(tokens, experts)
+        n = experts + (2 * experts + 2) + 2 * tokens
+        buf = _scratch(module, "_hip_group_buffers", 4 * n, flat.device)[:4 * n].view(torch.int32)
+        counts, offsets = buf[:experts], buf[experts:3 * experts + 2]
+        sorted_ids = buf[3 * experts + 2:]
+        shape = (experts, cfg.expert_dim, cfg.shared_expert_dim, cap)
+        _abi.check(lib.parrot_experts_gate_up_grouping_bf16(
+            ptr(flat), tokens, dim, *shape, ptr(indices), ptr(counts), ptr(offsets),
+            ptr(sorted_ids), ptr(gate_up), ptr(shared_gate_up), ptr(ws), nbytes, stream),
+            "parrot_experts_gate_up_grouping_bf16")
+        _abi.check(lib.parrot_experts_down_sorted_bf16(
+            tokens, dim, *shape, ptr(counts), ptr(offsets), ptr(sorted_ids), ptr(weights),
+            ptr(down), ptr(shared_down), ptr(ws), nbytes, stream),
+            "parrot_experts_down_sorted_bf16")
+    else:
+        group_args = (experts, cfg.expert_dim, cfg.shared_expert_dim, grouping.capacity,
+                      ptr(grouping.counts), ptr(grouping.offsets), ptr(grouping.perm),
+                      ptr(grouping.overflow))
+        _abi.check(lib.parrot_experts_gate_up_bf16(
+            ptr(flat), tokens, dim, *group_args, ptr(gate_up), ptr(shared_gate_up), ptr(ws),
+            nbytes, stream), "parrot_experts_gate_up_bf16")
+        _abi.check(lib.parrot_experts_down_bf16(
+            tokens, dim, *group_args, ptr(weights), ptr(down), ptr(shared_down), ptr(ws), nbytes,
+            stream), "parrot_experts_down_bf16")
+    if then_mix is None:
+        _abi.check(lib.parrot_experts_combine_bf16(
+            tokens, dim, cfg.expert_dim, cfg.shared_expert_dim, ptr(addend), ptr(out), ptr(ws),
+            nbytes, stream), "parrot_experts_combine_bf16")
+        return out
     depth, sources, output_norm = then_mix
     if len(sources) + 1 > MAX_DEPTH_SOURCES:
         raise RuntimeError(f"HIP depth mixing supports one to {MAX_DEPTH_SOURCES} sources")
@@ -349,6 +377,14 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
         float(output_norm.eps), None, ptr(mixed), stream), "parrot_experts_combine_depth_mix_bf16")
     del rows
     return out, mixed
+
+
+def groups_in_kernel(module: "MoE", tokens: int, dim: int) -> bool:
+    """Whether the gate/up launch groups the top-2 indices itself at this
+    size (no separate grouping pass; parrot_experts_group_in_kernel)."""
+    cfg = module.cfg
+    return bool(_abi.load().parrot_experts_group_in_kernel(
+        tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim))
 
 
 DECODE_MAX_TOKENS = 16  # rows the fused decode MoE takes
@@ -786,7 +822,7 @@ def rms_norm(module, x: Tensor) -> Tensor:
 _SourceArray = ctypes.c_void_p * MAX_DEPTH_SOURCES
 
 
-def _depth(module, sources: list[Tensor], output_norm) -> Tensor:
+def _depth(module, sources: list[Tensor], output_norm, router=None, logit_bias=None):
     if not 1 <= len(sources) <= MAX_DEPTH_SOURCES:
         raise RuntimeError(f"HIP depth mixing supports one to {MAX_DEPTH_SOURCES} sources")
     first = sources[0]
@@ -802,16 +838,30 @@ def _depth(module, sources: list[Tensor], output_norm) -> Tensor:
                            [flat[0].data_ptr()] * (MAX_DEPTH_SOURCES - len(flat))))
     out = torch.empty_like(flat[0])
     norm_w = None if output_norm is None else output_norm.weight
-    _abi.check(_abi.load().parrot_depth_mix_bf16(
-        ctypes.cast(array, ctypes.c_void_p), len(flat), ptr(module.query),
-        ptr(module.norm.weight), float(module.norm.eps), ptr(norm_w),
-        0.0 if output_norm is None else float(output_norm.eps), tokens, dim,
-        ptr(out) if output_norm is None else None,
-        None if output_norm is None else ptr(out), _stream(first.device)),
-        "parrot_depth_mix_bf16")
-    # Keep the source tensors alive until the kernel is enqueued (it is).
+    mix_args = (ctypes.cast(array, ctypes.c_void_p), len(flat), ptr(module.query),
+                ptr(module.norm.weight), float(module.norm.eps), ptr(norm_w),
+                0.0 if output_norm is None else float(output_norm.eps), tokens, dim,
+                ptr(out) if output_norm is None else None,
+                None if output_norm is None else ptr(out))
+    lib = _abi.load()
+    if router is None:
+        _abi.check(lib.parrot_depth_mix_bf16(*mix_args, _stream(first.device)),
+                   "parrot_depth_mix_bf16")
+        del flat  # the sources stay alive until the kernel is enqueued (it is)
+        return out
+    cfg = router.cfg
+    router_w = router.router.weight
+    if router_w.dtype != first.dtype or not router_w.is_contiguous():
+        raise RuntimeError("router weight must be contiguous and match the input dtype")
+    weights = torch.empty((tokens, 2), dtype=torch.float32, device=first.device)
+    indices = torch.empty((tokens, 2), dtype=torch.int64, device=first.device)
+    if logit_bias is not None:
+        logit_bias = logit_bias.to(device=first.device, dtype=torch.float32).contiguous()
+    _abi.check(lib.parrot_depth_mix_route_bf16(
+        *mix_args, ptr(router_w), ptr(logit_bias), cfg.n_experts, ptr(weights), ptr(indices),
+        _stream(first.device)), "parrot_depth_mix_route_bf16")
     del flat
-    return out
+    return out, RouteResult(None, weights, indices, None)
 
 
 def depth_mix(module, sources: list[Tensor]) -> Tensor:
@@ -823,3 +873,14 @@ def depth_mix_norm(module, sources: list[Tensor], output_norm) -> Tensor:
     """Depth mix rounded to bf16, then the consumer RMSNorm, in one kernel
     (cf. metal_depth_mix_norm, for every token count)."""
     return _depth(module, sources, output_norm)
+
+
+def depth_mix_norm_route(module, sources: list[Tensor], output_norm, moe: "MoE",
+                         logit_bias: Tensor | None = None) -> tuple[Tensor, RouteResult]:
+    """``depth_mix_norm`` of a MoE layer's input plus that layer's router
+    top-2 on the result, in one kernel: below 16384 tokens the weights and
+    indices equal ``route(moe, result)``'s bit for bit (no grouping, no
+    router stats)."""
+    if moe.cfg.top_k != 2 or moe.cfg.n_experts > MAX_EXPERTS:
+        raise RuntimeError(f"HIP routing supports top-2 of at most {MAX_EXPERTS} experts")
+    return _depth(module, sources, output_norm, router=moe, logit_bias=logit_bias)

@@ -116,10 +116,11 @@ int parrot_rms_norm_bf16(const void* x, const void* weight, void* out, int64_t r
                                         as_stream(stream)));
 }
 
-int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const void* query,
-                          const void* score_norm_weight, float score_eps,
-                          const void* out_norm_weight, float out_eps, int64_t tokens,
-                          int32_t dim, void* out_mix, void* out_norm, void* stream) {
+static int depth_mix_entry(const void* const* sources, int32_t n_sources, const void* query,
+                           const void* score_norm_weight, float score_eps,
+                           const void* out_norm_weight, float out_eps, int64_t tokens,
+                           int32_t dim, void* out_mix, void* out_norm,
+                           const parrot::RouteOut* route, void* stream) {
   if (!sources || !query || !score_norm_weight) return PARROT_ERR_NULL_POINTER;
   if (!out_mix && !out_norm) return PARROT_ERR_NULL_POINTER;
   if (out_norm && !out_norm_weight) return PARROT_ERR_NULL_POINTER;
@@ -142,8 +143,35 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
       srcs, n_sources, static_cast<const uint16_t*>(query),
       static_cast<const uint16_t*>(score_norm_weight), score_eps,
       static_cast<const uint16_t*>(out_norm_weight), out_eps, tokens, dim,
-      static_cast<uint16_t*>(out_mix), static_cast<uint16_t*>(out_norm), nullptr,
+      static_cast<uint16_t*>(out_mix), static_cast<uint16_t*>(out_norm), nullptr, route,
       as_stream(stream)));
+}
+
+int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const void* query,
+                          const void* score_norm_weight, float score_eps,
+                          const void* out_norm_weight, float out_eps, int64_t tokens,
+                          int32_t dim, void* out_mix, void* out_norm, void* stream) {
+  return depth_mix_entry(sources, n_sources, query, score_norm_weight, score_eps,
+                         out_norm_weight, out_eps, tokens, dim, out_mix, out_norm, nullptr,
+                         stream);
+}
+
+int parrot_depth_mix_route_bf16(const void* const* sources, int32_t n_sources,
+                                const void* query, const void* score_norm_weight,
+                                float score_eps, const void* out_norm_weight, float out_eps,
+                                int64_t tokens, int32_t dim, void* out_mix, void* out_norm,
+                                const void* router_weight, const float* logit_bias,
+                                int32_t experts, float* out_weights, int64_t* out_indices,
+                                void* stream) {
+  if (!out_norm || !router_weight || !out_weights || !out_indices) return PARROT_ERR_NULL_POINTER;
+  if (experts < 2 || experts > kMaxExperts) return PARROT_ERR_UNSUPPORTED;
+  if (dim % 32) return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(router_weight)) return PARROT_ERR_ALIGNMENT;
+  const parrot::RouteOut route{static_cast<const uint16_t*>(router_weight), logit_bias, experts,
+                               out_weights, out_indices};
+  return depth_mix_entry(sources, n_sources, query, score_norm_weight, score_eps,
+                         out_norm_weight, out_eps, tokens, dim, out_mix, out_norm, &route,
+                         stream);
 }
 
 int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* sin_table,
@@ -306,6 +334,18 @@ struct ExpertsCall {
 
 // Validation shared by the expert entry points; weights / map pointers a
 // stage does not read may be NULL (need_* = false).
+int check_experts_shape(int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
+                        int32_t shared_dim, int32_t capacity, void* workspace,
+                        size_t workspace_bytes, ExpertsWorkspace* ws) {
+  if (int rc = check_route_shape(tokens, experts, capacity)) return rc;
+  if (dim <= 0 || hidden_dim <= 0 || shared_dim <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (dim % 64 || hidden_dim % 64 || shared_dim % 64) return PARROT_ERR_UNSUPPORTED;
+  *ws = experts_ws(workspace, tokens, dim, hidden_dim, shared_dim);
+  if (!workspace || workspace_bytes < ws->bytes) return PARROT_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return PARROT_ERR_ALIGNMENT;
+  return PARROT_OK;
+}
+
 int check_experts(int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
                   int32_t shared_dim, int32_t capacity, const int32_t* counts,
                   const int32_t* offsets, const int32_t* perm, const int32_t* overflow,
@@ -344,6 +384,67 @@ int parrot_experts_gate_up_bf16(const void* x, int64_t tokens, int32_t dim, int3
                                            experts, hidden_dim, shared_dim, capacity, map, w,
                                            ws.hidden, ws.y_routed, ws.y_shared,
                                            as_stream(stream)));
+}
+
+int parrot_experts_group_in_kernel(int64_t tokens, int32_t dim, int32_t experts,
+                                   int32_t hidden_dim, int32_t shared_dim) {
+  if (experts < 2 || experts > kMaxExperts || dim <= 0 || hidden_dim <= 0 || shared_dim <= 0)
+    return 0;
+  return parrot::experts_group_in_kernel(tokens, dim, experts, hidden_dim, shared_dim) ? 1 : 0;
+}
+
+int parrot_experts_gate_up_grouping_bf16(const void* x, int64_t tokens, int32_t dim,
+                                         int32_t experts, int32_t hidden_dim,
+                                         int32_t shared_dim, int32_t capacity,
+                                         const int64_t* indices, int32_t* out_counts,
+                                         int32_t* out_offsets, int32_t* out_sorted,
+                                         const void* packed_gate_up, const void* shared_gate_up,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (!x || !indices || !out_counts || !out_offsets || !out_sorted || !packed_gate_up ||
+      !shared_gate_up)
+    return PARROT_ERR_NULL_POINTER;
+  ExpertsWorkspace ws;
+  if (int rc = check_experts_shape(tokens, dim, experts, hidden_dim, shared_dim, capacity,
+                                   workspace, workspace_bytes, &ws))
+    return rc;
+  if (tokens == 0) return PARROT_OK;
+  if (!parrot::experts_group_in_kernel(tokens, dim, experts, hidden_dim, shared_dim))
+    return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(packed_gate_up) || !aligned16(shared_gate_up))
+    return PARROT_ERR_ALIGNMENT;
+  parrot::GroupMap map{nullptr, nullptr, nullptr, nullptr, nullptr};
+  map.indices = indices;
+  map.counts_out = out_counts;
+  map.offsets_out = out_offsets;
+  map.sorted_out = out_sorted;
+  parrot::ExpertWeights w{static_cast<const uint16_t*>(packed_gate_up), nullptr,
+                          static_cast<const uint16_t*>(shared_gate_up), nullptr};
+  return status(parrot::launch_expert_gemm(1, static_cast<const uint16_t*>(x), tokens, dim,
+                                           experts, hidden_dim, shared_dim, capacity, map, w,
+                                           ws.hidden, ws.y_routed, ws.y_shared,
+                                           as_stream(stream)));
+}
+
+int parrot_experts_down_sorted_bf16(int64_t tokens, int32_t dim, int32_t experts,
+                                    int32_t hidden_dim, int32_t shared_dim, int32_t capacity,
+                                    const int32_t* counts, const int32_t* offsets,
+                                    const int32_t* sorted, const float* route_weights,
+                                    const void* down, const void* shared_down, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  if (!counts || !offsets || !sorted || !route_weights || !down || !shared_down)
+    return PARROT_ERR_NULL_POINTER;
+  ExpertsWorkspace ws;
+  if (int rc = check_experts_shape(tokens, dim, experts, hidden_dim, shared_dim, capacity,
+                                   workspace, workspace_bytes, &ws))
+    return rc;
+  if (!aligned16(down) || !aligned16(shared_down)) return PARROT_ERR_ALIGNMENT;
+  parrot::GroupMap map{counts, offsets, nullptr, nullptr, route_weights};
+  map.sorted = sorted;
+  parrot::ExpertWeights w{nullptr, static_cast<const uint16_t*>(down), nullptr,
+                          static_cast<const uint16_t*>(shared_down)};
+  return status(parrot::launch_expert_gemm(2, nullptr, tokens, dim, experts, hidden_dim,
+                                           shared_dim, capacity, map, w, ws.hidden, ws.y_routed,
+                                           ws.y_shared, as_stream(stream)));
 }
 
 int parrot_experts_down_bf16(int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
@@ -417,7 +518,7 @@ int parrot_experts_combine_depth_mix_bf16(
       srcs, n_sources, static_cast<const uint16_t*>(query),
       static_cast<const uint16_t*>(score_norm_weight), score_eps,
       static_cast<const uint16_t*>(out_norm_weight), out_eps, tokens, dim,
-      static_cast<uint16_t*>(out_mix), static_cast<uint16_t*>(out_norm), &comb,
+      static_cast<uint16_t*>(out_mix), static_cast<uint16_t*>(out_norm), &comb, nullptr,
       as_stream(stream)));
 }
 

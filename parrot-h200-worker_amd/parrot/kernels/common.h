@@ -184,6 +184,46 @@ __device__ __forceinline__ void row_top2(float l0, float l1, int experts, int& f
   runner_logit = key_value(runner);
 }
 
+// Top-2 of the token whose logits lane j of this DPP row holds for experts
+// j (l0) and j + 16 (l1; ignored unless experts > 16), route weights
+// renormalised over the two selected exponentials, and the optional logits
+// and probabilities.  Every lane of the row calls it; lane 0 of the row
+// writes the per-token outputs and returns the two ids in `ids`.
+__device__ __forceinline__ void select_top2(float l0, float l1, int experts, int64_t t,
+                                            bool valid, float* out_logits, float* probs,
+                                            float* weights, int64_t* indices, int* ids) {
+  const int j = threadIdx.x & 15;
+  const bool has0 = j < experts, has1 = j + 16 < experts;
+  int first, second;
+  float vb, vr;
+  row_top2(l0, l1, experts, first, second, vb, vr);
+  if (valid) {
+    if (out_logits != nullptr) {
+      if (has0) out_logits[t * experts + j] = l0;
+      if (has1) out_logits[t * experts + j + 16] = l1;
+    }
+    if (probs != nullptr) {
+      const float p0 = has0 ? __expf(l0 - vb) : 0.0f;
+      const float p1 = has1 ? __expf(l1 - vb) : 0.0f;
+      const float inv = 1.0f / row_sum(p0 + p1);
+      if (has0) probs[t * experts + j] = p0 * inv;
+      if (has1) probs[t * experts + j + 16] = p1 * inv;
+    }
+  }
+  if (j == 0) {
+    if (valid) {
+      const float e2 = __expf(vr - vb);
+      const float sel = 1.0f + e2;
+      indices[2 * t] = first;
+      indices[2 * t + 1] = second;
+      weights[2 * t] = 1.0f / sel;
+      weights[2 * t + 1] = e2 / sel;
+    }
+    ids[0] = valid ? first : -1;
+    ids[1] = valid ? second : -1;
+  }
+}
+
 // silu(g) * u with silu(g) = g / (1 + e^-g), evaluated in fp32.
 __device__ __forceinline__ float swiglu(float g, float u) {
   return (g / (1.0f + __expf(-g))) * u;
@@ -211,13 +251,24 @@ struct CombineSource {
   uint16_t* out;           // [T, dim]
 };
 
-// comb: optional (nullptr: every source is read from srcs).
+// Router top-2 computed inside the depth mix whose normalised output is the
+// MoE input (route_kernel's results, bit for bit).
+struct RouteOut {
+  const uint16_t* router_w;  // [E, dim]
+  const float* bias;         // optional [E]
+  int experts;
+  float* weights;            // [T, 2]
+  int64_t* indices;          // [T, 2]
+};
+
+// comb: optional (nullptr: every source is read from srcs).  route:
+// optional; needs out_norm.
 hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
                             const uint16_t* query, const uint16_t* score_w,
                             float score_eps, const uint16_t* out_norm_w,
                             float out_eps, int64_t tokens, int dim,
                             uint16_t* out_mix, uint16_t* out_norm, const CombineSource* comb,
-                            hipStream_t s);
+                            const RouteOut* route, hipStream_t s);
 
 // Routing: router projection (or given fp32 logits) + top-2 + per-block
 // stable ranks.  Writes block-local ranks into `positions` and per-block
@@ -264,7 +315,21 @@ struct GroupMap {
   const int32_t* perm;      // [E, C]
   const int32_t* overflow;  // [2T]
   const float* weights;     // [2T] route weights
+  // Grouping inside the gate/up launch (experts_group_in_kernel): phase 1
+  // reads the top-2 `indices` instead of counts / offsets / perm / overflow
+  // and writes `counts_out`, `offsets_out` and `sorted` (the assignment id of
+  // each hidden row); phase 2 then reads counts / offsets / sorted.
+  const int64_t* indices = nullptr;  // [2T]
+  int32_t* counts_out = nullptr;     // [E]
+  int32_t* offsets_out = nullptr;    // [2E+2]
+  const int32_t* sorted = nullptr;   // [2T], phase 2
+  int32_t* sorted_out = nullptr;     // [2T], phase 1
 };
+
+// Whether a gate/up launch can group its assignments itself (the streaming
+// kernel's shapes, at most 2048 assignments).
+bool experts_group_in_kernel(int64_t tokens, int dim, int experts, int hidden_dim,
+                             int shared_dim);
 
 // Grouped SwiGLU expert GEMM over every routed assignment plus the shared
 // expert.  Phase 1 (gate/up + SwiGLU) reads x and writes hidden

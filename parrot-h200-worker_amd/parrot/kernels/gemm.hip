@@ -43,6 +43,14 @@ struct GemmArgs {
   uint16_t* hidden_out;       // phase 1 output
   float* y_routed;            // phase 2 output [2T, dim]
   float* y_shared;            // phase 2 output [T, dim]
+  // Grouping inside phase 1 (group_find, group_rows): top-2 ids in; counts,
+  // offsets and the hidden rows' assignment ids out.  Phase 2 with `sorted`
+  // reads a row's assignment id there instead of perm / overflow.
+  const int64_t* indices;
+  int32_t* counts_out;
+  int32_t* offsets_out;
+  int32_t* sorted_out;
+  const int32_t* sorted;
 };
 
 // The row tile a workgroup owns: segment `seg` (E = the shared expert),
@@ -84,6 +92,16 @@ __device__ __forceinline__ bool find_tile(const GemmArgs& p, int T, Tile& t) {
   return false;
 }
 
+// The tile's fields are wavefront-uniform by construction; readfirstlane
+// lets the compiler see it, so the weight buffer descriptor built from them
+// stays in SGPRs (a descriptor it cannot prove uniform costs a readfirstlane
+// loop around every buffer load).
+__device__ __forceinline__ Tile uniform_tile(const Tile& t) {
+  return Tile{__builtin_amdgcn_readfirstlane(t.seg), __builtin_amdgcn_readfirstlane(t.mt),
+              __builtin_amdgcn_readfirstlane(t.rows), __builtin_amdgcn_readfirstlane(t.hbase),
+              __builtin_amdgcn_readfirstlane(t.obase)};
+}
+
 // Segment row of tile row r; padding rows past the segment's end clamp onto
 // the tile's first row (they are computed but never stored).
 __device__ __forceinline__ int segment_row(const Tile& t, int BM, int r) {
@@ -92,10 +110,153 @@ __device__ __forceinline__ int segment_row(const Tile& t, int BM, int r) {
 }
 
 // Assignment id of routed segment row s: in-capacity rows from the slot
-// map, the rest from the expert's part of the overflow list.
+// map, the rest from the expert's part of the overflow list (or, after a
+// phase 1 that grouped in-kernel, the hidden rows' id list).
 __device__ __forceinline__ int assignment_of(const GemmArgs& p, const Tile& t, int s) {
+  if (p.sorted != nullptr) return p.sorted[t.hbase + s];
   return s < p.capacity ? p.perm[static_cast<int64_t>(t.seg) * p.capacity + s]
                         : p.overflow[t.obase + s - p.capacity];
+}
+
+// ---------------------------------------------------------------------------
+// Grouping inside the gate/up launch, for up to kGroupMaxAssign assignments:
+// the tile, its rows and the grouping outputs straight from the top-2 ids,
+// with the same results as the route + group kernels (stable slot order:
+// segment row s of expert e is e's assignment of rank s in ascending
+// assignment order, in-capacity slots then overflow; ids outside
+// [0, experts) take no row).  Every routed workgroup
+//   1. (group_find) loads all 2T ids (one memory hop; wavefront w owns the
+//      64-id chunks w, w + 4, ...), histograms them with LDS atomics (one
+//      histogram per wavefront), and finds its tile from prefix sums of the
+//      counts over lanes;
+//   2. (group_rows, once its weight loads are in flight) ranks its expert's
+//      ids: a ballot per chunk gives the chunk's count (exchanged through
+//      LDS, prefix-summed over lanes) and each id's rank within the chunk
+//      (mbcnt).
+// Rows of the tile land in row_src (token) / row_dst (hidden row); padding
+// rows read token 0 and store nothing.  The workgroup of the first routed
+// tile row, column 0, writes counts and both offset tables; column-0
+// workgroups write the hidden rows' assignment ids.
+constexpr int kGroupChunksPerWave = 8;
+constexpr int kGroupMaxAssign = 4 * kGroupChunksPerWave * kWave;  // 2048
+
+// Inclusive prefix sum over lanes 0-31 (lanes 32-63: unspecified): row
+// shifts by 1, 2, 4, 8 within each 16-lane row, then lane 15 broadcast into
+// the second row.  Lanes shifted in from outside a row add 0.
+__device__ __forceinline__ int scan32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  return v;
+}
+
+struct GroupIds {
+  int ids[kGroupChunksPerWave];  // this lane's ids, chunk w + 4 j (-1: none)
+};
+
+template <int BM>
+__device__ __forceinline__ bool group_find(const GemmArgs& p, int T, Tile& t, GroupIds& g,
+                                           int* row_src, int* row_dst,
+                                           int (*hist_s)[kMaxExperts]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int shared_tiles = (T + BM - 1) / BM;
+  int m = static_cast<int>(blockIdx.y);
+  if (m < shared_tiles) {
+    t = Tile{p.experts, m, T, 2 * T, 0};
+    return true;
+  }
+  const int E = p.experts;
+  const int n_assign = 2 * T;
+#pragma unroll
+  for (int j = 0; j < kGroupChunksPerWave; ++j) {
+    const int a = (wave + 4 * j) * kWave + lane;
+    const int64_t e = a < n_assign ? p.indices[a] : -1;
+    g.ids[j] = e >= 0 && e < E ? static_cast<int>(e) : -1;
+  }
+  // One histogram per wavefront: its zeroing and its atomics are one
+  // wavefront's LDS operations, which execute in order.
+  if (lane < kMaxExperts) hist_s[wave][lane] = 0;
+#pragma unroll
+  for (int j = 0; j < kGroupChunksPerWave; ++j)
+    if (g.ids[j] >= 0) atomicAdd(&hist_s[wave][g.ids[j]], 1);
+  if (tid < BM) {
+    row_src[tid] = 0;
+    row_dst[tid] = -1;
+  }
+  __syncthreads();
+
+  // Lane e: expert e's count, its tiles and its overflow rows, and their
+  // exclusive prefixes over the experts before it.
+  const int count =
+      lane < E ? hist_s[0][lane] + hist_s[1][lane] + hist_s[2][lane] + hist_s[3][lane] : 0;
+  const int tiles = (count + BM - 1) / BM;
+  const int ovf = max(0, count - p.capacity);
+  const int tile0 = scan32(tiles) - tiles;
+  const int h_end = scan32(count);
+  const int o_end = scan32(ovf);
+  m -= shared_tiles;
+  if (blockIdx.x == 0 && m == 0 && wave == 0) {
+    const int h_total = __builtin_amdgcn_readlane(h_end, E - 1);
+    const int o_total = __builtin_amdgcn_readlane(o_end, E - 1);
+    if (lane < E) {
+      p.counts_out[lane] = count;
+      p.offsets_out[lane] = h_end - count;
+      p.offsets_out[E + 1 + lane] = o_end - ovf;
+    }
+    if (lane == E) {
+      p.offsets_out[E] = h_total;
+      p.offsets_out[2 * E + 1] = o_total;
+    }
+  }
+  const uint64_t hit = __ballot(lane < E && m >= tile0 && m < tile0 + tiles);
+  if (hit == 0) return false;  // uniform: no tile for this workgroup
+  const int seg = static_cast<int>(__builtin_ctzll(hit));
+  t = Tile{seg, m - __builtin_amdgcn_readlane(tile0, seg), __builtin_amdgcn_readlane(count, seg),
+           __builtin_amdgcn_readlane(h_end - count, seg),
+           __builtin_amdgcn_readlane(o_end - ovf, seg)};
+  return true;
+}
+
+template <int BM>
+__device__ __forceinline__ void group_rows(const GemmArgs& p, int T, const Tile& t,
+                                           const GroupIds& g, int* row_src, int* row_dst,
+                                           int* chunk_s) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nchunks = (2 * T + kWave - 1) / kWave;
+  uint64_t mask[kGroupChunksPerWave];
+#pragma unroll
+  for (int j = 0; j < kGroupChunksPerWave; ++j) {
+    mask[j] = __ballot(g.ids[j] == t.seg);
+    const int c = wave + 4 * j;
+    if (lane == 0 && c < nchunks) chunk_s[c] = __popcll(mask[j]);
+  }
+  __syncthreads();
+  // Lane c: the expert's ids in chunks before c.
+  const int per_chunk = lane < nchunks ? chunk_s[lane] : 0;
+  const int before = scan32(per_chunk) - per_chunk;
+#pragma unroll
+  for (int j = 0; j < kGroupChunksPerWave; ++j) {
+    const int c = wave + 4 * j;
+    if (c < nchunks && g.ids[j] == t.seg) {
+      const uint64_t mk = mask[j];
+      const int rank = __builtin_amdgcn_readlane(before, c) +
+                       static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                           static_cast<uint32_t>(mk >> 32),
+                           __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mk), 0u)));
+      const int r = rank - t.mt * BM;
+      if (r >= 0 && r < BM) {
+        const int a = c * kWave + lane;
+        row_src[r] = a >> 1;
+        row_dst[r] = t.hbase + rank;
+        if (blockIdx.x == 0) p.sorted_out[t.hbase + rank] = a;
+      }
+    }
+  }
 }
 
 template <int BM>
@@ -380,14 +541,24 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t a_lds[BM * kStreamKCap];
   __shared__ int row_src[BM];
   __shared__ int row_dst[BM];
+  __shared__ int hist_s[4][kMaxExperts];
+  __shared__ int chunk_s[kGroupMaxAssign / kWave];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
   const int T = static_cast<int>(p.tokens);
 
+  // Phase 1 groups in-kernel when given the top-2 ids (uniform per launch).
+  const bool self_grouped = PHASE == 1 && p.indices != nullptr;
   Tile t;
-  if (!find_tile<BM>(p, T, t)) return;
+  GroupIds gids;
+  if (self_grouped) {
+    if (!group_find<BM>(p, T, t, gids, row_src, row_dst, hist_s)) return;
+  } else if (!find_tile<BM>(p, T, t)) {
+    return;
+  }
+  t = uniform_tile(t);
   const bool shared = t.seg == p.experts;
   const int N = PHASE == 1 ? 2 * (shared ? p.shared_dim : p.hidden_dim) : p.dim;
   const int K = PHASE == 1 ? p.dim : (shared ? p.shared_dim : p.hidden_dim);
@@ -397,6 +568,16 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
   const int chunks = K / 8;                       // 16-byte chunks per A row
   const int swz = (chunks & 15) == 0 ? 15 : 7;   // XOR group size - 1
   const int ksteps = K / 32;
+
+  // ---- row ids: issued first, so waiting for them waits for no weight load
+  // Phase 1 gathers x rows by token (through the slot map) and writes hidden
+  // row hbase + s.  Phase 2 reads hidden row hbase + s, known without a load,
+  // so its A gather starts at once; the assignment ids it scatters to are
+  // needed only by the epilogue and arrive meanwhile.  With self_grouped,
+  // group_rows places the routed rows instead.
+  const int sc = segment_row(t, BM, tid);
+  const int asg = tid < BM && !shared && !self_grouped ? assignment_of(p, t, sc) : 0;
+  asm volatile("" ::: "memory");  // issue the id loads before the weight loads
 
   // ---- B: first PF k steps of this lane's fragments -------------------------
   const uint16_t* wbase = shared ? p.w_shared
@@ -417,21 +598,15 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
     for (int j = 0; j < kTilesN; ++j)
       bq[i][j] = buffer_load16(b_rsrc, b_off[j], static_cast<uint32_t>(min(i, ksteps - 1)) * 1024);
 
-  // ---- per-row source / destination ---------------------------------------
-  // Phase 1 gathers x rows by token (through the slot map) and writes hidden
-  // row hbase + s.  Phase 2 reads hidden row hbase + s, known without a load,
-  // so its A gather starts at once; the assignment ids it scatters to are
-  // needed only by the epilogue and arrive meanwhile.
-  const int sc = segment_row(t, BM, tid);
-  const int asg = tid < BM && !shared ? assignment_of(p, t, sc) : 0;
+  // ---- per-row source / destination (the weight loads are in flight) -------
+  if (self_grouped && !shared) group_rows<BM>(p, T, t, gids, row_src, row_dst, chunk_s);
   if (PHASE == 1) {
-    if (tid < BM) {
+    if (tid < BM && (shared || !self_grouped)) {
       row_src[tid] = shared ? sc : asg >> 1;
       row_dst[tid] = t.mt * BM + tid < t.rows ? t.hbase + sc : -1;
     }
     __syncthreads();
   }
-  asm volatile("" ::: "memory");  // issue the id loads before the A gather
 
   // ---- A: the whole tile, direct to LDS ------------------------------------
   {
@@ -642,6 +817,13 @@ TilePlan experts_tile_plan(int64_t tokens, int experts) {
 
 }  // namespace
 
+bool experts_group_in_kernel(int64_t tokens, int dim, int experts, int hidden_dim,
+                             int shared_dim) {
+  if (tokens < 1 || 2 * tokens > kGroupMaxAssign || experts > kMaxExperts) return false;
+  if (experts_tile_plan(tokens, experts) == TilePlan::kTiled64) return false;
+  return dim <= kStreamKCap && max(hidden_dim, shared_dim) <= kStreamKCap;
+}
+
 hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int dim,
                               int experts, int hidden_dim, int shared_dim, int capacity,
                               const GroupMap& map, const ExpertWeights& w, uint16_t* hidden,
@@ -663,6 +845,15 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
   args.weights = map.weights;
   args.y_routed = y_routed;
   args.y_shared = y_shared;
+  args.sorted = phase == 2 ? map.sorted : nullptr;
+  if (phase == 1 && map.indices != nullptr) {
+    if (!experts_group_in_kernel(tokens, dim, experts, hidden_dim, shared_dim))
+      return hipErrorInvalidValue;
+    args.indices = map.indices;
+    args.counts_out = map.counts_out;
+    args.offsets_out = map.offsets_out;
+    args.sorted_out = map.sorted_out;
+  }
   switch (experts_tile_plan(tokens, experts)) {
     case TilePlan::kStream16: return run_phase<TilePlan::kStream16>(phase, args, w, hidden, s);
     case TilePlan::kStream32: return run_phase<TilePlan::kStream32>(phase, args, w, hidden, s);

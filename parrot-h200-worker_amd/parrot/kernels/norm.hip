@@ -65,11 +65,26 @@ __global__ __launch_bounds__(64) void rms_norm_kernel(
 constexpr int kDepthDimsPerWave = 256;
 constexpr int kDepthMaxWaves = 8;  // dim <= 2048
 
+// With ROUTE > 0 the kernel also routes the token's normalised row (the MoE
+// input) to its top-2 experts, with route_kernel's arithmetic to the bit:
+// the logits are the same v_mfma_f32_16x16x32_bf16 chains over the 32-wide
+// k steps st = c, c + 4, c + 8, ... for c = 0..3 (the token in A row 0, rows
+// 1-15 zero: an MFMA output element depends only on its own row and column),
+// summed ((c0 + c1) + c2) + c3, plus the bias; then select_top2.  ROUTE is
+// the number of 16-expert tiles (1: E <= 16, 2: E <= 32).  Chain c runs on
+// wavefront c % waves; the router weights of a wavefront's first two chains
+// (six k steps each: dim 768) are loaded with the sources, the rest in the
+// chain itself.
+constexpr int kRouteChainSlots = 2;
+constexpr int kRouteStepSlots = 6;
+
+template <int ROUTE>
 __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     DepthSources srcs, int n_sources, const uint16_t* __restrict__ query,
     const uint16_t* __restrict__ score_w, float score_eps,
     const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
-    uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm, CombineSource comb) {
+    uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm, CombineSource comb,
+    RouteOut route) {
   __shared__ float part[kDepthMaxWaves][2 * kMaxDepthSources];
   __shared__ float part_out[kDepthMaxWaves];
   const int lane = threadIdx.x & (kWave - 1);
@@ -111,6 +126,27 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
 #pragma unroll
     for (int s = 0; s < kMaxDepthSources; ++s)
       if (s == n_sources - 1) v[s] = o;
+  }
+  // Router weights of this wavefront's first chains (ROUTE > 0).
+  const int steps = dim / 32;
+  const int koff = (lane >> 4) * 8;
+  const uint16_t* pb[2] = {nullptr, nullptr};
+  bf16x8 rb[kRouteChainSlots][kRouteStepSlots][ROUTE > 0 ? ROUTE : 1];
+  if constexpr (ROUTE > 0) {
+#pragma unroll
+    for (int h = 0; h < ROUTE; ++h)
+      pb[h] = route.router_w +
+              static_cast<int64_t>(min(16 * h + (lane & 15), route.experts - 1)) * dim + koff;
+#pragma unroll
+    for (int j = 0; j < kRouteChainSlots; ++j)
+#pragma unroll
+      for (int i = 0; i < kRouteStepSlots; ++i) {
+        const int c = wave + j * waves, st = c + 4 * i;
+        if (c < 4 && st < steps)
+#pragma unroll
+          for (int h = 0; h < ROUTE; ++h)
+            rb[j][i][h] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(pb[h] + st * 32));
+      }
   }
   float wq[4] = {0.f, 0.f, 0.f, 0.f};
   uint2 g_out = make_uint2(0u, 0u);
@@ -197,11 +233,69 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   float total = part_out[0];
   for (int w = 1; w < waves; ++w) total += part_out[w];
   const float r = rsqrtf(total / static_cast<float>(dim) + out_eps);
-  if (has) {
-    uint2 o;
-    o.x = pack_bf16x2(r0 * r * lo_bf16(g_out.x), r1 * r * hi_bf16(g_out.x));
-    o.y = pack_bf16x2(r2 * r * lo_bf16(g_out.y), r3 * r * hi_bf16(g_out.y));
-    reinterpret_cast<uint2*>(out_norm)[base + i] = o;
+  uint2 o;
+  o.x = pack_bf16x2(r0 * r * lo_bf16(g_out.x), r1 * r * hi_bf16(g_out.x));
+  o.y = pack_bf16x2(r2 * r * lo_bf16(g_out.y), r3 * r * hi_bf16(g_out.y));
+  if (has) reinterpret_cast<uint2*>(out_norm)[base + i] = o;
+  if constexpr (ROUTE > 0) {
+    __shared__ __attribute__((aligned(16))) uint16_t xn[kDepthDimsPerWave * kDepthMaxWaves];
+    __shared__ float chain_s[4][kMaxExperts];
+    __shared__ int ids_s[8];
+    if (has) reinterpret_cast<uint2*>(xn)[i] = o;
+    __syncthreads();
+    const bool row0 = (lane & 15) == 0;
+    auto a_frag = [&](int st) {
+      const uint4 av = row0 ? *reinterpret_cast<const uint4*>(&xn[st * 32 + koff])
+                            : make_uint4(0u, 0u, 0u, 0u);
+      return __builtin_bit_cast(bf16x8, av);
+    };
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = wave + j * waves;
+      if (c >= 4) break;  // uniform
+      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int i = 0; i < kRouteStepSlots; ++i) {
+        const int st = c + 4 * i;
+        if (st < steps) {
+          const bf16x8 a = a_frag(st);
+#pragma unroll
+          for (int h = 0; h < ROUTE; ++h) {
+            const bf16x8 b = j < kRouteChainSlots
+                                 ? rb[j < kRouteChainSlots ? j : 0][i][h]
+                                 : __builtin_bit_cast(
+                                       bf16x8, *reinterpret_cast<const uint4*>(pb[h] + st * 32));
+            acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[h], 0, 0, 0);
+          }
+        }
+      }
+      for (int st = c + 4 * kRouteStepSlots; st < steps; st += 4) {
+        const bf16x8 a = a_frag(st);
+#pragma unroll
+        for (int h = 0; h < ROUTE; ++h)
+          acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              a, __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(pb[h] + st * 32)),
+              acc[h], 0, 0, 0);
+      }
+      // Row 0 of the C fragment: lanes 0-15, register 0.
+      if (lane < 16) {
+        chain_s[c][lane] = acc[0][0];
+        chain_s[c][16 + lane] = ROUTE > 1 ? acc[1][0] : 0.0f;
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int experts = route.experts;
+      const int j = lane & 15;
+      auto logit = [&](int e) -> float {
+        const float v = ((chain_s[0][e] + chain_s[1][e]) + chain_s[2][e]) + chain_s[3][e];
+        return v + (route.bias != nullptr ? route.bias[e] : 0.0f);
+      };
+      const float l0 = j < experts ? logit(j) : 0.0f;
+      const float l1 = j + 16 < experts ? logit(j + 16) : 0.0f;
+      select_top2(l0, l1, experts, tok, lane < 16, nullptr, nullptr, route.weights,
+                  route.indices, &ids_s[2 * (lane >> 4)]);
+    }
   }
 }
 
@@ -238,14 +332,24 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
                             float score_eps, const uint16_t* out_norm_w,
                             float out_eps, int64_t tokens, int dim,
                             uint16_t* out_mix, uint16_t* out_norm, const CombineSource* comb,
-                            hipStream_t s) {
+                            const RouteOut* route, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
   const int waves = (dim + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
   if (waves > kDepthMaxWaves) return hipErrorInvalidValue;
   const CombineSource none{};
-  depth_mix_kernel<<<static_cast<unsigned>(tokens), kWave * waves, 0, s>>>(
-      srcs, n_sources, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
-      out_norm, comb != nullptr ? *comb : none);
+  const RouteOut no_route{};
+  if (route != nullptr && route->experts > 16)
+    depth_mix_kernel<2><<<static_cast<unsigned>(tokens), kWave * waves, 0, s>>>(
+        srcs, n_sources, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
+        out_norm, comb != nullptr ? *comb : none, *route);
+  else if (route != nullptr)
+    depth_mix_kernel<1><<<static_cast<unsigned>(tokens), kWave * waves, 0, s>>>(
+        srcs, n_sources, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
+        out_norm, comb != nullptr ? *comb : none, *route);
+  else
+    depth_mix_kernel<0><<<static_cast<unsigned>(tokens), kWave * waves, 0, s>>>(
+        srcs, n_sources, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
+        out_norm, comb != nullptr ? *comb : none, no_route);
   return hipGetLastError();
 }
 

@@ -28,46 +28,6 @@ __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
-// Top-2 of the token whose logits lane j of this DPP row holds for experts
-// j (l0) and j + 16 (l1; ignored unless experts > 16), route weights
-// renormalised over the two selected exponentials, and the optional logits
-// and probabilities.  Every lane of the row calls it; lane 0 of the row
-// writes the per-token outputs and returns the two ids in `ids`.
-__device__ __forceinline__ void select_top2(float l0, float l1, int experts, int64_t t,
-                                            bool valid, float* out_logits, float* probs,
-                                            float* weights, int64_t* indices, int* ids) {
-  const int j = threadIdx.x & 15;
-  const bool has0 = j < experts, has1 = j + 16 < experts;
-  int first, second;
-  float vb, vr;
-  row_top2(l0, l1, experts, first, second, vb, vr);
-  if (valid) {
-    if (out_logits != nullptr) {
-      if (has0) out_logits[t * experts + j] = l0;
-      if (has1) out_logits[t * experts + j + 16] = l1;
-    }
-    if (probs != nullptr) {
-      const float p0 = has0 ? __expf(l0 - vb) : 0.0f;
-      const float p1 = has1 ? __expf(l1 - vb) : 0.0f;
-      const float inv = 1.0f / row_sum(p0 + p1);
-      if (has0) probs[t * experts + j] = p0 * inv;
-      if (has1) probs[t * experts + j + 16] = p1 * inv;
-    }
-  }
-  if (j == 0) {
-    if (valid) {
-      const float e2 = __expf(vr - vb);
-      const float sel = 1.0f + e2;
-      indices[2 * t] = first;
-      indices[2 * t + 1] = second;
-      weights[2 * t] = 1.0f / sel;
-      weights[2 * t + 1] = e2 / sel;
-    }
-    ids[0] = valid ? first : -1;
-    ids[1] = valid ? second : -1;
-  }
-}
-
 // ---- block-local ranks and histograms from wavefront ballots ---------------
 // Each half-wavefront owns one route block of 32 assignments; lane l holds
 // assignment id `id` (-1 = padding or an id outside [0, experts)).  For every

@@ -660,17 +660,32 @@ class MoE(nn.Module):
         return result.view_as(x)
 
 
+    def routes_in_depth_mix(self, x: Tensor) -> bool:
+        """Whether this layer's input depth mix also computes its top-2 route
+        (hip_moe.depth_mix_norm_route): the grouped HIP path at sizes whose
+        gate/up launch groups the indices itself, where the separate route
+        and grouping launches are pure latency."""
+        if not (self._hip_route_applies(x) and self.cfg.depth_backend == "hip"):
+            return False
+        from . import hip_moe
+        tokens = x.numel() // x.shape[-1]
+        return (tokens > hip_moe.DECODE_MAX_TOKENS and
+                hip_moe.groups_in_kernel(self, tokens, x.shape[-1]))
+
     def inference_then_mix(self, x: Tensor, *, addend: Tensor | None, depth: "DepthMix",
-                           sources: list[Tensor], output_norm: "RMSNorm") -> tuple[Tensor, Tensor]:
+                           sources: list[Tensor], output_norm: "RMSNorm",
+                           routed=None) -> tuple[Tensor, Tensor]:
         """``inference(x, addend=addend)`` and the next module's input,
         ``depth.normalized(sources + [result], output_norm)``; on the grouped
-        HIP path the combine and that depth mix are one kernel."""
+        HIP path the combine and that depth mix are one kernel.  ``routed``:
+        x's top-2 route when its depth mix already computed it."""
         from . import hip_moe
         flat = x.reshape(-1, x.shape[-1])
         if (self._hip_route_applies(x) and flat.shape[0] > hip_moe.DECODE_MAX_TOKENS and
                 depth.cfg.depth_backend == "hip" and
                 len(sources) < hip_moe.MAX_DEPTH_SOURCES):
-            routed = hip_moe.route(self, flat, collect_stats=False)
+            if routed is None:
+                routed = hip_moe.route(self, flat, collect_stats=False)
             result, mixed = hip_moe.grouped_hip_experts(
                 self, flat, routed.indices, routed.weights, addend=addend,
                 grouping=routed.grouping, then_mix=(depth, sources, output_norm))
@@ -751,15 +766,29 @@ class Parrot(nn.Module):
             return norm(x)
         return self.depth_mix[index].normalized(stream.sources(), norm)
 
+    def _moe_input(self, block: Block, stream: _AttnRes | None, x: Tensor, index: int):
+        """MoE module ``index``'s normalised input and, when its depth mix
+        kernel also routes it (MoE.routes_in_depth_mix, with the MoE about
+        to close the open partial sum), its top-2 route; else (input, None)."""
+        if (stream is not None and stream.partial is not None and
+                not self.config.collect_router_stats):
+            sources = stream.sources()
+            if block.moe.routes_in_depth_mix(sources[0]):
+                from . import hip_moe
+                return hip_moe.depth_mix_norm_route(self.depth_mix[index], sources,
+                                                    block.moe_norm, block.moe)
+        return self._mixed_input(stream, x, index, block.moe_norm), None
+
     def _moe_closing(self, block: Block, h: Tensor, stream: _AttnRes, index: int,
-                     next_norm: RMSNorm) -> Tensor:
+                     next_norm: RMSNorm, routed=None) -> Tensor:
         """Close MoE module ``index`` (fused addend) and return the input of
         module ``index + 1``: its depth mix normalised by ``next_norm``, made
-        by the MoE's combine kernel on the HIP path."""
+        by the MoE's combine kernel on the HIP path.  ``routed``: h's top-2
+        route when its depth mix computed it."""
         older = list(stream.completed)  # the sources after closing: older + [result]
         result, mixed = block.moe.inference_then_mix(
             h, addend=stream.partial, depth=self.depth_mix[index + 1], sources=older,
-            output_norm=next_norm)
+            output_norm=next_norm, routed=routed)
         stream.close(result)
         return mixed
 
@@ -819,12 +848,12 @@ class Parrot(nn.Module):
                     stream.push(delta)
             index += 1
 
-            h = self._mixed_input(stream, x, index, block.moe_norm)
+            h, routed = self._moe_input(block, stream, x, index)
             if self._fuse_moe_addend(block, h, stream):
                 last = bi + 1 == len(self.blocks)
                 pending = self._moe_closing(
                     block, h, stream, index,
-                    self.final_norm if last else self.blocks[bi + 1].attention_norm)
+                    self.final_norm if last else self.blocks[bi + 1].attention_norm, routed)
             else:
                 delta, aux, usage = (checkpoint(block.moe, h, use_reentrant=False) if remat
                                      else block.moe(h))
@@ -909,13 +938,13 @@ class Parrot(nn.Module):
                 stream.push(delta)
             index += 1
 
-            h = self._mixed_input(stream, x, index, block.moe_norm)
+            h, routed = self._moe_input(block, stream, x, index)
             if stream is not None and stream.partial is not None and \
                     block.moe._hip_route_applies(h):
                 last = bi + 1 == len(self.blocks)
                 pending = self._moe_closing(
                     block, h, stream, index,
-                    self.final_norm if last else self.blocks[bi + 1].attention_norm)
+                    self.final_norm if last else self.blocks[bi + 1].attention_norm, routed)
             else:
                 delta = block.moe.inference(h, direct=False)
                 if stream is None:

@@ -204,3 +204,37 @@ def test_argument_validation_without_gpu(lib):
     assert lib.parrot_experts_combine_depth_mix_bf16(
         64, 64, 128, 64, null, fake, fake, 16, null, 1, fake, fake, 1e-6, fake, 1e-6, null, fake,
         null) == -4
+    # depth mix + route: out_norm and router required, experts 2..32, dim % 32
+    assert lib.parrot_depth_mix_route_bf16(
+        ctypes.cast(srcs, ctypes.c_void_p), 2, fake, fake, 1e-6, fake, 1e-6, 4, 64, null, null,
+        fake, null, 8, fake, fake, null) == -1
+    assert lib.parrot_depth_mix_route_bf16(
+        ctypes.cast(srcs, ctypes.c_void_p), 2, fake, fake, 1e-6, fake, 1e-6, 4, 64, null, fake,
+        fake, null, 33, fake, fake, null) == -3
+    assert lib.parrot_depth_mix_route_bf16(
+        ctypes.cast(srcs, ctypes.c_void_p), 2, fake, fake, 1e-6, fake, 1e-6, 4, 48, null, fake,
+        fake, null, 8, fake, fake, null) == -3
+    assert lib.parrot_depth_mix_route_bf16(
+        ctypes.cast(srcs, ctypes.c_void_p), 2, fake, fake, 1e-6, fake, 1e-6, 4, 64, null, fake,
+        fake + 8, null, 8, fake, fake, null) == -5
+    # in-kernel grouping: which shapes, and its entry points' checks
+    assert lib.parrot_experts_group_in_kernel(512, 768, 16, 512, 256) == 1
+    assert lib.parrot_experts_group_in_kernel(1024, 768, 32, 512, 256) == 1
+    assert lib.parrot_experts_group_in_kernel(1025, 768, 32, 512, 256) == 0  # > 2048 ids
+    assert lib.parrot_experts_group_in_kernel(1024, 768, 16, 512, 256) == 0  # 128 rows/expert
+    assert lib.parrot_experts_group_in_kernel(512, 1024, 16, 512, 256) == 0  # dim > 768
+    assert lib.parrot_experts_group_in_kernel(512, 768, 33, 512, 256) == 0
+    gws = lib.parrot_experts_workspace_bytes(512, 768, 512, 256)
+    assert lib.parrot_experts_gate_up_grouping_bf16(
+        fake, 512, 768, 16, 512, 256, 80, null, fake, fake, fake, fake, fake, fake, gws,
+        null) == -1
+    assert lib.parrot_experts_gate_up_grouping_bf16(
+        fake, 2048, 768, 16, 512, 256, 264, fake, fake, fake, fake, fake, fake, fake,
+        lib.parrot_experts_workspace_bytes(2048, 768, 512, 256), null) == -3
+    assert lib.parrot_experts_gate_up_grouping_bf16(
+        fake, 512, 768, 16, 512, 256, 80, fake, fake, fake, fake, fake, fake, fake, 16,
+        null) == -4
+    assert lib.parrot_experts_down_sorted_bf16(
+        512, 768, 16, 512, 256, 80, fake, fake, null, fake, fake, fake, fake, gws, null) == -1
+    assert lib.parrot_experts_down_sorted_bf16(
+        512, 96, 16, 512, 256, 80, fake, fake, fake, fake, fake, fake, fake, gws, null) == -3

@@ -134,3 +134,25 @@ def test_graph_replay_matches_eager():
             assert torch.equal(static_out, eager)
             model(ids)  # eager work between replays
             torch.cuda.synchronize()
+
+
+def test_routing_in_depth_mix_matches_separate_launches(monkeypatch):
+    """The forward and prefill whose MoE input depth mixes also route (and
+    whose gate/up launches group in-kernel) equal, bit for bit, the same
+    model with separate route and grouping launches."""
+    from parrot import ModelConfig
+    from parrot.model import MoE
+    _say("routing in the depth mix vs separate launches")
+    model = _hip_model(ModelConfig(n_layers=4, moe_backend="grouped_hip", depth_backend="hip",
+                                   collect_router_stats=False), 6)
+    ids = torch.randint(0, 32768, (2, 200), generator=torch.Generator().manual_seed(6)).cuda()
+    with torch.no_grad():
+        assert model.blocks[0].moe.routes_in_depth_mix(
+            torch.empty(400, 768, dtype=torch.bfloat16, device="cuda"))
+        fused = model(ids).logits
+        fused_prefill, _ = model.prefill(ids)
+        monkeypatch.setattr(MoE, "routes_in_depth_mix", lambda self, x: False)
+        separate = model(ids).logits
+        separate_prefill, _ = model.prefill(ids)
+    assert torch.equal(fused, separate)
+    assert torch.equal(fused_prefill, separate_prefill)

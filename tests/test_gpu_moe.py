@@ -251,3 +251,72 @@ def test_combine_then_depth_mix(tokens, n_older):
         ref = hip_moe.depth_mix_norm(depth, older + [plain], norm)
     assert torch.equal(fused, plain)
     assert torch.equal(mixed, ref)
+
+
+@pytest.mark.parametrize("tokens,experts,sources,skewed", [
+    (512, 16, 5, False), (17, 16, 1, False), (256, 32, 9, False), (1000, 32, 3, True),
+    (100, 8, 2, False), (4097, 16, 4, False)])
+def test_depth_mix_route(tokens, experts, sources, skewed):
+    """The depth mix that also routes its normalised output writes exactly
+    depth_mix_norm's rows and exactly route()'s weights and indices on them
+    (the same MFMA logit chains, token in A row 0)."""
+    from parrot import hip_moe
+    _say(f"depth mix + route T={tokens} E={experts} S={sources} skew={skewed}")
+    module = moe_module(experts, seed=2)
+    depth = _Depth(768).cuda().bfloat16()
+    norm = _Norm(768).cuda().bfloat16()
+    src = [inputs(tokens, seed=20 + s) * (1 + s) for s in range(sources)]
+    bias = skew_bias(experts) if skewed else None
+    with torch.no_grad():
+        normed, top2 = hip_moe.depth_mix_norm_route(depth, src, norm, module, logit_bias=bias)
+        ref = hip_moe.depth_mix_norm(depth, src, norm)
+        routed = hip_moe.route(module, ref, False, logit_bias=bias)
+    assert torch.equal(normed, ref)
+    assert torch.equal(top2.indices, routed.indices)
+    assert torch.equal(top2.weights, routed.weights)
+
+
+def _sorted_from_grouping(g, experts):
+    """Assignment id of each hidden row: expert-contiguous slot order, the
+    in-capacity slots perm[e, :] then the expert's overflow entries."""
+    counts = g.counts.cpu().tolist()
+    offsets = g.offsets.cpu().tolist()
+    perm = g.perm.cpu()
+    overflow = g.overflow.cpu()
+    rows = []
+    for e in range(experts):
+        inside = min(counts[e], g.capacity)
+        rows += perm[e, :inside].tolist()
+        start = offsets[experts + 1 + e]
+        rows += overflow[start:start + counts[e] - inside].tolist()
+    return torch.tensor(rows, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("tokens,experts,skewed", [
+    (512, 16, False), (300, 16, True), (17, 16, False), (1000, 32, True), (100, 8, False),
+    (1024, 32, False)])
+def test_experts_group_in_kernel(tokens, experts, skewed):
+    """The gate/up launch that groups the top-2 ids itself gives the same
+    MoE output as the route + group path, and the grouping it writes (counts,
+    offsets, the hidden rows' assignment ids) is that path's grouping."""
+    from parrot import hip_moe
+    _say(f"in-kernel grouping T={tokens} E={experts} skew={skewed}")
+    module = moe_module(experts, seed=8)
+    x = inputs(tokens, seed=8)
+    assert hip_moe.groups_in_kernel(module, tokens, x.shape[1])
+    bias = skew_bias(experts) if skewed else None
+    addend = inputs(tokens, seed=9)
+    with torch.no_grad():
+        routed = hip_moe.route(module, x, False, logit_bias=bias)
+        ref = hip_moe.grouped_hip_experts(module, x, routed.indices, routed.weights,
+                                          addend=addend, grouping=routed.grouping)
+        got = hip_moe.grouped_hip_experts(module, x, routed.indices, routed.weights,
+                                          addend=addend)
+    g = routed.grouping
+    _say(f"  overflow {int(g.offsets[-1])} of {2 * tokens}")
+    assert torch.equal(got, ref)
+    buf = module.__dict__["_hip_group_buffers"][:4 * (3 * experts + 2 + 2 * tokens)]
+    buf = buf.view(torch.int32).cpu()
+    assert torch.equal(buf[:experts], g.counts.cpu())
+    assert torch.equal(buf[experts:3 * experts + 2], g.offsets.cpu())
+    assert torch.equal(buf[3 * experts + 2:], _sorted_from_grouping(g, experts))
