@@ -100,6 +100,15 @@ class StageBench:
         counts = g.counts.cpu()
         self.hit = int((counts > 0).sum())
         self.overflow = int(g.offsets[-1].item())
+        # The forward's form at sizes the gate/up launch groups itself: the
+        # top-2 ids in; counts, offsets and the hidden rows' ids out.
+        self.in_kernel = bool(self.lib.parrot_experts_group_in_kernel(
+            self.T, self.dim, self.E, self.H, self.Hs))
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.g_counts = torch.empty(self.E, **i32)
+        self.g_offsets = torch.empty(2 * self.E + 2, **i32)
+        self.g_sorted = torch.empty(2 * self.T, **i32)
+        self.ids = self.routed.indices.reshape(-1).contiguous()
 
     def route(self):
         p, r, g = self.ptr, self.routed, self.g
@@ -122,6 +131,20 @@ class StageBench:
             p(g.perm), p(g.overflow), p(self.routed.weights), p(self.packed[1]),
             p(self.packed[3]), p(self.ews), self.ews_bytes, self.s)
 
+    def gate_up_grouping(self):
+        p = self.ptr
+        return self.lib.parrot_experts_gate_up_grouping_bf16(
+            p(self.x), self.T, self.dim, self.E, self.H, self.Hs, self.C, p(self.ids),
+            p(self.g_counts), p(self.g_offsets), p(self.g_sorted), p(self.packed[0]),
+            p(self.packed[2]), p(self.ews), self.ews_bytes, self.s)
+
+    def down_sorted(self):
+        p = self.ptr
+        return self.lib.parrot_experts_down_sorted_bf16(
+            self.T, self.dim, self.E, self.H, self.Hs, self.C, p(self.g_counts),
+            p(self.g_offsets), p(self.g_sorted), p(self.routed.weights), p(self.packed[1]),
+            p(self.packed[3]), p(self.ews), self.ews_bytes, self.s)
+
     def combine(self):
         p = self.ptr
         return self.lib.parrot_experts_combine_bf16(self.T, self.dim, self.H, self.Hs, None,
@@ -140,6 +163,10 @@ class StageBench:
     def bytes_down(self):
         T, d, H, Hs = self.T, self.dim, self.H, self.Hs
         return (self.hit * d * H + d * Hs + 2 * T * H + T * Hs) * 2 + 3 * T * d * 4 + 2 * T * 4
+
+    def bytes_grouping(self):
+        """Extra bytes of the in-kernel grouping: ids in, grouping out."""
+        return 2 * self.T * 8 + (3 * self.E + 2 + 2 * self.T) * 4
 
     def bytes_combine(self):
         return 3 * self.T * self.dim * 4 + self.T * self.dim * 2
@@ -191,6 +218,13 @@ def layer_kernels(moe, x, iters, logit_bias=None) -> tuple[dict, "StageBench"]:
         "overflow_assignments": sb.overflow,
         "capacity": sb.C,
     }
+    if sb.in_kernel:
+        # gate/up grouping first: down_sorted reads the grouping it writes.
+        res["gate_up_grouping"] = entry(event_time_us(sb.gate_up_grouping, iters, sb.stream),
+                                        sb.bytes_gate_up() + sb.bytes_grouping(),
+                                        sb.flops_gate_up())
+        res["down_sorted"] = entry(event_time_us(sb.down_sorted, iters, sb.stream),
+                                   sb.bytes_down() + (3 * sb.E + 2) * 4, sb.flops_down())
     return res, sb
 
 
@@ -413,7 +447,8 @@ TRAFFIC_COMMANDS = [
 def traffic_workload() -> None:
     """The dispatches the two --pmc passes count: the model forward that
     captures block 0's MoE input, then TRAFFIC_LAUNCHES launches of the
-    experts gate/up kernel on it (the last TRAFFIC_LAUNCHES dispatches named
+    experts gate/up kernel on it in the forward's form, grouping the top-2
+    ids in-kernel (the last TRAFFIC_LAUNCHES dispatches named
     TRAFFIC_KERNEL), then CALIBRATION_LAUNCHES of torch's `neg` over a bf16
     tensor of CALIBRATION_ELEMS elements: a plain streaming kernel whose HBM
     bytes are known exactly."""
@@ -422,9 +457,9 @@ def traffic_workload() -> None:
     sb = StageBench(model.blocks[0].moe, captured["x"])
     torch.cuda.synchronize()
     for _ in range(TRAFFIC_LAUNCHES):
-        rc = sb.gate_up()
+        rc = sb.gate_up_grouping()
         if rc:
-            raise RuntimeError(f"gate_up returned status {rc}")
+            raise RuntimeError(f"gate_up_grouping returned status {rc}")
     torch.cuda.synchronize()
     src = torch.ones(CALIBRATION_ELEMS, dtype=torch.bfloat16, device="cuda")
     dst = torch.empty_like(src)
@@ -433,7 +468,8 @@ def traffic_workload() -> None:
     torch.cuda.synchronize()
     print(json.dumps({"traffic_workload": "done", "kernel": TRAFFIC_KERNEL,
                       "launches": TRAFFIC_LAUNCHES, "calibration_launches": CALIBRATION_LAUNCHES,
-                      "experts_hit": sb.hit, "algorithmic_bytes": sb.bytes_gate_up()}), flush=True)
+                      "experts_hit": sb.hit,
+                      "algorithmic_bytes": sb.bytes_gate_up() + sb.bytes_grouping()}), flush=True)
 
 
 def _counter_rows(directory: str, counter: str) -> list[tuple[str, float]]:
@@ -608,10 +644,11 @@ def main():
         if not args.skip_sweep:
             log("token sweep")
             kernels["sweep_E16"] = sweep_kernels(moe0, max(20, args.kernel_iters // 4))
-        gu = c4["gate_up"]
+        # The forward's gate/up form at C4: grouping in-kernel.
+        gu = c4["gate_up_grouping"]
         traffic = load_traffic()
-        roofline = {"kernel": f"{TRAFFIC_KERNEL} (experts gate_up + SwiGLU), "
-                              "C4 in-model shape T=512 E=16",
+        roofline = {"kernel": f"{TRAFFIC_KERNEL} (experts gate_up + SwiGLU, grouping the "
+                              "top-2 ids in-kernel), C4 in-model shape T=512 E=16",
                     "bound": "hbm", "achieved": gu["gbps"], "peak": PEAK_HBM_GBPS,
                     "unit": "GB/s", "frac": gu["hbm_frac"], "traffic": traffic,
                     "algorithmic_bytes": gu["bytes"],

@@ -530,8 +530,13 @@ void grouped_gemm_kernel(GemmArgs p) {
 // Wavefront w owns output columns [w WN, w WN + WN) of the 4 WN-wide tile.
 constexpr int kStreamKCap = 768;  // largest K whose A tile fits the LDS budget
 
+// No amdgpu_waves_per_eu cap: with it ("1, 2") the hardware ran at most two
+// of these workgroups per CU, so at the bs1 x 512 shapes the down launch
+// started its last quarter of workgroups only when the first ones ended
+// (measured on MI355X: last workgroup start 4.2 us after the first, launch
+// 8.6 -> 7.2 us without the cap; LDS alone allows three per CU).
 template <int BM, int WN, int PF, int PHASE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
+__global__ __launch_bounds__(256)
 void grouped_gemm_stream_kernel(GemmArgs p) {
   constexpr int kTilesM = BM / 16;
   constexpr int kTilesN = WN / 16;
