@@ -639,9 +639,10 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) dst_row[mi][r] = row_dst[mi * 16 + 4 * (lane >> 4) + r];
   // Phase 2, routed rows: their route weights, loaded inside the first k
-  // step, right after its weight refill.  Loads retire in order, so issued
-  // before the loop they would hold up its first MFMAs; issued there, the
-  // first wait that covers them comes PF steps later.
+  // step, right after its weight refill (before the final pass when that is
+  // the only one).  Loads retire in order, so issued before the loop they
+  // would hold up its first MFMAs; issued there, the first wait that covers
+  // them comes PF steps later.
   float route_w[kTilesM][4];
 #pragma unroll
   for (int mi = 0; mi < kTilesM; ++mi)
@@ -662,36 +663,47 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < kTilesN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int s0 = 0; s0 < ksteps; s0 += PF) {
+  // One k step on ring slot i: A fragments from LDS, the MFMAs, then the
+  // slot's refill with step + PF unless the ring already holds the last
+  // steps.  The final pass is peeled off so it issues no loads: refills of
+  // steps past the end (reloads of the last one, to keep the loop uniform)
+  // cost a full memory round trip before the kernel could finish.
+  auto k_step = [&](int step, int i, bool refill) {
+    bf16x8 af[kTilesM];
 #pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int step = s0 + i;  // ksteps is a multiple of PF
-      bf16x8 af[kTilesM];
+    for (int mi = 0; mi < kTilesM; ++mi) {
+      const int r = mi * 16 + (lane & 15);
+      const int c = step * 4 + (lane >> 4);
+      const int pc = (c & ~swz) | ((c ^ r) & swz);
+      af[mi] = *reinterpret_cast<const bf16x8*>(&a_lds[(r * chunks + pc) * 8]);
+    }
 #pragma unroll
-      for (int mi = 0; mi < kTilesM; ++mi) {
-        const int r = mi * 16 + (lane & 15);
-        const int c = step * 4 + (lane >> 4);
-        const int pc = (c & ~swz) | ((c ^ r) & swz);
-        af[mi] = *reinterpret_cast<const bf16x8*>(&a_lds[(r * chunks + pc) * 8]);
-      }
+    for (int mi = 0; mi < kTilesM; ++mi)
 #pragma unroll
-      for (int mi = 0; mi < kTilesM; ++mi)
-#pragma unroll
-        for (int j = 0; j < kTilesN; ++j)
-          acc[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              af[mi], __builtin_bit_cast(bf16x8, bq[i][j]), acc[mi][j], 0, 0, 0);
-      const uint32_t next = static_cast<uint32_t>(min(step + PF, ksteps - 1)) * 1024;
+      for (int j = 0; j < kTilesN; ++j)
+        acc[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            af[mi], __builtin_bit_cast(bf16x8, bq[i][j]), acc[mi][j], 0, 0, 0);
+    if (refill) {
+      const uint32_t next = static_cast<uint32_t>(step + PF) * 1024;
 #pragma unroll
       for (int j = 0; j < kTilesN; ++j) bq[i][j] = buffer_load16(b_rsrc, b_off[j], next);
-      if (i == 0 && s0 == 0) load_route_weights();
-      // Keep the refill in its own step: left free, the scheduler sinks
-      // every refill to the end of the loop body, and the next pass's first
-      // MFMAs then wait on loads issued a few instructions earlier.  LDS
-      // reads and SALU work may still cross (mask 0x104), so the next
-      // step's A fragments are read while this step's MFMAs run.
-      __builtin_amdgcn_sched_barrier(0x104);
     }
+    if (refill && step == 0) load_route_weights();
+    // Keep the refill in its own step: left free, the scheduler sinks every
+    // refill to the end of the loop body, and the next pass's first MFMAs
+    // then wait on loads issued a few instructions earlier.  LDS reads and
+    // SALU work may still cross (mask 0x104), so the next step's A
+    // fragments are read while this step's MFMAs run.
+    __builtin_amdgcn_sched_barrier(0x104);
+  };
+  const int last = ksteps - PF;  // first step of the final pass
+  if (last == 0) load_route_weights();  // one pass only: no refilling step
+  for (int s0 = 0; s0 < last; s0 += PF) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) k_step(s0 + i, i, true);
   }
+#pragma unroll
+  for (int i = 0; i < PF; ++i) k_step(last + i, i, false);
 
   // ---- epilogue (as in grouped_gemm_kernel) ----------------------------------
   if (PHASE == 1) {
