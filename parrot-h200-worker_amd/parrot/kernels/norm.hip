@@ -85,7 +85,7 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
     uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm, CombineSource comb,
     RouteOut route) {
-  __shared__ float part[kDepthMaxWaves][2 * kMaxDepthSources];
+  __shared__ __attribute__((aligned(8))) float part[kDepthMaxWaves][2 * kMaxDepthSources];
   __shared__ float part_out[kDepthMaxWaves];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -96,37 +96,34 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   const bool has = i < chunks;
   const int64_t base = tok * chunks;
 
-  // Every source chunk, then the score weights (w_d * q_d) of the lane's dims.
+  // Every load of the workgroup is issued before the first wait.  All
+  // source slots are loaded (unread slots hold a valid row, cached after the
+  // first read) and the unread ones zeroed afterwards, lanes past the row
+  // load chunk 0 and zero it afterwards, and only uniform conditions
+  // (combine, addend, output norm) guard a load: a load behind a branch on
+  // a kernel argument, or inside a per-lane branch, costs a serial round
+  // trip each.
   const bool combine = comb.y_shared != nullptr;
   const int n_read = combine ? n_sources - 1 : n_sources;
+  const int ic = has ? i : 0;
+  const uint16_t* sp[kMaxDepthSources];
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = srcs.src[s];
   uint2 v[kMaxDepthSources];
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) {
-    v[s] = make_uint2(0u, 0u);
-    if (s < n_read && has) v[s] = reinterpret_cast<const uint2*>(srcs.src[s])[base + i];
-  }
+  for (int s = 0; s < kMaxDepthSources; ++s) v[s] = reinterpret_cast<const uint2*>(sp[s])[base + ic];
+  float4 sh = {0.f, 0.f, 0.f, 0.f}, y0 = sh, y1 = sh;
+  uint2 pa = make_uint2(0u, 0u);
   if (combine) {
-    // The MoE output row: bf16(shared + routed 0 + routed 1), then
-    // bf16(addend + that), exactly as the combine kernel; it is the new
-    // residual source and the last depth source.
-    uint2 o = make_uint2(0u, 0u);
-    if (has) {
-      const float4 sh = reinterpret_cast<const float4*>(comb.y_shared)[base + i];
-      const float4 r0 = reinterpret_cast<const float4*>(comb.y_routed)[(2 * tok) * chunks + i];
-      const float4 r1 = reinterpret_cast<const float4*>(comb.y_routed)[(2 * tok + 1) * chunks + i];
-      o.x = pack_bf16x2(sh.x + r0.x + r1.x, sh.y + r0.y + r1.y);
-      o.y = pack_bf16x2(sh.z + r0.z + r1.z, sh.w + r0.w + r1.w);
-      if (comb.addend != nullptr) {
-        const uint2 p = reinterpret_cast<const uint2*>(comb.addend)[base + i];
-        o.x = pack_bf16x2(lo_bf16(p.x) + lo_bf16(o.x), hi_bf16(p.x) + hi_bf16(o.x));
-        o.y = pack_bf16x2(lo_bf16(p.y) + lo_bf16(o.y), hi_bf16(p.y) + hi_bf16(o.y));
-      }
-      reinterpret_cast<uint2*>(comb.out)[base + i] = o;
-    }
-#pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s)
-      if (s == n_sources - 1) v[s] = o;
+    sh = reinterpret_cast<const float4*>(comb.y_shared)[base + ic];
+    y0 = reinterpret_cast<const float4*>(comb.y_routed)[(2 * tok) * chunks + ic];
+    y1 = reinterpret_cast<const float4*>(comb.y_routed)[(2 * tok + 1) * chunks + ic];
+    if (comb.addend != nullptr) pa = reinterpret_cast<const uint2*>(comb.addend)[base + ic];
   }
+  const uint2 q = reinterpret_cast<const uint2*>(query)[ic];
+  const uint2 g = reinterpret_cast<const uint2*>(score_w)[ic];
+  uint2 g_out = make_uint2(0u, 0u);
+  if (out_norm != nullptr) g_out = reinterpret_cast<const uint2*>(out_w)[ic];
   // Router weights of this wavefront's first chains (ROUTE > 0).
   const int steps = dim / 32;
   const int koff = (lane >> 4) * 8;
@@ -148,16 +145,34 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
             rb[j][i][h] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(pb[h] + st * 32));
       }
   }
+
+  // Unread slots and lanes past the row hold zeros from here on.
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s)
+    if (!has || s >= n_read) v[s] = make_uint2(0u, 0u);
+  if (combine) {
+    // The MoE output row: bf16(shared + routed 0 + routed 1), then
+    // bf16(addend + that), exactly as the combine kernel; it is the new
+    // residual source and the last depth source.
+    uint2 o;
+    o.x = pack_bf16x2(sh.x + y0.x + y1.x, sh.y + y0.y + y1.y);
+    o.y = pack_bf16x2(sh.z + y0.z + y1.z, sh.w + y0.w + y1.w);
+    if (comb.addend != nullptr) {
+      o.x = pack_bf16x2(lo_bf16(pa.x) + lo_bf16(o.x), hi_bf16(pa.x) + hi_bf16(o.x));
+      o.y = pack_bf16x2(lo_bf16(pa.y) + lo_bf16(o.y), hi_bf16(pa.y) + hi_bf16(o.y));
+    }
+    if (has) reinterpret_cast<uint2*>(comb.out)[base + i] = o;
+    else o = make_uint2(0u, 0u);
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s)
+      if (s == n_sources - 1) v[s] = o;
+  }
   float wq[4] = {0.f, 0.f, 0.f, 0.f};
-  uint2 g_out = make_uint2(0u, 0u);
   if (has) {
-    const uint2 q = reinterpret_cast<const uint2*>(query)[i];
-    const uint2 g = reinterpret_cast<const uint2*>(score_w)[i];
     wq[0] = lo_bf16(q.x) * lo_bf16(g.x);
     wq[1] = hi_bf16(q.x) * hi_bf16(g.x);
     wq[2] = lo_bf16(q.y) * lo_bf16(g.y);
     wq[3] = hi_bf16(q.y) * hi_bf16(g.y);
-    if (out_norm != nullptr) g_out = reinterpret_cast<const uint2*>(out_w)[i];
   }
 
   // Per-source partial sums, all wavefront reductions back to back.
@@ -187,18 +202,32 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   }
   __syncthreads();
 
+  // Cross-wavefront sums in wavefront order.  The loop bounds are
+  // compile-time (uniform guards inside), so each wavefront row's LDS reads
+  // go out together instead of one read, wait and add at a time.
+  float sst[kMaxDepthSources], dqt[kMaxDepthSources];
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) sst[s] = dqt[s] = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kDepthMaxWaves; ++w) {
+    if (w < waves) {
+#pragma unroll
+      for (int s = 0; s < kMaxDepthSources; ++s) {
+        if (s < n_sources) {
+          const float2 pv = *reinterpret_cast<const float2*>(&part[w][2 * s]);
+          sst[s] += pv.x;
+          dqt[s] += pv.y;
+        }
+      }
+    }
+  }
   float score[kMaxDepthSources];
   float mx = -INFINITY;
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) {
     score[s] = -INFINITY;
     if (s < n_sources) {
-      float sst = part[0][2 * s], dqt = part[0][2 * s + 1];
-      for (int w = 1; w < waves; ++w) {
-        sst += part[w][2 * s];
-        dqt += part[w][2 * s + 1];
-      }
-      score[s] = dqt * rsqrtf(sst / static_cast<float>(dim) + score_eps);
+      score[s] = dqt[s] * rsqrtf(sst[s] / static_cast<float>(dim) + score_eps);
       mx = fmaxf(mx, score[s]);
     }
   }
@@ -231,7 +260,9 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   if (lane == 0) part_out[wave] = sso;
   __syncthreads();
   float total = part_out[0];
-  for (int w = 1; w < waves; ++w) total += part_out[w];
+#pragma unroll
+  for (int w = 1; w < kDepthMaxWaves; ++w)
+    if (w < waves) total += part_out[w];
   const float r = rsqrtf(total / static_cast<float>(dim) + out_eps);
   uint2 o;
   o.x = pack_bf16x2(r0 * r * lo_bf16(g_out.x), r1 * r * hi_bf16(g_out.x));
