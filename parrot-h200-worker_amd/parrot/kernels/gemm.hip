@@ -549,6 +549,14 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
   __shared__ int hist_s[4][kMaxExperts];
   __shared__ int chunk_s[kGroupMaxAssign / kWave];
 
+  // Every kernel argument the prologue reads, in one batch of scalar loads:
+  // a field first read inside a branch costs a scalar round trip of its own.
+  asm volatile("" ::"s"(p.tokens), "s"(p.dim), "s"(p.experts), "s"(p.hidden_dim),
+               "s"(p.shared_dim), "s"(p.capacity), "s"(p.hstride), "s"(p.counts),
+               "s"(p.offsets), "s"(p.perm), "s"(p.overflow), "s"(p.sorted), "s"(p.indices),
+               "s"(p.w_routed), "s"(p.w_shared), "s"(p.a_src), "s"(p.weights),
+               "s"(p.hidden_out), "s"(p.y_routed), "s"(p.y_shared), "s"(p.counts_out),
+               "s"(p.offsets_out), "s"(p.sorted_out));
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
