@@ -156,6 +156,9 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
 
   // XCD-aware tile order: hardware id -> (XCD, slot) -> contiguous index j.
   const int total = static_cast<int>(gridDim.x);
+  // The prologue's kernel arguments in one batch of scalar loads (a field
+  // first read inside a branch or loop costs a scalar round trip of its own).
+  asm volatile("" ::"s"(p.x), "s"(p.lda), "s"(p.rows), "s"(p.K), "s"(p.N), "s"(p.w), "s"(total));
   const int id = static_cast<int>(blockIdx.x);
   const int xcd = id & 7, slot = id >> 3;
   const int q8 = total >> 3, r8 = total & 7;
