@@ -87,6 +87,20 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     RouteOut route) {
   __shared__ __attribute__((aligned(8))) float part[kDepthMaxWaves][2 * kMaxDepthSources];
   __shared__ float part_out[kDepthMaxWaves];
+  // The kernel arguments of the load phase in one batch of scalar loads,
+  // before anything uses one: a field first read inside a branch, or after
+  // an earlier batch was waited for, costs a scalar round trip of its own.
+  const uint16_t* sp[kMaxDepthSources];
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = srcs.src[s];
+  static_assert(kMaxDepthSources == 9, "the batch below names every source slot");
+  asm volatile("" ::"s"(sp[0]), "s"(sp[1]), "s"(sp[2]), "s"(sp[3]), "s"(sp[4]), "s"(sp[5]),
+               "s"(sp[6]), "s"(sp[7]), "s"(sp[8]), "s"(comb.y_shared), "s"(comb.y_routed),
+               "s"(comb.addend), "s"(query), "s"(score_w), "s"(out_w), "s"(out_norm),
+               "s"(n_sources), "s"(dim), "s"(comb.out), "s"(out_mix));
+  if constexpr (ROUTE > 0)
+    asm volatile("" ::"s"(route.router_w), "s"(route.bias), "s"(route.experts),
+                 "s"(route.weights), "s"(route.indices));
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int waves = blockDim.x >> 6;
@@ -106,9 +120,6 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   const bool combine = comb.y_shared != nullptr;
   const int n_read = combine ? n_sources - 1 : n_sources;
   const int ic = has ? i : 0;
-  const uint16_t* sp[kMaxDepthSources];
-#pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = srcs.src[s];
   uint2 v[kMaxDepthSources];
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) v[s] = reinterpret_cast<const uint2*>(sp[s])[base + ic];
