@@ -159,6 +159,10 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
   // The prologue's kernel arguments in one batch of scalar loads (a field
   // first read inside a branch or loop costs a scalar round trip of its own).
   asm volatile("" ::"s"(p.x), "s"(p.lda), "s"(p.rows), "s"(p.K), "s"(p.N), "s"(p.w), "s"(total));
+  if constexpr (EPI == kStore) asm volatile("" ::"s"(p.addend), "s"(p.ld_addend));
+  if constexpr (EPI == kRopeQkv)
+    asm volatile("" ::"s"(p.cos_t), "s"(p.sin_t), "s"(p.start), "s"(p.start_device), "s"(p.seq),
+                 "s"(p.max_positions), "s"(p.head_dim), "s"(p.heads), "s"(p.kv_heads));
   const int id = static_cast<int>(blockIdx.x);
   const int xcd = id & 7, slot = id >> 3;
   const int q8 = total >> 3, r8 = total & 7;
@@ -172,6 +176,45 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
   const int chunks = K / 8;                      // 16-byte chunks per row (multiple of 8)
   const int swz = (chunks & 15) == 0 ? 15 : 7;   // XOR group size - 1
   const int ksteps = KST > 0 ? KST : K / 32;
+
+  // ---- epilogue operands that depend only on this lane's rows and column,
+  // loaded before the tile so their round trip overlaps it: read in the
+  // epilogue they added one (the residual addend) or two (a device position,
+  // then the RoPE tables).  The loads are unconditional (a value loaded
+  // inside a branch is waited for at the branch's end): without an addend
+  // they read the weights' first row, waves past N clamp their column, and
+  // the table indices are clamped into the tables.
+  const int ecol = min(nw, p.N - 16) + (lane & 15);
+  uint16_t add_v[kTilesM][4];
+  float rope_c[kTilesM][4], rope_s[kTilesM][4];
+  if constexpr (EPI == kStore) {
+    const bool has_addend = p.addend != nullptr;
+    const uint16_t* ab = has_addend ? p.addend : p.w;
+    const int64_t ald = has_addend ? p.ld_addend : 0;
+#pragma unroll
+    for (int mi = 0; mi < kTilesM; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = min(m0 + mi * 16 + 4 * (lane >> 4) + r, p.rows - 1);
+        add_v[mi][r] = ab[static_cast<int64_t>(row) * ald + ecol];
+      }
+  }
+  if constexpr (EPI == kRopeQkv) {
+    const int d = p.head_dim;
+    const int w = ecol - (ecol / d) * d;
+    const int shift = p.start + (p.start_device != nullptr ? *p.start_device : 0);
+#pragma unroll
+    for (int mi = 0; mi < kTilesM; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = min(m0 + mi * 16 + 4 * (lane >> 4) + r, p.rows - 1);
+        const int tp = row - (row / p.seq) * p.seq;
+        const int pos = min(max(shift + tp, 0), p.max_positions - 1);
+        const int64_t ti = static_cast<int64_t>(pos) * (d / 2) + w / 2;
+        rope_c[mi][r] = p.cos_t[ti];
+        rope_s[mi][r] = p.sin_t[ti];
+      }
+  }
 
   // ---- A: the whole tile, direct to LDS (rows past the end read the last row)
   {
@@ -240,9 +283,7 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
         const int row = m0 + mi * 16 + 4 * (lane >> 4) + r;
         if (row >= p.rows) continue;
         uint16_t v = f32_to_bf16(acc[mi][r]);
-        if (p.addend != nullptr)
-          v = f32_to_bf16(bf16_to_f32(p.addend[static_cast<int64_t>(row) * p.ld_addend + col]) +
-                          bf16_to_f32(v));
+        if (p.addend != nullptr) v = f32_to_bf16(bf16_to_f32(add_v[mi][r]) + bf16_to_f32(v));
         p.out[static_cast<int64_t>(row) * p.ldo + col] = v;
       }
     return;
@@ -318,7 +359,6 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
   const int H = p.heads, Hk = p.kv_heads;
   const bool rotate = head < H + Hk;
   const bool odd = (lane & 1) != 0;
-  const int shift = p.start + (p.start_device != nullptr ? *p.start_device : 0);
 #pragma unroll
   for (int mi = 0; mi < kTilesM; ++mi) {
     float val[4];
@@ -330,11 +370,7 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
       const float other = swap_pair(self);
       val[r] = self;
       if (rotate) {
-        const int row = m0 + mi * 16 + 4 * (lane >> 4) + r;
-        const int tp = row - (row / p.seq) * p.seq;
-        const int pos = min(max(shift + tp, 0), p.max_positions - 1);
-        const int64_t ti = static_cast<int64_t>(pos) * (d / 2) + w / 2;
-        const float c = p.cos_t[ti], s = p.sin_t[ti];
+        const float c = rope_c[mi][r], s = rope_s[mi][r];
         val[r] = odd ? rope_odd(other, self, c, s) : rope_even(self, other, c, s);
       }
     }
