@@ -797,9 +797,8 @@ hipError_t run_stream(int phase, GemmArgs args, int n_max, hipStream_t s) {
 }
 
 // Tile plans.  kStreamBM: the streaming kernel with BM-row tiles when every
-// K fits its LDS budget (else the pipelined kernel with 32- or 64-row
-// tiles); kTiled64: the pipelined kernel with 64-row tiles.
-enum class TilePlan { kStream16, kStream32, kTiled64 };
+// K fits its LDS budget, else the pipelined kernel with 32-row tiles.
+enum class TilePlan { kStream16, kStream32 };
 
 template <TilePlan PLAN>
 hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t* hidden,
@@ -817,27 +816,19 @@ hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t*
     n_max = args.dim;
   }
   const int k_max = phase == 1 ? args.dim : max(args.hidden_dim, args.shared_dim);
-  if constexpr (PLAN != TilePlan::kTiled64) {
-    constexpr int BM = PLAN == TilePlan::kStream16 ? 16 : 32;
-    if (k_max <= kStreamKCap) return run_stream<BM>(phase, args, n_max, s);
-    return launch_phase<32, 128, 3>(phase, args, n_max, s);
-  } else {
-    return launch_phase<64, 128, 3>(phase, args, n_max, s);
-  }
+  constexpr int BM = PLAN == TilePlan::kStream16 ? 16 : 32;
+  if (k_max <= kStreamKCap) return run_stream<BM>(phase, args, n_max, s);
+  return launch_phase<32, 128, 3>(phase, args, n_max, s);
 }
 
-// Kernel and row tile per launch, chosen from T and E only (the per-expert
-// counts stay on the device).  Measured on MI355X: while an expert holds up
-// to ~3 x 32 rows the launch is weight-streaming bound and the streaming
-// kernel with 32-row tiles is fastest (more, smaller workgroups keep more
-// weight loads in flight, and the re-streamed tiles of one expert mostly hit
-// L2); with more rows per expert the pipelined kernel with 64-row tiles and a
-// 3-stage ring (two workgroups per CU) is.
-TilePlan experts_tile_plan(int64_t tokens, int experts) {
-  const int64_t per_expert = (2 * tokens + experts - 1) / experts;
-  if (tokens <= 16) return TilePlan::kStream16;
-  if (per_expert <= 96) return TilePlan::kStream32;
-  return TilePlan::kTiled64;
+// Kernel and row tile per launch, chosen from T only (the per-expert counts
+// stay on the device).  Measured on MI355X (E = 16 and 32, T = 1024 ...
+// 16384, and BASELINE config 3): the streaming kernel with 32-row tiles beats
+// the pipelined kernel with 64-row tiles at every size, by 10-35 % (config 3:
+// gate/up 53.7 -> 46.2 us, down 41.8 -> 36.0 us); 128-row and 256-column
+// pipelined tiles and 64-row streaming tiles were slower still.
+TilePlan experts_tile_plan(int64_t tokens) {
+  return tokens <= 16 ? TilePlan::kStream16 : TilePlan::kStream32;
 }
 
 }  // namespace
@@ -845,7 +836,8 @@ TilePlan experts_tile_plan(int64_t tokens, int experts) {
 bool experts_group_in_kernel(int64_t tokens, int dim, int experts, int hidden_dim,
                              int shared_dim) {
   if (tokens < 1 || 2 * tokens > kGroupMaxAssign || experts > kMaxExperts) return false;
-  if (experts_tile_plan(tokens, experts) == TilePlan::kTiled64) return false;
+  // Up to ~3 x 32 rows per expert on average (the shapes it was measured at).
+  if ((2 * tokens + experts - 1) / experts > 96) return false;
   return dim <= kStreamKCap && max(hidden_dim, shared_dim) <= kStreamKCap;
 }
 
@@ -879,11 +871,9 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
     args.offsets_out = map.offsets_out;
     args.sorted_out = map.sorted_out;
   }
-  switch (experts_tile_plan(tokens, experts)) {
-    case TilePlan::kStream16: return run_phase<TilePlan::kStream16>(phase, args, w, hidden, s);
-    case TilePlan::kStream32: return run_phase<TilePlan::kStream32>(phase, args, w, hidden, s);
-    default: return run_phase<TilePlan::kTiled64>(phase, args, w, hidden, s);
-  }
+  if (experts_tile_plan(tokens) == TilePlan::kStream16)
+    return run_phase<TilePlan::kStream16>(phase, args, w, hidden, s);
+  return run_phase<TilePlan::kStream32>(phase, args, w, hidden, s);
 }
 
 }  // namespace parrot

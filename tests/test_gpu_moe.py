@@ -119,7 +119,7 @@ def test_moe_layer(name, tokens, experts, skewed):
 
 @pytest.mark.parametrize("tokens,experts,dim,hidden,shared", [
     (40, 8, 1024, 1280, 256),     # small-T plan with K > 768: pipelined 32-row tiles
-    (1200, 8, 1024, 1280, 256),   # many rows per expert: pipelined 64-row tiles
+    (1200, 8, 1024, 1280, 256),   # many rows per expert, K > 768: pipelined 32-row tiles
     (300, 4, 2048, 512, 192),     # widest supported dim
 ])
 def test_moe_layer_other_widths(tokens, experts, dim, hidden, shared):
