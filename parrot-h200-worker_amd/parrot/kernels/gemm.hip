@@ -535,7 +535,13 @@ constexpr int kStreamKCap = 768;  // largest K whose A tile fits the LDS budget
 // started its last quarter of workgroups only when the first ones ended
 // (measured on MI355X: last workgroup start 4.2 us after the first, launch
 // 8.6 -> 7.2 us without the cap; LDS alone allows three per CU).
-template <int BM, int WN, int PF, int PHASE>
+//
+// KCH > 1 splits the A tile along k into KCH chunks that take turns in the
+// same LDS buffer (K % (64 KCH) == 0): 64-row tiles then fit the 32-row
+// tile's LDS budget, and every weight fragment loaded feeds twice the rows.
+// At the chunk boundary the workgroup waits for the next chunk's rows while
+// the weight ring keeps streaming.
+template <int BM, int WN, int PF, int PHASE, int KCH = 1>
 __global__ __launch_bounds__(256)
 void grouped_gemm_stream_kernel(GemmArgs p) {
   constexpr int kTilesM = BM / 16;
@@ -543,7 +549,7 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
   constexpr int BN = 4 * WN;
   static_assert(PHASE != 1 || WN == 32, "gate/up pairs need 32 columns per wavefront");
 
-  __shared__ __attribute__((aligned(16))) uint16_t a_lds[BM * kStreamKCap];
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[BM * kStreamKCap / KCH];
   __shared__ int row_src[BM];
   __shared__ int row_dst[BM];
   __shared__ int hist_s[4][kMaxExperts];
@@ -578,9 +584,10 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
   const int n0 = static_cast<int>(blockIdx.x) * BN;
   if (n0 >= N) return;
 
-  const int chunks = K / 8;                       // 16-byte chunks per A row
+  const int chunks = K / 8 / KCH;                 // 16-byte chunks per A row (per k chunk)
   const int swz = (chunks & 15) == 0 ? 15 : 7;   // XOR group size - 1
   const int ksteps = K / 32;
+  const int ksteps_c = ksteps / KCH;             // k steps per A chunk
 
   // ---- row ids: issued first, so waiting for them waits for no weight load
   // Phase 1 gathers x rows by token (through the slot map) and writes hidden
@@ -621,8 +628,8 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
     __syncthreads();
   }
 
-  // ---- A: the whole tile, direct to LDS ------------------------------------
-  {
+  // ---- A: the whole tile (or its first k chunk), direct to LDS -------------
+  auto gather_a = [&](int kc) {
     const int a_ld = PHASE == 1 ? p.dim : p.hstride;
     const int slots = BM * chunks;  // multiple of 64 (BM >= 16, chunks >= 8)
     for (int i = wave; i < slots / kWave; i += 4) {
@@ -631,10 +638,11 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
       const int pc = slot - r * chunks;
       const int c = (pc & ~swz) | ((pc ^ r) & swz);
       const int src = PHASE == 1 ? row_src[r] : t.hbase + segment_row(t, BM, r);
-      const uint16_t* g = p.a_src + static_cast<int64_t>(src) * a_ld + c * 8;
+      const uint16_t* g = p.a_src + static_cast<int64_t>(src) * a_ld + kc * (K / KCH) + c * 8;
       __builtin_amdgcn_global_load_lds(g, (lds_void_t*)(a_lds + i * kWave * 8), 16, 0, 0);
     }
-  }
+  };
+  gather_a(0);
   if (PHASE == 2 && tid < BM) row_dst[tid] = t.mt * BM + tid < t.rows ? (shared ? sc : asg) : -1;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -671,17 +679,28 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < kTilesN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  int chunk_base = 0, chunk_end = ksteps_c;  // k steps of the A chunk in LDS
   // One k step on ring slot i: A fragments from LDS, the MFMAs, then the
   // slot's refill with step + PF unless the ring already holds the last
   // steps.  The final pass is peeled off so it issues no loads: refills of
   // steps past the end (reloads of the last one, to keep the loop uniform)
   // cost a full memory round trip before the kernel could finish.
   auto k_step = [&](int step, int i, bool refill) {
+    if (KCH > 1 && step == chunk_end) {
+      // Every wavefront is done with the A chunk in LDS: the next replaces it.
+      chunk_base = chunk_end;
+      chunk_end += ksteps_c;
+      __syncthreads();
+      gather_a(chunk_base / ksteps_c);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+    const int sl = step - chunk_base;  // k step within the A chunk in LDS
     bf16x8 af[kTilesM];
 #pragma unroll
     for (int mi = 0; mi < kTilesM; ++mi) {
       const int r = mi * 16 + (lane & 15);
-      const int c = step * 4 + (lane >> 4);
+      const int c = sl * 4 + (lane >> 4);
       const int pc = (c & ~swz) | ((c ^ r) & swz);
       af[mi] = *reinterpret_cast<const bf16x8*>(&a_lds[(r * chunks + pc) * 8]);
     }
@@ -758,13 +777,13 @@ hipError_t launch_phase(int phase, const GemmArgs& args, int n_max, hipStream_t 
   return hipGetLastError();
 }
 
-template <int BM, int WN, int PF>
+template <int BM, int WN, int PF, int KCH>
 hipError_t launch_stream(int phase, const GemmArgs& args, int n_max, hipStream_t s) {
   const int T = static_cast<int>(args.tokens);
   const int m_tiles = (T + BM - 1) / BM + (2 * T) / BM + args.experts;
   const dim3 grid((n_max + 4 * WN - 1) / (4 * WN), m_tiles);
-  if (phase == 1) grouped_gemm_stream_kernel<BM, 32, PF, 1><<<grid, 256, 0, s>>>(args);
-  else grouped_gemm_stream_kernel<BM, WN, PF, 2><<<grid, 256, 0, s>>>(args);
+  if (phase == 1) grouped_gemm_stream_kernel<BM, 32, PF, 1, KCH><<<grid, 256, 0, s>>>(args);
+  else grouped_gemm_stream_kernel<BM, WN, PF, 2, KCH><<<grid, 256, 0, s>>>(args);
   return hipGetLastError();
 }
 
@@ -780,25 +799,27 @@ int stream_depth(int phase, const GemmArgs& a) {
   return 1;
 }
 
-template <int BM>
+template <int BM, int KCH>
 hipError_t run_stream(int phase, GemmArgs args, int n_max, hipStream_t s) {
   // Down projection: 16 columns per wavefront doubles the workgroups when
   // the row tiles are few.
   switch (stream_depth(phase, args)) {
-    case 8: return phase == 1 ? launch_stream<BM, 32, 8>(1, args, n_max, s)
-                              : launch_stream<BM, 16, 8>(2, args, n_max, s);
-    case 4: return phase == 1 ? launch_stream<BM, 32, 4>(1, args, n_max, s)
-                              : launch_stream<BM, 16, 4>(2, args, n_max, s);
-    case 2: return phase == 1 ? launch_stream<BM, 32, 2>(1, args, n_max, s)
-                              : launch_stream<BM, 16, 2>(2, args, n_max, s);
-    default: return phase == 1 ? launch_stream<BM, 32, 1>(1, args, n_max, s)
-                               : launch_stream<BM, 16, 1>(2, args, n_max, s);
+    case 8: return phase == 1 ? launch_stream<BM, 32, 8, KCH>(1, args, n_max, s)
+                              : launch_stream<BM, 16, 8, KCH>(2, args, n_max, s);
+    case 4: return phase == 1 ? launch_stream<BM, 32, 4, KCH>(1, args, n_max, s)
+                              : launch_stream<BM, 16, 4, KCH>(2, args, n_max, s);
+    case 2: return phase == 1 ? launch_stream<BM, 32, 2, KCH>(1, args, n_max, s)
+                              : launch_stream<BM, 16, 2, KCH>(2, args, n_max, s);
+    default: return phase == 1 ? launch_stream<BM, 32, 1, KCH>(1, args, n_max, s)
+                               : launch_stream<BM, 16, 1, KCH>(2, args, n_max, s);
   }
 }
 
 // Tile plans.  kStreamBM: the streaming kernel with BM-row tiles when every
-// K fits its LDS budget, else the pipelined kernel with 32-row tiles.
-enum class TilePlan { kStream16, kStream32 };
+// K fits its LDS budget (64-row tiles in two k chunks, when every K splits
+// into 128-element halves; else 32-row tiles), else the pipelined kernel
+// with 32-row tiles.
+enum class TilePlan { kStream16, kStream32, kStream64 };
 
 template <TilePlan PLAN>
 hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t* hidden,
@@ -816,19 +837,28 @@ hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t*
     n_max = args.dim;
   }
   const int k_max = phase == 1 ? args.dim : max(args.hidden_dim, args.shared_dim);
-  constexpr int BM = PLAN == TilePlan::kStream16 ? 16 : 32;
-  if (k_max <= kStreamKCap) return run_stream<BM>(phase, args, n_max, s);
-  return launch_phase<32, 128, 3>(phase, args, n_max, s);
+  if (k_max > kStreamKCap) return launch_phase<32, 128, 3>(phase, args, n_max, s);
+  if constexpr (PLAN == TilePlan::kStream64) {
+    const bool halves = phase == 1 ? args.dim % 128 == 0
+                                   : args.hidden_dim % 128 == 0 && args.shared_dim % 128 == 0;
+    if (halves) return run_stream<64, 2>(phase, args, n_max, s);
+  }
+  return run_stream<PLAN == TilePlan::kStream16 ? 16 : 32, 1>(phase, args, n_max, s);
 }
 
-// Kernel and row tile per launch, chosen from T only (the per-expert counts
-// stay on the device).  Measured on MI355X (E = 16 and 32, T = 1024 ...
-// 16384, and BASELINE config 3): the streaming kernel with 32-row tiles beats
-// the pipelined kernel with 64-row tiles at every size, by 10-35 % (config 3:
-// gate/up 53.7 -> 46.2 us, down 41.8 -> 36.0 us); 128-row and 256-column
-// pipelined tiles and 64-row streaming tiles were slower still.
-TilePlan experts_tile_plan(int64_t tokens) {
-  return tokens <= 16 ? TilePlan::kStream16 : TilePlan::kStream32;
+// Kernel and row tile per launch, chosen from T and E only (the per-expert
+// counts stay on the device).  Measured on MI355X (E = 16 and 32, T = 1024
+// ... 16384, and BASELINE config 3): the streaming kernel beats the pipelined
+// kernel with 64-row tiles at every size, by 10-35 % with 32-row tiles
+// (config 3: gate/up 53.7 -> 46.2 us, down 41.8 -> 36.0 us); 128-row and
+// 256-column pipelined tiles were slower still.  Past ~3 x 32 rows per
+// expert the weight fragments' trips from L2 set the pace (each 32-row tile
+// of an expert re-reads its weights), and 64-row tiles in two k chunks halve
+// them.
+TilePlan experts_tile_plan(int64_t tokens, int experts) {
+  const int64_t per_expert = (2 * tokens + experts - 1) / experts;
+  if (tokens <= 16) return TilePlan::kStream16;
+  return per_expert <= 96 ? TilePlan::kStream32 : TilePlan::kStream64;
 }
 
 }  // namespace
@@ -871,9 +901,11 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
     args.offsets_out = map.offsets_out;
     args.sorted_out = map.sorted_out;
   }
-  if (experts_tile_plan(tokens) == TilePlan::kStream16)
-    return run_phase<TilePlan::kStream16>(phase, args, w, hidden, s);
-  return run_phase<TilePlan::kStream32>(phase, args, w, hidden, s);
+  switch (experts_tile_plan(tokens, experts)) {
+    case TilePlan::kStream16: return run_phase<TilePlan::kStream16>(phase, args, w, hidden, s);
+    case TilePlan::kStream32: return run_phase<TilePlan::kStream32>(phase, args, w, hidden, s);
+    default: return run_phase<TilePlan::kStream64>(phase, args, w, hidden, s);
+  }
 }
 
 }  // namespace parrot
