@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 5
+#define PARROT_ABI_VERSION 6
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -165,6 +165,33 @@ int parrot_decode_attention_latent_f32(const float* q, const void* latent_new, v
                                        const int32_t* position, int32_t batch, int32_t heads,
                                        int32_t latent_dim, int32_t max_positions, float scale,
                                        float* out, void* stream);
+
+/* The MLA layers' decode-step projections before the latent attention, one
+ * launch: q_latent [tokens, query_rows] fp32 = x . absorbed_query^T with x
+ * [tokens, dim] bf16 and absorbed_query [query_rows, dim] bf16 (the absorbed
+ * query map, H * latent_dim rows), products and sums in fp32; latent
+ * [tokens, latent_dim] bf16 = bf16(x . kv_down^T), kv_down [latent_dim, dim]
+ * bf16.  tokens <= 16, dim % 128 == 0 and dim <= 2048, query_rows and
+ * latent_dim multiples of 16; x, absorbed_query and kv_down 16-byte aligned.
+ * Replaces F.linear(x.float(), absorbed_query.float()) and kv_down(x) in
+ * GlobalMLA.decode (parrot/model.py:417-422), the projections that
+ * metal_mla_attention_decode (parrot/metal_moe.py:293-326) fuses. */
+int parrot_mla_decode_in_bf16(const void* x, int32_t tokens, int32_t dim,
+                              const void* absorbed_query, int32_t query_rows,
+                              const void* kv_down, int32_t latent_dim, float* q_latent,
+                              void* latent, void* stream);
+
+/* The MLA layers' decode-step output projection after the latent attention:
+ * out [tokens, dim] bf16 = bf16(context . absorbed_output^T), then
+ * bf16(addend + that) when addend [tokens, dim] bf16 is given; context
+ * [tokens, width] fp32, absorbed_output [dim, width] bf16, fp32 products and
+ * sums.  tokens <= 16, width % 128 == 0, tokens * width * 4 <= 65536, dim %
+ * 16 == 0; context and absorbed_output 16-byte aligned.  Replaces
+ * F.linear(context, absorbed_output.float()).to(bf16) and the addend sum in
+ * GlobalMLA.decode (parrot/model.py:430-431). */
+int parrot_mla_decode_out_bf16(const float* context, int32_t tokens, int32_t width,
+                               const void* absorbed_output, int32_t dim, const void* addend,
+                               void* out, void* stream);
 
 /* Workspace bytes of parrot_decode_moe_bf16: hidden rows [3T, max(H, Hs)]
  * bf16. */

@@ -777,6 +777,57 @@ def decode_attention(q: Tensor, k_new: Tensor, v_new: Tensor, key_cache: Tensor,
     return out
 
 
+MLA_DECODE_MAX_TOKENS = 16
+
+
+def mla_decode_supported(tokens: int, dim: int, width: int) -> bool:
+    """Shapes parrot_mla_decode_in/out_bf16 take (width = heads x latent)."""
+    return (1 <= tokens <= MLA_DECODE_MAX_TOKENS and dim % 128 == 0 and dim <= 2048
+            and width % 128 == 0 and width <= 2048 and tokens * width * 4 <= 65536)
+
+
+def mla_decode_in(x: Tensor, absorbed_query: Tensor, kv_down: Tensor) -> tuple[Tensor, Tensor]:
+    """The MLA decode step's projections in one launch: x [b, 1, dim] bf16 ->
+    (q_latent [b, H * r] fp32 = x.float() absorbed_query.float()^T,
+    latent [b, 1, r] bf16 = kv_down(x)); cf. parrot/model.py:417-422."""
+    _require(x, "HIP MLA decode projections")
+    b, dim = x.shape[0], x.shape[-1]
+    for w in (absorbed_query, kv_down):
+        if w.dtype != x.dtype or not w.is_contiguous() or w.shape[-1] != dim:
+            raise RuntimeError("MLA decode weights must be contiguous [rows, dim] in x's dtype")
+    x2 = x.reshape(b, dim).contiguous()
+    q = torch.empty((b, absorbed_query.shape[0]), dtype=torch.float32, device=x.device)
+    latent = torch.empty((b, 1, kv_down.shape[0]), dtype=x.dtype, device=x.device)
+    _abi.check(_abi.load().parrot_mla_decode_in_bf16(
+        ptr(x2), b, dim, ptr(absorbed_query), absorbed_query.shape[0], ptr(kv_down),
+        kv_down.shape[0], ptr(q), ptr(latent), _stream(x.device)), "parrot_mla_decode_in_bf16")
+    return q, latent
+
+
+def mla_decode_out(context: Tensor, absorbed_output: Tensor,
+                   addend: Tensor | None = None) -> Tensor:
+    """bf16(context absorbed_output.float()^T) [b, 1, dim] (+ addend, a bf16
+    sum) in one launch; context [b, H * r] fp32; cf.
+    parrot/model.py:430-431."""
+    if context.dtype != torch.float32 or context.device.type != "cuda":
+        raise RuntimeError("HIP MLA decode output takes an fp32 ROCm context")
+    _require(absorbed_output, "HIP MLA decode output")
+    b, width = context.shape
+    dim = absorbed_output.shape[0]
+    if not absorbed_output.is_contiguous() or absorbed_output.shape[1] != width:
+        raise RuntimeError("absorbed output map must be contiguous [dim, heads x latent]")
+    context = context.contiguous()
+    out = torch.empty((b, 1, dim), dtype=absorbed_output.dtype, device=context.device)
+    if addend is not None:
+        if addend.shape != out.shape or addend.dtype != out.dtype:
+            raise RuntimeError("addend must match the [b, 1, dim] output")
+        addend = addend.contiguous()
+    _abi.check(_abi.load().parrot_mla_decode_out_bf16(
+        ptr(context), b, width, ptr(absorbed_output), dim, ptr(addend), ptr(out),
+        _stream(context.device)), "parrot_mla_decode_out_bf16")
+    return out
+
+
 def decode_attention_latent(q: Tensor, latent_new: Tensor, latent_cache: Tensor,
                             position: Tensor, heads: int, scale: float) -> Tensor:
     """One MLA decode step over the latent cache: store latent_new [b, 1, r]

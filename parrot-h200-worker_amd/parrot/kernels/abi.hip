@@ -238,6 +238,44 @@ int parrot_decode_attention_latent_f32(const float* q, const void* latent_new, v
       position, batch, heads, latent_dim, max_positions, scale, out, as_stream(stream)));
 }
 
+// Shapes of the MLA decode projections: up to 16 tokens, K a multiple of
+// 128 up to 2048, row counts multiples of 16, the staged input within 64 KB.
+static int check_mla_decode(int32_t tokens, int32_t k, int elem_bytes) {
+  if (tokens < 0 || k <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (tokens > 16 || k % 128 || k > 2048) return PARROT_ERR_UNSUPPORTED;
+  if (parrot::mla_decode_lds_bytes(tokens, k, elem_bytes) > 65536) return PARROT_ERR_UNSUPPORTED;
+  return PARROT_OK;
+}
+
+int parrot_mla_decode_in_bf16(const void* x, int32_t tokens, int32_t dim,
+                              const void* absorbed_query, int32_t query_rows,
+                              const void* kv_down, int32_t latent_dim, float* q_latent,
+                              void* latent, void* stream) {
+  if (!x || !absorbed_query || !kv_down || !q_latent || !latent) return PARROT_ERR_NULL_POINTER;
+  if (int rc = check_mla_decode(tokens, dim, 2)) return rc;
+  if (query_rows <= 0 || latent_dim <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (query_rows % 16 || latent_dim % 16) return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(absorbed_query) || !aligned16(kv_down))
+    return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_mla_decode_in(
+      static_cast<const uint16_t*>(x), tokens, dim, static_cast<const uint16_t*>(absorbed_query),
+      query_rows, static_cast<const uint16_t*>(kv_down), latent_dim, q_latent,
+      static_cast<uint16_t*>(latent), as_stream(stream)));
+}
+
+int parrot_mla_decode_out_bf16(const float* context, int32_t tokens, int32_t width,
+                               const void* absorbed_output, int32_t dim, const void* addend,
+                               void* out, void* stream) {
+  if (!context || !absorbed_output || !out) return PARROT_ERR_NULL_POINTER;
+  if (int rc = check_mla_decode(tokens, width, 4)) return rc;
+  if (dim <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (dim % 16) return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(context) || !aligned16(absorbed_output)) return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_mla_decode_out(
+      context, tokens, width, static_cast<const uint16_t*>(absorbed_output), dim,
+      static_cast<const uint16_t*>(addend), static_cast<uint16_t*>(out), as_stream(stream)));
+}
+
 size_t parrot_route_workspace_bytes(int64_t tokens, int32_t experts) {
   if (tokens < 0 || experts <= 0) return 0;
   return route_ws_bytes(tokens, experts);

@@ -360,6 +360,12 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_new,
                                    const int32_t* position, int batch, int heads, int kv_heads,
                                    int head_dim, int max_pos, int window, float scale,
                                    uint16_t* out, hipStream_t s);
+size_t mla_decode_lds_bytes(int tokens, int k, int elem_bytes);
+hipError_t launch_mla_decode_in(const uint16_t* x, int tokens, int dim, const uint16_t* wq,
+                                int nq, const uint16_t* wkv, int nl, float* q_out,
+                                uint16_t* lat_out, hipStream_t s);
+hipError_t launch_mla_decode_out(const float* ctx, int tokens, int width, const uint16_t* wo,
+                                 int dim, const uint16_t* addend, uint16_t* out, hipStream_t s);
 hipError_t launch_decode_attention_latent(const float* q, const uint16_t* latent_new,
                                           uint16_t* latent_cache, const int32_t* position,
                                           int batch, int heads, int latent_dim, int max_pos,

@@ -1,0 +1,164 @@
+// The MLA layers' decode-step projections around the latent attention
+// (parrot_decode_attention_latent_f32), for up to 16 tokens.
+//
+// Reference semantics (parrot/model.py:399-432, the absorbed decode path):
+//   latent   = kv_down(x)                                    bf16 [T, r]
+//   q_latent = F.linear(x.float(), absorbed_query.float())   fp32 [T, H r]
+//   result   = F.linear(context, absorbed_output.float()).to(bf16)
+//   out      = addend + result (bf16 add) when an addend is given
+// where absorbed_query [H r, dim] and absorbed_output [dim, H r] are the bf16
+// absorbed maps (parrot/model.py:366-397).  Every product is exact in fp32
+// (bf16 operands, or fp32 context times a bf16 weight) and the sums are fp32,
+// so the results differ from a library GEMM only by the order of the fp32
+// additions.
+//
+// Each is a weight stream (1.5 MB for either absorbed map at the default
+// widths) that a library GEMM runs as several launches plus dtype copies.
+// Here one launch each: a workgroup owns 16 output rows, one per 16-lane DPP
+// row; lane p of a row holds the row's 16-byte weight chunks p, p + 16, ...
+// (256 contiguous bytes per instruction across the row) in registers, the
+// tokens' inputs are staged in LDS once, and each token's 16 partial sums are
+// added by four DPP steps in a fixed order.
+#include "common.h"
+
+namespace parrot {
+
+namespace {
+
+constexpr int kGemvRows = 16;        // output rows per workgroup
+constexpr int kGemvMaxChunks = 16;   // 16-byte weight chunks per lane: K <= 2048
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  v += dpp<0x140>(v);  // row_mirror
+  return v;
+}
+
+__device__ __forceinline__ float dot_bf16x8(uint4 w, uint4 x) {
+  float s = lo_bf16(w.x) * lo_bf16(x.x);
+  s += hi_bf16(w.x) * hi_bf16(x.x);
+  s += lo_bf16(w.y) * lo_bf16(x.y);
+  s += hi_bf16(w.y) * hi_bf16(x.y);
+  s += lo_bf16(w.z) * lo_bf16(x.z);
+  s += hi_bf16(w.z) * hi_bf16(x.z);
+  s += lo_bf16(w.w) * lo_bf16(x.w);
+  s += hi_bf16(w.w) * hi_bf16(x.w);
+  return s;
+}
+
+__device__ __forceinline__ float dot_f32x8(uint4 w, float4 x0, float4 x1) {
+  float s = lo_bf16(w.x) * x0.x;
+  s += hi_bf16(w.x) * x0.y;
+  s += lo_bf16(w.y) * x0.z;
+  s += hi_bf16(w.y) * x0.w;
+  s += lo_bf16(w.z) * x1.x;
+  s += hi_bf16(w.z) * x1.y;
+  s += lo_bf16(w.w) * x1.z;
+  s += hi_bf16(w.w) * x1.w;
+  return s;
+}
+
+// Lane p's weight chunks of row `row` ([rows, K] bf16), issued at once.
+__device__ __forceinline__ void load_row_chunks(const uint16_t* w, int row, int K, int p,
+                                                uint4 (&wr)[kGemvMaxChunks]) {
+  const int nch = K / 128;
+  const uint4* src = reinterpret_cast<const uint4*>(w + static_cast<int64_t>(row) * K);
+#pragma unroll
+  for (int c = 0; c < kGemvMaxChunks; ++c)
+    wr[c] = c < nch ? src[c * 16 + p] : make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Copies `bytes` (a multiple of 16) from global memory into LDS.
+__device__ __forceinline__ void stage(const void* src, void* lds, int bytes) {
+  const uint4* s = static_cast<const uint4*>(src);
+  uint4* d = static_cast<uint4*>(lds);
+  for (int i = threadIdx.x; i < bytes / 16; i += blockDim.x) d[i] = s[i];
+}
+
+// Workgroups [0, nq / 16): q_latent rows of absorbed_query; the rest: latent
+// rows of kv_down.  x [T, K] bf16 is staged in LDS (T K 2 bytes).
+__global__ __launch_bounds__(256) void mla_decode_in_kernel(
+    const uint16_t* __restrict__ x, int tokens, int K, const uint16_t* __restrict__ wq, int nq,
+    const uint16_t* __restrict__ wkv, int nl, float* __restrict__ q_out,
+    uint16_t* __restrict__ lat_out) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  const int j = threadIdx.x >> 4, p = threadIdx.x & 15;
+  const int blocks_q = nq / kGemvRows;
+  const bool is_q = static_cast<int>(blockIdx.x) < blocks_q;  // uniform
+  const int row = (is_q ? blockIdx.x : blockIdx.x - blocks_q) * kGemvRows + j;
+  uint4 wr[kGemvMaxChunks];
+  load_row_chunks(is_q ? wq : wkv, row, K, p, wr);
+  stage(x, xs, tokens * K * 2);
+  __syncthreads();
+  const int nch = K / 128;
+  for (int t = 0; t < tokens; ++t) {
+    const uint4* xt = reinterpret_cast<const uint4*>(xs + t * K);
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kGemvMaxChunks; ++c)
+      if (c < nch) acc += dot_bf16x8(wr[c], xt[c * 16 + p]);
+    acc = row16_sum(acc);
+    if (p == 0) {
+      if (is_q) q_out[static_cast<int64_t>(t) * nq + row] = acc;
+      else lat_out[static_cast<int64_t>(t) * nl + row] = f32_to_bf16(acc);
+    }
+  }
+}
+
+// out [T, n] = bf16(context Wo^T) (+ addend, a second bf16 rounding);
+// context [T, K] fp32 is staged in LDS (T K 4 bytes).
+__global__ __launch_bounds__(256) void mla_decode_out_kernel(
+    const float* __restrict__ ctx, int tokens, int K, const uint16_t* __restrict__ wo, int n,
+    const uint16_t* __restrict__ addend, uint16_t* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) float cs[];
+  const int j = threadIdx.x >> 4, p = threadIdx.x & 15;
+  const int row = blockIdx.x * kGemvRows + j;
+  uint4 wr[kGemvMaxChunks];
+  load_row_chunks(wo, row, K, p, wr);
+  stage(ctx, cs, tokens * K * 4);
+  __syncthreads();
+  const int nch = K / 128;
+  for (int t = 0; t < tokens; ++t) {
+    const float4* ct = reinterpret_cast<const float4*>(cs + t * K);
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kGemvMaxChunks; ++c)
+      if (c < nch) acc += dot_f32x8(wr[c], ct[2 * (c * 16 + p)], ct[2 * (c * 16 + p) + 1]);
+    acc = row16_sum(acc);
+    if (p == 0) {
+      const int64_t o = static_cast<int64_t>(t) * n + row;
+      uint16_t v = f32_to_bf16(acc);
+      if (addend != nullptr) v = f32_to_bf16(bf16_to_f32(addend[o]) + bf16_to_f32(v));
+      out[o] = v;
+    }
+  }
+}
+
+}  // namespace
+
+size_t mla_decode_lds_bytes(int tokens, int k, int elem_bytes) {
+  return static_cast<size_t>(tokens) * k * elem_bytes;
+}
+
+hipError_t launch_mla_decode_in(const uint16_t* x, int tokens, int dim, const uint16_t* wq,
+                                int nq, const uint16_t* wkv, int nl, float* q_out,
+                                uint16_t* lat_out, hipStream_t s) {
+  if (tokens == 0) return hipSuccess;
+  const dim3 grid((nq + nl) / kGemvRows);
+  mla_decode_in_kernel<<<grid, 256, mla_decode_lds_bytes(tokens, dim, 2), s>>>(
+      x, tokens, dim, wq, nq, wkv, nl, q_out, lat_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_mla_decode_out(const float* ctx, int tokens, int width, const uint16_t* wo,
+                                 int dim, const uint16_t* addend, uint16_t* out, hipStream_t s) {
+  if (tokens == 0) return hipSuccess;
+  const dim3 grid(dim / kGemvRows);
+  mla_decode_out_kernel<<<grid, 256, mla_decode_lds_bytes(tokens, width, 4), s>>>(
+      ctx, tokens, width, wo, dim, addend, out);
+  return hipGetLastError();
+}
+
+}  // namespace parrot

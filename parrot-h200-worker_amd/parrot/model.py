@@ -543,6 +543,16 @@ class GlobalMLA(nn.Module):
             # One kernel stores the new latent and attends over the latent
             # cache at the device position (parrot/model.py:399-432).
             from . import hip_moe
+            width = c.n_heads * c.kv_latent_dim
+            if (hip_moe.mla_decode_supported(b, c.dim, width)
+                    and self.kv_down.weight.dtype == x.dtype):
+                # Three launches: projections, latent attention, output map.
+                absorbed_q, absorbed_o = self._absorbed()
+                q_latent, latent = hip_moe.mla_decode_in(x, absorbed_q, self.kv_down.weight)
+                context = hip_moe.decode_attention_latent(
+                    q_latent, latent, cache.latent, position_device, c.n_heads,
+                    c.head_dim ** -0.5)
+                return hip_moe.mla_decode_out(context, absorbed_o, addend)
             absorbed_q, absorbed_o = self._absorbed_f32()
             context = hip_moe.decode_attention_latent(
                 F.linear(x.float(), absorbed_q), self.kv_down(x), cache.latent, position_device,

@@ -137,6 +137,24 @@ def test_argument_validation_without_gpu(lib):
                                                   fake, null) == -1
     assert lib.parrot_decode_attention_latent_f32(fake, fake, fake, fake, 2, 8, 128, 1 << 16,
                                                   0.1, fake, null) == -3
+    # MLA decode projections: tokens <= 16, K % 128 <= 2048, rows % 16,
+    # staged input <= 64 KB, alignment
+    mla_in = lambda **kw: lib.parrot_mla_decode_in_bf16(*[kw.get(k, v) for k, v in (
+        ("x", fake), ("tokens", 2), ("dim", 768), ("wq", fake), ("nq", 1024), ("wkv", fake),
+        ("nl", 128), ("q", fake), ("lat", fake), ("stream", null))])
+    assert mla_in(x=null) == -1 and mla_in(lat=null) == -1
+    assert mla_in(tokens=-1) == -2 and mla_in(nq=0) == -2
+    assert mla_in(tokens=17) == -3 and mla_in(dim=704) == -3 and mla_in(dim=2176) == -3
+    assert mla_in(nq=1000) == -3 and mla_in(nl=120) == -3
+    assert mla_in(wq=fake + 8) == -5
+    mla_out = lambda **kw: lib.parrot_mla_decode_out_bf16(*[kw.get(k, v) for k, v in (
+        ("ctx", fake), ("tokens", 2), ("width", 1024), ("wo", fake), ("dim", 768),
+        ("addend", null), ("out", fake), ("stream", null))])
+    assert mla_out(ctx=null) == -1 and mla_out(out=null) == -1
+    assert mla_out(dim=0) == -2
+    assert mla_out(width=1000) == -3 and mla_out(dim=760) == -3
+    assert mla_out(tokens=16, width=2048) == -3  # 128 KB of staged context
+    assert mla_out(wo=fake + 4) == -5
     # dense projections: k % 64, k <= 2048, n % 16, strides and alignment
     assert lib.parrot_proj_bf16(null, 4, 768, 768, fake, 768, null, 0, fake, 768, null) == -1
     assert lib.parrot_proj_bf16(fake, 4, 96, 96, fake, 768, null, 0, fake, 768, null) == -3

@@ -84,6 +84,45 @@ def test_decode_attention_latent(position):
     assert (got - ref).abs().max() <= 1e-4 * ref.abs().max() + 1e-5
 
 
+@pytest.mark.parametrize("tokens,with_addend", [(1, True), (3, False), (8, True), (16, True)])
+def test_mla_decode_projections(tokens, with_addend):
+    """The MLA decode projections around the latent attention against fp32 CPU
+    products of the same bf16 weights (parrot/model.py:417-431)."""
+    from parrot import hip_moe
+    dim, heads, r = 768, 8, 128
+    width = heads * r
+    _say(f"mla decode projections T={tokens} addend={with_addend}")
+    g = torch.Generator().manual_seed(40 + tokens)
+    x = torch.randn(tokens, 1, dim, generator=g).bfloat16()
+    wq = (torch.randn(width, dim, generator=g) * 0.05).bfloat16()
+    wkv = (torch.randn(r, dim, generator=g) * 0.05).bfloat16()
+    wo = (torch.randn(dim, width, generator=g) * 0.05).bfloat16()
+    ctx = torch.randn(tokens, width, generator=g)
+    addend = torch.randn(tokens, 1, dim, generator=g).bfloat16() if with_addend else None
+    with torch.no_grad():
+        q, lat = hip_moe.mla_decode_in(x.cuda(), wq.cuda(), wkv.cuda())
+        out = hip_moe.mla_decode_out(ctx.cuda(), wo.cuda(),
+                                     None if addend is None else addend.cuda())
+    assert q.shape == (tokens, width) and q.dtype == torch.float32
+    assert lat.shape == (tokens, 1, r) and lat.dtype == torch.bfloat16
+    assert out.shape == (tokens, 1, dim) and out.dtype == torch.bfloat16
+    xf = x.float().view(tokens, dim)
+    # fp32 sums of exact products: only the order of additions differs
+    q_ref = xf @ wq.float().T
+    bound = 1e-5 * (xf.abs() @ wq.float().abs().T) + 1e-6
+    assert ((q.cpu() - q_ref).abs() <= bound).all()
+    # one bf16 rounding of an fp32 sum: at most one bf16 step apart
+    lat_ref = (xf @ wkv.float().T).view(tokens, 1, r)
+    assert ((lat.cpu().float() - lat_ref).abs() <= 2 ** -7 * lat_ref.abs() + 1e-6).all()
+    res_ref = (ctx @ wo.float().T).view(tokens, 1, dim)
+    if addend is None:
+        ref, tol = res_ref, 2 ** -7 * res_ref.abs() + 1e-6
+    else:
+        ref = addend.float() + res_ref.bfloat16().float()
+        tol = 2 ** -7 * (addend.float().abs() + 2 * res_ref.abs()) + 1e-6
+    assert ((out.cpu().float() - ref).abs() <= tol).all()
+
+
 def test_decode_graph_matches_eager():
     """DecodeGraph replays decode_next exactly, across MLA and local layers,
     and keeps the state consistent with eager steps in between."""
