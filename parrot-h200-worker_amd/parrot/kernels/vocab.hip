@@ -102,34 +102,66 @@ __global__ __launch_bounds__(256) void vocab_argmax_partials_kernel(
   }
 }
 
+// One workgroup per row of h.  The row's partials are read as float4 / int4,
+// every load of a lane issued before the first compare (a loop with a load,
+// a wait and a compare per partial took ~11 us for 8192 partials), then
+// reduced within each wavefront by xor shuffles and across the 4 wavefronts
+// through LDS.  `better` is a total order (value, then the lower index), so
+// the winner does not depend on the order of comparisons.
+constexpr int kReduceLoads = 8;  // 16-byte loads of each kind in flight per lane
+
+__device__ __forceinline__ void keep_better(float pv, int pi, float& v, int& i) {
+  if (better(pv, pi, v, i)) {
+    v = pv;
+    i = pi;
+  }
+}
+
 __global__ __launch_bounds__(256) void vocab_argmax_reduce_kernel(
     const float* __restrict__ part_v, const int32_t* __restrict__ part_i, int groups,
     int64_t* __restrict__ out) {
-  __shared__ float vs[256];
-  __shared__ int is[256];
+  __shared__ float vs[4];
+  __shared__ int is[4];
   const int r = blockIdx.x;
   const int tid = threadIdx.x;
+  const int n4 = groups / 4;  // groups % 4 == 0
+  const float4* pv4 = reinterpret_cast<const float4*>(part_v + static_cast<int64_t>(r) * groups);
+  const int4* pi4 = reinterpret_cast<const int4*>(part_i + static_cast<int64_t>(r) * groups);
   float v = -INFINITY;
   int i = 0x7fffffff;
-  for (int g = tid; g < groups; g += 256) {
-    const float pv = part_v[static_cast<int64_t>(r) * groups + g];
-    const int pi = part_i[static_cast<int64_t>(r) * groups + g];
-    if (better(pv, pi, v, i)) {
-      v = pv;
-      i = pi;
+  for (int g0 = tid; g0 < n4; g0 += 256 * kReduceLoads) {
+    float4 a[kReduceLoads];
+    int4 b[kReduceLoads];
+#pragma unroll
+    for (int u = 0; u < kReduceLoads; ++u) {
+      const int g = min(g0 + u * 256, n4 - 1);  // clamped: a repeat changes nothing
+      a[u] = pv4[g];
+      b[u] = pi4[g];
+    }
+#pragma unroll
+    for (int u = 0; u < kReduceLoads; ++u) {
+      keep_better(a[u].x, b[u].x, v, i);
+      keep_better(a[u].y, b[u].y, v, i);
+      keep_better(a[u].z, b[u].z, v, i);
+      keep_better(a[u].w, b[u].w, v, i);
     }
   }
-  vs[tid] = v;
-  is[tid] = i;
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const float ov = __shfl_xor(v, m);
+    const int oi = __shfl_xor(i, m);
+    keep_better(ov, oi, v, i);
+  }
+  if ((tid & (kWave - 1)) == 0) {
+    vs[tid >> 6] = v;
+    is[tid >> 6] = i;
+  }
   __syncthreads();
-  for (int stride = 128; stride > 0; stride >>= 1) {
-    if (tid < stride && better(vs[tid + stride], is[tid + stride], vs[tid], is[tid])) {
-      vs[tid] = vs[tid + stride];
-      is[tid] = is[tid + stride];
-    }
-    __syncthreads();
+  if (tid == 0) {
+#pragma unroll
+    for (int w = 1; w < 4; ++w) keep_better(vs[w], is[w], v, i);
+    out[r] = i;
   }
-  if (tid == 0) out[r] = is[0];
 }
 
 }  // namespace
