@@ -220,6 +220,23 @@ int parrot_decode_moe_bf16(const void* x, int64_t tokens, int32_t dim, int32_t e
                            int64_t* out_indices, float* out_weights, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* parrot_decode_moe_bf16 whose input rows it makes itself: x = the depth
+ * mix of `sources` normalised by the MoE's RMSNorm (moe_norm_weight,
+ * norm_eps), exactly as parrot_depth_mix_bf16 with out_norm computes it
+ * (sources, n_sources, query, score_norm_weight and score_eps as there).
+ * Saves that launch at decode.  dim <= 1024; other limits as
+ * parrot_decode_moe_bf16.  Replaces, for a decode step's MoE layer,
+ * metal_depth_mix_norm (parrot/metal_moe.py:455-477) followed by
+ * metal_experts_decode (parrot/metal_moe.py:182-221). */
+int parrot_depth_mix_decode_moe_bf16(
+    const void* const* sources, int32_t n_sources, const void* query,
+    const void* score_norm_weight, float score_eps, const void* moe_norm_weight,
+    float norm_eps, int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
+    int32_t shared_dim, const void* router_weight, const float* logit_bias,
+    const void* packed_gate_up, const void* packed_down, const void* shared_gate_up,
+    const void* shared_down, const void* addend, void* out, int64_t* out_indices,
+    float* out_weights, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes of parrot_vocab_argmax_bf16. */
 size_t parrot_vocab_argmax_workspace_bytes(int64_t rows, int32_t vocab);
 

@@ -60,6 +60,10 @@ SIGNATURES: dict[str, tuple] = {
     "parrot_decode_moe_bf16": (
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),
+    "parrot_depth_mix_decode_moe_bf16": (
+        ctypes.c_int,
+        [_p, _i32, _p, _p, _f32, _p, _f32, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p,
+         _p, _p, _p, _p, _p, _p, _sz, _p]),
     "parrot_decode_attention_latent_f32": (
         ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _f32, _p, _p]),
     "parrot_route_workspace_bytes": (_sz, [_i64, _i32]),

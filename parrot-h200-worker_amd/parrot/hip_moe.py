@@ -390,15 +390,30 @@ def groups_in_kernel(module: "MoE", tokens: int, dim: int) -> bool:
 DECODE_MAX_TOKENS = 16  # rows the fused decode MoE takes
 
 
-def decode_experts(module: "MoE", flat: Tensor, addend: Tensor | None = None,
-                   logit_bias: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+def decode_experts(module: "MoE", flat: Tensor | None, addend: Tensor | None = None,
+                   logit_bias: Tensor | None = None,
+                   mix: tuple | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """The whole MoE layer for at most DECODE_MAX_TOKENS rows in two launches
     (route + gate/up + SwiGLU, then down + weighted combine): returns
     ``(out, indices [T, 2] int64, weights [T, 2] fp32)`` with ``out`` =
     ``addend + delta`` when an addend is given (cf. metal_experts_decode,
-    parrot/metal_moe.py:182-221)."""
-    _require(flat, "The fused HIP decode MoE")
+    parrot/metal_moe.py:182-221).  ``mix = (depth_module, sources, norm)``:
+    the input rows are ``depth_mix_norm(depth_module, sources, norm)``, made
+    inside the same launches (``flat`` is then None; dim <= 1024)."""
     cfg = module.cfg
+    if mix is not None:
+        depth, sources, norm = mix
+        first = sources[0]
+        _require(first, "The fused HIP decode MoE")
+        tokens, dim = first.numel() // first.shape[-1], first.shape[-1]
+        flat_sources = [s.reshape(tokens, dim).contiguous() for s in sources]
+        for s in flat_sources:
+            if s.dtype != first.dtype or s.device != first.device:
+                raise RuntimeError("depth sources must share shape, dtype and device")
+        if not 1 <= len(flat_sources) <= MAX_DEPTH_SOURCES:
+            raise RuntimeError(f"HIP depth mixing supports one to {MAX_DEPTH_SOURCES} sources")
+        flat = flat_sources[0]  # device, dtype and shape of the rows
+    _require(flat, "The fused HIP decode MoE")
     tokens, dim = flat.shape
     if tokens > DECODE_MAX_TOKENS:
         raise RuntimeError(f"the fused decode MoE takes at most {DECODE_MAX_TOKENS} rows")
@@ -419,11 +434,22 @@ def decode_experts(module: "MoE", flat: Tensor, addend: Tensor | None = None,
     out = torch.empty_like(flat)
     indices = torch.empty((tokens, 2), dtype=torch.int64, device=flat.device)
     weights = torch.empty((tokens, 2), dtype=torch.float32, device=flat.device)
-    _abi.check(lib.parrot_decode_moe_bf16(
-        ptr(flat), tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim,
-        ptr(module.router.weight), ptr(bias), ptr(gate_up), ptr(down), ptr(shared_gate_up),
-        ptr(shared_down), ptr(addend), ptr(out), ptr(indices), ptr(weights), ptr(ws), nbytes,
-        _stream(flat.device)), "parrot_decode_moe_bf16")
+    tail = (ptr(module.router.weight), ptr(bias), ptr(gate_up), ptr(down), ptr(shared_gate_up),
+            ptr(shared_down), ptr(addend), ptr(out), ptr(indices), ptr(weights), ptr(ws), nbytes,
+            _stream(flat.device))
+    if mix is None:
+        _abi.check(lib.parrot_decode_moe_bf16(
+            ptr(flat), tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim, *tail),
+            "parrot_decode_moe_bf16")
+        return out, indices, weights
+    array = _SourceArray(*([t.data_ptr() for t in flat_sources] +
+                           [flat_sources[0].data_ptr()] * (MAX_DEPTH_SOURCES - len(flat_sources))))
+    _abi.check(lib.parrot_depth_mix_decode_moe_bf16(
+        ctypes.cast(array, ctypes.c_void_p), len(flat_sources), ptr(depth.query),
+        ptr(depth.norm.weight), float(depth.norm.eps), ptr(norm.weight), float(norm.eps),
+        tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim, *tail),
+        "parrot_depth_mix_decode_moe_bf16")
+    del flat_sources  # alive until the launch is enqueued (it is)
     return out, indices, weights
 
 

@@ -567,14 +567,16 @@ size_t parrot_decode_moe_workspace_bytes(int64_t tokens, int32_t hidden_dim,
   return round_up(3 * static_cast<size_t>(tokens) * hstride * sizeof(uint16_t));
 }
 
-int parrot_decode_moe_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,
-                           int32_t hidden_dim, int32_t shared_dim, const void* router_weight,
-                           const float* logit_bias, const void* packed_gate_up,
-                           const void* packed_down, const void* shared_gate_up,
-                           const void* shared_down, const void* addend, void* out,
-                           int64_t* out_indices, float* out_weights, void* workspace,
-                           size_t workspace_bytes, void* stream) {
-  if (!x || !router_weight || !packed_gate_up || !packed_down || !shared_gate_up ||
+// Shared checks and launch of the two decode MoE entry points.
+static int decode_moe_entry(const void* x, const parrot::DecodeMix* mix, int64_t tokens,
+                            int32_t dim, int32_t experts, int32_t hidden_dim,
+                            int32_t shared_dim, const void* router_weight,
+                            const float* logit_bias, const void* packed_gate_up,
+                            const void* packed_down, const void* shared_gate_up,
+                            const void* shared_down, const void* addend, void* out,
+                            int64_t* out_indices, float* out_weights, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if ((!x && !mix) || !router_weight || !packed_gate_up || !packed_down || !shared_gate_up ||
       !shared_down || !out || !out_indices || !out_weights)
     return PARROT_ERR_NULL_POINTER;
   if (tokens < 0 || dim <= 0 || hidden_dim <= 0 || shared_dim <= 0) return PARROT_ERR_BAD_SHAPE;
@@ -584,7 +586,7 @@ int parrot_decode_moe_bf16(const void* x, int64_t tokens, int32_t dim, int32_t e
   if (!workspace || workspace_bytes < parrot_decode_moe_workspace_bytes(tokens, hidden_dim,
                                                                         shared_dim))
     return PARROT_ERR_WORKSPACE;
-  if (!aligned16(x) || !aligned16(router_weight) || !aligned16(packed_gate_up) ||
+  if ((x && !aligned16(x)) || !aligned16(router_weight) || !aligned16(packed_gate_up) ||
       !aligned16(packed_down) || !aligned16(shared_gate_up) || !aligned16(shared_down) ||
       !aligned16(workspace))
     return PARROT_ERR_ALIGNMENT;
@@ -593,10 +595,57 @@ int parrot_decode_moe_bf16(const void* x, int64_t tokens, int32_t dim, int32_t e
                           static_cast<const uint16_t*>(shared_gate_up),
                           static_cast<const uint16_t*>(shared_down)};
   return status(parrot::launch_decode_moe(
-      static_cast<const uint16_t*>(x), static_cast<int>(tokens), dim, experts, hidden_dim,
+      static_cast<const uint16_t*>(x), mix, static_cast<int>(tokens), dim, experts, hidden_dim,
       shared_dim, static_cast<const uint16_t*>(router_weight), logit_bias, w,
       static_cast<const uint16_t*>(addend), static_cast<uint16_t*>(out), out_indices,
       out_weights, static_cast<uint16_t*>(workspace), as_stream(stream)));
+}
+
+int parrot_decode_moe_bf16(const void* x, int64_t tokens, int32_t dim, int32_t experts,
+                           int32_t hidden_dim, int32_t shared_dim, const void* router_weight,
+                           const float* logit_bias, const void* packed_gate_up,
+                           const void* packed_down, const void* shared_gate_up,
+                           const void* shared_down, const void* addend, void* out,
+                           int64_t* out_indices, float* out_weights, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (!x) return PARROT_ERR_NULL_POINTER;
+  return decode_moe_entry(x, nullptr, tokens, dim, experts, hidden_dim, shared_dim,
+                          router_weight, logit_bias, packed_gate_up, packed_down,
+                          shared_gate_up, shared_down, addend, out, out_indices, out_weights,
+                          workspace, workspace_bytes, stream);
+}
+
+int parrot_depth_mix_decode_moe_bf16(
+    const void* const* sources, int32_t n_sources, const void* query,
+    const void* score_norm_weight, float score_eps, const void* moe_norm_weight,
+    float norm_eps, int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
+    int32_t shared_dim, const void* router_weight, const float* logit_bias,
+    const void* packed_gate_up, const void* packed_down, const void* shared_gate_up,
+    const void* shared_down, const void* addend, void* out, int64_t* out_indices,
+    float* out_weights, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!sources || !query || !score_norm_weight || !moe_norm_weight) return PARROT_ERR_NULL_POINTER;
+  if (n_sources < 1 || n_sources > kMaxDepthSources || dim > 1024) return PARROT_ERR_UNSUPPORTED;
+  parrot::DecodeMix mix{};
+  uintptr_t bits = reinterpret_cast<uintptr_t>(query) |
+                   reinterpret_cast<uintptr_t>(score_norm_weight) |
+                   reinterpret_cast<uintptr_t>(moe_norm_weight);
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    const void* p = sources[s < n_sources ? s : 0];
+    if (!p) return PARROT_ERR_NULL_POINTER;
+    bits |= reinterpret_cast<uintptr_t>(p);
+    mix.srcs.src[s] = static_cast<const uint16_t*>(p);
+  }
+  if (bits & 7u) return PARROT_ERR_ALIGNMENT;
+  mix.n_sources = n_sources;
+  mix.query = static_cast<const uint16_t*>(query);
+  mix.score_w = static_cast<const uint16_t*>(score_norm_weight);
+  mix.score_eps = score_eps;
+  mix.out_w = static_cast<const uint16_t*>(moe_norm_weight);
+  mix.out_eps = norm_eps;
+  return decode_moe_entry(nullptr, &mix, tokens, dim, experts, hidden_dim, shared_dim,
+                          router_weight, logit_bias, packed_gate_up, packed_down,
+                          shared_gate_up, shared_down, addend, out, out_indices, out_weights,
+                          workspace, workspace_bytes, stream);
 }
 
 size_t parrot_vocab_argmax_workspace_bytes(int64_t rows, int32_t vocab) {

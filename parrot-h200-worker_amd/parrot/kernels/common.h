@@ -375,10 +375,23 @@ hipError_t launch_decode_attention_latent(const float* q, const uint16_t* latent
 // decode_moe.hip): route + gate/up + SwiGLU, then down + weighted combine
 // (+ addend).  `hidden` is scratch [3T, max(H, Hs)] bf16.
 int decode_moe_max_tokens();
-hipError_t launch_decode_moe(const uint16_t* x, int tokens, int dim, int experts, int hidden_dim,
-                             int shared_dim, const uint16_t* router_w, const float* bias,
-                             const ExpertWeights& w, const uint16_t* addend, uint16_t* out,
-                             int64_t* indices, float* weights, uint16_t* hidden, hipStream_t s);
+// The depth mix + RMSNorm that makes a decode MoE's input row per token
+// (n_sources == 0: the input x is given instead); dim <= 1024.
+struct DecodeMix {
+  DepthSources srcs;
+  int n_sources;
+  const uint16_t* query;
+  const uint16_t* score_w;
+  float score_eps;
+  const uint16_t* out_w;
+  float out_eps;
+};
+
+hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens, int dim,
+                             int experts, int hidden_dim, int shared_dim,
+                             const uint16_t* router_w, const float* bias, const ExpertWeights& w,
+                             const uint16_t* addend, uint16_t* out, int64_t* indices,
+                             float* weights, uint16_t* hidden, hipStream_t s);
 
 // Greedy token per row of h [rows <= vocab_argmax_max_rows(), dim] over a
 // [vocab, dim] head, fp32 logits (see vocab.hip); part_v / part_i hold

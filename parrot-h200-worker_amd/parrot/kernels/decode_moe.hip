@@ -14,11 +14,14 @@
 // At decode sizes the layer is a weight stream of ~2 x 2.4 MB per token plus
 // the shared expert, and launch latency dominates; the grouped path spends 5
 // launches (route, group, gate/up, down, combine).  Here:
-//   decode_up_kernel   grid (max(H, Hs) / 16 slices, 2T + 1 slots): slot
-//       2t + k is token t's k-th routed expert, slot 2T the shared expert for
-//       all tokens.  A routed workgroup recomputes its token's router logits
-//       and top-2 (every workgroup of a token does the same arithmetic in the
-//       same order, so they agree), then one 16-column slice of SwiGLU.
+//   decode_up_kernel   grid (max(H, Hs) / 16 slices, 3T slots): slot 2t + k
+//       is token t's k-th routed expert, slot 2T + t token t's shared expert.
+//       A routed workgroup recomputes its token's router logits and top-2
+//       (every workgroup of a token does the same arithmetic in the same
+//       order, so they agree), then one 16-column slice of SwiGLU.  Given the
+//       MoE input's depth sources instead of the input, every workgroup first
+//       mixes and normalises its token's row itself (depth_mix_core.h, the
+//       depth-mix kernel's arithmetic), which saves that kernel's launch.
 //   decode_down_kernel grid (dim / 16 slices, T): 16 output columns of one
 //       token: both weighted routed rows and the shared row, summed in the
 //       combine kernel's order, with the addend folded in.
@@ -27,7 +30,7 @@
 // .. +8), so lane l of wavefront w reads 16 contiguous bytes of k step
 // s = w, w + 4, ...; partial sums over (k chunk, wavefront) are added in a
 // fixed order through LDS.
-#include "common.h"
+#include "depth_mix_core.h"
 
 namespace parrot {
 
@@ -94,7 +97,7 @@ __device__ __forceinline__ void route_token(const uint16_t* x_row, const uint16_
 }
 
 __global__ __launch_bounds__(256) void decode_up_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
+    const uint16_t* __restrict__ x, DecodeMix mix, const uint16_t* __restrict__ wr,
     const float* __restrict__ bias, int tokens, int dim, int experts, int hidden_dim,
     int shared_dim, int hstride, const uint16_t* __restrict__ gate_up,
     const uint16_t* __restrict__ shared_gate_up, uint16_t* __restrict__ hidden,
@@ -103,29 +106,59 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   __shared__ int sel[2];
   __shared__ float sel_w[2];
   __shared__ float part[4][4][kDecodeMaxTokens][32];  // [wave][k chunk][token][gate 16 | up 16]
+  __shared__ DepthMixLds mix_lds;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [rows of this slot][dim]
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
   const int slot = blockIdx.y;
   const int slice = blockIdx.x;
-  const bool shared = slot == 2 * tokens;
+  const bool shared = slot >= 2 * tokens;
   const int H = shared ? shared_dim : hidden_dim;
   if (slice * 16 >= H) return;  // uniform
-  const int t0 = shared ? 0 : slot >> 1;
-  const int nt = shared ? tokens : 1;
-  // The slot's activation rows, staged in LDS as bf16; these loads are in
-  // flight together with the router's (the barrier in route_token, or the
-  // one below, orders them before use).
-  for (int i = tid; i < nt * dim / 8; i += 256)
-    reinterpret_cast<uint4*>(xs)[i] =
-        reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t0) * dim)[i];
+  const int t0 = shared ? slot - 2 * tokens : slot >> 1;
+  const int nt = 1;
+  if (mix.n_sources > 0) {
+    // The token's input row: depth mix + RMSNorm of its sources into LDS,
+    // every load issued before the first wait (lanes past the row read
+    // chunk 0 and are zeroed, unread slots read source 0 and are zeroed).
+    const int chunks = dim >> 2;
+    const bool has = tid < chunks;
+    const int ic = has ? tid : 0;
+    const int64_t base = static_cast<int64_t>(t0) * chunks;
+    uint2 v[kMaxDepthSources];
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s)
+      v[s] = reinterpret_cast<const uint2*>(mix.srcs.src[s])[base + ic];
+    const uint2 q = reinterpret_cast<const uint2*>(mix.query)[ic];
+    const uint2 g = reinterpret_cast<const uint2*>(mix.score_w)[ic];
+    const uint2 g_out = reinterpret_cast<const uint2*>(mix.out_w)[ic];
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s)
+      if (!has || s >= mix.n_sources) v[s] = make_uint2(0u, 0u);
+    const int waves = (dim + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
+    const uint2 mixed = depth_mix_chunk(v, q, g, has, mix.n_sources, waves, wave, lane, dim,
+                                        mix.score_eps, mix_lds);
+    const uint2 o = depth_mix_norm_chunk(mixed, g_out, has, waves, wave, lane, dim, mix.out_eps,
+                                         mix_lds);
+    if (has) reinterpret_cast<uint2*>(xs)[tid] = o;
+  } else {
+    // The slot's activation row, staged in LDS as bf16; these loads are in
+    // flight together with the router's (the barrier in route_token, or the
+    // one below, orders them before use).
+    for (int i = tid; i < nt * dim / 8; i += 256)
+      reinterpret_cast<uint4*>(xs)[i] =
+          reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t0) * dim)[i];
+  }
   const uint16_t* w;
   if (shared) {
     __syncthreads();
     w = shared_gate_up;
   } else {
-    route_token(x + static_cast<int64_t>(t0) * dim, wr, bias, dim, experts, lg, sel, sel_w);
+    // The router reads the row from LDS once it is mixed there.
+    if (mix.n_sources > 0) __syncthreads();
+    route_token(mix.n_sources > 0 ? xs : x + static_cast<int64_t>(t0) * dim, wr, bias, dim,
+                experts, lg, sel, sel_w);
     const int k = slot & 1;
     if (slice == 0 && k == 0 && tid < 2) {
       indices[2 * t0 + tid] = sel[tid];
@@ -186,7 +219,7 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
         gs += part[wv][cc][t][rr];
         us += part[wv][cc][t][16 + rr];
       }
-    const int64_t row = shared ? 2 * tokens + t : slot;
+    const int64_t row = shared ? 2 * tokens + t0 : slot;
     hidden[row * hstride + slice * 16 + rr] = f32_to_bf16(swiglu(gs, us));
   }
 }
@@ -264,16 +297,18 @@ __global__ __launch_bounds__(256) void decode_down_kernel(
 
 int decode_moe_max_tokens() { return kDecodeMaxTokens; }
 
-hipError_t launch_decode_moe(const uint16_t* x, int tokens, int dim, int experts, int hidden_dim,
-                             int shared_dim, const uint16_t* router_w, const float* bias,
-                             const ExpertWeights& w, const uint16_t* addend, uint16_t* out,
-                             int64_t* indices, float* weights, uint16_t* hidden, hipStream_t s) {
+hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens, int dim,
+                             int experts, int hidden_dim, int shared_dim,
+                             const uint16_t* router_w, const float* bias, const ExpertWeights& w,
+                             const uint16_t* addend, uint16_t* out, int64_t* indices,
+                             float* weights, uint16_t* hidden, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
   const int hstride = hidden_dim > shared_dim ? hidden_dim : shared_dim;
-  const size_t x_lds = static_cast<size_t>(tokens) * dim * sizeof(uint16_t);
-  decode_up_kernel<<<dim3(hstride / 16, 2 * tokens + 1), 256, x_lds, s>>>(
-      x, router_w, bias, tokens, dim, experts, hidden_dim, shared_dim, hstride, w.gate_up,
-      w.shared_gate_up, hidden, indices, weights);
+  const size_t x_lds = static_cast<size_t>(dim) * sizeof(uint16_t);  // one row per slot
+  const DecodeMix none{};
+  decode_up_kernel<<<dim3(hstride / 16, 3 * tokens), 256, x_lds, s>>>(
+      x, mix != nullptr ? *mix : none, router_w, bias, tokens, dim, experts, hidden_dim,
+      shared_dim, hstride, w.gate_up, w.shared_gate_up, hidden, indices, weights);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   decode_down_kernel<<<dim3(dim / 16, tokens), 256, 0, s>>>(
       hidden, tokens, dim, hidden_dim, shared_dim, hstride, indices, weights, w.down,

@@ -1,0 +1,144 @@
+// One token's Block AttnRes mix and output RMSNorm, shared by the depth-mix
+// kernel (norm.hip) and the decode MoE that mixes its own input
+// (decode_moe.hip), so both produce the same bits.
+//
+// Reference: Block AttnRes (parrot/model.py:680-710; parrot/metal_moe.py:
+// 419-477): score_s = <rmsnorm_w(v_s), q>, alpha = softmax_s(score),
+// mix = bf16(sum_s alpha_s v_s), then y = rmsnorm_out(mix) rounded to bf16.
+//
+// Layout: `waves` wavefronts hold the row, 256 dims each; lane l of
+// wavefront w owns the 4 consecutive dims of chunk i = 64 w + l (`has` when
+// i < dim / 4).  Wavefronts past `waves` of a larger workgroup take part in
+// the barriers with has == false.  Per-source sums (squares and query dot)
+// are wavefront sums combined across the wavefronts through LDS in
+// wavefront order, so every wavefront derives the same scores; the output
+// norm's sum of squares likewise.
+#pragma once
+#include "common.h"
+
+namespace parrot {
+
+constexpr int kDepthDimsPerWave = 256;
+constexpr int kDepthMaxWaves = 8;  // dim <= 2048
+
+struct __attribute__((aligned(8))) DepthMixLds {
+  float part[kDepthMaxWaves][2 * kMaxDepthSources];
+  float part_out[kDepthMaxWaves];
+};
+
+// The mix of this lane's chunk as packed bf16.  v: the chunk of each source
+// slot (zeros for unread slots and lanes past the row); q, g: the chunk of
+// the query and of the score norm's weight.  Contains one barrier.
+__device__ __forceinline__ uint2 depth_mix_chunk(const uint2 (&v)[kMaxDepthSources], uint2 q,
+                                                 uint2 g, bool has, int n_sources, int waves,
+                                                 int wave, int lane, int dim, float score_eps,
+                                                 DepthMixLds& sh) {
+  float wq[4] = {0.f, 0.f, 0.f, 0.f};
+  if (has) {
+    wq[0] = lo_bf16(q.x) * lo_bf16(g.x);
+    wq[1] = hi_bf16(q.x) * hi_bf16(g.x);
+    wq[2] = lo_bf16(q.y) * lo_bf16(g.y);
+    wq[3] = hi_bf16(q.y) * hi_bf16(g.y);
+  }
+
+  // Per-source partial sums, all wavefront reductions back to back.
+  float ss[kMaxDepthSources], dq[kMaxDepthSources];
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    const float e0 = lo_bf16(v[s].x), e1 = hi_bf16(v[s].x);
+    const float e2 = lo_bf16(v[s].y), e3 = hi_bf16(v[s].y);
+    ss[s] = e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3;
+    dq[s] = e0 * wq[0] + e1 * wq[1] + e2 * wq[2] + e3 * wq[3];
+  }
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    if (s < n_sources) {
+      ss[s] = wave_sum(ss[s]);
+      dq[s] = wave_sum(dq[s]);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s) {
+      if (s < n_sources) {
+        sh.part[wave][2 * s] = ss[s];
+        sh.part[wave][2 * s + 1] = dq[s];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Cross-wavefront sums in wavefront order.  The loop bounds are
+  // compile-time (uniform guards inside), so each wavefront row's LDS reads
+  // go out together instead of one read, wait and add at a time.
+  float sst[kMaxDepthSources], dqt[kMaxDepthSources];
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) sst[s] = dqt[s] = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kDepthMaxWaves; ++w) {
+    if (w < waves) {
+#pragma unroll
+      for (int s = 0; s < kMaxDepthSources; ++s) {
+        if (s < n_sources) {
+          const float2 pv = *reinterpret_cast<const float2*>(&sh.part[w][2 * s]);
+          sst[s] += pv.x;
+          dqt[s] += pv.y;
+        }
+      }
+    }
+  }
+  float score[kMaxDepthSources];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    score[s] = -INFINITY;
+    if (s < n_sources) {
+      score[s] = dqt[s] * rsqrtf(sst[s] / static_cast<float>(dim) + score_eps);
+      mx = fmaxf(mx, score[s]);
+    }
+  }
+  float denom = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s)
+    if (s < n_sources) denom += __expf(score[s] - mx);
+  const float inv = 1.0f / denom;
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    if (s < n_sources) {
+      const float a = __expf(score[s] - mx) * inv;
+      acc[0] += a * lo_bf16(v[s].x);
+      acc[1] += a * hi_bf16(v[s].x);
+      acc[2] += a * lo_bf16(v[s].y);
+      acc[3] += a * hi_bf16(v[s].y);
+    }
+  }
+  uint2 mixed;
+  mixed.x = pack_bf16x2(acc[0], acc[1]);
+  mixed.y = pack_bf16x2(acc[2], acc[3]);
+  return mixed;
+}
+
+// The output RMSNorm of the mixed row, this lane's chunk as packed bf16
+// (g_out: the chunk of the norm's weight).  Contains one barrier.
+__device__ __forceinline__ uint2 depth_mix_norm_chunk(uint2 mixed, uint2 g_out, bool has,
+                                                      int waves, int wave, int lane, int dim,
+                                                      float out_eps, DepthMixLds& sh) {
+  const float r0 = lo_bf16(mixed.x), r1 = hi_bf16(mixed.x);
+  const float r2 = lo_bf16(mixed.y), r3 = hi_bf16(mixed.y);
+  const float sso = wave_sum(has ? r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3 : 0.0f);
+  if (lane == 0) sh.part_out[wave] = sso;
+  __syncthreads();
+  float total = sh.part_out[0];
+#pragma unroll
+  for (int w = 1; w < kDepthMaxWaves; ++w)
+    if (w < waves) total += sh.part_out[w];
+  const float r = rsqrtf(total / static_cast<float>(dim) + out_eps);
+  uint2 o;
+  o.x = pack_bf16x2(r0 * r * lo_bf16(g_out.x), r1 * r * hi_bf16(g_out.x));
+  o.y = pack_bf16x2(r2 * r * lo_bf16(g_out.y), r3 * r * hi_bf16(g_out.y));
+  return o;
+}
+
+}  // namespace parrot

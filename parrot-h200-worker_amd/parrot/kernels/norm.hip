@@ -8,7 +8,7 @@
 // at the same point as the reference (parrot/model.py:125-127 for RMSNorm,
 // :149-155 for the depth mix, parrot/kernels/moe_bf16.metal:414-433 for the
 // mix rounded to bf16 before its consumer RMSNorm).
-#include "common.h"
+#include "depth_mix_core.h"
 
 namespace parrot {
 
@@ -56,14 +56,10 @@ __global__ __launch_bounds__(64) void rms_norm_kernel(
 // Block AttnRes: score_s = <rmsnorm_w(v_s), q>, alpha = softmax_s(score),
 // mix = bf16(sum_s alpha_s v_s); optionally y = rmsnorm_out(mix).
 // One workgroup per token and one wavefront per 256 dims: a lane owns 4
-// consecutive dims of every source, all of whose loads are issued up front.
-// The per-source sums (squares and query dot) are wavefront sums combined
-// across the wavefronts through LDS in wavefront order, so every wavefront
-// derives the same scores; the output norm's sum of squares likewise.
-// (A single wavefront per token serialises ~1500 VALU instructions of
-// unpacking and summing at dim 768 and leaves most SIMDs idle.)
-constexpr int kDepthDimsPerWave = 256;
-constexpr int kDepthMaxWaves = 8;  // dim <= 2048
+// consecutive dims of every source, all of whose loads are issued up front;
+// the arithmetic is depth_mix_core.h's.  (A single wavefront per token
+// serialises ~1500 VALU instructions of unpacking and summing at dim 768 and
+// leaves most SIMDs idle.)
 
 // With ROUTE > 0 the kernel also routes the token's normalised row (the MoE
 // input) to its top-2 experts, with route_kernel's arithmetic to the bit:
@@ -85,8 +81,7 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
     uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm, CombineSource comb,
     RouteOut route) {
-  __shared__ __attribute__((aligned(8))) float part[kDepthMaxWaves][2 * kMaxDepthSources];
-  __shared__ float part_out[kDepthMaxWaves];
+  __shared__ DepthMixLds mix_lds;
   // The kernel arguments of the load phase in one batch of scalar loads,
   // before anything uses one: a field first read inside a branch, or after
   // an earlier batch was waited for, costs a scalar round trip of its own.
@@ -178,106 +173,12 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     for (int s = 0; s < kMaxDepthSources; ++s)
       if (s == n_sources - 1) v[s] = o;
   }
-  float wq[4] = {0.f, 0.f, 0.f, 0.f};
-  if (has) {
-    wq[0] = lo_bf16(q.x) * lo_bf16(g.x);
-    wq[1] = hi_bf16(q.x) * hi_bf16(g.x);
-    wq[2] = lo_bf16(q.y) * lo_bf16(g.y);
-    wq[3] = hi_bf16(q.y) * hi_bf16(g.y);
-  }
-
-  // Per-source partial sums, all wavefront reductions back to back.
-  float ss[kMaxDepthSources], dq[kMaxDepthSources];
-#pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) {
-    const float e0 = lo_bf16(v[s].x), e1 = hi_bf16(v[s].x);
-    const float e2 = lo_bf16(v[s].y), e3 = hi_bf16(v[s].y);
-    ss[s] = e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3;
-    dq[s] = e0 * wq[0] + e1 * wq[1] + e2 * wq[2] + e3 * wq[3];
-  }
-#pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) {
-    if (s < n_sources) {
-      ss[s] = wave_sum(ss[s]);
-      dq[s] = wave_sum(dq[s]);
-    }
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s) {
-      if (s < n_sources) {
-        part[wave][2 * s] = ss[s];
-        part[wave][2 * s + 1] = dq[s];
-      }
-    }
-  }
-  __syncthreads();
-
-  // Cross-wavefront sums in wavefront order.  The loop bounds are
-  // compile-time (uniform guards inside), so each wavefront row's LDS reads
-  // go out together instead of one read, wait and add at a time.
-  float sst[kMaxDepthSources], dqt[kMaxDepthSources];
-#pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) sst[s] = dqt[s] = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kDepthMaxWaves; ++w) {
-    if (w < waves) {
-#pragma unroll
-      for (int s = 0; s < kMaxDepthSources; ++s) {
-        if (s < n_sources) {
-          const float2 pv = *reinterpret_cast<const float2*>(&part[w][2 * s]);
-          sst[s] += pv.x;
-          dqt[s] += pv.y;
-        }
-      }
-    }
-  }
-  float score[kMaxDepthSources];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) {
-    score[s] = -INFINITY;
-    if (s < n_sources) {
-      score[s] = dqt[s] * rsqrtf(sst[s] / static_cast<float>(dim) + score_eps);
-      mx = fmaxf(mx, score[s]);
-    }
-  }
-  float denom = 0.0f;
-#pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s)
-    if (s < n_sources) denom += __expf(score[s] - mx);
-  const float inv = 1.0f / denom;
-
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) {
-    if (s < n_sources) {
-      const float a = __expf(score[s] - mx) * inv;
-      acc[0] += a * lo_bf16(v[s].x);
-      acc[1] += a * hi_bf16(v[s].x);
-      acc[2] += a * lo_bf16(v[s].y);
-      acc[3] += a * hi_bf16(v[s].y);
-    }
-  }
-  uint2 mixed;
-  mixed.x = pack_bf16x2(acc[0], acc[1]);
-  mixed.y = pack_bf16x2(acc[2], acc[3]);
+  const uint2 mixed =
+      depth_mix_chunk(v, q, g, has, n_sources, waves, wave, lane, dim, score_eps, mix_lds);
   if (out_mix != nullptr && has) reinterpret_cast<uint2*>(out_mix)[base + i] = mixed;
   if (out_norm == nullptr) return;  // uniform over the workgroup
-
-  const float r0 = lo_bf16(mixed.x), r1 = hi_bf16(mixed.x);
-  const float r2 = lo_bf16(mixed.y), r3 = hi_bf16(mixed.y);
-  const float sso = wave_sum(has ? r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3 : 0.0f);
-  if (lane == 0) part_out[wave] = sso;
-  __syncthreads();
-  float total = part_out[0];
-#pragma unroll
-  for (int w = 1; w < kDepthMaxWaves; ++w)
-    if (w < waves) total += part_out[w];
-  const float r = rsqrtf(total / static_cast<float>(dim) + out_eps);
-  uint2 o;
-  o.x = pack_bf16x2(r0 * r * lo_bf16(g_out.x), r1 * r * hi_bf16(g_out.x));
-  o.y = pack_bf16x2(r2 * r * lo_bf16(g_out.y), r3 * r * hi_bf16(g_out.y));
+  const uint2 o = depth_mix_norm_chunk(mixed, g_out, has, waves, wave, lane, dim, out_eps,
+                                       mix_lds);
   if (has) reinterpret_cast<uint2*>(out_norm)[base + i] = o;
   if constexpr (ROUTE > 0) {
     __shared__ __attribute__((aligned(16))) uint16_t xn[kDepthDimsPerWave * kDepthMaxWaves];

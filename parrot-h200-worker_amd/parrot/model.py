@@ -789,6 +789,23 @@ class Parrot(nn.Module):
                                                     block.moe_norm, block.moe)
         return self._mixed_input(stream, x, index, block.moe_norm), None
 
+    def _decode_moe(self, block: Block, stream: _AttnRes, x: Tensor, index: int) -> Tensor:
+        """MoE module ``index`` of a decode step, closing the open partial sum
+        (``partial + delta``).  On the HIP path its input's depth mix + norm
+        runs inside the fused decode MoE's launches."""
+        sources = stream.sources()
+        first = sources[0]
+        if self.config.depth_backend == "hip" and block.moe._hip_route_applies(first):
+            from . import hip_moe
+            tokens, dim = first.numel() // first.shape[-1], first.shape[-1]
+            if tokens <= hip_moe.DECODE_MAX_TOKENS and dim <= 1024:
+                out = hip_moe.decode_experts(
+                    block.moe, None, addend=stream.partial,
+                    mix=(self.depth_mix[index], sources, block.moe_norm))[0]
+                return out.view_as(first)
+        h = self._mixed_input(stream, x, index, block.moe_norm)
+        return block.moe.inference(h, direct=True, addend=stream.partial)
+
     def _moe_closing(self, block: Block, h: Tensor, stream: _AttnRes, index: int,
                      next_norm: RMSNorm, routed=None) -> Tensor:
         """Close MoE module ``index`` (fused addend) and return the input of
@@ -1007,8 +1024,7 @@ class Parrot(nn.Module):
             index += 1
 
             if stream is not None:
-                h = self._mixed_input(stream, x, index, block.moe_norm)
-                stream.close(block.moe.inference(h, direct=True, addend=stream.partial))
+                stream.close(self._decode_moe(block, stream, x, index))
             else:
                 x = x + block.feedforward_inference(x, direct=True)
             index += 1

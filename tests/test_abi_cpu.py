@@ -137,6 +137,17 @@ def test_argument_validation_without_gpu(lib):
                                                   fake, null) == -1
     assert lib.parrot_decode_attention_latent_f32(fake, fake, fake, fake, 2, 8, 128, 1 << 16,
                                                   0.1, fake, null) == -3
+    # decode MoE with its input's depth mix: sources, n_sources, dim <= 1024
+    mix_moe = lambda **kw: lib.parrot_depth_mix_decode_moe_bf16(*[kw.get(k, v) for k, v in (
+        ("srcs", ctypes.cast(srcs, ctypes.c_void_p)), ("n", 2), ("q", fake), ("sw", fake),
+        ("se", 1e-6), ("nw", fake), ("ne", 1e-6), ("tokens", 2), ("dim", 768), ("e", 16),
+        ("h", 512), ("hs", 256), ("rw", fake), ("bias", null), ("gu", fake), ("dn", fake),
+        ("sgu", fake), ("sdn", fake), ("add", null), ("out", fake), ("idx", fake),
+        ("w", fake), ("ws", fake), ("wsb", 1 << 20), ("stream", null))])
+    assert mix_moe(srcs=null) == -1 and mix_moe(q=null) == -1 and mix_moe(nw=null) == -1
+    assert mix_moe(n=0) == -3 and mix_moe(n=10) == -3 and mix_moe(dim=1088) == -3
+    assert mix_moe(tokens=17) == -3 and mix_moe(wsb=16) == -4
+    assert mix_moe(q=fake + 4) == -5
     # MLA decode projections: tokens <= 16, K % 128 <= 2048, rows % 16,
     # staged input <= 64 KB, alignment
     mla_in = lambda **kw: lib.parrot_mla_decode_in_bf16(*[kw.get(k, v) for k, v in (

@@ -163,6 +163,31 @@ def test_decode_graph_matches_eager():
                                        getattr(theirs, name)[:, :, :48])
 
 
+@pytest.mark.parametrize("tokens,sources,with_addend", [
+    (1, 1, True), (1, 4, False), (3, 9, True), (8, 5, True), (16, 9, False)])
+def test_decode_moe_mixes_its_input(tokens, sources, with_addend):
+    """The decode MoE that makes its input rows itself (depth mix + norm of
+    the sources, per token inside the launch) equals depth_mix_norm followed
+    by the decode MoE, bit for bit: the same arithmetic in the same order."""
+    from moe_cases import inputs, moe_module
+    from test_gpu_moe import _Depth, _Norm
+    from parrot import hip_moe
+    _say(f"decode moe with its input mix T={tokens} S={sources} addend={with_addend}")
+    torch.manual_seed(60 + tokens + sources)
+    module = moe_module(16, seed=13)
+    depth = _Depth(768).cuda().bfloat16()
+    norm = _Norm(768).cuda().bfloat16()
+    src = [inputs(tokens, seed=70 + s) * (1 + s) for s in range(sources)]
+    addend = inputs(tokens, seed=90) if with_addend else None
+    with torch.no_grad():
+        h = hip_moe.depth_mix_norm(depth, src, norm)
+        ref, ref_idx, ref_w = hip_moe.decode_experts(module, h, addend=addend)
+        out, idx, w = hip_moe.decode_experts(module, None, addend=addend,
+                                             mix=(depth, src, norm))
+    assert torch.equal(idx, ref_idx) and torch.equal(w, ref_w)
+    assert torch.equal(out, ref)
+
+
 @pytest.mark.parametrize("tokens,experts,skewed,with_addend", [
     (1, 16, False, False), (2, 16, False, True), (5, 32, True, False), (8, 16, False, True),
     (16, 3, False, True), (16, 32, False, False)])
