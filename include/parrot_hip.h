@@ -166,6 +166,31 @@ int parrot_decode_attention_latent_f32(const float* q, const void* latent_new, v
                                        int32_t latent_dim, int32_t max_positions, float scale,
                                        float* out, void* stream);
 
+/* The decode step's q|k|v projection of a local (GQA) layer with RoPE, one
+ * launch: for each token t, q|k|v = h_t W^T rounded to bf16 (qkv_weight
+ * [(heads + 2 kv_heads) head_dim, dim] bf16 row-major, the q, k and v
+ * weights stacked), then q and k rotated by RoPE at position *position
+ * (cos_table / sin_table fp32 [max_positions, head_dim / 2], the position
+ * clamped into them) and rounded again; q [tokens, heads, 1, head_dim], k
+ * and v [tokens, kv_heads, 1, head_dim] bf16.  h is x [tokens, dim] bf16
+ * when x is non-NULL, else the depth mix of `sources` normalised by the
+ * attention norm (attention_norm_weight, norm_eps), exactly as
+ * parrot_depth_mix_bf16 with out_norm computes it (sources, n_sources,
+ * query, score_norm_weight, score_eps as there).  tokens <= 16, dim % 128 ==
+ * 0 and dim <= 1024, head_dim even, (heads + 2 kv_heads) head_dim % 16 == 0;
+ * x and qkv_weight 16-byte aligned.  The projection's fp32 sums run in
+ * another order than a GEMM's, so its bf16 values may differ from those of
+ * parrot_proj_rope_qkv_bf16 in the last place.  Replaces, for a decode step,
+ * metal_depth_mix_norm (parrot/metal_moe.py:455-477) and the q/k/v
+ * projections + _apply_rope of LocalGQA.decode (parrot/model.py:176-262). */
+int parrot_decode_qkv_bf16(const void* x, const void* const* sources, int32_t n_sources,
+                           const void* query, const void* score_norm_weight, float score_eps,
+                           const void* attention_norm_weight, float norm_eps, int32_t tokens,
+                           int32_t dim, const void* qkv_weight, int32_t heads,
+                           int32_t kv_heads, int32_t head_dim, const float* cos_table,
+                           const float* sin_table, int32_t max_positions,
+                           const int32_t* position, void* q, void* k, void* v, void* stream);
+
 /* The MLA layers' decode-step projections before the latent attention, one
  * launch: q_latent [tokens, query_rows] fp32 = x . absorbed_query^T with x
  * [tokens, dim] bf16 and absorbed_query [query_rows, dim] bf16 (the absorbed

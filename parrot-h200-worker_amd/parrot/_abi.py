@@ -87,6 +87,10 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [_p, _i32, _p, _p, _f32, _p, _f32, _i64, _i32, _p, _p, _p, _p, _i32, _p, _p, _p]),
     "parrot_experts_group_in_kernel": (ctypes.c_int, [_i64, _i32, _i32, _i32, _i32]),
+    "parrot_decode_qkv_bf16": (
+        ctypes.c_int,
+        [_p, _p, _i32, _p, _p, _f32, _p, _f32, _i32, _i32, _p, _i32, _i32, _i32, _p, _p, _i32,
+         _p, _p, _p, _p, _p]),
     "parrot_mla_decode_in_bf16": (
         ctypes.c_int, [_p, _i32, _i32, _p, _i32, _p, _i32, _p, _p, _p]),
     "parrot_mla_decode_out_bf16": (ctypes.c_int, [_p, _i32, _i32, _p, _i32, _p, _p, _p]),

@@ -803,6 +803,57 @@ def decode_attention(q: Tensor, k_new: Tensor, v_new: Tensor, key_cache: Tensor,
     return out
 
 
+def decode_qkv_supported(tokens: int, dim: int, heads: int, kv_heads: int,
+                         head_dim: int) -> bool:
+    """Shapes parrot_decode_qkv_bf16 takes."""
+    return (1 <= tokens <= 16 and dim % 128 == 0 and dim <= 1024 and head_dim % 2 == 0
+            and (heads + 2 * kv_heads) * head_dim % 16 == 0)
+
+
+def decode_qkv(x: Tensor | None, weight: Tensor, cos: Tensor, sin: Tensor, heads: int,
+               kv_heads: int, head_dim: int, position: Tensor,
+               mix: tuple | None = None) -> tuple[Tensor, Tensor, Tensor]:
+    """A decode step's q|k|v projection + RoPE at the device ``position`` in
+    one launch: x [b, 1, dim] bf16, or ``mix = (depth_module, sources, norm)``
+    whose ``depth_mix_norm`` the launch computes itself; ``weight`` the
+    stacked row-major q|k|v weight.  Returns q [b, heads, 1, d], k and v
+    [b, kv_heads, 1, d] (cf. LocalGQA.decode, parrot/model.py:176-262)."""
+    if mix is not None:
+        depth, sources, norm = mix
+        first = sources[0]
+        b, dim = first.numel() // first.shape[-1], first.shape[-1]
+        rows = [s.reshape(b, dim).contiguous() for s in sources]
+        for s in rows:
+            if s.dtype != first.dtype or s.device != first.device:
+                raise RuntimeError("depth sources must share shape, dtype and device")
+        if not 1 <= len(rows) <= MAX_DEPTH_SOURCES:
+            raise RuntimeError(f"HIP depth mixing supports one to {MAX_DEPTH_SOURCES} sources")
+        ref = rows[0]
+        array = _SourceArray(*([t.data_ptr() for t in rows] +
+                               [rows[0].data_ptr()] * (MAX_DEPTH_SOURCES - len(rows))))
+        mix_args = (None, ctypes.cast(array, ctypes.c_void_p), len(rows), ptr(depth.query),
+                    ptr(depth.norm.weight), float(depth.norm.eps), ptr(norm.weight),
+                    float(norm.eps))
+    else:
+        b, dim = x.shape[0], x.shape[-1]
+        ref = x.reshape(b, dim).contiguous()
+        mix_args = (ptr(ref), None, 0, None, None, 0.0, None, 0.0)
+    _require(ref, "HIP decode q|k|v projection")
+    if weight.dtype != ref.dtype or not weight.is_contiguous():
+        raise RuntimeError("q|k|v weight must be contiguous in the input's dtype")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise RuntimeError("RoPE tables must be fp32")
+    _check_position(position, ref.device)
+    q = ref.new_empty((b, heads, 1, head_dim))
+    k = ref.new_empty((b, kv_heads, 1, head_dim))
+    v = ref.new_empty((b, kv_heads, 1, head_dim))
+    _abi.check(_abi.load().parrot_decode_qkv_bf16(
+        *mix_args, b, dim, ptr(weight), heads, kv_heads, head_dim, ptr(cos), ptr(sin),
+        cos.shape[0], ptr(position), ptr(q), ptr(k), ptr(v), _stream(ref.device)),
+        "parrot_decode_qkv_bf16")
+    return q, k, v
+
+
 MLA_DECODE_MAX_TOKENS = 16
 
 

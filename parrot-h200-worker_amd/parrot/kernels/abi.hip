@@ -238,6 +238,61 @@ int parrot_decode_attention_latent_f32(const float* q, const void* latent_new, v
       position, batch, heads, latent_dim, max_positions, scale, out, as_stream(stream)));
 }
 
+int parrot_decode_qkv_bf16(const void* x, const void* const* sources, int32_t n_sources,
+                           const void* query, const void* score_norm_weight, float score_eps,
+                           const void* attention_norm_weight, float norm_eps, int32_t tokens,
+                           int32_t dim, const void* qkv_weight, int32_t heads,
+                           int32_t kv_heads, int32_t head_dim, const float* cos_table,
+                           const float* sin_table, int32_t max_positions,
+                           const int32_t* position, void* q, void* k, void* v, void* stream) {
+  if ((!x && !sources) || !qkv_weight || !cos_table || !sin_table || !position || !q || !k ||
+      !v)
+    return PARROT_ERR_NULL_POINTER;
+  if (tokens < 0 || dim <= 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
+      max_positions <= 0)
+    return PARROT_ERR_BAD_SHAPE;
+  const int64_t n = static_cast<int64_t>(heads + 2 * kv_heads) * head_dim;
+  if (tokens > 16 || dim % 128 || dim > parrot::decode_qkv_max_dim() || head_dim % 2 || n % 16)
+    return PARROT_ERR_UNSUPPORTED;
+  if ((x && !aligned16(x)) || !aligned16(qkv_weight)) return PARROT_ERR_ALIGNMENT;
+  parrot::DecodeQkvArgs a{};
+  if (!x) {
+    if (!query || !score_norm_weight || !attention_norm_weight) return PARROT_ERR_NULL_POINTER;
+    if (n_sources < 1 || n_sources > kMaxDepthSources) return PARROT_ERR_UNSUPPORTED;
+    uintptr_t bits = reinterpret_cast<uintptr_t>(query) |
+                     reinterpret_cast<uintptr_t>(score_norm_weight) |
+                     reinterpret_cast<uintptr_t>(attention_norm_weight);
+    for (int s = 0; s < kMaxDepthSources; ++s) {
+      const void* p = sources[s < n_sources ? s : 0];
+      if (!p) return PARROT_ERR_NULL_POINTER;
+      bits |= reinterpret_cast<uintptr_t>(p);
+      a.mix.srcs.src[s] = static_cast<const uint16_t*>(p);
+    }
+    if (bits & 7u) return PARROT_ERR_ALIGNMENT;
+    a.mix.n_sources = n_sources;
+    a.mix.query = static_cast<const uint16_t*>(query);
+    a.mix.score_w = static_cast<const uint16_t*>(score_norm_weight);
+    a.mix.score_eps = score_eps;
+    a.mix.out_w = static_cast<const uint16_t*>(attention_norm_weight);
+    a.mix.out_eps = norm_eps;
+  }
+  a.x = static_cast<const uint16_t*>(x);
+  a.tokens = tokens;
+  a.dim = dim;
+  a.w = static_cast<const uint16_t*>(qkv_weight);
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.cos_t = cos_table;
+  a.sin_t = sin_table;
+  a.max_positions = max_positions;
+  a.position = position;
+  a.q = static_cast<uint16_t*>(q);
+  a.k = static_cast<uint16_t*>(k);
+  a.v = static_cast<uint16_t*>(v);
+  return status(parrot::launch_decode_qkv(a, as_stream(stream)));
+}
+
 // Shapes of the MLA decode projections: up to 16 tokens, K a multiple of
 // 128 up to 2048, row counts multiples of 16, the staged input within 64 KB.
 static int check_mla_decode(int32_t tokens, int32_t k, int elem_bytes) {

@@ -387,6 +387,24 @@ struct DecodeMix {
   float out_eps;
 };
 
+// The decode step's q|k|v projection + RoPE of a local layer (decode_qkv.hip).
+struct DecodeQkvArgs {
+  DecodeMix mix;            // n_sources > 0: the input rows are mixed in the launch
+  const uint16_t* x;        // else the input rows [tokens, dim]
+  int tokens, dim;
+  const uint16_t* w;        // q|k|v weight [(H + 2 Hk) d, dim], row-major bf16
+  int heads, kv_heads, head_dim;
+  const float* cos_t;       // [max_positions, d / 2]
+  const float* sin_t;
+  int max_positions;
+  const int32_t* position;  // device position of the new token
+  uint16_t* q;              // [tokens, H, 1, d]
+  uint16_t* k;              // [tokens, Hk, 1, d]
+  uint16_t* v;              // [tokens, Hk, 1, d]
+};
+int decode_qkv_max_dim();
+hipError_t launch_decode_qkv(const DecodeQkvArgs& a, hipStream_t s);
+
 hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens, int dim,
                              int experts, int hidden_dim, int shared_dim,
                              const uint16_t* router_w, const float* bias, const ExpertWeights& w,

@@ -1,0 +1,64 @@
+// Decode GEMV building blocks: a workgroup of 256 lanes owns 16 output rows,
+// one per 16-lane DPP row; lane p of a row holds the row's 16-byte weight
+// chunks p, p + 16, ... (256 contiguous bytes per instruction across the
+// row), and the row's 16 partial sums are added by four DPP steps in a fixed
+// order.  Used by the MLA decode projections and the decode q|k|v
+// projection.
+#pragma once
+#include "common.h"
+
+namespace parrot {
+
+constexpr int kGemvRows = 16;        // output rows per workgroup
+constexpr int kGemvMaxChunks = 16;   // 16-byte weight chunks per lane: K <= 2048
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  v += dpp<0x140>(v);  // row_mirror
+  return v;
+}
+
+__device__ __forceinline__ float dot_bf16x8(uint4 w, uint4 x) {
+  float s = lo_bf16(w.x) * lo_bf16(x.x);
+  s += hi_bf16(w.x) * hi_bf16(x.x);
+  s += lo_bf16(w.y) * lo_bf16(x.y);
+  s += hi_bf16(w.y) * hi_bf16(x.y);
+  s += lo_bf16(w.z) * lo_bf16(x.z);
+  s += hi_bf16(w.z) * hi_bf16(x.z);
+  s += lo_bf16(w.w) * lo_bf16(x.w);
+  s += hi_bf16(w.w) * hi_bf16(x.w);
+  return s;
+}
+
+__device__ __forceinline__ float dot_f32x8(uint4 w, float4 x0, float4 x1) {
+  float s = lo_bf16(w.x) * x0.x;
+  s += hi_bf16(w.x) * x0.y;
+  s += lo_bf16(w.y) * x0.z;
+  s += hi_bf16(w.y) * x0.w;
+  s += lo_bf16(w.z) * x1.x;
+  s += hi_bf16(w.z) * x1.y;
+  s += lo_bf16(w.w) * x1.z;
+  s += hi_bf16(w.w) * x1.w;
+  return s;
+}
+
+// Lane p's weight chunks of row `row` ([rows, K] bf16), issued at once.
+__device__ __forceinline__ void load_row_chunks(const uint16_t* w, int row, int K, int p,
+                                                uint4 (&wr)[kGemvMaxChunks]) {
+  const int nch = K / 128;
+  const uint4* src = reinterpret_cast<const uint4*>(w + static_cast<int64_t>(row) * K);
+#pragma unroll
+  for (int c = 0; c < kGemvMaxChunks; ++c)
+    wr[c] = c < nch ? src[c * 16 + p] : make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Copies `bytes` (a multiple of 16) from global memory into LDS.
+__device__ __forceinline__ void stage(const void* src, void* lds, int bytes) {
+  const uint4* s = static_cast<const uint4*>(src);
+  uint4* d = static_cast<uint4*>(lds);
+  for (int i = threadIdx.x; i < bytes / 16; i += blockDim.x) d[i] = s[i];
+}
+
+}  // namespace parrot

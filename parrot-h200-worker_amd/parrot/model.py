@@ -375,9 +375,24 @@ class LocalGQA(nn.Module):
             self.__dict__["_qkv_weight"] = cached
         return cached[1]
 
-    def decode(self, x: Tensor, cache: LocalKVCache, position: int,
+    def decodes_mixed(self, first: Tensor, position_device: Tensor | None) -> bool:
+        """Whether ``decode`` can take its input as a depth mix (``mix=``)
+        and make it inside the q|k|v projection's launch."""
+        from . import hip_moe
+        c = self.cfg
+        return (self._hip(first) and position_device is not None and
+                hip_moe.decode_qkv_supported(first.numel() // first.shape[-1], c.dim, c.n_heads,
+                                             c.n_kv_heads, c.head_dim))
+
+    def decode(self, x: Tensor | None, cache: LocalKVCache, position: int,
                addend: Tensor | None = None, defer_sum: bool = False,
-               position_device: Tensor | None = None) -> Tensor:
+               position_device: Tensor | None = None, mix: tuple | None = None) -> Tensor:
+        """One decode step; ``mix = (depth_module, sources, norm)`` in place
+        of x gives the input as that depth mix + norm (see decodes_mixed)."""
+        if mix is not None:
+            if not self.decodes_mixed(mix[1][0], position_device):
+                raise RuntimeError("this decode step cannot take its input as a depth mix")
+            x = mix[1][0]  # shape, dtype and device of the input rows
         if x.shape[1] != 1:
             raise ValueError("decode expects one model position")
         if defer_sum:
@@ -389,7 +404,10 @@ class LocalGQA(nn.Module):
             # and value and attends over the window (parrot/model.py:239-262).
             from . import hip_moe
             cos, sin = _rope_tables(c, x.new_empty(0, dtype=torch.float32))
-            if self._fused_projections():
+            if mix is not None:
+                q, k, v = hip_moe.decode_qkv(None, self._packed_qkv(), cos, sin, c.n_heads,
+                                             c.n_kv_heads, c.head_dim, position_device, mix=mix)
+            elif self._fused_projections():
                 q, k, v = hip_moe.proj_rope_qkv(x, self._qkv_fragments(), cos, sin, c.n_heads,
                                                 c.n_kv_heads, c.head_dim,
                                                 start_device=position_device)
@@ -1008,15 +1026,24 @@ class Parrot(nn.Module):
         stream = _AttnRes(x, cfg.depth_block_size) if cfg.residual == "attnres" else None
         index = 0
         for block, cache in zip(self.blocks, state.layers):
-            h = self._mixed_input(stream, x, index, block.attention_norm)
             addend = stream.partial if stream is not None else None
             if isinstance(block.attention, LocalGQA):
                 if not isinstance(cache, LocalKVCache):
                     raise ValueError("Local attention received an MLA cache")
             elif not isinstance(cache, MLALatentCache):
                 raise ValueError("MLA attention received a local cache")
-            out = block.attention.decode(h, cache, state.position, addend=addend,
-                                         position_device=state.position_device)
+            if (stream is not None and isinstance(block.attention, LocalGQA) and
+                    self.config.depth_backend == "hip" and
+                    block.attention.decodes_mixed(stream.sources()[0], state.position_device)):
+                # The input's depth mix + norm runs inside the q|k|v launch.
+                out = block.attention.decode(
+                    None, cache, state.position, addend=addend,
+                    position_device=state.position_device,
+                    mix=(self.depth_mix[index], stream.sources(), block.attention_norm))
+            else:
+                h = self._mixed_input(stream, x, index, block.attention_norm)
+                out = block.attention.decode(h, cache, state.position, addend=addend,
+                                             position_device=state.position_device)
             if stream is None:
                 x = x + out
             else:

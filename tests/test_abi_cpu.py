@@ -137,6 +137,18 @@ def test_argument_validation_without_gpu(lib):
                                                   fake, null) == -1
     assert lib.parrot_decode_attention_latent_f32(fake, fake, fake, fake, 2, 8, 128, 1 << 16,
                                                   0.1, fake, null) == -3
+    # decode q|k|v: x or sources, tokens <= 16, dim % 128 <= 1024, head_dim even
+    qkv = lambda **kw: lib.parrot_decode_qkv_bf16(*[kw.get(k, v) for k, v in (
+        ("x", fake), ("srcs", null), ("n", 0), ("q0", null), ("sw", null), ("se", 1e-6),
+        ("nw", null), ("ne", 1e-6), ("tokens", 2), ("dim", 768), ("w", fake), ("h", 8),
+        ("hk", 2), ("d", 96), ("cos", fake), ("sin", fake), ("maxp", 4096), ("pos", fake),
+        ("q", fake), ("k", fake), ("v", fake), ("stream", null))])
+    assert qkv(x=null) == -1 and qkv(pos=null) == -1 and qkv(v=null) == -1
+    assert qkv(x=null, srcs=ctypes.cast(srcs, ctypes.c_void_p), n=2) == -1  # query missing
+    assert qkv(tokens=-1) == -2 and qkv(d=0) == -2 and qkv(maxp=0) == -2
+    assert qkv(tokens=17) == -3 and qkv(dim=1152) == -3 and qkv(dim=704) == -3
+    assert qkv(d=95) == -3 and qkv(h=3, hk=1, d=6) == -3
+    assert qkv(w=fake + 8) == -5
     # decode MoE with its input's depth mix: sources, n_sources, dim <= 1024
     mix_moe = lambda **kw: lib.parrot_depth_mix_decode_moe_bf16(*[kw.get(k, v) for k, v in (
         ("srcs", ctypes.cast(srcs, ctypes.c_void_p)), ("n", 2), ("q", fake), ("sw", fake),

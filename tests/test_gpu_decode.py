@@ -163,6 +163,42 @@ def test_decode_graph_matches_eager():
                                        getattr(theirs, name)[:, :, :48])
 
 
+@pytest.mark.parametrize("tokens,sources,position", [(1, 3, 0), (4, 9, 150), (16, 1, 299)])
+def test_decode_qkv(tokens, sources, position):
+    """The decode q|k|v projection + RoPE: from x, against the fused MFMA
+    projection + RoPE (the fp32 sums differ in order, so the bf16 values may
+    differ in the last place); from a depth mix, equal bit for bit to
+    depth_mix_norm followed by the x path."""
+    from test_gpu_moe import _Depth, _Norm
+    from test_gpu_proj import _packed
+    from parrot import hip_moe
+    from parrot.model import ModelConfig, _rope_tables
+    cfg = ModelConfig()
+    H, Hk, d, dim = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.dim
+    n = (H + 2 * Hk) * d
+    _say(f"decode qkv T={tokens} S={sources} p={position}")
+    g = torch.Generator().manual_seed(200 + tokens)
+    w = (torch.randn(n, dim, generator=g) * dim ** -0.5).bfloat16().cuda()
+    x = torch.randn(tokens, 1, dim, generator=g).bfloat16().cuda()
+    cos, sin = _rope_tables(cfg, torch.empty(0, device="cuda"))
+    pos = torch.tensor([position], dtype=torch.int32, device="cuda")
+    torch.manual_seed(300 + sources)
+    depth = _Depth(dim).cuda().bfloat16()
+    norm = _Norm(dim).cuda().bfloat16()
+    src = [(torch.randn(tokens, 1, dim, generator=g) * (1 + s)).bfloat16().cuda()
+           for s in range(sources)]
+    with torch.no_grad():
+        q, k, v = hip_moe.decode_qkv(x, w, cos, sin, H, Hk, d, pos)
+        q2, k2, v2 = hip_moe.proj_rope_qkv(x, _packed(w), cos, sin, H, Hk, d, start_device=pos)
+        h = hip_moe.depth_mix_norm(depth, [s.view(tokens, dim) for s in src], norm)
+        qh, kh, vh = hip_moe.decode_qkv(h.view(tokens, 1, dim), w, cos, sin, H, Hk, d, pos)
+        qm, km, vm = hip_moe.decode_qkv(None, w, cos, sin, H, Hk, d, pos, mix=(depth, src, norm))
+    assert q.shape == q2.shape and k.shape == k2.shape and v.shape == v2.shape
+    for got, ref in ((q, q2), (k, k2), (v, v2)):
+        assert (got.float() - ref.float()).abs().max() <= 2 ** -6 * ref.float().abs().max()
+    assert torch.equal(qm, qh) and torch.equal(km, kh) and torch.equal(vm, vh)
+
+
 @pytest.mark.parametrize("tokens,sources,with_addend", [
     (1, 1, True), (1, 4, False), (3, 9, True), (8, 5, True), (16, 9, False)])
 def test_decode_moe_mixes_its_input(tokens, sources, with_addend):
