@@ -431,7 +431,7 @@ def cpu_layer_baselines(seconds: float) -> dict:
 # ---------------------------------------------------------------------------
 
 TRAFFIC_FILE = ROOT / "profiles" / "experts_gate_up_C4_traffic.json"
-TRAFFIC_KERNEL = "grouped_gemm_stream_kernel<32, 32, 4, 1>"
+TRAFFIC_KERNEL = "grouped_gemm_stream_kernel<32, 32, 4, 1, 1>"
 TRAFFIC_LAUNCHES = 20
 CALIBRATION_ELEMS = 1 << 27       # bf16: 256 MiB read + 256 MiB written per launch
 CALIBRATION_LAUNCHES = 5
