@@ -196,15 +196,19 @@ int parrot_decode_qkv_bf16(const void* x, const void* const* sources, int32_t n_
  * [tokens, dim] bf16 and absorbed_query [query_rows, dim] bf16 (the absorbed
  * query map, H * latent_dim rows), products and sums in fp32; latent
  * [tokens, latent_dim] bf16 = bf16(x . kv_down^T), kv_down [latent_dim, dim]
- * bf16.  tokens <= 16, dim % 128 == 0 and dim <= 2048, query_rows and
- * latent_dim multiples of 16; x, absorbed_query and kv_down 16-byte aligned.
+ * bf16.  With x NULL the rows are the depth mix of `sources` normalised by
+ * the attention norm, as parrot_decode_qkv_bf16 takes them (dim <= 1024).
+ * tokens <= 16, dim % 128 == 0 and dim <= 2048, query_rows and latent_dim
+ * multiples of 16; x, absorbed_query and kv_down 16-byte aligned.
  * Replaces F.linear(x.float(), absorbed_query.float()) and kv_down(x) in
  * GlobalMLA.decode (parrot/model.py:417-422), the projections that
  * metal_mla_attention_decode (parrot/metal_moe.py:293-326) fuses. */
-int parrot_mla_decode_in_bf16(const void* x, int32_t tokens, int32_t dim,
-                              const void* absorbed_query, int32_t query_rows,
-                              const void* kv_down, int32_t latent_dim, float* q_latent,
-                              void* latent, void* stream);
+int parrot_mla_decode_in_bf16(const void* x, const void* const* sources, int32_t n_sources,
+                              const void* query, const void* score_norm_weight, float score_eps,
+                              const void* attention_norm_weight, float norm_eps,
+                              int32_t tokens, int32_t dim, const void* absorbed_query,
+                              int32_t query_rows, const void* kv_down, int32_t latent_dim,
+                              float* q_latent, void* latent, void* stream);
 
 /* The MLA layers' decode-step output projection after the latent attention:
  * out [tokens, dim] bf16 = bf16(context . absorbed_output^T), then

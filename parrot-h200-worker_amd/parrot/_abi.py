@@ -92,7 +92,8 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _p, _i32, _p, _p, _f32, _p, _f32, _i32, _i32, _p, _i32, _i32, _i32, _p, _p, _i32,
          _p, _p, _p, _p, _p]),
     "parrot_mla_decode_in_bf16": (
-        ctypes.c_int, [_p, _i32, _i32, _p, _i32, _p, _i32, _p, _p, _p]),
+        ctypes.c_int,
+        [_p, _p, _i32, _p, _p, _f32, _p, _f32, _i32, _i32, _p, _i32, _p, _i32, _p, _p, _p]),
     "parrot_mla_decode_out_bf16": (ctypes.c_int, [_p, _i32, _i32, _p, _i32, _p, _p, _p]),
     "parrot_experts_gate_up_grouping_bf16": (
         ctypes.c_int,

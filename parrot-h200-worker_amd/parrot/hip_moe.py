@@ -863,21 +863,51 @@ def mla_decode_supported(tokens: int, dim: int, width: int) -> bool:
             and width % 128 == 0 and width <= 2048 and tokens * width * 4 <= 65536)
 
 
-def mla_decode_in(x: Tensor, absorbed_query: Tensor, kv_down: Tensor) -> tuple[Tensor, Tensor]:
-    """The MLA decode step's projections in one launch: x [b, 1, dim] bf16 ->
-    (q_latent [b, H * r] fp32 = x.float() absorbed_query.float()^T,
-    latent [b, 1, r] bf16 = kv_down(x)); cf. parrot/model.py:417-422."""
-    _require(x, "HIP MLA decode projections")
-    b, dim = x.shape[0], x.shape[-1]
+def _decode_mix_args(mix: tuple) -> tuple[tuple, Tensor, list[Tensor]]:
+    """C-ABI arguments (sources .. norm eps) of a decode launch that makes
+    its input as ``depth_mix_norm(*mix)``; also the first source row block
+    (shape, dtype and device of the input) and the rows to keep alive."""
+    depth, sources, norm = mix
+    first = sources[0]
+    b, dim = first.numel() // first.shape[-1], first.shape[-1]
+    rows = [s.reshape(b, dim).contiguous() for s in sources]
+    for s in rows:
+        if s.dtype != first.dtype or s.device != first.device:
+            raise RuntimeError("depth sources must share shape, dtype and device")
+    if not 1 <= len(rows) <= MAX_DEPTH_SOURCES:
+        raise RuntimeError(f"HIP depth mixing supports one to {MAX_DEPTH_SOURCES} sources")
+    array = _SourceArray(*([t.data_ptr() for t in rows] +
+                           [rows[0].data_ptr()] * (MAX_DEPTH_SOURCES - len(rows))))
+    args = (ctypes.cast(array, ctypes.c_void_p), len(rows), ptr(depth.query),
+            ptr(depth.norm.weight), float(depth.norm.eps), ptr(norm.weight), float(norm.eps))
+    return args, rows[0], rows + [array]
+
+
+def mla_decode_in(x: Tensor | None, absorbed_query: Tensor, kv_down: Tensor,
+                  mix: tuple | None = None) -> tuple[Tensor, Tensor]:
+    """The MLA decode step's projections in one launch: x [b, 1, dim] bf16
+    (or ``mix = (depth_module, sources, norm)``, whose ``depth_mix_norm`` the
+    launch computes itself) -> (q_latent [b, H * r] fp32 = x.float()
+    absorbed_query.float()^T, latent [b, 1, r] bf16 = kv_down(x)); cf.
+    parrot/model.py:417-422."""
+    keep = None
+    if mix is not None:
+        mix_args, ref, keep = _decode_mix_args(mix)
+        mix_args = (None,) + mix_args
+    else:
+        ref = x.reshape(x.shape[0], x.shape[-1]).contiguous()
+        mix_args = (ptr(ref), None, 0, None, None, 0.0, None, 0.0)
+    _require(ref, "HIP MLA decode projections")
+    b, dim = ref.shape
     for w in (absorbed_query, kv_down):
-        if w.dtype != x.dtype or not w.is_contiguous() or w.shape[-1] != dim:
+        if w.dtype != ref.dtype or not w.is_contiguous() or w.shape[-1] != dim:
             raise RuntimeError("MLA decode weights must be contiguous [rows, dim] in x's dtype")
-    x2 = x.reshape(b, dim).contiguous()
-    q = torch.empty((b, absorbed_query.shape[0]), dtype=torch.float32, device=x.device)
-    latent = torch.empty((b, 1, kv_down.shape[0]), dtype=x.dtype, device=x.device)
+    q = torch.empty((b, absorbed_query.shape[0]), dtype=torch.float32, device=ref.device)
+    latent = torch.empty((b, 1, kv_down.shape[0]), dtype=ref.dtype, device=ref.device)
     _abi.check(_abi.load().parrot_mla_decode_in_bf16(
-        ptr(x2), b, dim, ptr(absorbed_query), absorbed_query.shape[0], ptr(kv_down),
-        kv_down.shape[0], ptr(q), ptr(latent), _stream(x.device)), "parrot_mla_decode_in_bf16")
+        *mix_args, b, dim, ptr(absorbed_query), absorbed_query.shape[0], ptr(kv_down),
+        kv_down.shape[0], ptr(q), ptr(latent), _stream(ref.device)), "parrot_mla_decode_in_bf16")
+    del keep  # alive until the launch is enqueued (it is)
     return q, latent
 
 

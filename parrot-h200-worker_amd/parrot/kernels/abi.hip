@@ -238,6 +238,32 @@ int parrot_decode_attention_latent_f32(const float* q, const void* latent_new, v
       position, batch, heads, latent_dim, max_positions, scale, out, as_stream(stream)));
 }
 
+// The depth mix a decode launch makes its input rows with: checks and fills
+// `mix` from the sources (as parrot_depth_mix_bf16 takes them) and the norms.
+static int make_decode_mix(const void* const* sources, int32_t n_sources, const void* query,
+                           const void* score_norm_weight, float score_eps,
+                           const void* norm_weight, float norm_eps, parrot::DecodeMix& mix) {
+  if (!sources || !query || !score_norm_weight || !norm_weight) return PARROT_ERR_NULL_POINTER;
+  if (n_sources < 1 || n_sources > kMaxDepthSources) return PARROT_ERR_UNSUPPORTED;
+  uintptr_t bits = reinterpret_cast<uintptr_t>(query) |
+                   reinterpret_cast<uintptr_t>(score_norm_weight) |
+                   reinterpret_cast<uintptr_t>(norm_weight);
+  for (int s = 0; s < kMaxDepthSources; ++s) {
+    const void* p = sources[s < n_sources ? s : 0];
+    if (!p) return PARROT_ERR_NULL_POINTER;
+    bits |= reinterpret_cast<uintptr_t>(p);
+    mix.srcs.src[s] = static_cast<const uint16_t*>(p);
+  }
+  if (bits & 7u) return PARROT_ERR_ALIGNMENT;
+  mix.n_sources = n_sources;
+  mix.query = static_cast<const uint16_t*>(query);
+  mix.score_w = static_cast<const uint16_t*>(score_norm_weight);
+  mix.score_eps = score_eps;
+  mix.out_w = static_cast<const uint16_t*>(norm_weight);
+  mix.out_eps = norm_eps;
+  return PARROT_OK;
+}
+
 int parrot_decode_qkv_bf16(const void* x, const void* const* sources, int32_t n_sources,
                            const void* query, const void* score_norm_weight, float score_eps,
                            const void* attention_norm_weight, float norm_eps, int32_t tokens,
@@ -257,24 +283,9 @@ int parrot_decode_qkv_bf16(const void* x, const void* const* sources, int32_t n_
   if ((x && !aligned16(x)) || !aligned16(qkv_weight)) return PARROT_ERR_ALIGNMENT;
   parrot::DecodeQkvArgs a{};
   if (!x) {
-    if (!query || !score_norm_weight || !attention_norm_weight) return PARROT_ERR_NULL_POINTER;
-    if (n_sources < 1 || n_sources > kMaxDepthSources) return PARROT_ERR_UNSUPPORTED;
-    uintptr_t bits = reinterpret_cast<uintptr_t>(query) |
-                     reinterpret_cast<uintptr_t>(score_norm_weight) |
-                     reinterpret_cast<uintptr_t>(attention_norm_weight);
-    for (int s = 0; s < kMaxDepthSources; ++s) {
-      const void* p = sources[s < n_sources ? s : 0];
-      if (!p) return PARROT_ERR_NULL_POINTER;
-      bits |= reinterpret_cast<uintptr_t>(p);
-      a.mix.srcs.src[s] = static_cast<const uint16_t*>(p);
-    }
-    if (bits & 7u) return PARROT_ERR_ALIGNMENT;
-    a.mix.n_sources = n_sources;
-    a.mix.query = static_cast<const uint16_t*>(query);
-    a.mix.score_w = static_cast<const uint16_t*>(score_norm_weight);
-    a.mix.score_eps = score_eps;
-    a.mix.out_w = static_cast<const uint16_t*>(attention_norm_weight);
-    a.mix.out_eps = norm_eps;
+    if (int rc = make_decode_mix(sources, n_sources, query, score_norm_weight, score_eps,
+                                 attention_norm_weight, norm_eps, a.mix))
+      return rc;
   }
   a.x = static_cast<const uint16_t*>(x);
   a.tokens = tokens;
@@ -302,19 +313,30 @@ static int check_mla_decode(int32_t tokens, int32_t k, int elem_bytes) {
   return PARROT_OK;
 }
 
-int parrot_mla_decode_in_bf16(const void* x, int32_t tokens, int32_t dim,
-                              const void* absorbed_query, int32_t query_rows,
-                              const void* kv_down, int32_t latent_dim, float* q_latent,
-                              void* latent, void* stream) {
-  if (!x || !absorbed_query || !kv_down || !q_latent || !latent) return PARROT_ERR_NULL_POINTER;
+int parrot_mla_decode_in_bf16(const void* x, const void* const* sources, int32_t n_sources,
+                              const void* query, const void* score_norm_weight, float score_eps,
+                              const void* attention_norm_weight, float norm_eps,
+                              int32_t tokens, int32_t dim, const void* absorbed_query,
+                              int32_t query_rows, const void* kv_down, int32_t latent_dim,
+                              float* q_latent, void* latent, void* stream) {
+  if ((!x && !sources) || !absorbed_query || !kv_down || !q_latent || !latent)
+    return PARROT_ERR_NULL_POINTER;
   if (int rc = check_mla_decode(tokens, dim, 2)) return rc;
   if (query_rows <= 0 || latent_dim <= 0) return PARROT_ERR_BAD_SHAPE;
   if (query_rows % 16 || latent_dim % 16) return PARROT_ERR_UNSUPPORTED;
-  if (!aligned16(x) || !aligned16(absorbed_query) || !aligned16(kv_down))
+  if ((x && !aligned16(x)) || !aligned16(absorbed_query) || !aligned16(kv_down))
     return PARROT_ERR_ALIGNMENT;
+  parrot::DecodeMix mix{};
+  if (!x) {
+    if (int rc = make_decode_mix(sources, n_sources, query, score_norm_weight, score_eps,
+                                 attention_norm_weight, norm_eps, mix))
+      return rc;
+    if (dim > 1024) return PARROT_ERR_UNSUPPORTED;
+  }
   return status(parrot::launch_mla_decode_in(
-      static_cast<const uint16_t*>(x), tokens, dim, static_cast<const uint16_t*>(absorbed_query),
-      query_rows, static_cast<const uint16_t*>(kv_down), latent_dim, q_latent,
+      static_cast<const uint16_t*>(x), x ? nullptr : &mix, tokens, dim,
+      static_cast<const uint16_t*>(absorbed_query), query_rows,
+      static_cast<const uint16_t*>(kv_down), latent_dim, q_latent,
       static_cast<uint16_t*>(latent), as_stream(stream)));
 }
 
@@ -678,25 +700,11 @@ int parrot_depth_mix_decode_moe_bf16(
     const void* packed_gate_up, const void* packed_down, const void* shared_gate_up,
     const void* shared_down, const void* addend, void* out, int64_t* out_indices,
     float* out_weights, void* workspace, size_t workspace_bytes, void* stream) {
-  if (!sources || !query || !score_norm_weight || !moe_norm_weight) return PARROT_ERR_NULL_POINTER;
-  if (n_sources < 1 || n_sources > kMaxDepthSources || dim > 1024) return PARROT_ERR_UNSUPPORTED;
   parrot::DecodeMix mix{};
-  uintptr_t bits = reinterpret_cast<uintptr_t>(query) |
-                   reinterpret_cast<uintptr_t>(score_norm_weight) |
-                   reinterpret_cast<uintptr_t>(moe_norm_weight);
-  for (int s = 0; s < kMaxDepthSources; ++s) {
-    const void* p = sources[s < n_sources ? s : 0];
-    if (!p) return PARROT_ERR_NULL_POINTER;
-    bits |= reinterpret_cast<uintptr_t>(p);
-    mix.srcs.src[s] = static_cast<const uint16_t*>(p);
-  }
-  if (bits & 7u) return PARROT_ERR_ALIGNMENT;
-  mix.n_sources = n_sources;
-  mix.query = static_cast<const uint16_t*>(query);
-  mix.score_w = static_cast<const uint16_t*>(score_norm_weight);
-  mix.score_eps = score_eps;
-  mix.out_w = static_cast<const uint16_t*>(moe_norm_weight);
-  mix.out_eps = norm_eps;
+  if (int rc = make_decode_mix(sources, n_sources, query, score_norm_weight, score_eps,
+                               moe_norm_weight, norm_eps, mix))
+    return rc;
+  if (dim > 1024) return PARROT_ERR_UNSUPPORTED;
   return decode_moe_entry(nullptr, &mix, tokens, dim, experts, hidden_dim, shared_dim,
                           router_weight, logit_bias, packed_gate_up, packed_down,
                           shared_gate_up, shared_down, addend, out, out_indices, out_weights,

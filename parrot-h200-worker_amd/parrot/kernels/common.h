@@ -361,9 +361,6 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_new,
                                    int head_dim, int max_pos, int window, float scale,
                                    uint16_t* out, hipStream_t s);
 size_t mla_decode_lds_bytes(int tokens, int k, int elem_bytes);
-hipError_t launch_mla_decode_in(const uint16_t* x, int tokens, int dim, const uint16_t* wq,
-                                int nq, const uint16_t* wkv, int nl, float* q_out,
-                                uint16_t* lat_out, hipStream_t s);
 hipError_t launch_mla_decode_out(const float* ctx, int tokens, int width, const uint16_t* wo,
                                  int dim, const uint16_t* addend, uint16_t* out, hipStream_t s);
 hipError_t launch_decode_attention_latent(const float* q, const uint16_t* latent_new,
@@ -403,6 +400,9 @@ struct DecodeQkvArgs {
   uint16_t* v;              // [tokens, Hk, 1, d]
 };
 int decode_qkv_max_dim();
+hipError_t launch_mla_decode_in(const uint16_t* x, const DecodeMix* mix, int tokens, int dim,
+                                const uint16_t* wq, int nq, const uint16_t* wkv, int nl,
+                                float* q_out, uint16_t* lat_out, hipStream_t s);
 hipError_t launch_decode_qkv(const DecodeQkvArgs& a, hipStream_t s);
 
 hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens, int dim,

@@ -20,29 +20,61 @@
 // tokens' inputs are staged in LDS once, and each token's 16 partial sums are
 // added by four DPP steps in a fixed order.
 #include "decode_gemv.h"
+#include "depth_mix_core.h"
 
 namespace parrot {
 
 namespace {
 
 // Workgroups [0, nq / 16): q_latent rows of absorbed_query; the rest: latent
-// rows of kv_down.  x [T, K] bf16 is staged in LDS (T K 2 bytes).
+// rows of kv_down.  x [T, K] bf16 is staged in LDS (T K 2 bytes); with a
+// depth mix (mix.n_sources > 0) workgroup (x, t) instead mixes and
+// normalises token t's row into LDS (depth_mix_core.h) and serves token t.
 __global__ __launch_bounds__(256) void mla_decode_in_kernel(
-    const uint16_t* __restrict__ x, int tokens, int K, const uint16_t* __restrict__ wq, int nq,
-    const uint16_t* __restrict__ wkv, int nl, float* __restrict__ q_out,
-    uint16_t* __restrict__ lat_out) {
+    const uint16_t* __restrict__ x, DecodeMix mix, int tokens, int K,
+    const uint16_t* __restrict__ wq, int nq, const uint16_t* __restrict__ wkv, int nl,
+    float* __restrict__ q_out, uint16_t* __restrict__ lat_out) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
-  const int j = threadIdx.x >> 4, p = threadIdx.x & 15;
+  __shared__ DepthMixLds mix_lds;
+  const int tid = threadIdx.x;
+  const int j = tid >> 4, p = tid & 15;
   const int blocks_q = nq / kGemvRows;
   const bool is_q = static_cast<int>(blockIdx.x) < blocks_q;  // uniform
   const int row = (is_q ? blockIdx.x : blockIdx.x - blocks_q) * kGemvRows + j;
   uint4 wr[kGemvMaxChunks];
   load_row_chunks(is_q ? wq : wkv, row, K, p, wr);
-  stage(x, xs, tokens * K * 2);
+  int t_begin = 0, t_end = tokens;
+  if (mix.n_sources > 0) {
+    t_begin = blockIdx.y;
+    t_end = t_begin + 1;
+    const int chunks = K >> 2;
+    const bool has = tid < chunks;
+    const int ic = has ? tid : 0;
+    const int64_t base = static_cast<int64_t>(t_begin) * chunks;
+    uint2 v[kMaxDepthSources];
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s)
+      v[s] = reinterpret_cast<const uint2*>(mix.srcs.src[s])[base + ic];
+    const uint2 q = reinterpret_cast<const uint2*>(mix.query)[ic];
+    const uint2 g = reinterpret_cast<const uint2*>(mix.score_w)[ic];
+    const uint2 g_out = reinterpret_cast<const uint2*>(mix.out_w)[ic];
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s)
+      if (!has || s >= mix.n_sources) v[s] = make_uint2(0u, 0u);
+    const int waves = (K + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
+    const int lane = tid & (kWave - 1), wave = tid >> 6;
+    const uint2 mixed = depth_mix_chunk(v, q, g, has, mix.n_sources, waves, wave, lane, K,
+                                        mix.score_eps, mix_lds);
+    const uint2 o = depth_mix_norm_chunk(mixed, g_out, has, waves, wave, lane, K, mix.out_eps,
+                                         mix_lds);
+    if (has) reinterpret_cast<uint2*>(xs)[tid] = o;
+  } else {
+    stage(x, xs, tokens * K * 2);
+  }
   __syncthreads();
   const int nch = K / 128;
-  for (int t = 0; t < tokens; ++t) {
-    const uint4* xt = reinterpret_cast<const uint4*>(xs + t * K);
+  for (int t = t_begin; t < t_end; ++t) {
+    const uint4* xt = reinterpret_cast<const uint4*>(xs + (t - t_begin) * K);
     float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < kGemvMaxChunks; ++c)
@@ -90,13 +122,15 @@ size_t mla_decode_lds_bytes(int tokens, int k, int elem_bytes) {
   return static_cast<size_t>(tokens) * k * elem_bytes;
 }
 
-hipError_t launch_mla_decode_in(const uint16_t* x, int tokens, int dim, const uint16_t* wq,
-                                int nq, const uint16_t* wkv, int nl, float* q_out,
-                                uint16_t* lat_out, hipStream_t s) {
+hipError_t launch_mla_decode_in(const uint16_t* x, const DecodeMix* mix, int tokens, int dim,
+                                const uint16_t* wq, int nq, const uint16_t* wkv, int nl,
+                                float* q_out, uint16_t* lat_out, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
-  const dim3 grid((nq + nl) / kGemvRows);
-  mla_decode_in_kernel<<<grid, 256, mla_decode_lds_bytes(tokens, dim, 2), s>>>(
-      x, tokens, dim, wq, nq, wkv, nl, q_out, lat_out);
+  const DecodeMix none{};
+  const bool mixing = mix != nullptr;
+  const dim3 grid((nq + nl) / kGemvRows, mixing ? tokens : 1);
+  mla_decode_in_kernel<<<grid, 256, mla_decode_lds_bytes(mixing ? 1 : tokens, dim, 2), s>>>(
+      x, mixing ? *mix : none, tokens, dim, wq, nq, wkv, nl, q_out, lat_out);
   return hipGetLastError();
 }
 

@@ -548,9 +548,25 @@ class GlobalMLA(nn.Module):
             self.__dict__["_absorbed_f32_weights"] = cached
         return cached[1]
 
-    def decode(self, x: Tensor, cache: MLALatentCache, position: int,
+    def decodes_mixed(self, first: Tensor, position_device: Tensor | None) -> bool:
+        """Whether ``decode`` can take its input as a depth mix (``mix=``)
+        and make it inside the projections' launch."""
+        from . import hip_moe
+        c = self.cfg
+        b = first.numel() // first.shape[-1]
+        return (c.uses_hip and _hip_inference(first) and position_device is not None and
+                c.dim <= 1024 and self.kv_down.weight.dtype == first.dtype and
+                hip_moe.mla_decode_supported(b, c.dim, c.n_heads * c.kv_latent_dim))
+
+    def decode(self, x: Tensor | None, cache: MLALatentCache, position: int,
                addend: Tensor | None = None, defer_sum: bool = False,
-               position_device: Tensor | None = None) -> Tensor:
+               position_device: Tensor | None = None, mix: tuple | None = None) -> Tensor:
+        """One decode step; ``mix = (depth_module, sources, norm)`` in place
+        of x gives the input as that depth mix + norm (see decodes_mixed)."""
+        if mix is not None:
+            if not self.decodes_mixed(mix[1][0], position_device):
+                raise RuntimeError("this decode step cannot take its input as a depth mix")
+            x = mix[1][0]  # shape, dtype and device of the input rows
         if x.shape[1] != 1:
             raise ValueError("decode expects one model position")
         if defer_sum:
@@ -566,7 +582,9 @@ class GlobalMLA(nn.Module):
                     and self.kv_down.weight.dtype == x.dtype):
                 # Three launches: projections, latent attention, output map.
                 absorbed_q, absorbed_o = self._absorbed()
-                q_latent, latent = hip_moe.mla_decode_in(x, absorbed_q, self.kv_down.weight)
+                q_latent, latent = hip_moe.mla_decode_in(None if mix is not None else x,
+                                                         absorbed_q, self.kv_down.weight,
+                                                         mix=mix)
                 context = hip_moe.decode_attention_latent(
                     q_latent, latent, cache.latent, position_device, c.n_heads,
                     c.head_dim ** -0.5)
@@ -1032,8 +1050,7 @@ class Parrot(nn.Module):
                     raise ValueError("Local attention received an MLA cache")
             elif not isinstance(cache, MLALatentCache):
                 raise ValueError("MLA attention received a local cache")
-            if (stream is not None and isinstance(block.attention, LocalGQA) and
-                    self.config.depth_backend == "hip" and
+            if (stream is not None and self.config.depth_backend == "hip" and
                     block.attention.decodes_mixed(stream.sources()[0], state.position_device)):
                 # The input's depth mix + norm runs inside the q|k|v launch.
                 out = block.attention.decode(

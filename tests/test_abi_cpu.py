@@ -163,9 +163,13 @@ def test_argument_validation_without_gpu(lib):
     # MLA decode projections: tokens <= 16, K % 128 <= 2048, rows % 16,
     # staged input <= 64 KB, alignment
     mla_in = lambda **kw: lib.parrot_mla_decode_in_bf16(*[kw.get(k, v) for k, v in (
-        ("x", fake), ("tokens", 2), ("dim", 768), ("wq", fake), ("nq", 1024), ("wkv", fake),
-        ("nl", 128), ("q", fake), ("lat", fake), ("stream", null))])
+        ("x", fake), ("srcs", null), ("n", 0), ("q0", null), ("sw", null), ("se", 1e-6),
+        ("nw", null), ("ne", 1e-6), ("tokens", 2), ("dim", 768), ("wq", fake), ("nq", 1024),
+        ("wkv", fake), ("nl", 128), ("q", fake), ("lat", fake), ("stream", null))])
     assert mla_in(x=null) == -1 and mla_in(lat=null) == -1
+    assert mla_in(x=null, srcs=ctypes.cast(srcs, ctypes.c_void_p), n=2) == -1  # query missing
+    assert mla_in(x=null, srcs=ctypes.cast(srcs, ctypes.c_void_p), n=2, q0=fake, sw=fake,
+                  nw=fake, dim=1152) == -3  # the mix holds dim <= 1024
     assert mla_in(tokens=-1) == -2 and mla_in(nq=0) == -2
     assert mla_in(tokens=17) == -3 and mla_in(dim=704) == -3 and mla_in(dim=2176) == -3
     assert mla_in(nq=1000) == -3 and mla_in(nl=120) == -3

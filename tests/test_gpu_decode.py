@@ -163,6 +163,29 @@ def test_decode_graph_matches_eager():
                                        getattr(theirs, name)[:, :, :48])
 
 
+@pytest.mark.parametrize("tokens,sources", [(1, 2), (5, 9), (16, 4)])
+def test_mla_decode_in_mixes_its_input(tokens, sources):
+    """The MLA decode projections from a depth mix equal depth_mix_norm
+    followed by the x path, bit for bit."""
+    from test_gpu_moe import _Depth, _Norm
+    from parrot import hip_moe
+    dim, width, r = 768, 1024, 128
+    _say(f"mla decode in with its input mix T={tokens} S={sources}")
+    g = torch.Generator().manual_seed(500 + tokens)
+    wq = (torch.randn(width, dim, generator=g) * 0.05).bfloat16().cuda()
+    wkv = (torch.randn(r, dim, generator=g) * 0.05).bfloat16().cuda()
+    torch.manual_seed(600 + sources)
+    depth = _Depth(dim).cuda().bfloat16()
+    norm = _Norm(dim).cuda().bfloat16()
+    src = [(torch.randn(tokens, 1, dim, generator=g) * (1 + s)).bfloat16().cuda()
+           for s in range(sources)]
+    with torch.no_grad():
+        h = hip_moe.depth_mix_norm(depth, [s.view(tokens, dim) for s in src], norm)
+        q_ref, lat_ref = hip_moe.mla_decode_in(h.view(tokens, 1, dim), wq, wkv)
+        q, lat = hip_moe.mla_decode_in(None, wq, wkv, mix=(depth, src, norm))
+    assert torch.equal(q, q_ref) and torch.equal(lat, lat_ref)
+
+
 @pytest.mark.parametrize("tokens,sources,position", [(1, 3, 0), (4, 9, 150), (16, 1, 299)])
 def test_decode_qkv(tokens, sources, position):
     """The decode q|k|v projection + RoPE: from x, against the fused MFMA
