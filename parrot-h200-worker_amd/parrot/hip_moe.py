@@ -401,18 +401,9 @@ def decode_experts(module: "MoE", flat: Tensor | None, addend: Tensor | None = N
     the input rows are ``depth_mix_norm(depth_module, sources, norm)``, made
     inside the same launches (``flat`` is then None; dim <= 1024)."""
     cfg = module.cfg
+    keep = None
     if mix is not None:
-        depth, sources, norm = mix
-        first = sources[0]
-        _require(first, "The fused HIP decode MoE")
-        tokens, dim = first.numel() // first.shape[-1], first.shape[-1]
-        flat_sources = [s.reshape(tokens, dim).contiguous() for s in sources]
-        for s in flat_sources:
-            if s.dtype != first.dtype or s.device != first.device:
-                raise RuntimeError("depth sources must share shape, dtype and device")
-        if not 1 <= len(flat_sources) <= MAX_DEPTH_SOURCES:
-            raise RuntimeError(f"HIP depth mixing supports one to {MAX_DEPTH_SOURCES} sources")
-        flat = flat_sources[0]  # device, dtype and shape of the rows
+        mix_args, flat, keep = _decode_mix_args(mix)  # flat: shape, dtype, device of the rows
     _require(flat, "The fused HIP decode MoE")
     tokens, dim = flat.shape
     if tokens > DECODE_MAX_TOKENS:
@@ -442,14 +433,10 @@ def decode_experts(module: "MoE", flat: Tensor | None, addend: Tensor | None = N
             ptr(flat), tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim, *tail),
             "parrot_decode_moe_bf16")
         return out, indices, weights
-    array = _SourceArray(*([t.data_ptr() for t in flat_sources] +
-                           [flat_sources[0].data_ptr()] * (MAX_DEPTH_SOURCES - len(flat_sources))))
     _abi.check(lib.parrot_depth_mix_decode_moe_bf16(
-        ctypes.cast(array, ctypes.c_void_p), len(flat_sources), ptr(depth.query),
-        ptr(depth.norm.weight), float(depth.norm.eps), ptr(norm.weight), float(norm.eps),
-        tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim, *tail),
+        *mix_args, tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim, *tail),
         "parrot_depth_mix_decode_moe_bf16")
-    del flat_sources  # alive until the launch is enqueued (it is)
+    del keep  # alive until the launch is enqueued (it is)
     return out, indices, weights
 
 
@@ -818,27 +805,15 @@ def decode_qkv(x: Tensor | None, weight: Tensor, cos: Tensor, sin: Tensor, heads
     whose ``depth_mix_norm`` the launch computes itself; ``weight`` the
     stacked row-major q|k|v weight.  Returns q [b, heads, 1, d], k and v
     [b, kv_heads, 1, d] (cf. LocalGQA.decode, parrot/model.py:176-262)."""
+    keep = None
     if mix is not None:
-        depth, sources, norm = mix
-        first = sources[0]
-        b, dim = first.numel() // first.shape[-1], first.shape[-1]
-        rows = [s.reshape(b, dim).contiguous() for s in sources]
-        for s in rows:
-            if s.dtype != first.dtype or s.device != first.device:
-                raise RuntimeError("depth sources must share shape, dtype and device")
-        if not 1 <= len(rows) <= MAX_DEPTH_SOURCES:
-            raise RuntimeError(f"HIP depth mixing supports one to {MAX_DEPTH_SOURCES} sources")
-        ref = rows[0]
-        array = _SourceArray(*([t.data_ptr() for t in rows] +
-                               [rows[0].data_ptr()] * (MAX_DEPTH_SOURCES - len(rows))))
-        mix_args = (None, ctypes.cast(array, ctypes.c_void_p), len(rows), ptr(depth.query),
-                    ptr(depth.norm.weight), float(depth.norm.eps), ptr(norm.weight),
-                    float(norm.eps))
+        mix_args, ref, keep = _decode_mix_args(mix)
+        mix_args = (None,) + mix_args
     else:
-        b, dim = x.shape[0], x.shape[-1]
-        ref = x.reshape(b, dim).contiguous()
+        ref = x.reshape(x.shape[0], x.shape[-1]).contiguous()
         mix_args = (ptr(ref), None, 0, None, None, 0.0, None, 0.0)
     _require(ref, "HIP decode q|k|v projection")
+    b, dim = ref.shape
     if weight.dtype != ref.dtype or not weight.is_contiguous():
         raise RuntimeError("q|k|v weight must be contiguous in the input's dtype")
     if cos.dtype != torch.float32 or sin.dtype != torch.float32:
@@ -851,6 +826,7 @@ def decode_qkv(x: Tensor | None, weight: Tensor, cos: Tensor, sin: Tensor, heads
         *mix_args, b, dim, ptr(weight), heads, kv_heads, head_dim, ptr(cos), ptr(sin),
         cos.shape[0], ptr(position), ptr(q), ptr(k), ptr(v), _stream(ref.device)),
         "parrot_decode_qkv_bf16")
+    del keep  # alive until the launch is enqueued (it is)
     return q, k, v
 
 
