@@ -105,9 +105,9 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   __shared__ float lg[kMaxExperts];
   __shared__ int sel[2];
   __shared__ float sel_w[2];
-  __shared__ float part[4][4][kDecodeMaxTokens][32];  // [wave][k chunk][token][gate 16 | up 16]
+  __shared__ float part[4][4][32];  // [wave][k chunk][gate 16 | up 16]
   __shared__ DepthMixLds mix_lds;
-  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [rows of this slot][dim]
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // the slot's token row [dim]
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -116,8 +116,7 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   const bool shared = slot >= 2 * tokens;
   const int H = shared ? shared_dim : hidden_dim;
   if (slice * 16 >= H) return;  // uniform
-  const int t0 = shared ? slot - 2 * tokens : slot >> 1;
-  const int nt = 1;
+  const int t0 = shared ? slot - 2 * tokens : slot >> 1;  // the slot's token
   if (mix.n_sources > 0) {
     // The token's input row: depth mix + RMSNorm of its sources into LDS,
     // every load issued before the first wait (lanes past the row read
@@ -146,7 +145,7 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
     // The slot's activation row, staged in LDS as bf16; these loads are in
     // flight together with the router's (the barrier in route_token, or the
     // one below, orders them before use).
-    for (int i = tid; i < nt * dim / 8; i += 256)
+    for (int i = tid; i < dim / 8; i += 256)
       reinterpret_cast<uint4*>(xs)[i] =
           reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t0) * dim)[i];
   }
@@ -174,9 +173,7 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   const uint4* wg = reinterpret_cast<const uint4*>(w) + (2 * slice) * ksteps * 64 + lane;
   const uint4* wu = wg + ksteps * 64;
   const int c = lane >> 4;
-  float ag[kDecodeMaxTokens], au[kDecodeMaxTokens];
-#pragma unroll
-  for (int t = 0; t < kDecodeMaxTokens; ++t) ag[t] = au[t] = 0.0f;
+  float ag = 0.0f, au = 0.0f;
   for (int s0 = wave; s0 < ksteps; s0 += 32) {
     uint4 g[8], u[8];
 #pragma unroll
@@ -189,35 +186,25 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
     for (int i = 0; i < 8; ++i) {
       const int st = s0 + 4 * i;
       if (st < ksteps) {
-#pragma unroll
-        for (int t = 0; t < kDecodeMaxTokens; ++t) {
-          if (t < nt) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(xs + t * dim + st * 32 + c * 8);
-            ag[t] += dot8(g[i], xv);
-            au[t] += dot8(u[i], xv);
-          }
-        }
+        const uint4 xv = *reinterpret_cast<const uint4*>(xs + st * 32 + c * 8);
+        ag += dot8(g[i], xv);
+        au += dot8(u[i], xv);
       }
     }
   }
   const int r = lane & 15;
-#pragma unroll
-  for (int t = 0; t < kDecodeMaxTokens; ++t) {
-    if (t < nt) {
-      part[wave][c][t][r] = ag[t];
-      part[wave][c][t][16 + r] = au[t];
-    }
-  }
+  part[wave][c][r] = ag;
+  part[wave][c][16 + r] = au;
   __syncthreads();
-  if (tid < nt * 16) {
-    const int t = tid >> 4, rr = tid & 15;
+  if (tid < 16) {
+    const int rr = tid;
     float gs = 0.0f, us = 0.0f;
 #pragma unroll
     for (int wv = 0; wv < 4; ++wv)
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) {
-        gs += part[wv][cc][t][rr];
-        us += part[wv][cc][t][16 + rr];
+        gs += part[wv][cc][rr];
+        us += part[wv][cc][16 + rr];
       }
     const int64_t row = shared ? 2 * tokens + t0 : slot;
     hidden[row * hstride + slice * 16 + rr] = f32_to_bf16(swiglu(gs, us));
