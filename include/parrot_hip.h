@@ -210,6 +210,17 @@ int parrot_mla_decode_in_bf16(const void* x, const void* const* sources, int32_t
                               int32_t query_rows, const void* kv_down, int32_t latent_dim,
                               float* q_latent, void* latent, void* stream);
 
+/* A decode step's bias-free linear map of up to 16 rows, one launch: out
+ * [tokens, n] bf16 = bf16(x . weight^T), then bf16(addend + that) when
+ * addend [tokens, n] bf16 is given; x [tokens, k] bf16, weight [n, k] bf16
+ * row-major (nn.Linear), fp32 products and sums.  tokens <= 16, k % 128 ==
+ * 0 and k <= 2048, tokens * k * 2 <= 65536, n % 16 == 0; x and weight
+ * 16-byte aligned.  Replaces, at decode, the attention output projection of
+ * LocalGQA with its residual add (parrot/model.py:167-230;
+ * attention_output_decode_bf16, parrot/kernels/moe_bf16.metal:1364-1389). */
+int parrot_decode_linear_bf16(const void* x, int32_t tokens, int32_t k, const void* weight,
+                              int32_t n, const void* addend, void* out, void* stream);
+
 /* The MLA layers' decode-step output projection after the latent attention:
  * out [tokens, dim] bf16 = bf16(context . absorbed_output^T), then
  * bf16(addend + that) when addend [tokens, dim] bf16 is given; context

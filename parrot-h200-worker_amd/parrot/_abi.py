@@ -95,6 +95,7 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [_p, _p, _i32, _p, _p, _f32, _p, _f32, _i32, _i32, _p, _i32, _p, _i32, _p, _p, _p]),
     "parrot_mla_decode_out_bf16": (ctypes.c_int, [_p, _i32, _i32, _p, _i32, _p, _p, _p]),
+    "parrot_decode_linear_bf16": (ctypes.c_int, [_p, _i32, _i32, _p, _i32, _p, _p, _p]),
     "parrot_experts_gate_up_grouping_bf16": (
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),

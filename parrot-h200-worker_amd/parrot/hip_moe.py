@@ -887,6 +887,34 @@ def mla_decode_in(x: Tensor | None, absorbed_query: Tensor, kv_down: Tensor,
     return q, latent
 
 
+def decode_linear(x: Tensor, weight: Tensor, addend: Tensor | None = None) -> Tensor:
+    """bf16(x weight^T) [.., n] (+ addend, a bf16 sum) for at most 16 rows
+    in one launch; x [.., k] bf16, weight [n, k] (cf. the decode output
+    projection of LocalGQA, parrot/model.py:167-230)."""
+    _require(x, "HIP decode linear")
+    k = x.shape[-1]
+    rows = x.numel() // k
+    n = weight.shape[0]
+    if weight.dtype != x.dtype or not weight.is_contiguous() or weight.shape[1] != k:
+        raise RuntimeError("decode linear weight must be contiguous [n, k] in x's dtype")
+    x2 = x.reshape(rows, k).contiguous()
+    out = x.new_empty(x.shape[:-1] + (n,))
+    if addend is not None:
+        if addend.shape != out.shape or addend.dtype != out.dtype:
+            raise RuntimeError("addend must match the output")
+        addend = addend.contiguous()
+    _abi.check(_abi.load().parrot_decode_linear_bf16(
+        ptr(x2), rows, k, ptr(weight), n, ptr(addend), ptr(out), _stream(x.device)),
+        "parrot_decode_linear_bf16")
+    return out
+
+
+def decode_linear_supported(rows: int, k: int, n: int) -> bool:
+    """Shapes parrot_decode_linear_bf16 takes."""
+    return 1 <= rows <= 16 and k % 128 == 0 and k <= 2048 and rows * k * 2 <= 65536 and \
+        n % 16 == 0
+
+
 def mla_decode_out(context: Tensor, absorbed_output: Tensor,
                    addend: Tensor | None = None) -> Tensor:
     """bf16(context absorbed_output.float()^T) [b, 1, dim] (+ addend, a bf16

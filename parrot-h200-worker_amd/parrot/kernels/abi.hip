@@ -340,6 +340,18 @@ int parrot_mla_decode_in_bf16(const void* x, const void* const* sources, int32_t
       static_cast<uint16_t*>(latent), as_stream(stream)));
 }
 
+int parrot_decode_linear_bf16(const void* x, int32_t tokens, int32_t k, const void* weight,
+                              int32_t n, const void* addend, void* out, void* stream) {
+  if (!x || !weight || !out) return PARROT_ERR_NULL_POINTER;
+  if (int rc = check_mla_decode(tokens, k, 2)) return rc;
+  if (n <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (n % 16) return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(weight)) return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_decode_linear(
+      static_cast<const uint16_t*>(x), tokens, k, static_cast<const uint16_t*>(weight), n,
+      static_cast<const uint16_t*>(addend), static_cast<uint16_t*>(out), as_stream(stream)));
+}
+
 int parrot_mla_decode_out_bf16(const float* context, int32_t tokens, int32_t width,
                                const void* absorbed_output, int32_t dim, const void* addend,
                                void* out, void* stream) {

@@ -361,6 +361,8 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_new,
                                    int head_dim, int max_pos, int window, float scale,
                                    uint16_t* out, hipStream_t s);
 size_t mla_decode_lds_bytes(int tokens, int k, int elem_bytes);
+hipError_t launch_decode_linear(const uint16_t* x, int tokens, int k, const uint16_t* w, int n,
+                                const uint16_t* addend, uint16_t* out, hipStream_t s);
 hipError_t launch_mla_decode_out(const float* ctx, int tokens, int width, const uint16_t* wo,
                                  int dim, const uint16_t* addend, uint16_t* out, hipStream_t s);
 hipError_t launch_decode_attention_latent(const float* q, const uint16_t* latent_new,

@@ -87,25 +87,34 @@ __global__ __launch_bounds__(256) void mla_decode_in_kernel(
   }
 }
 
-// out [T, n] = bf16(context Wo^T) (+ addend, a second bf16 rounding);
-// context [T, K] fp32 is staged in LDS (T K 4 bytes).
-__global__ __launch_bounds__(256) void mla_decode_out_kernel(
-    const float* __restrict__ ctx, int tokens, int K, const uint16_t* __restrict__ wo, int n,
+// out [T, n] = bf16(ctx Wo^T) (+ addend, a second bf16 rounding); ctx
+// [T, K] is fp32 (the MLA context) or bf16 (XT = uint16_t: the local
+// layers' attention output), staged in LDS (T K sizeof(XT) bytes).
+template <typename XT>
+__global__ __launch_bounds__(256) void decode_out_kernel(
+    const XT* __restrict__ ctx, int tokens, int K, const uint16_t* __restrict__ wo, int n,
     const uint16_t* __restrict__ addend, uint16_t* __restrict__ out) {
-  extern __shared__ __attribute__((aligned(16))) float cs[];
+  extern __shared__ __attribute__((aligned(16))) uint4 cs[];
   const int j = threadIdx.x >> 4, p = threadIdx.x & 15;
   const int row = blockIdx.x * kGemvRows + j;
   uint4 wr[kGemvMaxChunks];
   load_row_chunks(wo, row, K, p, wr);
-  stage(ctx, cs, tokens * K * 4);
+  stage(ctx, cs, tokens * K * static_cast<int>(sizeof(XT)));
   __syncthreads();
   const int nch = K / 128;
   for (int t = 0; t < tokens; ++t) {
-    const float4* ct = reinterpret_cast<const float4*>(cs + t * K);
     float acc = 0.0f;
+    if constexpr (sizeof(XT) == 4) {
+      const float4* ct = reinterpret_cast<const float4*>(cs) + t * K / 4;
 #pragma unroll
-    for (int c = 0; c < kGemvMaxChunks; ++c)
-      if (c < nch) acc += dot_f32x8(wr[c], ct[2 * (c * 16 + p)], ct[2 * (c * 16 + p) + 1]);
+      for (int c = 0; c < kGemvMaxChunks; ++c)
+        if (c < nch) acc += dot_f32x8(wr[c], ct[2 * (c * 16 + p)], ct[2 * (c * 16 + p) + 1]);
+    } else {
+      const uint4* ct = cs + t * K / 8;
+#pragma unroll
+      for (int c = 0; c < kGemvMaxChunks; ++c)
+        if (c < nch) acc += dot_bf16x8(wr[c], ct[c * 16 + p]);
+    }
     acc = row16_sum(acc);
     if (p == 0) {
       const int64_t o = static_cast<int64_t>(t) * n + row;
@@ -138,8 +147,17 @@ hipError_t launch_mla_decode_out(const float* ctx, int tokens, int width, const 
                                  int dim, const uint16_t* addend, uint16_t* out, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
   const dim3 grid(dim / kGemvRows);
-  mla_decode_out_kernel<<<grid, 256, mla_decode_lds_bytes(tokens, width, 4), s>>>(
+  decode_out_kernel<float><<<grid, 256, mla_decode_lds_bytes(tokens, width, 4), s>>>(
       ctx, tokens, width, wo, dim, addend, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_linear(const uint16_t* x, int tokens, int k, const uint16_t* w, int n,
+                                const uint16_t* addend, uint16_t* out, hipStream_t s) {
+  if (tokens == 0) return hipSuccess;
+  const dim3 grid(n / kGemvRows);
+  decode_out_kernel<uint16_t><<<grid, 256, mla_decode_lds_bytes(tokens, k, 2), s>>>(
+      x, tokens, k, w, n, addend, out);
   return hipGetLastError();
 }
 

@@ -174,6 +174,13 @@ def test_argument_validation_without_gpu(lib):
     assert mla_in(tokens=17) == -3 and mla_in(dim=704) == -3 and mla_in(dim=2176) == -3
     assert mla_in(nq=1000) == -3 and mla_in(nl=120) == -3
     assert mla_in(wq=fake + 8) == -5
+    lin = lambda **kw: lib.parrot_decode_linear_bf16(*[kw.get(k, v) for k, v in (
+        ("x", fake), ("tokens", 2), ("k", 768), ("w", fake), ("n", 768), ("add", null),
+        ("out", fake), ("stream", null))])
+    assert lin(x=null) == -1 and lin(out=null) == -1 and lin(n=0) == -2
+    assert lin(tokens=17) == -3 and lin(k=700) == -3 and lin(n=760) == -3
+    assert lin(k=2176) == -3  # k <= 2048
+    assert lin(w=fake + 8) == -5
     mla_out = lambda **kw: lib.parrot_mla_decode_out_bf16(*[kw.get(k, v) for k, v in (
         ("ctx", fake), ("tokens", 2), ("width", 1024), ("wo", fake), ("dim", 768),
         ("addend", null), ("out", fake), ("stream", null))])

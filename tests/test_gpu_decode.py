@@ -163,6 +163,30 @@ def test_decode_graph_matches_eager():
                                        getattr(theirs, name)[:, :, :48])
 
 
+@pytest.mark.parametrize("tokens,k,n,with_addend", [(1, 768, 768, True), (3, 768, 768, False),
+                                                    (16, 1024, 16, True), (8, 128, 2048, True)])
+def test_decode_linear(tokens, k, n, with_addend):
+    """The decode GEMV + addend against fp32 CPU products of the same bf16
+    operands: one bf16 rounding of an fp32 sum (order aside), then the bf16
+    addend sum."""
+    from parrot import hip_moe
+    _say(f"decode linear T={tokens} k={k} n={n} addend={with_addend}")
+    g = torch.Generator().manual_seed(700 + tokens + n)
+    x = torch.randn(tokens, 1, k, generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) * k ** -0.5).bfloat16()
+    addend = torch.randn(tokens, 1, n, generator=g).bfloat16() if with_addend else None
+    with torch.no_grad():
+        out = hip_moe.decode_linear(x.cuda(), w.cuda(), None if addend is None else addend.cuda())
+    assert out.shape == (tokens, 1, n) and out.dtype == torch.bfloat16
+    res = x.float() @ w.float().T
+    if addend is None:
+        ref, tol = res, 2 ** -7 * res.abs() + 1e-6
+    else:
+        ref = addend.float() + res.bfloat16().float()
+        tol = 2 ** -7 * (addend.float().abs() + 2 * res.abs()) + 1e-6
+    assert ((out.cpu().float() - ref).abs() <= tol).all()
+
+
 @pytest.mark.parametrize("tokens,sources", [(1, 2), (5, 9), (16, 4)])
 def test_mla_decode_in_mixes_its_input(tokens, sources):
     """The MLA decode projections from a depth mix equal depth_mix_norm
