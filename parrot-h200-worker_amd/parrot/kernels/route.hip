@@ -148,9 +148,11 @@ __global__ __launch_bounds__(256) void route_kernel(
 }
 
 // Long inputs: one workgroup routes 4 route blocks (64 tokens); wavefront w
-// computes the logits of route block 4 blockIdx.x + w over the full K, 8
-// k steps of loads in flight at a time.  Same block-local ranks and
-// histograms as route_kernel, so the group step is shared.
+// computes the logits of route block 4 blockIdx.x + w over the full K, STEPS
+// k steps of loads in flight at a time (TWO: a second 16-expert column tile,
+// for E > 16).  Same block-local ranks and histograms as route_kernel, so the
+// group step is shared.
+template <bool TWO, int STEPS>
 __global__ __launch_bounds__(256) void route_wide_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const float* __restrict__ bias, int64_t tokens, int dim, int experts,
@@ -172,24 +174,24 @@ __global__ __launch_bounds__(256) void route_wide_kernel(
     const uint16_t* pa = x + row * dim + koff;
     const uint16_t* pb0 = wr + static_cast<int64_t>(e0) * dim + koff;
     const uint16_t* pb1 = wr + static_cast<int64_t>(e1) * dim + koff;
-    const bool two = experts > 16;
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc1 = {0.f, 0.f, 0.f, 0.f};
     const int steps = dim / 32;
-    for (int c0 = 0; c0 < steps; c0 += kStepsPerChunk) {
-      bf16x8 a[kStepsPerChunk], b0[kStepsPerChunk], b1[kStepsPerChunk];
+    for (int c0 = 0; c0 < steps; c0 += STEPS) {
+      bf16x8 a[STEPS], b0[STEPS], b1[STEPS];
 #pragma unroll
-      for (int i = 0; i < kStepsPerChunk; ++i) {
+      for (int i = 0; i < STEPS; ++i) {
         const int st = min(c0 + i, steps - 1);  // unconditional loads, clamped
         a[i] = load_bf16x8(pa + st * 32);
         b0[i] = load_bf16x8(pb0 + st * 32);
-        b1[i] = load_bf16x8(pb1 + st * 32);
+        if constexpr (TWO) b1[i] = load_bf16x8(pb1 + st * 32);
       }
 #pragma unroll
-      for (int i = 0; i < kStepsPerChunk; ++i) {
+      for (int i = 0; i < STEPS; ++i) {
         if (c0 + i < steps) {
           acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b0[i], acc0, 0, 0, 0);
-          if (two) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b1[i], acc1, 0, 0, 0);
+          if constexpr (TWO)
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b1[i], acc1, 0, 0, 0);
         }
       }
     }
@@ -396,7 +398,7 @@ __global__ __launch_bounds__(256) void group_kernel(
 
 // The wide (64-token) route kernel takes over once its workgroups alone
 // cover every CU; below that the split-K kernel's shorter chain wins.
-constexpr int64_t kWideRouteTokens = 16384;
+constexpr int64_t kWideRouteTokens = 32768;  // the two shapes tie at 32K tokens
 
 hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
                         const float* given_logits, const float* bias,
@@ -410,9 +412,9 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
                                            out_logits, probs, weights, indices, positions,
                                            block_counts);
   } else if (tokens >= kWideRouteTokens) {
-    route_wide_kernel<<<(nrb + 3) / 4, 256, 0, s>>>(x, router_w, bias, tokens, dim, experts,
-                                                    out_logits, probs, weights, indices,
-                                                    positions, block_counts, nrb);
+    auto* kernel = experts > 16 ? route_wide_kernel<true, 8> : route_wide_kernel<false, 12>;
+    kernel<<<(nrb + 3) / 4, 256, 0, s>>>(x, router_w, bias, tokens, dim, experts, out_logits,
+                                         probs, weights, indices, positions, block_counts, nrb);
   } else {
     route_kernel<false><<<nrb, 256, 0, s>>>(x, router_w, given_logits, bias, tokens, dim,
                                             experts, out_logits, probs, weights, indices,
