@@ -236,18 +236,20 @@ __global__ __launch_bounds__(64) void rank_indices_kernel(
 
 // Adds rows lo + g, lo + g + n_groups, ... below `hi` of column e of the
 // int32 table [rows, experts] to `all`, and those below `split` also to
-// `below`; four independent loads per round trip (g = this thread's lane
-// group).
+// `below`; kColumnLoads independent loads per round trip (g = this thread's
+// lane group), clamped to row hi - 1 past the end.
+constexpr int kColumnLoads = 16;
+
 __device__ __forceinline__ void sum_column(const int32_t* table, int experts, int e, int g,
                                            int n_groups, int lo, int hi, int split, int& below,
                                            int& all) {
-  for (int i0 = lo + g; i0 < hi; i0 += 4 * n_groups) {
-    int v[4];
+  for (int i0 = lo + g; i0 < hi; i0 += kColumnLoads * n_groups) {
+    int v[kColumnLoads];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < kColumnLoads; ++k)
       v[k] = table[static_cast<int64_t>(min(i0 + k * n_groups, hi - 1)) * experts + e];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kColumnLoads; ++k) {
       const int i = i0 + k * n_groups;
       if (i < hi) {
         all += v[k];
