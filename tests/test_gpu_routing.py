@@ -57,7 +57,8 @@ def test_route_from_logits_bit_exact(tokens, experts, skewed):
 
 @pytest.mark.parametrize("tokens,experts,skewed", [(256, 32, False), (4096, 32, True),
                                                    (512, 16, False), (5, 16, False),
-                                                   (16421, 16, False), (20000, 32, True)])
+                                                   (16421, 16, False), (20000, 32, True),
+                                                   (32800, 16, False), (40000, 32, True)])
 def test_route_projection(tokens, experts, skewed):
     """HIP logits ~ fp32 logits; HIP top-2 == oracle top-2 of the HIP logits."""
     from parrot import hip_moe
