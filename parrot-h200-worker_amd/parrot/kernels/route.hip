@@ -150,10 +150,9 @@ __global__ __launch_bounds__(256) void route_kernel(
 // Long inputs: one workgroup routes 4 route blocks (64 tokens); wavefront w
 // computes the logits of route block 4 blockIdx.x + w over the full K, STEPS
 // k steps of loads in flight at a time (TWO: a second 16-expert column tile,
-// for E > 16).  With TWO, the router weights (32 rows, rows past E repeating
-// row E - 1 as the clamped global reads do) are first staged in LDS with a
-// row stride of dim + 8 elements, so the k-step loads that go to memory are
-// the token rows alone.  Same block-local ranks and histograms as
+// for E > 16).  The router weights (16 or 32 rows, rows past E repeating row
+// E - 1) are first staged in LDS with a row stride of dim + 8 elements, so
+// the k-step loads that go to memory are the token rows alone.  Same block-local ranks and histograms as
 // route_kernel, so the group step is shared.
 template <bool TWO, int STEPS>
 __global__ __launch_bounds__(256) void route_wide_kernel(
@@ -165,21 +164,19 @@ __global__ __launch_bounds__(256) void route_wide_kernel(
   constexpr int kTokens = 4 * kRouteTokensPerBlock;
   __shared__ float logit_s[kTokens][kMaxExperts + 1];
   __shared__ int ids_s[4 * kRouteAssignPerBlock];
-  extern __shared__ __attribute__((aligned(16))) uint16_t wr_s[];  // TWO: [32][dim + 8]
+  extern __shared__ __attribute__((aligned(16))) uint16_t wr_s[];  // [16 or 32][dim + 8]
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTokens;
   {
     const int64_t r = t0 + wave * 16 + (lane & 15);
     const int64_t row = r < tokens ? r : tokens - 1;
-    const int e0 = min(lane & 15, experts - 1);
     const int koff = (lane >> 4) * 8;
     const uint16_t* pa = x + row * dim + koff;
-    const uint16_t* pb0 = wr + static_cast<int64_t>(e0) * dim + koff;
-    if constexpr (TWO) {
+    {
       const int rs = dim + 8;  // LDS row stride, elements
       const int cpr = dim / 8;  // 16-byte chunks per row
-      for (int i = threadIdx.x; i < 32 * cpr; i += 256) {
+      for (int i = threadIdx.x; i < (TWO ? 32 : 16) * cpr; i += 256) {
         const int r = i / cpr;
         const int c = i - r * cpr;
         *reinterpret_cast<uint4*>(wr_s + r * rs + c * 8) = *reinterpret_cast<const uint4*>(
@@ -198,12 +195,8 @@ __global__ __launch_bounds__(256) void route_wide_kernel(
       for (int i = 0; i < STEPS; ++i) {
         const int st = min(c0 + i, steps - 1);  // unconditional loads, clamped
         a[i] = load_bf16x8(pa + st * 32);
-        if constexpr (TWO) {
-          b0[i] = load_bf16x8(lb0 + st * 32);
-          b1[i] = load_bf16x8(lb1 + st * 32);
-        } else {
-          b0[i] = load_bf16x8(pb0 + st * 32);
-        }
+        b0[i] = load_bf16x8(lb0 + st * 32);
+        if constexpr (TWO) b1[i] = load_bf16x8(lb1 + st * 32);
       }
 #pragma unroll
       for (int i = 0; i < STEPS; ++i) {
@@ -420,7 +413,7 @@ __global__ __launch_bounds__(256) void group_kernel(
 // The wide (64-token) route kernel takes over once its workgroups alone
 // cover every CU; below that the split-K kernel's shorter chain wins.
 constexpr int64_t kWideRouteTokens = 32768;  // the two shapes tie at 32K tokens
-constexpr int kWideRouteLdsBytes = 65536;     // staged router weights, E > 16
+constexpr int kWideRouteLdsBytes = 65536;     // the wide kernel's staged router weights
 
 hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
                         const float* given_logits, const float* bias,
@@ -434,10 +427,10 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
                                            out_logits, probs, weights, indices, positions,
                                            block_counts);
   } else if (tokens >= kWideRouteTokens &&
-             (experts <= 16 || 32 * (dim + 8) * 2 <= kWideRouteLdsBytes)) {
+             (experts > 16 ? 32 : 16) * (dim + 8) * 2 <= kWideRouteLdsBytes) {
     const bool two = experts > 16;
     auto* kernel = two ? route_wide_kernel<true, 8> : route_wide_kernel<false, 12>;
-    const size_t lds = two ? static_cast<size_t>(32) * (dim + 8) * 2 : 0;
+    const size_t lds = static_cast<size_t>(two ? 32 : 16) * (dim + 8) * 2;
     kernel<<<(nrb + 3) / 4, 256, lds, s>>>(x, router_w, bias, tokens, dim, experts, out_logits,
                                            probs, weights, indices, positions, block_counts, nrb);
   } else {
