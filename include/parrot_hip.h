@@ -73,11 +73,10 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
 /* parrot_depth_mix_bf16 (out_norm required) followed by the router of
  * parrot_route_bf16 on the normalised rows, in one launch: writes
  * out_weights fp32 [T, 2] and out_indices int64 [T, 2] exactly as
- * parrot_route_bf16 does for x = out_norm below 16384 tokens (the same
- * split-K logit arithmetic to the bit, the same top-2 and renormalised
- * weights; from 16384 tokens parrot_route_bf16 sums each logit in one chain,
- * so its logits may differ in the last bits).  No grouping outputs, no
- * router stats.
+ * parrot_route_bf16 does for x = out_norm, at every token count (the same
+ * logit arithmetic to the bit: four k-step chains by st % 4 summed in a
+ * fixed order, the same top-2 and renormalised weights).  No grouping
+ * outputs, no router stats.
  * router_weight bf16 [E, dim], 16-byte aligned; logit_bias optional fp32 [E];
  * 2 <= E <= 32; dim % 32 == 0, dim <= 2048.
  * Replaces, for a MoE layer's input, metal_depth_mix_norm

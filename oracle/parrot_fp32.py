@@ -20,13 +20,22 @@ import numpy as np
 import torch
 from torch.nn import functional as F
 
-from . import layers
+from . import layers, routing
 
 
 class ParrotFP32:
-    def __init__(self, cfg, state_dict: dict[str, torch.Tensor]):
+    """``forced_routing``: optional list of int64 [tokens, 2] top-2 index
+    arrays, consumed one per MoE call in execution order; a MoE layer then
+    uses those experts (weights renormalised over its own fp32 softmax at
+    those indices, as the reference's top-2 weights are, model.py:525-527)
+    instead of its own top-2.  Feeding the indices another implementation
+    chose separates the discontinuity of top-2 selection at near-tied router
+    logits from the arithmetic precision of everything else."""
+
+    def __init__(self, cfg, state_dict: dict[str, torch.Tensor], forced_routing=None):
         self.c = cfg
         self.p = {k: v.detach().float().cpu() for k, v in state_dict.items()}
+        self.forced_routing = None if forced_routing is None else list(forced_routing)
 
     # ---- building blocks ------------------------------------------------------
 
@@ -90,8 +99,16 @@ class ParrotFP32:
                     self._w(f"{pre}experts.{e}.down.weight")) for e in range(self.c.n_experts)]
         shared = (self._w(pre + "shared.gate.weight"), self._w(pre + "shared.up.weight"),
                   self._w(pre + "shared.down.weight"))
+        indices = weights = None
+        if self.forced_routing is not None:
+            indices = np.ascontiguousarray(self.forced_routing.pop(0), dtype=np.int64).reshape(-1, 2)
+            logits = layers.router_logits(h.reshape(-1, h.shape[-1]), self._w(pre + "router.weight"))
+            bias = None if logit_bias is None else np.asarray(logit_bias, dtype=np.float32)
+            _, _, probs = routing.top2(logits.numpy(), bias, want_probs=True)
+            p = np.take_along_axis(probs, indices, axis=1)
+            weights = p / (p[:, :1] + p[:, 1:])
         out, idx, w, logits = layers.moe_layer(h, self._w(pre + "router.weight"), experts, shared,
-                                               logit_bias)
+                                               logit_bias, indices, weights)
         return out.view_as(h), idx, w, logits
 
     def _norm(self, name: str, x):
@@ -158,7 +175,7 @@ class ParrotFP32:
 
         return self.head(self._run(x, attention, capture))
 
-    def prefill(self, ids: torch.Tensor):
+    def prefill(self, ids: torch.Tensor, capture: dict | None = None):
         """(logits of the last position [b, 1, V], cache state)."""
         c = self.c
         b, t = ids.shape
@@ -179,10 +196,11 @@ class ParrotFP32:
                 state["layers"].append(("local", kc, vc))
             return out
 
-        x = self._run(self._w("embedding.weight")[ids], attention)
+        x = self._run(self._w("embedding.weight")[ids], attention, capture)
         return self.head(x[:, -1:]), state
 
-    def decode_step(self, ids: torch.Tensor, state: dict) -> torch.Tensor:
+    def decode_step(self, ids: torch.Tensor, state: dict,
+                    capture: dict | None = None) -> torch.Tensor:
         """Logits [b, 1, V] for one new token per sequence; updates state."""
         c = self.c
         b = ids.shape[0]
@@ -214,7 +232,7 @@ class ParrotFP32:
                 y = self._attend(q, k, v, allowed, 1.0 / math.sqrt(c.head_dim))
             return F.linear(y.transpose(1, 2).reshape(b, 1, -1), self._w(pre + "out.weight"))
 
-        x = self._run(self._w("embedding.weight")[ids], attention)
+        x = self._run(self._w("embedding.weight")[ids], attention, capture)
         state["position"] = p + 1
         return self.head(x)
 

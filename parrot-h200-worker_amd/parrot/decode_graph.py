@@ -24,10 +24,11 @@ class DecodeGraph:
     ``[batch, 1, vocab]`` with ``logits=True``), exactly as
     ``model.decode_next`` / ``model.decode_step`` would on the same state.
     The returned tensor is the graph's static output, overwritten by the next
-    step.  The state must stay with this object: eager decode steps on it in
+    step.  Both run in inference mode, as ``prefill`` / ``decode_step`` do.  The state must stay with this object: eager decode steps on it in
     between are allowed (they advance both positions consistently).
     """
 
+    @torch.inference_mode()
     def __init__(self, model: Parrot, state: GenerationState, logits: bool = False):
         if state.position_device is None:
             raise RuntimeError("DecodeGraph needs a generation state from a HIP-backend prefill")
@@ -61,6 +62,7 @@ class DecodeGraph:
         self.state.position = position
         self.state.position_device.fill_(position)
 
+    @torch.inference_mode()
     def step(self, input_ids: Tensor) -> Tensor:
         if input_ids.shape != self.ids.shape:
             raise ValueError("decode input must be [cached batch, 1]")

@@ -47,17 +47,31 @@ def _require(x: Tensor, what: str, dtypes=(torch.bfloat16,)) -> None:
         raise RuntimeError(f"{what} is inference-only; disable gradients")
 
 
+def _capturing() -> bool:
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
 def _scratch(owner, name: str, nbytes: int, device: torch.device) -> Tensor:
     """Reusable byte workspace kept outside the module's state_dict
-    (cf. parrot/metal_moe.py:15-23).  A buffer that is outgrown stays
-    referenced (never freed): a HIP graph captured earlier may still read
-    and write it on replay."""
+    (cf. parrot/metal_moe.py:15-23), grown to the next power of two.
+
+    An outgrown buffer is dropped, unless a HIP graph capture used it: the
+    captured graph reads and writes it on every replay, so it stays
+    referenced (in ``_hip_captured_scratch``) for as long as the owner
+    lives.  Retention is therefore bounded by the captures, not by the
+    sizes seen."""
     cached = owner.__dict__.get(name)
     if cached is None or cached.numel() < nbytes or cached.device != device:
-        if cached is not None:
-            owner.__dict__.setdefault("_hip_retired_scratch", []).append(cached)
-        cached = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        if cached is not None and owner.__dict__.get(name + "_captured", False):
+            owner.__dict__.setdefault("_hip_captured_scratch", []).append(cached)
+        size = 256
+        while size < nbytes:
+            size *= 2
+        cached = torch.empty(size, dtype=torch.uint8, device=device)
         owner.__dict__[name] = cached
+        owner.__dict__[name + "_captured"] = False
+    if _capturing():
+        owner.__dict__[name + "_captured"] = True
     return cached
 
 
@@ -438,6 +452,19 @@ def decode_experts(module: "MoE", flat: Tensor | None, addend: Tensor | None = N
         "parrot_depth_mix_decode_moe_bf16")
     del keep  # alive until the launch is enqueued (it is)
     return out, indices, weights
+
+
+def vocab_logits(h: Tensor, weight: Tensor) -> Tensor:
+    """fp32 logits ``h @ weight^T`` for bf16 rows h [..., dim] and the tied
+    head weight [vocab, dim] (cf. the head F.linear, parrot/model.py:714-715):
+    the products of the bf16 operands accumulate in fp32 and the result is
+    written in fp32 (one library GEMM with an fp32 output type)."""
+    _require(h, "HIP vocabulary head")
+    if weight.dtype != h.dtype or weight.ndim != 2 or weight.shape[1] != h.shape[-1]:
+        raise RuntimeError("head weight must be a [vocab, dim] tensor of h's dtype")
+    flat = h.reshape(-1, h.shape[-1])
+    out = torch.mm(flat, weight.t(), out_dtype=torch.float32)
+    return out.view(*h.shape[:-1], weight.shape[0])
 
 
 def vocab_argmax(h: Tensor, weight: Tensor) -> Tensor:
@@ -1040,8 +1067,8 @@ def depth_mix_norm(module, sources: list[Tensor], output_norm) -> Tensor:
 def depth_mix_norm_route(module, sources: list[Tensor], output_norm, moe: "MoE",
                          logit_bias: Tensor | None = None) -> tuple[Tensor, RouteResult]:
     """``depth_mix_norm`` of a MoE layer's input plus that layer's router
-    top-2 on the result, in one kernel: below 16384 tokens the weights and
-    indices equal ``route(moe, result)``'s bit for bit (no grouping, no
+    top-2 on the result, in one kernel: at every token count the weights
+    and indices equal ``route(moe, result)``'s bit for bit (no grouping, no
     router stats)."""
     if moe.cfg.top_k != 2 or moe.cfg.n_experts > MAX_EXPERTS:
         raise RuntimeError(f"HIP routing supports top-2 of at most {MAX_EXPERTS} experts")

@@ -148,7 +148,8 @@ __global__ __launch_bounds__(256) void route_kernel(
 }
 
 // Long inputs: one workgroup routes 4 route blocks (64 tokens); wavefront w
-// computes the logits of route block 4 blockIdx.x + w over the full K, STEPS
+// computes the logits of route block 4 blockIdx.x + w over the full K
+// (bit-identical to route_kernel's split-K sum), STEPS
 // k steps of loads in flight at a time (TWO: a second 16-expert column tile,
 // for E > 16).  The router weights (16 or 32 rows, rows past E repeating row
 // E - 1) are first staged in LDS with a row stride of dim + 8 elements, so
@@ -186,8 +187,17 @@ __global__ __launch_bounds__(256) void route_wide_kernel(
     }
     const uint16_t* lb0 = wr_s + (lane & 15) * (dim + 8) + koff;
     const uint16_t* lb1 = wr_s + (16 + (lane & 15)) * (dim + 8) + koff;
-    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f};
-    f32x4 acc1 = {0.f, 0.f, 0.f, 0.f};
+    // One accumulator chain per k-step residue st % 4, summed as
+    // ((c0 + c1) + c2) + c3: the exact arithmetic of route_kernel, whose
+    // wavefront w accumulates the steps st = w (mod 4) in ascending order, so
+    // a token's logits (and its top-2) do not depend on the batch size.
+    static_assert(STEPS % 4 == 0, "a chunk must keep st % 4 == i % 4");
+    f32x4 acc0[4], acc1[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      acc0[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc1[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     const int steps = dim / 32;
     for (int c0 = 0; c0 < steps; c0 += STEPS) {
       bf16x8 a[STEPS], b0[STEPS], b1[STEPS];
@@ -201,16 +211,19 @@ __global__ __launch_bounds__(256) void route_wide_kernel(
 #pragma unroll
       for (int i = 0; i < STEPS; ++i) {
         if (c0 + i < steps) {
-          acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b0[i], acc0, 0, 0, 0);
+          acc0[i % 4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b0[i], acc0[i % 4], 0, 0, 0);
           if constexpr (TWO)
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b1[i], acc1, 0, 0, 0);
+            acc1[i % 4] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b1[i], acc1[i % 4], 0, 0, 0);
         }
       }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      logit_s[wave * 16 + 4 * (lane >> 4) + r][lane & 15] = acc0[r];
-      logit_s[wave * 16 + 4 * (lane >> 4) + r][16 + (lane & 15)] = acc1[r];
+      logit_s[wave * 16 + 4 * (lane >> 4) + r][lane & 15] =
+          ((acc0[0][r] + acc0[1][r]) + acc0[2][r]) + acc0[3][r];
+      logit_s[wave * 16 + 4 * (lane >> 4) + r][16 + (lane & 15)] =
+          ((acc1[0][r] + acc1[1][r]) + acc1[2][r]) + acc1[3][r];
     }
   }
   __syncthreads();

@@ -810,6 +810,17 @@ class Parrot(nn.Module):
 
     # -- helpers -------------------------------------------------------------
 
+    def _head(self, normed: Tensor) -> Tensor:
+        """Tied vocabulary head (reference parrot/model.py:714-715).  On the
+        HIP backend the logits come out in fp32, never rounded to bf16: a
+        bf16 rounding of ~0.5-magnitude logits (ulp 2^-8) ties or swaps
+        near-equal top logits, the head's share of greedy-argmax
+        disagreement with the fp32 reference."""
+        if self.config.uses_hip and _hip_inference(normed):
+            from . import hip_moe
+            return hip_moe.vocab_logits(normed, self.embedding.weight)
+        return F.linear(normed, self.embedding.weight)
+
     def _mixed_input(self, stream: _AttnRes | None, x: Tensor, index: int,
                      norm: RMSNorm) -> Tensor:
         """Normalised input of module ``index``: RMSNorm of the depth mix
@@ -942,7 +953,7 @@ class Parrot(nn.Module):
                 x = self.depth_mix[-1](stream.sources())
             # Loss-only callers can skip the last position's projection exactly.
             normed = self.final_norm(x[:, :-1] if supervised_logits_only else x)
-        logits = F.linear(normed, self.embedding.weight)
+        logits = self._head(normed)
 
         if cfg.collect_router_stats:
             aux_loss = torch.stack(aux_losses).mean()
@@ -1027,9 +1038,9 @@ class Parrot(nn.Module):
             if stream is not None:
                 x = self.depth_mix[-1](stream.sources())
             normed = self.final_norm(x[:, -1:])
-        logits = F.linear(normed, self.embedding.weight)
+        logits = self._head(normed)
         position_device = None
-        if cfg.uses_hip and _hip_inference(logits):
+        if cfg.uses_hip and _hip_inference(normed):
             position_device = torch.full((1,), t, dtype=torch.int32, device=logits.device)
         return logits, GenerationState(caches, t, b, position_device)
 
@@ -1088,7 +1099,7 @@ class Parrot(nn.Module):
             from . import hip_moe
             output = hip_moe.vocab_argmax(h, self.embedding.weight)
         else:
-            logits = F.linear(h, self.embedding.weight)
+            logits = self._head(h)
             output = logits.argmax(-1) if _next_token_only else logits
         state.position += 1
         if state.position_device is not None:

@@ -1,21 +1,39 @@
-"""GPU parity of the full model on the HIP backend against the fp32 oracle.
+"""GPU parity of the full model on the HIP backend against the fp32 oracle
+(4 and 5) and against the reference's own fixtures.
 
-Same seeded weights: the HIP model runs in bf16 on the GPU; the functional
-fp32 oracle (oracle/parrot_fp32.py) runs on CPU with those bf16 weights
-upcast.  Reported: logits max/mean abs error and argmax agreement.
+The HIP model runs in bf16 on the GPU.  The functional fp32 oracle
+(oracle/parrot_fp32.py) runs on CPU with the same bf16 weights upcast.  The
+rule is the one tests/parity.py states:
+  * vs the oracle forced to the HIP top-2 choices: tight logits bounds, and
+    argmax agreement on every position with a fp32 gap above MARGIN_FORCED;
+  * every HIP top-2 choice equals the forced oracle's fp32 top-2, except at
+    router near-ties (ROUTER_TIE);
+  * vs the free oracle: argmax agreement on every position with a fp32 gap
+    above MARGIN_FREE, plus a raw agreement floor.
+
+Measured on MI355X (C4 seed 2; C5 b = 1..8 seed 3), which sets the constants:
+  * free routing: the fp32 top-1/top-2 gap moves by at most 0.21 (C4) and
+    0.17 (C5); raw argmax agreement 0.953 (C4) and 1.0 (C5);
+  * forced routing: the gap moves by at most 0.014, logits max-abs <= 0.020,
+    mean-abs <= 2.8e-3, raw argmax 0.982 (C4) and 1.0 (C5);
+  * the largest fp32 router margin at a HIP top-2 difference is 0.0114
+    (84 of 8192 token-layers differ at C4, 200 of 18432 at C5 b = 8);
+  * no exact fp32 router ties occur (tests/test_oracle_golden.py).
 """
 import numpy as np
 import pytest
 import torch
 
 from conftest import tiny_model_config
-from oracle import parrot_fp32
+from oracle import parrot_fp32, routing
+from parity import RouteRecorder, format_report, logits_report, routing_report, say
 
 pytestmark = pytest.mark.gpu
 
-
-def _say(msg):
-    print(msg, flush=True)
+MARGIN_FREE = 0.25      # fp32 logit gap above which argmax must agree, free routing
+MARGIN_FORCED = 0.03    # the same with the oracle following the HIP top-2
+ROUTER_TIE = 0.02       # fp32 router-logit margin below which a top-2 choice may differ
+FORCED_MAX_ABS, FORCED_MEAN_ABS = 0.03, 3.5e-3   # logits vs the forced oracle (default model)
 
 
 def _hip_model(cfg, seed):
@@ -24,95 +42,206 @@ def _hip_model(cfg, seed):
     return Parrot(cfg).to(device="cuda", dtype=torch.bfloat16).eval()
 
 
-def _oracle(model):
-    return parrot_fp32.ParrotFP32(model.config, model.state_dict())
+def _oracle(model, forced=None):
+    return parrot_fp32.ParrotFP32(model.config, model.state_dict(), forced_routing=forced)
 
 
-def _compare(got, ref, min_agree):
-    got = got.float().cpu().reshape(-1, got.shape[-1])
-    ref = ref.float().cpu().reshape(-1, ref.shape[-1])
-    agree = (got.argmax(-1) == ref.argmax(-1)).float().mean().item()
-    d = (got - ref).abs()
-    _say(f"  logits max-abs {d.max():.3e} mean-abs {d.mean():.3e} argmax agree {agree:.4f}")
-    assert agree >= min_agree
-    return agree
+def _check(got, ref_forced, ref_free, route_rep, *, max_abs, mean_abs, forced_floor,
+           free_floor):
+    """Both comparisons are printed before anything is asserted."""
+    f = logits_report(got, ref_forced, MARGIN_FORCED)
+    say(f"  vs forced oracle: {format_report(f)}")
+    say(f"  routing: {route_rep['flips']} top-2 set differences and {route_rep['swaps']} order "
+        f"swaps in {route_rep['tokens']} token-layers; largest fp32 margin at one "
+        f"{route_rep['worst_margin']:.4f}")
+    r = logits_report(got, ref_free, MARGIN_FREE)
+    say(f"  vs free oracle:   {format_report(r)}")
+    assert route_rep["worst_margin"] < ROUTER_TIE
+    assert f["clear_miss"] == 0
+    assert f["agree"] >= forced_floor
+    assert f["max_abs"] <= max_abs and f["mean_abs"] <= mean_abs
+    assert r["clear_agree"] >= 0.999
+    assert r["agree"] >= free_floor
 
 
-def test_tiny_forward():
-    _say("tiny forward (grouped_hip + hip)")
+# ---------------------------------------------------------------------------
+# BASELINE config 1: the tiny model, batch 1 x 64, against the reference's
+# own fixture (tests/golden/tiny_forward.npz) and the oracle
+# ---------------------------------------------------------------------------
+
+def test_tiny_golden_router_logits_route_exactly(golden):
+    """The reference's per-layer router logits through the HIP top-2 give the
+    reference's top-2 indices and weights (no exact ties in the fixture)."""
+    from parrot import hip_moe
+    g = golden("tiny_forward")
+    for layer in range(g["router_logits"].shape[0]):
+        logits = torch.from_numpy(g["router_logits"][layer]).cuda()
+        res = hip_moe.route_from_logits(logits)
+        np.testing.assert_array_equal(res.indices.cpu().numpy(), g["top2_indices"][layer])
+        np.testing.assert_allclose(res.weights.cpu().numpy(), g["top2_weights"][layer],
+                                   atol=1e-6, rtol=0)
+
+
+def test_tiny_forward_vs_reference_fixture(golden, monkeypatch):
+    """C1: the HIP tiny model (seed 0, bf16 weights) on the fixture's ids.
+    Per-layer top-2 equals the reference's wherever the reference's fp32
+    router margin is clear; logits argmax equals the reference's wherever its
+    top-1/top-2 gap is clear; logits are then checked against the oracle on
+    the same bf16 weights."""
+    g = golden("tiny_forward")
+    say("tiny forward 1x64 vs the reference fixture")
     model = _hip_model(tiny_model_config(moe_backend="grouped_hip", depth_backend="hip",
                                          collect_router_stats=False), 0)
-    ids = torch.randint(0, 32768, (2, 64), generator=torch.Generator().manual_seed(0))
+    ids = torch.from_numpy(g["ids"])
+    rec = RouteRecorder(monkeypatch)
     with torch.no_grad():
         got = model(ids.cuda()).logits
-        ref = _oracle(model).forward(ids)
-    _compare(got, ref, 0.95)
+    hip_idx = rec.take()
+    assert len(hip_idx) == g["top2_indices"].shape[0]
+    # Routing vs the reference: the fixture holds the fp32-weight model, so a
+    # choice may differ only where the reference's own margin is small.
+    rep = routing_report(hip_idx, [torch.from_numpy(x) for x in g["router_logits"]])
+    say(f"  routing vs reference: {rep}")
+    assert rep["worst_margin"] < ROUTER_TIE
+    # Logits argmax vs the reference on clear gaps (top-8 of the fixture).
+    top8 = g["logits_top8_values"]
+    gap = top8[:, 0] - top8[:, 1]
+    hip_arg = got.float().cpu()[0].argmax(-1).numpy()
+    clear = gap > MARGIN_FREE / 4  # the tiny model's logits are ~3.5x smaller (dim 64)
+    say(f"  argmax vs reference: {np.mean(hip_arg == g['logits_argmax']):.4f}, on "
+        f"{clear.sum()} clear gaps {np.mean(hip_arg[clear] == g['logits_argmax'][clear]):.4f}")
+    assert np.array_equal(hip_arg[clear], g["logits_argmax"][clear])
+    sl = got.float().cpu()[0, :, :g["logits_slice"].shape[1]].numpy()
+    say(f"  logits slice vs reference: max-abs {np.abs(sl - g['logits_slice']).max():.3e}")
+    # Against the oracle on the same bf16 weights.
+    ref = _oracle(model).forward(ids)
+    forced_capture = {}
+    ref_forced = _oracle(model, forced=hip_idx).forward(ids, forced_capture)
+    _check(got, ref_forced, ref, routing_report(hip_idx, forced_capture["logits"]),
+           max_abs=0.01, mean_abs=1e-3, forced_floor=0.98, free_floor=0.95)
 
 
-def test_tiny_router_stats():
-    _say("tiny forward with router stats")
+def test_tiny_router_stats_vs_oracle(golden, monkeypatch):
+    """A13: expert_utilization and aux_loss of a grouped_hip forward with
+    router statistics on (reference parrot/model.py:552-569) equal the fp32
+    statistics of the HIP layers' own router inputs: utilization exactly
+    (counts / 2T from the same top-2), aux_loss within 1e-5."""
+    say("tiny forward with router stats vs the oracle")
+    g = golden("tiny_forward")
     model = _hip_model(tiny_model_config(moe_backend="grouped_hip", depth_backend="hip"), 0)
-    ids = torch.randint(0, 32768, (1, 64), generator=torch.Generator().manual_seed(1))
+    inputs = []
+    for block in model.blocks:
+        block.moe.register_forward_pre_hook(lambda mod, args: inputs.append(args[0].detach().clone()))
+    ids = torch.from_numpy(g["ids"]).cuda()
     with torch.no_grad():
-        out = model(ids.cuda())
-    util = out.expert_utilization.cpu()
-    torch.testing.assert_close(util.sum(-1), torch.ones(4))
-    assert torch.isfinite(out.aux_loss).item()
+        out = model(ids)
+    cfg = model.config
+    util_ref, aux_ref = [], []
+    for block, h in zip(model.blocks, inputs):
+        flat = h.float().cpu().reshape(-1, cfg.dim)
+        logits = flat @ block.moe.router.weight.detach().float().cpu().T
+        idx, _, probs = routing.top2(logits.numpy(), want_probs=True)
+        counts = np.bincount(idx.reshape(-1), minlength=cfg.n_experts).astype(np.float32)
+        util = counts / idx.size
+        util_ref.append(util)
+        aux_ref.append(cfg.n_experts * float((util * probs.mean(0)).sum()))
+    util_ref = np.stack(util_ref)
+    got_util = out.expert_utilization.float().cpu().numpy()
+    say(f"  utilization max diff {np.abs(got_util - util_ref).max():.2e}; aux_loss "
+        f"{out.aux_loss.item():.6f} vs {np.mean(aux_ref):.6f}")
+    np.testing.assert_array_equal(got_util, util_ref)
+    assert abs(out.aux_loss.item() - float(np.mean(aux_ref))) < 1e-5
+    # The reference's own statistics (fp32 weights) are close.
+    ref_stats = golden("tiny_forward_stats")
+    say(f"  vs the reference fixture: utilization max diff "
+        f"{np.abs(got_util - ref_stats['expert_utilization']).max():.4f}, aux_loss "
+        f"{out.aux_loss.item():.6f} vs {float(ref_stats['aux_loss']):.6f}")
+    assert abs(out.aux_loss.item() - float(ref_stats["aux_loss"])) < 5e-3
 
 
-def test_default_forward_512():
-    """default model (E=16), seed 2, batch 1 x 512.
+# ---------------------------------------------------------------------------
+# BASELINE config 4: default model, seed 2, batch 1 x 512
+# ---------------------------------------------------------------------------
 
-    The HIP path must agree with the fp32 oracle at least as well as the
-    plain PyTorch bf16 execution of the same model and weights (the
-    reference's pytorch backend in bf16), which bounds what bf16 can reach
-    on this random-init model: ~14% of positions have an fp32 top-1/top-2
-    logit gap below 0.02, while 16 layers of bf16 activations move the
-    logits by ~0.013 on average."""
-    from parrot import ModelConfig, Parrot
-    _say("default forward 1x512 (seed 2)")
+def test_default_forward_512(monkeypatch):
+    from parrot import ModelConfig
+    say("default forward 1x512 (seed 2)")
     model = _hip_model(ModelConfig(moe_backend="grouped_hip", depth_backend="hip",
                                    collect_router_stats=False), 2)
-    control = Parrot(ModelConfig(collect_router_stats=False))
-    control.load_state_dict(model.state_dict())
-    control = control.to(device="cuda", dtype=torch.bfloat16).eval()
     ids = torch.randint(0, 32768, (1, 512), generator=torch.Generator().manual_seed(2))
+    rec = RouteRecorder(monkeypatch)
     with torch.no_grad():
         got = model(ids.cuda()).logits
-        base = control(ids.cuda()).logits
+    assert got.dtype == torch.float32
+    hip_idx = rec.take()
+    assert len(hip_idx) == model.config.n_layers
     ref = _oracle(model).forward(ids)
-    agree = _compare(got, ref, 0.9)
-    control_agree = _compare(base, ref, 0.9)
-    _say(f"  argmax agreement: HIP {agree:.4f}, PyTorch bf16 control {control_agree:.4f}")
-    assert agree >= control_agree - 0.01
-    d = (got.float().cpu() - ref.float()).abs()
-    assert d.mean() < 0.02
+    capture = {}
+    ref_forced = _oracle(model, forced=hip_idx).forward(ids, capture)
+    _check(got, ref_forced, ref, routing_report(hip_idx, capture["logits"]),
+           max_abs=FORCED_MAX_ABS, mean_abs=FORCED_MEAN_ABS, forced_floor=0.975, free_floor=0.94)
 
 
-def test_prefill_and_decode():
-    """BASELINE config 5 shape at reduced length: prefill then greedy decode."""
+# ---------------------------------------------------------------------------
+# BASELINE config 5: prefill 128, then 16 decode steps at b = 1, 2, 4, 8,
+# teacher-forced with the free oracle's greedy tokens; eager and graph replay
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
+def test_prefill_and_decode_16_steps(batch, monkeypatch):
     from parrot import ModelConfig
-    _say("prefill 128 + 4 decode steps, batch 2")
+    from parrot.decode_graph import DecodeGraph
+    steps = 16
+    say(f"prefill 128 + {steps} decode steps, batch {batch} (seed 3)")
     model = _hip_model(ModelConfig(moe_backend="grouped_hip", depth_backend="hip",
                                    collect_router_stats=False), 3)
+    prompt = torch.randint(0, 32768, (batch, 128), generator=torch.Generator().manual_seed(3))
+    # Free oracle: reference logits and the teacher tokens.
     oracle = _oracle(model)
-    prompt = torch.randint(0, 32768, (2, 128), generator=torch.Generator().manual_seed(3))
-    logits, state = model.prefill(prompt.cuda())
     ref_logits, ref_state = oracle.prefill(prompt)
-    _compare(logits, ref_logits, 0.5)
-    for step in range(4):
-        nxt = ref_logits[:, -1].argmax(-1, keepdim=True)  # feed identical tokens
-        logits, state = model.decode_step(nxt.cuda(), state)
-        ref_logits = oracle.decode_step(nxt, ref_state)
-        _compare(logits, ref_logits, 0.5)
-    assert state.position == 132
+    refs, tokens = [ref_logits], []
+    for _ in range(steps):
+        tokens.append(refs[-1][:, -1].argmax(-1, keepdim=True))
+        refs.append(oracle.decode_step(tokens[-1], ref_state))
+    # HIP, eager, recording every layer's top-2.
+    rec = RouteRecorder(monkeypatch)
+    logits, state = model.prefill(prompt.cuda())
+    got = [logits.float().cpu()]
+    for tok in tokens:
+        logits, state = model.decode_step(tok.cuda(), state)
+        got.append(logits.float().cpu())
+    assert state.position == 128 + steps
+    hip_idx = rec.stop()
+    assert len(hip_idx) == (steps + 1) * model.config.n_layers
+    # HIP, graph-replayed decode steps: identical to eager.
+    _, gstate = model.prefill(prompt.cuda())
+    graph = DecodeGraph(model, gstate, logits=True)
+    for k, tok in enumerate(tokens):
+        out = graph.step(tok.cuda())
+        assert torch.equal(out.float().cpu(), got[k + 1]), f"graph step {k} differs from eager"
+    # Oracle forced to the HIP top-2 choices.
+    forced = _oracle(model, forced=hip_idx)
+    capture = {}
+    f_logits, f_state = forced.prefill(prompt, capture)
+    forced_refs = [f_logits]
+    for tok in tokens:
+        forced_refs.append(forced.decode_step(tok, f_state, capture))
+    got_all = torch.cat([g.reshape(batch, -1) for g in got])
+    _check(got_all, torch.cat([r.reshape(batch, -1) for r in forced_refs]),
+           torch.cat([r.reshape(batch, -1) for r in refs]),
+           routing_report(hip_idx, capture["logits"]),
+           max_abs=FORCED_MAX_ABS, mean_abs=FORCED_MEAN_ABS, forced_floor=0.94, free_floor=0.94)
 
+
+# ---------------------------------------------------------------------------
+# execution-mode equivalences
+# ---------------------------------------------------------------------------
 
 def test_graph_replay_matches_eager():
     """The forward captured in a HIP graph replays identically (several
     replays, with eager work and synchronisation in between)."""
     from parrot import ModelConfig
-    _say("graph capture replay")
+    say("graph capture replay")
     model = _hip_model(ModelConfig(n_layers=4, moe_backend="grouped_hip", depth_backend="hip",
                                    collect_router_stats=False), 5)
     ids = torch.randint(0, 32768, (1, 512), generator=torch.Generator().manual_seed(5)).cuda()
@@ -142,7 +271,7 @@ def test_routing_in_depth_mix_matches_separate_launches(monkeypatch):
     model with separate route and grouping launches."""
     from parrot import ModelConfig
     from parrot.model import MoE
-    _say("routing in the depth mix vs separate launches")
+    say("routing in the depth mix vs separate launches")
     model = _hip_model(ModelConfig(n_layers=4, moe_backend="grouped_hip", depth_backend="hip",
                                    collect_router_stats=False), 6)
     ids = torch.randint(0, 32768, (2, 200), generator=torch.Generator().manual_seed(6)).cuda()

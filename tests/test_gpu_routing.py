@@ -113,3 +113,23 @@ def test_routing_is_deterministic():
     n = int(a.grouping.offsets[-1])  # valid prefix of the overflow list
     assert torch.equal(a.grouping.overflow[:n], b.grouping.overflow[:n])
     assert torch.equal(a.indices, b.indices) and torch.equal(a.weights, b.weights)
+
+
+@pytest.mark.parametrize("experts", [16, 32])
+def test_wide_route_matches_split_k_chunks(experts):
+    """From 32768 tokens the router runs one 64-token kernel whose logits
+    keep four k-step chains (st % 4) summed in route_kernel's order, so a
+    token's logits, top-2 and weights are the same bits as when its rows are
+    routed in chunks below 32768 tokens (split-K kernel): routing does not
+    depend on the batch size."""
+    from parrot import hip_moe
+    _say(f"wide route vs split-K chunks T=32800 E={experts}")
+    module = moe_module(experts, seed=7)
+    x = inputs(32800, seed=7)
+    with torch.no_grad():
+        wide = hip_moe.route(module, x, collect_stats=False, return_logits=True)
+        parts = [hip_moe.route(module, x[lo:lo + 16400], collect_stats=False, return_logits=True)
+                 for lo in (0, 16400)]
+    assert torch.equal(wide.logits, torch.cat([p.logits for p in parts]))
+    assert torch.equal(wide.indices, torch.cat([p.indices for p in parts]))
+    assert torch.equal(wide.weights, torch.cat([p.weights for p in parts]))

@@ -136,3 +136,26 @@ def test_packed_weight_fragment_order():
     gu = _interleave_gate_up(gate, up)
     assert torch.equal(gu[:16], gate[:16]) and torch.equal(gu[16:32], up[:16])
     assert torch.equal(gu[32:48], gate[16:]) and torch.equal(gu[48:], up[16:])
+
+
+def test_scratch_retention_is_bounded():
+    """Outgrown workspaces are dropped unless a graph capture used them, and
+    sizes grow geometrically, so a sweep of growing sizes keeps one buffer."""
+    from parrot import hip_moe
+
+    class Owner:
+        pass
+
+    owner = Owner()
+    sizes = []
+    for nbytes in range(1000, 200_000, 997):
+        buf = hip_moe._scratch(owner, "_ws", nbytes, torch.device("cpu"))
+        assert buf.numel() >= nbytes and buf.numel() & (buf.numel() - 1) == 0
+        sizes.append(buf.numel())
+    assert len(set(sizes)) == 9  # 1 KiB .. 256 KiB, powers of two
+    assert "_hip_captured_scratch" not in owner.__dict__
+    # A buffer a capture used survives its replacement.
+    owner.__dict__["_ws_captured"] = True
+    used = owner.__dict__["_ws"]
+    hip_moe._scratch(owner, "_ws", 10 * used.numel(), torch.device("cpu"))
+    assert owner.__dict__["_hip_captured_scratch"] == [used]

@@ -147,3 +147,71 @@ def test_topk_tie_order_is_documented_difference(golden):
     np.testing.assert_allclose(w, t["weights"], atol=1e-7)
     # The oracle's rule differs from torch.topk on these rows, by design.
     assert not np.array_equal(idx, ref_idx)
+
+
+def test_forced_routing_reproduces_free_run(oracle_model, tiny_cfg, tiny_model, golden):
+    """Pins the oracle's forced-routing mode: forcing a run's own top-2
+    choices reproduces that run bit for bit (weights renormalised over the
+    oracle's own softmax, as the free run does); the order of the two
+    experts does not matter; forcing a different expert changes that token's
+    output and, beyond fp32 reassociation, nothing on earlier positions."""
+    ids = torch.from_numpy(golden("tiny_forward")["ids"])
+    sd = tiny_model.state_dict()
+    capture = {}
+    with torch.no_grad():
+        free = oracle_model.forward(ids, capture)
+        own = [np.asarray(ix) for ix in capture["indices"]]
+        same = parrot_fp32.ParrotFP32(tiny_cfg, sd, forced_routing=own).forward(ids)
+        swapped = parrot_fp32.ParrotFP32(tiny_cfg, sd,
+                                         forced_routing=[ix[:, ::-1] for ix in own]).forward(ids)
+        other = [ix.copy() for ix in own]
+        t = 40
+        other[1][t, 1] = next(e for e in range(8) if e not in other[1][t])
+        changed = parrot_fp32.ParrotFP32(tiny_cfg, sd, forced_routing=other).forward(ids)
+    assert torch.equal(same, free)
+    assert torch.equal(swapped, free)
+    # Earlier positions only see a different expert row count (BLAS blocking).
+    torch.testing.assert_close(changed[0, :t], free[0, :t], atol=1e-6, rtol=0)
+    assert (changed[0, t] - free[0, t]).abs().max() > 1e-3
+
+
+def _exact_ties(logits: np.ndarray) -> tuple[int, int]:
+    """Tokens whose top-3 router logits hold an exact fp32 tie at the top-2
+    selection (1st == 2nd or 2nd == 3rd), and tokens whose top-3 softmax
+    probabilities do."""
+    top = np.sort(logits, axis=-1)[:, ::-1][:, :3]
+    p = np.exp(logits - logits.max(-1, keepdims=True))
+    p = np.sort(p / p.sum(-1, keepdims=True), axis=-1)[:, ::-1][:, :3].astype(np.float32)
+    tie = lambda v: int(((v[:, 0] == v[:, 1]) | (v[:, 1] == v[:, 2])).sum())
+    return tie(top), tie(p)
+
+
+def test_exact_router_ties_on_the_baseline_configs():
+    """Where the build's tie rule (lower index first) and torch.topk's
+    unspecified order could differ: exact fp32 ties in the router logits or
+    probabilities at the top-2 boundary.  Counted on C2 (T=256, E=32), C3
+    (T=4096, E=32, skew bias) and the C4 MoE-layer shape (T=512, E=16), and
+    on every layer of the C4 full model: none occur."""
+    from moe_cases import inputs, moe_module, skew_bias
+    counts = {}
+    for name, tokens, experts, skewed in [("C2", 256, 32, False), ("C3", 4096, 32, True),
+                                          ("C4 layer", 512, 16, False)]:
+        module = moe_module(experts, seed=1, device="cpu")
+        x = inputs(tokens, seed=1, device="cpu")
+        logits = (x.float() @ module.router.weight.detach().float().T).numpy()
+        if skewed:
+            logits = logits + skew_bias(experts).numpy()
+        counts[name] = _exact_ties(logits)
+    from parrot import ModelConfig, Parrot
+    torch.manual_seed(2)
+    model = Parrot(ModelConfig(collect_router_stats=False)).to(torch.bfloat16)
+    oracle = parrot_fp32.ParrotFP32(model.config, model.state_dict())
+    del model
+    ids = torch.randint(0, 32768, (1, 512), generator=torch.Generator().manual_seed(2))
+    capture = {}
+    with torch.no_grad():
+        oracle.forward(ids, capture)
+    per_layer = [_exact_ties(lg.numpy()) for lg in capture["logits"]]
+    counts["C4 model"] = tuple(map(sum, zip(*per_layer)))
+    print(f"exact ties (logits, probabilities): {counts}")
+    assert all(c == (0, 0) for c in counts.values()), counts
