@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 6
+#define PARROT_ABI_VERSION 7
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -36,6 +36,12 @@ extern "C" {
 #define PARROT_ERR_UNSUPPORTED (-3)
 #define PARROT_ERR_WORKSPACE (-4)
 #define PARROT_ERR_ALIGNMENT (-5)
+#define PARROT_ERR_SCRATCH_LIMIT (-6)
+
+/* Bytes of the library's static device scratch array (per GPU), the
+ * workspace of parrot_grouped_experts_static_bf16: 4096 tokens at dim 768,
+ * H 512, Hs 256 (12 KiB per token). */
+#define PARROT_STATIC_SCRATCH_BYTES ((size_t)48 << 20)
 
 /* ABI version (PARROT_ABI_VERSION) of the loaded library. */
 int parrot_abi_version(void);
@@ -552,6 +558,29 @@ int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int3
                                 const void* down, const void* shared_gate_up,
                                 const void* shared_down, const void* addend, void* out,
                                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* parrot_grouped_experts_bf16 without a workspace argument and without any
+ * allocation: its intermediate rows live in a static device array of
+ * PARROT_STATIC_SCRATCH_BYTES bytes that every GPU the library runs on
+ * holds until the process ends.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc).  Same arguments, semantics and
+ * results as parrot_grouped_experts_bf16 (the same kernels).  Returns
+ * PARROT_ERR_SCRATCH_LIMIT when parrot_experts_workspace_bytes(tokens, dim,
+ * hidden_dim, shared_dim) exceeds PARROT_STATIC_SCRATCH_BYTES.  The first
+ * call on a device resolves the array's address for that device (the stream
+ * must belong to the calling thread's current device).  Nothing in the array
+ * needs to start at zero.  All calls on one GPU share the array: calls whose
+ * launches overlap on that GPU (several streams, or several threads) race
+ * and must be serialised by the caller. */
+int parrot_grouped_experts_static_bf16(const void* x, int64_t tokens, int32_t dim,
+                                       int32_t experts, int32_t hidden_dim, int32_t shared_dim,
+                                       int32_t capacity, const int32_t* counts,
+                                       const int32_t* offsets, const int32_t* perm,
+                                       const int32_t* overflow, const float* route_weights,
+                                       const void* packed_gate_up, const void* down,
+                                       const void* shared_gate_up, const void* shared_down,
+                                       const void* addend, void* out, void* stream);
 
 #ifdef __cplusplus
 }

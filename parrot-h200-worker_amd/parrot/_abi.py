@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (maps PyTorch's HIP runtime before the library)
 
 LIBRARY = Path(__file__).resolve().parent / "_lib" / "libparrot_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -106,7 +106,13 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
          _p, _sz, _p]),
+    "parrot_grouped_experts_static_bf16": (
+        ctypes.c_int,
+        [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+         _p]),
 }
+
+STATIC_SCRATCH_BYTES = 48 << 20  # PARROT_STATIC_SCRATCH_BYTES
 
 _lib: ctypes.CDLL | None = None
 

@@ -2,8 +2,12 @@
 //
 // Every entry point validates its arguments on the host and returns a
 // negative PARROT_ERR_* code before launching anything, or the hipError_t
-// of its launches.  Nothing here allocates, synchronises or keeps state.
+// of its launches.  Nothing here allocates or synchronises.  The only
+// global state is the per-device address of the static scratch array, set
+// once per device by parrot_grouped_experts_static_bf16.
 #include "../../../include/parrot_hip.h"
+
+#include <atomic>
 
 #include "common.h"
 
@@ -88,6 +92,8 @@ const char* parrot_status_string(int s) {
     case PARROT_ERR_UNSUPPORTED: return "shape outside the supported range of the HIP kernels";
     case PARROT_ERR_WORKSPACE: return "workspace missing or too small";
     case PARROT_ERR_ALIGNMENT: return "tensor pointer is not 16-byte aligned";
+    case PARROT_ERR_SCRATCH_LIMIT:
+      return "input needs more than the static scratch array (PARROT_STATIC_SCRATCH_BYTES)";
     default: break;
   }
   if (s > 0) return hipGetErrorString(static_cast<hipError_t>(s));
@@ -960,6 +966,60 @@ int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int3
   if (rc != PARROT_OK) return rc;
   return parrot_experts_combine_bf16(tokens, dim, hidden_dim, shared_dim, addend, out,
                                      workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+// ---- allocation-free grouped experts ----------------------------------------
+
+namespace {
+
+// The workspace of parrot_grouped_experts_static_bf16.  In host code the
+// name is only a handle: kernels get the device address that
+// hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[PARROT_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_address[kMaxDevices];
+
+// The current device's address of `scratch`, resolved on its first use on
+// that device (concurrent first calls store the same address).
+int static_scratch(void** address) {
+  int device = 0;
+  if (hipError_t e = hipGetDevice(&device); e != hipSuccess) return status(e);
+  if (device < 0 || device >= kMaxDevices) return PARROT_ERR_UNSUPPORTED;
+  void* p = g_scratch_address[device].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess)
+      return status(e);
+    if (p == nullptr) return PARROT_ERR_NULL_POINTER;
+    g_scratch_address[device].store(p, std::memory_order_release);
+  }
+  *address = p;
+  return PARROT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int parrot_grouped_experts_static_bf16(const void* x, int64_t tokens, int32_t dim,
+                                       int32_t experts, int32_t hidden_dim, int32_t shared_dim,
+                                       int32_t capacity, const int32_t* counts,
+                                       const int32_t* offsets, const int32_t* perm,
+                                       const int32_t* overflow, const float* route_weights,
+                                       const void* packed_gate_up, const void* down,
+                                       const void* shared_gate_up, const void* shared_down,
+                                       const void* addend, void* out, void* stream) {
+  if (tokens < 0 || dim <= 0 || hidden_dim <= 0 || shared_dim <= 0) return PARROT_ERR_BAD_SHAPE;
+  const size_t need = experts_ws(nullptr, tokens, dim, hidden_dim, shared_dim).bytes;
+  if (need > PARROT_STATIC_SCRATCH_BYTES) return PARROT_ERR_SCRATCH_LIMIT;
+  void* workspace = nullptr;
+  if (int rc = static_scratch(&workspace)) return rc;
+  return parrot_grouped_experts_bf16(x, tokens, dim, experts, hidden_dim, shared_dim, capacity,
+                                     counts, offsets, perm, overflow, route_weights,
+                                     packed_gate_up, down, shared_gate_up, shared_down, addend,
+                                     out, workspace, PARROT_STATIC_SCRATCH_BYTES, stream);
 }
 
 }  // extern "C"

@@ -44,7 +44,7 @@ def test_version_and_status_strings(lib):
     assert f"#define PARROT_ABI_VERSION {_abi.ABI_VERSION}" in header
     assert lib.parrot_abi_version() == _abi.ABI_VERSION
     assert lib.parrot_status_string(0) == b"ok"
-    for code in (-1, -2, -3, -4, -5):
+    for code in (-1, -2, -3, -4, -5, -6):
         assert lib.parrot_status_string(code) != b"unknown status"
 
 
@@ -290,3 +290,19 @@ def test_argument_validation_without_gpu(lib):
         512, 768, 16, 512, 256, 80, fake, fake, null, fake, fake, fake, fake, gws, null) == -1
     assert lib.parrot_experts_down_sorted_bf16(
         512, 96, 16, 512, 256, 80, fake, fake, fake, fake, fake, fake, fake, gws, null) == -3
+
+
+def test_static_scratch_entry_rejects_before_any_hip_call(lib):
+    """The allocation-free grouped experts entry states its limit in the
+    header and refuses larger inputs (and bad shapes) on the host."""
+    from parrot import _abi
+    header = HEADER.read_text()
+    assert "#define PARROT_STATIC_SCRATCH_BYTES ((size_t)48 << 20)" in header
+    assert _abi.STATIC_SCRATCH_BYTES == 48 << 20
+    fn = lib.parrot_grouped_experts_static_bf16
+    null = [None] * 11
+    # 4096 tokens at the default shapes fill the array exactly; 4097 do not fit.
+    assert lib.parrot_experts_workspace_bytes(4096, 768, 512, 256) == _abi.STATIC_SCRATCH_BYTES
+    assert fn(None, 4097, 768, 16, 512, 256, 1032, *null, None) == -6
+    assert fn(None, 100, 0, 16, 512, 256, 32, *null, None) == -2
+    assert fn(None, -1, 768, 16, 512, 256, 32, *null, None) == -2
