@@ -559,6 +559,20 @@ int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int3
                                 const void* shared_down, const void* addend, void* out,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* Attained-peak measurements (no counterpart in the reference; they state
+ * every roofline fraction against what this GPU reaches as well as against
+ * the vendor peak).
+ * parrot_peak_mfma_bf16: `blocks` workgroups of 4 wavefronts, each running
+ * `iters` rounds of independent bf16 MFMA chains on register operands
+ * (wide = 0: v_mfma_f32_16x16x32_bf16, 8 chains; wide = 1:
+ * v_mfma_f32_32x32x16_bf16, 4 chains); writes one float per thread to out
+ * [blocks * 256] and the flops of the launch to *flops.
+ * parrot_peak_copy: copies `bytes` (a multiple of 16, 16-byte aligned) from
+ * src to dst with `blocks` workgroups. */
+int parrot_peak_mfma_bf16(int32_t wide, int64_t blocks, int32_t iters, float* out,
+                          int64_t* flops, void* stream);
+int parrot_peak_copy(const void* src, void* dst, int64_t bytes, int64_t blocks, void* stream);
+
 /* parrot_grouped_experts_bf16 without a workspace argument and without any
  * allocation: its intermediate rows live in a static device array of
  * PARROT_STATIC_SCRATCH_BYTES bytes that every GPU the library runs on

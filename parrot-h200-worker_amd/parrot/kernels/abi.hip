@@ -970,6 +970,30 @@ int parrot_grouped_experts_bf16(const void* x, int64_t tokens, int32_t dim, int3
 
 }  // extern "C"
 
+// ---- attained-peak measurements ---------------------------------------------
+
+extern "C" {
+
+int parrot_peak_mfma_bf16(int32_t wide, int64_t blocks, int32_t iters, float* out,
+                          int64_t* flops, void* stream) {
+  if (!out || !flops) return PARROT_ERR_NULL_POINTER;
+  if (blocks < 1 || blocks > (int64_t{1} << 20) || iters < 1 || (wide != 0 && wide != 1))
+    return PARROT_ERR_BAD_SHAPE;
+  *flops = blocks * parrot::peak_mfma_flops_per_block(wide, iters);
+  return status(parrot::launch_peak_mfma(wide, blocks, iters, out, as_stream(stream)));
+}
+
+int parrot_peak_copy(const void* src, void* dst, int64_t bytes, int64_t blocks, void* stream) {
+  if (!src || !dst) return PARROT_ERR_NULL_POINTER;
+  if (bytes < 0 || bytes % 16 || blocks < 1 || blocks > (int64_t{1} << 20))
+    return PARROT_ERR_BAD_SHAPE;
+  if (!aligned16(src) || !aligned16(dst)) return PARROT_ERR_ALIGNMENT;
+  if (bytes == 0) return PARROT_OK;
+  return status(parrot::launch_peak_copy(src, dst, bytes, blocks, as_stream(stream)));
+}
+
+}  // extern "C"
+
 // ---- allocation-free grouped experts ----------------------------------------
 
 namespace {

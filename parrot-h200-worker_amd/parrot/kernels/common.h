@@ -457,4 +457,10 @@ hipError_t launch_proj_frag(const uint16_t* x, int rows, int seq, int k, int64_t
                             const uint16_t* w, int n, int head_dim, uint16_t* kf, uint16_t* vf,
                             hipStream_t s);
 
+// Attained-peak microkernels (peak.hip).
+hipError_t launch_peak_mfma(int wide, int64_t blocks, int iters, float* out, hipStream_t s);
+int64_t peak_mfma_flops_per_block(int wide, int iters);
+hipError_t launch_peak_copy(const void* src, void* dst, int64_t bytes, int64_t blocks,
+                            hipStream_t s);
+
 }  // namespace parrot

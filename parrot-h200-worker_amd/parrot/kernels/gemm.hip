@@ -66,9 +66,9 @@ struct Tile {
 // then a uniform scan over the lanes' tile counts with readlane picks the
 // segment -- one memory hop, no chain of dependent loads.
 template <int BM>
-__device__ __forceinline__ bool find_tile(const GemmArgs& p, int T, Tile& t) {
+__device__ __forceinline__ bool find_tile(const GemmArgs& p, int T, Tile& t,
+                                          int m = static_cast<int>(blockIdx.y)) {
   const int shared_tiles = (T + BM - 1) / BM;
-  int m = static_cast<int>(blockIdx.y);
   if (m < shared_tiles) {
     t = Tile{p.experts, m, T, 2 * T, 0};
     return true;
@@ -296,6 +296,18 @@ __device__ __forceinline__ bf16x8 lds_read_frag(const uint16_t* p) {
   return v;
 }
 
+// Waits until at most N LDS operations of this wavefront are outstanding
+// (they complete in order), then ties the fragments read before those N to
+// the wait so no use of them is scheduled before it.
+template <int N, int NA, int NB>
+__device__ __forceinline__ void lds_wait_upto(bf16x8 (&a)[NA], bf16x8 (&b)[NB]) {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N));
+#pragma unroll
+  for (int i = 0; i < NA; ++i) asm volatile("" : "+v"(a[i]));
+#pragma unroll
+  for (int i = 0; i < NB; ++i) asm volatile("" : "+v"(b[i]));
+}
+
 // Waits for every outstanding LDS read of this wavefront, then ties the
 // fragments to the wait so no use of them is scheduled before it.
 template <int NA, int NB>
@@ -509,6 +521,255 @@ void grouped_gemm_kernel(GemmArgs p) {
           if (dst < 0) continue;
           if (shared) p.y_shared[static_cast<int64_t>(dst) * p.dim + n] = acc[i][j][r];
           else p.y_routed[static_cast<int64_t>(dst) * p.dim + n] = p.weights[dst] * acc[i][j][r];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wide-MFMA tiles for large segments (hundreds to thousands of rows per
+// expert): the same LDS ring as grouped_gemm_kernel (direct-to-LDS stages of
+// 1 KB fragment-order blocks, BK = 64, one barrier per k step), with a
+// 128 x 128 workgroup tile computed on v_mfma_f32_32x32x16_bf16.  Measured
+// on MI355X, that MFMA keeps 92 % of the bf16 peak issuing from one
+// wavefront per SIMD where 16x16x32 keeps 70 %, and a 64 x 64 wavefront
+// tile reads 4 fragments from LDS per 4 MFMAs of 32 K flops each.
+//
+// 32x32x16 operands: lane l holds row (or column) l % 32, k 8 (l / 32) .. +7
+// of a 16-wide k step.  In the 16 x 32 fragment-order blocks that is block
+// (16-row group (l % 32) / 16, 32-k half u / 2), slot 2 (u % 2) + l / 32,
+// row l % 16: 16 lanes read 256 contiguous bytes, so the reads do not
+// conflict.  The C fragment gives lane l column l % 32 and rows
+// 8 (e / 4) + 4 (l / 32) + e % 4 of element e.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int BM, int BN, int BK, int S, int PHASE>
+__global__ __launch_bounds__(256)
+void grouped_gemm_wide_kernel(GemmArgs p) {
+  constexpr int kWaveM = BM / 2, kWaveN = BN / 2;       // 2 x 2 wavefronts
+  constexpr int kTilesM = kWaveM / 32, kTilesN = kWaveN / 32;
+  constexpr int KH = BK / 32;                           // 32-wide k halves per stage
+  constexpr int kSteps = BK / 16;                       // MFMA k steps per stage
+  constexpr int kABlocks = BM / 16 * KH;                // 16-row groups x k halves
+  constexpr int kBlocks = (BM + BN) / 16 * KH;
+  constexpr int P = kBlocks / 4;                        // loads per wavefront per stage
+  constexpr int kStageElems = kBlocks * 512;
+  static_assert(kBlocks % 4 == 0 && kTilesM >= 1 && kTilesN >= 1, "tile shape");
+  static_assert(BK == 32 || BK == 64, "stages of one or two 32-wide k blocks");
+  static_assert(S >= 2, "the ring needs at least two stages");
+
+  __shared__ __attribute__((aligned(16))) uint16_t ring[S][kStageElems];
+  __shared__ int row_src[BM];
+  __shared__ int row_dst[BM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int T = static_cast<int>(p.tokens);
+
+  // XCD-aware tile order.  Workgroups are dispatched round-robin over the 8
+  // XCDs by linear id, so the grid's own order would give XCD x column tile x
+  // of every row tile: every XCD's L2 would stream all of A.  Instead the
+  // workgroups of XCD x take row tiles x, x + 8, ... with all their column
+  // tiles in turn: the ~32 workgroups an XCD runs at once share 4 row tiles'
+  // A rows and the expert's weights in its L2.  The grid's row count is a
+  // multiple of 8 (launch_wide), so every (row, column) tile is taken once.
+  const int nx = static_cast<int>(gridDim.x);
+  const int id = static_cast<int>(blockIdx.y) * nx + static_cast<int>(blockIdx.x);
+  const int pos = id >> 3;
+  const int m_tile = (pos / nx) * 8 + (id & 7);
+  const int n_tile = pos - (pos / nx) * nx;
+
+  Tile t;
+  if (!find_tile<BM>(p, T, t, m_tile)) return;
+  t = uniform_tile(t);
+  const bool shared = t.seg == p.experts;
+  const int N = PHASE == 1 ? 2 * (shared ? p.shared_dim : p.hidden_dim) : p.dim;
+  const int K = PHASE == 1 ? p.dim : (shared ? p.shared_dim : p.hidden_dim);
+  const int n0 = n_tile * BN;
+  if (n0 >= N) return;
+  const int KT = K / BK;
+
+  // ---- per-row source / destination (as in grouped_gemm_kernel) -----------
+  const int sc = segment_row(t, BM, tid < BM ? tid : 0);
+  const int asg = tid < BM && !shared ? assignment_of(p, t, sc) : 0;
+  if (tid < BM) {
+    row_src[tid] = PHASE == 1 ? (shared ? sc : asg >> 1) : t.hbase + sc;
+    const bool live = t.mt * BM + tid < t.rows;
+    row_dst[tid] = !live ? -1 : PHASE == 1 ? t.hbase + sc : (shared ? sc : asg);
+  }
+  __syncthreads();
+
+  // ---- this lane's loads: one 16-byte piece of each of its P blocks -------
+  const int a_ld = PHASE == 1 ? p.dim : p.hstride;
+  const int64_t a_rows = PHASE == 1 ? p.tokens : 3 * p.tokens;
+  const __amdgpu_buffer_rsrc_t a_rsrc =
+      make_rsrc(p.a_src, static_cast<uint32_t>(a_rows * a_ld * 2));
+  const uint16_t* wbase = shared ? p.w_shared
+                                 : p.w_routed + static_cast<int64_t>(t.seg) * N * K;
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_rsrc(wbase, static_cast<uint32_t>(static_cast<int64_t>(N) * K * 2));
+  const int ksteps32 = K / 32;
+  uint32_t voff[P];
+  bool is_a[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int b = wave * P + i;
+    is_a[i] = b < kABlocks;
+    if (b < kABlocks) {
+      // A block (16-row group b / KH, k half b % KH): row 16 (b / KH) + l % 16,
+      // k 32 (b % KH) + 8 (l / 16); the stage adds 2 BK bytes of k.
+      const int r = row_src[(b / KH) * 16 + (lane & 15)];
+      voff[i] = static_cast<uint32_t>(r * a_ld + (b % KH) * 32 + (lane >> 4) * 8) * 2;
+    } else {
+      // B block (16-column group g, k half h) = packed block (n0 / 16 + g,
+      // KH kt + h); the stage adds KH blocks.  Groups past N read zero.
+      const int g = (b - kABlocks) / KH, h = (b - kABlocks) % KH;
+      voff[i] = static_cast<uint32_t>(((n0 / 16 + g) * ksteps32 + h) * 1024 + lane * 16);
+    }
+  }
+  auto issue = [&](uint16_t* stage, int kt) {
+    const int ks = min(kt, KT - 1);
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      uint16_t* dst = stage + (wave * P + i) * 512;
+      if (is_a[i]) buffer_to_lds16(a_rsrc, dst, voff[i], static_cast<uint32_t>(ks) * (2 * BK));
+      else buffer_to_lds16(b_rsrc, dst, voff[i], static_cast<uint32_t>(ks) * (KH * 1024));
+    }
+  };
+
+  // ---- fragment addresses (elements) within a stage, for k step u = 0 -----
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lane_part = (lane >> 5) * 128 + (lane & 15) * 8;
+  int a_frag[kTilesM], b_frag[kTilesN];
+#pragma unroll
+  for (int i = 0; i < kTilesM; ++i) {
+    const int rb = wm * (kWaveM / 16) + 2 * i + ((lane & 31) >> 4);
+    a_frag[i] = KH * rb * 512 + lane_part;
+  }
+#pragma unroll
+  for (int j = 0; j < kTilesN; ++j) {
+    const int g = wn * (kWaveN / 16) + 2 * j + ((lane & 31) >> 4);
+    b_frag[j] = (kABlocks + KH * g) * 512 + lane_part;
+  }
+
+  f32x16 acc[kTilesM][kTilesN];
+#pragma unroll
+  for (int i = 0; i < kTilesM; ++i)
+#pragma unroll
+    for (int j = 0; j < kTilesN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Route weights of this lane's output rows (phase 2, routed): issued here,
+  // they land while the k loop runs instead of stalling the epilogue.
+  float route_w[kTilesM][16];
+  if (PHASE == 2 && !shared) {
+#pragma unroll
+    for (int i = 0; i < kTilesM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wm * kWaveM + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        route_w[i][e] = p.weights[max(row_dst[row], 0)];
+      }
+  }
+
+  // kSteps 16-wide k steps per stage.  Fragment reads run two steps ahead of
+  // the MFMAs: a wavefront's LDS reads complete in order, so waiting until at
+  // most one step's reads are outstanding means step u's fragments have
+  // landed while step u + 1's are still in flight.
+  constexpr int kReads = kTilesM + kTilesN;  // LDS reads per k step
+  auto read_step = [&](const uint16_t* stage, int u, bf16x8 (&a)[kTilesM],
+                       bf16x8 (&b)[kTilesN]) {
+    const int du = (u >> 1) * 512 + (u & 1) * 256;
+#pragma unroll
+    for (int i = 0; i < kTilesM; ++i) a[i] = lds_read_frag(stage + a_frag[i] + du);
+#pragma unroll
+    for (int j = 0; j < kTilesN; ++j) b[j] = lds_read_frag(stage + b_frag[j] + du);
+  };
+  auto compute = [&](const uint16_t* stage) {
+    bf16x8 a[3][kTilesM], b[3][kTilesN];
+    read_step(stage, 0, a[0], b[0]);
+    read_step(stage, 1, a[1], b[1]);
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      const int c = u % 3;
+      if (u + 1 < kSteps) lds_wait_upto<kReads>(a[c], b[c]);
+      else lds_wait_upto<0>(a[c], b[c]);
+      if (u + 2 < kSteps) read_step(stage, u + 2, a[(u + 2) % 3], b[(u + 2) % 3]);
+#pragma unroll
+      for (int i = 0; i < kTilesM; ++i)
+#pragma unroll
+        for (int j = 0; j < kTilesN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st) issue(ring[st], st);
+  for (int kt = 0; kt < KT; ++kt) {
+    wait_vm_barrier<P * (S - 2)>();
+    issue(ring[(kt + S - 1) % S], kt + S - 1);
+    compute(ring[kt % S]);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- epilogue ----------------------------------------------------------------
+  const int wm0 = wm * kWaveM;
+  if (PHASE == 1) {
+    // Columns 32 c .. 32 c + 15 of the packed gate/up matrix are gate rows
+    // 16 c .. 16 c + 15 and the next 16 the matching up rows: lane l < 16 of
+    // each 32-lane half takes the up value of lane l + 16 (ds_swizzle,
+    // xor 16 within 32 lanes).  The tile's BM x BN / 2 hidden values are
+    // staged in LDS (the ring is free once every wavefront has passed the
+    // barrier) and stored as 16-byte row pieces.
+    constexpr int kHalf = BN / 2;
+    constexpr int kOutLd = kHalf + 8;  // staged row stride, elements (shifts banks by 4 rows)
+    static_assert(BM * kOutLd <= S * kStageElems, "staged hidden tile must fit the ring");
+    uint16_t* out_s = &ring[0][0];
+    __syncthreads();
+    const bool gate_lane = (lane & 31) < 16;
+#pragma unroll
+    for (int j = 0; j < kTilesN; ++j) {
+      const int hl = (wn * kWaveN + 32 * j) / 2 + (lane & 15);  // hidden column within the tile
+#pragma unroll
+      for (int i = 0; i < kTilesM; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float up = __int_as_float(
+              __builtin_amdgcn_ds_swizzle(__float_as_int(acc[i][j][e]), 0x401F));
+          const int row = wm0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          if (gate_lane) out_s[row * kOutLd + hl] = f32_to_bf16(swiglu(acc[i][j][e], up));
+        }
+      }
+    }
+    __syncthreads();
+    const int h0 = n0 / 2;
+    constexpr int kPieces = kHalf / 8;  // 16-byte pieces per staged row
+    for (int c = tid; c < BM * kPieces; c += 256) {
+      const int row = c / kPieces, piece = c - row * kPieces;
+      const int dst = row_dst[row];
+      const int h = h0 + piece * 8;
+      if (dst >= 0 && 2 * h < N)
+        *reinterpret_cast<uint4*>(p.hidden_out + static_cast<int64_t>(dst) * p.hstride + h) =
+            *reinterpret_cast<const uint4*>(out_s + row * kOutLd + piece * 8);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kTilesN; ++j) {
+      const int n = n0 + wn * kWaveN + 32 * j + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < kTilesM; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = wm0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          const int dst = row_dst[row];
+          if (dst < 0) continue;
+          if (shared) p.y_shared[static_cast<int64_t>(dst) * p.dim + n] = acc[i][j][e];
+          else p.y_routed[static_cast<int64_t>(dst) * p.dim + n] = route_w[i][e] * acc[i][j][e];
         }
       }
     }
@@ -777,6 +1038,18 @@ hipError_t launch_phase(int phase, const GemmArgs& args, int n_max, hipStream_t 
   return hipGetLastError();
 }
 
+template <int BM, int BN, int BK, int S>
+hipError_t launch_wide(int phase, const GemmArgs& args, int n_max, hipStream_t s) {
+  const int T = static_cast<int>(args.tokens);
+  const int m_tiles = (T + BM - 1) / BM + (2 * T) / BM + args.experts;
+  // Rows of tiles rounded up to a multiple of the 8 XCDs (the kernel's tile
+  // order takes every eighth row tile per XCD).
+  const dim3 grid((n_max + BN - 1) / BN, (m_tiles + 7) / 8 * 8);
+  if (phase == 1) grouped_gemm_wide_kernel<BM, BN, BK, S, 1><<<grid, 256, 0, s>>>(args);
+  else grouped_gemm_wide_kernel<BM, BN, BK, S, 2><<<grid, 256, 0, s>>>(args);
+  return hipGetLastError();
+}
+
 template <int BM, int WN, int PF, int KCH>
 hipError_t launch_stream(int phase, const GemmArgs& args, int n_max, hipStream_t s) {
   const int T = static_cast<int>(args.tokens);
@@ -819,7 +1092,16 @@ hipError_t run_stream(int phase, GemmArgs args, int n_max, hipStream_t s) {
 // K fits its LDS budget (64-row tiles in two k chunks, when every K splits
 // into 128-element halves; else 32-row tiles), else the pipelined kernel
 // with 32-row tiles.
-enum class TilePlan { kStream16, kStream32, kStream64 };
+enum class TilePlan { kStream16, kStream32, kStream64, kWide128 };
+
+// Average rows per expert from which the wide-MFMA tiles take over, per
+// phase.  Measured on MI355X (E = 16 uniform, T = 4K ... 64K, and BASELINE
+// config 3, E = 32 with 2 experts holding ~95 % of the rows): down is 18-31 %
+// faster on wide tiles from 256 rows per expert; gate/up only from 512 --
+// at config 3 its 30 small experts (~10 rows each) pay for whole 128 x 128
+// tiles with 1 KB x 24 weight blocks each (wide 49.8 us vs streaming 41.2).
+constexpr int64_t kWideRowsGateUp = 512;
+constexpr int64_t kWideRowsDown = 256;
 
 template <TilePlan PLAN>
 hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t* hidden,
@@ -836,6 +1118,7 @@ hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t*
     args.w_shared = w.shared_down;
     n_max = args.dim;
   }
+  if constexpr (PLAN == TilePlan::kWide128) return launch_wide<128, 128, 32, 3>(phase, args, n_max, s);
   const int k_max = phase == 1 ? args.dim : max(args.hidden_dim, args.shared_dim);
   if (k_max > kStreamKCap) return launch_phase<32, 128, 3>(phase, args, n_max, s);
   if constexpr (PLAN == TilePlan::kStream64) {
@@ -854,11 +1137,14 @@ hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t*
 // 256-column pipelined tiles were slower still.  Past ~3 x 32 rows per
 // expert the weight fragments' trips from L2 set the pace (each 32-row tile
 // of an expert re-reads its weights), and 64-row tiles in two k chunks halve
-// them.
-TilePlan experts_tile_plan(int64_t tokens, int experts) {
+// them.  From kWideRowsGateUp / kWideRowsDown rows per expert the wide-MFMA
+// 128 x 128 tiles take over (grouped_gemm_wide_kernel).
+TilePlan experts_tile_plan(int phase, int64_t tokens, int experts) {
   const int64_t per_expert = (2 * tokens + experts - 1) / experts;
   if (tokens <= 16) return TilePlan::kStream16;
-  return per_expert <= 96 ? TilePlan::kStream32 : TilePlan::kStream64;
+  if (per_expert <= 96) return TilePlan::kStream32;
+  const int64_t wide_from = phase == 1 ? kWideRowsGateUp : kWideRowsDown;
+  return per_expert < wide_from ? TilePlan::kStream64 : TilePlan::kWide128;
 }
 
 }  // namespace
@@ -901,10 +1187,11 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
     args.offsets_out = map.offsets_out;
     args.sorted_out = map.sorted_out;
   }
-  switch (experts_tile_plan(tokens, experts)) {
+  switch (experts_tile_plan(phase, tokens, experts)) {
     case TilePlan::kStream16: return run_phase<TilePlan::kStream16>(phase, args, w, hidden, s);
     case TilePlan::kStream32: return run_phase<TilePlan::kStream32>(phase, args, w, hidden, s);
-    default: return run_phase<TilePlan::kStream64>(phase, args, w, hidden, s);
+    case TilePlan::kStream64: return run_phase<TilePlan::kStream64>(phase, args, w, hidden, s);
+    default: return run_phase<TilePlan::kWide128>(phase, args, w, hidden, s);
   }
 }
 
