@@ -60,6 +60,15 @@ def parse_args():
     p.add_argument("--traffic-workload", action="store_true",
                    help="only launch the dispatches the two rocprofv3 --pmc passes count: the "
                         "dominant kernel at the in-model shape and a calibration copy")
+    p.add_argument("--pmc-workload", action="store_true",
+                   help="only launch the counter workload: every hot-path kernel at C2, C3, "
+                        "the C4 layer and T=65536, segments separated by a 16-byte marker copy")
+    p.add_argument("--summarize-pmc", nargs=2, metavar=("PASS_A_DIR", "PASS_B_DIR"),
+                   help="(no GPU) turn the counter CSVs of the two --pmc passes over "
+                        "--pmc-workload into profiles/counters_hot_path.json")
+    p.add_argument("--summarize-trace", metavar="TRACE_DIR",
+                   help="(no GPU) per-kernel durations of a rocprofv3 --kernel-trace run of "
+                        "bench.py into profiles/kernel_trace_bench.json")
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="(no GPU) turn the counter CSVs of the FETCH_SIZE and WRITE_SIZE "
                         "passes into the traffic summary under profiles/")
@@ -109,6 +118,7 @@ class StageBench:
         self.g_offsets = torch.empty(2 * self.E + 2, **i32)
         self.g_sorted = torch.empty(2 * self.T, **i32)
         self.ids = self.routed.indices.reshape(-1).contiguous()
+        self.top2_ids = torch.empty_like(self.routed.indices)
 
     def route(self):
         p, r, g = self.ptr, self.routed, self.g
@@ -116,6 +126,40 @@ class StageBench:
             p(self.x), p(self.moe.router.weight), p(self.bias), self.T, self.dim, self.E, self.C,
             None, None, p(r.weights), p(r.indices), p(g.positions), p(g.counts), p(g.offsets),
             p(g.perm), p(g.overflow), p(self.rws), self.rws_bytes, self.s)
+
+    def route_top2(self):
+        p, r = self.ptr, self.routed
+        return self.lib.parrot_route_top2_bf16(
+            p(self.x), p(self.moe.router.weight), p(self.bias), self.T, self.dim, self.E,
+            p(r.weights), p(self.top2_ids), self.s)
+
+    def layer(self):
+        """The standalone MoE layer as MoE.inference runs it: top-2 + the
+        grouping gate/up, down and combine where the gate/up launch groups
+        in-kernel, else route + grouping, gate/up, down and combine."""
+        steps = ((self.route_top2, self.gate_up_grouping_top2, self.down_sorted, self.combine)
+                 if self.in_kernel else (self.route, self.gate_up, self.down, self.combine))
+        for step in steps:
+            rc = step()
+            if rc:
+                return rc
+        return 0
+
+    def gate_up_grouping_top2(self):
+        p = self.ptr
+        return self.lib.parrot_experts_gate_up_grouping_bf16(
+            p(self.x), self.T, self.dim, self.E, self.H, self.Hs, self.C, p(self.top2_ids),
+            p(self.g_counts), p(self.g_offsets), p(self.g_sorted), p(self.packed[0]),
+            p(self.packed[2]), p(self.ews), self.ews_bytes, self.s)
+
+    def layer_min_bytes(self):
+        """Hit experts' weights once, the shared expert, the router, x in and
+        out written (the layer's HBM floor)."""
+        T, d, H, Hs, E = self.T, self.dim, self.H, self.Hs, self.E
+        return (self.hit * 3 * d * H + 3 * d * Hs + E * d + 2 * T * d) * 2
+
+    def layer_flops(self):
+        return 2 * self.T * self.dim * self.E + self.flops_gate_up() + self.flops_down()
 
     def gate_up(self):
         p, g = self.ptr, self.g
@@ -196,14 +240,62 @@ def event_time_us(fn, iters: int, stream) -> float:
     return start.elapsed_time(end) * 1000.0 / iters
 
 
+# Attained peaks of this GPU (attained_peaks), once measured: every entry then
+# also states its fraction of what the copy / MFMA-loop kernels reach.
+ATTAINED: dict = {}
+
+
 def entry(us: float, nbytes: int, flops: int | None = None) -> dict:
     gbps = nbytes / (us * 1e-6) / 1e9
     out = {"us": round(us, 3), "bytes": int(nbytes), "gbps": round(gbps, 1),
            "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4)}
+    if ATTAINED.get("copy_gbps"):
+        out["hbm_frac_attained"] = round(gbps / ATTAINED["copy_gbps"], 4)
     if flops is not None:
         tf = flops / (us * 1e-6) / 1e12
         out.update(flops=int(flops), tflops=round(tf, 2), mfma_frac=round(tf / PEAK_BF16_TFLOPS, 4))
+        if ATTAINED.get("mfma_bf16_tflops"):
+            out["mfma_frac_attained"] = round(tf / ATTAINED["mfma_bf16_tflops"], 4)
     return out
+
+
+def attained_peaks() -> dict:
+    """What this GPU reaches: the bf16 MFMA-loop microkernel at both MFMA
+    shapes (4096 workgroups, register operands) and a 1 GiB device copy
+    (this library's copy kernel and torch's copy_), HIP events, best of 3."""
+    import ctypes
+
+    import torch
+    from parrot import _abi
+    lib = _abi.load()
+    s = torch.cuda.current_stream()
+    res = {}
+    out = torch.empty(4096 * 256, device="cuda")
+    flops = ctypes.c_int64()
+    for wide, iters, name in ((1, 2000, "mfma_32x32x16_tflops"), (0, 4000, "mfma_16x16x32_tflops")):
+        def run():
+            return lib.parrot_peak_mfma_bf16(wide, 4096, iters, out.data_ptr(), ctypes.byref(flops),
+                                             s.cuda_stream)
+        us = min(event_time_us(run, 3, s) for _ in range(3))
+        res[name] = round(flops.value / (us * 1e-6) / 1e12, 1)
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    own = min(event_time_us(lambda: lib.parrot_peak_copy(src.data_ptr(), dst.data_ptr(), n, 8192,
+                                                         s.cuda_stream), 5, s) for _ in range(3))
+
+    def torch_copy():
+        dst.copy_(src)
+        return 0
+    tc = min(event_time_us(torch_copy, 5, s) for _ in range(3))
+    res["copy_kernel_gbps"] = round(2 * n / (own * 1e-6) / 1e9, 1)
+    res["torch_copy_gbps"] = round(2 * n / (tc * 1e-6) / 1e9, 1)
+    res["mfma_bf16_tflops"] = max(res["mfma_32x32x16_tflops"], res["mfma_16x16x32_tflops"])
+    res["copy_gbps"] = max(res["copy_kernel_gbps"], res["torch_copy_gbps"])
+    res["vendor"] = {"mfma_bf16_tflops": PEAK_BF16_TFLOPS, "hbm_gbps": PEAK_HBM_GBPS}
+    del src, dst, out
+    torch.cuda.empty_cache()
+    return res
 
 
 def layer_kernels(moe, x, iters, logit_bias=None) -> tuple[dict, "StageBench"]:
@@ -225,6 +317,15 @@ def layer_kernels(moe, x, iters, logit_bias=None) -> tuple[dict, "StageBench"]:
                                         sb.flops_gate_up())
         res["down_sorted"] = entry(event_time_us(sb.down_sorted, iters, sb.stream),
                                    sb.bytes_down() + (3 * sb.E + 2) * 4, sb.flops_down())
+        res["route_top2"] = entry(event_time_us(sb.route_top2, iters, sb.stream),
+                                  sb.T * sb.dim * 2 + sb.E * sb.dim * 2 + sb.T * 2 * (8 + 4))
+    # The whole standalone layer, back to back on one stream, against the
+    # layer's HBM floor (hit experts' weights once + x in + out) and its flops.
+    layer = entry(event_time_us(sb.layer, iters, sb.stream), sb.layer_min_bytes(), sb.layer_flops())
+    layer["launches"] = ("route_top2 + gate_up(grouping in-kernel) + down + combine"
+                         if sb.in_kernel else "route(+grouping) + gate_up + down + combine")
+    layer["tokens_per_s"] = round(sb.T / (layer["us"] * 1e-6), 1)
+    res["layer"] = layer
     return res, sb
 
 
@@ -519,12 +620,257 @@ def summarize_traffic(fetch_dir: str, write_dir: str) -> dict:
     return summary
 
 
+TRAFFIC_SEGMENT = "C4_layer_T512_E16: gate/up grouping in-kernel"
+
+
 def load_traffic() -> int | None:
-    try:
-        summary = json.loads(TRAFFIC_FILE.read_text())
-    except (OSError, ValueError):
+    """HBM bytes per launch of the roofline kernel: from the committed
+    counter summary of every hot-path kernel, else from the older
+    two-pass traffic file."""
+    counters = load_json(PMC_FILE)
+    if counters and TRAFFIC_SEGMENT in counters.get("segments", {}):
+        return counters["segments"][TRAFFIC_SEGMENT]["hbm_bytes"]
+    summary = load_json(TRAFFIC_FILE)
+    if not summary:
         return None
     return summary.get("traffic_bytes") if summary.get("kernel") == TRAFFIC_KERNEL else None
+
+
+# ---------------------------------------------------------------------------
+# Counter evidence for every hot-path kernel (two rocprofv3 --pmc passes)
+# ---------------------------------------------------------------------------
+
+PMC_FILE = ROOT / "profiles" / "counters_hot_path.json"
+PMC_MANIFEST = "gpurun_out/pmc_manifest.json"
+PMC_REPEATS = 5
+PMC_PASSES = {
+    "A": "FETCH_SIZE SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE",
+    "B": "WRITE_SIZE",
+}
+PMC_COMMANDS = [f"rocprofv3 --pmc {c} -f csv -d gpurun_out/pmc_{k} -o pmc "
+                f"-- python3 bench.py --pmc-workload" for k, c in PMC_PASSES.items()] + [
+    "python3 bench.py --summarize-pmc gpurun_out/pmc_A gpurun_out/pmc_B"]
+MARKER_KERNEL = ("parrot", "copy_kernel")  # a 16-byte parrot_peak_copy opens every segment
+
+
+def pmc_workload() -> None:
+    """The dispatches the --pmc passes count, in segments: a marker copy, then
+    PMC_REPEATS launches of one stage.  Calibration first (torch.neg over a
+    known byte count, the MFMA loop over a known flop count), then route,
+    grouping, gate/up, down and combine at C2, C3, block 0's input of the C4
+    forward and T=65536 (E=16), RMSNorm and the 9-source depth mix at 512 and
+    65536 tokens.  Writes the segment list to PMC_MANIFEST."""
+    import ctypes
+
+    import torch
+    from parrot import _abi
+    from parrot._abi import ptr
+    lib = _abi.load()
+    model, _, captured = build_model()
+    s = torch.cuda.current_stream()
+    moe0 = model.blocks[0].moe
+    benches = {"C4_layer_T512_E16": StageBench(moe0, captured["x"])}
+    for name, tokens, skew in (("C2_T256_E32", 256, False), ("C3_T4096_E32_skew", 4096, True)):
+        moe, x, bias = _layer_case(tokens, skew)
+        benches[name] = StageBench(moe, x, bias)
+    big = torch.randn(65536, moe0.cfg.dim, device="cuda",
+                      generator=torch.Generator(device="cuda").manual_seed(7)).bfloat16()
+    benches["T65536_E16"] = StageBench(moe0, big)
+    d = moe0.cfg.dim
+    norm_cases = {}
+    for T in (512, 65536):
+        x = torch.randn(T, d, device="cuda").bfloat16()
+        srcs = [torch.randn(T, d, device="cuda").bfloat16() for _ in range(9)]
+        arr = (ctypes.c_void_p * 9)(*[t.data_ptr() for t in srcs])
+        norm_cases[T] = (x, torch.empty_like(x), srcs, arr)
+    w = torch.ones(d, device="cuda", dtype=torch.bfloat16)
+    q = torch.randn(d, device="cuda").bfloat16()
+    calib_src = torch.ones(CALIBRATION_ELEMS, dtype=torch.bfloat16, device="cuda")
+    calib_dst = torch.empty_like(calib_src)
+    loop_out = torch.empty(1024 * 256, device="cuda")
+    loop_flops = ctypes.c_int64()
+    mark_a = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    mark_b = torch.empty_like(mark_a)
+    torch.cuda.synchronize()
+
+    manifest = []
+
+    def segment(label, fn, nbytes=None, flops=None):
+        _abi.check(lib.parrot_peak_copy(ptr(mark_a), ptr(mark_b), 16, 1, s.cuda_stream), "marker")
+        for _ in range(PMC_REPEATS):
+            rc = fn()
+            if rc:
+                raise RuntimeError(f"{label}: status {rc}")
+        manifest.append({"label": label, "bytes": nbytes, "flops": flops})
+
+    def neg():
+        torch.neg(calib_src, out=calib_dst)
+        return 0
+
+    segment("calibration: torch.neg bf16", neg, 2 * CALIBRATION_ELEMS * 2)
+    segment("calibration: MFMA loop 32x32x16",
+            lambda: lib.parrot_peak_mfma_bf16(1, 1024, 500, ptr(loop_out), ctypes.byref(loop_flops),
+                                              s.cuda_stream))
+    manifest[-1]["flops"] = loop_flops.value
+    for cfg, sb in benches.items():
+        segment(f"{cfg}: route + grouping", sb.route, sb.bytes_route())
+        if sb.in_kernel:
+            segment(f"{cfg}: route top-2", sb.route_top2,
+                    sb.T * sb.dim * 2 + sb.E * sb.dim * 2 + sb.T * 2 * (8 + 4))
+            segment(f"{cfg}: gate/up grouping in-kernel", sb.gate_up_grouping,
+                    sb.bytes_gate_up() + sb.bytes_grouping(), sb.flops_gate_up())
+            segment(f"{cfg}: down (in-kernel grouping)", sb.down_sorted,
+                    sb.bytes_down() + (3 * sb.E + 2) * 4, sb.flops_down())
+        else:
+            segment(f"{cfg}: gate/up", sb.gate_up, sb.bytes_gate_up(), sb.flops_gate_up())
+            segment(f"{cfg}: down", sb.down, sb.bytes_down(), sb.flops_down())
+        segment(f"{cfg}: combine", sb.combine, sb.bytes_combine())
+    for T, (x, y, srcs, arr) in norm_cases.items():
+        segment(f"T{T}: rms_norm",
+                lambda: lib.parrot_rms_norm_bf16(ptr(x), ptr(w), ptr(y), T, d, 1e-6, s.cuda_stream),
+                2 * T * d * 2 + d * 2)
+        segment(f"T{T}: depth mix + norm, 9 sources",
+                lambda: lib.parrot_depth_mix_bf16(ctypes.cast(arr, ctypes.c_void_p), 9, ptr(q),
+                                                  ptr(w), 1e-6, ptr(w), 1e-6, T, d, None, ptr(y),
+                                                  s.cuda_stream),
+                9 * T * d * 2 + 3 * d * 2 + T * d * 2)
+    torch.cuda.synchronize()
+    Path(PMC_MANIFEST).parent.mkdir(parents=True, exist_ok=True)
+    Path(PMC_MANIFEST).write_text(json.dumps(manifest, indent=1))
+    print(json.dumps({"pmc_workload": "done", "segments": len(manifest),
+                      "repeats": PMC_REPEATS}), flush=True)
+
+
+def _dispatches(directory: str) -> list[dict]:
+    """Per-dispatch rows (kernel, counters, duration) of a counter_collection
+    CSV in dispatch order."""
+    import csv
+    by_id: dict[int, dict] = {}
+    for path in sorted(Path(directory).rglob("*counter_collection.csv")):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                key = int(r["Dispatch_Id"])
+                d = by_id.setdefault(key, {"kernel": r["Kernel_Name"], "counters": {},
+                                           "ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+                d["counters"][r["Counter_Name"]] = float(r["Counter_Value"])
+    return [by_id[k] for k in sorted(by_id)]
+
+
+def _segments(rows: list[dict]) -> list[list[dict]]:
+    segs, cur = [], None
+    for r in rows:
+        if all(part in r["kernel"] for part in MARKER_KERNEL):
+            cur = []
+            segs.append(cur)
+        elif cur is not None:
+            cur.append(r)
+    return segs
+
+
+def summarize_pmc(dir_a: str, dir_b: str) -> dict:
+    manifest = json.loads(Path(PMC_MANIFEST).read_text())
+    seg_a, seg_b = _segments(_dispatches(dir_a)), _segments(_dispatches(dir_b))
+    if len(seg_a) < len(manifest) or len(seg_b) < len(manifest):
+        raise SystemExit(f"found {len(seg_a)} / {len(seg_b)} segments for {len(manifest)} labels")
+    seg_a, seg_b = seg_a[-len(manifest):], seg_b[-len(manifest):]
+
+    def per_launch(seg, counter):
+        return sum(r["counters"].get(counter, 0.0) for r in seg) / PMC_REPEATS
+
+    # Calibration: counter KiB per byte moved, MFMA ops and busy cycles per flop.
+    calib = 2 * CALIBRATION_ELEMS  # bytes each way
+    fetch_scale = calib / 1024 / per_launch(seg_a[0], "FETCH_SIZE")
+    write_scale = calib / 1024 / per_launch(seg_b[0], "WRITE_SIZE")
+    loop = seg_a[1]
+    loop_flops = manifest[1]["flops"]
+    flop_per_mop = loop_flops / per_launch(loop, "SQ_INSTS_VALU_MFMA_MOPS_BF16")
+    loop_busy = per_launch(loop, "SQ_VALU_MFMA_BUSY_CYCLES") / per_launch(loop, "GRBM_GUI_ACTIVE")
+    loop_ns = sum(r["ns"] for r in loop) / PMC_REPEATS
+    entries = {}
+    for m, a, b in list(zip(manifest, seg_a, seg_b))[2:]:
+        ns = sum(r["ns"] for r in a) / PMC_REPEATS
+        fetch = per_launch(a, "FETCH_SIZE") * fetch_scale * 1024
+        write = per_launch(b, "WRITE_SIZE") * write_scale * 1024
+        e = {"kernels": sorted({r["kernel"].split("(")[0][:120] for r in a}),
+             "us_under_pmc": round(ns / 1e3, 3),
+             "fetch_bytes": int(fetch), "write_bytes": int(write),
+             "hbm_bytes": int(fetch + write),
+             "hbm_gbps": round((fetch + write) / ns, 1) if ns else None}
+        if m["bytes"]:
+            e["algorithmic_bytes"] = m["bytes"]
+            e["traffic_over_algorithmic"] = round((fetch + write) / m["bytes"], 3)
+        mops = per_launch(a, "SQ_INSTS_VALU_MFMA_MOPS_BF16")
+        if m["flops"] and mops:
+            e["algorithmic_flops"] = m["flops"]
+            e["mfma_flops_counted"] = int(mops * flop_per_mop)
+            e["mfma_tflops"] = round(mops * flop_per_mop / ns / 1e3, 1)
+            busy = per_launch(a, "SQ_VALU_MFMA_BUSY_CYCLES") / per_launch(a, "GRBM_GUI_ACTIVE")
+            e["mfma_busy_vs_loop"] = round(busy / loop_busy, 4)
+        entries[m["label"]] = e
+    summary = {
+        "what": "per-launch HBM bytes (FETCH_SIZE, WRITE_SIZE) and MFMA counters of every "
+                "hot-path kernel, median workload of PMC_REPEATS launches per segment",
+        "calibration": {
+            "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
+            "bytes_each_way": calib, "kernel": "torch.neg bf16, %d elements" % CALIBRATION_ELEMS,
+            "flop_per_mfma_op": round(flop_per_mop, 3),
+            "mfma_loop": {"flops": loop_flops, "us_under_pmc": round(loop_ns / 1e3, 2),
+                          "tflops": round(loop_flops / loop_ns / 1e3, 1),
+                          "busy_cycles_over_gui_active": round(loop_busy, 4)}},
+        "segments": entries,
+        "commands": PMC_COMMANDS,
+    }
+    PMC_FILE.write_text(json.dumps(summary, indent=1) + "\n")
+    return summary
+
+
+TRACE_FILE = ROOT / "profiles" / "kernel_trace_bench.json"
+
+
+def summarize_trace(directory: str) -> dict:
+    """Per-kernel dispatch counts and mean durations of a rocprofv3
+    --kernel-trace run of bench.py; for the roofline kernel, the dispatches
+    of its timed back-to-back loop (runs of >= 20 in a row) apart from those
+    inside the graph-replayed forwards."""
+    import csv
+    rows = []
+    for path in sorted(Path(directory).rglob("*kernel_trace.csv")):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"],
+                             int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    rows.sort()
+    stats: dict[str, list[int]] = {}
+    for _, name, ns in rows:
+        stats.setdefault(name, []).append(ns)
+    loop, graph, run = [], [], []
+    for _, name, ns in rows + [(None, "", 0)]:
+        if TRAFFIC_KERNEL in name:
+            run.append(ns)
+            continue
+        (loop if len(run) >= 20 else graph).extend(run)
+        run = []
+    summary = {
+        "roofline_kernel": TRAFFIC_KERNEL,
+        "loop_dispatches": len(loop),
+        "loop_mean_us": round(statistics.mean(loop) / 1e3, 3) if loop else None,
+        "in_forward_dispatches": len(graph),
+        "in_forward_mean_us": round(statistics.mean(graph) / 1e3, 3) if graph else None,
+        "kernels": {n[:160]: {"calls": len(v), "mean_us": round(statistics.mean(v) / 1e3, 3),
+                              "total_us": round(sum(v) / 1e3, 1)}
+                    for n, v in sorted(stats.items(), key=lambda kv: -sum(kv[1]))[:40]},
+        "command": "rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/bench_trace -o bench "
+                   "-- python3 bench.py; python3 bench.py --summarize-trace gpurun_out/bench_trace",
+    }
+    TRACE_FILE.write_text(json.dumps(summary, indent=1) + "\n")
+    return summary
+
+
+def load_json(path: Path) -> dict | None:
+    try:
+        return json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
 
 
 # ---------------------------------------------------------------------------
@@ -570,6 +916,12 @@ def main():
     if args.summarize_traffic:
         print(json.dumps(summarize_traffic(*args.summarize_traffic)))
         return
+    if args.summarize_pmc:
+        print(json.dumps(summarize_pmc(*args.summarize_pmc))[:2000])
+        return
+    if args.summarize_trace:
+        print(json.dumps(summarize_trace(args.summarize_trace))[:2000])
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
@@ -578,6 +930,9 @@ def main():
         sys.exit(2)
     if args.traffic_workload:
         traffic_workload()
+        return
+    if args.pmc_workload:
+        pmc_workload()
         return
 
     import torch
@@ -632,7 +987,11 @@ def main():
 
     kernels = {}
     roofline = None
+    peaks = None
     if not args.skip_kernels:
+        log("attained peaks")
+        peaks = attained_peaks()
+        ATTAINED.update(peaks)
         log("per-kernel timing")
         c4, _ = layer_kernels(moe0, captured["x"], args.kernel_iters)
         kernels["C4_in_model_T512_E16"] = c4
@@ -651,8 +1010,27 @@ def main():
                               "top-2 ids in-kernel), C4 in-model shape T=512 E=16",
                     "bound": "hbm", "achieved": gu["gbps"], "peak": PEAK_HBM_GBPS,
                     "unit": "GB/s", "frac": gu["hbm_frac"], "traffic": traffic,
-                    "algorithmic_bytes": gu["bytes"],
-                    "traffic_source": str(TRAFFIC_FILE.relative_to(ROOT)) if traffic else None}
+                    "algorithmic_bytes": gu["bytes"], "event_us": gu["us"],
+                    "attained_peak": peaks["copy_gbps"],
+                    "frac_of_attained": round(gu["gbps"] / peaks["copy_gbps"], 4),
+                    "traffic_source": (str(PMC_FILE.relative_to(ROOT)) if load_json(PMC_FILE)
+                                       else str(TRAFFIC_FILE.relative_to(ROOT))) if traffic
+                    else None}
+        trace = load_json(TRACE_FILE)
+        if trace and trace.get("roofline_kernel") == TRAFFIC_KERNEL and trace.get("loop_mean_us"):
+            # The committed kernel trace of this command: the same loop's mean
+            # dispatch duration, and the kernel inside the graph-replayed forward.
+            roofline["trace_source"] = str(TRACE_FILE.relative_to(ROOT))
+            roofline["trace_loop_us"] = trace["loop_mean_us"]
+            roofline["trace_loop_frac"] = round(
+                gu["bytes"] / (trace["loop_mean_us"] * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)
+            if trace.get("in_forward_mean_us"):
+                roofline["in_forward_us"] = trace["in_forward_mean_us"]
+                roofline["in_forward_frac"] = round(
+                    gu["bytes"] / (trace["in_forward_mean_us"] * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)
+        counters = load_json(PMC_FILE)
+        if counters:
+            kernels["counters_source"] = str(PMC_FILE.relative_to(ROOT))
 
     decode = None
     if not args.skip_decode:
@@ -681,6 +1059,7 @@ def main():
         "eager_ms_per_step": round(eager_ms, 3),
         "eager_tokens_per_s": round(TOKENS / (eager_ms / 1e3), 1),
         "roofline": roofline,
+        "attained_peaks": peaks,
         "kernels": kernels,
         "decode": decode,
         "cpu_baseline": None,

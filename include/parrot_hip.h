@@ -439,6 +439,16 @@ int parrot_route_bf16(const void* x, const void* router_weight, const float* log
                       int32_t* out_offsets, int32_t* out_perm, int32_t* out_overflow,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* The router and top-2 of parrot_route_bf16 alone: out_weights fp32 [T, 2]
+ * and out_indices int64 [T, 2], the same bits as parrot_route_bf16 gives, and
+ * no grouping outputs (for callers whose expert launch groups the indices
+ * itself, parrot_experts_gate_up_grouping_bf16).  Replaces metal_route
+ * (parrot/metal_moe.py:58-81) where grouped_mps_experts then recounts the
+ * slots itself (parrot/metal_moe.py:384-387). */
+int parrot_route_top2_bf16(const void* x, const void* router_weight, const float* logit_bias,
+                           int64_t tokens, int32_t dim, int32_t experts, float* out_weights,
+                           int64_t* out_indices, void* stream);
+
 /* As parrot_route_bf16, starting from given fp32 logits [T, E] (the
  * "identical router logits" entry of the parity contract). */
 int parrot_route_from_logits_f32(const float* logits, const float* logit_bias, int64_t tokens,

@@ -106,6 +106,7 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
          _p, _sz, _p]),
+    "parrot_route_top2_bf16": (ctypes.c_int, [_p, _p, _p, _i64, _i32, _i32, _p, _p, _p]),
     "parrot_peak_mfma_bf16": (ctypes.c_int, [_i32, _i64, _i32, _p, _p, _p]),
     "parrot_peak_copy": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),
     "parrot_grouped_experts_static_bf16": (

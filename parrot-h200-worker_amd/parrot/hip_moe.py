@@ -166,6 +166,39 @@ def route(module: "MoE", flat: Tensor, collect_stats: bool,
     return RouteResult(probs, weights, indices, g, logits)
 
 
+def route_top2(module: "MoE", flat: Tensor, logit_bias: Tensor | None = None) -> RouteResult:
+    """The router and top-2 of ``route`` alone (the same weights and indices
+    to the bit), without grouping: for expert launches that group the
+    indices themselves (``groups_in_kernel``)."""
+    _require(flat, "HIP routing")
+    tokens, dim = flat.shape
+    experts = module.cfg.n_experts
+    if experts > MAX_EXPERTS or module.cfg.top_k != 2:
+        raise RuntimeError(f"HIP routing supports top-2 of at most {MAX_EXPERTS} experts")
+    flat = flat.contiguous()
+    router_w = module.router.weight
+    if router_w.dtype != flat.dtype or not router_w.is_contiguous():
+        raise RuntimeError("router weight must be contiguous and match the input dtype")
+    dev = flat.device
+    weights = torch.empty((tokens, 2), dtype=torch.float32, device=dev)
+    indices = torch.empty((tokens, 2), dtype=torch.int64, device=dev)
+    if logit_bias is not None:
+        logit_bias = logit_bias.to(device=dev, dtype=torch.float32).contiguous()
+    _abi.check(_abi.load().parrot_route_top2_bf16(
+        ptr(flat), ptr(router_w), ptr(logit_bias), tokens, dim, experts, ptr(weights),
+        ptr(indices), _stream(dev)), "parrot_route_top2_bf16")
+    return RouteResult(None, weights, indices, None)
+
+
+def route_for_experts(module: "MoE", flat: Tensor) -> RouteResult:
+    """The routing an inference MoE layer needs before its expert launches:
+    top-2 only where the gate/up launch groups the indices itself, else the
+    top-2 with its grouping."""
+    if groups_in_kernel(module, flat.shape[0], flat.shape[1]):
+        return route_top2(module, flat)
+    return route(module, flat, collect_stats=False)
+
+
 def route_from_logits(logits: Tensor, logit_bias: Tensor | None = None,
                       collect_stats: bool = False) -> RouteResult:
     """Top-2 + grouping from given fp32 router logits [T, E] (parity entry)."""

@@ -416,6 +416,21 @@ int parrot_route_bf16(const void* x, const void* router_weight, const float* log
                       workspace_bytes, stream);
 }
 
+int parrot_route_top2_bf16(const void* x, const void* router_weight, const float* logit_bias,
+                           int64_t tokens, int32_t dim, int32_t experts, float* out_weights,
+                           int64_t* out_indices, void* stream) {
+  if (!x || !router_weight || !out_weights || !out_indices) return PARROT_ERR_NULL_POINTER;
+  if (tokens < 0 || tokens > (int64_t{1} << 29)) return PARROT_ERR_BAD_SHAPE;
+  if (experts < 2 || experts > kMaxExperts) return PARROT_ERR_UNSUPPORTED;
+  if (dim <= 0 || dim % 32) return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(router_weight)) return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_route(static_cast<const uint16_t*>(x),
+                                     static_cast<const uint16_t*>(router_weight), nullptr,
+                                     logit_bias, tokens, dim, experts, nullptr, nullptr,
+                                     out_weights, out_indices, nullptr, nullptr,
+                                     as_stream(stream)));
+}
+
 int parrot_route_from_logits_f32(const float* logits, const float* logit_bias, int64_t tokens,
                                  int32_t experts, int32_t capacity, float* out_probs,
                                  float* out_weights, int64_t* out_indices,

@@ -34,10 +34,11 @@ __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
 // expert, a ballot of the lanes holding it gives the stable rank (set bits
 // below the lane, v_mbcnt) and the block's count (popcount).  Writes
 // positions[a] for valid ids and block_counts[block, e] for blocks below
-// n_blocks.
+// n_blocks; with positions == NULL (top-2 only) there is nothing to rank.
 __device__ __forceinline__ void rank_half_waves(int id, int64_t block, int64_t n_blocks,
                                                 int64_t n_assign, int experts,
                                                 int32_t* positions, int32_t* block_counts) {
+  if (positions == nullptr) return;  // uniform: a top-2-only launch
   const int lane = threadIdx.x & (kWave - 1);
   const uint64_t half = lane < 32 ? 0x00000000ffffffffull : 0xffffffff00000000ull;
   int rank = 0, count = 0;

@@ -706,7 +706,7 @@ class MoE(nn.Module):
         if flat.shape[0] <= hip_moe.DECODE_MAX_TOKENS:
             # Decode-sized inputs: the whole layer in two launches.
             return hip_moe.decode_experts(self, flat, addend=addend)[0].view_as(x)
-        routed = hip_moe.route(self, flat, collect_stats=False)
+        routed = hip_moe.route_for_experts(self, flat)
         result = hip_moe.grouped_hip_experts(self, flat, routed.indices, routed.weights,
                                              addend=addend, grouping=routed.grouping)
         return result.view_as(x)
@@ -737,7 +737,7 @@ class MoE(nn.Module):
                 depth.cfg.depth_backend == "hip" and
                 len(sources) < hip_moe.MAX_DEPTH_SOURCES):
             if routed is None:
-                routed = hip_moe.route(self, flat, collect_stats=False)
+                routed = hip_moe.route_for_experts(self, flat)
             result, mixed = hip_moe.grouped_hip_experts(
                 self, flat, routed.indices, routed.weights, addend=addend,
                 grouping=routed.grouping, then_mix=(depth, sources, output_norm))

@@ -29,15 +29,15 @@ from oracle import routing
 
 class RouteRecorder:
     """Records the top-2 indices of every HIP MoE layer in execution order,
-    whichever entry computed them (route, the routing depth mix, or the fused
-    decode MoE)."""
+    whichever entry computed them (route, route_top2, the routing depth mix,
+    or the fused decode MoE)."""
 
     def __init__(self, monkeypatch):
         from parrot import hip_moe
         self.indices: list[np.ndarray] = []
         self.active = True
-        route, mix_route, decode = (hip_moe.route, hip_moe.depth_mix_norm_route,
-                                    hip_moe.decode_experts)
+        route, top2, mix_route, decode = (hip_moe.route, hip_moe.route_top2,
+                                          hip_moe.depth_mix_norm_route, hip_moe.decode_experts)
 
         def rec(ix):
             if self.active:  # copying to the host synchronises: never under capture
@@ -45,6 +45,11 @@ class RouteRecorder:
 
         def route_rec(*a, **k):
             r = route(*a, **k)
+            rec(r.indices)
+            return r
+
+        def top2_rec(*a, **k):
+            r = top2(*a, **k)
             rec(r.indices)
             return r
 
@@ -59,6 +64,7 @@ class RouteRecorder:
             return out
 
         monkeypatch.setattr(hip_moe, "route", route_rec)
+        monkeypatch.setattr(hip_moe, "route_top2", top2_rec)
         monkeypatch.setattr(hip_moe, "depth_mix_norm_route", mix_route_rec)
         monkeypatch.setattr(hip_moe, "decode_experts", decode_rec)
 

@@ -133,3 +133,20 @@ def test_wide_route_matches_split_k_chunks(experts):
     assert torch.equal(wide.logits, torch.cat([p.logits for p in parts]))
     assert torch.equal(wide.indices, torch.cat([p.indices for p in parts]))
     assert torch.equal(wide.weights, torch.cat([p.weights for p in parts]))
+
+
+@pytest.mark.parametrize("tokens,experts,skewed", [(256, 32, False), (4096, 32, True),
+                                                   (513, 16, False), (32800, 16, False)])
+def test_route_top2_matches_route(tokens, experts, skewed):
+    """The top-2-only entry gives route()'s weights and indices bit for bit."""
+    from parrot import hip_moe
+    _say(f"route_top2 T={tokens} E={experts} skew={skewed}")
+    module = moe_module(experts, seed=2)
+    x = inputs(tokens, seed=2)
+    bias = skew_bias(experts) if skewed else None
+    with torch.no_grad():
+        full = hip_moe.route(module, x, collect_stats=False, logit_bias=bias)
+        top2 = hip_moe.route_top2(module, x, logit_bias=bias)
+    assert top2.grouping is None
+    assert torch.equal(full.indices, top2.indices)
+    assert torch.equal(full.weights, top2.weights)
