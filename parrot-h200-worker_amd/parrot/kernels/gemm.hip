@@ -51,7 +51,30 @@ struct GemmArgs {
   int32_t* offsets_out;
   int32_t* sorted_out;
   const int32_t* sorted;
+  // Tile order (streaming kernel): 0 = the grid's own (XCD x gets column tile
+  // x of every row tile), 1 = row-major per XCD (every column tile of row
+  // tiles x, x + 8, ...); see xcd_tile.
+  int rows_per_xcd;
 };
+
+// (row tile, column tile) of this workgroup.  Workgroups are dispatched
+// round-robin over the 8 XCDs by linear id; with `rows_per_xcd` the workgroups
+// of XCD x take row tiles x, x + 8, ... with all their column tiles in turn
+// (the grid's row count is then a multiple of 8), so an XCD's L2 holds a few
+// row tiles' A rows and the weights of their experts, instead of every row
+// tile's A rows and one column tile of every expert's weights.
+struct TileIndex {
+  int m, n;
+};
+
+__device__ __forceinline__ TileIndex xcd_tile(bool rows_per_xcd) {
+  if (!rows_per_xcd) return TileIndex{static_cast<int>(blockIdx.y), static_cast<int>(blockIdx.x)};
+  const int nx = static_cast<int>(gridDim.x);
+  const int id = static_cast<int>(blockIdx.y) * nx + static_cast<int>(blockIdx.x);
+  const int pos = id >> 3;
+  const int q = pos / nx;
+  return TileIndex{q * 8 + (id & 7), pos - q * nx};
+}
 
 // The row tile a workgroup owns: segment `seg` (E = the shared expert),
 // M-tile `mt` of its `rows` rows; the segment's hidden rows start at `hbase`
@@ -159,12 +182,12 @@ struct GroupIds {
 template <int BM>
 __device__ __forceinline__ bool group_find(const GemmArgs& p, int T, Tile& t, GroupIds& g,
                                            int* row_src, int* row_dst,
-                                           int (*hist_s)[kMaxExperts]) {
+                                           int (*hist_s)[kMaxExperts], TileIndex ti) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int shared_tiles = (T + BM - 1) / BM;
-  int m = static_cast<int>(blockIdx.y);
+  int m = ti.m;
   if (m < shared_tiles) {
     t = Tile{p.experts, m, T, 2 * T, 0};
     return true;
@@ -199,7 +222,7 @@ __device__ __forceinline__ bool group_find(const GemmArgs& p, int T, Tile& t, Gr
   const int h_end = scan32(count);
   const int o_end = scan32(ovf);
   m -= shared_tiles;
-  if (blockIdx.x == 0 && m == 0 && wave == 0) {
+  if (ti.n == 0 && m == 0 && wave == 0) {
     const int h_total = __builtin_amdgcn_readlane(h_end, E - 1);
     const int o_total = __builtin_amdgcn_readlane(o_end, E - 1);
     if (lane < E) {
@@ -224,7 +247,7 @@ __device__ __forceinline__ bool group_find(const GemmArgs& p, int T, Tile& t, Gr
 template <int BM>
 __device__ __forceinline__ void group_rows(const GemmArgs& p, int T, const Tile& t,
                                            const GroupIds& g, int* row_src, int* row_dst,
-                                           int* chunk_s) {
+                                           int* chunk_s, bool first_column) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nchunks = (2 * T + kWave - 1) / kWave;
@@ -253,7 +276,7 @@ __device__ __forceinline__ void group_rows(const GemmArgs& p, int T, const Tile&
         const int a = c * kWave + lane;
         row_src[r] = a >> 1;
         row_dst[r] = t.hbase + rank;
-        if (blockIdx.x == 0) p.sorted_out[t.hbase + rank] = a;
+        if (first_column) p.sorted_out[t.hbase + rank] = a;
       }
     }
   }
@@ -831,18 +854,19 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
 
   // Phase 1 groups in-kernel when given the top-2 ids (uniform per launch).
   const bool self_grouped = PHASE == 1 && p.indices != nullptr;
+  const TileIndex ti = xcd_tile(p.rows_per_xcd != 0);
   Tile t;
   GroupIds gids;
   if (self_grouped) {
-    if (!group_find<BM>(p, T, t, gids, row_src, row_dst, hist_s)) return;
-  } else if (!find_tile<BM>(p, T, t)) {
+    if (!group_find<BM>(p, T, t, gids, row_src, row_dst, hist_s, ti)) return;
+  } else if (!find_tile<BM>(p, T, t, ti.m)) {
     return;
   }
   t = uniform_tile(t);
   const bool shared = t.seg == p.experts;
   const int N = PHASE == 1 ? 2 * (shared ? p.shared_dim : p.hidden_dim) : p.dim;
   const int K = PHASE == 1 ? p.dim : (shared ? p.shared_dim : p.hidden_dim);
-  const int n0 = static_cast<int>(blockIdx.x) * BN;
+  const int n0 = ti.n * BN;
   if (n0 >= N) return;
 
   const int chunks = K / 8 / KCH;                 // 16-byte chunks per A row (per k chunk)
@@ -880,7 +904,7 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
       bq[i][j] = buffer_load16(b_rsrc, b_off[j], static_cast<uint32_t>(min(i, ksteps - 1)) * 1024);
 
   // ---- per-row source / destination (the weight loads are in flight) -------
-  if (self_grouped && !shared) group_rows<BM>(p, T, t, gids, row_src, row_dst, chunk_s);
+  if (self_grouped && !shared) group_rows<BM>(p, T, t, gids, row_src, row_dst, chunk_s, ti.n == 0);
   if (PHASE == 1) {
     if (tid < BM && (shared || !self_grouped)) {
       row_src[tid] = shared ? sc : asg >> 1;
@@ -1054,7 +1078,8 @@ template <int BM, int WN, int PF, int KCH>
 hipError_t launch_stream(int phase, const GemmArgs& args, int n_max, hipStream_t s) {
   const int T = static_cast<int>(args.tokens);
   const int m_tiles = (T + BM - 1) / BM + (2 * T) / BM + args.experts;
-  const dim3 grid((n_max + 4 * WN - 1) / (4 * WN), m_tiles);
+  const dim3 grid((n_max + 4 * WN - 1) / (4 * WN),
+                  args.rows_per_xcd ? (m_tiles + 7) / 8 * 8 : m_tiles);
   if (phase == 1) grouped_gemm_stream_kernel<BM, 32, PF, 1, KCH><<<grid, 256, 0, s>>>(args);
   else grouped_gemm_stream_kernel<BM, WN, PF, 2, KCH><<<grid, 256, 0, s>>>(args);
   return hipGetLastError();
@@ -1147,6 +1172,20 @@ TilePlan experts_tile_plan(int phase, int64_t tokens, int experts) {
   return per_expert < wide_from ? TilePlan::kStream64 : TilePlan::kWide128;
 }
 
+// Streaming-kernel tile order for gate/up: row-major per XCD once the
+// gathered A rows (x) pass kXcdRowsABytes -- the grid's own order has every
+// XCD read all of A, one column tile of weights at a time.  Measured on
+// MI355X: config 3 (A 6.3 MB) gate/up 41.2 -> 32.6 us and E = 16 T = 2048
+// (3.1 MB) 24.8 -> 23.0 us row-major; config 2 (0.4 MB) 11.9 -> 13.1 us and
+// T = 512 (0.8 MB) 10.2 -> 14.0 us, where every XCD's L2 holds all of A and
+// one column tile of every expert, the grid order wins.  Down (A = the
+// hidden rows) measured no better row-major and keeps the grid order.
+constexpr int64_t kXcdRowsABytes = int64_t{2} << 20;
+
+int stream_rows_per_xcd(int phase, int64_t tokens, int dim, int, int, int) {
+  return phase == 1 && tokens * dim * 2 > kXcdRowsABytes ? 1 : 0;
+}
+
 }  // namespace
 
 bool experts_group_in_kernel(int64_t tokens, int dim, int experts, int hidden_dim,
@@ -1179,6 +1218,7 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
   args.y_routed = y_routed;
   args.y_shared = y_shared;
   args.sorted = phase == 2 ? map.sorted : nullptr;
+  args.rows_per_xcd = stream_rows_per_xcd(phase, tokens, dim, experts, hidden_dim, shared_dim);
   if (phase == 1 && map.indices != nullptr) {
     if (!experts_group_in_kernel(tokens, dim, experts, hidden_dim, shared_dim))
       return hipErrorInvalidValue;
