@@ -292,10 +292,13 @@ size_t parrot_vocab_argmax_workspace_bytes(int64_t rows, int32_t vocab);
  * Replaces argmax(F.linear(h, embedding.weight)) of decode_next
  * (parrot/model.py:714-715, 922, 927-931) and the Metal kernels
  * vocab_argmax_partials_bf16 / vocab_argmax_reduce_bf16
- * (parrot/kernels/moe_bf16.metal:1541-1621). */
+ * (parrot/kernels/moe_bf16.metal:1541-1621).
+ * advance_position (optional, int32 on the device): incremented by one
+ * after the argmax -- the decode step's position counter, advanced by the
+ * step's last launch instead of a launch of its own. */
 int parrot_vocab_argmax_bf16(const void* hidden, int64_t rows, int32_t dim, const void* weight,
-                             int32_t vocab, int64_t* out_tokens, void* workspace,
-                             size_t workspace_bytes, void* stream);
+                             int32_t vocab, int64_t* out_tokens, int32_t* advance_position,
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* Causal attention with an optional sliding window, for prefill and full
  * forwards: out[b, i, h, :] = softmax_j(q[b,h,i] . k[b,h',j] * scale)

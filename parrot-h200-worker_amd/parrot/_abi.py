@@ -56,7 +56,7 @@ SIGNATURES: dict[str, tuple] = {
     "parrot_proj_rope_qkv_bf16": (
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),
-    "parrot_vocab_argmax_bf16": (ctypes.c_int, [_p, _i64, _i32, _p, _i32, _p, _p, _sz, _p]),
+    "parrot_vocab_argmax_bf16": (ctypes.c_int, [_p, _i64, _i32, _p, _i32, _p, _p, _p, _sz, _p]),
     "parrot_decode_moe_bf16": (
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),

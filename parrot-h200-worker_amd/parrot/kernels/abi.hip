@@ -751,8 +751,8 @@ size_t parrot_vocab_argmax_workspace_bytes(int64_t rows, int32_t vocab) {
 }
 
 int parrot_vocab_argmax_bf16(const void* hidden, int64_t rows, int32_t dim, const void* weight,
-                             int32_t vocab, int64_t* out_tokens, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+                             int32_t vocab, int64_t* out_tokens, int32_t* advance_position,
+                             void* workspace, size_t workspace_bytes, void* stream) {
   if (!hidden || !weight || !out_tokens) return PARROT_ERR_NULL_POINTER;
   if (rows < 0 || dim <= 0 || vocab <= 0) return PARROT_ERR_BAD_SHAPE;
   if (rows > parrot::vocab_argmax_max_rows() || dim % 8 || dim > 2048)
@@ -767,7 +767,7 @@ int parrot_vocab_argmax_bf16(const void* hidden, int64_t rows, int32_t dim, cons
                                                round_up(n * sizeof(float)));
   return status(parrot::launch_vocab_argmax(
       static_cast<const uint16_t*>(hidden), static_cast<int>(rows), dim,
-      static_cast<const uint16_t*>(weight), vocab, part_v, part_i, out_tokens,
+      static_cast<const uint16_t*>(weight), vocab, part_v, part_i, out_tokens, advance_position,
       as_stream(stream)));
 }
 

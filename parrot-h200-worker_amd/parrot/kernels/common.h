@@ -419,7 +419,7 @@ hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens
 int vocab_argmax_max_rows();
 int vocab_argmax_groups(int vocab);
 hipError_t launch_vocab_argmax(const uint16_t* h, int rows, int dim, const uint16_t* w, int vocab,
-                               float* part_v, int32_t* part_i, int64_t* out, hipStream_t s);
+                               float* part_v, int32_t* part_i, int64_t* out, int32_t* advance, hipStream_t s);
 
 // Causal / sliding-window attention (see attention.hip).  Strides are in
 // elements: [batch, head, row] for q and k (unit stride along head_dim),

@@ -60,6 +60,8 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return r;
 }
 
+constexpr int kVPre = 8;  // value rows per thread loaded at kernel entry
+
 // CH = head_dim / 8 16-byte chunks per key / value row.
 template <typename QT, typename OT, int CH>
 __global__ __launch_bounds__(256) void decode_attention_kernel(
@@ -91,6 +93,29 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   const uint16_t* kc = k_cache + kv_index * max_pos * D;
   const uint16_t* vc = v_cache + kv_index * max_pos * D;
 
+  // The first pass of key rows (key lo + tid) and the first kVPre value rows
+  // of this thread's (slot, chunk) are loaded here, together with the query:
+  // none of them depends on another, so the scores and the value pass do not
+  // each wait for a memory round trip of their own.
+  auto key_row = [&](int key) -> const uint4* {
+    return reinterpret_cast<const uint4*>(key == pos ? kn : kc + static_cast<int64_t>(key) * D);
+  };
+  auto value_row = [&](int key) -> const uint4* {
+    return reinterpret_cast<const uint4*>(key == pos ? vn : vc + static_cast<int64_t>(key) * D);
+  };
+  uint4 kr0[CH];
+  {
+    const uint4* row = key_row(lo + min(tid, L - 1));
+#pragma unroll
+    for (int c = 0; c < CH; ++c) kr0[c] = row[c];
+  }
+  const int chunk = tid % CH;
+  const int slot = tid / CH;
+  uint4 vpre[kVPre];
+#pragma unroll
+  for (int u = 0; u < kVPre; ++u)
+    vpre[u] = value_row(lo + min(slot + u * kSlots, L - 1))[chunk];
+
   // The first head of each kv group stores the new key / value row.
   if (h % rep == 0) {
     for (int i = tid; i < D; i += 256) {
@@ -101,15 +126,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   for (int i = tid; i < D; i += 256) qs[i] = to_f32(q[(static_cast<int64_t>(b) * heads + h) * D + i]);
   __syncthreads();
 
-  // Scores: one key per thread per pass, every chunk of its row in flight.
-  float mx = -INFINITY;
-  for (int j = tid; j < L; j += 256) {
-    const int key = lo + j;
-    const uint4* row = reinterpret_cast<const uint4*>(
-        key == pos ? kn : kc + static_cast<int64_t>(key) * D);
-    uint4 kr[CH];
-#pragma unroll
-    for (int c = 0; c < CH; ++c) kr[c] = row[c];
+  auto score = [&](const uint4 (&kr)[CH]) -> float {
     float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -118,7 +135,22 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
              hi_bf16(kr[c].y) * qc[3] + lo_bf16(kr[c].z) * qc[4] + hi_bf16(kr[c].z) * qc[5] +
              lo_bf16(kr[c].w) * qc[6] + hi_bf16(kr[c].w) * qc[7];
     }
-    acc *= scale;
+    return acc * scale;
+  };
+
+  // Scores: one key per thread per pass, every chunk of its row in flight.
+  float mx = -INFINITY;
+  if (tid < L) {
+    const float acc = score(kr0);
+    s[tid] = acc;
+    mx = acc;
+  }
+  for (int j = tid + 256; j < L; j += 256) {
+    const uint4* row = key_row(lo + j);
+    uint4 kr[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) kr[c] = row[c];
+    const float acc = score(kr);
     s[j] = acc;
     mx = fmaxf(mx, acc);
   }
@@ -132,34 +164,38 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   sum = block_sum(sum, red);  // also orders the probability writes before the reads below
 
   // Values: thread = (key slot, 16-byte chunk); slot k takes keys k,
-  // k + kSlots, ..., four rows in flight at a time.  Partials per slot are
-  // added in slot order below.
-  const int chunk = tid % CH;
-  const int slot = tid / CH;
+  // k + kSlots, ...: the first kVPre from the rows loaded at entry, then
+  // four rows in flight at a time.  Partials per slot are added in slot
+  // order below.
   float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  auto accumulate = [&](const uint4& vr, float p) {
+    a[0] += p * lo_bf16(vr.x);
+    a[1] += p * hi_bf16(vr.x);
+    a[2] += p * lo_bf16(vr.y);
+    a[3] += p * hi_bf16(vr.y);
+    a[4] += p * lo_bf16(vr.z);
+    a[5] += p * hi_bf16(vr.z);
+    a[6] += p * lo_bf16(vr.w);
+    a[7] += p * hi_bf16(vr.w);
+  };
   if (slot < kSlots) {
-    for (int j0 = slot; j0 < L; j0 += 4 * kSlots) {
+#pragma unroll
+    for (int u = 0; u < kVPre; ++u) {
+      const int j = slot + u * kSlots;
+      accumulate(vpre[u], j < L ? s[min(j, L - 1)] : 0.0f);
+    }
+    for (int j0 = slot + kVPre * kSlots; j0 < L; j0 += 4 * kSlots) {
       uint4 vr[4];
       float p[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int j = min(j0 + u * kSlots, L - 1);
         const int key = lo + j;
-        vr[u] = reinterpret_cast<const uint4*>(
-            key == pos ? vn : vc + static_cast<int64_t>(key) * D)[chunk];
+        vr[u] = value_row(key)[chunk];
         p[u] = j0 + u * kSlots < L ? s[j] : 0.0f;
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        a[0] += p[u] * lo_bf16(vr[u].x);
-        a[1] += p[u] * hi_bf16(vr[u].x);
-        a[2] += p[u] * lo_bf16(vr[u].y);
-        a[3] += p[u] * hi_bf16(vr[u].y);
-        a[4] += p[u] * lo_bf16(vr[u].z);
-        a[5] += p[u] * hi_bf16(vr[u].z);
-        a[6] += p[u] * lo_bf16(vr[u].w);
-        a[7] += p[u] * hi_bf16(vr[u].w);
-      }
+      for (int u = 0; u < 4; ++u) accumulate(vr[u], p[u]);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) part[slot * D + chunk * 8 + i] = a[i];

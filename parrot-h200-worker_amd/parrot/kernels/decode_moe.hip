@@ -38,6 +38,20 @@ namespace {
 
 constexpr int kDecodeMaxTokens = 16;
 
+// LDS layout of decode_up_kernel: the token row (dim bf16, 16-byte aligned),
+// then the router weights (experts x dim bf16, padded to whole 1 KB groups).
+// The router weights are staged only up to kRouterLdsBudget bytes (E = 32 at
+// dim 768); past it the router reads them from memory as before.
+constexpr size_t kRouterLdsBudget = 48 * 1024;
+__host__ __device__ __forceinline__ int router_lds_offset(int dim) { return (dim + 7) / 8 * 8; }
+__host__ __device__ __forceinline__ bool router_in_lds(int dim, int experts) {
+  return static_cast<size_t>(experts) * dim * sizeof(uint16_t) <= kRouterLdsBudget;
+}
+__host__ __device__ __forceinline__ size_t decode_up_lds_bytes(int dim, int experts) {
+  const size_t chunks = router_in_lds(dim, experts) ? static_cast<size_t>(experts) * dim / 8 : 0;
+  return (router_lds_offset(dim) + (chunks + kWave - 1) / kWave * kWave * 8) * sizeof(uint16_t);
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
 
 __device__ __forceinline__ float dot8(uint4 a, uint4 b) {
@@ -107,7 +121,9 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   __shared__ float sel_w[2];
   __shared__ float part[4][4][32];  // [wave][k chunk][gate 16 | up 16]
   __shared__ DepthMixLds mix_lds;
-  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // the slot's token row [dim]
+  // The slot's token row [dim], then (routed slots) the router weights
+  // [experts, dim] at element offset xs_elems.
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -117,6 +133,20 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   const int H = shared ? shared_dim : hidden_dim;
   if (slice * 16 >= H) return;  // uniform
   const int t0 = shared ? slot - 2 * tokens : slot >> 1;  // the slot's token
+  const bool staged = router_in_lds(dim, experts);  // uniform
+  uint16_t* wr_s = xs + router_lds_offset(dim);
+  if (!shared && staged) {
+    // Router weights straight into LDS (16 bytes per lane, a wavefront's
+    // 64 lanes fill 1 KB), issued before the input mix so they arrive with
+    // its sources instead of after it; lanes past the end reread the last
+    // chunk into the region's padding.
+    const int chunks = experts * dim / 8;
+    for (int g = wave; g * kWave < chunks; g += 4) {
+      const int c = min(g * kWave + lane, chunks - 1);
+      __builtin_amdgcn_global_load_lds(wr + static_cast<int64_t>(c) * 8,
+                                       (lds_void_t*)(wr_s + g * kWave * 8), 16, 0, 0);
+    }
+  }
   if (mix.n_sources > 0) {
     // The token's input row: depth mix + RMSNorm of its sources into LDS,
     // every load issued before the first wait (lanes past the row read
@@ -154,10 +184,12 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
     __syncthreads();
     w = shared_gate_up;
   } else {
-    // The router reads the row from LDS once it is mixed there.
-    if (mix.n_sources > 0) __syncthreads();
-    route_token(mix.n_sources > 0 ? xs : x + static_cast<int64_t>(t0) * dim, wr, bias, dim,
-                experts, lg, sel, sel_w);
+    // The router reads the row from LDS once it is mixed there, and its
+    // weights from LDS once their direct-to-LDS loads have landed.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    route_token(mix.n_sources > 0 ? xs : x + static_cast<int64_t>(t0) * dim,
+                staged ? wr_s : wr, bias, dim, experts, lg, sel, sel_w);
     const int k = slot & 1;
     if (slice == 0 && k == 0 && tid < 2) {
       indices[2 * t0 + tid] = sel[tid];
@@ -291,9 +323,8 @@ hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens
                              float* weights, uint16_t* hidden, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
   const int hstride = hidden_dim > shared_dim ? hidden_dim : shared_dim;
-  const size_t x_lds = static_cast<size_t>(dim) * sizeof(uint16_t);  // one row per slot
   const DecodeMix none{};
-  decode_up_kernel<<<dim3(hstride / 16, 3 * tokens), 256, x_lds, s>>>(
+  decode_up_kernel<<<dim3(hstride / 16, 3 * tokens), 256, decode_up_lds_bytes(dim, experts), s>>>(
       x, mix != nullptr ? *mix : none, router_w, bias, tokens, dim, experts, hidden_dim,
       shared_dim, hstride, w.gate_up, w.shared_gate_up, hidden, indices, weights);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;

@@ -119,7 +119,7 @@ __device__ __forceinline__ void keep_better(float pv, int pi, float& v, int& i) 
 
 __global__ __launch_bounds__(256) void vocab_argmax_reduce_kernel(
     const float* __restrict__ part_v, const int32_t* __restrict__ part_i, int groups,
-    int64_t* __restrict__ out) {
+    int64_t* __restrict__ out, int32_t* __restrict__ advance) {
   __shared__ float vs[4];
   __shared__ int is[4];
   const int r = blockIdx.x;
@@ -161,6 +161,9 @@ __global__ __launch_bounds__(256) void vocab_argmax_reduce_kernel(
 #pragma unroll
     for (int w = 1; w < 4; ++w) keep_better(vs[w], is[w], v, i);
     out[r] = i;
+    // The decode step's last launch: it advances the device position the
+    // step's attention kernels read (no kernel of this launch reads it).
+    if (r == 0 && advance != nullptr) *advance += 1;
   }
 }
 
@@ -174,7 +177,8 @@ int vocab_argmax_groups(int vocab) {
 }
 
 hipError_t launch_vocab_argmax(const uint16_t* h, int rows, int dim, const uint16_t* w, int vocab,
-                               float* part_v, int32_t* part_i, int64_t* out, hipStream_t s) {
+                               float* part_v, int32_t* part_i, int64_t* out, int32_t* advance,
+                               hipStream_t s) {
   if (rows == 0) return hipSuccess;
   const int blocks = (vocab + kVocabRowsPerGroup - 1) / kVocabRowsPerGroup;
   const size_t lds = static_cast<size_t>(rows) * dim * sizeof(uint16_t);
@@ -200,7 +204,8 @@ hipError_t launch_vocab_argmax(const uint16_t* h, int rows, int dim, const uint1
 #undef PARROT_VOCAB_RB
 #undef PARROT_VOCAB
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-  vocab_argmax_reduce_kernel<<<rows, 256, 0, s>>>(part_v, part_i, vocab_argmax_groups(vocab), out);
+  vocab_argmax_reduce_kernel<<<rows, 256, 0, s>>>(part_v, part_i, vocab_argmax_groups(vocab), out,
+                                                  advance);
   return hipGetLastError();
 }
 

@@ -1093,16 +1093,19 @@ class Parrot(nn.Module):
             h = self.depth_mix[-1].normalized(stream.sources(), self.final_norm)
         else:
             h = self.final_norm(x)
+        advanced = False
         if _next_token_only and state.position_device is not None and h.shape[0] <= 16:
             # Greedy token straight from fp32 logits, never materialised
-            # (cf. vocab_argmax_partials/reduce_bf16, moe_bf16.metal:1541-1621).
+            # (cf. vocab_argmax_partials/reduce_bf16, moe_bf16.metal:1541-1621);
+            # the same launch advances the device position.
             from . import hip_moe
-            output = hip_moe.vocab_argmax(h, self.embedding.weight)
+            output = hip_moe.vocab_argmax(h, self.embedding.weight, advance=state.position_device)
+            advanced = True
         else:
             logits = self._head(h)
             output = logits.argmax(-1) if _next_token_only else logits
         state.position += 1
-        if state.position_device is not None:
+        if state.position_device is not None and not advanced:
             state.position_device.add_(1)
         return output, state
 

@@ -331,3 +331,37 @@ def test_vocab_argmax(rows, vocab, dim):
     assert got[0].item() == 11
     clear = (top2.values[:, 0] - top2.values[:, 1]) > 1e-4
     assert torch.equal(got[clear], ref[clear])
+
+
+def test_vocab_argmax_advances_the_position():
+    """The argmax launch increments the device position counter once (the
+    decode step's last launch advances it) and picks the same tokens."""
+    from parrot import hip_moe
+    gen = torch.Generator().manual_seed(11)
+    h = torch.randn(3, 768, generator=gen).bfloat16().cuda()
+    w = (torch.randn(32768, 768, generator=gen) * 0.02).bfloat16().cuda()
+    pos = torch.full((1,), 41, dtype=torch.int32, device="cuda")
+    with torch.no_grad():
+        plain = hip_moe.vocab_argmax(h, w)
+        with_advance = hip_moe.vocab_argmax(h, w, advance=pos)
+    assert torch.equal(plain, with_advance)
+    assert int(pos.item()) == 42
+
+
+@pytest.mark.parametrize("dim,experts", [(2048, 32), (64, 3)])
+def test_decode_moe_router_weights_in_memory_or_lds(dim, experts):
+    """dim 2048 at E = 32 (128 KB of router weights, read from memory) and
+    dim 64 at E = 3 (staged in LDS, a partial 1 KB group): the decode MoE
+    against the fp32 oracle on its own routing."""
+    from moe_cases import MAX_ABS, MEAN_ABS, error_stats, inputs, moe_module, oracle_moe
+    from parrot import hip_moe
+    _say(f"decode moe dim={dim} E={experts}")
+    module = moe_module(experts, seed=13, dim=dim)
+    x = inputs(3, seed=13, dim=dim)
+    with torch.no_grad():
+        out, idx, w = hip_moe.decode_experts(module, x)
+        full = hip_moe.route(module, x, collect_stats=False)
+    ref, _, _, _ = oracle_moe(module, x, indices=idx.cpu().numpy(), weights=w.cpu().numpy())
+    mx, mean = error_stats(out, ref)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS
+    assert torch.equal(full.indices, idx)
