@@ -24,8 +24,12 @@ class DecodeGraph:
     ``[batch, 1, vocab]`` with ``logits=True``), exactly as
     ``model.decode_next`` / ``model.decode_step`` would on the same state.
     The returned tensor is the graph's static output, overwritten by the next
-    step.  Both run in inference mode, as ``prefill`` / ``decode_step`` do.  The state must stay with this object: eager decode steps on it in
-    between are allowed (they advance both positions consistently).
+    step; for greedy tokens it is the graph's input buffer itself (the step's
+    last launch writes the tokens there), so feeding it back to ``step``
+    costs no copy.  Both run in inference mode, as ``prefill`` /
+    ``decode_step`` do.  The state must stay with this object: eager decode
+    steps on it in between are allowed (they advance both positions
+    consistently).
     """
 
     @torch.inference_mode()
@@ -55,7 +59,13 @@ class DecodeGraph:
         self._rewind(start)
 
     def _run(self) -> Tensor:
-        out, _ = self.model.decode_step(self.ids, self.state, _next_token_only=not self.logits)
+        if self.logits:
+            out, _ = self.model.decode_step(self.ids, self.state)
+        else:
+            # The tokens land in the input buffer, read by the next replay's
+            # first launch (the embedding gather), after this step's reads.
+            out, _ = self.model.decode_step(self.ids, self.state, _next_token_only=True,
+                                            _out=self.ids)
         return out
 
     def _rewind(self, position: int) -> None:
@@ -68,7 +78,8 @@ class DecodeGraph:
             raise ValueError("decode input must be [cached batch, 1]")
         if self.state.position >= self.model.config.max_seq_len:
             raise ValueError("Generation state has reached max_seq_len")
-        self.ids.copy_(input_ids)
+        if input_ids.data_ptr() != self.ids.data_ptr():
+            self.ids.copy_(input_ids)
         self.graph.replay()
         self.state.position += 1
         return self.out

@@ -500,14 +500,20 @@ def vocab_logits(h: Tensor, weight: Tensor) -> Tensor:
     return out.view(*h.shape[:-1], weight.shape[0])
 
 
-def vocab_argmax(h: Tensor, weight: Tensor, advance: Tensor | None = None) -> Tensor:
+def vocab_argmax(h: Tensor, weight: Tensor, advance: Tensor | None = None,
+                 out: Tensor | None = None) -> Tensor:
     """Greedy tokens argmax(h @ weight^T) over fp32 logits for h [..., dim]
     (at most 16 rows) and the head weight [vocab, dim]; returns int64 ids of
     shape h.shape[:-1] (cf. vocab_argmax_partials/reduce_bf16,
     parrot/kernels/moe_bf16.metal:1541-1621).  ``advance``: an int32 device
-    counter the same launch increments by one (a decode step's position)."""
+    counter the same launch increments by one (a decode step's position).
+    ``out``: a contiguous int64 tensor of one id per row to write them into
+    (a decode graph's input ids, so the next replay reads them in place)."""
     if advance is not None and (advance.dtype != torch.int32 or advance.device != h.device):
         raise RuntimeError("advance must be an int32 tensor on h's device")
+    if out is not None and (out.dtype != torch.int64 or out.device != h.device or
+                            not out.is_contiguous() or out.numel() != h.numel() // h.shape[-1]):
+        raise RuntimeError("out must be a contiguous int64 tensor of one id per row on h's device")
     _require(h, "HIP vocabulary argmax")
     flat = h.reshape(-1, h.shape[-1]).contiguous()
     rows, dim = flat.shape
@@ -517,7 +523,8 @@ def vocab_argmax(h: Tensor, weight: Tensor, advance: Tensor | None = None) -> Te
     lib = _abi.load()
     nbytes = lib.parrot_vocab_argmax_workspace_bytes(16, vocab)
     ws = _scratch(weight, "_hip_vocab_workspace", nbytes, h.device)
-    out = torch.empty(rows, dtype=torch.int64, device=h.device)
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=h.device)
     _abi.check(lib.parrot_vocab_argmax_bf16(ptr(flat), rows, dim, ptr(weight), vocab, ptr(out),
                                             ptr(advance), ptr(ws), nbytes, _stream(h.device)),
                "parrot_vocab_argmax_bf16")

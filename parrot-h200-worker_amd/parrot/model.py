@@ -1046,8 +1046,11 @@ class Parrot(nn.Module):
 
     @torch.inference_mode()
     def decode_step(self, input_ids: Tensor, state: GenerationState, *,
-                    _next_token_only: bool = False) -> tuple[Tensor, GenerationState]:
-        """Append one token per sequence to an existing generation state."""
+                    _next_token_only: bool = False,
+                    _out: Tensor | None = None) -> tuple[Tensor, GenerationState]:
+        """Append one token per sequence to an existing generation state.
+        ``_out`` (with ``_next_token_only``): an int64 [batch, 1] tensor the
+        greedy tokens are written into and returned as."""
         cfg = self.config
         if self.training:
             raise RuntimeError("decode_step requires model.eval()")
@@ -1099,11 +1102,14 @@ class Parrot(nn.Module):
             # (cf. vocab_argmax_partials/reduce_bf16, moe_bf16.metal:1541-1621);
             # the same launch advances the device position.
             from . import hip_moe
-            output = hip_moe.vocab_argmax(h, self.embedding.weight, advance=state.position_device)
+            output = hip_moe.vocab_argmax(h, self.embedding.weight, advance=state.position_device,
+                                          out=_out)
             advanced = True
         else:
             logits = self._head(h)
             output = logits.argmax(-1) if _next_token_only else logits
+            if _next_token_only and _out is not None:
+                output = _out.copy_(output)
         state.position += 1
         if state.position_device is not None and not advanced:
             state.position_device.add_(1)

@@ -163,6 +163,34 @@ def test_decode_graph_matches_eager():
                                        getattr(theirs, name)[:, :, :48])
 
 
+def test_decode_graph_feeds_tokens_back_in_place():
+    """Greedy generation feeds each step's output back: the tokens land in
+    the graph's input buffer (no copy before the next replay), and the steps
+    still equal eager decoding."""
+    from parrot import ModelConfig, Parrot
+    from parrot.decode_graph import DecodeGraph
+    _say("decode graph in-place token feedback")
+    torch.manual_seed(5)
+    model = Parrot(ModelConfig(n_layers=4, moe_backend="grouped_hip", depth_backend="hip",
+                               collect_router_stats=False)).to(device="cuda",
+                                                               dtype=torch.bfloat16).eval()
+    prompt = torch.randint(0, 32768, (1, 24), generator=torch.Generator().manual_seed(5)).cuda()
+    with torch.inference_mode():
+        logits, state = model.prefill(prompt)
+        eager_state = copy.deepcopy(state)
+        e = logits[:, -1].argmax(-1, keepdim=True)
+        graph = DecodeGraph(model, state)
+        a = graph.step(e.clone())
+        assert a.data_ptr() == graph.ids.data_ptr() and a.shape == (1, 1)
+        e, eager_state = model.decode_next(e, eager_state)
+        assert torch.equal(a, e)
+        for step in range(4):
+            a = graph.step(a)
+            e, eager_state = model.decode_next(e, eager_state)
+            assert torch.equal(a, e), step
+        assert int(state.position_device.item()) == eager_state.position == 29
+
+
 @pytest.mark.parametrize("tokens,k,n,with_addend", [(1, 768, 768, True), (3, 768, 768, False),
                                                     (16, 1024, 16, True), (8, 128, 2048, True)])
 def test_decode_linear(tokens, k, n, with_addend):
