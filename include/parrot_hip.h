@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 7
+#define PARROT_ABI_VERSION 8
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -156,6 +156,26 @@ int parrot_decode_attention_bf16(const void* q, const void* k_new, const void* v
                                  int32_t head_dim, int32_t max_positions, int32_t window,
                                  float scale, void* out, void* stream);
 
+/* parrot_decode_attention_bf16 with the output projection of each head
+ * deferred (the reference's defer_sum / PendingResidual, parrot/model.py:
+ * 103-106, 301-316, 868-889, and the per-head output stage of
+ * local_attention_decode_bf16, parrot/kernels/moe_bf16.metal:1203-1362):
+ * instead of the attention output it writes contributions [batch, heads,
+ * dim] fp32, contributions[b, h, n] = sum_i y[b, h, i] * out_weight[n,
+ * h * head_dim + i] over i in order, where y is the head's attention output
+ * rounded to bf16 and out_weight [dim, heads * head_dim] bf16 (16-byte
+ * aligned) is the output projection.  Summed over heads (in head order),
+ * rounded to bf16 and added to the addend they give the attention module's
+ * output; parrot_depth_mix_decode_moe_pending_bf16 does that in its input
+ * mix.  dim % 4 == 0, dim <= 1024; LDS as parrot_decode_attention_bf16 plus
+ * 4 * head_dim bytes; other limits as there. */
+int parrot_decode_attention_heads_bf16(const void* q, const void* k_new, const void* v_new,
+                                       void* key_cache, void* value_cache,
+                                       const int32_t* position, int32_t batch, int32_t heads,
+                                       int32_t kv_heads, int32_t head_dim, int32_t max_positions,
+                                       int32_t window, float scale, const void* out_weight,
+                                       int32_t dim, float* contributions, void* stream);
+
 /* Decode-step attention of the MLA layers over the joint latent cache.
  * q [batch, H, latent_dim] fp32 (the query through the absorbed key
  * up-projection), latent_new [batch, latent_dim] bf16, latent_cache
@@ -277,6 +297,28 @@ int parrot_depth_mix_decode_moe_bf16(
     const void* const* sources, int32_t n_sources, const void* query,
     const void* score_norm_weight, float score_eps, const void* moe_norm_weight,
     float norm_eps, int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
+    int32_t shared_dim, const void* router_weight, const float* logit_bias,
+    const void* packed_gate_up, const void* packed_down, const void* shared_gate_up,
+    const void* shared_down, const void* addend, void* out, int64_t* out_indices,
+    float* out_weights, void* workspace, size_t workspace_bytes, void* stream);
+
+/* parrot_depth_mix_decode_moe_bf16 whose last depth source is pending: row
+ * t of source n_sources - 1 is resolved in the launch as bf16(base[t] +
+ * bf16(sum over lanes l in order of contributions[t, l, :])) (without a
+ * base: the rounded sum), the reference's depth_mix_norm_pending_bf16
+ * (parrot/kernels/moe_bf16.metal:437-560, via metal_depth_mix_norm_pending,
+ * parrot/metal_moe.py:480-500), and written to resolved [tokens, dim]; the
+ * sources entry of that slot is only a placeholder (any valid row block).
+ * contributions [tokens, lanes, dim] fp32 (16-byte aligned), 1 <= lanes <=
+ * 16; base and resolved bf16, 8-byte aligned (base may be NULL).  The
+ * addend may be `resolved` itself: the routed launch that stores it runs
+ * before the one that adds the addend.  Other arguments and limits as
+ * parrot_depth_mix_decode_moe_bf16. */
+int parrot_depth_mix_decode_moe_pending_bf16(
+    const void* const* sources, int32_t n_sources, const void* query,
+    const void* score_norm_weight, float score_eps, const void* moe_norm_weight,
+    float norm_eps, const float* contributions, int32_t lanes, const void* base,
+    void* resolved, int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
     int32_t shared_dim, const void* router_weight, const float* logit_bias,
     const void* packed_gate_up, const void* packed_down, const void* shared_gate_up,
     const void* shared_down, const void* addend, void* out, int64_t* out_indices,

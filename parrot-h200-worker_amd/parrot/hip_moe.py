@@ -438,17 +438,26 @@ DECODE_MAX_TOKENS = 16  # rows the fused decode MoE takes
 
 
 def decode_experts(module: "MoE", flat: Tensor | None, addend: Tensor | None = None,
-                   logit_bias: Tensor | None = None,
-                   mix: tuple | None = None) -> tuple[Tensor, Tensor, Tensor]:
+                   logit_bias: Tensor | None = None, mix: tuple | None = None,
+                   pending: tuple | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """The whole MoE layer for at most DECODE_MAX_TOKENS rows in two launches
     (route + gate/up + SwiGLU, then down + weighted combine): returns
     ``(out, indices [T, 2] int64, weights [T, 2] fp32)`` with ``out`` =
     ``addend + delta`` when an addend is given (cf. metal_experts_decode,
     parrot/metal_moe.py:182-221).  ``mix = (depth_module, sources, norm)``:
     the input rows are ``depth_mix_norm(depth_module, sources, norm)``, made
-    inside the same launches (``flat`` is then None; dim <= 1024)."""
+    inside the same launches (``flat`` is then None; dim <= 1024).
+    ``pending = (contributions [T, lanes, dim] fp32, base [T, 1, dim] or
+    None, resolved [T, 1, dim])`` with ``mix``: the last depth source is a
+    deferred module output (the reference's PendingResidual), resolved in
+    the launch as bf16(base + bf16(sum of the lanes)) into ``resolved``, as
+    metal_depth_mix_norm_pending does (parrot/metal_moe.py:480-500); the
+    sources' last entry is only a placeholder and ``addend`` may be
+    ``resolved``."""
     cfg = module.cfg
     keep = None
+    if pending is not None and mix is None:
+        raise RuntimeError("a pending depth source needs the input mix in the launch")
     if mix is not None:
         mix_args, flat, keep = _decode_mix_args(mix)  # flat: shape, dtype, device of the rows
     _require(flat, "The fused HIP decode MoE")
@@ -480,9 +489,25 @@ def decode_experts(module: "MoE", flat: Tensor | None, addend: Tensor | None = N
             ptr(flat), tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim, *tail),
             "parrot_decode_moe_bf16")
         return out, indices, weights
-    _abi.check(lib.parrot_depth_mix_decode_moe_bf16(
-        *mix_args, tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim, *tail),
-        "parrot_depth_mix_decode_moe_bf16")
+    if pending is None:
+        _abi.check(lib.parrot_depth_mix_decode_moe_bf16(
+            *mix_args, tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim, *tail),
+            "parrot_depth_mix_decode_moe_bf16")
+    else:
+        contributions, base, resolved = pending
+        if (contributions.dtype != torch.float32 or contributions.dim() != 3 or
+                contributions.shape[0] != tokens or contributions.shape[2] != dim or
+                not contributions.is_contiguous() or contributions.device != flat.device):
+            raise RuntimeError("pending contributions must be contiguous fp32 [T, lanes, dim]")
+        for t in (base, resolved):
+            if t is not None and (t.dtype != flat.dtype or t.numel() != tokens * dim or
+                                  not t.is_contiguous() or t.device != flat.device):
+                raise RuntimeError("pending base / resolved rows must be contiguous [T, 1, dim]"
+                                   " in the input dtype")
+        _abi.check(lib.parrot_depth_mix_decode_moe_pending_bf16(
+            *mix_args, ptr(contributions), contributions.shape[1], ptr(base), ptr(resolved),
+            tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim, *tail),
+            "parrot_depth_mix_decode_moe_pending_bf16")
     del keep  # alive until the launch is enqueued (it is)
     return out, indices, weights
 
@@ -857,6 +882,50 @@ def decode_attention(q: Tensor, k_new: Tensor, v_new: Tensor, key_cache: Tensor,
         ptr(q), ptr(k_new), ptr(v_new), ptr(key_cache), ptr(value_cache), ptr(position),
         b, heads, kv_heads, d, max_pos, window, scale, ptr(out), _stream(q.device)),
         "parrot_decode_attention_bf16")
+    return out
+
+
+DEFER_MAX_TOKENS = 2  # rows up to which decode attention defers its output sum
+
+
+def decode_attention_heads_supported(tokens: int, dim: int) -> bool:
+    """Shapes for which a decode step defers the attention output sum
+    (``decode_attention_heads`` + the pending decode MoE mix): at most
+    DEFER_MAX_TOKENS rows, since each head's attention runs in four
+    workgroups (one per quarter of the output columns)."""
+    return 1 <= tokens <= DEFER_MAX_TOKENS and dim % 4 == 0 and dim <= 1024
+
+
+def decode_attention_heads(q: Tensor, k_new: Tensor, v_new: Tensor, key_cache: Tensor,
+                           value_cache: Tensor, position: Tensor, window: int, scale: float,
+                           out_weight: Tensor) -> Tensor:
+    """``decode_attention`` with the output projection deferred per head (the
+    reference's defer_sum, parrot/model.py:301-316): returns contributions
+    [b, H, dim] fp32, contributions[b, h] = y_bf16[b, h] @ out_weight[:, h d :
+    h d + d]^T.  Their sum over heads, rounded to bf16 and added to the
+    addend, is the attention module's output; ``decode_experts(...,
+    pending=...)`` resolves it inside its input mix."""
+    _require(q, "HIP decode attention")
+    b, heads, t, d = q.shape
+    _, kv_heads, max_pos, _ = key_cache.shape
+    if t != 1 or k_new.shape != (b, kv_heads, 1, d) or v_new.shape != k_new.shape:
+        raise RuntimeError("decode attention takes one new position per sequence")
+    if key_cache.shape != (b, kv_heads, max_pos, d) or value_cache.shape != key_cache.shape:
+        raise RuntimeError("cache shapes do not match the heads")
+    if not (key_cache.is_contiguous() and value_cache.is_contiguous()):
+        raise RuntimeError("caches must be contiguous")
+    dim = out_weight.shape[0]
+    if (out_weight.dtype != q.dtype or out_weight.shape != (dim, heads * d) or
+            not out_weight.is_contiguous()):
+        raise RuntimeError("output projection must be a contiguous [dim, heads * head_dim] "
+                           "weight of q's dtype")
+    _check_position(position, q.device)
+    q, k_new, v_new = q.contiguous(), k_new.contiguous(), v_new.contiguous()
+    out = torch.empty((b, heads, dim), dtype=torch.float32, device=q.device)
+    _abi.check(_abi.load().parrot_decode_attention_heads_bf16(
+        ptr(q), ptr(k_new), ptr(v_new), ptr(key_cache), ptr(value_cache), ptr(position),
+        b, heads, kv_heads, d, max_pos, window, scale, ptr(out_weight), dim, ptr(out),
+        _stream(q.device)), "parrot_decode_attention_heads_bf16")
     return out
 
 

@@ -231,6 +231,33 @@ int parrot_decode_attention_bf16(const void* q, const void* k_new, const void* v
       max_positions, window, scale, static_cast<uint16_t*>(out), as_stream(stream)));
 }
 
+int parrot_decode_attention_heads_bf16(const void* q, const void* k_new, const void* v_new,
+                                       void* key_cache, void* value_cache,
+                                       const int32_t* position, int32_t batch, int32_t heads,
+                                       int32_t kv_heads, int32_t head_dim, int32_t max_positions,
+                                       int32_t window, float scale, const void* out_weight,
+                                       int32_t dim, float* contributions, void* stream) {
+  if (!q || !k_new || !v_new || !key_cache || !value_cache || !position || !out_weight ||
+      !contributions)
+    return PARROT_ERR_NULL_POINTER;
+  if (int rc = check_decode_shape(batch, heads, kv_heads, head_dim, max_positions, window))
+    return rc;
+  if (dim <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (dim % parrot::kDecodeHeadsQuarters || dim / parrot::kDecodeHeadsQuarters > 256 ||
+      parrot::decode_attention_lds_bytes(window, max_positions, head_dim) +
+              static_cast<size_t>(head_dim) * sizeof(float) > parrot::kMaxDecodeLds)
+    return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(k_new) || !aligned16(v_new) || !aligned16(key_cache) ||
+      !aligned16(value_cache) || !aligned16(out_weight))
+    return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_decode_attention_heads(
+      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_new),
+      static_cast<const uint16_t*>(v_new), static_cast<uint16_t*>(key_cache),
+      static_cast<uint16_t*>(value_cache), position, batch, heads, kv_heads, head_dim,
+      max_positions, window, scale, static_cast<const uint16_t*>(out_weight), dim, contributions,
+      as_stream(stream)));
+}
+
 int parrot_decode_attention_latent_f32(const float* q, const void* latent_new, void* latent_cache,
                                        const int32_t* position, int32_t batch, int32_t heads,
                                        int32_t latent_dim, int32_t max_positions, float scale,
@@ -738,6 +765,35 @@ int parrot_depth_mix_decode_moe_bf16(
                                moe_norm_weight, norm_eps, mix))
     return rc;
   if (dim > 1024) return PARROT_ERR_UNSUPPORTED;
+  return decode_moe_entry(nullptr, &mix, tokens, dim, experts, hidden_dim, shared_dim,
+                          router_weight, logit_bias, packed_gate_up, packed_down,
+                          shared_gate_up, shared_down, addend, out, out_indices, out_weights,
+                          workspace, workspace_bytes, stream);
+}
+
+int parrot_depth_mix_decode_moe_pending_bf16(
+    const void* const* sources, int32_t n_sources, const void* query,
+    const void* score_norm_weight, float score_eps, const void* moe_norm_weight,
+    float norm_eps, const float* contributions, int32_t lanes, const void* base,
+    void* resolved, int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
+    int32_t shared_dim, const void* router_weight, const float* logit_bias,
+    const void* packed_gate_up, const void* packed_down, const void* shared_gate_up,
+    const void* shared_down, const void* addend, void* out, int64_t* out_indices,
+    float* out_weights, void* workspace, size_t workspace_bytes, void* stream) {
+  parrot::DecodeMix mix{};
+  if (int rc = make_decode_mix(sources, n_sources, query, score_norm_weight, score_eps,
+                               moe_norm_weight, norm_eps, mix))
+    return rc;
+  if (!contributions || !resolved) return PARROT_ERR_NULL_POINTER;
+  if (lanes < 1 || lanes > parrot::kMaxPendingLanes || dim > 1024 || dim % 4)
+    return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(contributions) || reinterpret_cast<uintptr_t>(resolved) % 8 ||
+      reinterpret_cast<uintptr_t>(base) % 8)
+    return PARROT_ERR_ALIGNMENT;
+  mix.pend = contributions;
+  mix.pend_lanes = lanes;
+  mix.pend_base = static_cast<const uint16_t*>(base);
+  mix.pend_out = static_cast<uint16_t*>(resolved);
   return decode_moe_entry(nullptr, &mix, tokens, dim, experts, hidden_dim, shared_dim,
                           router_weight, logit_bias, packed_gate_up, packed_down,
                           shared_gate_up, shared_down, addend, out, out_indices, out_weights,

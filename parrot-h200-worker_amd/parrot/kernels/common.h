@@ -360,6 +360,19 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_new,
                                    const int32_t* position, int batch, int heads, int kv_heads,
                                    int head_dim, int max_pos, int window, float scale,
                                    uint16_t* out, hipStream_t s);
+// The deferred form for bf16 queries: per-head contributions of the output
+// projection, contributions [batch, heads, dim] fp32 = the head's output
+// (rounded to bf16) times its [dim, head_dim] slice of out_weight [dim,
+// heads x head_dim]; kDecodeHeadsQuarters workgroups per head split the
+// output columns (dim / kDecodeHeadsQuarters <= 256).  The launch's LDS is
+// decode_attention_lds_bytes + head_dim floats.
+constexpr int kDecodeHeadsQuarters = 4;
+hipError_t launch_decode_attention_heads(const uint16_t* q, const uint16_t* k_new,
+                                         const uint16_t* v_new, uint16_t* k_cache,
+                                         uint16_t* v_cache, const int32_t* position, int batch,
+                                         int heads, int kv_heads, int head_dim, int max_pos,
+                                         int window, float scale, const uint16_t* out_weight,
+                                         int dim, float* contributions, hipStream_t s);
 size_t mla_decode_lds_bytes(int tokens, int k, int elem_bytes);
 hipError_t launch_decode_linear(const uint16_t* x, int tokens, int k, const uint16_t* w, int n,
                                 const uint16_t* addend, uint16_t* out, hipStream_t s);
@@ -376,6 +389,12 @@ hipError_t launch_decode_attention_latent(const float* q, const uint16_t* latent
 int decode_moe_max_tokens();
 // The depth mix + RMSNorm that makes a decode MoE's input row per token
 // (n_sources == 0: the input x is given instead); dim <= 1024.
+//
+// A pending last source (pend != nullptr; decode MoE only) is resolved in
+// the launch, as the reference's depth_mix_norm_pending_bf16: row t of
+// source n_sources - 1 is bf16(base + bf16(sum over lanes l in order of
+// pend[t, l, :])) (just the rounded sum without a base), and the launch
+// writes that row to pend_out [tokens, dim].
 struct DecodeMix {
   DepthSources srcs;
   int n_sources;
@@ -384,7 +403,12 @@ struct DecodeMix {
   float score_eps;
   const uint16_t* out_w;
   float out_eps;
+  const float* pend;          // [tokens, pend_lanes, dim] fp32
+  int pend_lanes;             // 1 .. kMaxPendingLanes
+  const uint16_t* pend_base;  // [tokens, dim] or nullptr
+  uint16_t* pend_out;         // [tokens, dim]
 };
+constexpr int kMaxPendingLanes = 16;
 
 // The decode step's q|k|v projection + RoPE of a local layer (decode_qkv.hip).
 struct DecodeQkvArgs {

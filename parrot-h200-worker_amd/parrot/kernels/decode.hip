@@ -62,17 +62,37 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 
 constexpr int kVPre = 8;  // value rows per thread loaded at kernel entry
 
+// Output-projection operands of decode_attention_kernel with Q > 0: the
+// [dim, heads x head_dim] bf16 weight and the fp32 per-head contributions
+// [batch, heads, dim] it writes.
+struct HeadsOut {
+  const uint16_t* weight;
+  int dim;
+  float* contributions;
+};
+
 // CH = head_dim / 8 16-byte chunks per key / value row.
-template <typename QT, typename OT, int CH>
+//
+// Q = 0: one workgroup per (head, sequence) writes the head's output row.
+// Q > 0 (bf16 query and output, the deferred residual): Q workgroups per
+// (head, sequence) each attend over the window (the same arithmetic, so the
+// same bits) and project the head's bf16-rounded output onto a Q-th of the
+// output width: contributions[b, h, n] = sum_i out[i] * W[n, h D + i] in
+// index order.  Each thread's weight row piece is loaded at entry, so the
+// projection's operands arrive during the attention.  The contributions'
+// sum over heads is left to the consumer (the reference's PendingResidual).
+template <typename QT, typename OT, int CH, int Q>
 __global__ __launch_bounds__(256) void decode_attention_kernel(
     const QT* __restrict__ q, const uint16_t* __restrict__ k_new,
     const uint16_t* __restrict__ v_new, uint16_t* __restrict__ k_cache,
     uint16_t* __restrict__ v_cache, const int32_t* __restrict__ position, int heads,
-    int kv_heads, int max_pos, int window, float scale, OT* __restrict__ out) {
+    int kv_heads, int max_pos, int window, float scale, OT* __restrict__ out, HeadsOut ho) {
   constexpr int D = CH * 8;
   constexpr int kSlots = 256 / CH;  // value pass: key slots x chunks
+  static_assert(D <= 256, "one query element per thread");
   extern __shared__ float smem[];
-  const int h = blockIdx.x;
+  const int h = Q > 0 ? static_cast<int>(blockIdx.x) / Q : static_cast<int>(blockIdx.x);
+  const int quarter = Q > 0 ? static_cast<int>(blockIdx.x) % Q : 0;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int rep = heads / kv_heads;
@@ -82,6 +102,10 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   float* qs = s + lcap;            // [D]
   float* part = qs + D;            // [kSlots][D]
   float* red = part + kSlots * D;  // [4]
+  float* ob = red + 4;             // [D] (Q > 0) the head's rounded output
+
+  // Q > 0: thread t < dim / Q owns output column n = quarter dim / Q + t.
+  const int nq = Q > 0 ? ho.dim / Q : 0;
 
   const int pos = *position;
   if (pos < 0 || pos >= max_pos) return;  // uniform: nothing to attend to
@@ -103,6 +127,12 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   auto value_row = [&](int key) -> const uint4* {
     return reinterpret_cast<const uint4*>(key == pos ? vn : vc + static_cast<int64_t>(key) * D);
   };
+  // This thread's elements of the new key / value rows (stored below) and
+  // of the query (D <= 256), loaded first: their uses then wait for none of
+  // the row loads behind them (loads complete in order).
+  const int ie = min(tid, D - 1);
+  const uint16_t kne = kn[ie], vne = vn[ie];
+  const float qv = to_f32(q[(static_cast<int64_t>(b) * heads + h) * D + ie]);
   uint4 kr0[CH];
   {
     const uint4* row = key_row(lo + min(tid, L - 1));
@@ -116,14 +146,23 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   for (int u = 0; u < kVPre; ++u)
     vpre[u] = value_row(lo + min(slot + u * kSlots, L - 1))[chunk];
 
-  // The first head of each kv group stores the new key / value row.
-  if (h % rep == 0) {
-    for (int i = tid; i < D; i += 256) {
-      k_cache[(kv_index * max_pos + pos) * D + i] = kn[i];
-      if (v_cache != k_cache) v_cache[(kv_index * max_pos + pos) * D + i] = vn[i];
-    }
+  // Q > 0: the D weights W[n, h D .. h D + D) (16-byte aligned) of this
+  // thread's output column, issued after every load the attention waits
+  // for, so they arrive during it.
+  uint4 wo[Q > 0 ? CH : 1];
+  if constexpr (Q > 0) {
+    asm volatile("" ::: "memory");
+    const uint4* wrow = reinterpret_cast<const uint4*>(
+        ho.weight + static_cast<int64_t>(quarter * nq + min(tid, nq - 1)) * heads * D + h * D);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) wo[c] = wrow[c];
   }
-  for (int i = tid; i < D; i += 256) qs[i] = to_f32(q[(static_cast<int64_t>(b) * heads + h) * D + i]);
+  // The first head of each kv group stores the new key / value row.
+  if (h % rep == 0 && quarter == 0 && tid < D) {
+    k_cache[(kv_index * max_pos + pos) * D + tid] = kne;
+    if (v_cache != k_cache) v_cache[(kv_index * max_pos + pos) * D + tid] = vne;
+  }
+  if (tid < D) qs[tid] = qv;
   __syncthreads();
 
   auto score = [&](const uint4 (&kr)[CH]) -> float {
@@ -202,24 +241,47 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   }
   __syncthreads();
   const float inv = 1.0f / sum;
-  for (int i = tid; i < D; i += 256) {
-    float o = 0.0f;
-    for (int k = 0; k < kSlots; ++k) o += part[k * D + i];
-    store_out(out + (static_cast<int64_t>(b) * heads + h) * D + i, o * inv);
+  if constexpr (Q == 0) {
+    for (int i = tid; i < D; i += 256) {
+      float o = 0.0f;
+      for (int k = 0; k < kSlots; ++k) o += part[k * D + i];
+      store_out(out + (static_cast<int64_t>(b) * heads + h) * D + i, o * inv);
+    }
+  } else {
+    // The head's output rounded to bf16, as the output projection of the
+    // undeferred path reads it, then this workgroup's output columns.
+    for (int i = tid; i < D; i += 256) {
+      float o = 0.0f;
+      for (int k = 0; k < kSlots; ++k) o += part[k * D + i];
+      ob[i] = to_f32(f32_to_bf16(o * inv));
+    }
+    __syncthreads();
+    if (tid < nq) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const float* oc = ob + c * 8;
+        acc += lo_bf16(wo[c].x) * oc[0] + hi_bf16(wo[c].x) * oc[1] + lo_bf16(wo[c].y) * oc[2] +
+               hi_bf16(wo[c].y) * oc[3] + lo_bf16(wo[c].z) * oc[4] + hi_bf16(wo[c].z) * oc[5] +
+               lo_bf16(wo[c].w) * oc[6] + hi_bf16(wo[c].w) * oc[7];
+      }
+      ho.contributions[(static_cast<int64_t>(b) * heads + h) * ho.dim + quarter * nq + tid] = acc;
+    }
   }
 }
 
-template <typename QT, typename OT>
+template <typename QT, typename OT, int Q = 0>
 hipError_t launch_decode(const QT* q, const uint16_t* k_new, const uint16_t* v_new,
                          uint16_t* k_cache, uint16_t* v_cache, const int32_t* position, int batch,
                          int heads, int kv_heads, int head_dim, int max_pos, int window,
-                         float scale, OT* out, hipStream_t s) {
-  const size_t lds = decode_attention_lds_bytes(window, max_pos, head_dim);
-  const dim3 grid(heads, batch);
-#define PARROT_DECODE(CH)                                                                      \
-  decode_attention_kernel<QT, OT, CH><<<grid, 256, lds, s>>>(q, k_new, v_new, k_cache, v_cache, \
-                                                              position, heads, kv_heads,       \
-                                                              max_pos, window, scale, out)
+                         float scale, OT* out, hipStream_t s, HeadsOut ho = HeadsOut{}) {
+  const size_t lds = decode_attention_lds_bytes(window, max_pos, head_dim) +
+                     (Q > 0 ? static_cast<size_t>(head_dim) * sizeof(float) : 0);
+  const dim3 grid(heads * (Q > 0 ? Q : 1), batch);
+#define PARROT_DECODE(CH)                                                                   \
+  decode_attention_kernel<QT, OT, CH, Q><<<grid, 256, lds, s>>>(                            \
+      q, k_new, v_new, k_cache, v_cache, position, heads, kv_heads, max_pos, window, scale, \
+      out, ho)
   switch (head_dim / 8) {
     case 1: PARROT_DECODE(1); break;
     case 2: PARROT_DECODE(2); break;
@@ -259,6 +321,20 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_new,
   if (batch == 0) return hipSuccess;
   return launch_decode(q, k_new, v_new, k_cache, v_cache, position, batch, heads, kv_heads,
                        head_dim, max_pos, window, scale, out, s);
+}
+
+hipError_t launch_decode_attention_heads(const uint16_t* q, const uint16_t* k_new,
+                                         const uint16_t* v_new, uint16_t* k_cache,
+                                         uint16_t* v_cache, const int32_t* position, int batch,
+                                         int heads, int kv_heads, int head_dim, int max_pos,
+                                         int window, float scale, const uint16_t* out_weight,
+                                         int dim, float* contributions, hipStream_t s) {
+  if (batch == 0) return hipSuccess;
+  if (dim % kDecodeHeadsQuarters != 0 || dim / kDecodeHeadsQuarters > 256)
+    return hipErrorInvalidValue;
+  return launch_decode<uint16_t, uint16_t, kDecodeHeadsQuarters>(
+      q, k_new, v_new, k_cache, v_cache, position, batch, heads, kv_heads, head_dim, max_pos,
+      window, scale, nullptr, s, HeadsOut{out_weight, dim, contributions});
 }
 
 hipError_t launch_decode_attention_latent(const float* q, const uint16_t* latent_new,

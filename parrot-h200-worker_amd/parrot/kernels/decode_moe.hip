@@ -162,6 +162,43 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
     const uint2 q = reinterpret_cast<const uint2*>(mix.query)[ic];
     const uint2 g = reinterpret_cast<const uint2*>(mix.score_w)[ic];
     const uint2 g_out = reinterpret_cast<const uint2*>(mix.out_w)[ic];
+    if (mix.pend != nullptr) {
+      // The pending last source: this chunk's contributions summed over the
+      // lanes in order (the loads of up to 8 lanes in flight at once),
+      // rounded, then added to the base with a second rounding; the
+      // token's first routed workgroup of slice 0 stores the resolved row.
+      const float4* pc = reinterpret_cast<const float4*>(mix.pend) +
+                         static_cast<int64_t>(t0) * mix.pend_lanes * chunks + ic;
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int l0 = 0; l0 < mix.pend_lanes; l0 += 8) {
+        float4 c[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          c[u] = pc[static_cast<int64_t>(min(l0 + u, mix.pend_lanes - 1)) * chunks];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (l0 + u < mix.pend_lanes) {
+            acc[0] += c[u].x;
+            acc[1] += c[u].y;
+            acc[2] += c[u].z;
+            acc[3] += c[u].w;
+          }
+        }
+      }
+      uint2 r;
+      r.x = pack_bf16x2(acc[0], acc[1]);
+      r.y = pack_bf16x2(acc[2], acc[3]);
+      if (mix.pend_base != nullptr) {
+        const uint2 pb = reinterpret_cast<const uint2*>(mix.pend_base)[base + ic];
+        r.x = pack_bf16x2(lo_bf16(pb.x) + lo_bf16(r.x), hi_bf16(pb.x) + hi_bf16(r.x));
+        r.y = pack_bf16x2(lo_bf16(pb.y) + lo_bf16(r.y), hi_bf16(pb.y) + hi_bf16(r.y));
+      }
+#pragma unroll
+      for (int s = 0; s < kMaxDepthSources; ++s)
+        if (s == mix.n_sources - 1) v[s] = r;
+      if (has && !shared && slice == 0 && (slot & 1) == 0)
+        reinterpret_cast<uint2*>(mix.pend_out)[base + ic] = r;
+    }
 #pragma unroll
     for (int s = 0; s < kMaxDepthSources; ++s)
       if (!has || s >= mix.n_sources) v[s] = make_uint2(0u, 0u);

@@ -133,6 +133,15 @@ class MLALatentCache:
 
 
 @dataclass
+class PendingResidual:
+    """A decode module output whose final sum is deferred to its consumer
+    (reference parrot/model.py:103-106): ``bf16(base + bf16(sum over lanes
+    of contributions))``, contributions fp32 [batch, lanes, dim]."""
+    base: Tensor | None
+    contributions: Tensor
+
+
+@dataclass
 class GenerationState:
     layers: list[LocalKVCache | MLALatentCache]
     position: int
@@ -384,6 +393,16 @@ class LocalGQA(nn.Module):
                 hip_moe.decode_qkv_supported(first.numel() // first.shape[-1], c.dim, c.n_heads,
                                              c.n_kv_heads, c.head_dim))
 
+    def defers_sum(self, x: Tensor, position_device: Tensor | None) -> bool:
+        """Whether decode(defer_sum=True) takes this input: the HIP decode
+        path at at most two rows, which returns the per-head contributions of
+        the output projection instead of their sum."""
+        if not (self._hip(x) and position_device is not None):
+            return False
+        from . import hip_moe
+        b = x.numel() // x.shape[-1]
+        return hip_moe.decode_attention_heads_supported(b, x.shape[-1])
+
     def decode(self, x: Tensor | None, cache: LocalKVCache, position: int,
                addend: Tensor | None = None, defer_sum: bool = False,
                position_device: Tensor | None = None, mix: tuple | None = None) -> Tensor:
@@ -395,10 +414,10 @@ class LocalGQA(nn.Module):
             x = mix[1][0]  # shape, dtype and device of the input rows
         if x.shape[1] != 1:
             raise ValueError("decode expects one model position")
-        if defer_sum:
-            raise RuntimeError("deferred attention reduction is not supported on this backend")
         c = self.cfg
         b = x.shape[0]
+        if defer_sum and not self.defers_sum(x, position_device):
+            raise RuntimeError("deferred attention reduction is not supported for this input")
         if self._hip(x) and position_device is not None:
             # RoPE at the device position, then one kernel stores the new key
             # and value and attends over the window (parrot/model.py:239-262).
@@ -415,6 +434,12 @@ class LocalGQA(nn.Module):
                 q, k, v = hip_moe.rope_qkv(F.linear(x, self._packed_qkv()), cos, sin, c.n_heads,
                                            c.n_kv_heads, c.head_dim, 0, False,
                                            start_device=position_device)
+            if defer_sum:
+                # Per-head contributions of the output projection; the caller
+                # wraps them (with the addend) in a PendingResidual.
+                return hip_moe.decode_attention_heads(q, k, v, cache.key, cache.value,
+                                                      position_device, c.window_size,
+                                                      c.head_dim ** -0.5, self.out.weight)
             y = hip_moe.decode_attention(q, k, v, cache.key, cache.value, position_device,
                                          c.window_size, c.head_dim ** -0.5)
             width = c.n_heads * c.head_dim
@@ -842,20 +867,62 @@ class Parrot(nn.Module):
                                                     block.moe_norm, block.moe)
         return self._mixed_input(stream, x, index, block.moe_norm), None
 
+    def _fuses_decode_moe(self, block: Block, first: Tensor) -> bool:
+        """Whether a decode step's MoE module makes its input's depth mix +
+        norm inside the fused decode MoE's launches."""
+        if self.config.depth_backend != "hip" or not block.moe._hip_route_applies(first):
+            return False
+        from . import hip_moe
+        tokens, dim = first.numel() // first.shape[-1], first.shape[-1]
+        return tokens <= hip_moe.DECODE_MAX_TOKENS and dim <= 1024
+
+    def _defers_attention(self, block: Block, stream: _AttnRes, index: int,
+                          state: GenerationState) -> bool:
+        """Whether attention module ``index`` of a decode step leaves its
+        output's sum to the MoE's input mix: local layers on the HIP path at
+        at most two rows, when the module does not close a depth block (its
+        output is then read by that mix alone)."""
+        first = stream.sources()[0]
+        return (isinstance(block.attention, LocalGQA) and
+                (index + 1) % self.config.depth_block_size != 0 and
+                block.attention.defers_sum(first, state.position_device) and
+                self._fuses_decode_moe(block, first))
+
+    @staticmethod
+    def _resolve(pending: PendingResidual, dtype: torch.dtype) -> Tensor:
+        """``base + round(sum of the contributions)`` in ``dtype`` (the
+        pending item's value) with torch ops, for consumers that do not
+        resolve it themselves."""
+        delta = pending.contributions.sum(1, keepdim=True).to(dtype)
+        if pending.base is None:
+            return delta
+        return (pending.base.float() + delta.float()).to(dtype)
+
     def _decode_moe(self, block: Block, stream: _AttnRes, x: Tensor, index: int) -> Tensor:
         """MoE module ``index`` of a decode step, closing the open partial sum
         (``partial + delta``).  On the HIP path its input's depth mix + norm
-        runs inside the fused decode MoE's launches."""
+        runs inside the fused decode MoE's launches, resolving a pending
+        attention output there too."""
         sources = stream.sources()
         first = sources[0]
-        if self.config.depth_backend == "hip" and block.moe._hip_route_applies(first):
+        pending = stream.partial if isinstance(stream.partial, PendingResidual) else None
+        if self._fuses_decode_moe(block, first):
             from . import hip_moe
-            tokens, dim = first.numel() // first.shape[-1], first.shape[-1]
-            if tokens <= hip_moe.DECODE_MAX_TOKENS and dim <= 1024:
+            mix_depth = self.depth_mix[index]
+            if pending is None:
                 out = hip_moe.decode_experts(
                     block.moe, None, addend=stream.partial,
-                    mix=(self.depth_mix[index], sources, block.moe_norm))[0]
-                return out.view_as(first)
+                    mix=(mix_depth, sources, block.moe_norm))[0]
+            else:
+                resolved = torch.empty_like(first)
+                placeholder = pending.base if pending.base is not None else first
+                out = hip_moe.decode_experts(
+                    block.moe, None, addend=resolved,
+                    mix=(mix_depth, sources[:-1] + [placeholder], block.moe_norm),
+                    pending=(pending.contributions, pending.base, resolved))[0]
+            return out.view_as(first)
+        if pending is not None:
+            stream.partial = self._resolve(pending, first.dtype)
         h = self._mixed_input(stream, x, index, block.moe_norm)
         return block.moe.inference(h, direct=True, addend=stream.partial)
 
@@ -1073,10 +1140,18 @@ class Parrot(nn.Module):
             if (stream is not None and self.config.depth_backend == "hip" and
                     block.attention.decodes_mixed(stream.sources()[0], state.position_device)):
                 # The input's depth mix + norm runs inside the q|k|v launch.
-                out = block.attention.decode(
-                    None, cache, state.position, addend=addend,
-                    position_device=state.position_device,
-                    mix=(self.depth_mix[index], stream.sources(), block.attention_norm))
+                mix = (self.depth_mix[index], stream.sources(), block.attention_norm)
+                if self._defers_attention(block, stream, index, state):
+                    # The output projection's sum over heads is left to the
+                    # MoE's input mix (the reference's PendingResidual).
+                    delta = block.attention.decode(
+                        None, cache, state.position, defer_sum=True,
+                        position_device=state.position_device, mix=mix)
+                    out = PendingResidual(addend, delta)
+                else:
+                    out = block.attention.decode(
+                        None, cache, state.position, addend=addend,
+                        position_device=state.position_device, mix=mix)
             else:
                 h = self._mixed_input(stream, x, index, block.attention_norm)
                 out = block.attention.decode(h, cache, state.position, addend=addend,

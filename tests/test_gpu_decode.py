@@ -58,6 +58,87 @@ def test_decode_attention_window(position):
     assert (got - ref).abs().max() <= 2 ** -8 * ref.abs().max() + 1e-5
 
 
+@pytest.mark.parametrize("batch,position", [(1, 0), (2, 63), (1, 200), (3, 64)])
+def test_decode_attention_heads(batch, position):
+    """The deferred form: the same cache update as decode_attention, and
+    per-head contributions equal to the products of decode_attention's own
+    bf16 output with each head's slice of the output projection (fp64 on
+    the CPU, fp32 reassociation tolerance).  Summed over heads, rounded and
+    added to an addend they match the undeferred projection within one bf16
+    rounding of each sum."""
+    from parrot import hip_moe
+    H, Hk, d, max_pos, window, dim = 8, 2, 96, 256, 64, 768
+    _say(f"decode attention heads b={batch} p={position}")
+    g = torch.Generator().manual_seed(100 + position + batch)
+    kc = torch.randn(batch, Hk, max_pos, d, generator=g).bfloat16()
+    vc = torch.randn(batch, Hk, max_pos, d, generator=g).bfloat16()
+    q = torch.randn(batch, H, 1, d, generator=g).bfloat16().cuda()
+    kn = torch.randn(batch, Hk, 1, d, generator=g).bfloat16().cuda()
+    vn = torch.randn(batch, Hk, 1, d, generator=g).bfloat16().cuda()
+    wo = (torch.randn(dim, H * d, generator=g) * (H * d) ** -0.5).bfloat16().cuda()
+    addend = torch.randn(batch, 1, dim, generator=g).bfloat16().cuda()
+    pos = torch.tensor([position], dtype=torch.int32, device="cuda")
+    kc_a, vc_a, kc_b, vc_b = kc.cuda(), vc.cuda(), kc.cuda(), vc.cuda()
+    with torch.no_grad():
+        y = hip_moe.decode_attention(q, kn, vn, kc_a, vc_a, pos, window, d ** -0.5)
+        contrib = hip_moe.decode_attention_heads(q, kn, vn, kc_b, vc_b, pos, window, d ** -0.5,
+                                                 wo)
+        undeferred = hip_moe.decode_linear(y.view(batch, 1, H * d), wo, addend)
+    assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b)
+    assert contrib.shape == (batch, H, dim) and contrib.dtype == torch.float32
+    yd = y.double().cpu().view(batch, H, d)
+    w = wo.double().cpu().view(dim, H, d)
+    ref = torch.einsum("bhi,nhi->bhn", yd, w)
+    scale = torch.einsum("bhi,nhi->bhn", yd.abs(), w.abs())
+    assert ((contrib.double().cpu() - ref).abs() <= 1e-6 * scale + 1e-7).all()
+    # The resolved module output against the undeferred GEMV + addend.
+    acc = contrib[:, 0].clone()
+    for h in range(1, H):
+        acc = acc + contrib[:, h]
+    resolved = (addend.float().view(batch, dim) + acc.bfloat16().float()).bfloat16()
+    got, want = resolved.float().cpu(), undeferred.float().cpu().view(batch, dim)
+    tol = 2 ** -7 * (addend.float().cpu().view(batch, dim).abs() + 2 * acc.abs().cpu()) + 1e-6
+    assert ((got - want).abs() <= tol).all()
+
+
+@pytest.mark.parametrize("tokens,lanes,with_base,sources", [
+    (1, 8, True, 3), (2, 8, False, 1), (5, 11, True, 9), (16, 1, True, 4)])
+def test_decode_moe_resolves_a_pending_source(tokens, lanes, with_base, sources):
+    """A pending last depth source resolved inside the decode MoE's input
+    mix: the resolved rows equal bf16(base + bf16(the lanes summed in order))
+    computed on the CPU, and the MoE's outputs equal those of the same launch
+    given the resolved rows as an ordinary source, bit for bit."""
+    from moe_cases import inputs, moe_module
+    from test_gpu_moe import _Depth, _Norm
+    from parrot import hip_moe
+    _say(f"decode moe pending T={tokens} lanes={lanes} base={with_base} S={sources}")
+    torch.manual_seed(40 + tokens + lanes)
+    module = moe_module(16, seed=17)
+    depth = _Depth(768).cuda().bfloat16()
+    norm = _Norm(768).cuda().bfloat16()
+    src = [inputs(tokens, seed=50 + s).view(tokens, 1, 768) * (1 + s) for s in range(sources - 1)]
+    g = torch.Generator().manual_seed(60 + tokens)
+    contrib = (torch.randn(tokens, lanes, 768, generator=g) * 0.3).cuda()
+    base = inputs(tokens, seed=61).view(tokens, 1, 768) if with_base else None
+    acc = torch.zeros(tokens, 768)
+    for l in range(lanes):
+        acc = acc + contrib[:, l].cpu()
+    ref = acc.bfloat16()
+    if base is not None:
+        ref = (base.cpu().float().view(tokens, 768) + ref.float()).bfloat16()
+    ref = ref.view(tokens, 1, 768).cuda()
+    placeholder = base if base is not None else (src[0] if src else ref)
+    with torch.no_grad():
+        resolved = torch.empty(tokens, 1, 768, dtype=torch.bfloat16, device="cuda")
+        out, idx, w = hip_moe.decode_experts(
+            module, None, addend=resolved, mix=(depth, src + [placeholder], norm),
+            pending=(contrib, base, resolved))
+        out2, idx2, w2 = hip_moe.decode_experts(module, None, addend=ref,
+                                                mix=(depth, src + [ref], norm))
+    assert torch.equal(resolved, ref)
+    assert torch.equal(idx, idx2) and torch.equal(w, w2) and torch.equal(out, out2)
+
+
 @pytest.mark.parametrize("position", [0, 150, 299])
 def test_decode_attention_latent(position):
     from parrot import hip_moe
