@@ -38,19 +38,14 @@ namespace {
 
 constexpr int kDecodeMaxTokens = 16;
 
-// LDS layout of decode_up_kernel: the token row (dim bf16, 16-byte aligned),
-// then the router weights (experts x dim bf16, padded to whole 1 KB groups).
-// The router weights are staged only up to kRouterLdsBudget bytes (E = 32 at
-// dim 768); past it the router reads them from memory as before.
-constexpr size_t kRouterLdsBudget = 48 * 1024;
-__host__ __device__ __forceinline__ int router_lds_offset(int dim) { return (dim + 7) / 8 * 8; }
-__host__ __device__ __forceinline__ bool router_in_lds(int dim, int experts) {
-  return static_cast<size_t>(experts) * dim * sizeof(uint16_t) <= kRouterLdsBudget;
+// decode_up_kernel's LDS row (the slot's token row, dim bf16) is dynamic.
+__host__ __device__ __forceinline__ size_t decode_up_lds_bytes(int dim) {
+  return static_cast<size_t>((dim + 7) / 8 * 8) * sizeof(uint16_t);
 }
-__host__ __device__ __forceinline__ size_t decode_up_lds_bytes(int dim, int experts) {
-  const size_t chunks = router_in_lds(dim, experts) ? static_cast<size_t>(experts) * dim / 8 : 0;
-  return (router_lds_offset(dim) + (chunks + kWave - 1) / kWave * kWave * 8) * sizeof(uint16_t);
-}
+
+// Router k steps per wavefront whose weight fragments are loaded at kernel
+// entry (dim 768: all of them); the rest are loaded in the chain itself.
+constexpr int kRouteStepSlots = 6;
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
 
@@ -61,43 +56,75 @@ __device__ __forceinline__ float dot8(uint4 a, uint4 b) {
          lo_bf16(a.w) * lo_bf16(b.w) + hi_bf16(a.w) * hi_bf16(b.w);
 }
 
-// Router logits of token t for all experts into lg[0..E), then top-2.
-// Thread (e = tid / 8, part = tid % 8) sums the dim / 8 columns of its part;
-// the 8 parts of an expert are added in a fixed order by DPP (xor 1, xor 2,
-// half-row mirror) inside 8-lane groups.
-__device__ __forceinline__ void route_token(const uint16_t* x_row, const uint16_t* wr,
-                                            const float* bias, int dim, int experts, float* lg,
-                                            int* sel, float* sel_w) {
+// One 16-byte chunk of an LDS array, read as LDS (ds_read_b128) rather
+// than through a generic pointer (flat_load, which also waits on the vector
+// memory counter).
+typedef uint32_t lds_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 lds_chunk(const uint16_t* base, int chunk) {
+  const lds_u32x4 v = ((const __attribute__((address_space(3))) lds_u32x4*)base)[chunk];
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// The slot's router logits and top-2, with route_kernel's arithmetic to the
+// bit: wavefront c runs the v_mfma_f32_16x16x32_bf16 chain over the 32-wide
+// k steps st = c, c + 4, ... (the token row from LDS in A row 0, rows 1-15
+// zero; an MFMA output element depends only on its own row and column), one
+// 16-expert column tile per ROUTE; the chains are summed ((c0 + c1) + c2) +
+// c3, plus the bias, then top-2 with ties to the lower index and weights
+// 1 / (1 + e), e / (1 + e), e = exp(l2 - l1).  rb: the fragments of the
+// first kRouteStepSlots steps, loaded at kernel entry; pb: the lane's router
+// row (column l % 16 of tile h) at its k offset, for the later steps.
+template <int ROUTE>
+__device__ __forceinline__ void route_slot(const uint16_t* x_lds,
+                                           const bf16x8 (&rb)[kRouteStepSlots][ROUTE],
+                                           const uint16_t* const (&pb)[ROUTE], const float* bias,
+                                           int dim, int experts, float (*chain_s)[kMaxExperts],
+                                           int* sel, float* sel_w) {
   const int tid = threadIdx.x;
-  const int e = tid >> 3, part = tid & 7;
-  float acc = 0.0f;
-  if (e < experts) {
-    const int n = dim / 64;  // 16-byte chunks per part (dim % 64 == 0)
-    const uint4* xa = reinterpret_cast<const uint4*>(x_row) + part * n;
-    const uint4* wa = reinterpret_cast<const uint4*>(wr + static_cast<int64_t>(e) * dim) + part * n;
-    for (int c0 = 0; c0 < n; c0 += 12) {  // 12 chunks (dim 768) in flight at once
-      uint4 xv[12], wv[12];
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int steps = dim / 32;
+  const bool row0 = (lane & 15) == 0;
+  auto a_frag = [&](int st) {
+    const uint4 av = row0 ? lds_chunk(x_lds, st * 4 + (lane >> 4)) : make_uint4(0u, 0u, 0u, 0u);
+    return __builtin_bit_cast(bf16x8, av);
+  };
+  f32x4 acc[ROUTE];
 #pragma unroll
-      for (int u = 0; u < 12; ++u) {
-        const int c = min(c0 + u, n - 1);
-        xv[u] = xa[c];
-        wv[u] = wa[c];
-      }
+  for (int h = 0; h < ROUTE; ++h) acc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int u = 0; u < 12; ++u)
-        if (c0 + u < n) acc += dot8(xv[u], wv[u]);
+  for (int i = 0; i < kRouteStepSlots; ++i) {
+    const int st = wave + 4 * i;
+    if (st < steps) {
+      const bf16x8 a = a_frag(st);
+#pragma unroll
+      for (int h = 0; h < ROUTE; ++h)
+        acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, rb[i][h], acc[h], 0, 0, 0);
     }
   }
-  acc += dpp<0xb1>(acc);
-  acc += dpp<0x4e>(acc);
-  acc += dpp<0x141>(acc);
-  if (part == 0 && e < experts) lg[e] = acc + (bias != nullptr ? bias[e] : 0.0f);
+  for (int st = wave + 4 * kRouteStepSlots; st < steps; st += 4) {
+    const bf16x8 a = a_frag(st);
+#pragma unroll
+    for (int h = 0; h < ROUTE; ++h)
+      acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          a, __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(pb[h] + st * 32)),
+          acc[h], 0, 0, 0);
+  }
+  // Row 0 of the C fragment: lanes 0-15, register 0.
+  if (lane < 16) {
+    chain_s[wave][lane] = acc[0][0];
+    chain_s[wave][16 + lane] = ROUTE > 1 ? acc[ROUTE - 1][0] : 0.0f;
+  }
   __syncthreads();
   if (tid < 16) {
+    auto logit = [&](int e) -> float {
+      const float v = ((chain_s[0][e] + chain_s[1][e]) + chain_s[2][e]) + chain_s[3][e];
+      return v + (bias != nullptr ? bias[e] : 0.0f);
+    };
     int first, second;
     float vb, vr;
-    row_top2(tid < experts ? lg[tid] : 0.0f, tid + 16 < experts ? lg[tid + 16] : 0.0f, experts,
-             first, second, vb, vr);
+    row_top2(tid < experts ? logit(tid) : 0.0f, tid + 16 < experts ? logit(tid + 16) : 0.0f,
+             experts, first, second, vb, vr);
     if (tid == 0) {
       const float e2 = __expf(vr - vb);
       const float den = 1.0f + e2;
@@ -110,19 +137,19 @@ __device__ __forceinline__ void route_token(const uint16_t* x_row, const uint16_
   __syncthreads();
 }
 
+template <int ROUTE, bool MIX>
 __global__ __launch_bounds__(256) void decode_up_kernel(
     const uint16_t* __restrict__ x, DecodeMix mix, const uint16_t* __restrict__ wr,
     const float* __restrict__ bias, int tokens, int dim, int experts, int hidden_dim,
     int shared_dim, int hstride, const uint16_t* __restrict__ gate_up,
     const uint16_t* __restrict__ shared_gate_up, uint16_t* __restrict__ hidden,
     int64_t* __restrict__ indices, float* __restrict__ weights) {
-  __shared__ float lg[kMaxExperts];
+  __shared__ float chain_s[4][kMaxExperts];
   __shared__ int sel[2];
   __shared__ float sel_w[2];
   __shared__ float part[4][4][32];  // [wave][k chunk][gate 16 | up 16]
   __shared__ DepthMixLds mix_lds;
-  // The slot's token row [dim], then (routed slots) the router weights
-  // [experts, dim] at element offset xs_elems.
+  // The slot's token row [dim].
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -133,21 +160,26 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   const int H = shared ? shared_dim : hidden_dim;
   if (slice * 16 >= H) return;  // uniform
   const int t0 = shared ? slot - 2 * tokens : slot >> 1;  // the slot's token
-  const bool staged = router_in_lds(dim, experts);  // uniform
-  uint16_t* wr_s = xs + router_lds_offset(dim);
-  if (!shared && staged) {
-    // Router weights straight into LDS (16 bytes per lane, a wavefront's
-    // 64 lanes fill 1 KB), issued before the input mix so they arrive with
-    // its sources instead of after it; lanes past the end reread the last
-    // chunk into the region's padding.
-    const int chunks = experts * dim / 8;
-    for (int g = wave; g * kWave < chunks; g += 4) {
-      const int c = min(g * kWave + lane, chunks - 1);
-      __builtin_amdgcn_global_load_lds(wr + static_cast<int64_t>(c) * 8,
-                                       (lds_void_t*)(wr_s + g * kWave * 8), 16, 0, 0);
-    }
-  }
-  if (mix.n_sources > 0) {
+  // Router weight fragments of this wavefront's chain, loaded right after
+  // the input row's loads with no branch between (every slot loads them, the
+  // shared slot's go unused; clamped, unconditional loads), so the waits for
+  // the input count them exactly and they arrive during the mix.
+  const int koff = (lane >> 4) * 8;
+  const uint16_t* pb[ROUTE];
+  bf16x8 rb[kRouteStepSlots][ROUTE];
+  auto load_router = [&]() {
+    const int last = dim / 32 - 1;
+#pragma unroll
+    for (int h = 0; h < ROUTE; ++h)
+      pb[h] = wr + static_cast<int64_t>(min(16 * h + (lane & 15), experts - 1)) * dim + koff;
+#pragma unroll
+    for (int i = 0; i < kRouteStepSlots; ++i)
+#pragma unroll
+      for (int h = 0; h < ROUTE; ++h)
+        rb[i][h] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const uint4*>(pb[h] + min(wave + 4 * i, last) * 32));
+  };
+  if constexpr (MIX) {
     // The token's input row: depth mix + RMSNorm of its sources into LDS,
     // every load issued before the first wait (lanes past the row read
     // chunk 0 and are zeroed, unread slots read source 0 and are zeroed).
@@ -162,36 +194,51 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
     const uint2 q = reinterpret_cast<const uint2*>(mix.query)[ic];
     const uint2 g = reinterpret_cast<const uint2*>(mix.score_w)[ic];
     const uint2 g_out = reinterpret_cast<const uint2*>(mix.out_w)[ic];
-    if (mix.pend != nullptr) {
-      // The pending last source: this chunk's contributions summed over the
-      // lanes in order (the loads of up to 8 lanes in flight at once),
-      // rounded, then added to the base with a second rounding; the
-      // token's first routed workgroup of slice 0 stores the resolved row.
-      const float4* pc = reinterpret_cast<const float4*>(mix.pend) +
-                         static_cast<int64_t>(t0) * mix.pend_lanes * chunks + ic;
+    // The pending last source's first 8 lanes and its base, loaded
+    // unconditionally (from the query row when there is none).
+    const bool pending = mix.pend != nullptr;  // uniform
+    const int lanes = pending ? mix.pend_lanes : 1;
+    const int64_t pstride = pending ? chunks : 0;
+    const float4* pc = pending ? reinterpret_cast<const float4*>(mix.pend) +
+                                     static_cast<int64_t>(t0) * lanes * chunks + ic
+                               : reinterpret_cast<const float4*>(mix.query);
+    float4 c[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) c[u] = pc[min(u, lanes - 1) * pstride];
+    const uint2 pbv = *(mix.pend_base != nullptr
+                            ? reinterpret_cast<const uint2*>(mix.pend_base) + base + ic
+                            : reinterpret_cast<const uint2*>(mix.query));
+    // Fences: the loads above go out before the router's, and the router's
+    // before any use of the input (no load sunk into a branch below).
+    asm volatile("" ::: "memory");
+    load_router();
+    asm volatile("" ::: "memory");
+    if (pending) {
+      // This chunk's contributions summed over the lanes in order, rounded,
+      // then added to the base with a second rounding; the token's first
+      // routed workgroup of slice 0 stores the resolved row.  Lanes past
+      // the end add -0, the exact identity, so no add sits behind a branch.
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int l0 = 0; l0 < mix.pend_lanes; l0 += 8) {
-        float4 c[8];
+      auto add = [&](const float4& cv, bool on) {
+        acc[0] += on ? cv.x : -0.0f;
+        acc[1] += on ? cv.y : -0.0f;
+        acc[2] += on ? cv.z : -0.0f;
+        acc[3] += on ? cv.w : -0.0f;
+      };
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          c[u] = pc[static_cast<int64_t>(min(l0 + u, mix.pend_lanes - 1)) * chunks];
+      for (int u = 0; u < 8; ++u) add(c[u], u < lanes);
+      for (int l0 = 8; l0 < lanes; l0 += 8) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (l0 + u < mix.pend_lanes) {
-            acc[0] += c[u].x;
-            acc[1] += c[u].y;
-            acc[2] += c[u].z;
-            acc[3] += c[u].w;
-          }
-        }
+        for (int u = 0; u < 8; ++u) c[u] = pc[min(l0 + u, lanes - 1) * pstride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) add(c[u], l0 + u < lanes);
       }
       uint2 r;
       r.x = pack_bf16x2(acc[0], acc[1]);
       r.y = pack_bf16x2(acc[2], acc[3]);
       if (mix.pend_base != nullptr) {
-        const uint2 pb = reinterpret_cast<const uint2*>(mix.pend_base)[base + ic];
-        r.x = pack_bf16x2(lo_bf16(pb.x) + lo_bf16(r.x), hi_bf16(pb.x) + hi_bf16(r.x));
-        r.y = pack_bf16x2(lo_bf16(pb.y) + lo_bf16(r.y), hi_bf16(pb.y) + hi_bf16(r.y));
+        r.x = pack_bf16x2(lo_bf16(pbv.x) + lo_bf16(r.x), hi_bf16(pbv.x) + hi_bf16(r.x));
+        r.y = pack_bf16x2(lo_bf16(pbv.y) + lo_bf16(r.y), hi_bf16(pbv.y) + hi_bf16(r.y));
       }
 #pragma unroll
       for (int s = 0; s < kMaxDepthSources; ++s)
@@ -209,9 +256,9 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
                                          mix_lds);
     if (has) reinterpret_cast<uint2*>(xs)[tid] = o;
   } else {
-    // The slot's activation row, staged in LDS as bf16; these loads are in
-    // flight together with the router's (the barrier in route_token, or the
-    // one below, orders them before use).
+    // The slot's activation row, staged in LDS as bf16 (the barrier before
+    // the router, or the shared slot's below, orders it before use).
+    load_router();
     for (int i = tid; i < dim / 8; i += 256)
       reinterpret_cast<uint4*>(xs)[i] =
           reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t0) * dim)[i];
@@ -221,12 +268,10 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
     __syncthreads();
     w = shared_gate_up;
   } else {
-    // The router reads the row from LDS once it is mixed there, and its
-    // weights from LDS once their direct-to-LDS loads have landed.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // The router reads the row from LDS once every wavefront has written
+    // its part there.
     __syncthreads();
-    route_token(mix.n_sources > 0 ? xs : x + static_cast<int64_t>(t0) * dim,
-                staged ? wr_s : wr, bias, dim, experts, lg, sel, sel_w);
+    route_slot<ROUTE>(xs, rb, pb, bias, dim, experts, chain_s, sel, sel_w);
     const int k = slot & 1;
     if (slice == 0 && k == 0 && tid < 2) {
       indices[2 * t0 + tid] = sel[tid];
@@ -361,9 +406,19 @@ hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens
   if (tokens == 0) return hipSuccess;
   const int hstride = hidden_dim > shared_dim ? hidden_dim : shared_dim;
   const DecodeMix none{};
-  decode_up_kernel<<<dim3(hstride / 16, 3 * tokens), 256, decode_up_lds_bytes(dim, experts), s>>>(
-      x, mix != nullptr ? *mix : none, router_w, bias, tokens, dim, experts, hidden_dim,
-      shared_dim, hstride, w.gate_up, w.shared_gate_up, hidden, indices, weights);
+  const dim3 up_grid(hstride / 16, 3 * tokens);
+  const size_t up_lds = decode_up_lds_bytes(dim);
+  const DecodeMix m = mix != nullptr ? *mix : none;
+  const bool mixing = m.n_sources > 0;
+  auto up = [&](auto kernel) {
+    kernel<<<up_grid, 256, up_lds, s>>>(x, m, router_w, bias, tokens, dim, experts, hidden_dim,
+                                        shared_dim, hstride, w.gate_up, w.shared_gate_up, hidden,
+                                        indices, weights);
+  };
+  if (experts <= 16)
+    mixing ? up(decode_up_kernel<1, true>) : up(decode_up_kernel<1, false>);
+  else
+    mixing ? up(decode_up_kernel<2, true>) : up(decode_up_kernel<2, false>);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   decode_down_kernel<<<dim3(dim / 16, tokens), 256, 0, s>>>(
       hidden, tokens, dim, hidden_dim, shared_dim, hstride, indices, weights, w.down,
