@@ -5,6 +5,8 @@
 // order.  Used by the MLA decode projections and the decode q|k|v
 // projection.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace parrot {
@@ -52,6 +54,32 @@ __device__ __forceinline__ void load_row_chunks(const uint16_t* w, int row, int 
 #pragma unroll
   for (int c = 0; c < kGemvMaxChunks; ++c)
     wr[c] = c < nch ? src[c * 16 + p] : make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The same for kernels instantiated per chunk count NCH >= K / 128: every
+// load is unconditional (chunks past K / 128 reread the last one and are
+// left out of the sums), so a kernel can issue other loads before and after
+// these and the compiler's waits still count them exactly.
+template <int NCH>
+__device__ __forceinline__ void load_row_chunks_n(const uint16_t* w, int row, int K, int p,
+                                                  uint4 (&wr)[NCH]) {
+  const int last = K / 128 - 1;
+  const uint4* src = reinterpret_cast<const uint4*>(w + static_cast<int64_t>(row) * K);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) wr[c] = src[min(c, last) * 16 + p];
+}
+
+// The chunk counts those kernels are instantiated for; K / 128 rounds up to
+// the next.  `launch` is called with std::integral_constant<int, NCH>.
+template <typename F>
+__host__ hipError_t with_gemv_chunks(int K, F&& launch) {
+  const int nch = K / 128;
+  if (nch <= 2) return launch(std::integral_constant<int, 2>{});
+  if (nch <= 4) return launch(std::integral_constant<int, 4>{});
+  if (nch <= 6) return launch(std::integral_constant<int, 6>{});
+  if (nch <= 8) return launch(std::integral_constant<int, 8>{});
+  if (nch <= 12) return launch(std::integral_constant<int, 12>{});
+  return launch(std::integral_constant<int, 16>{});
 }
 
 // Copies `bytes` (a multiple of 16) from global memory into LDS.

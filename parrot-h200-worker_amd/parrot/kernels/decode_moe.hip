@@ -151,6 +151,20 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   __shared__ DepthMixLds mix_lds;
   // The slot's token row [dim].
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  // The kernel arguments of the load phase in one batch of scalar loads
+  // (each field first read on its own would cost a scalar round trip).
+  if constexpr (MIX) {
+    const uint16_t* sp[kMaxDepthSources];
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = mix.srcs.src[s];
+    static_assert(kMaxDepthSources == 9, "the batch below names every source slot");
+    asm volatile("" ::"s"(sp[0]), "s"(sp[1]), "s"(sp[2]), "s"(sp[3]), "s"(sp[4]), "s"(sp[5]),
+                 "s"(sp[6]), "s"(sp[7]), "s"(sp[8]), "s"(mix.query), "s"(mix.score_w),
+                 "s"(mix.out_w), "s"(mix.pend), "s"(mix.pend_lanes), "s"(mix.pend_base),
+                 "s"(mix.n_sources));
+  }
+  asm volatile("" ::"s"(wr), "s"(tokens), "s"(dim), "s"(experts), "s"(hidden_dim),
+               "s"(shared_dim));
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -331,46 +345,65 @@ __global__ __launch_bounds__(256) void decode_down_kernel(
     const uint16_t* __restrict__ down, const uint16_t* __restrict__ shared_down,
     const uint16_t* __restrict__ addend, uint16_t* __restrict__ out) {
   __shared__ float part[3][4][4][16];  // [contribution][wave][k chunk][column]
+  // The kernel arguments in one batch of scalar loads, then the token's two
+  // expert ids (scalar loads too): the routed weights' addresses wait for
+  // them, the hidden rows and the shared expert's weights do not.
+  asm volatile("" ::"s"(hidden), "s"(indices), "s"(weights), "s"(down), "s"(shared_down),
+               "s"(addend), "s"(out), "s"(tokens), "s"(dim), "s"(hidden_dim), "s"(shared_dim),
+               "s"(hstride));
+  const int t = blockIdx.y;
+  const int64_t ex[2] = {indices[2 * t], indices[2 * t + 1]};
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
   const int slice = blockIdx.x;  // output columns [16 slice, 16 slice + 16)
-  const int t = blockIdx.y;
   const int c = lane >> 4;
   // Contribution 0 / 1: routed slot 2t + k (expert indices[2t + k], K = H);
   // contribution 2: the shared expert (K = Hs).  Wavefront w takes k steps
   // w, w + 4, ...; the loads of up to 4 steps of all three are issued
-  // before any arithmetic.
-  const uint4* wb[3];
+  // before any arithmetic: the hidden rows and the shared weights first,
+  // the routed weights last.
   const uint16_t* hrow[3];
   int ks[3];
 #pragma unroll
   for (int q = 0; q < 3; ++q) {
     const bool sh = q == 2;
     ks[q] = (sh ? shared_dim : hidden_dim) / 32;
-    const uint16_t* w = sh ? shared_down
-                           : down + indices[2 * t + q] * static_cast<int64_t>(dim) * hidden_dim;
-    wb[q] = reinterpret_cast<const uint4*>(w) + slice * ks[q] * 64 + lane;
     hrow[q] = hidden + (sh ? 2 * tokens + t : 2 * t + q) * static_cast<int64_t>(hstride) + c * 8;
   }
+  const uint4* wsh = reinterpret_cast<const uint4*>(shared_down) + slice * ks[2] * 64 + lane;
   float acc[3] = {0.0f, 0.0f, 0.0f};
-  const int kmax = max(ks[0], ks[2]);
-  for (int s0 = wave; s0 < kmax; s0 += 16) {
+  auto batch = [&](int s0) {
     uint4 wv[3][4], hv[3][4];
 #pragma unroll
     for (int q = 0; q < 3; ++q)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int st = min(s0 + 4 * i, ks[q] - 1);
-        wv[q][i] = wb[q][st * 64];
-        hv[q][i] = *reinterpret_cast<const uint4*>(hrow[q] + st * 32);
-      }
+      for (int i = 0; i < 4; ++i)
+        hv[q][i] = *reinterpret_cast<const uint4*>(hrow[q] + min(s0 + 4 * i, ks[q] - 1) * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wv[2][i] = wsh[min(s0 + 4 * i, ks[2] - 1) * 64];
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);  // the expert ids' first use (a wait) after these loads
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint4* wb = reinterpret_cast<const uint4*>(
+                            down + ex[q] * static_cast<int64_t>(dim) * hidden_dim) +
+                        slice * ks[q] * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wv[q][i] = wb[min(s0 + 4 * i, ks[q] - 1) * 64];
+    }
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int q = 0; q < 3; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (s0 + 4 * i < ks[q]) acc[q] += dot8(wv[q][i], hv[q][i]);
-  }
+  };
+  // The first batch straight-line (its loads are clamped, so it is safe for
+  // a wavefront past the k range), so that no address computation is
+  // hoisted ahead of its loads; more batches only past 16 k steps.
+  batch(wave);
+  for (int s0 = wave + 16; s0 < max(ks[0], ks[2]); s0 += 16) batch(s0);
 #pragma unroll
   for (int q = 0; q < 3; ++q) part[q][wave][c][lane & 15] = acc[q];
   __syncthreads();

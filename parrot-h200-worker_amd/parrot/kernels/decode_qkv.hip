@@ -25,9 +25,25 @@ namespace {
 
 constexpr int kQkvMaxDim = 1024;  // the mix holds a row with 4 wavefronts of 256 dims
 
+// Loads go out in the order they are needed, each batch behind the one
+// before with no wait between: the kernel arguments (one scalar batch), the
+// device position (a scalar load), the input row's sources, the weight
+// chunks (NCH per lane, unconditional), then the position's cos / sin.  The
+// mix waits only for its sources; the weights arrive while it runs.
+template <bool MIX, int NCH>
 __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
   __shared__ DepthMixLds mix_lds;
   __shared__ __attribute__((aligned(16))) uint16_t xs[kQkvMaxDim];
+  const DecodeMix& m = a.mix;
+  const uint16_t* sp[kMaxDepthSources];
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = m.srcs.src[s];
+  static_assert(kMaxDepthSources == 9, "the batch below names every source slot");
+  asm volatile("" ::"s"(sp[0]), "s"(sp[1]), "s"(sp[2]), "s"(sp[3]), "s"(sp[4]), "s"(sp[5]),
+               "s"(sp[6]), "s"(sp[7]), "s"(sp[8]), "s"(m.query), "s"(m.score_w), "s"(m.out_w),
+               "s"(a.w), "s"(a.position), "s"(a.cos_t), "s"(a.sin_t), "s"(a.dim),
+               "s"(a.head_dim), "s"(a.max_positions), "s"(a.x));
+  const int raw_pos = *a.position;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -40,36 +56,23 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
   const int w = col - head * d;
   const int H = a.heads, Hk = a.kv_heads;
 
-  uint4 wr[kGemvMaxChunks];
-  load_row_chunks(a.w, col, K, p, wr);
-  const int pos = min(max(*a.position, 0), a.max_positions - 1);
+  const int chunks = K >> 2;
+  const bool has = tid < chunks;
+  DecodeMixLoads ml;
+  if constexpr (MIX) decode_mix_load(m, static_cast<int64_t>(t) * chunks, has ? tid : 0, ml);
+  asm volatile("" ::: "memory");
+  uint4 wr[NCH];
+  load_row_chunks_n<NCH>(a.w, col, K, p, wr);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);  // the position's first use (a wait) after every load above
+  const int pos = min(max(raw_pos, 0), a.max_positions - 1);
   const int64_t ti = static_cast<int64_t>(pos) * (d / 2) + w / 2;
   const float rc = a.cos_t[ti], rs = a.sin_t[ti];
+  asm volatile("" ::: "memory");
 
-  if (a.mix.n_sources > 0) {
-    // Token t's input row: depth mix + RMSNorm of its sources into LDS, every
-    // load issued before the first wait (lanes past the row read chunk 0 and
-    // are zeroed, unread slots read source 0 and are zeroed).
-    const DecodeMix& m = a.mix;
-    const int chunks = K >> 2;
-    const bool has = tid < chunks;
-    const int ic = has ? tid : 0;
-    const int64_t base = static_cast<int64_t>(t) * chunks;
-    uint2 v[kMaxDepthSources];
-#pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s)
-      v[s] = reinterpret_cast<const uint2*>(m.srcs.src[s])[base + ic];
-    const uint2 q = reinterpret_cast<const uint2*>(m.query)[ic];
-    const uint2 g = reinterpret_cast<const uint2*>(m.score_w)[ic];
-    const uint2 g_out = reinterpret_cast<const uint2*>(m.out_w)[ic];
-#pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s)
-      if (!has || s >= m.n_sources) v[s] = make_uint2(0u, 0u);
-    const int waves = (K + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
-    const uint2 mixed =
-        depth_mix_chunk(v, q, g, has, m.n_sources, waves, wave, lane, K, m.score_eps, mix_lds);
-    const uint2 o =
-        depth_mix_norm_chunk(mixed, g_out, has, waves, wave, lane, K, m.out_eps, mix_lds);
+  if constexpr (MIX) {
+    // Token t's input row: depth mix + RMSNorm of its sources into LDS.
+    const uint2 o = decode_mix_row(m, ml, has, wave, lane, K, mix_lds);
     if (has) reinterpret_cast<uint2*>(xs)[tid] = o;
   } else {
     for (int i = tid; i < K / 8; i += 256)
@@ -82,7 +85,7 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
   const int nch = K / 128;
   float acc = 0.0f;
 #pragma unroll
-  for (int c = 0; c < kGemvMaxChunks; ++c)
+  for (int c = 0; c < NCH; ++c)
     if (c < nch) acc += dot_bf16x8(wr[c], xt[c * 16 + p]);
   acc = row16_sum(acc);
   // Round as the projection output, then rotate with the partner column.
@@ -109,8 +112,13 @@ int decode_qkv_max_dim() { return kQkvMaxDim; }
 hipError_t launch_decode_qkv(const DecodeQkvArgs& a, hipStream_t s) {
   if (a.tokens == 0) return hipSuccess;
   const int n = (a.heads + 2 * a.kv_heads) * a.head_dim;
-  decode_qkv_kernel<<<dim3(n / kGemvRows, a.tokens), 256, 0, s>>>(a);
-  return hipGetLastError();
+  const dim3 grid(n / kGemvRows, a.tokens);
+  const bool mixing = a.mix.n_sources > 0;
+  return with_gemv_chunks(a.dim, [&](auto nch) {
+    if (mixing) decode_qkv_kernel<true, nch><<<grid, 256, 0, s>>>(a);
+    else decode_qkv_kernel<false, nch><<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
+  });
 }
 
 }  // namespace parrot

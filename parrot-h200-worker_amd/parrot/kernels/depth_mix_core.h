@@ -141,4 +141,36 @@ __device__ __forceinline__ uint2 depth_mix_norm_chunk(uint2 mixed, uint2 g_out, 
   return o;
 }
 
+// Decode kernels that mix their own input row (one token per workgroup,
+// lane chunk i = threadIdx.x): decode_mix_load issues the loads of the
+// chunk (every source slot; lanes past the row read chunk 0) without waiting
+// for them, so a kernel can issue its weight loads behind them;
+// decode_mix_row zeroes unread slots and lanes past the row, then mixes and
+// normalises (two barriers).
+struct DecodeMixLoads {
+  uint2 v[kMaxDepthSources];
+  uint2 q, g, g_out;
+};
+
+__device__ __forceinline__ void decode_mix_load(const DecodeMix& m, int64_t base, int ic,
+                                                DecodeMixLoads& l) {
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s)
+    l.v[s] = reinterpret_cast<const uint2*>(m.srcs.src[s])[base + ic];
+  l.q = reinterpret_cast<const uint2*>(m.query)[ic];
+  l.g = reinterpret_cast<const uint2*>(m.score_w)[ic];
+  l.g_out = reinterpret_cast<const uint2*>(m.out_w)[ic];
+}
+
+__device__ __forceinline__ uint2 decode_mix_row(const DecodeMix& m, DecodeMixLoads& l, bool has,
+                                                int wave, int lane, int dim, DepthMixLds& sh) {
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s)
+    if (!has || s >= m.n_sources) l.v[s] = make_uint2(0u, 0u);
+  const int waves = (dim + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
+  const uint2 mixed =
+      depth_mix_chunk(l.v, l.q, l.g, has, m.n_sources, waves, wave, lane, dim, m.score_eps, sh);
+  return depth_mix_norm_chunk(mixed, l.g_out, has, waves, wave, lane, dim, m.out_eps, sh);
+}
+
 }  // namespace parrot

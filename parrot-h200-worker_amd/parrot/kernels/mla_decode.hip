@@ -28,45 +28,45 @@ namespace {
 
 // Workgroups [0, nq / 16): q_latent rows of absorbed_query; the rest: latent
 // rows of kv_down.  x [T, K] bf16 is staged in LDS (T K 2 bytes); with a
-// depth mix (mix.n_sources > 0) workgroup (x, t) instead mixes and
-// normalises token t's row into LDS (depth_mix_core.h) and serves token t.
+// depth mix (MIX) workgroup (x, t) instead mixes and normalises token t's row
+// into LDS (depth_mix_core.h) and serves token t.  The mix's source loads go
+// out first (the kernel arguments in one scalar batch before them), then the
+// weight chunks (NCH per lane, unconditional), so the mix waits only for its
+// sources and the weights arrive while it runs.
+template <bool MIX, int NCH>
 __global__ __launch_bounds__(256) void mla_decode_in_kernel(
     const uint16_t* __restrict__ x, DecodeMix mix, int tokens, int K,
     const uint16_t* __restrict__ wq, int nq, const uint16_t* __restrict__ wkv, int nl,
     float* __restrict__ q_out, uint16_t* __restrict__ lat_out) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   __shared__ DepthMixLds mix_lds;
+  if constexpr (MIX) {
+    const uint16_t* sp[kMaxDepthSources];
+#pragma unroll
+    for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = mix.srcs.src[s];
+    static_assert(kMaxDepthSources == 9, "the batch below names every source slot");
+    asm volatile("" ::"s"(sp[0]), "s"(sp[1]), "s"(sp[2]), "s"(sp[3]), "s"(sp[4]), "s"(sp[5]),
+                 "s"(sp[6]), "s"(sp[7]), "s"(sp[8]), "s"(mix.query), "s"(mix.score_w),
+                 "s"(mix.out_w), "s"(wq), "s"(wkv), "s"(K), "s"(nq));
+  }
   const int tid = threadIdx.x;
   const int j = tid >> 4, p = tid & 15;
   const int blocks_q = nq / kGemvRows;
   const bool is_q = static_cast<int>(blockIdx.x) < blocks_q;  // uniform
   const int row = (is_q ? blockIdx.x : blockIdx.x - blocks_q) * kGemvRows + j;
-  uint4 wr[kGemvMaxChunks];
-  load_row_chunks(is_q ? wq : wkv, row, K, p, wr);
-  int t_begin = 0, t_end = tokens;
-  if (mix.n_sources > 0) {
-    t_begin = blockIdx.y;
-    t_end = t_begin + 1;
-    const int chunks = K >> 2;
-    const bool has = tid < chunks;
-    const int ic = has ? tid : 0;
-    const int64_t base = static_cast<int64_t>(t_begin) * chunks;
-    uint2 v[kMaxDepthSources];
-#pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s)
-      v[s] = reinterpret_cast<const uint2*>(mix.srcs.src[s])[base + ic];
-    const uint2 q = reinterpret_cast<const uint2*>(mix.query)[ic];
-    const uint2 g = reinterpret_cast<const uint2*>(mix.score_w)[ic];
-    const uint2 g_out = reinterpret_cast<const uint2*>(mix.out_w)[ic];
-#pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s)
-      if (!has || s >= mix.n_sources) v[s] = make_uint2(0u, 0u);
-    const int waves = (K + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
+  const int chunks = K >> 2;
+  const bool has = tid < chunks;
+  const int t_begin = MIX ? static_cast<int>(blockIdx.y) : 0;
+  const int t_end = MIX ? t_begin + 1 : tokens;
+  DecodeMixLoads ml;
+  if constexpr (MIX) decode_mix_load(mix, static_cast<int64_t>(t_begin) * chunks, has ? tid : 0, ml);
+  asm volatile("" ::: "memory");
+  uint4 wr[NCH];
+  load_row_chunks_n<NCH>(is_q ? wq : wkv, row, K, p, wr);
+  asm volatile("" ::: "memory");
+  if constexpr (MIX) {
     const int lane = tid & (kWave - 1), wave = tid >> 6;
-    const uint2 mixed = depth_mix_chunk(v, q, g, has, mix.n_sources, waves, wave, lane, K,
-                                        mix.score_eps, mix_lds);
-    const uint2 o = depth_mix_norm_chunk(mixed, g_out, has, waves, wave, lane, K, mix.out_eps,
-                                         mix_lds);
+    const uint2 o = decode_mix_row(mix, ml, has, wave, lane, K, mix_lds);
     if (has) reinterpret_cast<uint2*>(xs)[tid] = o;
   } else {
     stage(x, xs, tokens * K * 2);
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void mla_decode_in_kernel(
     const uint4* xt = reinterpret_cast<const uint4*>(xs + (t - t_begin) * K);
     float acc = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kGemvMaxChunks; ++c)
+    for (int c = 0; c < NCH; ++c)
       if (c < nch) acc += dot_bf16x8(wr[c], xt[c * 16 + p]);
     acc = row16_sum(acc);
     if (p == 0) {
@@ -135,12 +135,19 @@ hipError_t launch_mla_decode_in(const uint16_t* x, const DecodeMix* mix, int tok
                                 const uint16_t* wq, int nq, const uint16_t* wkv, int nl,
                                 float* q_out, uint16_t* lat_out, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
-  const DecodeMix none{};
   const bool mixing = mix != nullptr;
+  const DecodeMix m = mixing ? *mix : DecodeMix{};
   const dim3 grid((nq + nl) / kGemvRows, mixing ? tokens : 1);
-  mla_decode_in_kernel<<<grid, 256, mla_decode_lds_bytes(mixing ? 1 : tokens, dim, 2), s>>>(
-      x, mixing ? *mix : none, tokens, dim, wq, nq, wkv, nl, q_out, lat_out);
-  return hipGetLastError();
+  const size_t lds = mla_decode_lds_bytes(mixing ? 1 : tokens, dim, 2);
+  return with_gemv_chunks(dim, [&](auto nch) {
+    if (mixing)
+      mla_decode_in_kernel<true, nch><<<grid, 256, lds, s>>>(x, m, tokens, dim, wq, nq, wkv, nl,
+                                                             q_out, lat_out);
+    else
+      mla_decode_in_kernel<false, nch><<<grid, 256, lds, s>>>(x, m, tokens, dim, wq, nq, wkv,
+                                                              nl, q_out, lat_out);
+    return hipGetLastError();
+  });
 }
 
 hipError_t launch_mla_decode_out(const float* ctx, int tokens, int width, const uint16_t* wo,
