@@ -91,6 +91,11 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   constexpr int kSlots = 256 / CH;  // value pass: key slots x chunks
   static_assert(D <= 256, "one query element per thread");
   extern __shared__ float smem[];
+  // The kernel arguments in one batch of scalar loads, before any use.
+  asm volatile("" ::"s"(q), "s"(k_new), "s"(v_new), "s"(k_cache), "s"(v_cache), "s"(position),
+               "s"(heads), "s"(kv_heads), "s"(max_pos), "s"(window), "s"(scale));
+  if constexpr (Q > 0) asm volatile("" ::"s"(ho.weight), "s"(ho.dim), "s"(ho.contributions));
+  __builtin_amdgcn_sched_barrier(0);
   const int h = Q > 0 ? static_cast<int>(blockIdx.x) / Q : static_cast<int>(blockIdx.x);
   const int quarter = Q > 0 ? static_cast<int>(blockIdx.x) % Q : 0;
   const int b = blockIdx.y;
@@ -107,13 +112,22 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   // Q > 0: thread t < dim / Q owns output column n = quarter dim / Q + t.
   const int nq = Q > 0 ? ho.dim / Q : 0;
 
+  // This thread's elements of the new key / value rows (stored below) and
+  // of the query (D <= 256), then the device position: none depends on the
+  // position, so they are in flight together, and the cache rows behind
+  // them wait for one round trip.  These loads go first, so their uses wait
+  // for none of the row loads behind them (loads complete in order).
+  const int64_t kv_index = static_cast<int64_t>(b) * kv_heads + kvh;
+  const uint16_t* kn = k_new + kv_index * D;
+  const uint16_t* vn = v_new + kv_index * D;
+  const int ie = min(tid, D - 1);
+  const uint16_t kne = kn[ie], vne = vn[ie];
+  const float qv = to_f32(q[(static_cast<int64_t>(b) * heads + h) * D + ie]);
+  asm volatile("" ::: "memory");
   const int pos = *position;
   if (pos < 0 || pos >= max_pos) return;  // uniform: nothing to attend to
   const int lo = max(0, pos - window + 1);
   const int L = pos - lo + 1;
-  const int64_t kv_index = static_cast<int64_t>(b) * kv_heads + kvh;
-  const uint16_t* kn = k_new + kv_index * D;
-  const uint16_t* vn = v_new + kv_index * D;
   const uint16_t* kc = k_cache + kv_index * max_pos * D;
   const uint16_t* vc = v_cache + kv_index * max_pos * D;
 
@@ -127,12 +141,6 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   auto value_row = [&](int key) -> const uint4* {
     return reinterpret_cast<const uint4*>(key == pos ? vn : vc + static_cast<int64_t>(key) * D);
   };
-  // This thread's elements of the new key / value rows (stored below) and
-  // of the query (D <= 256), loaded first: their uses then wait for none of
-  // the row loads behind them (loads complete in order).
-  const int ie = min(tid, D - 1);
-  const uint16_t kne = kn[ie], vne = vn[ie];
-  const float qv = to_f32(q[(static_cast<int64_t>(b) * heads + h) * D + ie]);
   uint4 kr0[CH];
   {
     const uint4* row = key_row(lo + min(tid, L - 1));

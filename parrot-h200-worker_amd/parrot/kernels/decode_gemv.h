@@ -11,6 +11,8 @@
 
 namespace parrot {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kGemvRows = 16;        // output rows per workgroup
 constexpr int kGemvMaxChunks = 16;   // 16-byte weight chunks per lane: K <= 2048
 

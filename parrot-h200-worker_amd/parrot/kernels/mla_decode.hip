@@ -19,6 +19,8 @@
 // (256 contiguous bytes per instruction across the row) in registers, the
 // tokens' inputs are staged in LDS once, and each token's 16 partial sums are
 // added by four DPP steps in a fixed order.
+#include <algorithm>
+
 #include "decode_gemv.h"
 #include "depth_mix_core.h"
 
@@ -89,17 +91,46 @@ __global__ __launch_bounds__(256) void mla_decode_in_kernel(
 
 // out [T, n] = bf16(ctx Wo^T) (+ addend, a second bf16 rounding); ctx
 // [T, K] is fp32 (the MLA context) or bf16 (XT = uint16_t: the local
-// layers' attention output), staged in LDS (T K sizeof(XT) bytes).
-template <typename XT>
+// layers' attention output), staged in LDS (T K sizeof(XT) bytes).  The
+// kernel arguments come in one scalar batch, then the first (up to) 1024
+// 16-byte chunks of ctx (4 per lane, clamped), then the weight chunks (NCH
+// per lane, unconditional): the staging waits only for ctx, and the weights
+// arrive meanwhile.  Longer ctx (more than 16 KB) is staged 4 chunks per
+// lane per round trip after that.
+template <typename XT, int NCH>
 __global__ __launch_bounds__(256) void decode_out_kernel(
     const XT* __restrict__ ctx, int tokens, int K, const uint16_t* __restrict__ wo, int n,
     const uint16_t* __restrict__ addend, uint16_t* __restrict__ out) {
   extern __shared__ __attribute__((aligned(16))) uint4 cs[];
-  const int j = threadIdx.x >> 4, p = threadIdx.x & 15;
+  asm volatile("" ::"s"(ctx), "s"(tokens), "s"(K), "s"(wo), "s"(n), "s"(addend), "s"(out));
+  __builtin_amdgcn_sched_barrier(0);
+  const int tid = threadIdx.x;
+  const int j = tid >> 4, p = tid & 15;
   const int row = blockIdx.x * kGemvRows + j;
-  uint4 wr[kGemvMaxChunks];
-  load_row_chunks(wo, row, K, p, wr);
-  stage(ctx, cs, tokens * K * static_cast<int>(sizeof(XT)));
+  const int chunks = tokens * K * static_cast<int>(sizeof(XT)) / 16;
+  // Staged through a plain vector type: an array of the uint4 struct copied
+  // into LDS is kept in scratch memory across the fences below.
+  const u32x4* src = reinterpret_cast<const u32x4*>(ctx);
+  u32x4* dst = reinterpret_cast<u32x4*>(cs);
+  u32x4 c0[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) c0[u] = src[min(tid + 256 * u, chunks - 1)];
+  asm volatile("" ::: "memory");
+  uint4 wr[NCH];
+  load_row_chunks_n<NCH>(wo, row, K, p, wr);
+  asm volatile("" ::: "memory");
+  // The LDS holds at least 1024 chunks (decode_out_lds_bytes), so the first
+  // batch is stored without a branch (slots past ctx get copies).
+#pragma unroll
+  for (int u = 0; u < 4; ++u) dst[tid + 256 * u] = c0[u];
+  for (int base = tid + 1024; base < chunks; base += 1024) {
+    u32x4 c1[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) c1[u] = src[min(base + 256 * u, chunks - 1)];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (base + 256 * u < chunks) dst[base + 256 * u] = c1[u];
+  }
   __syncthreads();
   const int nch = K / 128;
   for (int t = 0; t < tokens; ++t) {
@@ -107,12 +138,12 @@ __global__ __launch_bounds__(256) void decode_out_kernel(
     if constexpr (sizeof(XT) == 4) {
       const float4* ct = reinterpret_cast<const float4*>(cs) + t * K / 4;
 #pragma unroll
-      for (int c = 0; c < kGemvMaxChunks; ++c)
+      for (int c = 0; c < NCH; ++c)
         if (c < nch) acc += dot_f32x8(wr[c], ct[2 * (c * 16 + p)], ct[2 * (c * 16 + p) + 1]);
     } else {
       const uint4* ct = cs + t * K / 8;
 #pragma unroll
-      for (int c = 0; c < kGemvMaxChunks; ++c)
+      for (int c = 0; c < NCH; ++c)
         if (c < nch) acc += dot_bf16x8(wr[c], ct[c * 16 + p]);
     }
     acc = row16_sum(acc);
@@ -130,6 +161,13 @@ __global__ __launch_bounds__(256) void decode_out_kernel(
 size_t mla_decode_lds_bytes(int tokens, int k, int elem_bytes) {
   return static_cast<size_t>(tokens) * k * elem_bytes;
 }
+
+namespace {
+// decode_out_kernel's LDS: the staged input, at least 1024 16-byte chunks.
+size_t decode_out_lds_bytes(int tokens, int k, int elem_bytes) {
+  return std::max<size_t>(mla_decode_lds_bytes(tokens, k, elem_bytes), 1024 * 16);
+}
+}  // namespace
 
 hipError_t launch_mla_decode_in(const uint16_t* x, const DecodeMix* mix, int tokens, int dim,
                                 const uint16_t* wq, int nq, const uint16_t* wkv, int nl,
@@ -154,18 +192,22 @@ hipError_t launch_mla_decode_out(const float* ctx, int tokens, int width, const 
                                  int dim, const uint16_t* addend, uint16_t* out, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
   const dim3 grid(dim / kGemvRows);
-  decode_out_kernel<float><<<grid, 256, mla_decode_lds_bytes(tokens, width, 4), s>>>(
-      ctx, tokens, width, wo, dim, addend, out);
-  return hipGetLastError();
+  return with_gemv_chunks(width, [&](auto nch) {
+    decode_out_kernel<float, nch><<<grid, 256, decode_out_lds_bytes(tokens, width, 4), s>>>(
+        ctx, tokens, width, wo, dim, addend, out);
+    return hipGetLastError();
+  });
 }
 
 hipError_t launch_decode_linear(const uint16_t* x, int tokens, int k, const uint16_t* w, int n,
                                 const uint16_t* addend, uint16_t* out, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
   const dim3 grid(n / kGemvRows);
-  decode_out_kernel<uint16_t><<<grid, 256, mla_decode_lds_bytes(tokens, k, 2), s>>>(
-      x, tokens, k, w, n, addend, out);
-  return hipGetLastError();
+  return with_gemv_chunks(k, [&](auto nch) {
+    decode_out_kernel<uint16_t, nch><<<grid, 256, decode_out_lds_bytes(tokens, k, 2), s>>>(
+        x, tokens, k, w, n, addend, out);
+    return hipGetLastError();
+  });
 }
 
 }  // namespace parrot
