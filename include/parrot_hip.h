@@ -167,8 +167,9 @@ int parrot_decode_attention_bf16(const void* q, const void* k_new, const void* v
  * aligned) is the output projection.  Summed over heads (in head order),
  * rounded to bf16 and added to the addend they give the attention module's
  * output; parrot_depth_mix_decode_moe_pending_bf16 does that in its input
- * mix.  dim % 4 == 0, dim <= 1024; LDS as parrot_decode_attention_bf16 plus
- * 4 * head_dim bytes; other limits as there. */
+ * mix.  Each head runs in 16 workgroups, one per 1/16 of the output
+ * columns: dim % 16 == 0, dim <= 4096; LDS as parrot_decode_attention_bf16
+ * plus 4 * head_dim bytes; other limits as there. */
 int parrot_decode_attention_heads_bf16(const void* q, const void* k_new, const void* v_new,
                                        void* key_cache, void* value_cache,
                                        const int32_t* position, int32_t batch, int32_t heads,

@@ -885,15 +885,17 @@ def decode_attention(q: Tensor, k_new: Tensor, v_new: Tensor, key_cache: Tensor,
     return out
 
 
-DEFER_MAX_TOKENS = 2  # rows up to which decode attention defers its output sum
+DEFER_MAX_TOKENS = 4  # rows up to which decode attention defers its output sum
+DECODE_HEADS_PARTS = 16  # workgroups per head of parrot_decode_attention_heads_bf16
 
 
 def decode_attention_heads_supported(tokens: int, dim: int) -> bool:
     """Shapes for which a decode step defers the attention output sum
     (``decode_attention_heads`` + the pending decode MoE mix): at most
-    DEFER_MAX_TOKENS rows, since each head's attention runs in four
-    workgroups (one per quarter of the output columns)."""
-    return 1 <= tokens <= DEFER_MAX_TOKENS and dim % 4 == 0 and dim <= 1024
+    DEFER_MAX_TOKENS rows, since each head's attention runs in
+    DECODE_HEADS_PARTS workgroups (one per 1/16 of the output columns)."""
+    return (1 <= tokens <= DEFER_MAX_TOKENS and dim % DECODE_HEADS_PARTS == 0
+            and dim // DECODE_HEADS_PARTS <= 256)
 
 
 def decode_attention_heads(q: Tensor, k_new: Tensor, v_new: Tensor, key_cache: Tensor,

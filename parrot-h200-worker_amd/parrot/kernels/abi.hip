@@ -243,7 +243,7 @@ int parrot_decode_attention_heads_bf16(const void* q, const void* k_new, const v
   if (int rc = check_decode_shape(batch, heads, kv_heads, head_dim, max_positions, window))
     return rc;
   if (dim <= 0) return PARROT_ERR_BAD_SHAPE;
-  if (dim % parrot::kDecodeHeadsQuarters || dim / parrot::kDecodeHeadsQuarters > 256 ||
+  if (dim % parrot::kDecodeHeadsParts || dim / parrot::kDecodeHeadsParts > 256 ||
       parrot::decode_attention_lds_bytes(window, max_positions, head_dim) +
               static_cast<size_t>(head_dim) * sizeof(float) > parrot::kMaxDecodeLds)
     return PARROT_ERR_UNSUPPORTED;

@@ -363,10 +363,10 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_new,
 // The deferred form for bf16 queries: per-head contributions of the output
 // projection, contributions [batch, heads, dim] fp32 = the head's output
 // (rounded to bf16) times its [dim, head_dim] slice of out_weight [dim,
-// heads x head_dim]; kDecodeHeadsQuarters workgroups per head split the
-// output columns (dim / kDecodeHeadsQuarters <= 256).  The launch's LDS is
+// heads x head_dim]; kDecodeHeadsParts workgroups per head split the
+// output columns (dim / kDecodeHeadsParts <= 256).  The launch's LDS is
 // decode_attention_lds_bytes + head_dim floats.
-constexpr int kDecodeHeadsQuarters = 4;
+constexpr int kDecodeHeadsParts = 16;
 hipError_t launch_decode_attention_heads(const uint16_t* q, const uint16_t* k_new,
                                          const uint16_t* v_new, uint16_t* k_cache,
                                          uint16_t* v_cache, const int32_t* position, int batch,

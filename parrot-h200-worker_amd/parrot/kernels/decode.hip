@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   if constexpr (Q > 0) asm volatile("" ::"s"(ho.weight), "s"(ho.dim), "s"(ho.contributions));
   __builtin_amdgcn_sched_barrier(0);
   const int h = Q > 0 ? static_cast<int>(blockIdx.x) / Q : static_cast<int>(blockIdx.x);
-  const int quarter = Q > 0 ? static_cast<int>(blockIdx.x) % Q : 0;
+  const int part_n = Q > 0 ? static_cast<int>(blockIdx.x) % Q : 0;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int rep = heads / kv_heads;
@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   float* red = part + kSlots * D;  // [4]
   float* ob = red + 4;             // [D] (Q > 0) the head's rounded output
 
-  // Q > 0: thread t < dim / Q owns output column n = quarter dim / Q + t.
+  // Q > 0: thread t < dim / Q owns output column n = part_n dim / Q + t.
   const int nq = Q > 0 ? ho.dim / Q : 0;
 
   // This thread's elements of the new key / value rows (stored below) and
@@ -161,12 +161,12 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   if constexpr (Q > 0) {
     asm volatile("" ::: "memory");
     const uint4* wrow = reinterpret_cast<const uint4*>(
-        ho.weight + static_cast<int64_t>(quarter * nq + min(tid, nq - 1)) * heads * D + h * D);
+        ho.weight + static_cast<int64_t>(part_n * nq + min(tid, nq - 1)) * heads * D + h * D);
 #pragma unroll
     for (int c = 0; c < CH; ++c) wo[c] = wrow[c];
   }
   // The first head of each kv group stores the new key / value row.
-  if (h % rep == 0 && quarter == 0 && tid < D) {
+  if (h % rep == 0 && part_n == 0 && tid < D) {
     k_cache[(kv_index * max_pos + pos) * D + tid] = kne;
     if (v_cache != k_cache) v_cache[(kv_index * max_pos + pos) * D + tid] = vne;
   }
@@ -273,7 +273,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
                hi_bf16(wo[c].y) * oc[3] + lo_bf16(wo[c].z) * oc[4] + hi_bf16(wo[c].z) * oc[5] +
                lo_bf16(wo[c].w) * oc[6] + hi_bf16(wo[c].w) * oc[7];
       }
-      ho.contributions[(static_cast<int64_t>(b) * heads + h) * ho.dim + quarter * nq + tid] = acc;
+      ho.contributions[(static_cast<int64_t>(b) * heads + h) * ho.dim + part_n * nq + tid] = acc;
     }
   }
 }
@@ -338,9 +338,9 @@ hipError_t launch_decode_attention_heads(const uint16_t* q, const uint16_t* k_ne
                                          int window, float scale, const uint16_t* out_weight,
                                          int dim, float* contributions, hipStream_t s) {
   if (batch == 0) return hipSuccess;
-  if (dim % kDecodeHeadsQuarters != 0 || dim / kDecodeHeadsQuarters > 256)
+  if (dim % kDecodeHeadsParts != 0 || dim / kDecodeHeadsParts > 256)
     return hipErrorInvalidValue;
-  return launch_decode<uint16_t, uint16_t, kDecodeHeadsQuarters>(
+  return launch_decode<uint16_t, uint16_t, kDecodeHeadsParts>(
       q, k_new, v_new, k_cache, v_cache, position, batch, heads, kv_heads, head_dim, max_pos,
       window, scale, nullptr, s, HeadsOut{out_weight, dim, contributions});
 }

@@ -58,7 +58,7 @@ def test_decode_attention_window(position):
     assert (got - ref).abs().max() <= 2 ** -8 * ref.abs().max() + 1e-5
 
 
-@pytest.mark.parametrize("batch,position", [(1, 0), (2, 63), (1, 200), (3, 64)])
+@pytest.mark.parametrize("batch,position", [(1, 0), (2, 63), (1, 200), (3, 64), (4, 150)])
 def test_decode_attention_heads(batch, position):
     """The deferred form: the same cache update as decode_attention, and
     per-head contributions equal to the products of decode_attention's own
