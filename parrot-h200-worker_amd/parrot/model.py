@@ -395,8 +395,9 @@ class LocalGQA(nn.Module):
 
     def defers_sum(self, x: Tensor, position_device: Tensor | None) -> bool:
         """Whether decode(defer_sum=True) takes this input: the HIP decode
-        path at at most two rows, which returns the per-head contributions of
-        the output projection instead of their sum."""
+        path at at most hip_moe.DEFER_MAX_TOKENS rows, which returns the
+        per-head contributions of the output projection instead of their
+        sum."""
         if not (self._hip(x) and position_device is not None):
             return False
         from . import hip_moe
@@ -880,8 +881,8 @@ class Parrot(nn.Module):
                           state: GenerationState) -> bool:
         """Whether attention module ``index`` of a decode step leaves its
         output's sum to the MoE's input mix: local layers on the HIP path at
-        at most two rows, when the module does not close a depth block (its
-        output is then read by that mix alone)."""
+        at most hip_moe.DEFER_MAX_TOKENS rows, when the module does not close
+        a depth block (its output is then read by that mix alone)."""
         first = stream.sources()[0]
         return (isinstance(block.attention, LocalGQA) and
                 (index + 1) % self.config.depth_block_size != 0 and
