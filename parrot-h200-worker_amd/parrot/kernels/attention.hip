@@ -79,6 +79,13 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
   __shared__ float f_s[kAttnWaves][kAttnRows];
   __shared__ float o_s[kAttnWaves][D][kAttnRows + 1];
 
+  // The kernel arguments in one batch of scalar loads before any use (a
+  // field first read on its own costs a scalar round trip).
+  asm volatile("" ::"s"(a.q), "s"(a.k), "s"(a.vt), "s"(a.qs[0]), "s"(a.qs[1]), "s"(a.qs[2]),
+               "s"(a.ks[0]), "s"(a.ks[1]), "s"(a.ks[2]), "s"(a.vs[0]), "s"(a.vs[1]),
+               "s"(a.vs[2]), "s"(a.seq), "s"(a.heads), "s"(a.kv_heads), "s"(a.window),
+               "s"(a.scale_log2), "s"(a.out));
+  __builtin_amdgcn_sched_barrier(0);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4;

@@ -18,6 +18,10 @@ __global__ __launch_bounds__(256) void combine_kernel(
     const float4* __restrict__ y_routed, const float4* __restrict__ y_shared,
     const uint2* __restrict__ addend, int64_t tokens, int quads_per_row,
     uint2* __restrict__ out) {
+  // The kernel arguments in one batch of scalar loads before any use.
+  asm volatile("" ::"s"(y_routed), "s"(y_shared), "s"(addend), "s"(tokens), "s"(quads_per_row),
+               "s"(out));
+  __builtin_amdgcn_sched_barrier(0);
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= tokens * quads_per_row) return;
   const int64_t t = i / quads_per_row;

@@ -76,6 +76,19 @@ __device__ __forceinline__ TileIndex xcd_tile(bool rows_per_xcd) {
   return TileIndex{q * 8 + (id & 7), pos - q * nx};
 }
 
+// Every kernel argument a GEMM prologue reads (and the grid width), in one
+// batch of scalar loads before any use: a field first read inside a branch
+// costs a scalar round trip of its own.
+__device__ __forceinline__ void load_gemm_args(const GemmArgs& p) {
+  asm volatile("" ::"s"(p.tokens), "s"(p.dim), "s"(p.experts), "s"(p.hidden_dim),
+               "s"(p.shared_dim), "s"(p.capacity), "s"(p.hstride), "s"(p.counts),
+               "s"(p.offsets), "s"(p.perm), "s"(p.overflow), "s"(p.sorted), "s"(p.indices),
+               "s"(p.w_routed), "s"(p.w_shared), "s"(p.a_src), "s"(p.weights),
+               "s"(p.hidden_out), "s"(p.y_routed), "s"(p.y_shared), "s"(p.counts_out),
+               "s"(p.offsets_out), "s"(p.sorted_out), "s"(p.rows_per_xcd), "s"(gridDim.x));
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // The row tile a workgroup owns: segment `seg` (E = the shared expert),
 // M-tile `mt` of its `rows` rows; the segment's hidden rows start at `hbase`
 // and its part of the overflow list at `obase`.
@@ -384,6 +397,7 @@ void grouped_gemm_kernel(GemmArgs p) {
   // Uniform by construction; readfirstlane lets the compiler keep the
   // per-wavefront load choice (A or B buffer, LDS block) in SGPRs.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  load_gemm_args(p);
   const int T = static_cast<int>(p.tokens);
 
   Tile t;
@@ -589,6 +603,7 @@ void grouped_gemm_wide_kernel(GemmArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  load_gemm_args(p);
   const int T = static_cast<int>(p.tokens);
 
   // XCD-aware tile order.  Workgroups are dispatched round-robin over the 8
@@ -839,14 +854,7 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
   __shared__ int hist_s[4][kMaxExperts];
   __shared__ int chunk_s[kGroupMaxAssign / kWave];
 
-  // Every kernel argument the prologue reads, in one batch of scalar loads:
-  // a field first read inside a branch costs a scalar round trip of its own.
-  asm volatile("" ::"s"(p.tokens), "s"(p.dim), "s"(p.experts), "s"(p.hidden_dim),
-               "s"(p.shared_dim), "s"(p.capacity), "s"(p.hstride), "s"(p.counts),
-               "s"(p.offsets), "s"(p.perm), "s"(p.overflow), "s"(p.sorted), "s"(p.indices),
-               "s"(p.w_routed), "s"(p.w_shared), "s"(p.a_src), "s"(p.weights),
-               "s"(p.hidden_out), "s"(p.y_routed), "s"(p.y_shared), "s"(p.counts_out),
-               "s"(p.offsets_out), "s"(p.sorted_out));
+  load_gemm_args(p);
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;

@@ -21,6 +21,9 @@ template <int MAXC>
 __global__ __launch_bounds__(64) void rms_norm_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     uint16_t* __restrict__ out, int64_t rows, int dim, float eps) {
+  // The kernel arguments in one batch of scalar loads before any use.
+  asm volatile("" ::"s"(x), "s"(w), "s"(out), "s"(rows), "s"(dim), "s"(eps));
+  __builtin_amdgcn_sched_barrier(0);
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;  // uniform per wavefront

@@ -72,6 +72,11 @@ __global__ __launch_bounds__(256) void route_kernel(
     float* __restrict__ probs, float* __restrict__ weights,
     int64_t* __restrict__ indices, int32_t* __restrict__ positions,
     int32_t* __restrict__ block_counts) {
+  // The kernel arguments in one batch of scalar loads before any use.
+  asm volatile("" ::"s"(x), "s"(wr), "s"(given), "s"(bias), "s"(tokens), "s"(dim), "s"(experts),
+               "s"(out_logits), "s"(probs), "s"(weights), "s"(indices), "s"(positions),
+               "s"(block_counts));
+  __builtin_amdgcn_sched_barrier(0);
   __shared__ float part_s[4][kRouteTokensPerBlock][kMaxExperts + 1];
   __shared__ int ids_s[kRouteAssignPerBlock];
   const int lane = threadIdx.x & (kWave - 1);
@@ -163,6 +168,11 @@ __global__ __launch_bounds__(256) void route_wide_kernel(
     float* __restrict__ out_logits, float* __restrict__ probs, float* __restrict__ weights,
     int64_t* __restrict__ indices, int32_t* __restrict__ positions,
     int32_t* __restrict__ block_counts, int n_blocks) {
+  // The kernel arguments in one batch of scalar loads before any use.
+  asm volatile("" ::"s"(x), "s"(wr), "s"(bias), "s"(tokens), "s"(dim), "s"(experts),
+               "s"(out_logits), "s"(probs), "s"(weights), "s"(indices), "s"(positions),
+               "s"(block_counts), "s"(n_blocks));
+  __builtin_amdgcn_sched_barrier(0);
   constexpr int kTokens = 4 * kRouteTokensPerBlock;
   __shared__ float logit_s[kTokens][kMaxExperts + 1];
   __shared__ int ids_s[4 * kRouteAssignPerBlock];
@@ -250,6 +260,10 @@ __global__ __launch_bounds__(256) void route_wide_kernel(
 __global__ __launch_bounds__(64) void rank_indices_kernel(
     const int64_t* __restrict__ indices, int64_t tokens, int experts,
     int32_t* __restrict__ positions, int32_t* __restrict__ block_counts, int n_blocks) {
+  // The kernel arguments in one batch of scalar loads before any use.
+  asm volatile("" ::"s"(indices), "s"(tokens), "s"(experts), "s"(positions), "s"(block_counts),
+               "s"(n_blocks));
+  __builtin_amdgcn_sched_barrier(0);
   // Lanes 0-31 hold route block 2 bx, lanes 32-63 route block 2 bx + 1.
   const int64_t a = static_cast<int64_t>(blockIdx.x) * 2 * kRouteAssignPerBlock + threadIdx.x;
   const int64_t e = a < 2 * tokens ? indices[a] : -1;
@@ -295,6 +309,9 @@ __device__ __forceinline__ int lane_groups(int experts) { return experts <= 16 ?
 __global__ __launch_bounds__(256) void chunk_sum_kernel(const int32_t* __restrict__ block_counts,
                                                         int n_blocks, int experts,
                                                         int32_t* __restrict__ chunk_totals) {
+  // The kernel arguments in one batch of scalar loads before any use.
+  asm volatile("" ::"s"(block_counts), "s"(n_blocks), "s"(experts), "s"(chunk_totals));
+  __builtin_amdgcn_sched_barrier(0);
   __shared__ int part_s[16][kMaxExperts];
   const int n_groups = lane_groups(experts);
   const int e_stride = 256 / n_groups;
@@ -330,6 +347,11 @@ __global__ __launch_bounds__(256) void group_kernel(
     int32_t* __restrict__ positions, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
     int32_t* __restrict__ overflow) {
+  // The kernel arguments in one batch of scalar loads before any use.
+  asm volatile("" ::"s"(indices), "s"(tokens), "s"(experts), "s"(capacity), "s"(n_route_blocks),
+               "s"(block_counts), "s"(chunk_totals), "s"(n_chunks), "s"(positions), "s"(counts),
+               "s"(offsets), "s"(perm), "s"(overflow));
+  __builtin_amdgcn_sched_barrier(0);
   __shared__ int before_s[16][kMaxExperts];
   __shared__ int total_s[16][kMaxExperts];
   __shared__ int base_s[kBlocksPerGroup][kMaxExperts];

@@ -120,6 +120,9 @@ __device__ __forceinline__ void keep_better(float pv, int pi, float& v, int& i) 
 __global__ __launch_bounds__(256) void vocab_argmax_reduce_kernel(
     const float* __restrict__ part_v, const int32_t* __restrict__ part_i, int groups,
     int64_t* __restrict__ out, int32_t* __restrict__ advance) {
+  // The kernel arguments in one batch of scalar loads before any use.
+  asm volatile("" ::"s"(part_v), "s"(part_i), "s"(groups), "s"(out), "s"(advance));
+  __builtin_amdgcn_sched_barrier(0);
   __shared__ float vs[4];
   __shared__ int is[4];
   const int r = blockIdx.x;
