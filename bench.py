@@ -298,7 +298,17 @@ def attained_peaks() -> dict:
     return res
 
 
-def layer_kernels(moe, x, iters, logit_bias=None) -> tuple[dict, "StageBench"]:
+def trace_marker(sb: "StageBench") -> None:
+    """A 16-byte parrot_peak_copy on the stage stream: in a kernel trace of
+    bench.py it opens the roofline kernel's timed loop (summarize_trace)."""
+    from parrot import _abi
+    buf = sb.torch.zeros(32, dtype=sb.torch.uint8, device=sb.x.device)
+    _abi.check(sb.lib.parrot_peak_copy(sb.ptr(buf), sb.ptr(buf[16:]), 16, 1,
+                                       sb.stream.cuda_stream), "trace marker")
+
+
+def layer_kernels(moe, x, iters, logit_bias=None, mark_roofline=False
+                  ) -> tuple[dict, "StageBench"]:
     sb = StageBench(moe, x, logit_bias)
     res = {
         "route_group": entry(event_time_us(sb.route, iters, sb.stream), sb.bytes_route()),
@@ -312,6 +322,8 @@ def layer_kernels(moe, x, iters, logit_bias=None) -> tuple[dict, "StageBench"]:
     }
     if sb.in_kernel:
         # gate/up grouping first: down_sorted reads the grouping it writes.
+        if mark_roofline:
+            trace_marker(sb)
         res["gate_up_grouping"] = entry(event_time_us(sb.gate_up_grouping, iters, sb.stream),
                                         sb.bytes_gate_up() + sb.bytes_grouping(),
                                         sb.flops_gate_up())
@@ -830,8 +842,8 @@ TRACE_FILE = ROOT / "profiles" / "kernel_trace_bench.json"
 def summarize_trace(directory: str) -> dict:
     """Per-kernel dispatch counts and mean durations of a rocprofv3
     --kernel-trace run of bench.py; for the roofline kernel, the dispatches
-    of its timed back-to-back loop (runs of >= 20 in a row) apart from those
-    inside the graph-replayed forwards."""
+    of its timed back-to-back loop (the run after bench.py's marker copy)
+    apart from those inside the graph-replayed forwards (runs of < 20)."""
     import csv
     rows = []
     for path in sorted(Path(directory).rglob("*kernel_trace.csv")):
@@ -843,13 +855,22 @@ def summarize_trace(directory: str) -> dict:
     stats: dict[str, list[int]] = {}
     for _, name, ns in rows:
         stats.setdefault(name, []).append(ns)
-    loop, graph, run = [], [], []
+    # The timed loop: the run of the roofline kernel right after the 16-byte
+    # marker copy bench.py issues before it (its 5 warm-up launches
+    # included); the in-forward dispatches: its runs shorter than 20.
+    loop, graph, run, after_marker, prev = [], [], [], False, ""
     for _, name, ns in rows + [(None, "", 0)]:
         if TRAFFIC_KERNEL in name:
+            if not run:
+                after_marker = all(part in prev for part in MARKER_KERNEL)
             run.append(ns)
+            prev = name
             continue
-        (loop if len(run) >= 20 else graph).extend(run)
-        run = []
+        if run and after_marker and not loop:
+            loop.extend(run)
+        elif len(run) < 20:
+            graph.extend(run)
+        run, prev = [], name
     summary = {
         "roofline_kernel": TRAFFIC_KERNEL,
         "loop_dispatches": len(loop),
@@ -993,7 +1014,7 @@ def main():
         peaks = attained_peaks()
         ATTAINED.update(peaks)
         log("per-kernel timing")
-        c4, _ = layer_kernels(moe0, captured["x"], args.kernel_iters)
+        c4, _ = layer_kernels(moe0, captured["x"], args.kernel_iters, mark_roofline=True)
         kernels["C4_in_model_T512_E16"] = c4
         kernels.update(norm_kernels(model, args.kernel_iters))
         for name, tokens, skew in (("C2_T256_E32", 256, False), ("C3_T4096_E32_skew", 4096, True)):

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   asm volatile("" ::"s"(sp[0]), "s"(sp[1]), "s"(sp[2]), "s"(sp[3]), "s"(sp[4]), "s"(sp[5]),
                "s"(sp[6]), "s"(sp[7]), "s"(sp[8]), "s"(comb.y_shared), "s"(comb.y_routed),
                "s"(comb.addend), "s"(query), "s"(score_w), "s"(out_w), "s"(out_norm),
-               "s"(n_sources), "s"(dim), "s"(comb.out), "s"(out_mix));
+               "s"(n_sources), "s"(dim), "s"(comb.out), "s"(out_mix), "s"(blockDim.x));
   if constexpr (ROUTE > 0)
     asm volatile("" ::"s"(route.router_w), "s"(route.bias), "s"(route.experts),
                  "s"(route.weights), "s"(route.indices));
