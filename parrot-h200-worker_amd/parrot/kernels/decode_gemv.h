@@ -71,17 +71,21 @@ __device__ __forceinline__ void load_row_chunks_n(const uint16_t* w, int row, in
   for (int c = 0; c < NCH; ++c) wr[c] = src[min(c, last) * 16 + p];
 }
 
-// The chunk counts those kernels are instantiated for; K / 128 rounds up to
-// the next.  `launch` is called with std::integral_constant<int, NCH>.
-template <typename F>
+// The chunk counts those kernels are instantiated for, up to MAX; K / 128
+// rounds up to the next, and K past 128 MAX is rejected.  `launch` is
+// called with std::integral_constant<int, NCH>.
+template <int MAX = kGemvMaxChunks, typename F>
 __host__ hipError_t with_gemv_chunks(int K, F&& launch) {
   const int nch = K / 128;
   if (nch <= 2) return launch(std::integral_constant<int, 2>{});
   if (nch <= 4) return launch(std::integral_constant<int, 4>{});
   if (nch <= 6) return launch(std::integral_constant<int, 6>{});
   if (nch <= 8) return launch(std::integral_constant<int, 8>{});
-  if (nch <= 12) return launch(std::integral_constant<int, 12>{});
-  return launch(std::integral_constant<int, 16>{});
+  if constexpr (MAX > 8) {
+    if (nch <= 12) return launch(std::integral_constant<int, 12>{});
+    if (nch <= 16) return launch(std::integral_constant<int, 16>{});
+  }
+  return hipErrorInvalidValue;
 }
 
 // Copies `bytes` (a multiple of 16) from global memory into LDS.

@@ -137,7 +137,7 @@ __device__ __forceinline__ void route_slot(const uint16_t* x_lds,
   __syncthreads();
 }
 
-template <int ROUTE, bool MIX>
+template <int ROUTE, int NS>
 __global__ __launch_bounds__(256) void decode_up_kernel(
     const uint16_t* __restrict__ x, DecodeMix mix, const uint16_t* __restrict__ wr,
     const float* __restrict__ bias, int tokens, int dim, int experts, int hidden_dim,
@@ -153,15 +153,14 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   // The kernel arguments of the load phase in one batch of scalar loads
   // (each field first read on its own would cost a scalar round trip).
-  if constexpr (MIX) {
+  if constexpr (NS > 0) {
     const uint16_t* sp[kMaxDepthSources];
 #pragma unroll
     for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = mix.srcs.src[s];
     static_assert(kMaxDepthSources == 9, "the batch below names every source slot");
     asm volatile("" ::"s"(sp[0]), "s"(sp[1]), "s"(sp[2]), "s"(sp[3]), "s"(sp[4]), "s"(sp[5]),
                  "s"(sp[6]), "s"(sp[7]), "s"(sp[8]), "s"(mix.query), "s"(mix.score_w),
-                 "s"(mix.out_w), "s"(mix.pend), "s"(mix.pend_lanes), "s"(mix.pend_base),
-                 "s"(mix.n_sources));
+                 "s"(mix.out_w), "s"(mix.pend), "s"(mix.pend_lanes), "s"(mix.pend_base));
   }
   asm volatile("" ::"s"(wr), "s"(tokens), "s"(dim), "s"(experts), "s"(hidden_dim),
                "s"(shared_dim));
@@ -193,18 +192,17 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
         rb[i][h] = __builtin_bit_cast(
             bf16x8, *reinterpret_cast<const uint4*>(pb[h] + min(wave + 4 * i, last) * 32));
   };
-  if constexpr (MIX) {
-    // The token's input row: depth mix + RMSNorm of its sources into LDS,
-    // every load issued before the first wait (lanes past the row read
-    // chunk 0 and are zeroed, unread slots read source 0 and are zeroed).
+  if constexpr (NS > 0) {
+    // The token's input row: depth mix + RMSNorm of its NS sources into
+    // LDS, every load issued before the first wait (lanes past the row read
+    // chunk 0 and are zeroed).
     const int chunks = dim >> 2;
     const bool has = tid < chunks;
     const int ic = has ? tid : 0;
     const int64_t base = static_cast<int64_t>(t0) * chunks;
     uint2 v[kMaxDepthSources];
 #pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s)
-      v[s] = reinterpret_cast<const uint2*>(mix.srcs.src[s])[base + ic];
+    for (int s = 0; s < NS; ++s) v[s] = reinterpret_cast<const uint2*>(mix.srcs.src[s])[base + ic];
     const uint2 q = reinterpret_cast<const uint2*>(mix.query)[ic];
     const uint2 g = reinterpret_cast<const uint2*>(mix.score_w)[ic];
     const uint2 g_out = reinterpret_cast<const uint2*>(mix.out_w)[ic];
@@ -254,18 +252,16 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
         r.x = pack_bf16x2(lo_bf16(pbv.x) + lo_bf16(r.x), hi_bf16(pbv.x) + hi_bf16(r.x));
         r.y = pack_bf16x2(lo_bf16(pbv.y) + lo_bf16(r.y), hi_bf16(pbv.y) + hi_bf16(r.y));
       }
-#pragma unroll
-      for (int s = 0; s < kMaxDepthSources; ++s)
-        if (s == mix.n_sources - 1) v[s] = r;
+      v[NS - 1] = r;
       if (has && !shared && slice == 0 && (slot & 1) == 0)
         reinterpret_cast<uint2*>(mix.pend_out)[base + ic] = r;
     }
 #pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s)
-      if (!has || s >= mix.n_sources) v[s] = make_uint2(0u, 0u);
+    for (int s = 0; s < NS; ++s)
+      if (!has) v[s] = make_uint2(0u, 0u);
     const int waves = (dim + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
-    const uint2 mixed = depth_mix_chunk(v, q, g, has, mix.n_sources, waves, wave, lane, dim,
-                                        mix.score_eps, mix_lds);
+    const uint2 mixed =
+        depth_mix_chunk<NS>(v, q, g, has, waves, wave, lane, dim, mix.score_eps, mix_lds);
     const uint2 o = depth_mix_norm_chunk(mixed, g_out, has, waves, wave, lane, dim, mix.out_eps,
                                          mix_lds);
     if (has) reinterpret_cast<uint2*>(xs)[tid] = o;
@@ -448,11 +444,16 @@ hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens
                                         shared_dim, hstride, w.gate_up, w.shared_gate_up, hidden,
                                         indices, weights);
   };
-  if (experts <= 16)
-    mixing ? up(decode_up_kernel<1, true>) : up(decode_up_kernel<1, false>);
+  hipError_t e = hipSuccess;
+  if (mixing)
+    e = with_sources(m.n_sources, [&](auto ns) {
+      experts <= 16 ? up(decode_up_kernel<1, ns>) : up(decode_up_kernel<2, ns>);
+      return hipSuccess;
+    });
   else
-    mixing ? up(decode_up_kernel<2, true>) : up(decode_up_kernel<2, false>);
-  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    experts <= 16 ? up(decode_up_kernel<1, 0>) : up(decode_up_kernel<2, 0>);
+  if (e == hipSuccess) e = hipGetLastError();
+  if (e != hipSuccess) return e;
   decode_down_kernel<<<dim3(dim / 16, tokens), 256, 0, s>>>(
       hidden, tokens, dim, hidden_dim, shared_dim, hstride, indices, weights, w.down,
       w.shared_down, addend, out);

@@ -30,7 +30,7 @@ constexpr int kQkvMaxDim = 1024;  // the mix holds a row with 4 wavefronts of 25
 // device position (a scalar load), the input row's sources, the weight
 // chunks (NCH per lane, unconditional), then the position's cos / sin.  The
 // mix waits only for its sources; the weights arrive while it runs.
-template <bool MIX, int NCH>
+template <int NS, int NCH>  // NS > 0: the input is the depth mix of NS sources
 __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
   __shared__ DepthMixLds mix_lds;
   __shared__ __attribute__((aligned(16))) uint16_t xs[kQkvMaxDim];
@@ -59,7 +59,8 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
   const int chunks = K >> 2;
   const bool has = tid < chunks;
   DecodeMixLoads ml;
-  if constexpr (MIX) decode_mix_load(m, static_cast<int64_t>(t) * chunks, has ? tid : 0, ml);
+  if constexpr (NS > 0)
+    decode_mix_load<NS>(m, static_cast<int64_t>(t) * chunks, has ? tid : 0, ml);
   asm volatile("" ::: "memory");
   uint4 wr[NCH];
   load_row_chunks_n<NCH>(a.w, col, K, p, wr);
@@ -70,9 +71,9 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
   const float rc = a.cos_t[ti], rs = a.sin_t[ti];
   asm volatile("" ::: "memory");
 
-  if constexpr (MIX) {
+  if constexpr (NS > 0) {
     // Token t's input row: depth mix + RMSNorm of its sources into LDS.
-    const uint2 o = decode_mix_row(m, ml, has, wave, lane, K, mix_lds);
+    const uint2 o = decode_mix_row<NS>(m, ml, has, wave, lane, K, mix_lds);
     if (has) reinterpret_cast<uint2*>(xs)[tid] = o;
   } else {
     for (int i = tid; i < K / 8; i += 256)
@@ -113,11 +114,15 @@ hipError_t launch_decode_qkv(const DecodeQkvArgs& a, hipStream_t s) {
   if (a.tokens == 0) return hipSuccess;
   const int n = (a.heads + 2 * a.kv_heads) * a.head_dim;
   const dim3 grid(n / kGemvRows, a.tokens);
-  const bool mixing = a.mix.n_sources > 0;
-  return with_gemv_chunks(a.dim, [&](auto nch) {
-    if (mixing) decode_qkv_kernel<true, nch><<<grid, 256, 0, s>>>(a);
-    else decode_qkv_kernel<false, nch><<<grid, 256, 0, s>>>(a);
-    return hipGetLastError();
+  return with_gemv_chunks<8>(a.dim, [&](auto nch) {
+    if (a.mix.n_sources == 0) {
+      decode_qkv_kernel<0, nch><<<grid, 256, 0, s>>>(a);
+      return hipGetLastError();
+    }
+    return with_sources(a.mix.n_sources, [&](auto ns) {
+      decode_qkv_kernel<ns, nch><<<grid, 256, 0, s>>>(a);
+      return hipGetLastError();
+    });
   });
 }
 

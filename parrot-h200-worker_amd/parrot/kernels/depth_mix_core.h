@@ -14,6 +14,8 @@
 // wavefront order, so every wavefront derives the same scores; the output
 // norm's sum of squares likewise.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace parrot {
@@ -26,13 +28,16 @@ struct __attribute__((aligned(8))) DepthMixLds {
   float part_out[kDepthMaxWaves];
 };
 
-// The mix of this lane's chunk as packed bf16.  v: the chunk of each source
-// slot (zeros for unread slots and lanes past the row); q, g: the chunk of
-// the query and of the score norm's weight.  Contains one barrier.
+// The mix of this lane's chunk as packed bf16 over NS sources (a compile-time
+// count: the loops below then hold only the sources read, which at one to
+// five sources halves the instructions of a runtime count with guards).
+// v: the chunk of each source (zeros for lanes past the row); q, g: the chunk
+// of the query and of the score norm's weight.  Contains one barrier.
+template <int NS>
 __device__ __forceinline__ uint2 depth_mix_chunk(const uint2 (&v)[kMaxDepthSources], uint2 q,
-                                                 uint2 g, bool has, int n_sources, int waves,
-                                                 int wave, int lane, int dim, float score_eps,
-                                                 DepthMixLds& sh) {
+                                                 uint2 g, bool has, int waves, int wave, int lane,
+                                                 int dim, float score_eps, DepthMixLds& sh) {
+  static_assert(NS >= 1 && NS <= kMaxDepthSources, "one to kMaxDepthSources sources");
   float wq[4] = {0.f, 0.f, 0.f, 0.f};
   if (has) {
     wq[0] = lo_bf16(q.x) * lo_bf16(g.x);
@@ -42,28 +47,24 @@ __device__ __forceinline__ uint2 depth_mix_chunk(const uint2 (&v)[kMaxDepthSourc
   }
 
   // Per-source partial sums, all wavefront reductions back to back.
-  float ss[kMaxDepthSources], dq[kMaxDepthSources];
+  float ss[NS], dq[NS];
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const float e0 = lo_bf16(v[s].x), e1 = hi_bf16(v[s].x);
     const float e2 = lo_bf16(v[s].y), e3 = hi_bf16(v[s].y);
     ss[s] = e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3;
     dq[s] = e0 * wq[0] + e1 * wq[1] + e2 * wq[2] + e3 * wq[3];
   }
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) {
-    if (s < n_sources) {
-      ss[s] = wave_sum(ss[s]);
-      dq[s] = wave_sum(dq[s]);
-    }
+  for (int s = 0; s < NS; ++s) {
+    ss[s] = wave_sum(ss[s]);
+    dq[s] = wave_sum(dq[s]);
   }
   if (lane == 0) {
 #pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s) {
-      if (s < n_sources) {
-        sh.part[wave][2 * s] = ss[s];
-        sh.part[wave][2 * s + 1] = dq[s];
-      }
+    for (int s = 0; s < NS; ++s) {
+      sh.part[wave][2 * s] = ss[s];
+      sh.part[wave][2 * s + 1] = dq[s];
     }
   }
   __syncthreads();
@@ -71,48 +72,40 @@ __device__ __forceinline__ uint2 depth_mix_chunk(const uint2 (&v)[kMaxDepthSourc
   // Cross-wavefront sums in wavefront order.  The loop bounds are
   // compile-time (uniform guards inside), so each wavefront row's LDS reads
   // go out together instead of one read, wait and add at a time.
-  float sst[kMaxDepthSources], dqt[kMaxDepthSources];
+  float sst[NS], dqt[NS];
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) sst[s] = dqt[s] = 0.0f;
+  for (int s = 0; s < NS; ++s) sst[s] = dqt[s] = 0.0f;
 #pragma unroll
   for (int w = 0; w < kDepthMaxWaves; ++w) {
     if (w < waves) {
 #pragma unroll
-      for (int s = 0; s < kMaxDepthSources; ++s) {
-        if (s < n_sources) {
-          const float2 pv = *reinterpret_cast<const float2*>(&sh.part[w][2 * s]);
-          sst[s] += pv.x;
-          dqt[s] += pv.y;
-        }
+      for (int s = 0; s < NS; ++s) {
+        const float2 pv = *reinterpret_cast<const float2*>(&sh.part[w][2 * s]);
+        sst[s] += pv.x;
+        dqt[s] += pv.y;
       }
     }
   }
-  float score[kMaxDepthSources];
+  float score[NS];
   float mx = -INFINITY;
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) {
-    score[s] = -INFINITY;
-    if (s < n_sources) {
-      score[s] = dqt[s] * rsqrtf(sst[s] / static_cast<float>(dim) + score_eps);
-      mx = fmaxf(mx, score[s]);
-    }
+  for (int s = 0; s < NS; ++s) {
+    score[s] = dqt[s] * rsqrtf(sst[s] / static_cast<float>(dim) + score_eps);
+    mx = fmaxf(mx, score[s]);
   }
   float denom = 0.0f;
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s)
-    if (s < n_sources) denom += __expf(score[s] - mx);
+  for (int s = 0; s < NS; ++s) denom += __expf(score[s] - mx);
   const float inv = 1.0f / denom;
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) {
-    if (s < n_sources) {
-      const float a = __expf(score[s] - mx) * inv;
-      acc[0] += a * lo_bf16(v[s].x);
-      acc[1] += a * hi_bf16(v[s].x);
-      acc[2] += a * lo_bf16(v[s].y);
-      acc[3] += a * hi_bf16(v[s].y);
-    }
+  for (int s = 0; s < NS; ++s) {
+    const float a = __expf(score[s] - mx) * inv;
+    acc[0] += a * lo_bf16(v[s].x);
+    acc[1] += a * hi_bf16(v[s].x);
+    acc[2] += a * lo_bf16(v[s].y);
+    acc[3] += a * hi_bf16(v[s].y);
   }
   uint2 mixed;
   mixed.x = pack_bf16x2(acc[0], acc[1]);
@@ -143,34 +136,54 @@ __device__ __forceinline__ uint2 depth_mix_norm_chunk(uint2 mixed, uint2 g_out, 
 
 // Decode kernels that mix their own input row (one token per workgroup,
 // lane chunk i = threadIdx.x): decode_mix_load issues the loads of the
-// chunk (every source slot; lanes past the row read chunk 0) without waiting
+// chunk (the NS sources; lanes past the row read chunk 0) without waiting
 // for them, so a kernel can issue its weight loads behind them;
-// decode_mix_row zeroes unread slots and lanes past the row, then mixes and
-// normalises (two barriers).
+// decode_mix_row zeroes lanes past the row, then mixes and normalises (two
+// barriers).
 struct DecodeMixLoads {
   uint2 v[kMaxDepthSources];
   uint2 q, g, g_out;
 };
 
+template <int NS>
 __device__ __forceinline__ void decode_mix_load(const DecodeMix& m, int64_t base, int ic,
                                                 DecodeMixLoads& l) {
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s)
-    l.v[s] = reinterpret_cast<const uint2*>(m.srcs.src[s])[base + ic];
+  for (int s = 0; s < NS; ++s) l.v[s] = reinterpret_cast<const uint2*>(m.srcs.src[s])[base + ic];
   l.q = reinterpret_cast<const uint2*>(m.query)[ic];
   l.g = reinterpret_cast<const uint2*>(m.score_w)[ic];
   l.g_out = reinterpret_cast<const uint2*>(m.out_w)[ic];
 }
 
+template <int NS>
 __device__ __forceinline__ uint2 decode_mix_row(const DecodeMix& m, DecodeMixLoads& l, bool has,
                                                 int wave, int lane, int dim, DepthMixLds& sh) {
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s)
-    if (!has || s >= m.n_sources) l.v[s] = make_uint2(0u, 0u);
+  for (int s = 0; s < NS; ++s)
+    if (!has) l.v[s] = make_uint2(0u, 0u);
   const int waves = (dim + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
   const uint2 mixed =
-      depth_mix_chunk(l.v, l.q, l.g, has, m.n_sources, waves, wave, lane, dim, m.score_eps, sh);
+      depth_mix_chunk<NS>(l.v, l.q, l.g, has, waves, wave, lane, dim, m.score_eps, sh);
   return depth_mix_norm_chunk(mixed, l.g_out, has, waves, wave, lane, dim, m.out_eps, sh);
+}
+
+// Calls `launch` with std::integral_constant<int, n> for a source count n
+// in 1 .. kMaxDepthSources (the kernels' NS); other counts are rejected.
+template <typename F>
+__host__ hipError_t with_sources(int n, F&& launch) {
+  static_assert(kMaxDepthSources == 9, "the cases below name every count");
+  switch (n) {
+    case 1: return launch(std::integral_constant<int, 1>{});
+    case 2: return launch(std::integral_constant<int, 2>{});
+    case 3: return launch(std::integral_constant<int, 3>{});
+    case 4: return launch(std::integral_constant<int, 4>{});
+    case 5: return launch(std::integral_constant<int, 5>{});
+    case 6: return launch(std::integral_constant<int, 6>{});
+    case 7: return launch(std::integral_constant<int, 7>{});
+    case 8: return launch(std::integral_constant<int, 8>{});
+    case 9: return launch(std::integral_constant<int, 9>{});
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace parrot

@@ -35,14 +35,14 @@ namespace {
 // out first (the kernel arguments in one scalar batch before them), then the
 // weight chunks (NCH per lane, unconditional), so the mix waits only for its
 // sources and the weights arrive while it runs.
-template <bool MIX, int NCH>
+template <int NS, int NCH>  // NS > 0: each token's input is the depth mix of NS sources
 __global__ __launch_bounds__(256) void mla_decode_in_kernel(
     const uint16_t* __restrict__ x, DecodeMix mix, int tokens, int K,
     const uint16_t* __restrict__ wq, int nq, const uint16_t* __restrict__ wkv, int nl,
     float* __restrict__ q_out, uint16_t* __restrict__ lat_out) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   __shared__ DepthMixLds mix_lds;
-  if constexpr (MIX) {
+  if constexpr (NS > 0) {
     const uint16_t* sp[kMaxDepthSources];
 #pragma unroll
     for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = mix.srcs.src[s];
@@ -58,17 +58,18 @@ __global__ __launch_bounds__(256) void mla_decode_in_kernel(
   const int row = (is_q ? blockIdx.x : blockIdx.x - blocks_q) * kGemvRows + j;
   const int chunks = K >> 2;
   const bool has = tid < chunks;
-  const int t_begin = MIX ? static_cast<int>(blockIdx.y) : 0;
-  const int t_end = MIX ? t_begin + 1 : tokens;
+  const int t_begin = NS > 0 ? static_cast<int>(blockIdx.y) : 0;
+  const int t_end = NS > 0 ? t_begin + 1 : tokens;
   DecodeMixLoads ml;
-  if constexpr (MIX) decode_mix_load(mix, static_cast<int64_t>(t_begin) * chunks, has ? tid : 0, ml);
+  if constexpr (NS > 0)
+    decode_mix_load<NS>(mix, static_cast<int64_t>(t_begin) * chunks, has ? tid : 0, ml);
   asm volatile("" ::: "memory");
   uint4 wr[NCH];
   load_row_chunks_n<NCH>(is_q ? wq : wkv, row, K, p, wr);
   asm volatile("" ::: "memory");
-  if constexpr (MIX) {
+  if constexpr (NS > 0) {
     const int lane = tid & (kWave - 1), wave = tid >> 6;
-    const uint2 o = decode_mix_row(mix, ml, has, wave, lane, K, mix_lds);
+    const uint2 o = decode_mix_row<NS>(mix, ml, has, wave, lane, K, mix_lds);
     if (has) reinterpret_cast<uint2*>(xs)[tid] = o;
   } else {
     stage(x, xs, tokens * K * 2);
@@ -177,14 +178,18 @@ hipError_t launch_mla_decode_in(const uint16_t* x, const DecodeMix* mix, int tok
   const DecodeMix m = mixing ? *mix : DecodeMix{};
   const dim3 grid((nq + nl) / kGemvRows, mixing ? tokens : 1);
   const size_t lds = mla_decode_lds_bytes(mixing ? 1 : tokens, dim, 2);
-  return with_gemv_chunks(dim, [&](auto nch) {
-    if (mixing)
-      mla_decode_in_kernel<true, nch><<<grid, 256, lds, s>>>(x, m, tokens, dim, wq, nq, wkv, nl,
-                                                             q_out, lat_out);
-    else
-      mla_decode_in_kernel<false, nch><<<grid, 256, lds, s>>>(x, m, tokens, dim, wq, nq, wkv,
-                                                              nl, q_out, lat_out);
-    return hipGetLastError();
+  if (!mixing)
+    return with_gemv_chunks(dim, [&](auto nch) {
+      mla_decode_in_kernel<0, nch><<<grid, 256, lds, s>>>(x, m, tokens, dim, wq, nq, wkv, nl,
+                                                          q_out, lat_out);
+      return hipGetLastError();
+    });
+  return with_gemv_chunks<8>(dim, [&](auto nch) {
+    return with_sources(m.n_sources, [&](auto ns) {
+      mla_decode_in_kernel<ns, nch><<<grid, 256, lds, s>>>(x, m, tokens, dim, wq, nq, wkv, nl,
+                                                           q_out, lat_out);
+      return hipGetLastError();
+    });
   });
 }
 

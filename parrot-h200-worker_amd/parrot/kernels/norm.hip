@@ -77,9 +77,9 @@ __global__ __launch_bounds__(64) void rms_norm_kernel(
 constexpr int kRouteChainSlots = 2;
 constexpr int kRouteStepSlots = 6;
 
-template <int ROUTE>
+template <int ROUTE, int NS>
 __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
-    DepthSources srcs, int n_sources, const uint16_t* __restrict__ query,
+    DepthSources srcs, const uint16_t* __restrict__ query,
     const uint16_t* __restrict__ score_w, float score_eps,
     const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
     uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm, CombineSource comb,
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   asm volatile("" ::"s"(sp[0]), "s"(sp[1]), "s"(sp[2]), "s"(sp[3]), "s"(sp[4]), "s"(sp[5]),
                "s"(sp[6]), "s"(sp[7]), "s"(sp[8]), "s"(comb.y_shared), "s"(comb.y_routed),
                "s"(comb.addend), "s"(query), "s"(score_w), "s"(out_w), "s"(out_norm),
-               "s"(n_sources), "s"(dim), "s"(comb.out), "s"(out_mix), "s"(blockDim.x));
+               "s"(dim), "s"(comb.out), "s"(out_mix), "s"(blockDim.x));
   if constexpr (ROUTE > 0)
     asm volatile("" ::"s"(route.router_w), "s"(route.bias), "s"(route.experts),
                  "s"(route.weights), "s"(route.indices));
@@ -108,19 +108,17 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   const bool has = i < chunks;
   const int64_t base = tok * chunks;
 
-  // Every load of the workgroup is issued before the first wait.  All
-  // source slots are loaded (unread slots hold a valid row, cached after the
-  // first read) and the unread ones zeroed afterwards, lanes past the row
-  // load chunk 0 and zero it afterwards, and only uniform conditions
-  // (combine, addend, output norm) guard a load: a load behind a branch on
-  // a kernel argument, or inside a per-lane branch, costs a serial round
-  // trip each.
+  // Every load of the workgroup is issued before the first wait.  The NS
+  // source slots are loaded (with a combine, the last one too: it holds a
+  // valid row and is replaced below), lanes past the row load chunk 0 and
+  // zero it afterwards, and only uniform conditions (combine, addend, output
+  // norm) guard a load: a load behind a branch on a kernel argument, or
+  // inside a per-lane branch, costs a serial round trip each.
   const bool combine = comb.y_shared != nullptr;
-  const int n_read = combine ? n_sources - 1 : n_sources;
   const int ic = has ? i : 0;
   uint2 v[kMaxDepthSources];
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s) v[s] = reinterpret_cast<const uint2*>(sp[s])[base + ic];
+  for (int s = 0; s < NS; ++s) v[s] = reinterpret_cast<const uint2*>(sp[s])[base + ic];
   float4 sh = {0.f, 0.f, 0.f, 0.f}, y0 = sh, y1 = sh;
   uint2 pa = make_uint2(0u, 0u);
   if (combine) {
@@ -155,10 +153,10 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
       }
   }
 
-  // Unread slots and lanes past the row hold zeros from here on.
+  // Lanes past the row hold zeros from here on.
 #pragma unroll
-  for (int s = 0; s < kMaxDepthSources; ++s)
-    if (!has || s >= n_read) v[s] = make_uint2(0u, 0u);
+  for (int s = 0; s < NS; ++s)
+    if (!has) v[s] = make_uint2(0u, 0u);
   if (combine) {
     // The MoE output row: bf16(shared + routed 0 + routed 1), then
     // bf16(addend + that), exactly as the combine kernel; it is the new
@@ -172,12 +170,9 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     }
     if (has) reinterpret_cast<uint2*>(comb.out)[base + i] = o;
     else o = make_uint2(0u, 0u);
-#pragma unroll
-    for (int s = 0; s < kMaxDepthSources; ++s)
-      if (s == n_sources - 1) v[s] = o;
+    v[NS - 1] = o;
   }
-  const uint2 mixed =
-      depth_mix_chunk(v, q, g, has, n_sources, waves, wave, lane, dim, score_eps, mix_lds);
+  const uint2 mixed = depth_mix_chunk<NS>(v, q, g, has, waves, wave, lane, dim, score_eps, mix_lds);
   if (out_mix != nullptr && has) reinterpret_cast<uint2*>(out_mix)[base + i] = mixed;
   if (out_norm == nullptr) return;  // uniform over the workgroup
   const uint2 o = depth_mix_norm_chunk(mixed, g_out, has, waves, wave, lane, dim, out_eps,
@@ -284,19 +279,23 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
   if (waves > kDepthMaxWaves) return hipErrorInvalidValue;
   const CombineSource none{};
   const RouteOut no_route{};
-  if (route != nullptr && route->experts > 16)
-    depth_mix_kernel<2><<<static_cast<unsigned>(tokens), kWave * waves, 0, s>>>(
-        srcs, n_sources, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
-        out_norm, comb != nullptr ? *comb : none, *route);
-  else if (route != nullptr)
-    depth_mix_kernel<1><<<static_cast<unsigned>(tokens), kWave * waves, 0, s>>>(
-        srcs, n_sources, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
-        out_norm, comb != nullptr ? *comb : none, *route);
-  else
-    depth_mix_kernel<0><<<static_cast<unsigned>(tokens), kWave * waves, 0, s>>>(
-        srcs, n_sources, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
-        out_norm, comb != nullptr ? *comb : none, no_route);
-  return hipGetLastError();
+  const CombineSource c = comb != nullptr ? *comb : none;
+  const unsigned grid = static_cast<unsigned>(tokens);
+  return with_sources(n_sources, [&](auto ns) {
+    if (route != nullptr && route->experts > 16)
+      depth_mix_kernel<2, ns><<<grid, kWave * waves, 0, s>>>(
+          srcs, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix, out_norm,
+          c, *route);
+    else if (route != nullptr)
+      depth_mix_kernel<1, ns><<<grid, kWave * waves, 0, s>>>(
+          srcs, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix, out_norm,
+          c, *route);
+    else
+      depth_mix_kernel<0, ns><<<grid, kWave * waves, 0, s>>>(
+          srcs, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix, out_norm,
+          c, no_route);
+    return hipGetLastError();
+  });
 }
 
 }  // namespace parrot
