@@ -14,14 +14,15 @@
 // At decode sizes the layer is a weight stream of ~2 x 2.4 MB per token plus
 // the shared expert, and launch latency dominates; the grouped path spends 5
 // launches (route, group, gate/up, down, combine).  Here:
-//   decode_up_kernel   grid (max(H, Hs) / 16 slices, 3T slots): slot 2t + k
+//   decode_up_kernel   grid (max(H, Hs) / SW slices, 3T slots): slot 2t + k
 //       is token t's k-th routed expert, slot 2T + t token t's shared expert.
 //       A routed workgroup recomputes its token's router logits and top-2
 //       (every workgroup of a token does the same arithmetic in the same
-//       order, so they agree), then one 16-column slice of SwiGLU.  Given the
-//       MoE input's depth sources instead of the input, every workgroup first
-//       mixes and normalises its token's row itself (depth_mix_core.h, the
-//       depth-mix kernel's arithmetic), which saves that kernel's launch.
+//       order, so they agree), then one SW-column slice of SwiGLU (SW = 8
+//       at one or two tokens, else 16).  Given the MoE input's depth sources
+//       instead of the input, every workgroup first mixes and normalises its
+//       token's row itself (depth_mix_core.h, the depth-mix kernel's
+//       arithmetic), which saves that kernel's launch.
 //   decode_down_kernel grid (dim / 16 slices, T): 16 output columns of one
 //       token: both weighted routed rows and the shared row, summed in the
 //       combine kernel's order, with the addend folded in.
@@ -137,7 +138,7 @@ __device__ __forceinline__ void route_slot(const uint16_t* x_lds,
   __syncthreads();
 }
 
-template <int ROUTE, int NS>
+template <int ROUTE, int NS, int SW>  // SW: hidden columns per workgroup (8 or 16)
 __global__ __launch_bounds__(256) void decode_up_kernel(
     const uint16_t* __restrict__ x, DecodeMix mix, const uint16_t* __restrict__ wr,
     const float* __restrict__ bias, int tokens, int dim, int experts, int hidden_dim,
@@ -147,7 +148,9 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   __shared__ float chain_s[4][kMaxExperts];
   __shared__ int sel[2];
   __shared__ float sel_w[2];
-  __shared__ float part[4][4][32];  // [wave][k chunk][gate 16 | up 16]
+  // SW = 16: [wave][k chunk][gate 16 | up 16]; SW = 8: [wave][k chunk, step
+  // parity][gate 8 | up 8].
+  __shared__ float part[4][SW == 16 ? 4 : 8][2 * SW];
   __shared__ DepthMixLds mix_lds;
   // The slot's token row [dim].
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
@@ -171,7 +174,7 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
   const int slice = blockIdx.x;
   const bool shared = slot >= 2 * tokens;
   const int H = shared ? shared_dim : hidden_dim;
-  if (slice * 16 >= H) return;  // uniform
+  if (slice * SW >= H) return;  // uniform
   const int t0 = shared ? slot - 2 * tokens : slot >> 1;  // the slot's token
   // Router weight fragments of this wavefront's chain, loaded right after
   // the input row's loads with no branch between (every slot loads them, the
@@ -289,49 +292,96 @@ __global__ __launch_bounds__(256) void decode_up_kernel(
     }
     w = gate_up + static_cast<int64_t>(sel[k]) * 2 * hidden_dim * dim;
   }
-  // Packed rows [32 slice, 32 slice + 32): gate group 2 slice, up group
-  // 2 slice + 1; block (g, s) at ((g * ksteps) + s) KB.  Wavefront w takes
-  // k steps w, w + 4, ..., the weight fragments of up to 8 of them in
-  // flight at once.
   const int ksteps = dim / 32;
-  const uint4* wg = reinterpret_cast<const uint4*>(w) + (2 * slice) * ksteps * 64 + lane;
-  const uint4* wu = wg + ksteps * 64;
-  const int c = lane >> 4;
-  float ag = 0.0f, au = 0.0f;
-  for (int s0 = wave; s0 < ksteps; s0 += 32) {
-    uint4 g[8], u[8];
+  const int64_t hrow = (shared ? 2 * tokens + t0 : slot) * static_cast<int64_t>(hstride);
+  if constexpr (SW == 16) {
+    // Packed rows [32 slice, 32 slice + 32): gate group 2 slice, up group
+    // 2 slice + 1; block (g, s) at ((g * ksteps) + s) KB.  Wavefront w
+    // takes k steps w, w + 4, ..., the weight fragments of up to 8 of them
+    // in flight at once.
+    const uint4* wg = reinterpret_cast<const uint4*>(w) + (2 * slice) * ksteps * 64 + lane;
+    const uint4* wu = wg + ksteps * 64;
+    const int c = lane >> 4;
+    float ag = 0.0f, au = 0.0f;
+    for (int s0 = wave; s0 < ksteps; s0 += 32) {
+      uint4 g[8], u[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int st = min(s0 + 4 * i, ksteps - 1);
-      g[i] = wg[st * 64];
-      u[i] = wu[st * 64];
-    }
+      for (int i = 0; i < 8; ++i) {
+        const int st = min(s0 + 4 * i, ksteps - 1);
+        g[i] = wg[st * 64];
+        u[i] = wu[st * 64];
+      }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int st = s0 + 4 * i;
-      if (st < ksteps) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(xs + st * 32 + c * 8);
-        ag += dot8(g[i], xv);
-        au += dot8(u[i], xv);
+      for (int i = 0; i < 8; ++i) {
+        const int st = s0 + 4 * i;
+        if (st < ksteps) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(xs + st * 32 + c * 8);
+          ag += dot8(g[i], xv);
+          au += dot8(u[i], xv);
+        }
       }
     }
-  }
-  const int r = lane & 15;
-  part[wave][c][r] = ag;
-  part[wave][c][16 + r] = au;
-  __syncthreads();
-  if (tid < 16) {
-    const int rr = tid;
-    float gs = 0.0f, us = 0.0f;
+    const int r = lane & 15;
+    part[wave][c][r] = ag;
+    part[wave][c][16 + r] = au;
+    __syncthreads();
+    if (tid < 16) {
+      float gs = 0.0f, us = 0.0f;
 #pragma unroll
-    for (int wv = 0; wv < 4; ++wv)
+      for (int wv = 0; wv < 4; ++wv)
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) {
-        gs += part[wv][cc][rr];
-        us += part[wv][cc][16 + rr];
+        for (int cc = 0; cc < 4; ++cc) {
+          gs += part[wv][cc][tid];
+          us += part[wv][cc][16 + tid];
+        }
+      hidden[hrow + slice * 16 + tid] = f32_to_bf16(swiglu(gs, us));
+    }
+  } else {
+    // Hidden columns [8 slice, 8 slice + 8): rows 8 h .. 8 h + 7 (h = slice
+    // % 2) of gate group 2 (slice / 2) and of up group 2 (slice / 2) + 1.
+    // Lane l takes row r = l % 8 of them, k chunk kc = (l / 8) % 4 of a
+    // 32-wide k step and the step of parity sp = l / 32 in a pair, so one
+    // wavefront load covers two k steps of a half block as 4 contiguous
+    // 128-byte runs; wavefront w takes step pairs w, w + 4, w + 8 per batch
+    // (at dim 768, all 12 pairs in one).
+    const int r = lane & 7, kc = (lane >> 3) & 3, sp = lane >> 5;
+    const uint4* wg = reinterpret_cast<const uint4*>(w) + (2 * (slice >> 1)) * ksteps * 64 +
+                      (slice & 1) * 8 + r + 16 * kc;
+    const uint4* wu = wg + ksteps * 64;
+    float ag = 0.0f, au = 0.0f;
+    for (int p0 = wave; 2 * p0 < ksteps; p0 += 12) {
+      uint4 g[3], u[3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int st = min(2 * (p0 + 4 * i) + sp, ksteps - 1);
+        g[i] = wg[st * 64];
+        u[i] = wu[st * 64];
       }
-    const int64_t row = shared ? 2 * tokens + t0 : slot;
-    hidden[row * hstride + slice * 16 + rr] = f32_to_bf16(swiglu(gs, us));
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int st = 2 * (p0 + 4 * i) + sp;
+        if (st < ksteps) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(xs + st * 32 + kc * 8);
+          ag += dot8(g[i], xv);
+          au += dot8(u[i], xv);
+        }
+      }
+    }
+    part[wave][lane >> 3][r] = ag;
+    part[wave][lane >> 3][8 + r] = au;
+    __syncthreads();
+    if (tid < 16) {
+      // Lanes 0-7: gate rows, 8-15: up rows, each summed over (wavefront,
+      // k chunk, step parity) in a fixed order; lane j < 8 then takes up row
+      // j from lane j + 8.
+      float v = 0.0f;
+#pragma unroll
+      for (int wv = 0; wv < 4; ++wv)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v += part[wv][j][tid];
+      const float us = __shfl_xor(v, 8);
+      if (tid < 8) hidden[hrow + slice * 8 + tid] = f32_to_bf16(swiglu(v, us));
+    }
   }
 }
 
@@ -435,7 +485,11 @@ hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens
   if (tokens == 0) return hipSuccess;
   const int hstride = hidden_dim > shared_dim ? hidden_dim : shared_dim;
   const DecodeMix none{};
-  const dim3 up_grid(hstride / 16, 3 * tokens);
+  // Eight hidden columns per workgroup at one or two tokens (more workgroups
+  // streaming less of an expert each), sixteen past that (the input mix is
+  // repeated by every workgroup of a token).
+  const bool narrow = tokens <= 2;
+  const dim3 up_grid(hstride / (narrow ? 8 : 16), 3 * tokens);
   const size_t up_lds = decode_up_lds_bytes(dim);
   const DecodeMix m = mix != nullptr ? *mix : none;
   const bool mixing = m.n_sources > 0;
@@ -445,13 +499,17 @@ hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens
                                         indices, weights);
   };
   hipError_t e = hipSuccess;
+  auto up_sw = [&](auto ns) {
+    if (narrow)
+      experts <= 16 ? up(decode_up_kernel<1, ns, 8>) : up(decode_up_kernel<2, ns, 8>);
+    else
+      experts <= 16 ? up(decode_up_kernel<1, ns, 16>) : up(decode_up_kernel<2, ns, 16>);
+    return hipSuccess;
+  };
   if (mixing)
-    e = with_sources(m.n_sources, [&](auto ns) {
-      experts <= 16 ? up(decode_up_kernel<1, ns>) : up(decode_up_kernel<2, ns>);
-      return hipSuccess;
-    });
+    e = with_sources(m.n_sources, up_sw);
   else
-    experts <= 16 ? up(decode_up_kernel<1, 0>) : up(decode_up_kernel<2, 0>);
+    up_sw(std::integral_constant<int, 0>{});
   if (e == hipSuccess) e = hipGetLastError();
   if (e != hipSuccess) return e;
   decode_down_kernel<<<dim3(dim / 16, tokens), 256, 0, s>>>(

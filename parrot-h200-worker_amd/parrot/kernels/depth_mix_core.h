@@ -23,6 +23,23 @@ namespace parrot {
 constexpr int kDepthDimsPerWave = 256;
 constexpr int kDepthMaxWaves = 8;  // dim <= 2048
 
+// A wavefront sum with wave_sum's order, in lane 63 only (where the depth
+// mix writes its partials from): the 16-lane row sums r0..r3 by the same DPP
+// steps, then ((r0 + r1) + r2) + r3 by three row broadcasts masked to rows
+// 1, 2 and 3 in turn (the other rows add -0, the exact identity).  No
+// readlane: the totals stay in VGPRs.
+__device__ __forceinline__ float wave_total_lane63(float v) {
+  constexpr int kNegZero = static_cast<int>(0x80000000u);
+  v += dpp<0xb1>(v);
+  v += dpp<0x4e>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(kNegZero, __float_as_int(v), 0x142, 0x2, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(kNegZero, __float_as_int(v), 0x142, 0x4, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(kNegZero, __float_as_int(v), 0x142, 0x8, 0xf, false));
+  return v;
+}
+
 struct __attribute__((aligned(8))) DepthMixLds {
   float part[kDepthMaxWaves][2 * kMaxDepthSources];
   float part_out[kDepthMaxWaves];
@@ -57,10 +74,10 @@ __device__ __forceinline__ uint2 depth_mix_chunk(const uint2 (&v)[kMaxDepthSourc
   }
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    ss[s] = wave_sum(ss[s]);
-    dq[s] = wave_sum(dq[s]);
+    ss[s] = wave_total_lane63(ss[s]);
+    dq[s] = wave_total_lane63(dq[s]);
   }
-  if (lane == 0) {
+  if (lane == 63) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       sh.part[wave][2 * s] = ss[s];
@@ -120,8 +137,8 @@ __device__ __forceinline__ uint2 depth_mix_norm_chunk(uint2 mixed, uint2 g_out, 
                                                       float out_eps, DepthMixLds& sh) {
   const float r0 = lo_bf16(mixed.x), r1 = hi_bf16(mixed.x);
   const float r2 = lo_bf16(mixed.y), r3 = hi_bf16(mixed.y);
-  const float sso = wave_sum(has ? r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3 : 0.0f);
-  if (lane == 0) sh.part_out[wave] = sso;
+  const float sso = wave_total_lane63(has ? r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3 : 0.0f);
+  if (lane == 63) sh.part_out[wave] = sso;
   __syncthreads();
   float total = sh.part_out[0];
 #pragma unroll
