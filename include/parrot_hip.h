@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 8
+#define PARROT_ABI_VERSION 9
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -216,6 +216,25 @@ int parrot_decode_qkv_bf16(const void* x, const void* const* sources, int32_t n_
                            int32_t kv_heads, int32_t head_dim, const float* cos_table,
                            const float* sin_table, int32_t max_positions,
                            const int32_t* position, void* q, void* k, void* v, void* stream);
+
+/* parrot_decode_qkv_bf16 for the first layer of a decode step, with the
+ * token embedding in the launch: h_t is the attention norm of the depth mix
+ * of one source, row token_ids[t] of embedding [vocab, dim] bf16 (16-byte
+ * aligned; an id outside [0, vocab) reads the nearest row, where the
+ * reference's nn.Embedding raises), and that row is also stored to embedded
+ * [tokens, dim] (16-byte aligned), the later layers' first depth source.
+ * Replaces the embedding lookup of Parrot.decode_step (parrot/model.py:830,
+ * nn.Embedding) and its launch; other limits and outputs as
+ * parrot_decode_qkv_bf16. */
+int parrot_decode_qkv_embed_bf16(const int64_t* token_ids, const void* embedding, int32_t vocab,
+                                 void* embedded, const void* query, const void* score_norm_weight,
+                                 float score_eps, const void* attention_norm_weight,
+                                 float norm_eps, int32_t tokens, int32_t dim,
+                                 const void* qkv_weight, int32_t heads, int32_t kv_heads,
+                                 int32_t head_dim, const float* cos_table,
+                                 const float* sin_table, int32_t max_positions,
+                                 const int32_t* position, void* q, void* k, void* v,
+                                 void* stream);
 
 /* The MLA layers' decode-step projections before the latent attention, one
  * launch: q_latent [tokens, query_rows] fp32 = x . absorbed_query^T with x

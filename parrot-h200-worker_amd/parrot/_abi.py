@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (maps PyTorch's HIP runtime before the library)
 
 LIBRARY = Path(__file__).resolve().parent / "_lib" / "libparrot_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -98,6 +98,10 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [_p, _p, _i32, _p, _p, _f32, _p, _f32, _i32, _i32, _p, _i32, _i32, _i32, _p, _p, _i32,
          _p, _p, _p, _p, _p]),
+    "parrot_decode_qkv_embed_bf16": (
+        ctypes.c_int,
+        [_p, _p, _i32, _p, _p, _p, _f32, _p, _f32, _i32, _i32, _p, _i32, _i32, _i32, _p, _p,
+         _i32, _p, _p, _p, _p, _p]),
     "parrot_mla_decode_in_bf16": (
         ctypes.c_int,
         [_p, _p, _i32, _p, _p, _f32, _p, _f32, _i32, _i32, _p, _i32, _p, _i32, _p, _p, _p]),

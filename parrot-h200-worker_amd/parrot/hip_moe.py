@@ -940,12 +940,21 @@ def decode_qkv_supported(tokens: int, dim: int, heads: int, kv_heads: int,
 
 def decode_qkv(x: Tensor | None, weight: Tensor, cos: Tensor, sin: Tensor, heads: int,
                kv_heads: int, head_dim: int, position: Tensor,
-               mix: tuple | None = None) -> tuple[Tensor, Tensor, Tensor]:
+               mix: tuple | None = None,
+               embed: tuple | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """A decode step's q|k|v projection + RoPE at the device ``position`` in
     one launch: x [b, 1, dim] bf16, or ``mix = (depth_module, sources, norm)``
     whose ``depth_mix_norm`` the launch computes itself; ``weight`` the
     stacked row-major q|k|v weight.  Returns q [b, heads, 1, d], k and v
-    [b, kv_heads, 1, d] (cf. LocalGQA.decode, parrot/model.py:176-262)."""
+    [b, kv_heads, 1, d] (cf. LocalGQA.decode, parrot/model.py:176-262).
+
+    ``embed = (token_ids [b, 1] int64, embedding weight [vocab, dim])`` with a
+    one-source ``mix``: the source is the tokens' embedding rows, gathered in
+    the same launch and written into that source tensor (the reference's
+    ``self.embedding(input_ids)``, parrot/model.py:830)."""
+    if embed is not None:
+        return _decode_qkv_embed(weight, cos, sin, heads, kv_heads, head_dim, position, mix,
+                                 embed)
     keep = None
     if mix is not None:
         mix_args, ref, keep = _decode_mix_args(mix)
@@ -968,6 +977,41 @@ def decode_qkv(x: Tensor | None, weight: Tensor, cos: Tensor, sin: Tensor, heads
         cos.shape[0], ptr(position), ptr(q), ptr(k), ptr(v), _stream(ref.device)),
         "parrot_decode_qkv_bf16")
     del keep  # alive until the launch is enqueued (it is)
+    return q, k, v
+
+
+def _decode_qkv_embed(weight: Tensor, cos: Tensor, sin: Tensor, heads: int, kv_heads: int,
+                      head_dim: int, position: Tensor, mix: tuple,
+                      embed: tuple) -> tuple[Tensor, Tensor, Tensor]:
+    ids, table = embed
+    depth, sources, norm = mix
+    if len(sources) != 1:
+        raise RuntimeError("the embedded q|k|v launch mixes exactly one source")
+    out = sources[0]
+    _require(out, "HIP decode q|k|v projection")
+    b, dim = out.numel() // out.shape[-1], out.shape[-1]
+    if not out.is_contiguous():
+        raise RuntimeError("embedding output must be contiguous")
+    if ids.dtype != torch.int64 or ids.numel() != b or ids.device != out.device:
+        raise RuntimeError("token ids must be int64 [b, 1] on the output's device")
+    if (table.dtype != out.dtype or table.dim() != 2 or table.shape[1] != dim or
+            not table.is_contiguous()):
+        raise RuntimeError("embedding table must be a contiguous [vocab, dim] weight of the "
+                           "output dtype")
+    if weight.dtype != out.dtype or not weight.is_contiguous():
+        raise RuntimeError("q|k|v weight must be contiguous in the input's dtype")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise RuntimeError("RoPE tables must be fp32")
+    _check_position(position, out.device)
+    ids = ids.contiguous()
+    q = out.new_empty((b, heads, 1, head_dim))
+    k = out.new_empty((b, kv_heads, 1, head_dim))
+    v = out.new_empty((b, kv_heads, 1, head_dim))
+    _abi.check(_abi.load().parrot_decode_qkv_embed_bf16(
+        ptr(ids), ptr(table), table.shape[0], ptr(out), ptr(depth.query),
+        ptr(depth.norm.weight), float(depth.norm.eps), ptr(norm.weight), float(norm.eps), b, dim,
+        ptr(weight), heads, kv_heads, head_dim, ptr(cos), ptr(sin), cos.shape[0], ptr(position),
+        ptr(q), ptr(k), ptr(v), _stream(out.device)), "parrot_decode_qkv_embed_bf16")
     return q, k, v
 
 

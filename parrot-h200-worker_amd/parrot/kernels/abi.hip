@@ -337,6 +337,54 @@ int parrot_decode_qkv_bf16(const void* x, const void* const* sources, int32_t n_
   return status(parrot::launch_decode_qkv(a, as_stream(stream)));
 }
 
+int parrot_decode_qkv_embed_bf16(const int64_t* token_ids, const void* embedding, int32_t vocab,
+                                 void* embedded, const void* query, const void* score_norm_weight,
+                                 float score_eps, const void* attention_norm_weight,
+                                 float norm_eps, int32_t tokens, int32_t dim,
+                                 const void* qkv_weight, int32_t heads, int32_t kv_heads,
+                                 int32_t head_dim, const float* cos_table,
+                                 const float* sin_table, int32_t max_positions,
+                                 const int32_t* position, void* q, void* k, void* v,
+                                 void* stream) {
+  if (!token_ids || !embedding || !embedded) return PARROT_ERR_NULL_POINTER;
+  if (vocab <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (!aligned16(embedding) || !aligned16(embedded)) return PARROT_ERR_ALIGNMENT;
+  // The single depth source is the gathered row (its slot names the output
+  // buffer, which the launch writes and the later layers read).
+  const void* sources[1] = {embedded};
+  if (!qkv_weight || !cos_table || !sin_table || !position || !q || !k || !v)
+    return PARROT_ERR_NULL_POINTER;
+  if (tokens < 0 || dim <= 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
+      max_positions <= 0)
+    return PARROT_ERR_BAD_SHAPE;
+  const int64_t n = static_cast<int64_t>(heads + 2 * kv_heads) * head_dim;
+  if (tokens > 16 || dim % 128 || dim > parrot::decode_qkv_max_dim() || head_dim % 2 || n % 16)
+    return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(qkv_weight)) return PARROT_ERR_ALIGNMENT;
+  parrot::DecodeQkvArgs a{};
+  if (int rc = make_decode_mix(sources, 1, query, score_norm_weight, score_eps,
+                               attention_norm_weight, norm_eps, a.mix))
+    return rc;
+  a.tokens = tokens;
+  a.dim = dim;
+  a.w = static_cast<const uint16_t*>(qkv_weight);
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.cos_t = cos_table;
+  a.sin_t = sin_table;
+  a.max_positions = max_positions;
+  a.position = position;
+  a.q = static_cast<uint16_t*>(q);
+  a.k = static_cast<uint16_t*>(k);
+  a.v = static_cast<uint16_t*>(v);
+  a.gather_ids = token_ids;
+  a.gather_table = static_cast<const uint16_t*>(embedding);
+  a.gather_rows = vocab;
+  a.gather_out = static_cast<uint16_t*>(embedded);
+  return status(parrot::launch_decode_qkv(a, as_stream(stream)));
+}
+
 // Shapes of the MLA decode projections: up to 16 tokens, K a multiple of
 // 128 up to 2048, row counts multiples of 16, the staged input within 64 KB.
 static int check_mla_decode(int32_t tokens, int32_t k, int elem_bytes) {

@@ -424,6 +424,13 @@ struct DecodeQkvArgs {
   uint16_t* q;              // [tokens, H, 1, d]
   uint16_t* k;              // [tokens, Hk, 1, d]
   uint16_t* v;              // [tokens, Hk, 1, d]
+  // With gather_ids, the mix's single source is gathered in the launch:
+  // row gather_ids[t] (clamped into [0, gather_rows)) of gather_table
+  // [gather_rows, dim], also stored to gather_out [tokens, dim].
+  const int64_t* gather_ids;
+  const uint16_t* gather_table;
+  int gather_rows;
+  uint16_t* gather_out;
 };
 int decode_qkv_max_dim();
 hipError_t launch_mla_decode_in(const uint16_t* x, const DecodeMix* mix, int tokens, int dim,

@@ -30,8 +30,11 @@ constexpr int kQkvMaxDim = 1024;  // the mix holds a row with 4 wavefronts of 25
 // device position (a scalar load), the input row's sources, the weight
 // chunks (NCH per lane, unconditional), then the position's cos / sin.  The
 // mix waits only for its sources; the weights arrive while it runs.
-template <int NS, int NCH>  // NS > 0: the input is the depth mix of NS sources
+// GATHER (with NS = 1): the source is the embedding row of the token id,
+// gathered here (the id's load goes first, the row's after the weights').
+template <int NS, int NCH, bool GATHER = false>  // NS > 0: the input is the depth mix of NS sources
 __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
+  static_assert(!GATHER || NS == 1, "a gathered row is the only source");
   __shared__ DepthMixLds mix_lds;
   __shared__ __attribute__((aligned(16))) uint16_t xs[kQkvMaxDim];
   const DecodeMix& m = a.mix;
@@ -43,6 +46,9 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
                "s"(sp[6]), "s"(sp[7]), "s"(sp[8]), "s"(m.query), "s"(m.score_w), "s"(m.out_w),
                "s"(a.w), "s"(a.position), "s"(a.cos_t), "s"(a.sin_t), "s"(a.dim),
                "s"(a.head_dim), "s"(a.max_positions), "s"(a.x));
+  if constexpr (GATHER)
+    asm volatile("" ::"s"(a.gather_ids), "s"(a.gather_table), "s"(a.gather_rows),
+                 "s"(a.gather_out));
   const int raw_pos = *a.position;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -59,13 +65,25 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
   const int chunks = K >> 2;
   const bool has = tid < chunks;
   DecodeMixLoads ml;
-  if constexpr (NS > 0)
+  int64_t id_raw = 0;
+  if constexpr (GATHER) {
+    id_raw = a.gather_ids[t];
+    ml.q = reinterpret_cast<const uint2*>(m.query)[has ? tid : 0];
+    ml.g = reinterpret_cast<const uint2*>(m.score_w)[has ? tid : 0];
+    ml.g_out = reinterpret_cast<const uint2*>(m.out_w)[has ? tid : 0];
+  } else if constexpr (NS > 0) {
     decode_mix_load<NS>(m, static_cast<int64_t>(t) * chunks, has ? tid : 0, ml);
+  }
   asm volatile("" ::: "memory");
   uint4 wr[NCH];
   load_row_chunks_n<NCH>(a.w, col, K, p, wr);
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);  // the position's first use (a wait) after every load above
+  __builtin_amdgcn_sched_barrier(0);  // the id's and position's first uses (waits) after these
+  if constexpr (GATHER) {
+    const int64_t id = min(max(id_raw, int64_t{0}), static_cast<int64_t>(a.gather_rows - 1));
+    ml.v[0] = reinterpret_cast<const uint2*>(a.gather_table)[id * chunks + (has ? tid : 0)];
+    asm volatile("" ::: "memory");
+  }
   const int pos = min(max(raw_pos, 0), a.max_positions - 1);
   const int64_t ti = static_cast<int64_t>(pos) * (d / 2) + w / 2;
   const float rc = a.cos_t[ti], rs = a.sin_t[ti];
@@ -73,6 +91,9 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
 
   if constexpr (NS > 0) {
     // Token t's input row: depth mix + RMSNorm of its sources into LDS.
+    if constexpr (GATHER)
+      if (blockIdx.x == 0 && has)
+        reinterpret_cast<uint2*>(a.gather_out)[static_cast<int64_t>(t) * chunks + tid] = ml.v[0];
     const uint2 o = decode_mix_row<NS>(m, ml, has, wave, lane, K, mix_lds);
     if (has) reinterpret_cast<uint2*>(xs)[tid] = o;
   } else {
@@ -115,6 +136,11 @@ hipError_t launch_decode_qkv(const DecodeQkvArgs& a, hipStream_t s) {
   const int n = (a.heads + 2 * a.kv_heads) * a.head_dim;
   const dim3 grid(n / kGemvRows, a.tokens);
   return with_gemv_chunks<8>(a.dim, [&](auto nch) {
+    if (a.gather_ids != nullptr) {
+      if (a.mix.n_sources != 1) return hipErrorInvalidValue;
+      decode_qkv_kernel<1, nch, true><<<grid, 256, 0, s>>>(a);
+      return hipGetLastError();
+    }
     if (a.mix.n_sources == 0) {
       decode_qkv_kernel<0, nch><<<grid, 256, 0, s>>>(a);
       return hipGetLastError();

@@ -406,9 +406,15 @@ class LocalGQA(nn.Module):
 
     def decode(self, x: Tensor | None, cache: LocalKVCache, position: int,
                addend: Tensor | None = None, defer_sum: bool = False,
-               position_device: Tensor | None = None, mix: tuple | None = None) -> Tensor:
+               position_device: Tensor | None = None, mix: tuple | None = None,
+               embed: tuple | None = None) -> Tensor:
         """One decode step; ``mix = (depth_module, sources, norm)`` in place
-        of x gives the input as that depth mix + norm (see decodes_mixed)."""
+        of x gives the input as that depth mix + norm (see decodes_mixed).
+        ``embed = (token_ids, embedding weight)`` with a one-source mix: that
+        source is filled with the tokens' embedding rows by the same launch
+        (hip_moe.decode_qkv)."""
+        if embed is not None and mix is None:
+            raise RuntimeError("an embedded decode input needs the one-source mix it fills")
         if mix is not None:
             if not self.decodes_mixed(mix[1][0], position_device):
                 raise RuntimeError("this decode step cannot take its input as a depth mix")
@@ -426,7 +432,8 @@ class LocalGQA(nn.Module):
             cos, sin = _rope_tables(c, x.new_empty(0, dtype=torch.float32))
             if mix is not None:
                 q, k, v = hip_moe.decode_qkv(None, self._packed_qkv(), cos, sin, c.n_heads,
-                                             c.n_kv_heads, c.head_dim, position_device, mix=mix)
+                                             c.n_kv_heads, c.head_dim, position_device, mix=mix,
+                                             embed=embed)
             elif self._fused_projections():
                 q, k, v = hip_moe.proj_rope_qkv(x, self._qkv_fragments(), cos, sin, c.n_heads,
                                                 c.n_kv_heads, c.head_dim,
@@ -1112,6 +1119,23 @@ class Parrot(nn.Module):
             position_device = torch.full((1,), t, dtype=torch.int32, device=logits.device)
         return logits, GenerationState(caches, t, b, position_device)
 
+    def _decode_embedding(self, input_ids: Tensor,
+                          state: GenerationState) -> tuple[Tensor, tuple | None]:
+        """The decode step's embedding rows (parrot/model.py:830), or, when the
+        first layer's q|k|v launch mixes its input on the HIP path, an unfilled
+        row buffer and the (ids, weight) that launch gathers it from."""
+        cfg = self.config
+        first = self.blocks[0].attention if self.blocks else None
+        if (cfg.residual == "attnres" and cfg.depth_backend == "hip" and
+                isinstance(first, LocalGQA) and input_ids.is_cuda and
+                state.position_device is not None and input_ids.dtype == torch.int64):
+            weight = self.embedding.weight
+            x = torch.empty((input_ids.shape[0], 1, cfg.dim), dtype=weight.dtype,
+                            device=input_ids.device)
+            if first.decodes_mixed(x, state.position_device):
+                return x, (input_ids, weight)
+        return self.embedding(input_ids), None
+
     @torch.inference_mode()
     def decode_step(self, input_ids: Tensor, state: GenerationState, *,
                     _next_token_only: bool = False,
@@ -1128,7 +1152,7 @@ class Parrot(nn.Module):
             raise ValueError("Generation state has reached max_seq_len")
         if len(state.layers) != cfg.n_layers:
             raise ValueError("Generation state does not match model depth")
-        x = self.embedding(input_ids)
+        x, embed = self._decode_embedding(input_ids, state)
         stream = _AttnRes(x, cfg.depth_block_size) if cfg.residual == "attnres" else None
         index = 0
         for block, cache in zip(self.blocks, state.layers):
@@ -1140,19 +1164,21 @@ class Parrot(nn.Module):
                 raise ValueError("MLA attention received a local cache")
             if (stream is not None and self.config.depth_backend == "hip" and
                     block.attention.decodes_mixed(stream.sources()[0], state.position_device)):
-                # The input's depth mix + norm runs inside the q|k|v launch.
+                # The input's depth mix + norm runs inside the q|k|v launch
+                # (the first layer's also gathers the embedding rows).
                 mix = (self.depth_mix[index], stream.sources(), block.attention_norm)
+                extra = {"embed": embed} if index == 0 and embed is not None else {}
                 if self._defers_attention(block, stream, index, state):
                     # The output projection's sum over heads is left to the
                     # MoE's input mix (the reference's PendingResidual).
                     delta = block.attention.decode(
                         None, cache, state.position, defer_sum=True,
-                        position_device=state.position_device, mix=mix)
+                        position_device=state.position_device, mix=mix, **extra)
                     out = PendingResidual(addend, delta)
                 else:
                     out = block.attention.decode(
                         None, cache, state.position, addend=addend,
-                        position_device=state.position_device, mix=mix)
+                        position_device=state.position_device, mix=mix, **extra)
             else:
                 h = self._mixed_input(stream, x, index, block.attention_norm)
                 out = block.attention.decode(h, cache, state.position, addend=addend,

@@ -149,6 +149,15 @@ def test_argument_validation_without_gpu(lib):
     assert qkv(tokens=17) == -3 and qkv(dim=1152) == -3 and qkv(dim=704) == -3
     assert qkv(d=95) == -3 and qkv(h=3, hk=1, d=6) == -3
     assert qkv(w=fake + 8) == -5
+    # ... with the embedding gather: ids, table, row buffer, vocab > 0
+    embed = lambda **kw: lib.parrot_decode_qkv_embed_bf16(*[kw.get(k, v) for k, v in (
+        ("ids", fake), ("table", fake), ("vocab", 1000), ("rows", fake), ("q0", fake),
+        ("sw", fake), ("se", 1e-6), ("nw", fake), ("ne", 1e-6), ("tokens", 2), ("dim", 768),
+        ("w", fake), ("h", 8), ("hk", 2), ("d", 96), ("cos", fake), ("sin", fake),
+        ("maxp", 4096), ("pos", fake), ("q", fake), ("k", fake), ("v", fake), ("stream", null))])
+    assert embed(ids=null) == -1 and embed(rows=null) == -1 and embed(q0=null) == -1
+    assert embed(vocab=0) == -2 and embed(tokens=17) == -3 and embed(dim=1152) == -3
+    assert embed(table=fake + 8) == -5 and embed(rows=fake + 2) == -5
     # decode MoE with its input's depth mix: sources, n_sources, dim <= 1024
     mix_moe = lambda **kw: lib.parrot_depth_mix_decode_moe_bf16(*[kw.get(k, v) for k, v in (
         ("srcs", ctypes.cast(srcs, ctypes.c_void_p)), ("n", 2), ("q", fake), ("sw", fake),

@@ -355,6 +355,44 @@ def test_decode_qkv(tokens, sources, position):
     assert torch.equal(qm, qh) and torch.equal(km, kh) and torch.equal(vm, vh)
 
 
+@pytest.mark.parametrize("tokens,position", [(1, 0), (5, 150), (16, 299)])
+def test_decode_qkv_embeds_its_input(tokens, position):
+    """The first layer's q|k|v launch that gathers its input rows from the
+    token ids: the rows it stores equal the embedding lookup, and q / k / v
+    equal the one-source mix path over those rows, bit for bit.  Ids outside
+    the table read the nearest row (the first and last tokens here)."""
+    from test_gpu_moe import _Depth, _Norm
+    from parrot import hip_moe
+    from parrot.model import ModelConfig, _rope_tables
+    cfg = ModelConfig()
+    H, Hk, d, dim, vocab = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.dim, 1000
+    n = (H + 2 * Hk) * d
+    _say(f"decode qkv with its embedding T={tokens} p={position}")
+    g = torch.Generator().manual_seed(400 + tokens)
+    w = (torch.randn(n, dim, generator=g) * dim ** -0.5).bfloat16().cuda()
+    table = torch.randn(vocab, dim, generator=g).bfloat16().cuda()
+    ids = torch.randint(0, vocab, (tokens, 1), generator=g)
+    ids[0, 0] = vocab - 1
+    rows = table[ids.view(-1)].view(tokens, 1, dim)
+    if tokens > 1:
+        ids[-1, 0] = vocab + 7  # nearest row: vocab - 1
+        rows[-1, 0] = table[vocab - 1]
+    ids = ids.cuda()
+    cos, sin = _rope_tables(cfg, torch.empty(0, device="cuda"))
+    pos = torch.tensor([position], dtype=torch.int32, device="cuda")
+    torch.manual_seed(500 + tokens)
+    depth = _Depth(dim).cuda().bfloat16()
+    norm = _Norm(dim).cuda().bfloat16()
+    out = torch.full((tokens, 1, dim), float("nan"), dtype=torch.bfloat16, device="cuda")
+    with torch.no_grad():
+        qe, ke, ve = hip_moe.decode_qkv(None, w, cos, sin, H, Hk, d, pos,
+                                        mix=(depth, [out], norm), embed=(ids, table))
+        qm, km, vm = hip_moe.decode_qkv(None, w, cos, sin, H, Hk, d, pos,
+                                        mix=(depth, [rows], norm))
+    assert torch.equal(out, rows)
+    assert torch.equal(qe, qm) and torch.equal(ke, km) and torch.equal(ve, vm)
+
+
 @pytest.mark.parametrize("tokens,sources,with_addend", [
     (1, 1, True), (1, 4, False), (3, 9, True), (8, 5, True), (16, 9, False)])
 def test_decode_moe_mixes_its_input(tokens, sources, with_addend):
