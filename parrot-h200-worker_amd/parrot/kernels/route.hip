@@ -82,6 +82,14 @@ __global__ __launch_bounds__(256) void route_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRouteTokensPerBlock;
+  // This thread's two bias entries for the selection below (experts j and
+  // j + 16 of its DPP row).
+  const int jb = threadIdx.x & 15;
+  float bias0 = 0.0f, bias1 = 0.0f;
+  auto load_bias = [&]() {
+    bias0 = bias[min(jb, experts - 1)];
+    bias1 = bias[min(jb + 16, experts - 1)];
+  };
 
   if constexpr (!GIVEN_LOGITS) {
     const int64_t row = t0 + (lane & 15) < tokens ? t0 + (lane & 15) : tokens - 1;
@@ -114,12 +122,14 @@ __global__ __launch_bounds__(256) void route_kernel(
         }
       }
     }
+    if (bias != nullptr) load_bias();  // in flight across the partial sums' barrier
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       part_s[wave][4 * (lane >> 4) + r][lane & 15] = acc0[r];
       part_s[wave][4 * (lane >> 4) + r][16 + (lane & 15)] = acc1[r];
     }
   } else {
+    if (bias != nullptr) load_bias();
     for (int i = threadIdx.x; i < kRouteTokensPerBlock * experts; i += 256) {
       const int tl = i / experts;
       const int e = i - tl * experts;
@@ -133,16 +143,17 @@ __global__ __launch_bounds__(256) void route_kernel(
     // Token tl = tid / 16 on DPP row tid / 16; lane j holds experts j, j + 16.
     const int tl = threadIdx.x >> 4;
     const int j = threadIdx.x & 15;
-    auto logit = [&](int e) -> float {
+    auto logit = [&](int e, float b) -> float {
       float v = part_s[0][tl][e];
       if constexpr (!GIVEN_LOGITS) v = ((v + part_s[1][tl][e]) + part_s[2][tl][e]) + part_s[3][tl][e];
-      return v + (bias != nullptr ? bias[e] : 0.0f);
+      return v + b;
     };
-    const float l0 = j < experts ? logit(j) : 0.0f;
-    const float l1 = j + 16 < experts ? logit(j + 16) : 0.0f;
+    const float l0 = j < experts ? logit(j, bias0) : 0.0f;
+    const float l1 = j + 16 < experts ? logit(j + 16, bias1) : 0.0f;
     select_top2(l0, l1, experts, t0 + tl, t0 + tl < tokens, out_logits, probs, weights, indices,
                 &ids_s[2 * tl]);
   }
+  if (positions == nullptr) return;  // uniform: a top-2-only launch ranks nothing
   __syncthreads();
   // Wavefront 0 ranks the block in lanes 0-31; lanes 32-63 carry no
   // assignments and name no block (index gridDim.x is past the last).
