@@ -110,15 +110,22 @@ class StageBench:
         self.hit = int((counts > 0).sum())
         self.overflow = int(g.offsets[-1].item())
         # The forward's form at sizes the gate/up launch groups itself: the
-        # top-2 ids in; counts, offsets and the hidden rows' ids out.
-        self.in_kernel = bool(self.lib.parrot_experts_group_in_kernel(
+        # top-2 ids (mode 1) or the route block table (mode 2) in; counts,
+        # offsets and the hidden rows' ids out.
+        self.group_mode = int(self.lib.parrot_experts_group_in_kernel(
             self.T, self.dim, self.E, self.H, self.Hs))
+        self.in_kernel = self.group_mode != 0
+        self.blocks = (torch.empty(((self.T + 15) // 16, 64), dtype=torch.uint8, device=dev)
+                       if self.group_mode == 2 else None)
         i32 = dict(dtype=torch.int32, device=dev)
         self.g_counts = torch.empty(self.E, **i32)
         self.g_offsets = torch.empty(2 * self.E + 2, **i32)
         self.g_sorted = torch.empty(2 * self.T, **i32)
         self.ids = self.routed.indices.reshape(-1).contiguous()
         self.top2_ids = torch.empty_like(self.routed.indices)
+        if self.blocks is not None:
+            # The table gate_up_grouping reads when timed on its own.
+            _abi.check(self.route_top2(), "parrot_route_top2_blocks_bf16")
 
     def route(self):
         p, r, g = self.ptr, self.routed, self.g
@@ -129,6 +136,10 @@ class StageBench:
 
     def route_top2(self):
         p, r = self.ptr, self.routed
+        if self.blocks is not None:
+            return self.lib.parrot_route_top2_blocks_bf16(
+                p(self.x), p(self.moe.router.weight), p(self.bias), self.T, self.dim, self.E,
+                p(r.weights), p(self.top2_ids), p(self.blocks), self.s)
         return self.lib.parrot_route_top2_bf16(
             p(self.x), p(self.moe.router.weight), p(self.bias), self.T, self.dim, self.E,
             p(r.weights), p(self.top2_ids), self.s)
@@ -147,6 +158,8 @@ class StageBench:
 
     def gate_up_grouping_top2(self):
         p = self.ptr
+        if self.blocks is not None:
+            return self.gate_up_grouping()
         return self.lib.parrot_experts_gate_up_grouping_bf16(
             p(self.x), self.T, self.dim, self.E, self.H, self.Hs, self.C, p(self.top2_ids),
             p(self.g_counts), p(self.g_offsets), p(self.g_sorted), p(self.packed[0]),
@@ -177,6 +190,11 @@ class StageBench:
 
     def gate_up_grouping(self):
         p = self.ptr
+        if self.blocks is not None:
+            return self.lib.parrot_experts_gate_up_grouping_blocks_bf16(
+                p(self.x), self.T, self.dim, self.E, self.H, self.Hs, self.C, p(self.blocks),
+                p(self.g_counts), p(self.g_offsets), p(self.g_sorted), p(self.packed[0]),
+                p(self.packed[2]), p(self.ews), self.ews_bytes, self.s)
         return self.lib.parrot_experts_gate_up_grouping_bf16(
             p(self.x), self.T, self.dim, self.E, self.H, self.Hs, self.C, p(self.ids),
             p(self.g_counts), p(self.g_offsets), p(self.g_sorted), p(self.packed[0]),
@@ -209,8 +227,10 @@ class StageBench:
         return (self.hit * d * H + d * Hs + 2 * T * H + T * Hs) * 2 + 3 * T * d * 4 + 2 * T * 4
 
     def bytes_grouping(self):
-        """Extra bytes of the in-kernel grouping: ids in, grouping out."""
-        return 2 * self.T * 8 + (3 * self.E + 2 + 2 * self.T) * 4
+        """Extra bytes of the in-kernel grouping: ids (or the route block
+        table) in, grouping out."""
+        ids = 2 * self.T * 8 if self.blocks is None else self.blocks.numel()
+        return ids + (3 * self.E + 2 + 2 * self.T) * 4
 
     def bytes_combine(self):
         return 3 * self.T * self.dim * 4 + self.T * self.dim * 2
@@ -330,12 +350,15 @@ def layer_kernels(moe, x, iters, logit_bias=None, mark_roofline=False
         res["down_sorted"] = entry(event_time_us(sb.down_sorted, iters, sb.stream),
                                    sb.bytes_down() + (3 * sb.E + 2) * 4, sb.flops_down())
         res["route_top2"] = entry(event_time_us(sb.route_top2, iters, sb.stream),
-                                  sb.T * sb.dim * 2 + sb.E * sb.dim * 2 + sb.T * 2 * (8 + 4))
+                                  sb.T * sb.dim * 2 + sb.E * sb.dim * 2 + sb.T * 2 * (8 + 4) +
+                                  (0 if sb.blocks is None else sb.blocks.numel()))
     # The whole standalone layer, back to back on one stream, against the
     # layer's HBM floor (hit experts' weights once + x in + out) and its flops.
     layer = entry(event_time_us(sb.layer, iters, sb.stream), sb.layer_min_bytes(), sb.layer_flops())
-    layer["launches"] = ("route_top2 + gate_up(grouping in-kernel) + down + combine"
-                         if sb.in_kernel else "route(+grouping) + gate_up + down + combine")
+    layer["launches"] = (
+        "route_top2 + gate_up(grouping in-kernel) + down + combine" if sb.group_mode == 1 else
+        "route_top2(+block table) + gate_up(grouping in-kernel) + down + combine"
+        if sb.group_mode == 2 else "route(+grouping) + gate_up + down + combine")
     layer["tokens_per_s"] = round(sb.T / (layer["us"] * 1e-6), 1)
     res["layer"] = layer
     return res, sb

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 9
+#define PARROT_ABI_VERSION 10
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -514,6 +514,20 @@ int parrot_route_top2_bf16(const void* x, const void* router_weight, const float
                            int64_t tokens, int32_t dim, int32_t experts, float* out_weights,
                            int64_t* out_indices, void* stream);
 
+/* parrot_route_top2_bf16 that also writes the route block table out_blocks
+ * uint8 [ceil(T / 16), 64] (16-byte aligned), one row per 16 tokens: bytes
+ * 0-31 the block's 32 expert ids in assignment order (assignment 2t + k;
+ * 255 for the padding tokens of the last block), bytes 32-63 the block's
+ * number of assignments to each expert (0 past E).  The table is what
+ * parrot_experts_gate_up_grouping_blocks_bf16 groups from; T < 32768
+ * (PARROT_ERR_UNSUPPORTED above).  Replaces metal_route
+ * (parrot/metal_moe.py:58-81) with moe_count_assignments' per-expert counts
+ * (parrot/kernels/moe_bf16.metal:650-660) taken per 16 tokens. */
+int parrot_route_top2_blocks_bf16(const void* x, const void* router_weight,
+                                  const float* logit_bias, int64_t tokens, int32_t dim,
+                                  int32_t experts, float* out_weights, int64_t* out_indices,
+                                  void* out_blocks, void* stream);
+
 /* As parrot_route_bf16, starting from given fp32 logits [T, E] (the
  * "identical router logits" entry of the parity contract). */
 int parrot_route_from_logits_f32(const float* logits, const float* logit_bias, int64_t tokens,
@@ -568,9 +582,12 @@ int parrot_experts_combine_bf16(int64_t tokens, int32_t dim, int32_t hidden_dim,
                                 int32_t shared_dim, const void* addend, void* out,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
-/* 1 when parrot_experts_gate_up_grouping_bf16 supports this shape (the
- * streaming kernel's shapes: 2T <= 2048 assignments, at most 96 rows per
- * expert on average, dim, H, Hs <= 768), else 0. */
+/* Whether the gate/up launch can group in-kernel at this shape (dim, H,
+ * Hs <= 768 and the streaming tiles' plan): 1 from the top-2 indices
+ * (parrot_experts_gate_up_grouping_bf16: 2T <= 2048 assignments, at most
+ * 96 rows per expert on average), 2 from the route block table only
+ * (parrot_experts_gate_up_grouping_blocks_bf16: T <= 4096), else 0.  The
+ * block table form also takes every shape that answers 1. */
 int parrot_experts_group_in_kernel(int64_t tokens, int32_t dim, int32_t experts,
                                    int32_t hidden_dim, int32_t shared_dim);
 
@@ -595,8 +612,21 @@ int parrot_experts_gate_up_grouping_bf16(const void* x, int64_t tokens, int32_t 
                                          const void* packed_gate_up, const void* shared_gate_up,
                                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* parrot_experts_gate_up_grouping_bf16 grouping from the route block table
+ * of parrot_route_top2_blocks_bf16 (route_blocks, 16-byte aligned) instead
+ * of the indices, with the same outputs; for the shapes where
+ * parrot_experts_group_in_kernel answers 1 or 2.  Replaces
+ * moe_count_assignments (parrot/kernels/moe_bf16.metal:650-660) and the
+ * gate/up steps of grouped_mps_experts (parrot/metal_moe.py:384-408). */
+int parrot_experts_gate_up_grouping_blocks_bf16(
+    const void* x, int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
+    int32_t shared_dim, int32_t capacity, const void* route_blocks, int32_t* out_counts,
+    int32_t* out_offsets, int32_t* out_sorted, const void* packed_gate_up,
+    const void* shared_gate_up, void* workspace, size_t workspace_bytes, void* stream);
+
 /* parrot_experts_down_bf16 with the grouping written by
- * parrot_experts_gate_up_grouping_bf16 (counts, offsets, sorted).
+ * parrot_experts_gate_up_grouping_bf16 or ..._blocks_bf16 (counts,
+ * offsets, sorted).
  * Replaces the down steps of grouped_mps_experts
  * (parrot/metal_moe.py:409-415). */
 int parrot_experts_down_sorted_bf16(int64_t tokens, int32_t dim, int32_t experts,

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (maps PyTorch's HIP runtime before the library)
 
 LIBRARY = Path(__file__).resolve().parent / "_lib" / "libparrot_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -110,6 +110,9 @@ SIGNATURES: dict[str, tuple] = {
     "parrot_experts_gate_up_grouping_bf16": (
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),
+    "parrot_experts_gate_up_grouping_blocks_bf16": (
+        ctypes.c_int,
+        [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),
     "parrot_experts_down_sorted_bf16": (
         ctypes.c_int,
         [_i64, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),
@@ -118,6 +121,8 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
          _p, _sz, _p]),
     "parrot_route_top2_bf16": (ctypes.c_int, [_p, _p, _p, _i64, _i32, _i32, _p, _p, _p]),
+    "parrot_route_top2_blocks_bf16": (
+        ctypes.c_int, [_p, _p, _p, _i64, _i32, _i32, _p, _p, _p, _p]),
     "parrot_peak_mfma_bf16": (ctypes.c_int, [_i32, _i64, _i32, _p, _p, _p]),
     "parrot_peak_copy": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),
     "parrot_grouped_experts_static_bf16": (

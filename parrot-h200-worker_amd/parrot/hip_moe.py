@@ -110,6 +110,10 @@ class RouteResult:
     indices: Tensor
     grouping: Grouping
     logits: Tensor | None = None
+    # The route block table (route_top2(..., blocks=True)): uint8
+    # [ceil(T / 16), 64], what the gate/up launch groups from past the sizes
+    # it groups from the indices.
+    blocks: Tensor | None = None
 
 
 def _alloc_grouping(tokens: int, experts: int, cap: int, device) -> Grouping:
@@ -166,10 +170,13 @@ def route(module: "MoE", flat: Tensor, collect_stats: bool,
     return RouteResult(probs, weights, indices, g, logits)
 
 
-def route_top2(module: "MoE", flat: Tensor, logit_bias: Tensor | None = None) -> RouteResult:
+def route_top2(module: "MoE", flat: Tensor, logit_bias: Tensor | None = None,
+               blocks: bool = False) -> RouteResult:
     """The router and top-2 of ``route`` alone (the same weights and indices
     to the bit), without grouping: for expert launches that group the
-    indices themselves (``groups_in_kernel``)."""
+    indices themselves (``group_mode``).  ``blocks``: also the route block
+    table (per 16 tokens: their 32 expert ids and the count per expert),
+    which those launches group from past 2048 assignments."""
     _require(flat, "HIP routing")
     tokens, dim = flat.shape
     experts = module.cfg.n_experts
@@ -184,6 +191,12 @@ def route_top2(module: "MoE", flat: Tensor, logit_bias: Tensor | None = None) ->
     indices = torch.empty((tokens, 2), dtype=torch.int64, device=dev)
     if logit_bias is not None:
         logit_bias = logit_bias.to(device=dev, dtype=torch.float32).contiguous()
+    if blocks:
+        table = torch.empty(((tokens + 15) // 16, 64), dtype=torch.uint8, device=dev)
+        _abi.check(_abi.load().parrot_route_top2_blocks_bf16(
+            ptr(flat), ptr(router_w), ptr(logit_bias), tokens, dim, experts, ptr(weights),
+            ptr(indices), ptr(table), _stream(dev)), "parrot_route_top2_blocks_bf16")
+        return RouteResult(None, weights, indices, None, blocks=table)
     _abi.check(_abi.load().parrot_route_top2_bf16(
         ptr(flat), ptr(router_w), ptr(logit_bias), tokens, dim, experts, ptr(weights),
         ptr(indices), _stream(dev)), "parrot_route_top2_bf16")
@@ -192,10 +205,14 @@ def route_top2(module: "MoE", flat: Tensor, logit_bias: Tensor | None = None) ->
 
 def route_for_experts(module: "MoE", flat: Tensor) -> RouteResult:
     """The routing an inference MoE layer needs before its expert launches:
-    top-2 only where the gate/up launch groups the indices itself, else the
-    top-2 with its grouping."""
-    if groups_in_kernel(module, flat.shape[0], flat.shape[1]):
+    top-2 only where the gate/up launch groups the indices itself (with the
+    route block table where it groups from that), else the top-2 with its
+    grouping."""
+    mode = group_mode(module, flat.shape[0], flat.shape[1])
+    if mode == GROUP_FROM_IDS:
         return route_top2(module, flat)
+    if mode == GROUP_FROM_BLOCKS:
+        return route_top2(module, flat, blocks=True)
     return route(module, flat, collect_stats=False)
 
 
@@ -324,7 +341,7 @@ def invalidate_packed_weights(module: torch.nn.Module) -> None:
 def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: Tensor,
                         positions: Tensor | None = None, counts: Tensor | None = None,
                         addend: Tensor | None = None, grouping: Grouping | None = None,
-                        then_mix: tuple | None = None):
+                        then_mix: tuple | None = None, route_blocks: Tensor | None = None):
     """Routed + shared SwiGLU experts and weighted combine; returns
     ``addend + delta`` (each rounded to the input dtype) when ``addend`` is
     given, else the MoE delta.
@@ -332,7 +349,11 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
     ``then_mix = (depth_module, sources, output_norm)``: the combine also runs
     the next module's depth mix over ``sources + [result]`` (the kernel's
     result row is the last source) and returns ``(result, normalised mix)``;
-    ``sources`` are [tokens, dim] views in stream order."""
+    ``sources`` are [tokens, dim] views in stream order.
+
+    ``route_blocks``: the route block table of these indices
+    (``route_top2(..., blocks=True)``), for the gate/up launch to group
+    from where it cannot group from the indices."""
     _require(flat, "The grouped HIP backend")
     cfg = module.cfg
     tokens, dim = flat.shape
@@ -347,6 +368,13 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
             grouping = cached
         elif groups_in_kernel(module, tokens, dim):
             # The gate/up launch groups the indices itself.
+            self_group = True
+            route_blocks = None
+        elif (route_blocks is not None and
+              group_mode(module, tokens, dim) == GROUP_FROM_BLOCKS):
+            # ... from the route block table.
+            if route_blocks.dtype != torch.uint8 or route_blocks.shape != ((tokens + 15) // 16, 64):
+                raise RuntimeError("route block table must be uint8 [ceil(tokens / 16), 64]")
             self_group = True
         else:
             # Slots are recomputed from the indices in the deterministic stable
@@ -383,10 +411,16 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
         counts, offsets = buf[:experts], buf[experts:3 * experts + 2]
         sorted_ids = buf[3 * experts + 2:]
         shape = (experts, cfg.expert_dim, cfg.shared_expert_dim, cap)
-        _abi.check(lib.parrot_experts_gate_up_grouping_bf16(
-            ptr(flat), tokens, dim, *shape, ptr(indices), ptr(counts), ptr(offsets),
-            ptr(sorted_ids), ptr(gate_up), ptr(shared_gate_up), ptr(ws), nbytes, stream),
-            "parrot_experts_gate_up_grouping_bf16")
+        if route_blocks is not None:
+            _abi.check(lib.parrot_experts_gate_up_grouping_blocks_bf16(
+                ptr(flat), tokens, dim, *shape, ptr(route_blocks.contiguous()), ptr(counts),
+                ptr(offsets), ptr(sorted_ids), ptr(gate_up), ptr(shared_gate_up), ptr(ws),
+                nbytes, stream), "parrot_experts_gate_up_grouping_blocks_bf16")
+        else:
+            _abi.check(lib.parrot_experts_gate_up_grouping_bf16(
+                ptr(flat), tokens, dim, *shape, ptr(indices), ptr(counts), ptr(offsets),
+                ptr(sorted_ids), ptr(gate_up), ptr(shared_gate_up), ptr(ws), nbytes, stream),
+                "parrot_experts_gate_up_grouping_bf16")
         _abi.check(lib.parrot_experts_down_sorted_bf16(
             tokens, dim, *shape, ptr(counts), ptr(offsets), ptr(sorted_ids), ptr(weights),
             ptr(down), ptr(shared_down), ptr(ws), nbytes, stream),
@@ -426,12 +460,23 @@ def grouped_hip_experts(module: "MoE", flat: Tensor, indices: Tensor, weights: T
     return out, mixed
 
 
-def groups_in_kernel(module: "MoE", tokens: int, dim: int) -> bool:
-    """Whether the gate/up launch groups the top-2 indices itself at this
-    size (no separate grouping pass; parrot_experts_group_in_kernel)."""
+GROUP_NONE, GROUP_FROM_IDS, GROUP_FROM_BLOCKS = 0, 1, 2
+
+
+def group_mode(module: "MoE", tokens: int, dim: int) -> int:
+    """How the gate/up launch can group at this size, with no separate
+    grouping pass (parrot_experts_group_in_kernel): GROUP_FROM_IDS from the
+    top-2 indices, GROUP_FROM_BLOCKS from the route block table only, or
+    GROUP_NONE."""
     cfg = module.cfg
-    return bool(_abi.load().parrot_experts_group_in_kernel(
+    return int(_abi.load().parrot_experts_group_in_kernel(
         tokens, dim, cfg.n_experts, cfg.expert_dim, cfg.shared_expert_dim))
+
+
+def groups_in_kernel(module: "MoE", tokens: int, dim: int) -> bool:
+    """Whether the gate/up launch groups the top-2 indices themselves at
+    this size (the form the routed depth mix feeds)."""
+    return group_mode(module, tokens, dim) == GROUP_FROM_IDS
 
 
 DECODE_MAX_TOKENS = 16  # rows the fused decode MoE takes

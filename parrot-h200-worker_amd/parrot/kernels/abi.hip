@@ -468,7 +468,7 @@ static int route_common(const void* x, const void* router_weight, const float* l
   hipError_t e = parrot::launch_route(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(router_weight), logits,
       logit_bias, tokens, dim, experts, out_logits, out_probs, out_weights, out_indices,
-      out_positions, block_counts, s);
+      out_positions, block_counts, nullptr, s);
   if (e != hipSuccess) return status(e);
   return status(parrot::launch_group(out_indices, tokens, experts, capacity, block_counts,
                                      route_chunk_totals(workspace, tokens, experts),
@@ -491,9 +491,9 @@ int parrot_route_bf16(const void* x, const void* router_weight, const float* log
                       workspace_bytes, stream);
 }
 
-int parrot_route_top2_bf16(const void* x, const void* router_weight, const float* logit_bias,
-                           int64_t tokens, int32_t dim, int32_t experts, float* out_weights,
-                           int64_t* out_indices, void* stream) {
+static int route_top2_common(const void* x, const void* router_weight, const float* logit_bias,
+                             int64_t tokens, int32_t dim, int32_t experts, float* out_weights,
+                             int64_t* out_indices, uint8_t* out_blocks, void* stream) {
   if (!x || !router_weight || !out_weights || !out_indices) return PARROT_ERR_NULL_POINTER;
   if (tokens < 0 || tokens > (int64_t{1} << 29)) return PARROT_ERR_BAD_SHAPE;
   if (experts < 2 || experts > kMaxExperts) return PARROT_ERR_UNSUPPORTED;
@@ -502,8 +502,26 @@ int parrot_route_top2_bf16(const void* x, const void* router_weight, const float
   return status(parrot::launch_route(static_cast<const uint16_t*>(x),
                                      static_cast<const uint16_t*>(router_weight), nullptr,
                                      logit_bias, tokens, dim, experts, nullptr, nullptr,
-                                     out_weights, out_indices, nullptr, nullptr,
+                                     out_weights, out_indices, nullptr, nullptr, out_blocks,
                                      as_stream(stream)));
+}
+
+int parrot_route_top2_bf16(const void* x, const void* router_weight, const float* logit_bias,
+                           int64_t tokens, int32_t dim, int32_t experts, float* out_weights,
+                           int64_t* out_indices, void* stream) {
+  return route_top2_common(x, router_weight, logit_bias, tokens, dim, experts, out_weights,
+                           out_indices, nullptr, stream);
+}
+
+int parrot_route_top2_blocks_bf16(const void* x, const void* router_weight,
+                                  const float* logit_bias, int64_t tokens, int32_t dim,
+                                  int32_t experts, float* out_weights, int64_t* out_indices,
+                                  void* out_blocks, void* stream) {
+  if (!out_blocks) return PARROT_ERR_NULL_POINTER;
+  if (tokens > 0 && !parrot::route_block_rows_supported(tokens)) return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(out_blocks)) return PARROT_ERR_ALIGNMENT;
+  return route_top2_common(x, router_weight, logit_bias, tokens, dim, experts, out_weights,
+                           out_indices, static_cast<uint8_t*>(out_blocks), stream);
 }
 
 int parrot_route_from_logits_f32(const float* logits, const float* logit_bias, int64_t tokens,
@@ -613,30 +631,38 @@ int parrot_experts_group_in_kernel(int64_t tokens, int32_t dim, int32_t experts,
                                    int32_t hidden_dim, int32_t shared_dim) {
   if (experts < 2 || experts > kMaxExperts || dim <= 0 || hidden_dim <= 0 || shared_dim <= 0)
     return 0;
-  return parrot::experts_group_in_kernel(tokens, dim, experts, hidden_dim, shared_dim) ? 1 : 0;
+  return static_cast<int>(
+      parrot::experts_group_in_kernel(tokens, dim, experts, hidden_dim, shared_dim));
 }
 
-int parrot_experts_gate_up_grouping_bf16(const void* x, int64_t tokens, int32_t dim,
-                                         int32_t experts, int32_t hidden_dim,
-                                         int32_t shared_dim, int32_t capacity,
-                                         const int64_t* indices, int32_t* out_counts,
-                                         int32_t* out_offsets, int32_t* out_sorted,
-                                         const void* packed_gate_up, const void* shared_gate_up,
-                                         void* workspace, size_t workspace_bytes, void* stream) {
-  if (!x || !indices || !out_counts || !out_offsets || !out_sorted || !packed_gate_up ||
-      !shared_gate_up)
+// The gate/up launch that groups in-kernel, from the top-2 indices
+// (kGroupFromIds shapes) or from the route's block table (kGroupFromIds or
+// kGroupFromBlocks shapes).
+static int gate_up_grouping_common(const void* x, int64_t tokens, int32_t dim, int32_t experts,
+                                   int32_t hidden_dim, int32_t shared_dim, int32_t capacity,
+                                   const int64_t* indices, const uint8_t* blocks,
+                                   int32_t* out_counts, int32_t* out_offsets,
+                                   int32_t* out_sorted, const void* packed_gate_up,
+                                   const void* shared_gate_up, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (!x || (!indices && !blocks) || !out_counts || !out_offsets || !out_sorted ||
+      !packed_gate_up || !shared_gate_up)
     return PARROT_ERR_NULL_POINTER;
   ExpertsWorkspace ws;
   if (int rc = check_experts_shape(tokens, dim, experts, hidden_dim, shared_dim, capacity,
                                    workspace, workspace_bytes, &ws))
     return rc;
   if (tokens == 0) return PARROT_OK;
-  if (!parrot::experts_group_in_kernel(tokens, dim, experts, hidden_dim, shared_dim))
+  const parrot::GroupInKernel mode =
+      parrot::experts_group_in_kernel(tokens, dim, experts, hidden_dim, shared_dim);
+  if (mode == parrot::kGroupNone || (indices && mode != parrot::kGroupFromIds))
     return PARROT_ERR_UNSUPPORTED;
-  if (!aligned16(x) || !aligned16(packed_gate_up) || !aligned16(shared_gate_up))
+  if (!aligned16(x) || !aligned16(packed_gate_up) || !aligned16(shared_gate_up) ||
+      (blocks && !aligned16(blocks)))
     return PARROT_ERR_ALIGNMENT;
   parrot::GroupMap map{nullptr, nullptr, nullptr, nullptr, nullptr};
   map.indices = indices;
+  map.route_blocks = blocks;
   map.counts_out = out_counts;
   map.offsets_out = out_offsets;
   map.sorted_out = out_sorted;
@@ -646,6 +672,32 @@ int parrot_experts_gate_up_grouping_bf16(const void* x, int64_t tokens, int32_t 
                                            experts, hidden_dim, shared_dim, capacity, map, w,
                                            ws.hidden, ws.y_routed, ws.y_shared,
                                            as_stream(stream)));
+}
+
+int parrot_experts_gate_up_grouping_bf16(const void* x, int64_t tokens, int32_t dim,
+                                         int32_t experts, int32_t hidden_dim,
+                                         int32_t shared_dim, int32_t capacity,
+                                         const int64_t* indices, int32_t* out_counts,
+                                         int32_t* out_offsets, int32_t* out_sorted,
+                                         const void* packed_gate_up, const void* shared_gate_up,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (!indices) return PARROT_ERR_NULL_POINTER;
+  return gate_up_grouping_common(x, tokens, dim, experts, hidden_dim, shared_dim, capacity,
+                                 indices, nullptr, out_counts, out_offsets, out_sorted,
+                                 packed_gate_up, shared_gate_up, workspace, workspace_bytes,
+                                 stream);
+}
+
+int parrot_experts_gate_up_grouping_blocks_bf16(
+    const void* x, int64_t tokens, int32_t dim, int32_t experts, int32_t hidden_dim,
+    int32_t shared_dim, int32_t capacity, const void* route_blocks, int32_t* out_counts,
+    int32_t* out_offsets, int32_t* out_sorted, const void* packed_gate_up,
+    const void* shared_gate_up, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!route_blocks) return PARROT_ERR_NULL_POINTER;
+  return gate_up_grouping_common(x, tokens, dim, experts, hidden_dim, shared_dim, capacity,
+                                 nullptr, static_cast<const uint8_t*>(route_blocks),
+                                 out_counts, out_offsets, out_sorted, packed_gate_up,
+                                 shared_gate_up, workspace, workspace_bytes, stream);
 }
 
 int parrot_experts_down_sorted_bf16(int64_t tokens, int32_t dim, int32_t experts,

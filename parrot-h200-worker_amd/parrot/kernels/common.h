@@ -17,6 +17,12 @@ constexpr int kMaxDepthSources = 9;
 constexpr int kRouteTokensPerBlock = 16;
 constexpr int kRouteAssignPerBlock = 2 * kRouteTokensPerBlock;
 constexpr int kScanChunk = 256;  // route blocks per chunk of the two-level histogram scan
+// A route block's row of the block table (launch_route's `block_rows`, read
+// by the gate/up launch that groups in-kernel): bytes 0-31 the block's 32
+// expert ids in assignment order (kNoExpert for padding tokens), bytes
+// 32-63 its number of assignments to each expert (0 past E).
+constexpr int kRouteBlockRowBytes = 64;
+constexpr uint32_t kNoExpert = 0xff;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -272,12 +278,18 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
 
 // Routing: router projection (or given fp32 logits) + top-2 + per-block
 // stable ranks.  Writes block-local ranks into `positions` and per-block
-// expert histograms into `block_counts` [n_blocks, experts].
+// expert histograms into `block_counts` [n_blocks, experts]; with
+// `block_rows` (tokens below kWideRouteTokens), the block table
+// [n_blocks, kRouteBlockRowBytes].
 hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
                         const float* given_logits, const float* bias,
                         int64_t tokens, int dim, int experts, float* out_logits,
                         float* probs, float* weights, int64_t* indices,
-                        int32_t* positions, int32_t* block_counts, hipStream_t s);
+                        int32_t* positions, int32_t* block_counts, uint8_t* block_rows,
+                        hipStream_t s);
+
+// Whether launch_route writes `block_rows` for this many tokens.
+bool route_block_rows_supported(int64_t tokens);
 
 // Number of 16-token route blocks (= rows of block_counts) for `tokens`.
 int route_blocks(int64_t tokens);
@@ -320,6 +332,9 @@ struct GroupMap {
   // and writes `counts_out`, `offsets_out` and `sorted` (the assignment id of
   // each hidden row); phase 2 then reads counts / offsets / sorted.
   const int64_t* indices = nullptr;  // [2T]
+  // ... or the route's block table (launch_route's block_rows) instead of
+  // the indices, past the assignments the indices form takes.
+  const uint8_t* route_blocks = nullptr;  // [ceil(T / 16), kRouteBlockRowBytes]
   int32_t* counts_out = nullptr;     // [E]
   int32_t* offsets_out = nullptr;    // [2E+2]
   const int32_t* sorted = nullptr;   // [2T], phase 2
@@ -327,9 +342,12 @@ struct GroupMap {
 };
 
 // Whether a gate/up launch can group its assignments itself (the streaming
-// kernel's shapes, at most 2048 assignments).
-bool experts_group_in_kernel(int64_t tokens, int dim, int experts, int hidden_dim,
-                             int shared_dim);
+// kernel's shapes): kGroupFromIds from the top-2 indices (at most 2048
+// assignments, ~3 x 32 rows per expert), kGroupFromBlocks from the route's
+// block table (at most 256 route blocks), else kGroupNone.
+enum GroupInKernel { kGroupNone = 0, kGroupFromIds = 1, kGroupFromBlocks = 2 };
+GroupInKernel experts_group_in_kernel(int64_t tokens, int dim, int experts, int hidden_dim,
+                                      int shared_dim);
 
 // Grouped SwiGLU expert GEMM over every routed assignment plus the shared
 // expert.  Phase 1 (gate/up + SwiGLU) reads x and writes hidden

@@ -47,6 +47,7 @@ struct GemmArgs {
   // offsets and the hidden rows' assignment ids out.  Phase 2 with `sorted`
   // reads a row's assignment id there instead of perm / overflow.
   const int64_t* indices;
+  const uint8_t* route_blocks;  // or the route's block table (group_find_blocks)
   int32_t* counts_out;
   int32_t* offsets_out;
   int32_t* sorted_out;
@@ -85,7 +86,8 @@ __device__ __forceinline__ void load_gemm_args(const GemmArgs& p) {
                "s"(p.offsets), "s"(p.perm), "s"(p.overflow), "s"(p.sorted), "s"(p.indices),
                "s"(p.w_routed), "s"(p.w_shared), "s"(p.a_src), "s"(p.weights),
                "s"(p.hidden_out), "s"(p.y_routed), "s"(p.y_shared), "s"(p.counts_out),
-               "s"(p.offsets_out), "s"(p.sorted_out), "s"(p.rows_per_xcd), "s"(gridDim.x));
+               "s"(p.offsets_out), "s"(p.sorted_out), "s"(p.rows_per_xcd), "s"(gridDim.x),
+               "s"(p.route_blocks));
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -189,8 +191,48 @@ __device__ __forceinline__ int scan32(int v) {
 }
 
 struct GroupIds {
-  int ids[kGroupChunksPerWave];  // this lane's ids, chunk w + 4 j (-1: none)
+  // group_find: this lane's ids, chunk w + 4 j (-1: none); group_find_blocks:
+  // the count words of this thread's route block (zero past the last).
+  int ids[kGroupChunksPerWave];
 };
+
+// The routed tile of row tile m (counted past the shared expert's tiles)
+// from lane e's count of expert e: its tiles and overflow rows, and their
+// exclusive prefixes over the experts before it.  The first routed
+// workgroup of column 0 writes counts and both offset tables.  False
+// (uniform) when no expert has tile m.
+template <int BM>
+__device__ __forceinline__ bool locate_tile(const GemmArgs& p, int count, int m, TileIndex ti,
+                                            Tile& t) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int E = p.experts;
+  const int tiles = (count + BM - 1) / BM;
+  const int ovf = max(0, count - p.capacity);
+  const int tile0 = scan32(tiles) - tiles;
+  const int h_end = scan32(count);
+  const int o_end = scan32(ovf);
+  if (ti.n == 0 && m == 0 && wave == 0) {
+    const int h_total = __builtin_amdgcn_readlane(h_end, E - 1);
+    const int o_total = __builtin_amdgcn_readlane(o_end, E - 1);
+    if (lane < E) {
+      p.counts_out[lane] = count;
+      p.offsets_out[lane] = h_end - count;
+      p.offsets_out[E + 1 + lane] = o_end - ovf;
+    }
+    if (lane == E) {
+      p.offsets_out[E] = h_total;
+      p.offsets_out[2 * E + 1] = o_total;
+    }
+  }
+  const uint64_t hit = __ballot(lane < E && m >= tile0 && m < tile0 + tiles);
+  if (hit == 0) return false;  // uniform: no tile for this workgroup
+  const int seg = static_cast<int>(__builtin_ctzll(hit));
+  t = Tile{seg, m - __builtin_amdgcn_readlane(tile0, seg), __builtin_amdgcn_readlane(count, seg),
+           __builtin_amdgcn_readlane(h_end - count, seg),
+           __builtin_amdgcn_readlane(o_end - ovf, seg)};
+  return true;
+}
 
 template <int BM>
 __device__ __forceinline__ bool group_find(const GemmArgs& p, int T, Tile& t, GroupIds& g,
@@ -225,36 +267,10 @@ __device__ __forceinline__ bool group_find(const GemmArgs& p, int T, Tile& t, Gr
   }
   __syncthreads();
 
-  // Lane e: expert e's count, its tiles and its overflow rows, and their
-  // exclusive prefixes over the experts before it.
+  // Lane e: expert e's count.
   const int count =
       lane < E ? hist_s[0][lane] + hist_s[1][lane] + hist_s[2][lane] + hist_s[3][lane] : 0;
-  const int tiles = (count + BM - 1) / BM;
-  const int ovf = max(0, count - p.capacity);
-  const int tile0 = scan32(tiles) - tiles;
-  const int h_end = scan32(count);
-  const int o_end = scan32(ovf);
-  m -= shared_tiles;
-  if (ti.n == 0 && m == 0 && wave == 0) {
-    const int h_total = __builtin_amdgcn_readlane(h_end, E - 1);
-    const int o_total = __builtin_amdgcn_readlane(o_end, E - 1);
-    if (lane < E) {
-      p.counts_out[lane] = count;
-      p.offsets_out[lane] = h_end - count;
-      p.offsets_out[E + 1 + lane] = o_end - ovf;
-    }
-    if (lane == E) {
-      p.offsets_out[E] = h_total;
-      p.offsets_out[2 * E + 1] = o_total;
-    }
-  }
-  const uint64_t hit = __ballot(lane < E && m >= tile0 && m < tile0 + tiles);
-  if (hit == 0) return false;  // uniform: no tile for this workgroup
-  const int seg = static_cast<int>(__builtin_ctzll(hit));
-  t = Tile{seg, m - __builtin_amdgcn_readlane(tile0, seg), __builtin_amdgcn_readlane(count, seg),
-           __builtin_amdgcn_readlane(h_end - count, seg),
-           __builtin_amdgcn_readlane(o_end - ovf, seg)};
-  return true;
+  return locate_tile<BM>(p, count, m - shared_tiles, ti, t);
 }
 
 template <int BM>
@@ -290,6 +306,128 @@ __device__ __forceinline__ void group_rows(const GemmArgs& p, int T, const Tile&
         row_src[r] = a >> 1;
         row_dst[r] = t.hbase + rank;
         if (first_column) p.sorted_out[t.hbase + rank] = a;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Grouping inside the gate/up launch from the route's block table (up to
+// kGroupMaxRouteBlocks route blocks, one per thread): the same tile, rows
+// and outputs as group_find / group_rows, without reading all 2T ids.
+//   1. (group_find_blocks) thread b loads the count half of route block b's
+//      table row; the per-expert counts are those bytes summed over the
+//      workgroup, as 16-bit pairs (a wavefront's sums stay below 2^16);
+//   2. (group_rows_blocks) thread b takes block b's count of its tile's
+//      expert from the same bytes, an exclusive scan over the blocks gives
+//      the block's first rank, and only the threads whose ranks meet the
+//      tile load their block's ids and place those rows in assignment
+//      order.  Reading the id half only there keeps the table traffic of a
+//      launch (every workgroup reads every block's counts) at 32 bytes per
+//      block per workgroup.
+constexpr int kGroupMaxRouteBlocks = 256;
+
+// Inclusive prefix sum over the 64 lanes: row shifts by 1, 2, 4, 8, then
+// lane 15 broadcast into the next row and lane 31 into rows 2 and 3.
+__device__ __forceinline__ uint32_t scan64(uint32_t v) {
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+
+template <int BM>
+__device__ __forceinline__ bool group_find_blocks(const GemmArgs& p, int T, Tile& t, GroupIds& g,
+                                                  int* row_src, int* row_dst,
+                                                  int (*hist_s)[kMaxExperts], TileIndex ti) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int shared_tiles = (T + BM - 1) / BM;
+  const int m = ti.m;
+  if (m < shared_tiles) {
+    t = Tile{p.experts, m, T, 2 * T, 0};
+    return true;
+  }
+  const int E = p.experts;
+  const int n_blocks = (T + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock;
+  const bool mine = tid < n_blocks;
+  const uint4* row = reinterpret_cast<const uint4*>(
+      p.route_blocks + static_cast<int64_t>(mine ? tid : 0) * kRouteBlockRowBytes);
+  const uint4 cnt0 = row[2], cnt1 = row[3];
+  const uint32_t cw[8] = {cnt0.x, cnt0.y, cnt0.z, cnt0.w, cnt1.x, cnt1.y, cnt1.z, cnt1.w};
+  // Kept for group_rows_blocks: this block's count words (zero past the end).
+#pragma unroll
+  for (int k = 0; k < 8; ++k) g.ids[k] = static_cast<int>(mine ? cw[k] : 0u);
+  if (tid < BM) {
+    row_src[tid] = 0;
+    row_dst[tid] = -1;
+  }
+  // Count word k holds experts 4k .. 4k + 3 (byte r = expert 4k + r): its
+  // even bytes (experts 4k, 4k + 2) and odd bytes (4k + 1, 4k + 3) as
+  // 16-bit pairs, summed over the wavefront into lane 63.
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t w = static_cast<uint32_t>(g.ids[k]);
+    const uint32_t even = scan64(w & 0x00ff00ffu);
+    const uint32_t odd = scan64((w >> 8) & 0x00ff00ffu);
+    if (lane == kWave - 1) {
+      hist_s[wave][2 * k] = static_cast<int>(even);
+      hist_s[wave][2 * k + 1] = static_cast<int>(odd);
+    }
+  }
+  __syncthreads();
+  // Lane e: expert e's count, from pair 2 (e / 4) + (e % 2), half (e / 2) % 2.
+  int count = 0;
+  if (lane < E) {
+    const int w = 2 * (lane >> 2) + (lane & 1);
+    const int sh = (lane & 2) ? 16 : 0;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) count += (static_cast<uint32_t>(hist_s[v][w]) >> sh) & 0xffffu;
+  }
+  return locate_tile<BM>(p, count, m - shared_tiles, ti, t);
+}
+
+template <int BM>
+__device__ __forceinline__ void group_rows_blocks(const GemmArgs& p, const Tile& t,
+                                                  const GroupIds& g, int* row_src, int* row_dst,
+                                                  int* scan_s, bool first_column) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Block tid's count of expert t.seg: byte seg % 4 of count word seg / 4.
+  uint32_t word = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) word = k == (t.seg >> 2) ? static_cast<uint32_t>(g.ids[k]) : word;
+  const int c = static_cast<int>((word >> (8 * (t.seg & 3))) & 0xffu);
+  const int inc = static_cast<int>(scan64(static_cast<uint32_t>(c)));
+  if (lane == kWave - 1) scan_s[wave] = inc;
+  __syncthreads();
+  int base = inc - c;
+#pragma unroll
+  for (int v = 0; v < 3; ++v) base += v < wave ? scan_s[v] : 0;
+  const int r_lo = t.mt * BM;
+  if (c > 0 && base < r_lo + BM && base + c > r_lo) {
+    const uint4* row =
+        reinterpret_cast<const uint4*>(p.route_blocks + static_cast<int64_t>(tid) * kRouteBlockRowBytes);
+    const uint4 id0 = row[0], id1 = row[1];
+    const uint32_t ids[8] = {id0.x, id0.y, id0.z, id0.w, id1.x, id1.y, id1.z, id1.w};
+    int rank = base;
+#pragma unroll
+    for (int j = 0; j < kRouteAssignPerBlock; ++j) {
+      const int id = static_cast<int>((ids[j >> 2] >> (8 * (j & 3))) & 0xffu);
+      if (id == t.seg) {
+        const int r = rank - r_lo;
+        if (r >= 0 && r < BM) {
+          const int a = tid * kRouteAssignPerBlock + j;
+          row_src[r] = a >> 1;
+          row_dst[r] = t.hbase + rank;
+          if (first_column) p.sorted_out[t.hbase + rank] = a;
+        }
+        ++rank;
       }
     }
   }
@@ -860,13 +998,18 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
   const int wave = tid >> 6;
   const int T = static_cast<int>(p.tokens);
 
-  // Phase 1 groups in-kernel when given the top-2 ids (uniform per launch).
-  const bool self_grouped = PHASE == 1 && p.indices != nullptr;
+  // Phase 1 groups in-kernel when given the top-2 ids or the route's block
+  // table (uniform per launch).
+  const bool from_blocks = PHASE == 1 && p.route_blocks != nullptr;
+  const bool self_grouped = PHASE == 1 && (p.indices != nullptr || from_blocks);
   const TileIndex ti = xcd_tile(p.rows_per_xcd != 0);
   Tile t;
   GroupIds gids;
   if (self_grouped) {
-    if (!group_find<BM>(p, T, t, gids, row_src, row_dst, hist_s, ti)) return;
+    const bool found = from_blocks
+                           ? group_find_blocks<BM>(p, T, t, gids, row_src, row_dst, hist_s, ti)
+                           : group_find<BM>(p, T, t, gids, row_src, row_dst, hist_s, ti);
+    if (!found) return;
   } else if (!find_tile<BM>(p, T, t, ti.m)) {
     return;
   }
@@ -912,7 +1055,10 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
       bq[i][j] = buffer_load16(b_rsrc, b_off[j], static_cast<uint32_t>(min(i, ksteps - 1)) * 1024);
 
   // ---- per-row source / destination (the weight loads are in flight) -------
-  if (self_grouped && !shared) group_rows<BM>(p, T, t, gids, row_src, row_dst, chunk_s, ti.n == 0);
+  if (self_grouped && !shared) {
+    if (from_blocks) group_rows_blocks<BM>(p, t, gids, row_src, row_dst, chunk_s, ti.n == 0);
+    else group_rows<BM>(p, T, t, gids, row_src, row_dst, chunk_s, ti.n == 0);
+  }
   if (PHASE == 1) {
     if (tid < BM && (shared || !self_grouped)) {
       row_src[tid] = shared ? sc : asg >> 1;
@@ -1196,12 +1342,19 @@ int stream_rows_per_xcd(int phase, int64_t tokens, int dim, int, int, int) {
 
 }  // namespace
 
-bool experts_group_in_kernel(int64_t tokens, int dim, int experts, int hidden_dim,
-                             int shared_dim) {
-  if (tokens < 1 || 2 * tokens > kGroupMaxAssign || experts > kMaxExperts) return false;
-  // Up to ~3 x 32 rows per expert on average (the shapes it was measured at).
-  if ((2 * tokens + experts - 1) / experts > 96) return false;
-  return dim <= kStreamKCap && max(hidden_dim, shared_dim) <= kStreamKCap;
+GroupInKernel experts_group_in_kernel(int64_t tokens, int dim, int experts, int hidden_dim,
+                                      int shared_dim) {
+  if (tokens < 1 || experts > kMaxExperts) return kGroupNone;
+  if (dim > kStreamKCap || max(hidden_dim, shared_dim) > kStreamKCap) return kGroupNone;
+  // The streaming kernel groups; the wide tiles' plan does not.
+  if (experts_tile_plan(1, tokens, experts) == TilePlan::kWide128) return kGroupNone;
+  // From the ids: up to ~3 x 32 rows per expert on average (the shapes it
+  // was measured at).
+  if (2 * tokens <= kGroupMaxAssign && (2 * tokens + experts - 1) / experts <= 96)
+    return kGroupFromIds;
+  if (route_blocks(tokens) <= kGroupMaxRouteBlocks && route_block_rows_supported(tokens))
+    return kGroupFromBlocks;
+  return kGroupNone;
 }
 
 hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int dim,
@@ -1227,10 +1380,13 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
   args.y_shared = y_shared;
   args.sorted = phase == 2 ? map.sorted : nullptr;
   args.rows_per_xcd = stream_rows_per_xcd(phase, tokens, dim, experts, hidden_dim, shared_dim);
-  if (phase == 1 && map.indices != nullptr) {
-    if (!experts_group_in_kernel(tokens, dim, experts, hidden_dim, shared_dim))
+  if (phase == 1 && (map.indices != nullptr || map.route_blocks != nullptr)) {
+    const GroupInKernel mode = experts_group_in_kernel(tokens, dim, experts, hidden_dim,
+                                                       shared_dim);
+    if (mode == kGroupNone || (map.route_blocks == nullptr && mode != kGroupFromIds))
       return hipErrorInvalidValue;
-    args.indices = map.indices;
+    args.indices = map.route_blocks != nullptr ? nullptr : map.indices;
+    args.route_blocks = map.route_blocks;
     args.counts_out = map.counts_out;
     args.offsets_out = map.offsets_out;
     args.sorted_out = map.sorted_out;

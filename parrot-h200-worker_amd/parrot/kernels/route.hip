@@ -55,6 +55,29 @@ __device__ __forceinline__ void rank_half_waves(int id, int64_t block, int64_t n
   if ((lane & 31) < experts && block < n_blocks) block_counts[block * experts + (lane & 31)] = count;
 }
 
+// The block table row of one route block (kRouteBlockRowBytes bytes, the
+// layout common.h states), written by wavefront 0 whose lanes 0-31 hold the
+// block's assignment ids (-1 = padding) and lanes 32-63 none: a ballot per
+// expert counts its ids (lane 32 + e keeps expert e's count), so lane l
+// holds byte l of the row, and lanes 0-15 store it as 16 dwords.
+__device__ __forceinline__ void write_block_row(int id, int64_t block, int experts,
+                                                uint8_t* block_rows) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t byte = lane < 32 ? (id >= 0 ? static_cast<uint32_t>(id) : kNoExpert) : 0u;
+#pragma unroll 1
+  for (int e = 0; e < experts; ++e) {
+    const uint64_t m = __ballot(id == e);
+    if (lane == 32 + e) byte = static_cast<uint32_t>(__popcll(m));
+  }
+  const int b0 = 4 * (lane & 15);
+  const uint32_t word = static_cast<uint32_t>(__shfl(static_cast<int>(byte), b0)) |
+                        static_cast<uint32_t>(__shfl(static_cast<int>(byte), b0 + 1)) << 8 |
+                        static_cast<uint32_t>(__shfl(static_cast<int>(byte), b0 + 2)) << 16 |
+                        static_cast<uint32_t>(__shfl(static_cast<int>(byte), b0 + 3)) << 24;
+  if (lane < 16)
+    reinterpret_cast<uint32_t*>(block_rows + block * kRouteBlockRowBytes)[lane] = word;
+}
+
 // One workgroup routes one 16-token route block.  The router projection
 // [16 x dim] . [dim x E] runs on v_mfma_f32_16x16x32_bf16 with the 32-wide
 // k steps split round-robin over the 4 wavefronts; each wavefront issues the
@@ -62,6 +85,8 @@ __device__ __forceinline__ void rank_half_waves(int id, int64_t block, int64_t n
 // in a fixed order through LDS.  Fragments: lane l holds row/col (l & 15)
 // and the 8 k values at (l >> 4) * 8 of a step; C holds column (l & 15),
 // rows 4 (l >> 4) + r.  With GIVEN_LOGITS the fp32 logits are read instead.
+// Wavefront 0 then ranks the block (with `positions`) and writes its block
+// table row (with `block_rows`).
 // This split-K shape keeps short inputs (prefill, decode) latency-bound at
 // the minimum.
 template <bool GIVEN_LOGITS>
@@ -71,11 +96,11 @@ __global__ __launch_bounds__(256) void route_kernel(
     int64_t tokens, int dim, int experts, float* __restrict__ out_logits,
     float* __restrict__ probs, float* __restrict__ weights,
     int64_t* __restrict__ indices, int32_t* __restrict__ positions,
-    int32_t* __restrict__ block_counts) {
+    int32_t* __restrict__ block_counts, uint8_t* __restrict__ block_rows) {
   // The kernel arguments in one batch of scalar loads before any use.
   asm volatile("" ::"s"(x), "s"(wr), "s"(given), "s"(bias), "s"(tokens), "s"(dim), "s"(experts),
                "s"(out_logits), "s"(probs), "s"(weights), "s"(indices), "s"(positions),
-               "s"(block_counts));
+               "s"(block_counts), "s"(block_rows));
   __builtin_amdgcn_sched_barrier(0);
   __shared__ float part_s[4][kRouteTokensPerBlock][kMaxExperts + 1];
   __shared__ int ids_s[kRouteAssignPerBlock];
@@ -153,14 +178,17 @@ __global__ __launch_bounds__(256) void route_kernel(
     select_top2(l0, l1, experts, t0 + tl, t0 + tl < tokens, out_logits, probs, weights, indices,
                 &ids_s[2 * tl]);
   }
-  if (positions == nullptr) return;  // uniform: a top-2-only launch ranks nothing
+  // Uniform: a top-2-only launch neither ranks nor tabulates the block.
+  if (positions == nullptr && block_rows == nullptr) return;
   __syncthreads();
   // Wavefront 0 ranks the block in lanes 0-31; lanes 32-63 carry no
   // assignments and name no block (index gridDim.x is past the last).
   if (threadIdx.x < kWave) {
     const bool mine = threadIdx.x < kRouteAssignPerBlock;
-    rank_half_waves(mine ? ids_s[threadIdx.x] : -1, mine ? blockIdx.x : gridDim.x, gridDim.x,
-                    2 * tokens, experts, positions, block_counts);
+    const int id = mine ? ids_s[threadIdx.x] : -1;
+    rank_half_waves(id, mine ? blockIdx.x : gridDim.x, gridDim.x, 2 * tokens, experts, positions,
+                    block_counts);
+    if (block_rows != nullptr) write_block_row(id, blockIdx.x, experts, block_rows);
   }
 }
 
@@ -466,13 +494,15 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
                         const float* given_logits, const float* bias,
                         int64_t tokens, int dim, int experts, float* out_logits,
                         float* probs, float* weights, int64_t* indices,
-                        int32_t* positions, int32_t* block_counts, hipStream_t s) {
+                        int32_t* positions, int32_t* block_counts, uint8_t* block_rows,
+                        hipStream_t s) {
   if (tokens == 0) return hipSuccess;
+  if (block_rows != nullptr && !route_block_rows_supported(tokens)) return hipErrorInvalidValue;
   const int nrb = route_blocks(tokens);
   if (given_logits != nullptr) {
     route_kernel<true><<<nrb, 256, 0, s>>>(x, router_w, given_logits, bias, tokens, dim, experts,
                                            out_logits, probs, weights, indices, positions,
-                                           block_counts);
+                                           block_counts, block_rows);
   } else if (tokens >= kWideRouteTokens &&
              (experts > 16 ? 32 : 16) * (dim + 8) * 2 <= kWideRouteLdsBytes) {
     const bool two = experts > 16;
@@ -483,10 +513,12 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
   } else {
     route_kernel<false><<<nrb, 256, 0, s>>>(x, router_w, given_logits, bias, tokens, dim,
                                             experts, out_logits, probs, weights, indices,
-                                            positions, block_counts);
+                                            positions, block_counts, block_rows);
   }
   return hipGetLastError();
 }
+
+bool route_block_rows_supported(int64_t tokens) { return tokens < kWideRouteTokens; }
 
 hipError_t launch_rank_indices(const int64_t* indices, int64_t tokens, int experts,
                                int32_t* positions, int32_t* block_counts, hipStream_t s) {

@@ -741,7 +741,8 @@ class MoE(nn.Module):
             return hip_moe.decode_experts(self, flat, addend=addend)[0].view_as(x)
         routed = hip_moe.route_for_experts(self, flat)
         result = hip_moe.grouped_hip_experts(self, flat, routed.indices, routed.weights,
-                                             addend=addend, grouping=routed.grouping)
+                                             addend=addend, grouping=routed.grouping,
+                                             route_blocks=routed.blocks)
         return result.view_as(x)
 
 
@@ -773,7 +774,8 @@ class MoE(nn.Module):
                 routed = hip_moe.route_for_experts(self, flat)
             result, mixed = hip_moe.grouped_hip_experts(
                 self, flat, routed.indices, routed.weights, addend=addend,
-                grouping=routed.grouping, then_mix=(depth, sources, output_norm))
+                grouping=routed.grouping, then_mix=(depth, sources, output_norm),
+                route_blocks=routed.blocks)
             return result.view_as(x), mixed.view_as(x)
         result = self.inference(x, direct=False, addend=addend)
         return result, depth.normalized(sources + [result], output_norm)

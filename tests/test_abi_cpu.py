@@ -279,12 +279,37 @@ def test_argument_validation_without_gpu(lib):
         ctypes.cast(srcs, ctypes.c_void_p), 2, fake, fake, 1e-6, fake, 1e-6, 4, 64, null, fake,
         fake + 8, null, 8, fake, fake, null) == -5
     # in-kernel grouping: which shapes, and its entry points' checks
+    # 1: from the ids; 2: from the route block table only; 0: neither
     assert lib.parrot_experts_group_in_kernel(512, 768, 16, 512, 256) == 1
     assert lib.parrot_experts_group_in_kernel(1024, 768, 32, 512, 256) == 1
-    assert lib.parrot_experts_group_in_kernel(1025, 768, 32, 512, 256) == 0  # > 2048 ids
-    assert lib.parrot_experts_group_in_kernel(1024, 768, 16, 512, 256) == 0  # 128 rows/expert
+    assert lib.parrot_experts_group_in_kernel(1025, 768, 32, 512, 256) == 2  # > 2048 ids
+    assert lib.parrot_experts_group_in_kernel(1024, 768, 16, 512, 256) == 2  # 128 rows/expert
+    assert lib.parrot_experts_group_in_kernel(4096, 768, 32, 512, 256) == 2  # config 3
+    assert lib.parrot_experts_group_in_kernel(4097, 768, 32, 512, 256) == 0  # > 256 blocks
+    assert lib.parrot_experts_group_in_kernel(4096, 768, 16, 512, 256) == 0  # wide tiles
     assert lib.parrot_experts_group_in_kernel(512, 1024, 16, 512, 256) == 0  # dim > 768
     assert lib.parrot_experts_group_in_kernel(512, 768, 33, 512, 256) == 0
+    # the route block table: T < 32768, 16-byte aligned
+    assert lib.parrot_route_top2_blocks_bf16(fake, fake, null, 64, 768, 16, fake, fake, null,
+                                             null) == -1
+    assert lib.parrot_route_top2_blocks_bf16(fake, fake, null, 32768, 768, 16, fake, fake,
+                                             fake, null) == -3
+    assert lib.parrot_route_top2_blocks_bf16(fake, fake, null, 64, 768, 16, fake, fake,
+                                             fake + 8, null) == -5
+    bws = lib.parrot_experts_workspace_bytes(4096, 768, 512, 256)
+    blocks = lambda **kw: lib.parrot_experts_gate_up_grouping_blocks_bf16(*[
+        kw.get(k, v) for k, v in (
+            ("x", fake), ("T", 4096), ("dim", 768), ("E", 32), ("H", 512), ("Hs", 256),
+            ("C", 512), ("tab", fake), ("cnt", fake), ("off", fake), ("srt", fake),
+            ("gu", fake), ("sgu", fake), ("ws", fake), ("wsb", bws), ("stream", null))])
+    assert blocks(tab=null) == -1 and blocks(srt=null) == -1
+    assert blocks(T=4097, wsb=lib.parrot_experts_workspace_bytes(4097, 768, 512, 256)) == -3
+    assert blocks(E=16, C=1024) == -3  # wide tiles at 512 rows per expert
+    assert blocks(tab=fake + 8) == -5
+    # the ids form stays within its own shapes
+    assert lib.parrot_experts_gate_up_grouping_bf16(
+        fake, 4096, 768, 32, 512, 256, 512, fake, fake, fake, fake, fake, fake, fake, bws,
+        null) == -3
     gws = lib.parrot_experts_workspace_bytes(512, 768, 512, 256)
     assert lib.parrot_experts_gate_up_grouping_bf16(
         fake, 512, 768, 16, 512, 256, 80, null, fake, fake, fake, fake, fake, fake, gws,

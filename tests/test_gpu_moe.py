@@ -320,3 +320,54 @@ def test_experts_group_in_kernel(tokens, experts, skewed):
     assert torch.equal(buf[:experts], g.counts.cpu())
     assert torch.equal(buf[experts:3 * experts + 2], g.offsets.cpu())
     assert torch.equal(buf[3 * experts + 2:], _sorted_from_grouping(g, experts))
+
+
+@pytest.mark.parametrize("tokens,experts,skewed", [
+    (4096, 32, True), (2048, 16, False), (1025, 32, False), (300, 16, True), (17, 16, False),
+    (4096, 32, False)])
+def test_experts_group_from_route_blocks(tokens, experts, skewed):
+    """The gate/up launch that groups from the route block table (the form
+    past 2048 assignments; it also takes the smaller shapes) gives the route +
+    group path's MoE output bit for bit, and writes that path's grouping
+    (counts, offsets, the hidden rows' assignment ids); through the C-ABI
+    entries as the standalone layer calls them."""
+    from parrot import _abi, hip_moe
+    from parrot._abi import ptr
+    _say(f"grouping from the route block table T={tokens} E={experts} skew={skewed}")
+    module = moe_module(experts, seed=10)
+    x = inputs(tokens, seed=10)
+    cfg = module.cfg
+    dim, H, Hs = x.shape[1], cfg.expert_dim, cfg.shared_expert_dim
+    lib = _abi.load()
+    assert lib.parrot_experts_group_in_kernel(tokens, dim, experts, H, Hs) in (1, 2)
+    bias = skew_bias(experts) if skewed else None
+    with torch.no_grad():
+        routed = hip_moe.route(module, x, False, logit_bias=bias)
+        ref = hip_moe.grouped_hip_experts(module, x, routed.indices, routed.weights,
+                                          grouping=routed.grouping)
+        tab = hip_moe.route_top2(module, x, logit_bias=bias, blocks=True)
+    assert torch.equal(tab.indices, routed.indices) and torch.equal(tab.weights, routed.weights)
+    g = routed.grouping
+    _say(f"  overflow {int(g.offsets[-1])} of {2 * tokens}, max count {int(g.counts.max())}")
+    gate_up, down, shared_gate_up, shared_down = hip_moe.pack_expert_weights(module)
+    nbytes = lib.parrot_experts_workspace_bytes(tokens, dim, H, Hs)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    i32 = dict(dtype=torch.int32, device="cuda")
+    counts, offsets = torch.empty(experts, **i32), torch.empty(2 * experts + 2, **i32)
+    sorted_ids = torch.empty(2 * tokens, **i32)
+    out = torch.empty_like(x)
+    cap = hip_moe.capacity(tokens, experts)
+    s = torch.cuda.current_stream().cuda_stream
+    _abi.check(lib.parrot_experts_gate_up_grouping_blocks_bf16(
+        ptr(x), tokens, dim, experts, H, Hs, cap, ptr(tab.blocks), ptr(counts), ptr(offsets),
+        ptr(sorted_ids), ptr(gate_up), ptr(shared_gate_up), ptr(ws), nbytes, s), "gate/up")
+    _abi.check(lib.parrot_experts_down_sorted_bf16(
+        tokens, dim, experts, H, Hs, cap, ptr(counts), ptr(offsets), ptr(sorted_ids),
+        ptr(tab.weights), ptr(down), ptr(shared_down), ptr(ws), nbytes, s), "down")
+    _abi.check(lib.parrot_experts_combine_bf16(tokens, dim, H, Hs, None, ptr(out), ptr(ws),
+                                               nbytes, s), "combine")
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert torch.equal(counts.cpu(), g.counts.cpu())
+    assert torch.equal(offsets.cpu(), g.offsets.cpu())
+    assert torch.equal(sorted_ids.cpu(), _sorted_from_grouping(g, experts))

@@ -150,3 +150,18 @@ def test_route_top2_matches_route(tokens, experts, skewed):
     assert top2.grouping is None
     assert torch.equal(full.indices, top2.indices)
     assert torch.equal(full.weights, top2.weights)
+    if tokens >= 32768:
+        return  # the block table is written below the wide router's sizes
+    with torch.no_grad():
+        tab = hip_moe.route_top2(module, x, logit_bias=bias, blocks=True)
+    assert torch.equal(full.indices, tab.indices) and torch.equal(full.weights, tab.weights)
+    # The table from the indices: per 16 tokens the 32 ids in assignment
+    # order (255 for padding tokens), then the count of each expert.
+    ids = full.indices.reshape(-1).cpu().numpy()
+    n_blocks = (tokens + 15) // 16
+    padded = np.full(n_blocks * 32, 255, dtype=np.int64)
+    padded[:ids.size] = ids
+    rows = padded.reshape(n_blocks, 32)
+    counts = np.stack([(rows == e).sum(axis=1) for e in range(32)], axis=1)
+    want = np.concatenate([rows, counts], axis=1).astype(np.uint8)
+    assert np.array_equal(tab.blocks.cpu().numpy(), want)
