@@ -509,7 +509,7 @@ hipError_t launch_decode_moe(const uint16_t* x, const DecodeMix* mix, int tokens
   if (mixing)
     e = with_sources(m.n_sources, up_sw);
   else
-    up_sw(std::integral_constant<int, 0>{});
+    e = up_sw(std::integral_constant<int, 0>{});
   if (e == hipSuccess) e = hipGetLastError();
   if (e != hipSuccess) return e;
   decode_down_kernel<<<dim3(dim / 16, tokens), 256, 0, s>>>(
