@@ -29,6 +29,10 @@ __global__ __launch_bounds__(256) void combine_kernel(
   const float4 s = y_shared[i];
   const float4 a = y_routed[(2 * t) * quads_per_row + q];
   const float4 b = y_routed[(2 * t + 1) * quads_per_row + q];
+  // The addend's load goes out with the rows' (uniform branch), not after
+  // their sum.
+  const uint2 p = addend != nullptr ? addend[i] : make_uint2(0u, 0u);
+  asm volatile("" ::: "memory");
   float v0 = s.x + a.x + b.x;
   float v1 = s.y + a.y + b.y;
   float v2 = s.z + a.z + b.z;
@@ -37,7 +41,6 @@ __global__ __launch_bounds__(256) void combine_kernel(
   o.x = pack_bf16x2(v0, v1);
   o.y = pack_bf16x2(v2, v3);
   if (addend != nullptr) {
-    const uint2 p = addend[i];
     o.x = pack_bf16x2(lo_bf16(p.x) + lo_bf16(o.x), hi_bf16(p.x) + hi_bf16(o.x));
     o.y = pack_bf16x2(lo_bf16(p.y) + lo_bf16(o.y), hi_bf16(p.y) + hi_bf16(o.y));
   }

@@ -31,12 +31,22 @@ __global__ __launch_bounds__(64) void rms_norm_kernel(
   const uint2* xr = reinterpret_cast<const uint2*>(x + row * dim);
   const uint2* wr = reinterpret_cast<const uint2*>(w);
   uint2* yr = reinterpret_cast<uint2*>(out + row * dim);
-  uint2 v[MAXC];
-  float ss = 0.0f;
+  uint2 v[MAXC], g[MAXC];
+  // The row's chunks, then the weight's: the weight load is in flight during
+  // the reduction instead of a second round trip after it.
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
     const int i = lane + c * kWave;
     v[c] = i < chunks ? xr[i] : make_uint2(0u, 0u);
+  }
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int i = lane + c * kWave;
+    g[c] = i < chunks ? wr[i] : make_uint2(0u, 0u);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
     const float a = lo_bf16(v[c].x), b = hi_bf16(v[c].x);
     const float d = lo_bf16(v[c].y), e = hi_bf16(v[c].y);
     ss += a * a + b * b + d * d + e * e;
@@ -47,10 +57,11 @@ __global__ __launch_bounds__(64) void rms_norm_kernel(
   for (int c = 0; c < MAXC; ++c) {
     const int i = lane + c * kWave;
     if (i < chunks) {
-      const uint2 g = wr[i];
       uint2 o;
-      o.x = pack_bf16x2(lo_bf16(v[c].x) * r * lo_bf16(g.x), hi_bf16(v[c].x) * r * hi_bf16(g.x));
-      o.y = pack_bf16x2(lo_bf16(v[c].y) * r * lo_bf16(g.y), hi_bf16(v[c].y) * r * hi_bf16(g.y));
+      o.x = pack_bf16x2(lo_bf16(v[c].x) * r * lo_bf16(g[c].x),
+                        hi_bf16(v[c].x) * r * hi_bf16(g[c].x));
+      o.y = pack_bf16x2(lo_bf16(v[c].y) * r * lo_bf16(g[c].y),
+                        hi_bf16(v[c].y) * r * hi_bf16(g[c].y));
       yr[i] = o;
     }
   }
