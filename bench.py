@@ -6,8 +6,9 @@ Parrot model -- 16 layers, E=16 experts, top-2 + shared expert, Block
 AttnRes, 32768-vocab tied head -- random-init with seed 2, bf16, router
 statistics off, forward over batch 1 x 512 token ids drawn uniformly from
 [0, 32768) (synthetic data).  MoE, RMSNorm and depth mixing run on the HIP
-kernels (moe_backend="grouped_hip", depth_backend="hip"); attention, the
-embedding and the vocabulary head are PyTorch-ROCm.
+kernels (moe_backend="grouped_hip", depth_backend="hip"), and so do the
+attention blocks and their projections; the embedding gather and the
+vocabulary head GEMM are PyTorch-ROCm (hipBLASLt).
 
 A step is one full forward.  The timed loop replays the forward captured in
 a HIP graph (each replay recomputes everything from the static input ids);
@@ -66,6 +67,9 @@ def parse_args():
     p.add_argument("--summarize-pmc", nargs=2, metavar=("PASS_A_DIR", "PASS_B_DIR"),
                    help="(no GPU) turn the counter CSVs of the two --pmc passes over "
                         "--pmc-workload into profiles/counters_hot_path.json")
+    p.add_argument("--summarize-steps", metavar="TRACE_DIR",
+                   help="write the forward and decode kernel-trace summaries under profiles/ "
+                        "from a rocprofv3 --kernel-trace run of bench.py --skip-kernels")
     p.add_argument("--summarize-trace", metavar="TRACE_DIR",
                    help="(no GPU) per-kernel durations of a rocprofv3 --kernel-trace run of "
                         "bench.py into profiles/kernel_trace_bench.json")
@@ -869,6 +873,7 @@ def summarize_pmc(dir_a: str, dir_b: str) -> dict:
 
 
 TRACE_FILE = ROOT / "profiles" / "kernel_trace_bench.json"
+BENCH_FILE = ROOT / "profiles" / "bench_forward_bs1x512.json"
 
 
 def summarize_trace(directory: str) -> dict:
@@ -917,6 +922,116 @@ def summarize_trace(directory: str) -> dict:
     }
     TRACE_FILE.write_text(json.dumps(summary, indent=1) + "\n")
     return summary
+
+
+def _short_kernel(name: str) -> str:
+    """A kernel name without its argument list and namespaces."""
+    n = name[5:] if name.startswith("void ") else name
+    for ns in ("parrot::(anonymous namespace)::", "(anonymous namespace)::"):
+        n = n.replace(ns, "")
+    depth, cut = 0, len(n)
+    for i, ch in enumerate(n):  # the argument list: the first '(' outside <...>
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            cut = i
+            break
+    return n[:cut][:72]
+
+
+def _step_table(steps: list[list[dict]]) -> tuple[str, float, float, float]:
+    """Markdown table of per-kernel time over `steps` (lists of dispatches),
+    with the launches, kernel time and first-start-to-last-end per step."""
+    per: dict[tuple, list[int]] = {}
+    for st in steps:
+        for r in st:
+            per.setdefault((_short_kernel(r["name"]), r["gx"], r["gy"], r["wg"]), []).append(r["ns"])
+    n = len(steps)
+    busy = sum(r["ns"] for st in steps for r in st) / n / 1e3
+    span = sum(st[-1]["end"] - st[0]["start"] for st in steps) / n / 1e3
+    launches = sum(len(st) for st in steps) / n
+    lines = ["| kernel | grid x | grid y | wg | per step | mean us | median us | min us | "
+             "us per step | share % |", "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for (name, gx, gy, wg), v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        tot = sum(v) / n / 1e3
+        lines.append(f"| `{name}` | {gx} | {gy} | {wg} | {len(v) / n:g} | "
+                     f"{statistics.mean(v) / 1e3:.2f} | {statistics.median(v) / 1e3:.2f} | "
+                     f"{min(v) / 1e3:.2f} | {tot:.1f} | {100 * tot / busy:.1f} |")
+    return "\n".join(lines), launches, busy, span
+
+
+def summarize_steps(directory: str) -> str:
+    """Per-kernel time of the graph-replayed forwards and decode steps in a
+    rocprofv3 --kernel-trace run of `bench.py --skip-cpu-baseline
+    --skip-kernels`: profiles/forward_bs1x512_kernel_trace.md and
+    profiles/decode_graph_kernel_trace.md."""
+    import csv
+    rows = []
+    for path in sorted(Path(directory).rglob("*kernel_trace.csv")):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                rows.append({"id": int(r["Dispatch_Id"]), "name": r["Kernel_Name"],
+                             "start": int(r["Start_Timestamp"]), "end": int(r["End_Timestamp"]),
+                             "ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"]),
+                             "gx": int(r["Grid_Size_X"]), "gy": int(r["Grid_Size_Y"]),
+                             "wg": int(r["Workgroup_Size_X"])})
+    rows.sort(key=lambda r: r["id"])
+    command = ("rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/prof_steps -o steps -- "
+               "python3 -u bench.py --skip-cpu-baseline --skip-kernels\n"
+               "python3 bench.py --summarize-steps gpurun_out/prof_steps")
+    bench = load_json(BENCH_FILE) or {}
+    # Forwards: from one bs1 x 512 embedding gather to the next; the timed
+    # graph replays are the last `steps` of the most common launch count.
+    starts = [i for i, r in enumerate(rows)
+              if "gather" in r["name"] and r["gx"] == TOKENS * 128]
+    segs = [rows[a:b] for a, b in zip(starts, starts[1:] + [len(rows)])]
+    counts = [len(sg) for sg in segs]
+    mode = max(set(counts), key=counts.count) if counts else 0
+    fwd = [sg for sg in segs if len(sg) == mode][-bench.get("steps", 20):]
+    table, launches, busy, span = _step_table(fwd) if fwd else ("(no forwards)", 0, 0, 0)
+    ms = bench.get("ms_per_step")
+    (ROOT / "profiles" / "forward_bs1x512_kernel_trace.md").write_text(
+        "# Kernel trace: Parrot bf16 forward, batch 1 x 512 (HIP-graph replay)\n\n"
+        "Command (GPU box, repo root):\n\n```\n" + command + "\n```\n\n"
+        f"The last {len(fwd)} forwards of the trace (the timed graph replays), split at each "
+        f"forward's embedding gather.  Per forward: {launches:g} launches, {busy:.1f} us of "
+        f"kernel time, {span:.1f} us from the first launch's start to the last one's end"
+        + (f" (the committed bench line: {ms * 1e3:.1f} us per step)" if ms else "")
+        + ".  Durations in us (End - Start), under the profiler.\n\n" + table + "\n")
+    # Decode steps: each ends with the vocabulary argmax reduce; the batch is
+    # the decode attention kernel's grid y; the last 16 steps of each batch
+    # size are the graph replays.
+    steps, cur = [], []
+    for r in rows:
+        cur.append(r)
+        if "vocab_argmax_reduce" in r["name"]:
+            steps.append(cur)
+            cur = []
+    by_batch: dict[int, list] = {}
+    for st in steps:
+        att = [r for r in st if "decode_attention_kernel" in r["name"]]
+        if att:
+            by_batch.setdefault(att[0]["gy"], []).append(st)
+    dec = bench.get("decode", {})
+    parts = ["# Kernel trace: cached decode steps (HIP-graph replay), BASELINE config 5\n\n"
+             "Command (GPU box, repo root):\n\n```\n" + command + "\n```\n\n"
+             "bench.py's decode measurement: prefill 128 tokens, then greedy steps, eager and "
+             "then replayed from a captured `DecodeGraph`.  Steps are split after each step's "
+             "last launch (the vocabulary argmax reduce) and grouped by batch (the decode "
+             "attention kernel's grid y); the last 16 steps of each batch size (graph "
+             "replays) are summarised.  Durations under the profiler.\n"]
+    for b in sorted(by_batch):
+        sts = by_batch[b][-16:]
+        table, launches, busy, span = _step_table(sts)
+        ref = dec.get(f"b{b}", {}).get("graph_decode_ms_per_step")
+        parts.append(f"\n## batch {b}\n\nPer step: {launches:g} launches, {busy:.1f} us of "
+                     f"kernel time, {span:.1f} us first start to last end"
+                     + (f"; committed bench line: {ref * 1e3:.0f} us per step" if ref else "")
+                     + ".\n\n" + table + "\n")
+    (ROOT / "profiles" / "decode_graph_kernel_trace.md").write_text("".join(parts))
+    return f"forwards {len(fwd)} x {mode} launches; decode batches {sorted(by_batch)}"
 
 
 def load_json(path: Path) -> dict | None:
@@ -971,6 +1086,9 @@ def main():
         return
     if args.summarize_pmc:
         print(json.dumps(summarize_pmc(*args.summarize_pmc))[:2000])
+        return
+    if args.summarize_steps:
+        print(summarize_steps(args.summarize_steps))
         return
     if args.summarize_trace:
         print(json.dumps(summarize_trace(args.summarize_trace))[:2000])

@@ -43,6 +43,9 @@ template <int NCH, int RB>
 __global__ __launch_bounds__(256) void vocab_argmax_partials_kernel(
     const uint16_t* __restrict__ h, int rows, int dim, const uint16_t* __restrict__ w, int vocab,
     float* __restrict__ part_v, int32_t* __restrict__ part_i) {
+  // The kernel arguments in one batch of scalar loads before any use.
+  asm volatile("" ::"s"(h), "s"(rows), "s"(dim), "s"(w), "s"(vocab), "s"(part_v), "s"(part_i));
+  __builtin_amdgcn_sched_barrier(0);
   extern __shared__ __attribute__((aligned(16))) uint16_t hs[];  // [rows][dim]
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
