@@ -105,6 +105,99 @@ __global__ __launch_bounds__(256) void vocab_argmax_partials_kernel(
   }
 }
 
+// Two or more rows of h: the dots are a GEMM [vocab x dim] . [dim x rows]
+// on v_mfma_f32_16x16x32_bf16, so the VALU work per head byte no longer grows
+// with the rows (the wavefront-sum kernel above runs 9.5 / 12 / 18 / 30 us
+// at 1 / 2 / 4 / 8 rows).  Wavefront w of workgroup g takes vocabulary rows
+// v0 = 64 g + 16 w .. v0 + 15 as the A operand (lane l: row l % 16) and the
+// rows of h, staged in LDS with a padded stride, as B (lane l: h row l % 16,
+// zero past `rows`).  The k order pairs the steps: steps 2j and 2j + 1 give
+// lane group c = l / 16 the elements 64 j + 16 c .. + 7 and + 8 .. + 15, so
+// each lane reads 32 contiguous bytes of its vocabulary row per pair and a
+// pair of load instructions covers 128 contiguous bytes of every row.  The
+// C fragment gives lane l the logits of h row l % 16 and vocabulary rows
+// v0 + 4 (l / 16) + r; the best (value, lower index) of each h row is taken
+// over r and then over the four lane groups, and lane n < rows writes h row
+// n's partial for this wavefront.  The fp32 sums are MFMA sums over the
+// same bf16 products, in another order than the wavefront sums.
+constexpr int kVocabMfmaRows = 64;  // vocabulary rows per workgroup
+constexpr int kVocabMfmaSteps = 24;  // k steps of head loads in flight per lane
+
+__global__ __launch_bounds__(256) void vocab_argmax_mfma_kernel(
+    const uint16_t* __restrict__ h, int rows, int dim, const uint16_t* __restrict__ w, int vocab,
+    float* __restrict__ part_v, int32_t* __restrict__ part_i) {
+  // The kernel arguments in one batch of scalar loads before any use.
+  asm volatile("" ::"s"(h), "s"(rows), "s"(dim), "s"(w), "s"(vocab), "s"(part_v), "s"(part_i));
+  __builtin_amdgcn_sched_barrier(0);
+  extern __shared__ __attribute__((aligned(16))) uint16_t hs[];  // [rows][dim + 8]
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int c = lane >> 4;
+  const int steps = dim / 32;  // even: dim % 64 == 0
+  const int hstride = dim + 8;
+  const int v0 = blockIdx.x * kVocabMfmaRows + wave * 16;
+  const uint16_t* wrow =
+      w + static_cast<int64_t>(min(v0 + (lane & 15), vocab - 1)) * dim + 16 * c;
+  // Element offset (within a row) of this lane's 8 values at k step s.
+  auto koff = [&](int s) { return 64 * (s >> 1) + 8 * (s & 1); };
+  const int n = lane & 15;  // this lane's h row (B column)
+  const bool live = n < rows;
+  const uint16_t* hrow = hs + (live ? n : 0) * hstride + 16 * c;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < steps; s0 += kVocabMfmaSteps) {
+    bf16x8 a[kVocabMfmaSteps];
+#pragma unroll
+    for (int i = 0; i < kVocabMfmaSteps; ++i)
+      a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                            wrow + koff(min(s0 + i, steps - 1))));
+    if (s0 == 0) {
+      // h into LDS behind the first head loads (rows x dim / 8 chunks).
+      const int chunks = dim / 8;
+      for (int i = tid; i < rows * chunks; i += 256) {
+        const int r = i / chunks;
+        *reinterpret_cast<uint4*>(hs + r * hstride + (i - r * chunks) * 8) =
+            reinterpret_cast<const uint4*>(h)[i];
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < kVocabMfmaSteps; ++i) {
+      const int st = s0 + i;
+      if (st < steps) {
+        const uint4 hv = live ? *reinterpret_cast<const uint4*>(hrow + koff(st))
+                              : make_uint4(0u, 0u, 0u, 0u);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], __builtin_bit_cast(bf16x8, hv),
+                                                      acc, 0, 0, 0);
+      }
+    }
+  }
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int v = v0 + 4 * c + r;
+    if (v < vocab && better(acc[r], v, bv, bi)) {
+      bv = acc[r];
+      bi = v;
+    }
+  }
+#pragma unroll
+  for (int m = 16; m < kWave; m <<= 1) {
+    const float ov = __shfl_xor(bv, m);
+    const int oi = __shfl_xor(bi, m);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane < rows) {
+    const int64_t groups = static_cast<int64_t>(gridDim.x) * 4;
+    part_v[lane * groups + blockIdx.x * 4 + wave] = bv;
+    part_i[lane * groups + blockIdx.x * 4 + wave] = bi;
+  }
+}
+
 // One workgroup per row of h.  The row's partials are read as float4 / int4,
 // every load of a lane issued before the first compare (a loop with a load,
 // a wait and a compare per partial took ~11 us for 8192 partials), then
@@ -186,6 +279,16 @@ hipError_t launch_vocab_argmax(const uint16_t* h, int rows, int dim, const uint1
                                float* part_v, int32_t* part_i, int64_t* out, int32_t* advance,
                                hipStream_t s) {
   if (rows == 0) return hipSuccess;
+  // Two or more rows: the MFMA kernel (h staged in at most 64 KB of LDS).
+  const size_t mfma_lds = static_cast<size_t>(rows) * (dim + 8) * sizeof(uint16_t);
+  if (rows >= 2 && dim % 64 == 0 && mfma_lds <= 65536) {
+    const int blocks = (vocab + kVocabMfmaRows - 1) / kVocabMfmaRows;
+    vocab_argmax_mfma_kernel<<<blocks, 256, mfma_lds, s>>>(h, rows, dim, w, vocab, part_v,
+                                                           part_i);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    vocab_argmax_reduce_kernel<<<rows, 256, 0, s>>>(part_v, part_i, 4 * blocks, out, advance);
+    return hipGetLastError();
+  }
   const int blocks = (vocab + kVocabRowsPerGroup - 1) / kVocabRowsPerGroup;
   const size_t lds = static_cast<size_t>(rows) * dim * sizeof(uint16_t);
   const int nch = (dim / 8 + 63) / 64;
