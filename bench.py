@@ -323,6 +323,31 @@ def attained_peaks() -> dict:
     res["mfma_bf16_tflops"] = max(res["mfma_32x32x16_tflops"], res["mfma_16x16x32_tflops"])
     res["copy_gbps"] = max(res["copy_kernel_gbps"], res["torch_copy_gbps"])
     res["vendor"] = {"mfma_bf16_tflops": PEAK_BF16_TFLOPS, "hbm_gbps": PEAK_HBM_GBPS}
+    # Latency floors of one launch in a dependent back-to-back chain, the
+    # regime of every model-size kernel here: a 16-byte copy (one
+    # workgroup), and copies of 1 / 8 / 24 MiB warm (the same buffer each
+    # time: L2 and memory-side cache hits) and cold (rotating over 512 MiB of
+    # buffers, twice the memory-side cache, so every read comes from HBM).
+    floors = {"launch_16B_us": round(min(event_time_us(
+        lambda: lib.parrot_peak_copy(src.data_ptr(), dst.data_ptr(), 16, 1, s.cuda_stream),
+        200, s) for _ in range(3)), 2)}
+    for mib in (1, 8, 24):
+        nb = mib << 20
+        blocks = max(64, min(8192, nb // 4096))
+        floors[f"copy_{mib}MiB_warm_us"] = round(min(event_time_us(
+            lambda: lib.parrot_peak_copy(src.data_ptr(), dst.data_ptr(), nb, blocks,
+                                         s.cuda_stream), 100, s) for _ in range(3)), 2)
+        slots = (512 << 20) // nb
+        turn = [0]
+
+        def cold():
+            o = (turn[0] % slots) * nb
+            turn[0] += 1
+            return lib.parrot_peak_copy(src.data_ptr() + o, dst.data_ptr() + o, nb, blocks,
+                                        s.cuda_stream)
+        floors[f"copy_{mib}MiB_cold_us"] = round(min(event_time_us(cold, slots, s)
+                                                     for _ in range(3)), 2)
+    res["latency_floors"] = floors
     del src, dst, out
     torch.cuda.empty_cache()
     return res
