@@ -108,12 +108,22 @@ class RouteResult:
     probabilities: Tensor | None
     weights: Tensor
     indices: Tensor
-    grouping: Grouping
+    grouping: Grouping | None
     logits: Tensor | None = None
     # The route block table (route_top2(..., blocks=True)): uint8
     # [ceil(T / 16), 64], what the gate/up launch groups from past the sizes
     # it groups from the indices.
     blocks: Tensor | None = None
+
+    def __iter__(self):
+        """Unpacks as metal_route's 5-tuple (parrot/metal_moe.py:58-81):
+        ``probabilities, weights, indices, positions, counts =
+        hip_moe.route(module, flat, collect_stats)``, the call site of
+        parrot/model.py:515-519.  Without a grouping (route_top2) positions
+        and counts are None."""
+        g = self.grouping
+        return iter((self.probabilities, self.weights, self.indices,
+                     None if g is None else g.positions, None if g is None else g.counts))
 
 
 def _alloc_grouping(tokens: int, experts: int, cap: int, device) -> Grouping:

@@ -165,3 +165,20 @@ def test_route_top2_matches_route(tokens, experts, skewed):
     counts = np.stack([(rows == e).sum(axis=1) for e in range(32)], axis=1)
     want = np.concatenate([rows, counts], axis=1).astype(np.uint8)
     assert np.array_equal(tab.blocks.cpu().numpy(), want)
+
+
+def test_route_unpacks_as_metal_route():
+    """route() unpacks as metal_route's 5-tuple (parrot/metal_moe.py:58-81),
+    so the reference's call site (parrot/model.py:515-519) reads it as is."""
+    from parrot import hip_moe
+    _say("route unpacks as metal_route")
+    module = moe_module(16, seed=1)
+    x = inputs(300, seed=2)
+    with torch.no_grad():
+        res = hip_moe.route(module, x, collect_stats=True)
+        probabilities, weights, indices, positions, counts = res
+        plain = hip_moe.route(module, x, collect_stats=False)
+    assert probabilities is res.probabilities and probabilities.shape == (300, 16)
+    assert weights is res.weights and indices is res.indices
+    assert positions is res.grouping.positions and counts is res.grouping.counts
+    assert int(counts.sum()) == 600 and tuple(plain)[0] is None

@@ -159,3 +159,18 @@ def test_scratch_retention_is_bounded():
     used = owner.__dict__["_ws"]
     hip_moe._scratch(owner, "_ws", 10 * used.numel(), torch.device("cpu"))
     assert owner.__dict__["_hip_captured_scratch"] == [used]
+
+
+def test_route_result_unpacks_as_metal_route():
+    """RouteResult unpacks in metal_route's order (parrot/metal_moe.py:58-81):
+    probabilities, weights, indices, positions, counts; a top-2-only result
+    has no positions or counts."""
+    import torch
+
+    from parrot import hip_moe
+    t = [torch.zeros(1) + i for i in range(6)]
+    g = hip_moe.Grouping(positions=t[3], counts=t[4], offsets=t[5], perm=t[5], overflow=t[5],
+                         capacity=8)
+    out = tuple(hip_moe.RouteResult(t[0], t[1], t[2], g))
+    assert all(a is b for a, b in zip(out, t[:5])) and len(out) == 5
+    assert tuple(hip_moe.RouteResult(None, t[1], t[2], None)) == (None, t[1], t[2], None, None)
