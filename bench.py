@@ -987,7 +987,7 @@ def _step_table(steps: list[list[dict]]) -> tuple[str, float, float, float]:
     return "\n".join(lines), launches, busy, span
 
 
-def summarize_steps(directory: str) -> str:
+def summarize_steps(directory: str, out_dir: Path | None = None) -> str:
     """Per-kernel time of the graph-replayed forwards and decode steps in a
     rocprofv3 --kernel-trace run of `bench.py --skip-cpu-baseline
     --skip-kernels`: profiles/forward_bs1x512_kernel_trace.md and
@@ -1007,6 +1007,7 @@ def summarize_steps(directory: str) -> str:
                "python3 -u bench.py --skip-cpu-baseline --skip-kernels\n"
                "python3 bench.py --summarize-steps gpurun_out/prof_steps")
     bench = load_json(BENCH_FILE) or {}
+    out_dir = ROOT / "profiles" if out_dir is None else Path(out_dir)
     # Forwards: from one bs1 x 512 embedding gather to the next; the timed
     # graph replays are the last `steps` of the most common launch count.
     starts = [i for i, r in enumerate(rows)
@@ -1017,7 +1018,7 @@ def summarize_steps(directory: str) -> str:
     fwd = [sg for sg in segs if len(sg) == mode][-bench.get("steps", 20):]
     table, launches, busy, span = _step_table(fwd) if fwd else ("(no forwards)", 0, 0, 0)
     ms = bench.get("ms_per_step")
-    (ROOT / "profiles" / "forward_bs1x512_kernel_trace.md").write_text(
+    (out_dir / "forward_bs1x512_kernel_trace.md").write_text(
         "# Kernel trace: Parrot bf16 forward, batch 1 x 512 (HIP-graph replay)\n\n"
         "Command (GPU box, repo root):\n\n```\n" + command + "\n```\n\n"
         f"The last {len(fwd)} forwards of the trace (the timed graph replays), split at each "
@@ -1055,7 +1056,7 @@ def summarize_steps(directory: str) -> str:
                      f"kernel time, {span:.1f} us first start to last end"
                      + (f"; committed bench line: {ref * 1e3:.0f} us per step" if ref else "")
                      + ".\n\n" + table + "\n")
-    (ROOT / "profiles" / "decode_graph_kernel_trace.md").write_text("".join(parts))
+    (out_dir / "decode_graph_kernel_trace.md").write_text("".join(parts))
     return f"forwards {len(fwd)} x {mode} launches; decode batches {sorted(by_batch)}"
 
 
