@@ -447,7 +447,7 @@ def cpu_baseline(model, ids, seconds: float) -> dict:
         oracle.forward(cpu_ids)  # warmup
         samples = []
         t_start = time.perf_counter()
-        while len(samples) < 3 or (time.perf_counter() - t_start < seconds and len(samples) < 20):
+        while len(samples) < 3 or (time.perf_counter() - t_start < seconds and len(samples) < 200):
             t0 = time.perf_counter()
             oracle.forward(cpu_ids)
             samples.append(time.perf_counter() - t0)
