@@ -64,8 +64,8 @@ def parse_args():
     p.add_argument("--pmc-workload", action="store_true",
                    help="only launch the counter workload: every hot-path kernel at C2, C3, "
                         "the C4 layer and T=65536, segments separated by a 16-byte marker copy")
-    p.add_argument("--summarize-pmc", nargs=2, metavar=("PASS_A_DIR", "PASS_B_DIR"),
-                   help="(no GPU) turn the counter CSVs of the two --pmc passes over "
+    p.add_argument("--summarize-pmc", nargs="+", metavar="PASS_DIR",
+                   help="(no GPU) turn the counter CSVs of the --pmc passes (A, B, C) over "
                         "--pmc-workload into profiles/counters_hot_path.json")
     p.add_argument("--summarize-steps", metavar="TRACE_DIR",
                    help="write the forward and decode kernel-trace summaries under profiles/ "
@@ -719,10 +719,13 @@ PMC_REPEATS = 5
 PMC_PASSES = {
     "A": "FETCH_SIZE SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE",
     "B": "WRITE_SIZE",
+    # L2 -> CU reads: requests from the vector L1s to the L2s, and L2 hits
+    # and misses (the weights' re-reads by row tiles land here, not in HBM).
+    "C": "TCP_TCC_READ_REQ_sum TCC_HIT_sum TCC_MISS_sum",
 }
 PMC_COMMANDS = [f"rocprofv3 --pmc {c} -f csv -d gpurun_out/pmc_{k} -o pmc "
                 f"-- python3 bench.py --pmc-workload" for k, c in PMC_PASSES.items()] + [
-    "python3 bench.py --summarize-pmc gpurun_out/pmc_A gpurun_out/pmc_B"]
+    "python3 bench.py --summarize-pmc gpurun_out/pmc_A gpurun_out/pmc_B gpurun_out/pmc_C"]
 MARKER_KERNEL = ("parrot", "copy_kernel")  # a 16-byte parrot_peak_copy opens every segment
 
 
@@ -840,12 +843,16 @@ def _segments(rows: list[dict]) -> list[list[dict]]:
     return segs
 
 
-def summarize_pmc(dir_a: str, dir_b: str) -> dict:
+def summarize_pmc(dir_a: str, dir_b: str, dir_c: str | None = None) -> dict:
     manifest = json.loads(Path(PMC_MANIFEST).read_text())
     seg_a, seg_b = _segments(_dispatches(dir_a)), _segments(_dispatches(dir_b))
-    if len(seg_a) < len(manifest) or len(seg_b) < len(manifest):
+    seg_c = _segments(_dispatches(dir_c)) if dir_c else None
+    if len(seg_a) < len(manifest) or len(seg_b) < len(manifest) or (
+            seg_c is not None and len(seg_c) < len(manifest)):
         raise SystemExit(f"found {len(seg_a)} / {len(seg_b)} segments for {len(manifest)} labels")
     seg_a, seg_b = seg_a[-len(manifest):], seg_b[-len(manifest):]
+    if seg_c is not None:
+        seg_c = seg_c[-len(manifest):]
 
     def per_launch(seg, counter):
         return sum(r["counters"].get(counter, 0.0) for r in seg) / PMC_REPEATS
@@ -859,8 +866,11 @@ def summarize_pmc(dir_a: str, dir_b: str) -> dict:
     flop_per_mop = loop_flops / per_launch(loop, "SQ_INSTS_VALU_MFMA_MOPS_BF16")
     loop_busy = per_launch(loop, "SQ_VALU_MFMA_BUSY_CYCLES") / per_launch(loop, "GRBM_GUI_ACTIVE")
     loop_ns = sum(r["ns"] for r in loop) / PMC_REPEATS
+    # L2 -> CU: bytes per TCP -> TCC read request, from the calibration read.
+    req_bytes = (calib / per_launch(seg_c[0], "TCP_TCC_READ_REQ_sum")
+                 if seg_c is not None else None)
     entries = {}
-    for m, a, b in list(zip(manifest, seg_a, seg_b))[2:]:
+    for i, (m, a, b) in enumerate(list(zip(manifest, seg_a, seg_b))[2:], start=2):
         ns = sum(r["ns"] for r in a) / PMC_REPEATS
         fetch = per_launch(a, "FETCH_SIZE") * fetch_scale * 1024
         write = per_launch(b, "WRITE_SIZE") * write_scale * 1024
@@ -879,13 +889,23 @@ def summarize_pmc(dir_a: str, dir_b: str) -> dict:
             e["mfma_tflops"] = round(mops * flop_per_mop / ns / 1e3, 1)
             busy = per_launch(a, "SQ_VALU_MFMA_BUSY_CYCLES") / per_launch(a, "GRBM_GUI_ACTIVE")
             e["mfma_busy_vs_loop"] = round(busy / loop_busy, 4)
+        if seg_c is not None:
+            c = seg_c[i]
+            l2_read = per_launch(c, "TCP_TCC_READ_REQ_sum") * req_bytes
+            hit, miss = per_launch(c, "TCC_HIT_sum"), per_launch(c, "TCC_MISS_sum")
+            e["l2_to_cu_read_bytes"] = int(l2_read)
+            if m["bytes"]:
+                e["l2_reads_over_algorithmic"] = round(l2_read / m["bytes"], 3)
+            e["l2_hit_rate"] = round(hit / (hit + miss), 4) if hit + miss else None
         entries[m["label"]] = e
     summary = {
-        "what": "per-launch HBM bytes (FETCH_SIZE, WRITE_SIZE) and MFMA counters of every "
-                "hot-path kernel, median workload of PMC_REPEATS launches per segment",
+        "what": "per-launch HBM bytes (FETCH_SIZE, WRITE_SIZE), MFMA counters and L2 -> CU "
+                "read bytes (TCP_TCC_READ_REQ) with the L2 hit rate of every hot-path kernel, "
+                "median workload of PMC_REPEATS launches per segment",
         "calibration": {
             "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
             "bytes_each_way": calib, "kernel": "torch.neg bf16, %d elements" % CALIBRATION_ELEMS,
+            "bytes_per_tcp_tcc_read_req": round(req_bytes, 2) if req_bytes else None,
             "flop_per_mfma_op": round(flop_per_mop, 3),
             "mfma_loop": {"flops": loop_flops, "us_under_pmc": round(loop_ns / 1e3, 2),
                           "tflops": round(loop_flops / loop_ns / 1e3, 1),
