@@ -192,17 +192,31 @@ class StageBench:
             p(g.perm), p(g.overflow), p(self.routed.weights), p(self.packed[1]),
             p(self.packed[3]), p(self.ews), self.ews_bytes, self.s)
 
-    def gate_up_grouping(self):
+    def gate_up_grouping(self, weights=None):
+        """``weights``: (routed gate/up, shared gate/up) packed copies to read
+        in place of the layer's own (the cold-cache rotation)."""
         p = self.ptr
+        gu, sh = (self.packed[0], self.packed[2]) if weights is None else weights
         if self.blocks is not None:
             return self.lib.parrot_experts_gate_up_grouping_blocks_bf16(
                 p(self.x), self.T, self.dim, self.E, self.H, self.Hs, self.C, p(self.blocks),
-                p(self.g_counts), p(self.g_offsets), p(self.g_sorted), p(self.packed[0]),
-                p(self.packed[2]), p(self.ews), self.ews_bytes, self.s)
+                p(self.g_counts), p(self.g_offsets), p(self.g_sorted), p(gu), p(sh),
+                p(self.ews), self.ews_bytes, self.s)
         return self.lib.parrot_experts_gate_up_grouping_bf16(
             p(self.x), self.T, self.dim, self.E, self.H, self.Hs, self.C, p(self.ids),
-            p(self.g_counts), p(self.g_offsets), p(self.g_sorted), p(self.packed[0]),
-            p(self.packed[2]), p(self.ews), self.ews_bytes, self.s)
+            p(self.g_counts), p(self.g_offsets), p(self.g_sorted), p(gu), p(sh),
+            p(self.ews), self.ews_bytes, self.s)
+
+    def with_x(self, x, stage):
+        """A call of ``stage`` (a method name) reading token rows ``x`` (a copy
+        of the layer's input) instead of the layer's own."""
+        def call():
+            own, self.x = self.x, x
+            try:
+                return getattr(self, stage)()
+            finally:
+                self.x = own
+        return call
 
     def down_sorted(self):
         p = self.ptr
@@ -270,15 +284,55 @@ def stage_time_us(fn, iters: int, stream, reps: int = 3) -> float:
     return min(event_time_us(fn, iters, stream) for _ in range(reps))
 
 
+# MI355X's memory-side cache (Infinity Cache): a loop that relaunches a kernel
+# over the same buffers finds a working set below this size there, not in HBM.
+MALL_BYTES = 256 << 20
+COLD_ROTATION_BYTES = 512 << 20
+
+
+def rotation(calls: list):
+    """One callable that takes `calls` in turn: each launch reads its own
+    copy of the inputs, last read len(calls) - 1 launches earlier."""
+    turn = [0]
+
+    def call():
+        fn = calls[turn[0] % len(calls)]
+        turn[0] += 1
+        return fn()
+    return call
+
+
+def copies_for_cold(nbytes: int) -> int:
+    """Input copies a rotation needs so that at least COLD_ROTATION_BYTES
+    (twice the memory-side cache) are read between two reads of one copy."""
+    return max(2, -(-COLD_ROTATION_BYTES // max(1, nbytes)))
+
+
+def cold_time_us(calls: list, stream, laps: int = 2, reps: int = 3) -> float:
+    """Average launch duration over a rotation of input copies (HIP events,
+    best of `reps` loops of `laps` passes): every launch finds its inputs
+    evicted from L2 and the memory-side cache, as a kernel inside the
+    forward finds its layer's weights."""
+    fn = rotation(calls)
+    return min(event_time_us(fn, laps * len(calls), stream) for _ in range(reps))
+
+
 # Attained peaks of this GPU (attained_peaks), once measured: every entry then
 # also states its fraction of what the copy / MFMA-loop kernels reach.
 ATTAINED: dict = {}
 
 
-def entry(us: float, nbytes: int, flops: int | None = None) -> dict:
+def entry(us: float, nbytes: int, flops: int | None = None, cold: bool = False) -> dict:
+    """A kernel-table entry.  ``mall_resident``: the loop relaunched the
+    kernel over the same buffers and they fit the memory-side cache, so the
+    time is a warm one (reads served from that cache, not HBM); entries timed
+    over a rotation of input copies (``cold``) read from HBM."""
     gbps = nbytes / (us * 1e-6) / 1e9
     out = {"us": round(us, 3), "bytes": int(nbytes), "gbps": round(gbps, 1),
-           "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4)}
+           "hbm_frac": round(gbps / PEAK_HBM_GBPS, 4),
+           "mall_resident": (not cold) and nbytes < MALL_BYTES}
+    if cold:
+        out["cold"] = True
     if ATTAINED.get("copy_gbps"):
         out["hbm_frac_attained"] = round(gbps / ATTAINED["copy_gbps"], 4)
     if flops is not None:
@@ -377,14 +431,27 @@ def layer_kernels(moe, x, iters, logit_bias=None, mark_roofline=False
     }
     if sb.in_kernel:
         # gate/up grouping first: down_sorted reads the grouping it writes.
+        gu_bytes = sb.bytes_gate_up() + sb.bytes_grouping()
         if mark_roofline:
+            # The roofline loop, cold: the launches rotate over copies of the
+            # packed gate/up weights (>= 512 MiB read between two reads of a
+            # copy), as the forward's launch finds its layer's weights in
+            # HBM.  One timed loop between two marker copies: the kernel
+            # trace summary takes exactly the dispatches after the first.
+            w_bytes = (sb.packed[0].numel() * sb.packed[0].element_size() +
+                       sb.packed[2].numel() * sb.packed[2].element_size())
+            weights = [(sb.packed[0].clone(), sb.packed[2].clone())
+                       for _ in range(copies_for_cold(w_bytes))]
+            calls = [lambda w=w: sb.gate_up_grouping(w) for w in weights]
             trace_marker(sb)
-        # The roofline loop is one timed loop: the kernel trace summary takes
-        # exactly the dispatches after the marker.
-        timer = event_time_us if mark_roofline else stage_time_us
-        res["gate_up_grouping"] = entry(timer(sb.gate_up_grouping, iters, sb.stream),
-                                        sb.bytes_gate_up() + sb.bytes_grouping(),
-                                        sb.flops_gate_up())
+            res["gate_up_grouping_cold"] = entry(
+                event_time_us(rotation(calls), 4 * len(calls), sb.stream), gu_bytes,
+                sb.flops_gate_up(), cold=True)
+            res["gate_up_grouping_cold"]["weight_copies"] = len(calls)
+            trace_marker(sb)
+            del calls, weights
+        res["gate_up_grouping"] = entry(stage_time_us(sb.gate_up_grouping, iters, sb.stream),
+                                        gu_bytes, sb.flops_gate_up())
         res["down_sorted"] = entry(stage_time_us(sb.down_sorted, iters, sb.stream),
                                    sb.bytes_down() + (3 * sb.E + 2) * 4, sb.flops_down())
         res["route_top2"] = entry(stage_time_us(sb.route_top2, iters, sb.stream),
@@ -472,6 +539,7 @@ def cpu_baseline(model, ids, seconds: float) -> dict:
 # ---------------------------------------------------------------------------
 
 SWEEP_TOKENS = (512, 4096, 16384, 65536)
+COLD_SWEEP_TOKENS = 16384  # from here the sweep also times the bandwidth kernels cold
 
 
 def sweep_kernels(moe, iters: int) -> dict:
@@ -502,11 +570,32 @@ def sweep_kernels(moe, iters: int) -> dict:
         srcs = [torch.randn(T, d, device=dev, generator=gen).bfloat16() for _ in range(9)]
         arr = (ctypes.c_void_p * 9)(*[t.data_ptr() for t in srcs])
         q = torch.randn(d, device=dev, generator=gen).bfloat16()
-        res["depth_mix_norm_s9"] = entry(stage_time_us(
-            lambda: lib.parrot_depth_mix_bf16(ctypes.cast(arr, ctypes.c_void_p), 9, ptr(q),
-                                              ptr(w), 1e-6, ptr(w), 1e-6, T, d, None, ptr(y),
-                                              s.cuda_stream), n, s),
-            9 * T * d * 2 + 3 * d * 2 + T * d * 2)
+
+        def mix(a):
+            return lambda: lib.parrot_depth_mix_bf16(ctypes.cast(a, ctypes.c_void_p), 9, ptr(q),
+                                                     ptr(w), 1e-6, ptr(w), 1e-6, T, d, None,
+                                                     ptr(y), s.cuda_stream)
+        mix_bytes = 9 * T * d * 2 + 3 * d * 2 + T * d * 2
+        res["depth_mix_norm_s9"] = entry(stage_time_us(mix(arr), n, s), mix_bytes)
+        if T >= COLD_SWEEP_TOKENS:
+            # Cold: every launch reads its own copy of the inputs (rotations
+            # over >= 512 MiB), so the bandwidth kernels' fractions are HBM's.
+            xs = [x.clone() for _ in range(copies_for_cold(T * d * 2))]
+            res["route_group_cold"] = entry(cold_time_us(
+                [sb.with_x(xk, "route") for xk in xs], s), sb.bytes_route(), cold=True)
+            res["route_top2_cold"] = entry(cold_time_us(
+                [sb.with_x(xk, "route_top2") for xk in xs], s),
+                T * d * 2 + sb.E * d * 2 + T * 2 * (8 + 4), cold=True)
+            res["rms_norm_cold"] = entry(cold_time_us(
+                [lambda xk=xk: lib.parrot_rms_norm_bf16(ptr(xk), ptr(w), ptr(y), T, d, 1e-6,
+                                                        s.cuda_stream) for xk in xs], s),
+                2 * T * d * 2 + d * 2, cold=True)
+            del xs
+            sets = [[t.clone() for t in srcs] for _ in range(copies_for_cold(9 * T * d * 2) - 1)]
+            arrs = [arr] + [(ctypes.c_void_p * 9)(*[t.data_ptr() for t in st]) for st in sets]
+            res["depth_mix_norm_s9_cold"] = entry(cold_time_us([mix(a) for a in arrs], s),
+                                                  mix_bytes, cold=True)
+            del sets, arrs
         out[f"T{T}"] = res
         del sb, srcs, x, y
         torch.cuda.empty_cache()
@@ -1220,14 +1309,18 @@ def main():
         if not args.skip_sweep:
             log("token sweep")
             kernels["sweep_E16"] = sweep_kernels(moe0, max(20, args.kernel_iters // 4))
-        # The forward's gate/up form at C4: grouping in-kernel.
-        gu = c4["gate_up_grouping"]
+        # The forward's gate/up form at C4: grouping in-kernel, timed cold
+        # (weights from HBM, as inside the forward); the warm loop beside it.
+        gu, warm = c4["gate_up_grouping_cold"], c4["gate_up_grouping"]
         traffic = load_traffic()
         roofline = {"kernel": f"{TRAFFIC_KERNEL} (experts gate_up + SwiGLU, grouping the "
-                              "top-2 ids in-kernel), C4 in-model shape T=512 E=16",
+                              "top-2 ids in-kernel), C4 in-model shape T=512 E=16, cold: "
+                              f"launches rotate over {gu['weight_copies']} copies of the "
+                              "packed weights",
                     "bound": "hbm", "achieved": gu["gbps"], "peak": PEAK_HBM_GBPS,
                     "unit": "GB/s", "frac": gu["hbm_frac"], "traffic": traffic,
                     "algorithmic_bytes": gu["bytes"], "event_us": gu["us"],
+                    "warm_event_us": warm["us"], "warm_frac": warm["hbm_frac"],
                     "attained_peak": peaks["copy_gbps"],
                     "frac_of_attained": round(gu["gbps"] / peaks["copy_gbps"], 4),
                     "traffic_source": (str(PMC_FILE.relative_to(ROOT)) if load_json(PMC_FILE)

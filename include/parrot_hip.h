@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 10
+#define PARROT_ABI_VERSION 11
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -176,6 +176,17 @@ int parrot_decode_attention_heads_bf16(const void* q, const void* k_new, const v
                                        int32_t kv_heads, int32_t head_dim, int32_t max_positions,
                                        int32_t window, float scale, const void* out_weight,
                                        int32_t dim, float* contributions, void* stream);
+
+/* PARROT_OK when parrot_decode_attention_heads_bf16 takes this shape and its
+ * contributions fit the pending input mix of
+ * parrot_depth_mix_decode_moe_pending_bf16 (one lane per head: heads <= 16,
+ * dim <= 1024, dim % 4 == 0); otherwise the status either call would return.
+ * No pointer, no launch: the shape predicate of the deferred decode step
+ * (LocalGQA.decode(defer_sum=True), parrot/model.py:301-316), which takes the
+ * undeferred path when this fails. */
+int parrot_decode_attention_heads_check(int32_t batch, int32_t heads, int32_t kv_heads,
+                                        int32_t head_dim, int32_t max_positions, int32_t window,
+                                        int32_t dim);
 
 /* Decode-step attention of the MLA layers over the joint latent cache.
  * q [batch, H, latent_dim] fp32 (the query through the absorbed key

@@ -13,6 +13,12 @@ Rounding points of the HIP forward (each a toggle below):
 Routing is the oracle's own fp32 top-2 of the (rounded) MoE input, or forced
 to given indices (``force``).  Everything else follows oracle/parrot_fp32.py
 (reference jkpdino/parrot-h200-worker parrot/model.py:658-746).
+
+``acc64`` accumulates every linear map in float64 before its fp32 result is
+rounded: the same rounding points with another accumulation order.  Two such
+bf16 forwards differ only where a pre-rounding value sits within fp32
+reassociation of a bf16 rounding boundary; comparing them measures how far
+that alone carries a bf16 forward (its noise floor).
 """
 from __future__ import annotations
 
@@ -33,10 +39,17 @@ def _same(x: torch.Tensor) -> torch.Tensor:
     return x
 
 
+def _linear(acc64: bool):
+    if not acc64:
+        return F.linear
+    return lambda x, w: F.linear(x.double(), w.double()).float()
+
+
 def forward(o, ids: torch.Tensor, *, act=True, stream=True, head_in=True, logit=True,
-            force=None, capture: list | None = None) -> torch.Tensor:
+            force=None, capture: list | None = None, acc64: bool = False) -> torch.Tensor:
     """Logits of ParrotFP32 ``o`` on ``ids`` with the selected rounding
     points; ``capture`` collects each MoE layer's top-2 indices."""
+    lin = _linear(acc64)
     ra = bf16 if act else _same
     rs = bf16 if stream else _same
     c = o.c
@@ -49,10 +62,10 @@ def forward(o, ids: torch.Tensor, *, act=True, stream=True, head_in=True, logit=
             pre = ra(o._mix(index, sources))
             if is_moe:
                 h = ra(o._norm(f"blocks.{i}.moe_norm", pre))
-                delta = _moe(o, i, h, ra, None if force is None else force[i], capture)
+                delta = _moe(o, i, h, ra, None if force is None else force[i], capture, lin)
             else:
                 h = ra(o._norm(f"blocks.{i}.attention_norm", pre))
-                delta = _attention(o, i, h, ra)
+                delta = _attention(o, i, h, ra, lin)
             partial = delta if partial is None else rs(partial + delta)
             if (index + 1) % c.depth_block_size == 0:
                 completed.append(partial)
@@ -61,14 +74,14 @@ def forward(o, ids: torch.Tensor, *, act=True, stream=True, head_in=True, logit=
     mixed = ra(o._mix(index, completed + ([] if partial is None else [partial])))
     h = o._norm("final_norm", mixed)
     h = bf16(h) if head_in else h
-    out = F.linear(h, o._w("embedding.weight"))
+    out = lin(h, o._w("embedding.weight"))
     return bf16(out) if logit else out
 
 
-def _moe(o, i, h, ra, forced, capture):
+def _moe(o, i, h, ra, forced, capture, lin=F.linear):
     pre = f"blocks.{i}.moe."
     flat = h.reshape(-1, h.shape[-1])
-    logits = F.linear(flat, o._w(pre + "router.weight"))
+    logits = lin(flat, o._w(pre + "router.weight"))
     if forced is None:
         idx, w, _ = routing.top2(logits.numpy())
     else:
@@ -80,9 +93,9 @@ def _moe(o, i, h, ra, forced, capture):
         capture.append(idx)
 
     def swiglu(rows, name):
-        hidden = ra(F.silu(F.linear(rows, o._w(name + "gate.weight"))) *
-                    F.linear(rows, o._w(name + "up.weight")))
-        return F.linear(hidden, o._w(name + "down.weight"))
+        hidden = ra(F.silu(lin(rows, o._w(name + "gate.weight"))) *
+                    lin(rows, o._w(name + "up.weight")))
+        return lin(hidden, o._w(name + "down.weight"))
 
     out = swiglu(flat, pre + "shared.")
     it = torch.from_numpy(idx)
@@ -95,7 +108,7 @@ def _moe(o, i, h, ra, forced, capture):
     return ra(out).view_as(h)
 
 
-def _attention(o, i, h, ra):
+def _attention(o, i, h, ra, lin=F.linear):
     c, pre = o.c, f"blocks.{i}.attention."
     b, t, _ = h.shape
 
@@ -103,17 +116,17 @@ def _attention(o, i, h, ra):
         return y.view(b, t, n, c.head_dim).transpose(1, 2)
 
     if (i + 1) % c.global_every:
-        q = heads(ra(F.linear(h, o._w(pre + "q.weight"))), c.n_heads)
-        k = heads(ra(F.linear(h, o._w(pre + "k.weight"))), c.n_kv_heads)
-        v = heads(ra(F.linear(h, o._w(pre + "v.weight"))), c.n_kv_heads)
+        q = heads(ra(lin(h, o._w(pre + "q.weight"))), c.n_heads)
+        k = heads(ra(lin(h, o._w(pre + "k.weight"))), c.n_kv_heads)
+        v = heads(ra(lin(h, o._w(pre + "v.weight"))), c.n_kv_heads)
         q, k = ra(o._rope(q, 0)), ra(o._rope(k, 0))
         qi, ki = torch.arange(t)[:, None], torch.arange(t)[None, :]
         allowed = (ki <= qi) & (ki > qi - c.window_size)
     else:
-        latent = ra(F.linear(h, o._w(pre + "kv_down.weight")))
-        q = heads(ra(F.linear(h, o._w(pre + "q.weight"))), c.n_heads)
-        k = heads(ra(F.linear(latent, o._w(pre + "k_up.weight"))), c.n_heads)
-        v = heads(ra(F.linear(latent, o._w(pre + "v_up.weight"))), c.n_heads)
+        latent = ra(lin(h, o._w(pre + "kv_down.weight")))
+        q = heads(ra(lin(h, o._w(pre + "q.weight"))), c.n_heads)
+        k = heads(ra(lin(latent, o._w(pre + "k_up.weight"))), c.n_heads)
+        v = heads(ra(lin(latent, o._w(pre + "v_up.weight"))), c.n_heads)
         allowed = torch.arange(t)[None, :] <= torch.arange(t)[:, None]
     y = ra(o._attend(q, k, v, allowed, 1.0 / math.sqrt(c.head_dim)))
-    return ra(F.linear(y.transpose(1, 2).reshape(b, t, -1), o._w(pre + "out.weight")))
+    return ra(lin(y.transpose(1, 2).reshape(b, t, -1), o._w(pre + "out.weight")))

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (maps PyTorch's HIP runtime before the library)
 
 LIBRARY = Path(__file__).resolve().parent / "_lib" / "libparrot_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -38,6 +38,8 @@ SIGNATURES: dict[str, tuple] = {
     "parrot_decode_attention_heads_bf16": (
         ctypes.c_int,
         [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p, _i32, _p, _p]),
+    "parrot_decode_attention_heads_check": (
+        ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "parrot_decode_moe_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "parrot_vocab_argmax_workspace_bytes": (_sz, [_i64, _i32]),
     "parrot_causal_attention_bf16": (

@@ -944,13 +944,19 @@ DEFER_MAX_TOKENS = 4  # rows up to which decode attention defers its output sum
 DECODE_HEADS_PARTS = 16  # workgroups per head of parrot_decode_attention_heads_bf16
 
 
-def decode_attention_heads_supported(tokens: int, dim: int) -> bool:
+def decode_attention_heads_supported(tokens: int, dim: int, heads: int, kv_heads: int,
+                                     head_dim: int, max_positions: int, window: int) -> bool:
     """Shapes for which a decode step defers the attention output sum
     (``decode_attention_heads`` + the pending decode MoE mix): at most
     DEFER_MAX_TOKENS rows, since each head's attention runs in
-    DECODE_HEADS_PARTS workgroups (one per 1/16 of the output columns)."""
-    return (1 <= tokens <= DEFER_MAX_TOKENS and dim % DECODE_HEADS_PARTS == 0
-            and dim // DECODE_HEADS_PARTS <= 256)
+    DECODE_HEADS_PARTS workgroups (one per 1/16 of the output columns), and
+    the shape limits both kernels check (parrot_decode_attention_heads_check:
+    at most 16 heads, one pending lane each, and the heads kernel's LDS).
+    Other shapes take the undeferred decode."""
+    if not 1 <= tokens <= DEFER_MAX_TOKENS:
+        return False
+    return _abi.load().parrot_decode_attention_heads_check(
+        tokens, heads, kv_heads, head_dim, max_positions, window, dim) == 0
 
 
 def decode_attention_heads(q: Tensor, k_new: Tensor, v_new: Tensor, key_cache: Tensor,

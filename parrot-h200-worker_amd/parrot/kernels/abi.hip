@@ -231,6 +231,31 @@ int parrot_decode_attention_bf16(const void* q, const void* k_new, const void* v
       max_positions, window, scale, static_cast<uint16_t*>(out), as_stream(stream)));
 }
 
+static int check_decode_heads_shape(int32_t batch, int32_t heads, int32_t kv_heads,
+                                    int32_t head_dim, int32_t max_positions, int32_t window,
+                                    int32_t dim) {
+  if (int rc = check_decode_shape(batch, heads, kv_heads, head_dim, max_positions, window))
+    return rc;
+  if (dim <= 0) return PARROT_ERR_BAD_SHAPE;
+  if (dim % parrot::kDecodeHeadsParts || dim / parrot::kDecodeHeadsParts > 256 ||
+      parrot::decode_attention_lds_bytes(window, max_positions, head_dim) +
+              static_cast<size_t>(head_dim) * sizeof(float) > parrot::kMaxDecodeLds)
+    return PARROT_ERR_UNSUPPORTED;
+  return PARROT_OK;
+}
+
+int parrot_decode_attention_heads_check(int32_t batch, int32_t heads, int32_t kv_heads,
+                                        int32_t head_dim, int32_t max_positions, int32_t window,
+                                        int32_t dim) {
+  if (int rc = check_decode_heads_shape(batch, heads, kv_heads, head_dim, max_positions, window,
+                                        dim))
+    return rc;
+  // The pending input mix of parrot_depth_mix_decode_moe_pending_bf16 takes
+  // one lane per head.
+  if (heads > parrot::kMaxPendingLanes || dim > 1024 || dim % 4) return PARROT_ERR_UNSUPPORTED;
+  return PARROT_OK;
+}
+
 int parrot_decode_attention_heads_bf16(const void* q, const void* k_new, const void* v_new,
                                        void* key_cache, void* value_cache,
                                        const int32_t* position, int32_t batch, int32_t heads,
@@ -240,13 +265,9 @@ int parrot_decode_attention_heads_bf16(const void* q, const void* k_new, const v
   if (!q || !k_new || !v_new || !key_cache || !value_cache || !position || !out_weight ||
       !contributions)
     return PARROT_ERR_NULL_POINTER;
-  if (int rc = check_decode_shape(batch, heads, kv_heads, head_dim, max_positions, window))
+  if (int rc = check_decode_heads_shape(batch, heads, kv_heads, head_dim, max_positions, window,
+                                        dim))
     return rc;
-  if (dim <= 0) return PARROT_ERR_BAD_SHAPE;
-  if (dim % parrot::kDecodeHeadsParts || dim / parrot::kDecodeHeadsParts > 256 ||
-      parrot::decode_attention_lds_bytes(window, max_positions, head_dim) +
-              static_cast<size_t>(head_dim) * sizeof(float) > parrot::kMaxDecodeLds)
-    return PARROT_ERR_UNSUPPORTED;
   if (!aligned16(k_new) || !aligned16(v_new) || !aligned16(key_cache) ||
       !aligned16(value_cache) || !aligned16(out_weight))
     return PARROT_ERR_ALIGNMENT;

@@ -279,9 +279,15 @@ hipError_t launch_vocab_argmax(const uint16_t* h, int rows, int dim, const uint1
                                float* part_v, int32_t* part_i, int64_t* out, int32_t* advance,
                                hipStream_t s) {
   if (rows == 0) return hipSuccess;
-  // Two or more rows: the MFMA kernel (h staged in at most 64 KB of LDS).
+  // The MFMA kernel whenever the widest batch fits (16 rows of h staged in at
+  // most 64 KB of LDS), at every row count: the kernel is chosen from dim
+  // alone, so a row's logits are summed in the same order whether it is
+  // decoded alone or in a batch, and its greedy token does not depend on
+  // the batch it is in.  An MFMA output element depends only on its own
+  // row and column; the unused B columns are zero.
   const size_t mfma_lds = static_cast<size_t>(rows) * (dim + 8) * sizeof(uint16_t);
-  if (rows >= 2 && dim % 64 == 0 && mfma_lds <= 65536) {
+  const size_t mfma_lds_max = static_cast<size_t>(kVocabMaxRows) * (dim + 8) * sizeof(uint16_t);
+  if (dim % 64 == 0 && mfma_lds_max <= 65536) {
     const int blocks = (vocab + kVocabMfmaRows - 1) / kVocabMfmaRows;
     vocab_argmax_mfma_kernel<<<blocks, 256, mfma_lds, s>>>(h, rows, dim, w, vocab, part_v,
                                                            part_i);

@@ -393,16 +393,21 @@ class LocalGQA(nn.Module):
                 hip_moe.decode_qkv_supported(first.numel() // first.shape[-1], c.dim, c.n_heads,
                                              c.n_kv_heads, c.head_dim))
 
-    def defers_sum(self, x: Tensor, position_device: Tensor | None) -> bool:
-        """Whether decode(defer_sum=True) takes this input: the HIP decode
-        path at at most hip_moe.DEFER_MAX_TOKENS rows, which returns the
-        per-head contributions of the output projection instead of their
-        sum."""
+    def defers_sum(self, x: Tensor, position_device: Tensor | None,
+                   cache: LocalKVCache) -> bool:
+        """Whether decode(defer_sum=True) takes this input and cache: the HIP
+        decode path at at most hip_moe.DEFER_MAX_TOKENS rows and within the
+        shape limits of the per-head kernel and the pending mix, which
+        returns the per-head contributions of the output projection instead
+        of their sum."""
         if not (self._hip(x) and position_device is not None):
             return False
         from . import hip_moe
+        c = self.cfg
         b = x.numel() // x.shape[-1]
-        return hip_moe.decode_attention_heads_supported(b, x.shape[-1])
+        return hip_moe.decode_attention_heads_supported(
+            b, x.shape[-1], c.n_heads, c.n_kv_heads, c.head_dim, cache.key.shape[2],
+            c.window_size)
 
     def decode(self, x: Tensor | None, cache: LocalKVCache, position: int,
                addend: Tensor | None = None, defer_sum: bool = False,
@@ -423,7 +428,7 @@ class LocalGQA(nn.Module):
             raise ValueError("decode expects one model position")
         c = self.cfg
         b = x.shape[0]
-        if defer_sum and not self.defers_sum(x, position_device):
+        if defer_sum and not self.defers_sum(x, position_device, cache):
             raise RuntimeError("deferred attention reduction is not supported for this input")
         if self._hip(x) and position_device is not None:
             # RoPE at the device position, then one kernel stores the new key
@@ -895,7 +900,8 @@ class Parrot(nn.Module):
         first = stream.sources()[0]
         return (isinstance(block.attention, LocalGQA) and
                 (index + 1) % self.config.depth_block_size != 0 and
-                block.attention.defers_sum(first, state.position_device) and
+                block.attention.defers_sum(first, state.position_device,
+                                           state.layers[index // 2]) and
                 self._fuses_decode_moe(block, first))
 
     @staticmethod
@@ -1135,6 +1141,14 @@ class Parrot(nn.Module):
             x = torch.empty((input_ids.shape[0], 1, cfg.dim), dtype=weight.dtype,
                             device=input_ids.device)
             if first.decodes_mixed(x, state.position_device):
+                # The launch clamps ids outside the table to its nearest row
+                # (a graph replay has no error channel).  An eager step checks
+                # them first and raises as nn.Embedding does.
+                if not torch.cuda.is_current_stream_capturing():
+                    bad = (input_ids < 0) | (input_ids >= weight.shape[0])
+                    if bool(bad.any()):
+                        raise IndexError("decode_step token id out of range of the "
+                                         f"{weight.shape[0]}-row embedding")
                 return x, (input_ids, weight)
         return self.embedding(input_ids), None
 

@@ -68,6 +68,35 @@ def test_workspace_sizes(lib):
     assert big >= 3 * 512 * 512 * 2 + 3 * 512 * 768 * 4
 
 
+def test_decode_heads_predicate(lib):
+    """The deferred decode step's shape predicate (hip_moe.
+    decode_attention_heads_supported, the C ABI's
+    parrot_decode_attention_heads_check): the default model's local layers
+    defer at one to four rows; more than 16 query heads (one pending lane
+    each), a window whose scores overflow the heads kernel's LDS, or more
+    rows take the undeferred decode."""
+    from parrot import hip_moe
+    default = dict(dim=768, heads=8, kv_heads=2, head_dim=96, max_positions=4096, window=2048)
+    for tokens in (1, 2, 4):
+        assert hip_moe.decode_attention_heads_supported(tokens, **default)
+    assert not hip_moe.decode_attention_heads_supported(5, **default)
+    assert not hip_moe.decode_attention_heads_supported(0, **default)
+    assert hip_moe.decode_attention_heads_supported(1, **{**default, "heads": 16})
+    assert not hip_moe.decode_attention_heads_supported(
+        1, **{**default, "heads": 32, "kv_heads": 4, "head_dim": 32})
+    # 16000 fp32 scores alone fill the 64 KB of LDS
+    assert not hip_moe.decode_attention_heads_supported(
+        1, **{**default, "max_positions": 16384, "window": 16000})
+    assert hip_moe.decode_attention_heads_supported(
+        1, **{**default, "max_positions": 16384, "window": 8192})
+    assert not hip_moe.decode_attention_heads_supported(1, **{**default, "dim": 776})
+    assert not hip_moe.decode_attention_heads_supported(1, **{**default, "dim": 2048})
+    assert lib.parrot_decode_attention_heads_check(1, 32, 4, 32, 4096, 2048, 768) == -3
+    assert lib.parrot_decode_attention_heads_check(1, 8, 3, 96, 4096, 2048, 768) == -3
+    assert lib.parrot_decode_attention_heads_check(1, 8, 2, 96, 4096, 0, 768) == -2
+    assert lib.parrot_decode_attention_heads_check(1, 8, 2, 96, 4096, 2048, 768) == 0
+
+
 def test_argument_validation_without_gpu(lib):
     """Rejected before launch: no device is touched."""
     from parrot import _abi

@@ -512,3 +512,87 @@ def test_decode_moe_router_weights_in_memory_or_lds(dim, experts):
     mx, mean = error_stats(out, ref)
     assert mx <= MAX_ABS and mean <= MEAN_ABS
     assert torch.equal(full.indices, idx)
+
+
+def test_decode_with_32_heads_runs_undeferred(monkeypatch):
+    """A model with 32 query heads (more lanes than the pending decode mix
+    takes) decodes on the undeferred path: the per-head kernel is never
+    called, and prefill + decode steps match the fp32 oracle forced to the
+    HIP top-2 choices (the full-model rule of tests/parity.py)."""
+    from oracle import parrot_fp32
+    from parity import RouteRecorder, format_report, logits_report
+    from parrot import ModelConfig, Parrot, hip_moe
+    _say("decode with 32 query heads (undeferred)")
+
+    def refuse(*a, **k):
+        raise AssertionError("the deferred per-head decode attention was chosen")
+    monkeypatch.setattr(hip_moe, "decode_attention_heads", refuse)
+    torch.manual_seed(7)
+    cfg = ModelConfig(n_layers=4, n_heads=32, n_kv_heads=4, head_dim=64,
+                      moe_backend="grouped_hip", depth_backend="hip", collect_router_stats=False)
+    model = Parrot(cfg).to(device="cuda", dtype=torch.bfloat16).eval()
+    prompt = torch.randint(0, 32768, (1, 24), generator=torch.Generator().manual_seed(7))
+    rec = RouteRecorder(monkeypatch)
+    logits, state = model.prefill(prompt.cuda())
+    got, tokens = [logits.float().cpu()], []
+    for _ in range(4):
+        tokens.append(got[-1][:, -1].argmax(-1, keepdim=True))
+        logits, state = model.decode_step(tokens[-1].cuda(), state)
+        got.append(logits.float().cpu())
+    hip_idx = rec.stop()
+    forced = parrot_fp32.ParrotFP32(cfg, model.state_dict(), forced_routing=hip_idx)
+    ref, f_state = forced.prefill(prompt)
+    refs = [ref]
+    for tok in tokens:
+        refs.append(forced.decode_step(tok, f_state))
+    r = logits_report(torch.cat([g.reshape(-1, g.shape[-1]) for g in got]),
+                      torch.cat([x.reshape(-1, x.shape[-1]) for x in refs]), 0.03)
+    _say(f"  vs forced oracle: {format_report(r)}")
+    assert r["clear_miss"] == 0 and r["max_abs"] <= 0.03 and r["mean_abs"] <= 3.5e-3
+
+
+def test_vocab_argmax_is_batch_invariant():
+    """A row's greedy token does not depend on the batch it is decoded in:
+    rows with planted near-ties (two head rows whose logits differ by one
+    bf16 ulp of one weight, within fp32 reassociation of each other) give
+    the same token alone and inside batches of 2, 5 and 16 rows."""
+    from parrot import hip_moe
+    _say("vocab argmax batch invariance")
+    g = torch.Generator().manual_seed(13)
+    vocab, dim, n = 32768, 768, 32
+    w = (torch.randn(vocab, dim, generator=g) * 0.02).bfloat16()
+    h = torch.randn(n, dim, generator=g).bfloat16()
+    for i in range(n):
+        a, b = 100 + 2 * i, 101 + 2 * i
+        w[a] = (h[i].float() * 0.05).bfloat16()
+        w[b] = w[a]
+        j = int(h[i].float().abs().argmin())  # the smallest |h| element: a tiny logit change
+        w[b, j] = (w[a, j:j + 1].view(torch.int16) + 1).view(torch.bfloat16)[0]  # one bf16 ulp
+    wc, hc = w.cuda(), h.cuda()
+    with torch.no_grad():
+        alone = torch.stack([hip_moe.vocab_argmax(hc[i:i + 1], wc)[0] for i in range(n)]).cpu()
+        for size in (2, 5, 16):
+            for start in range(0, n - size + 1, size):
+                batch = hip_moe.vocab_argmax(hc[start:start + size], wc).cpu()
+                assert torch.equal(batch, alone[start:start + size]), (size, start)
+    assert all(int(alone[i]) in (100 + 2 * i, 101 + 2 * i) for i in range(n))
+
+
+def test_eager_decode_step_rejects_out_of_range_ids():
+    """Eager decode_step raises on a token id outside the embedding table, as
+    the reference's nn.Embedding does, instead of reading a clamped row (the
+    fused first-layer launch clamps, for graph replay)."""
+    from parrot import ModelConfig, Parrot
+    torch.manual_seed(3)
+    model = Parrot(ModelConfig(n_layers=4, moe_backend="grouped_hip", depth_backend="hip",
+                               collect_router_stats=False)).to(device="cuda",
+                                                               dtype=torch.bfloat16).eval()
+    prompt = torch.randint(0, 32768, (2, 8), generator=torch.Generator().manual_seed(3)).cuda()
+    _, state = model.prefill(prompt)
+    for bad in (32768, -1):
+        ids = torch.tensor([[5], [bad]], device="cuda")
+        with pytest.raises(IndexError):
+            model.decode_step(ids, state)
+    assert state.position == 8
+    logits, state = model.decode_step(torch.tensor([[5], [7]], device="cuda"), state)
+    assert state.position == 9 and torch.isfinite(logits.float()).all()

@@ -179,7 +179,72 @@ def test_default_forward_512(monkeypatch):
     capture = {}
     ref_forced = _oracle(model, forced=hip_idx).forward(ids, capture)
     _check(got, ref_forced, ref, routing_report(hip_idx, capture["logits"]),
-           max_abs=FORCED_MAX_ABS, mean_abs=FORCED_MEAN_ABS, forced_floor=0.975, free_floor=0.94)
+           max_abs=FORCED_MAX_ABS, mean_abs=FORCED_MEAN_ABS, forced_floor=0.977, free_floor=0.948)
+
+
+def test_default_forward_bf16_noise_floor(monkeypatch):
+    """C4's argmax disagreement with fp32 is bf16 arithmetic, not a kernel
+    error: pooled over four seeded inputs of the default model (seed 2 is
+    C4; 2,048 positions), the HIP forward is as close to the fp32 oracle and
+    to the bf16 emulation of the same rounding points
+    (oracle/rounding_emulation.py), both forced to the HIP top-2 choices, as
+    that emulation is to itself with another accumulation order (every
+    linear map accumulated in float64 before rounding).
+
+    That last distance is the floor of any bf16 forward: one-ulp rounding
+    differences at fp32 reassociation grow over sixteen layers to the size of
+    the bf16 error itself, so two bf16 forwards agree on ~99 % of argmax
+    positions (tests/test_error_budget_cpu.py::test_bf16_noise_floor).
+    Bars, each from the pooled counts:
+      * argmax(HIP) vs argmax(emulation) agree at least as often as the two
+        emulations do, less 0.5 point;
+      * HIP vs forced fp32 argmax agreement at least the emulation's less
+        0.5 point; logits mean-abs at most 1.15x and max-abs at most 1.5x the
+        emulation's (the HIP forward rounds attention probabilities to bf16
+        for their product with V, a rounding point the emulation leaves
+        out)."""
+    from oracle import rounding_emulation
+    from parrot import ModelConfig
+    cfg = ModelConfig(moe_backend="grouped_hip", depth_backend="hip", collect_router_stats=False)
+    got_all, emu_all, emu64_all, ref_all = [], [], [], []
+    rec = RouteRecorder(monkeypatch)
+    for seed in (2, 3, 4, 5):
+        model = _hip_model(cfg, seed)
+        ids = torch.randint(0, 32768, (1, 512), generator=torch.Generator().manual_seed(seed))
+        with torch.no_grad():
+            got = model(ids.cuda()).logits.float().cpu()
+        hip_idx = rec.take()
+        oracle = _oracle(model, forced=hip_idx)
+        del model
+        torch.cuda.empty_cache()
+        with torch.no_grad():
+            ref = oracle.forward(ids)
+            emu = rounding_emulation.forward(oracle, ids, logit=False, force=hip_idx)
+            emu64 = rounding_emulation.forward(oracle, ids, logit=False, force=hip_idx, acc64=True)
+        for dst, t in ((got_all, got), (emu_all, emu), (emu64_all, emu64), (ref_all, ref)):
+            dst.append(t.reshape(-1, t.shape[-1]))
+        say(f"  seed {seed}: argmax vs forced fp32 HIP {_agree(got, ref):.4f} emulation "
+            f"{_agree(emu, ref):.4f}; HIP vs emulation {_agree(got, emu):.4f}, emulation vs "
+            f"float64-accumulated emulation {_agree(emu, emu64):.4f}")
+        del oracle
+    got, emu, emu64, ref = (torch.cat(x) for x in (got_all, emu_all, emu64_all, ref_all))
+    floor = _agree(emu, emu64)
+    hip_emu, hip_ref, emu_ref = _agree(got, emu), _agree(got, ref), _agree(emu, ref)
+    d_hip, d_emu = (got - ref).abs(), (emu - ref).abs()
+    say(f"  pooled over {got.shape[0]} positions: HIP vs emulation {hip_emu:.4f} (floor: "
+        f"emulation vs float64 emulation {floor:.4f}); vs forced fp32 HIP {hip_ref:.4f} "
+        f"emulation {emu_ref:.4f}; logits vs fp32 mean-abs HIP {d_hip.mean().item():.3e} "
+        f"emulation {d_emu.mean().item():.3e}, max-abs HIP {d_hip.max().item():.3e} emulation "
+        f"{d_emu.max().item():.3e}")
+    assert hip_emu >= floor - 0.005
+    assert hip_ref >= emu_ref - 0.005
+    assert d_hip.mean().item() <= 1.15 * d_emu.mean().item()
+    assert d_hip.max().item() <= 1.5 * d_emu.max().item()
+
+
+def _agree(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.reshape(-1, a.shape[-1]), b.reshape(-1, b.shape[-1])
+    return (a.argmax(-1) == b.argmax(-1)).float().mean().item()
 
 
 # ---------------------------------------------------------------------------
@@ -230,7 +295,7 @@ def test_prefill_and_decode_16_steps(batch, monkeypatch):
     _check(got_all, torch.cat([r.reshape(batch, -1) for r in forced_refs]),
            torch.cat([r.reshape(batch, -1) for r in refs]),
            routing_report(hip_idx, capture["logits"]),
-           max_abs=FORCED_MAX_ABS, mean_abs=FORCED_MEAN_ABS, forced_floor=0.94, free_floor=0.94)
+           max_abs=FORCED_MAX_ABS, mean_abs=FORCED_MEAN_ABS, forced_floor=0.995, free_floor=0.995)
 
 
 # ---------------------------------------------------------------------------
