@@ -58,6 +58,8 @@ def parse_args():
     p.add_argument("--skip-sweep", action="store_true",
                    help="skip the token-count sweep of the per-kernel timings")
     p.add_argument("--skip-decode", action="store_true")
+    p.add_argument("--sweep-only", action="store_true",
+                   help="only the token-count sweep of the per-kernel timings (one JSON line)")
     p.add_argument("--traffic-workload", action="store_true",
                    help="only launch the dispatches the two rocprofv3 --pmc passes count: the "
                         "dominant kernel at the in-model shape and a calibration copy")
@@ -1245,6 +1247,10 @@ def main():
 
     model, ids, captured = build_model()
     moe0 = model.blocks[0].moe
+    if args.sweep_only:
+        print(json.dumps({"sweep_E16": sweep_kernels(moe0, max(20, args.kernel_iters // 4))}),
+              flush=True)
+        return
 
     log("eager forward")
     with torch.no_grad():

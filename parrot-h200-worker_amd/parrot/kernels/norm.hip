@@ -251,6 +251,144 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   }
 }
 
+// The depth mix at large token counts: one wavefront per token, four
+// tokens per workgroup, no LDS and no barrier.  The wavefront does, slice by
+// slice, what the wavefronts of depth_mix_kernel do side by side: lane l
+// owns the 4-dim chunks l, l + 64, ... (slice w = the chunks of wavefront w
+// there), every slice's per-source partials are reduced by the same DPP
+// steps (wave_total_lane63) and the slice totals added in slice order, so
+// the scores, the mix and its norm are the same bits for every token
+// whichever kernel runs it (a token's result does not depend on the batch).
+// What changes is the cost per byte: depth_mix_kernel keeps a token's three
+// wavefronts waiting on each other at two barriers and LDS round trips, so
+// at large token counts a CU holds ~8 tokens in flight; here a token is one
+// wavefront.  NCH: slices (wavefronts of the other kernel), dim <= 256 NCH.
+// The kernel is
+// bound by its VALU work (~1,800 instructions per token at 9 sources, 700 of
+// them the 54 wavefront reductions that the bit-identity with the other
+// kernel asks for): 4.5 TB/s at 65536 tokens against 3.9 TB/s for one
+// workgroup per token.
+constexpr int kDepthWaveTokensPerGroup = 4;
+constexpr int kDepthWaveMinTokens = 4096;  // from here launch_depth_mix takes this kernel
+
+template <int NS, int NCH>
+__global__ __launch_bounds__(64 * kDepthWaveTokensPerGroup) void depth_mix_wave_kernel(
+    DepthSources srcs, const uint16_t* __restrict__ query,
+    const uint16_t* __restrict__ score_w, float score_eps,
+    const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
+    uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm) {
+  const uint16_t* sp[kMaxDepthSources];
+#pragma unroll
+  for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = srcs.src[s];
+  static_assert(kMaxDepthSources == 9, "the batch below names every source slot");
+  asm volatile("" ::"s"(sp[0]), "s"(sp[1]), "s"(sp[2]), "s"(sp[3]), "s"(sp[4]), "s"(sp[5]),
+               "s"(sp[6]), "s"(sp[7]), "s"(sp[8]), "s"(query), "s"(score_w), "s"(out_w),
+               "s"(out_norm), "s"(dim), "s"(out_mix), "s"(tokens));
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * kDepthWaveTokensPerGroup +
+                      __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (tok >= tokens) return;  // uniform per wavefront; no barrier follows
+  const int chunks = dim >> 2;
+  const int64_t base = tok * chunks;
+  bool has[NCH];
+  int ic[NCH];
+#pragma unroll
+  for (int w = 0; w < NCH; ++w) {
+    has[w] = w * kWave + lane < chunks;
+    ic[w] = has[w] ? w * kWave + lane : 0;  // clamped: every load is unconditional
+  }
+  uint2 v[NCH][kMaxDepthSources];
+#pragma unroll
+  for (int w = 0; w < NCH; ++w)
+#pragma unroll
+    for (int s = 0; s < NS; ++s) v[w][s] = reinterpret_cast<const uint2*>(sp[s])[base + ic[w]];
+  uint2 q[NCH], g[NCH], g_out[NCH];
+#pragma unroll
+  for (int w = 0; w < NCH; ++w) {
+    q[w] = reinterpret_cast<const uint2*>(query)[ic[w]];
+    g[w] = reinterpret_cast<const uint2*>(score_w)[ic[w]];
+    g_out[w] = reinterpret_cast<const uint2*>(out_norm != nullptr ? out_w : score_w)[ic[w]];
+  }
+  // Per slice: the chunk's partials (depth_mix_chunk's products and sums),
+  // reduced to lane 63, read as a wave-uniform value, added in slice order.
+  float sst[NS], dqt[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) sst[s] = dqt[s] = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NCH; ++w) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      if (!has[w]) v[w][s] = make_uint2(0u, 0u);
+    float wq[4] = {0.f, 0.f, 0.f, 0.f};
+    if (has[w]) {
+      wq[0] = lo_bf16(q[w].x) * lo_bf16(g[w].x);
+      wq[1] = hi_bf16(q[w].x) * hi_bf16(g[w].x);
+      wq[2] = lo_bf16(q[w].y) * lo_bf16(g[w].y);
+      wq[3] = hi_bf16(q[w].y) * hi_bf16(g[w].y);
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const float e0 = lo_bf16(v[w][s].x), e1 = hi_bf16(v[w][s].x);
+      const float e2 = lo_bf16(v[w][s].y), e3 = hi_bf16(v[w][s].y);
+      const float ss = wave_total_lane63(e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3);
+      const float dq = wave_total_lane63(e0 * wq[0] + e1 * wq[1] + e2 * wq[2] + e3 * wq[3]);
+      sst[s] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 63));
+      dqt[s] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dq), 63));
+    }
+  }
+  float score[NS];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    score[s] = dqt[s] * rsqrtf(sst[s] / static_cast<float>(dim) + score_eps);
+    mx = fmaxf(mx, score[s]);
+  }
+  float denom = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) denom += __expf(score[s] - mx);
+  const float inv = 1.0f / denom;
+  float alpha[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) alpha[s] = __expf(score[s] - mx) * inv;
+  uint2 mixed[NCH];
+  float sso_total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NCH; ++w) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      acc[0] += alpha[s] * lo_bf16(v[w][s].x);
+      acc[1] += alpha[s] * hi_bf16(v[w][s].x);
+      acc[2] += alpha[s] * lo_bf16(v[w][s].y);
+      acc[3] += alpha[s] * hi_bf16(v[w][s].y);
+    }
+    mixed[w].x = pack_bf16x2(acc[0], acc[1]);
+    mixed[w].y = pack_bf16x2(acc[2], acc[3]);
+    if (out_mix != nullptr && has[w])
+      reinterpret_cast<uint2*>(out_mix)[base + w * kWave + lane] = mixed[w];
+    if (out_norm != nullptr) {
+      const float r0 = lo_bf16(mixed[w].x), r1 = hi_bf16(mixed[w].x);
+      const float r2 = lo_bf16(mixed[w].y), r3 = hi_bf16(mixed[w].y);
+      const float sso =
+          wave_total_lane63(has[w] ? r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3 : 0.0f);
+      const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sso), 63));
+      sso_total = w == 0 ? t : sso_total + t;
+    }
+  }
+  if (out_norm == nullptr) return;
+  const float r = rsqrtf(sso_total / static_cast<float>(dim) + out_eps);
+#pragma unroll
+  for (int w = 0; w < NCH; ++w) {
+    if (!has[w]) continue;
+    const float r0 = lo_bf16(mixed[w].x), r1 = hi_bf16(mixed[w].x);
+    const float r2 = lo_bf16(mixed[w].y), r3 = hi_bf16(mixed[w].y);
+    uint2 o;
+    o.x = pack_bf16x2(r0 * r * lo_bf16(g_out[w].x), r1 * r * hi_bf16(g_out[w].x));
+    o.y = pack_bf16x2(r2 * r * lo_bf16(g_out[w].y), r3 * r * hi_bf16(g_out[w].y));
+    reinterpret_cast<uint2*>(out_norm)[base + w * kWave + lane] = o;
+  }
+}
+
 // Chunks of 4 elements per lane, rounded up to an instantiated count.
 int chunk_bucket(int dim) {
   const int per_lane = (dim / 4 + kWave - 1) / kWave;
@@ -293,6 +431,22 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
   const CombineSource c = comb != nullptr ? *comb : none;
   const unsigned grid = static_cast<unsigned>(tokens);
   return with_sources(n_sources, [&](auto ns) {
+    if (route == nullptr && comb == nullptr && tokens >= kDepthWaveMinTokens && waves <= 4) {
+      const unsigned groups = static_cast<unsigned>(
+          (tokens + kDepthWaveTokensPerGroup - 1) / kDepthWaveTokensPerGroup);
+      auto wave_kernel = [&](auto nch) {
+        depth_mix_wave_kernel<ns, nch><<<groups, kWave * kDepthWaveTokensPerGroup, 0, s>>>(
+            srcs, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
+            out_norm);
+      };
+      switch (waves) {
+        case 1: wave_kernel(std::integral_constant<int, 1>{}); break;
+        case 2: wave_kernel(std::integral_constant<int, 2>{}); break;
+        case 3: wave_kernel(std::integral_constant<int, 3>{}); break;
+        default: wave_kernel(std::integral_constant<int, 4>{}); break;
+      }
+      return hipGetLastError();
+    }
     if (route != nullptr && route->experts > 16)
       depth_mix_kernel<2, ns><<<grid, kWave * waves, 0, s>>>(
           srcs, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix, out_norm,

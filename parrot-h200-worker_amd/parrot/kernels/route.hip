@@ -483,12 +483,141 @@ __global__ __launch_bounds__(256) void group_kernel(
   }
 }
 
+// Long inputs: persistent wavefronts, each routing 16-token route blocks
+// gw, gw + (all wavefronts), ... on its own (no barrier: its LDS is its own).
+// A block's rows are read a third of a row (256 k values) at a time, as two
+// 512-byte contiguous runs per load instruction (rows 2p and 2p + 1 in
+// lanes 0-31 and 32-63), instead of the MFMA fragment pattern (16 rows x 64
+// bytes per instruction, which route_kernel and route_wide_kernel use and
+// which held them to ~3.5 TB/s at 64K tokens).  The chunks go to LDS (the
+// 16-byte chunk c of row r at r * 512 + ((c ^ r) << 4): conflict-free writes
+// and fragment reads) and the A fragments are read back from there; the
+// router's B fragments for every k step stay in registers (the router is the
+// same for every block).  As soon as a third is in LDS, the loads of the
+// next third (or of the next block's first) are issued into the same
+// registers, so the memory stream runs through the MFMAs, the top-2, the
+// ranking and the stores.  (Two thirds in flight need a second register set,
+// which only fits with B read from LDS as well: 27.3 against 23.5 us at 64K
+// tokens.)  Arithmetic: route_kernel's (four accumulator chains by k-step
+// residue, summed ((c0 + c1) + c2) + c3 over the same fragments):
+// bit-identical.  dim == 32 kStreamSteps (the model's 768), E <= 16 and
+// tokens * dim * 2 < 2^31 (32-bit row offsets).
+constexpr int kStreamSteps = 24;
+constexpr int kStreamThirds = 3;                 // k chunks of 8 steps
+constexpr int kStreamThirdBytes = 512;           // per row
+constexpr int kStreamWavesPerGroup = 4;
+constexpr int kStreamGroupsPerCu = 2;            // the registers leave two workgroups per CU
+
+struct StreamWaveLds {
+  uint8_t rows[kRouteTokensPerBlock * kStreamThirdBytes];
+  float logits[kRouteTokensPerBlock][kRouteTokensPerBlock + 1];
+  int ids[kRouteAssignPerBlock];
+};
+
+__global__ __launch_bounds__(64 * kStreamWavesPerGroup) void route_stream_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
+    const float* __restrict__ bias, int64_t tokens, int dim, int experts,
+    float* __restrict__ out_logits, float* __restrict__ probs, float* __restrict__ weights,
+    int64_t* __restrict__ indices, int32_t* __restrict__ positions,
+    int32_t* __restrict__ block_counts, int n_blocks) {
+  asm volatile("" ::"s"(x), "s"(wr), "s"(bias), "s"(tokens), "s"(dim), "s"(experts),
+               "s"(out_logits), "s"(probs), "s"(weights), "s"(indices), "s"(positions),
+               "s"(block_counts), "s"(n_blocks));
+  __builtin_amdgcn_sched_barrier(0);
+  __shared__ StreamWaveLds lds[kStreamWavesPerGroup];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  StreamWaveLds& L = lds[wave];
+  const int stride = __builtin_amdgcn_readfirstlane(gridDim.x * kStreamWavesPerGroup);
+  int rb = __builtin_amdgcn_readfirstlane(blockIdx.x * kStreamWavesPerGroup + wave);
+  if (rb >= n_blocks) return;  // uniform per wavefront; no barrier follows
+  const int half = lane >> 5, cl = lane & 31;
+  const int j = lane & 15, h = lane >> 4;
+  const int last_row = static_cast<int>(tokens) - 1;
+  // Load p of a third reads row 2p + half of its block (rows past the input
+  // read the last row), 16-byte chunk 32 third + cl.
+  auto chunk = [&](int blk, int p, int third) {
+    const int row = min(blk * kRouteTokensPerBlock + half + 2 * p, last_row);
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(x) +
+                                           (row * dim * 2 + ((32 * third + cl) << 4)));
+  };
+#define PARROT_LOAD_THIRD(BLK, T)                                                      \
+  a0 = chunk(BLK, 0, T); a1 = chunk(BLK, 1, T); a2 = chunk(BLK, 2, T);                 \
+  a3 = chunk(BLK, 3, T); a4 = chunk(BLK, 4, T); a5 = chunk(BLK, 5, T);                 \
+  a6 = chunk(BLK, 6, T); a7 = chunk(BLK, 7, T);
+  auto put = [&](int p, uint4 v) {
+    const int r = 2 * p + half;
+    *reinterpret_cast<uint4*>(L.rows + r * kStreamThirdBytes + ((cl ^ r) << 4)) = v;
+  };
+  uint4 a0, a1, a2, a3, a4, a5, a6, a7;
+  PARROT_LOAD_THIRD(rb, 0)
+  bf16x8 b[kStreamSteps];
+  {
+    const uint16_t* pb = wr + static_cast<int64_t>(min(j, experts - 1)) * dim + h * 8;
+#pragma unroll
+    for (int i = 0; i < kStreamSteps; ++i) b[i] = load_bf16x8(pb + i * 32);
+  }
+  const float bias0 = bias != nullptr && j < experts ? bias[j] : 0.0f;
+  for (;;) {
+    const int next = rb + stride;
+    f32x4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < kStreamThirds; ++t) {
+      put(0, a0); put(1, a1); put(2, a2); put(3, a3);
+      put(4, a4); put(5, a5); put(6, a6); put(7, a7);
+      // The next third, or the next block's first (this block's again past
+      // the last: a repeat that is never used).
+      if (t + 1 < kStreamThirds) {
+        PARROT_LOAD_THIRD(rb, t + 1)
+      } else {
+        PARROT_LOAD_THIRD(min(next, n_blocks - 1), 0)
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int st = 8 * t + i;
+        const int c = 4 * i + h;  // this lane's A fragment: row j, chunk 4 st + lane / 16
+        const uint4 av = *reinterpret_cast<const uint4*>(L.rows + j * kStreamThirdBytes +
+                                                         ((c ^ j) << 4));
+        acc[st % 4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
+                                                              b[st], acc[st % 4], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      L.logits[4 * h + r][j] = ((acc[0][r] + acc[1][r]) + acc[2][r]) + acc[3][r];
+    const int64_t t0 = static_cast<int64_t>(rb) * kRouteTokensPerBlock;
+#pragma unroll 1
+    for (int pass = 0; pass < 4; ++pass) {
+      const int tl = pass * 4 + h;
+      select_top2(L.logits[tl][j] + bias0, 0.0f, experts, t0 + tl, t0 + tl < tokens, out_logits,
+                  probs, weights, indices, &L.ids[2 * tl]);
+    }
+    rank_half_waves(lane < 32 ? L.ids[lane] : -1, lane < 32 ? rb : n_blocks, n_blocks,
+                    2 * tokens, experts, positions, block_counts);
+    rb = next;
+    if (rb >= n_blocks) break;
+  }
+#undef PARROT_LOAD_THIRD
+}
+
 }  // namespace
 
 // The wide (64-token) route kernel takes over once its workgroups alone
 // cover every CU; below that the split-K kernel's shorter chain wins.
 constexpr int64_t kWideRouteTokens = 32768;  // the two shapes tie at 32K tokens
 constexpr int kWideRouteLdsBytes = 65536;     // the wide kernel's staged router weights
+constexpr int64_t kStreamRouteTokens = 32768;  // route_stream_kernel from here (E <= 16, dim 768;
+                                              // at 16K tokens the split-K shape is ahead)
+
+// Compute units of the current device (the persistent route grid's size):
+// a host-side property query, no stream work, so graph capture may call it.
+static hipError_t device_cus(int* cus) {
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  return hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
+}
 
 hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
                         const float* given_logits, const float* bias,
@@ -503,6 +632,16 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* router_w,
     route_kernel<true><<<nrb, 256, 0, s>>>(x, router_w, given_logits, bias, tokens, dim, experts,
                                            out_logits, probs, weights, indices, positions,
                                            block_counts, block_rows);
+  } else if (tokens >= kStreamRouteTokens && block_rows == nullptr &&
+             dim == 32 * kStreamSteps && experts <= 16 && tokens * dim * 2 < (int64_t{1} << 31)) {
+    // One workgroup per CU slot the kernel's registers leave.
+    int cus = 0;
+    if (hipError_t e = device_cus(&cus); e != hipSuccess) return e;
+    const int groups = (nrb + kStreamWavesPerGroup - 1) / kStreamWavesPerGroup;
+    const int grid = min(groups, kStreamGroupsPerCu * cus);
+    route_stream_kernel<<<grid, 64 * kStreamWavesPerGroup, 0, s>>>(
+        x, router_w, bias, tokens, dim, experts, out_logits, probs, weights, indices, positions,
+        block_counts, nrb);
   } else if (tokens >= kWideRouteTokens &&
              (experts > 16 ? 32 : 16) * (dim + 8) * 2 <= kWideRouteLdsBytes) {
     const bool two = experts > 16;

@@ -79,6 +79,35 @@ def test_depth_mix_and_norm(sources, tokens, dim):
     _ulp_ok(fused, ref_norm)
 
 
+@pytest.mark.parametrize("sources,dim", [(9, 768), (2, 768), (5, 1024), (3, 64), (1, 448)])
+def test_depth_mix_wave_kernel_equals_token_kernel(sources, dim):
+    """From 4096 tokens the depth mix runs one wavefront per token
+    (depth_mix_wave_kernel) instead of one workgroup per token: every token's
+    mix and normalised mix are the same bits either way (the same products,
+    DPP reductions and slice order), so a token's result does not depend on
+    the batch it is in.  Checked by mixing 5,000 tokens at once against the
+    same rows mixed in chunks below the threshold."""
+    from parrot import hip_moe
+    _say(f"depth mix wave kernel S={sources} dim={dim}")
+    torch.manual_seed(sources * 7 + dim)
+    depth = _Depth(dim).cuda().bfloat16()
+    out_norm = _Norm(dim).cuda().bfloat16()
+    tokens = 5000
+    src = [(torch.randn(tokens, dim) * (1 + s)).cuda().bfloat16() for s in range(sources)]
+    with torch.no_grad():
+        mix = hip_moe.depth_mix(depth, src)
+        fused = hip_moe.depth_mix_norm(depth, src, out_norm)
+        parts = [(0, 1), (1, 1000), (1000, 3000), (3000, 5000)]
+        mix_ref = torch.cat([hip_moe.depth_mix(depth, [x[a:b] for x in src]) for a, b in parts])
+        fused_ref = torch.cat([hip_moe.depth_mix_norm(depth, [x[a:b] for x in src], out_norm)
+                               for a, b in parts])
+    assert torch.equal(mix, mix_ref)
+    assert torch.equal(fused, fused_ref)
+    cpu = [x.float().cpu() for x in src]
+    ref = layers.depth_mix(cpu, depth.query.float().cpu(), depth.norm.weight.float().cpu(), 1e-6)
+    _ulp_ok(mix, ref, scale=torch.stack(cpu).abs().amax(0))
+
+
 MOE_CASES = [
     ("C2", 256, 32, False),
     ("C3", 4096, 32, True),
