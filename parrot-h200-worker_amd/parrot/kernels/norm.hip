@@ -252,24 +252,24 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
 }
 
 // The depth mix at large token counts: one wavefront per token, four
-// tokens per workgroup, no LDS and no barrier.  The wavefront does, slice by
-// slice, what the wavefronts of depth_mix_kernel do side by side: lane l
-// owns the 4-dim chunks l, l + 64, ... (slice w = the chunks of wavefront w
-// there), every slice's per-source partials are reduced by the same DPP
-// steps (wave_total_lane63) and the slice totals added in slice order, so
-// the scores, the mix and its norm are the same bits for every token
-// whichever kernel runs it (a token's result does not depend on the batch).
-// What changes is the cost per byte: depth_mix_kernel keeps a token's three
-// wavefronts waiting on each other at two barriers and LDS round trips, so
-// at large token counts a CU holds ~8 tokens in flight; here a token is one
-// wavefront.  NCH: slices (wavefronts of the other kernel), dim <= 256 NCH.
-// The kernel is
-// bound by its VALU work (~1,800 instructions per token at 9 sources, 700 of
-// them the 54 wavefront reductions that the bit-identity with the other
-// kernel asks for): 4.5 TB/s at 65536 tokens against 3.9 TB/s for one
-// workgroup per token.
+// tokens per workgroup, no barrier.  The wavefront does, slice by slice, what
+// the wavefronts of depth_mix_kernel do side by side: lane l owns the 4-dim
+// chunks l, l + 64, ... (slice w = the chunks of wavefront w there), every
+// slice's per-source partials are summed in the same order as
+// wave_total_lane63 sums them, and the slice totals are added in slice
+// order, so the scores, the mix and its norm are the same bits for every
+// token whichever kernel runs it (a token's result does not depend on the
+// batch).  What changes is the cost per byte: depth_mix_kernel keeps a
+// token's three wavefronts waiting on each other at two barriers and LDS
+// round trips, so at large token counts a CU holds ~8 tokens in flight; here
+// a token is one wavefront.  The kernel is bound by its VALU work, most of
+// it the per-quantity reductions, so the rows' sums are combined through
+// LDS (one lane per quantity) instead of by three row broadcasts per
+// quantity.  NCH: slices (wavefronts of the other kernel), dim <= 256 NCH.
 constexpr int kDepthWaveTokensPerGroup = 4;
 constexpr int kDepthWaveMinTokens = 4096;  // from here launch_depth_mix takes this kernel
+
+constexpr int kDepthWaveSlices = 4;  // dim <= 1024
 
 template <int NS, int NCH>
 __global__ __launch_bounds__(64 * kDepthWaveTokensPerGroup) void depth_mix_wave_kernel(
@@ -277,6 +277,11 @@ __global__ __launch_bounds__(64 * kDepthWaveTokensPerGroup) void depth_mix_wave_
     const uint16_t* __restrict__ score_w, float score_eps,
     const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
     uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm) {
+  static_assert(NCH <= kDepthWaveSlices, "dim <= 256 kDepthWaveSlices");
+  // Per wavefront: the DPP-row sums of every (slice, row, quantity).  Only
+  // the wavefront that writes them reads them (LDS operations of a
+  // wavefront complete in order): no barrier.
+  __shared__ float red_s[kDepthWaveTokensPerGroup][kDepthWaveSlices][4][2 * kMaxDepthSources];
   const uint16_t* sp[kMaxDepthSources];
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = srcs.src[s];
@@ -310,10 +315,13 @@ __global__ __launch_bounds__(64 * kDepthWaveTokensPerGroup) void depth_mix_wave_
     g_out[w] = reinterpret_cast<const uint2*>(out_norm != nullptr ? out_w : score_w)[ic[w]];
   }
   // Per slice: the chunk's partials (depth_mix_chunk's products and sums),
-  // reduced to lane 63, read as a wave-uniform value, added in slice order.
-  float sst[NS], dqt[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) sst[s] = dqt[s] = 0.0f;
+  // each summed over its 16-lane DPP row by wave_total_lane63's first four
+  // steps (row_sum: every lane of row r then holds the row's sum r_r); lane 0
+  // of each row stores its row sums in LDS.  Lane 2s (+1) then adds, per
+  // slice, ((r_0 + r_1) + r_2) + r_3 -- lane 63's total of
+  // wave_total_lane63, whose three row broadcasts cost three instructions
+  // each per quantity -- and the slice totals in slice order.
+  float (&red)[kDepthWaveSlices][4][2 * kMaxDepthSources] = red_s[threadIdx.x >> 6];
 #pragma unroll
   for (int w = 0; w < NCH; ++w) {
 #pragma unroll
@@ -326,15 +334,30 @@ __global__ __launch_bounds__(64 * kDepthWaveTokensPerGroup) void depth_mix_wave_
       wq[2] = lo_bf16(q[w].y) * lo_bf16(g[w].y);
       wq[3] = hi_bf16(q[w].y) * hi_bf16(g[w].y);
     }
+    float rs[2 * kMaxDepthSources];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const float e0 = lo_bf16(v[w][s].x), e1 = hi_bf16(v[w][s].x);
       const float e2 = lo_bf16(v[w][s].y), e3 = hi_bf16(v[w][s].y);
-      const float ss = wave_total_lane63(e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3);
-      const float dq = wave_total_lane63(e0 * wq[0] + e1 * wq[1] + e2 * wq[2] + e3 * wq[3]);
-      sst[s] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 63));
-      dqt[s] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dq), 63));
+      rs[2 * s] = row_sum(e0 * e0 + e1 * e1 + e2 * e2 + e3 * e3);
+      rs[2 * s + 1] = row_sum(e0 * wq[0] + e1 * wq[1] + e2 * wq[2] + e3 * wq[3]);
     }
+    if ((lane & 15) == 0) {
+#pragma unroll
+      for (int i = 0; i < 2 * NS; ++i) red[w][lane >> 4][i] = rs[i];
+    }
+  }
+  float tot = 0.0f;
+  if (lane < 2 * NS) {
+#pragma unroll
+    for (int w = 0; w < NCH; ++w)
+      tot += ((red[w][0][lane] + red[w][1][lane]) + red[w][2][lane]) + red[w][3][lane];
+  }
+  float sst[NS], dqt[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    sst[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 2 * s));
+    dqt[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 2 * s + 1));
   }
   float score[NS];
   float mx = -INFINITY;
