@@ -10,9 +10,9 @@
 // wavefront w owns the 4 consecutive dims of chunk i = 64 w + l (`has` when
 // i < dim / 4).  Wavefronts past `waves` of a larger workgroup take part in
 // the barriers with has == false.  Per-source sums (squares and query dot)
-// are wavefront sums combined across the wavefronts through LDS in
-// wavefront order, so every wavefront derives the same scores; the output
-// norm's sum of squares likewise.
+// are wavefront sums (in wave_total_lane63's order) combined across the
+// wavefronts through LDS in wavefront order, so every wavefront derives the
+// same scores; the output norm's sum of squares likewise.
 #pragma once
 #include <type_traits>
 
@@ -40,8 +40,9 @@ __device__ __forceinline__ float wave_total_lane63(float v) {
   return v;
 }
 
-struct __attribute__((aligned(8))) DepthMixLds {
-  float part[kDepthMaxWaves][2 * kMaxDepthSources];
+struct __attribute__((aligned(16))) DepthMixLds {
+  // Per (wavefront, DPP row): the row sums of every per-source quantity.
+  float rows[kDepthMaxWaves][4][2 * kMaxDepthSources];
   float part_out[kDepthMaxWaves];
 };
 
@@ -63,7 +64,9 @@ __device__ __forceinline__ uint2 depth_mix_chunk(const uint2 (&v)[kMaxDepthSourc
     wq[3] = hi_bf16(q.y) * hi_bf16(g.y);
   }
 
-  // Per-source partial sums, all wavefront reductions back to back.
+  // Per-source partial sums, each summed over its 16-lane DPP row by
+  // wave_total_lane63's first four steps (row_sum: every lane of row r then
+  // holds the row's sum r_r); lane 0 of each row stores the row sums.
   float ss[NS], dq[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
@@ -74,34 +77,37 @@ __device__ __forceinline__ uint2 depth_mix_chunk(const uint2 (&v)[kMaxDepthSourc
   }
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    ss[s] = wave_total_lane63(ss[s]);
-    dq[s] = wave_total_lane63(dq[s]);
+    ss[s] = row_sum(ss[s]);
+    dq[s] = row_sum(dq[s]);
   }
-  if (lane == 63) {
+  if ((lane & 15) == 0) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      sh.part[wave][2 * s] = ss[s];
-      sh.part[wave][2 * s + 1] = dq[s];
+      sh.rows[wave][lane >> 4][2 * s] = ss[s];
+      sh.rows[wave][lane >> 4][2 * s + 1] = dq[s];
     }
   }
   __syncthreads();
 
-  // Cross-wavefront sums in wavefront order.  The loop bounds are
-  // compile-time (uniform guards inside), so each wavefront row's LDS reads
-  // go out together instead of one read, wait and add at a time.
+  // Lane 2s (+1) of every wavefront adds, per wavefront, ((r_0 + r_1) + r_2)
+  // + r_3 (the wavefront total of wave_total_lane63, whose three row
+  // broadcasts would cost three instructions per quantity), then the
+  // wavefront totals in wavefront order; the totals are read back as
+  // wave-uniform values.  The loop bounds are compile-time (uniform guards
+  // inside), so the LDS reads go out together.
+  float tot = 0.0f;
+  if (lane < 2 * NS) {
+#pragma unroll
+    for (int w = 0; w < kDepthMaxWaves; ++w)
+      if (w < waves)
+        tot += ((sh.rows[w][0][lane] + sh.rows[w][1][lane]) + sh.rows[w][2][lane]) +
+               sh.rows[w][3][lane];
+  }
   float sst[NS], dqt[NS];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) sst[s] = dqt[s] = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kDepthMaxWaves; ++w) {
-    if (w < waves) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const float2 pv = *reinterpret_cast<const float2*>(&sh.part[w][2 * s]);
-        sst[s] += pv.x;
-        dqt[s] += pv.y;
-      }
-    }
+  for (int s = 0; s < NS; ++s) {
+    sst[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 2 * s));
+    dqt[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 2 * s + 1));
   }
   float score[NS];
   float mx = -INFINITY;

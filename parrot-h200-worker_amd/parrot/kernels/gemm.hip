@@ -54,7 +54,6 @@ struct GemmArgs {
   const int32_t* sorted;
   // Tile order (streaming kernel): 0 = the grid's own (XCD x gets column tile
   // x of every row tile), 1 = row-major per XCD (every column tile of row
-  // tiles x, x + 8, ...), 2 = column-stable per XCD (every row tile of column
   // tiles x, x + 8, ...); see xcd_tile.
   int rows_per_xcd;
 };
@@ -69,31 +68,13 @@ struct TileIndex {
   int m, n;
 };
 
-// With order 2 (column-stable), XCD x takes every row tile of column tiles
-// x, x + 8, ... in turn, so each column slice of an expert's weights is read
-// into one L2 only, however many row tiles the expert has; when the column
-// tiles are 8 a + 4 (the down projection's 12 at dim 768), the last four are
-// shared by XCD pairs x, x + 4, which take their even and odd row tiles
-// (the grid's row count is then even).  Order 0 gives XCD x column tile
-// (12 m + x) mod 8 of row tile m: consecutive row tiles of one expert land
-// on different XCDs and each fetches the expert's weights.
-__device__ __forceinline__ TileIndex xcd_tile(int order) {
-  if (order == 0) return TileIndex{static_cast<int>(blockIdx.y), static_cast<int>(blockIdx.x)};
+__device__ __forceinline__ TileIndex xcd_tile(bool rows_per_xcd) {
+  if (!rows_per_xcd) return TileIndex{static_cast<int>(blockIdx.y), static_cast<int>(blockIdx.x)};
   const int nx = static_cast<int>(gridDim.x);
   const int id = static_cast<int>(blockIdx.y) * nx + static_cast<int>(blockIdx.x);
   const int pos = id >> 3;
-  const int x = id & 7;
-  if (order == 1) {
-    const int q = pos / nx;
-    return TileIndex{q * 8 + x, pos - q * nx};
-  }
-  const int rows = static_cast<int>(gridDim.y);
-  const int full = (nx >> 3) * rows;  // slots of the XCD's own column tiles
-  if (pos < full) {
-    const int j = pos / rows;
-    return TileIndex{pos - j * rows, x + 8 * j};
-  }
-  return TileIndex{2 * (pos - full) + (x >> 2), (nx & ~7) + (x & 3)};
+  const int q = pos / nx;
+  return TileIndex{q * 8 + (id & 7), pos - q * nx};
 }
 
 // Every kernel argument a GEMM prologue reads (and the grid width), in one
@@ -1021,7 +1002,7 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
   // table (uniform per launch).
   const bool from_blocks = PHASE == 1 && p.route_blocks != nullptr;
   const bool self_grouped = PHASE == 1 && (p.indices != nullptr || from_blocks);
-  const TileIndex ti = xcd_tile(p.rows_per_xcd);
+  const TileIndex ti = xcd_tile(p.rows_per_xcd != 0);
   Tile t;
   GroupIds gids;
   if (self_grouped) {
@@ -1252,9 +1233,7 @@ hipError_t launch_stream(int phase, const GemmArgs& args, int n_max, hipStream_t
   const int T = static_cast<int>(args.tokens);
   const int m_tiles = (T + BM - 1) / BM + (2 * T) / BM + args.experts;
   const dim3 grid((n_max + 4 * WN - 1) / (4 * WN),
-                  args.rows_per_xcd == 1 ? (m_tiles + 7) / 8 * 8
-                  : args.rows_per_xcd == 2 ? (m_tiles + 1) / 2 * 2
-                                           : m_tiles);
+                  args.rows_per_xcd ? (m_tiles + 7) / 8 * 8 : m_tiles);
   if (phase == 1) grouped_gemm_stream_kernel<BM, 32, PF, 1, KCH><<<grid, 256, 0, s>>>(args);
   else grouped_gemm_stream_kernel<BM, WN, PF, 2, KCH><<<grid, 256, 0, s>>>(args);
   return hipGetLastError();
@@ -1357,13 +1336,8 @@ TilePlan experts_tile_plan(int phase, int64_t tokens, int experts) {
 // hidden rows) measured no better row-major and keeps the grid order.
 constexpr int64_t kXcdRowsABytes = int64_t{2} << 20;
 
-// Down: column-stable (order 2) when its 64-column tiles are 8 a or 8 a + 4
-// per row (dim 768: 12), so an expert's down weights are fetched into one
-// L2 per column slice instead of one per row tile of the expert.
 int stream_rows_per_xcd(int phase, int64_t tokens, int dim, int, int, int) {
-  if (phase == 1) return tokens * dim * 2 > kXcdRowsABytes ? 1 : 0;
-  const int nx = (dim + 63) / 64;
-  return nx >= 8 && (nx % 8 == 0 || nx % 8 == 4) ? 2 : 0;
+  return phase == 1 && tokens * dim * 2 > kXcdRowsABytes ? 1 : 0;
 }
 
 }  // namespace
