@@ -60,9 +60,6 @@ def parse_args():
     p.add_argument("--skip-decode", action="store_true")
     p.add_argument("--sweep-only", action="store_true",
                    help="only the token-count sweep of the per-kernel timings (one JSON line)")
-    p.add_argument("--traffic-workload", action="store_true",
-                   help="only launch the dispatches the two rocprofv3 --pmc passes count: the "
-                        "dominant kernel at the in-model shape and a calibration copy")
     p.add_argument("--pmc-workload", action="store_true",
                    help="only launch the counter workload: every hot-path kernel at C2, C3, "
                         "the C4 layer and T=65536, segments separated by a 16-byte marker copy")
@@ -75,9 +72,6 @@ def parse_args():
     p.add_argument("--summarize-trace", metavar="TRACE_DIR",
                    help="(no GPU) per-kernel durations of a rocprofv3 --kernel-trace run of "
                         "bench.py into profiles/kernel_trace_bench.json")
-    p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                   help="(no GPU) turn the counter CSVs of the FETCH_SIZE and WRITE_SIZE "
-                        "passes into the traffic summary under profiles/")
     return p.parse_args()
 
 
@@ -692,116 +686,25 @@ def cpu_layer_baselines(seconds: float) -> dict:
 
 
 # ---------------------------------------------------------------------------
-# HBM traffic of the dominant kernel (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)
+# HBM traffic of the dominant kernel, from the counter passes below
 # ---------------------------------------------------------------------------
 
-TRAFFIC_FILE = ROOT / "profiles" / "experts_gate_up_C4_traffic.json"
 TRAFFIC_KERNEL = "grouped_gemm_stream_kernel<32, 32, 4, 1, 1>"
-TRAFFIC_LAUNCHES = 20
-CALIBRATION_ELEMS = 1 << 27       # bf16: 256 MiB read + 256 MiB written per launch
-CALIBRATION_LAUNCHES = 5
-TRAFFIC_COMMANDS = [
-    "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc_fetch -o traffic "
-    "-- python3 bench.py --traffic-workload",
-    "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc_write -o traffic "
-    "-- python3 bench.py --traffic-workload",
-    "python3 bench.py --summarize-traffic gpurun_out/pmc_fetch gpurun_out/pmc_write",
-]
-
-
-def traffic_workload() -> None:
-    """The dispatches the two --pmc passes count: the model forward that
-    captures block 0's MoE input, then TRAFFIC_LAUNCHES launches of the
-    experts gate/up kernel on it in the forward's form, grouping the top-2
-    ids in-kernel (the last TRAFFIC_LAUNCHES dispatches named
-    TRAFFIC_KERNEL), then CALIBRATION_LAUNCHES of torch's `neg` over a bf16
-    tensor of CALIBRATION_ELEMS elements: a plain streaming kernel whose HBM
-    bytes are known exactly."""
-    import torch
-    model, ids, captured = build_model()
-    sb = StageBench(model.blocks[0].moe, captured["x"])
-    torch.cuda.synchronize()
-    for _ in range(TRAFFIC_LAUNCHES):
-        rc = sb.gate_up_grouping()
-        if rc:
-            raise RuntimeError(f"gate_up_grouping returned status {rc}")
-    torch.cuda.synchronize()
-    src = torch.ones(CALIBRATION_ELEMS, dtype=torch.bfloat16, device="cuda")
-    dst = torch.empty_like(src)
-    for _ in range(CALIBRATION_LAUNCHES):
-        torch.neg(src, out=dst)
-    torch.cuda.synchronize()
-    print(json.dumps({"traffic_workload": "done", "kernel": TRAFFIC_KERNEL,
-                      "launches": TRAFFIC_LAUNCHES, "calibration_launches": CALIBRATION_LAUNCHES,
-                      "experts_hit": sb.hit,
-                      "algorithmic_bytes": sb.bytes_gate_up() + sb.bytes_grouping()}), flush=True)
-
-
-def _counter_rows(directory: str, counter: str) -> list[tuple[str, float]]:
-    """(kernel name, value) per dispatch, in dispatch order, from the
-    counter_collection CSVs rocprofv3 wrote under `directory`."""
-    import csv
-    rows = []
-    for path in sorted(Path(directory).rglob("*counter_collection.csv")):
-        with open(path, newline="") as f:
-            for r in csv.DictReader(f):
-                if r.get("Counter_Name") != counter:
-                    continue
-                key = int(r.get("Dispatch_Id") or r.get("Correlation_Id") or len(rows))
-                rows.append((key, r["Kernel_Name"], float(r["Counter_Value"])))
-    rows.sort()
-    return [(name, value) for _, name, value in rows]
-
-
-def summarize_traffic(fetch_dir: str, write_dir: str) -> dict:
-    def per_launch(directory, counter):
-        rows = _counter_rows(directory, counter)
-        gemm = [v for n, v in rows if TRAFFIC_KERNEL in n][-TRAFFIC_LAUNCHES:]
-        copy = [v for n, v in rows if "neg" in n][-CALIBRATION_LAUNCHES:]
-        if len(gemm) < TRAFFIC_LAUNCHES or len(copy) < CALIBRATION_LAUNCHES:
-            raise SystemExit(f"{directory}: found {len(gemm)} {TRAFFIC_KERNEL} and {len(copy)} "
-                             f"calibration dispatches of {counter}")
-        return statistics.median(gemm), statistics.median(copy)
-
-    copy_kib = CALIBRATION_ELEMS * 2 / 1024
-    fetch_gemm, fetch_copy = per_launch(fetch_dir, "FETCH_SIZE")
-    write_gemm, write_copy = per_launch(write_dir, "WRITE_SIZE")
-    fetch_scale, write_scale = copy_kib / fetch_copy, copy_kib / write_copy
-    summary = {
-        "kernel": TRAFFIC_KERNEL,
-        "workload": "experts gate/up + SwiGLU, block 0's MoE input of the bs1x512 forward "
-                    "(seed 2), T=512 E=16",
-        "unit": "KiB per dispatch (median)",
-        "fetch_kib": round(fetch_gemm, 1), "write_kib": round(write_gemm, 1),
-        "calibration": {"kernel": "torch.neg, bf16, %d elements" % CALIBRATION_ELEMS,
-                        "bytes_each_way_kib": copy_kib, "fetch_kib": round(fetch_copy, 1),
-                        "write_kib": round(write_copy, 1)},
-        "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
-        "traffic_bytes": int(round((fetch_gemm * fetch_scale + write_gemm * write_scale) * 1024)),
-        "commands": TRAFFIC_COMMANDS,
-    }
-    TRAFFIC_FILE.write_text(json.dumps(summary, indent=1) + "\n")
-    return summary
-
-
 TRAFFIC_SEGMENT = "C4_layer_T512_E16: gate/up grouping in-kernel"
+CALIBRATION_ELEMS = 1 << 27       # bf16: 256 MiB read + 256 MiB written per launch
 
 
 def load_traffic() -> int | None:
-    """HBM bytes per launch of the roofline kernel: from the committed
-    counter summary of every hot-path kernel, else from the older
-    two-pass traffic file."""
+    """HBM bytes per launch of the roofline kernel, from the committed
+    counter summary of every hot-path kernel."""
     counters = load_json(PMC_FILE)
     if counters and TRAFFIC_SEGMENT in counters.get("segments", {}):
         return counters["segments"][TRAFFIC_SEGMENT]["hbm_bytes"]
-    summary = load_json(TRAFFIC_FILE)
-    if not summary:
-        return None
-    return summary.get("traffic_bytes") if summary.get("kernel") == TRAFFIC_KERNEL else None
+    return None
 
 
 # ---------------------------------------------------------------------------
-# Counter evidence for every hot-path kernel (two rocprofv3 --pmc passes)
+# Counter evidence for every hot-path kernel (three rocprofv3 --pmc passes)
 # ---------------------------------------------------------------------------
 
 PMC_FILE = ROOT / "profiles" / "counters_hot_path.json"
@@ -881,9 +784,9 @@ def pmc_workload() -> None:
     manifest[-1]["flops"] = loop_flops.value
     for cfg, sb in benches.items():
         segment(f"{cfg}: route + grouping", sb.route, sb.bytes_route())
+        segment(f"{cfg}: route top-2", sb.route_top2,
+                sb.T * sb.dim * 2 + sb.E * sb.dim * 2 + sb.T * 2 * (8 + 4))
         if sb.in_kernel:
-            segment(f"{cfg}: route top-2", sb.route_top2,
-                    sb.T * sb.dim * 2 + sb.E * sb.dim * 2 + sb.T * 2 * (8 + 4))
             segment(f"{cfg}: gate/up grouping in-kernel", sb.gate_up_grouping,
                     sb.bytes_gate_up() + sb.bytes_grouping(), sb.flops_gate_up())
             segment(f"{cfg}: down (in-kernel grouping)", sb.down_sorted,
@@ -965,7 +868,7 @@ def summarize_pmc(dir_a: str, dir_b: str, dir_c: str | None = None) -> dict:
         ns = sum(r["ns"] for r in a) / PMC_REPEATS
         fetch = per_launch(a, "FETCH_SIZE") * fetch_scale * 1024
         write = per_launch(b, "WRITE_SIZE") * write_scale * 1024
-        e = {"kernels": sorted({r["kernel"].split("(")[0][:120] for r in a}),
+        e = {"kernels": sorted({_short_kernel(r["kernel"]) for r in a}),
              "us_under_pmc": round(ns / 1e3, 3),
              "fetch_bytes": int(fetch), "write_bytes": int(write),
              "hbm_bytes": int(fetch + write),
@@ -1054,7 +957,8 @@ def summarize_trace(directory: str) -> dict:
                               "total_us": round(sum(v) / 1e3, 1)}
                     for n, v in sorted(stats.items(), key=lambda kv: -sum(kv[1]))[:40]},
         "command": "rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/bench_trace -o bench "
-                   "-- python3 bench.py; python3 bench.py --summarize-trace gpurun_out/bench_trace",
+                   "-- python3 bench.py --skip-cpu-baseline --skip-decode; "
+                   "python3 bench.py --summarize-trace gpurun_out/bench_trace",
     }
     TRACE_FILE.write_text(json.dumps(summary, indent=1) + "\n")
     return summary
@@ -1218,9 +1122,6 @@ def build_model():
 
 def main():
     args = parse_args()
-    if args.summarize_traffic:
-        print(json.dumps(summarize_traffic(*args.summarize_traffic)))
-        return
     if args.summarize_pmc:
         print(json.dumps(summarize_pmc(*args.summarize_pmc))[:2000])
         return
@@ -1236,9 +1137,6 @@ def main():
               f"WORLD_SIZE={world}); the MoE hot path has no multi-GPU implementation and "
               "every GPU box here has a single MI355X.", file=sys.stderr)
         sys.exit(2)
-    if args.traffic_workload:
-        traffic_workload()
-        return
     if args.pmc_workload:
         pmc_workload()
         return
@@ -1329,9 +1227,7 @@ def main():
                     "warm_event_us": warm["us"], "warm_frac": warm["hbm_frac"],
                     "attained_peak": peaks["copy_gbps"],
                     "frac_of_attained": round(gu["gbps"] / peaks["copy_gbps"], 4),
-                    "traffic_source": (str(PMC_FILE.relative_to(ROOT)) if load_json(PMC_FILE)
-                                       else str(TRAFFIC_FILE.relative_to(ROOT))) if traffic
-                    else None}
+                    "traffic_source": str(PMC_FILE.relative_to(ROOT)) if traffic else None}
         trace = load_json(TRACE_FILE)
         if trace and trace.get("roofline_kernel") == TRAFFIC_KERNEL and trace.get("loop_mean_us"):
             # The committed kernel trace of this command: the same loop's mean
