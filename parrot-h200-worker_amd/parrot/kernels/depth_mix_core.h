@@ -46,6 +46,36 @@ struct __attribute__((aligned(16))) DepthMixLds {
   float part_out[kDepthMaxWaves];
 };
 
+// The mixing weights alpha_s (wave-uniform) from the per-quantity totals in
+// lanes 0 .. 2 NS - 1 (lane 2s: source s's sum of squares, lane 2s + 1: its
+// query dot): score_s = dot_s * rsqrt(ss_s / dim + eps), alpha = softmax over
+// the sources in order.  Lane 2s evaluates its own score and exponential (one
+// division, one rsqrt and one exp per lane instead of one per source in
+// every lane); the maximum and the denominator are taken over the scores
+// read back in source order, so every value is what the per-source loop
+//   mx = max_s score_s; denom = sum_s exp(score_s - mx); alpha_s =
+//   exp(score_s - mx) / denom (as exp(...) * (1 / denom))
+// gives, bit for bit.
+template <int NS>
+__device__ __forceinline__ void depth_mix_weights(float tot, int dim, float score_eps,
+                                                  float (&alpha)[NS]) {
+  const float dot = dpp<0xb1>(tot);  // lane 2s: lane 2s + 1's total
+  const float score = dot * rsqrtf(tot / static_cast<float>(dim) + score_eps);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score), 2 * s)));
+  const float e = __expf(score - mx);
+  float denom = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 2 * s));
+  const float a = e * (1.0f / denom);
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    alpha[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 2 * s));
+}
+
 // The mix of this lane's chunk as packed bf16 over NS sources (a compile-time
 // count: the loops below then hold only the sources read, which at one to
 // five sources halves the instructions of a runtime count with guards).
@@ -103,32 +133,16 @@ __device__ __forceinline__ uint2 depth_mix_chunk(const uint2 (&v)[kMaxDepthSourc
         tot += ((sh.rows[w][0][lane] + sh.rows[w][1][lane]) + sh.rows[w][2][lane]) +
                sh.rows[w][3][lane];
   }
-  float sst[NS], dqt[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    sst[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 2 * s));
-    dqt[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 2 * s + 1));
-  }
-  float score[NS];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    score[s] = dqt[s] * rsqrtf(sst[s] / static_cast<float>(dim) + score_eps);
-    mx = fmaxf(mx, score[s]);
-  }
-  float denom = 0.0f;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) denom += __expf(score[s] - mx);
-  const float inv = 1.0f / denom;
+  float alpha[NS];
+  depth_mix_weights<NS>(tot, dim, score_eps, alpha);
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    const float a = __expf(score[s] - mx) * inv;
-    acc[0] += a * lo_bf16(v[s].x);
-    acc[1] += a * hi_bf16(v[s].x);
-    acc[2] += a * lo_bf16(v[s].y);
-    acc[3] += a * hi_bf16(v[s].y);
+    acc[0] += alpha[s] * lo_bf16(v[s].x);
+    acc[1] += alpha[s] * hi_bf16(v[s].x);
+    acc[2] += alpha[s] * lo_bf16(v[s].y);
+    acc[3] += alpha[s] * hi_bf16(v[s].y);
   }
   uint2 mixed;
   mixed.x = pack_bf16x2(acc[0], acc[1]);

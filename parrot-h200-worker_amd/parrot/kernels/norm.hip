@@ -282,6 +282,7 @@ __global__ __launch_bounds__(64 * kDepthWaveTokensPerGroup) void depth_mix_wave_
   // the wavefront that writes them reads them (LDS operations of a
   // wavefront complete in order): no barrier.
   __shared__ float red_s[kDepthWaveTokensPerGroup][kDepthWaveSlices][4][2 * kMaxDepthSources];
+  __shared__ float red_out_s[kDepthWaveTokensPerGroup][kDepthWaveSlices][4];
   const uint16_t* sp[kMaxDepthSources];
 #pragma unroll
   for (int s = 0; s < kMaxDepthSources; ++s) sp[s] = srcs.src[s];
@@ -353,28 +354,10 @@ __global__ __launch_bounds__(64 * kDepthWaveTokensPerGroup) void depth_mix_wave_
     for (int w = 0; w < NCH; ++w)
       tot += ((red[w][0][lane] + red[w][1][lane]) + red[w][2][lane]) + red[w][3][lane];
   }
-  float sst[NS], dqt[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    sst[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 2 * s));
-    dqt[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 2 * s + 1));
-  }
-  float score[NS];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    score[s] = dqt[s] * rsqrtf(sst[s] / static_cast<float>(dim) + score_eps);
-    mx = fmaxf(mx, score[s]);
-  }
-  float denom = 0.0f;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) denom += __expf(score[s] - mx);
-  const float inv = 1.0f / denom;
   float alpha[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) alpha[s] = __expf(score[s] - mx) * inv;
+  depth_mix_weights<NS>(tot, dim, score_eps, alpha);
   uint2 mixed[NCH];
-  float sso_total = 0.0f;
+  float (&red_out)[kDepthWaveSlices][4] = red_out_s[threadIdx.x >> 6];
 #pragma unroll
   for (int w = 0; w < NCH; ++w) {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -390,15 +373,24 @@ __global__ __launch_bounds__(64 * kDepthWaveTokensPerGroup) void depth_mix_wave_
     if (out_mix != nullptr && has[w])
       reinterpret_cast<uint2*>(out_mix)[base + w * kWave + lane] = mixed[w];
     if (out_norm != nullptr) {
+      // The output norm's sum of squares: per slice, row sums to LDS as
+      // above, combined below in depth_mix_norm_chunk's order.
       const float r0 = lo_bf16(mixed[w].x), r1 = hi_bf16(mixed[w].x);
       const float r2 = lo_bf16(mixed[w].y), r3 = hi_bf16(mixed[w].y);
-      const float sso =
-          wave_total_lane63(has[w] ? r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3 : 0.0f);
-      const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sso), 63));
-      sso_total = w == 0 ? t : sso_total + t;
+      const float sso = row_sum(has[w] ? r0 * r0 + r1 * r1 + r2 * r2 + r3 * r3 : 0.0f);
+      if ((lane & 15) == 0) red_out[w][lane >> 4] = sso;
     }
   }
   if (out_norm == nullptr) return;
+  float sso_total = 0.0f;
+  if (lane == 0) {
+#pragma unroll
+    for (int w = 0; w < NCH; ++w) {
+      const float t = ((red_out[w][0] + red_out[w][1]) + red_out[w][2]) + red_out[w][3];
+      sso_total = w == 0 ? t : sso_total + t;
+    }
+  }
+  sso_total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sso_total), 0));
   const float r = rsqrtf(sso_total / static_cast<float>(dim) + out_eps);
 #pragma unroll
   for (int w = 0; w < NCH; ++w) {
