@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
     o.x = pack_bf16x2(lo_bf16(p.x) + lo_bf16(o.x), hi_bf16(p.x) + hi_bf16(o.x));
     o.y = pack_bf16x2(lo_bf16(p.y) + lo_bf16(o.y), hi_bf16(p.y) + hi_bf16(o.y));
   }
-  out[i] = o;
+  store_stream(out + i, o);
 }
 
 }  // namespace

@@ -26,6 +26,16 @@ constexpr uint32_t kNoExpert = 0xff;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// A streaming store of 4 bf16: the nt hint keeps a long output's lines from
+// displacing cached inputs and lets HBM take the writes in larger bursts.
+__device__ __forceinline__ void store_stream(uint2* dst, uint2 v) {
+  u32x2 t;
+  t.x = v.x;
+  t.y = v.y;
+  __builtin_nontemporal_store(t, reinterpret_cast<u32x2*>(dst));
+}
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);

@@ -371,7 +371,7 @@ __global__ __launch_bounds__(64 * kDepthWaveTokensPerGroup) void depth_mix_wave_
     mixed[w].x = pack_bf16x2(acc[0], acc[1]);
     mixed[w].y = pack_bf16x2(acc[2], acc[3]);
     if (out_mix != nullptr && has[w])
-      reinterpret_cast<uint2*>(out_mix)[base + w * kWave + lane] = mixed[w];
+      store_stream(reinterpret_cast<uint2*>(out_mix) + base + w * kWave + lane, mixed[w]);
     if (out_norm != nullptr) {
       // The output norm's sum of squares: per slice, row sums to LDS as
       // above, combined below in depth_mix_norm_chunk's order.
@@ -400,7 +400,7 @@ __global__ __launch_bounds__(64 * kDepthWaveTokensPerGroup) void depth_mix_wave_
     uint2 o;
     o.x = pack_bf16x2(r0 * r * lo_bf16(g_out[w].x), r1 * r * hi_bf16(g_out[w].x));
     o.y = pack_bf16x2(r2 * r * lo_bf16(g_out[w].y), r3 * r * hi_bf16(g_out[w].y));
-    reinterpret_cast<uint2*>(out_norm)[base + w * kWave + lane] = o;
+    store_stream(reinterpret_cast<uint2*>(out_norm) + base + w * kWave + lane, o);
   }
 }
 
