@@ -251,7 +251,7 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   }
 }
 
-// The depth mix at large token counts: one wavefront per token, four
+// The depth mix at large token counts: one wavefront per token, two
 // tokens per workgroup, no barrier.  The wavefront does, slice by slice, what
 // the wavefronts of depth_mix_kernel do side by side: lane l owns the 4-dim
 // chunks l, l + 64, ... (slice w = the chunks of wavefront w there), every
@@ -265,8 +265,10 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
 // a token is one wavefront.  The kernel is bound by its VALU work, most of
 // it the per-quantity reductions, so the rows' sums are combined through
 // LDS (one lane per quantity) instead of by three row broadcasts per
-// quantity.  NCH: slices (wavefronts of the other kernel), dim <= 256 NCH.
-constexpr int kDepthWaveTokensPerGroup = 4;
+// quantity.  Two tokens per workgroup measured 1-3 % faster than one or
+// four at 65536 tokens (MI355X, sources read from HBM), eight 13 % slower.
+// NCH: slices (wavefronts of the other kernel), dim <= 256 NCH.
+constexpr int kDepthWaveTokensPerGroup = 2;
 constexpr int kDepthWaveMinTokens = 4096;  // from here launch_depth_mix takes this kernel
 
 constexpr int kDepthWaveSlices = 4;  // dim <= 1024
