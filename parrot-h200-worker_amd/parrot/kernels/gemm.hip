@@ -710,6 +710,11 @@ void grouped_gemm_kernel(GemmArgs p) {
 // on MI355X, that MFMA keeps 92 % of the bf16 peak issuing from one
 // wavefront per SIMD where 16x16x32 keeps 70 %, and a 64 x 64 wavefront
 // tile reads 4 fragments from LDS per 4 MFMAs of 32 K flops each.
+// WAVES_M x WAVES_N wavefronts share the tile: 2 x 2 for 128 x 128 tiles
+// (64 x 64 per wavefront), 2 x 4 for 256 x 256 ones (128 x 64 per wavefront:
+// 6 fragment reads per 8 MFMAs, and half the stage bytes per flop, at one
+// workgroup per CU).  The 256 x 256 tile's route weights go through LDS:
+// its 128 accumulators per lane leave no registers for them.
 //
 // 32x32x16 operands: lane l holds row (or column) l % 32, k 8 (l / 32) .. +7
 // of a 16-wide k step.  In the 16 x 32 fragment-order blocks that is block
@@ -719,24 +724,31 @@ void grouped_gemm_kernel(GemmArgs p) {
 // 8 (e / 4) + 4 (l / 32) + e % 4 of element e.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int BM, int BN, int BK, int S, int PHASE>
-__global__ __launch_bounds__(256)
+template <int BM, int BN, int BK, int S, int PHASE, int WAVES_M = 2, int WAVES_N = 2>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N)
 void grouped_gemm_wide_kernel(GemmArgs p) {
-  constexpr int kWaveM = BM / 2, kWaveN = BN / 2;       // 2 x 2 wavefronts
+  constexpr int kWaves = WAVES_M * WAVES_N;
+  constexpr int kThreads = 64 * kWaves;
+  constexpr int kWaveM = BM / WAVES_M, kWaveN = BN / WAVES_N;  // wavefront tile
   constexpr int kTilesM = kWaveM / 32, kTilesN = kWaveN / 32;
   constexpr int KH = BK / 32;                           // 32-wide k halves per stage
   constexpr int kSteps = BK / 16;                       // MFMA k steps per stage
   constexpr int kABlocks = BM / 16 * KH;                // 16-row groups x k halves
   constexpr int kBlocks = (BM + BN) / 16 * KH;
-  constexpr int P = kBlocks / 4;                        // loads per wavefront per stage
+  constexpr int P = kBlocks / kWaves;                   // loads per wavefront per stage
   constexpr int kStageElems = kBlocks * 512;
-  static_assert(kBlocks % 4 == 0 && kTilesM >= 1 && kTilesN >= 1, "tile shape");
+  static_assert(kBlocks % kWaves == 0 && kTilesM >= 1 && kTilesN >= 1, "tile shape");
+  static_assert(BM <= kThreads, "one thread per tile row sets up the row ids");
   static_assert(BK == 32 || BK == 64, "stages of one or two 32-wide k blocks");
   static_assert(S >= 2, "the ring needs at least two stages");
 
   __shared__ __attribute__((aligned(16))) uint16_t ring[S][kStageElems];
   __shared__ int row_src[BM];
   __shared__ int row_dst[BM];
+  // Route weights of the tile's rows, for wavefront tiles whose registers
+  // cannot also hold them (kRouteInLds).
+  constexpr bool kRouteInLds = kTilesM * kTilesN * 16 > 64;
+  __shared__ float row_w[kRouteInLds ? BM : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -774,6 +786,7 @@ void grouped_gemm_wide_kernel(GemmArgs p) {
     row_src[tid] = PHASE == 1 ? (shared ? sc : asg >> 1) : t.hbase + sc;
     const bool live = t.mt * BM + tid < t.rows;
     row_dst[tid] = !live ? -1 : PHASE == 1 ? t.hbase + sc : (shared ? sc : asg);
+    if (kRouteInLds && PHASE == 2) row_w[tid] = live && !shared ? p.weights[asg] : 0.0f;
   }
   __syncthreads();
 
@@ -816,7 +829,7 @@ void grouped_gemm_wide_kernel(GemmArgs p) {
   };
 
   // ---- fragment addresses (elements) within a stage, for k step u = 0 -----
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int lane_part = (lane >> 5) * 128 + (lane & 15) * 8;
   int a_frag[kTilesM], b_frag[kTilesN];
 #pragma unroll
@@ -840,8 +853,8 @@ void grouped_gemm_wide_kernel(GemmArgs p) {
 
   // Route weights of this lane's output rows (phase 2, routed): issued here,
   // they land while the k loop runs instead of stalling the epilogue.
-  float route_w[kTilesM][16];
-  if (PHASE == 2 && !shared) {
+  float route_w[kRouteInLds ? 1 : kTilesM][16];
+  if (!kRouteInLds && PHASE == 2 && !shared) {
 #pragma unroll
     for (int i = 0; i < kTilesM; ++i)
 #pragma unroll
@@ -924,7 +937,7 @@ void grouped_gemm_wide_kernel(GemmArgs p) {
     __syncthreads();
     const int h0 = n0 / 2;
     constexpr int kPieces = kHalf / 8;  // 16-byte pieces per staged row
-    for (int c = tid; c < BM * kPieces; c += 256) {
+    for (int c = tid; c < BM * kPieces; c += kThreads) {
       const int row = c / kPieces, piece = c - row * kPieces;
       const int dst = row_dst[row];
       const int h = h0 + piece * 8;
@@ -945,7 +958,9 @@ void grouped_gemm_wide_kernel(GemmArgs p) {
           const int dst = row_dst[row];
           if (dst < 0) continue;
           if (shared) p.y_shared[static_cast<int64_t>(dst) * p.dim + n] = acc[i][j][e];
-          else p.y_routed[static_cast<int64_t>(dst) * p.dim + n] = route_w[i][e] * acc[i][j][e];
+          else
+            p.y_routed[static_cast<int64_t>(dst) * p.dim + n] =
+                (kRouteInLds ? row_w[row] : route_w[kRouteInLds ? 0 : i][e]) * acc[i][j][e];
         }
       }
     }
@@ -1216,15 +1231,18 @@ hipError_t launch_phase(int phase, const GemmArgs& args, int n_max, hipStream_t 
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int S>
+template <int BM, int BN, int BK, int S, int WAVES_M = 2, int WAVES_N = 2>
 hipError_t launch_wide(int phase, const GemmArgs& args, int n_max, hipStream_t s) {
   const int T = static_cast<int>(args.tokens);
   const int m_tiles = (T + BM - 1) / BM + (2 * T) / BM + args.experts;
   // Rows of tiles rounded up to a multiple of the 8 XCDs (the kernel's tile
   // order takes every eighth row tile per XCD).
   const dim3 grid((n_max + BN - 1) / BN, (m_tiles + 7) / 8 * 8);
-  if (phase == 1) grouped_gemm_wide_kernel<BM, BN, BK, S, 1><<<grid, 256, 0, s>>>(args);
-  else grouped_gemm_wide_kernel<BM, BN, BK, S, 2><<<grid, 256, 0, s>>>(args);
+  constexpr int kThreads = 64 * WAVES_M * WAVES_N;
+  if (phase == 1)
+    grouped_gemm_wide_kernel<BM, BN, BK, S, 1, WAVES_M, WAVES_N><<<grid, kThreads, 0, s>>>(args);
+  else
+    grouped_gemm_wide_kernel<BM, BN, BK, S, 2, WAVES_M, WAVES_N><<<grid, kThreads, 0, s>>>(args);
   return hipGetLastError();
 }
 
@@ -1271,7 +1289,7 @@ hipError_t run_stream(int phase, GemmArgs args, int n_max, hipStream_t s) {
 // K fits its LDS budget (64-row tiles in two k chunks, when every K splits
 // into 128-element halves; else 32-row tiles), else the pipelined kernel
 // with 32-row tiles.
-enum class TilePlan { kStream16, kStream32, kStream64, kWide128 };
+enum class TilePlan { kStream16, kStream32, kStream64, kWide128, kWide256 };
 
 // Average rows per expert from which the wide-MFMA tiles take over, per
 // phase.  Measured on MI355X (E = 16 uniform, T = 4K ... 64K, and BASELINE
@@ -1281,6 +1299,14 @@ enum class TilePlan { kStream16, kStream32, kStream64, kWide128 };
 // tiles with 1 KB x 24 weight blocks each (wide 49.8 us vs streaming 41.2).
 constexpr int64_t kWideRowsGateUp = 512;
 constexpr int64_t kWideRowsDown = 256;
+// Down on 256 x 256 tiles (eight wavefronts, one workgroup per CU) from this
+// many rows per expert.  Measured on MI355X (E = 16, HIP events): down
+// T = 32768 171 -> 163 us, T = 65536 327 -> 305 us; T = 16384 (2048 rows per
+// expert) 75 -> 82 us.  Gate/up stays on 128 x 128 tiles: 256 x 256 measured
+// 107 -> 156 us at T = 16384 and 385 -> 498 us at T = 65536 (with one
+// workgroup per CU nothing overlaps a tile's prologue and its hidden-tile
+// epilogue).
+constexpr int64_t kWide256RowsDown = 4096;
 
 template <TilePlan PLAN>
 hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t* hidden,
@@ -1298,6 +1324,8 @@ hipError_t run_phase(int phase, GemmArgs args, const ExpertWeights& w, uint16_t*
     n_max = args.dim;
   }
   if constexpr (PLAN == TilePlan::kWide128) return launch_wide<128, 128, 32, 3>(phase, args, n_max, s);
+  if constexpr (PLAN == TilePlan::kWide256)
+    return launch_wide<256, 256, 32, 4, 2, 4>(phase, args, n_max, s);
   const int k_max = phase == 1 ? args.dim : max(args.hidden_dim, args.shared_dim);
   if (k_max > kStreamKCap) return launch_phase<32, 128, 3>(phase, args, n_max, s);
   if constexpr (PLAN == TilePlan::kStream64) {
@@ -1323,7 +1351,8 @@ TilePlan experts_tile_plan(int phase, int64_t tokens, int experts) {
   if (tokens <= 16) return TilePlan::kStream16;
   if (per_expert <= 96) return TilePlan::kStream32;
   const int64_t wide_from = phase == 1 ? kWideRowsGateUp : kWideRowsDown;
-  return per_expert < wide_from ? TilePlan::kStream64 : TilePlan::kWide128;
+  if (per_expert < wide_from) return TilePlan::kStream64;
+  return phase == 2 && per_expert >= kWide256RowsDown ? TilePlan::kWide256 : TilePlan::kWide128;
 }
 
 // Streaming-kernel tile order for gate/up: row-major per XCD once the
@@ -1395,7 +1424,8 @@ hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int 
     case TilePlan::kStream16: return run_phase<TilePlan::kStream16>(phase, args, w, hidden, s);
     case TilePlan::kStream32: return run_phase<TilePlan::kStream32>(phase, args, w, hidden, s);
     case TilePlan::kStream64: return run_phase<TilePlan::kStream64>(phase, args, w, hidden, s);
-    default: return run_phase<TilePlan::kWide128>(phase, args, w, hidden, s);
+    case TilePlan::kWide128: return run_phase<TilePlan::kWide128>(phase, args, w, hidden, s);
+    default: return run_phase<TilePlan::kWide256>(phase, args, w, hidden, s);
   }
 }
 

@@ -117,6 +117,9 @@ MOE_CASES = [
     ("C5_b8", 8, 16, False),
     ("odd", 130, 16, False),
     ("large", 16384, 16, False),
+    # 4,096 rows per expert: down on 256 x 256 tiles (gate/up on 128 x 128)
+    ("wide256", 8192, 4, False),
+    ("wide256_skew", 8192, 4, True),
 ]
 
 
