@@ -5,8 +5,12 @@ argmax disagreement between a bf16 forward and the fp32 reference.
 Rounding points of the HIP forward (each a toggle below):
   act      every activation a kernel writes in bf16: the depth-mix output and
            its RMSNorm, q / k / v (before and after RoPE), the attention
-           output, every projection output, the expert hidden rows and the
-           MoE output (parrot/kernels/moe_bf16.metal:675 for the hidden rows);
+           output, every projection output, the expert hidden rows
+           (parrot/kernels/moe_bf16.metal:675), the shared expert's output
+           and each route-weighted expert output (the rows the down
+           projection writes; parrot/metal_moe.py:407-409 rounds expert
+           outputs to bf16, parrot/model.py:550 each weighted contribution),
+           and the MoE output;
   stream   the AttnRes partial sums (partial + delta rounded to bf16);
   head_in  the final RMSNorm output fed to the vocabulary head;
   logit    the vocabulary head's output.
@@ -97,14 +101,14 @@ def _moe(o, i, h, ra, forced, capture, lin=F.linear):
                     lin(rows, o._w(name + "up.weight")))
         return lin(hidden, o._w(name + "down.weight"))
 
-    out = swiglu(flat, pre + "shared.")
+    out = ra(swiglu(flat, pre + "shared."))
     it = torch.from_numpy(idx)
     wt = torch.from_numpy(np.asarray(w, dtype=np.float32))
     for e in range(o.c.n_experts):
         rows, slots = torch.where(it == e)
         if rows.numel():
-            out = out.index_add(0, rows, swiglu(flat[rows], f"{pre}experts.{e}.") *
-                                wt[rows, slots, None])
+            out = out.index_add(0, rows, ra(swiglu(flat[rows], f"{pre}experts.{e}.") *
+                                           wt[rows, slots, None]))
     return ra(out).view_as(h)
 
 

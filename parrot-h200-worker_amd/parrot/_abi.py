@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (maps PyTorch's HIP runtime before the library)
 
 LIBRARY = Path(__file__).resolve().parent / "_lib" / "libparrot_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -133,7 +133,7 @@ SIGNATURES: dict[str, tuple] = {
          _p]),
 }
 
-STATIC_SCRATCH_BYTES = 48 << 20  # PARROT_STATIC_SCRATCH_BYTES
+STATIC_SCRATCH_BYTES = 30 << 20  # PARROT_STATIC_SCRATCH_BYTES
 
 _lib: ctypes.CDLL | None = None
 

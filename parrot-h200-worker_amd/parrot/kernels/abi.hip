@@ -44,8 +44,8 @@ int32_t* route_chunk_totals(void* workspace, int64_t tokens, int32_t experts) {
 
 struct ExpertsWorkspace {
   uint16_t* hidden;
-  float* y_routed;
-  float* y_shared;
+  uint16_t* y_routed;  // bf16 [2T, dim], route-weighted expert outputs
+  uint16_t* y_shared;  // bf16 [T, dim]
   size_t bytes;
 };
 
@@ -53,13 +53,13 @@ ExpertsWorkspace experts_ws(void* base, int64_t tokens, int32_t dim, int32_t hid
                             int32_t shared_dim) {
   const size_t hstride = static_cast<size_t>(hidden_dim > shared_dim ? hidden_dim : shared_dim);
   const size_t h_bytes = round_up(3 * static_cast<size_t>(tokens) * hstride * sizeof(uint16_t));
-  const size_t yr_bytes = round_up(2 * static_cast<size_t>(tokens) * dim * sizeof(float));
-  const size_t ys_bytes = round_up(static_cast<size_t>(tokens) * dim * sizeof(float));
+  const size_t yr_bytes = round_up(2 * static_cast<size_t>(tokens) * dim * sizeof(uint16_t));
+  const size_t ys_bytes = round_up(static_cast<size_t>(tokens) * dim * sizeof(uint16_t));
   char* p = static_cast<char*>(base);
   ExpertsWorkspace ws;
   ws.hidden = reinterpret_cast<uint16_t*>(p);
-  ws.y_routed = reinterpret_cast<float*>(p + h_bytes);
-  ws.y_shared = reinterpret_cast<float*>(p + h_bytes + yr_bytes);
+  ws.y_routed = reinterpret_cast<uint16_t*>(p + h_bytes);
+  ws.y_shared = reinterpret_cast<uint16_t*>(p + h_bytes + yr_bytes);
   ws.bytes = h_bytes + yr_bytes + ys_bytes;
   return ws;
 }

@@ -41,13 +41,22 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// IEEE round-to-nearest-even fp32 -> bf16; NaN stays NaN (quietened).
+// IEEE round-to-nearest-even fp32 -> bf16; NaN stays NaN.  gfx950's
+// v_cvt_pk_bf16_f32, first operand only: over all 2^32 fp32 patterns its low
+// half equals the integer rounding u + 0x7fff + ((u >> 16) & 1) for every
+// non-NaN input, denormals included, and keeps NaNs NaN (checked on MI355X).
+// The second operand's half rounds fp32 denormals whose discarded bits are
+// just above one half (0x00XX8001) down on this part, so the instruction is
+// written out here: two conversions the compiler merged into one packed
+// instruction would route one of them through that half.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, 0" : "=v"(r) : "v"(f));
+  return static_cast<uint16_t>(r);
 }
+
+// v rounded to bf16 (round to nearest even), as fp32.
+__device__ __forceinline__ float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_bf16(lo)) |
@@ -261,8 +270,8 @@ struct DepthSources {
 // launch_combine computes it) is produced in the kernel, written to `out`
 // and used as the last of the n_sources depth sources.
 struct CombineSource {
-  const float* y_routed;   // [2 T, dim], route weights applied
-  const float* y_shared;   // [T, dim]
+  const uint16_t* y_routed;  // bf16 [2 T, dim], route weights applied
+  const uint16_t* y_shared;  // bf16 [T, dim]
   const uint16_t* addend;  // optional [T, dim]
   uint16_t* out;           // [T, dim]
 };
@@ -362,11 +371,12 @@ GroupInKernel experts_group_in_kernel(int64_t tokens, int dim, int experts, int 
 // Grouped SwiGLU expert GEMM over every routed assignment plus the shared
 // expert.  Phase 1 (gate/up + SwiGLU) reads x and writes hidden
 // [3T, max(H, Hs)] bf16; phase 2 (down) reads hidden and writes y_routed
-// [2T, dim] fp32 (route-weighted, assignment order) and y_shared [T, dim].
+// [2T, dim] (route-weighted, assignment order) and y_shared [T, dim], each
+// value the bf16 rounding of its fp32 result.
 hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int dim,
                               int experts, int hidden_dim, int shared_dim, int capacity,
                               const GroupMap& map, const ExpertWeights& w, uint16_t* hidden,
-                              float* y_routed, float* y_shared, hipStream_t s);
+                              uint16_t* y_routed, uint16_t* y_shared, hipStream_t s);
 
 // RoPE + head-major split of a packed q|k|v projection (see rope.hip).
 // The first position is start (+ *start_device when non-null); positions
@@ -494,7 +504,7 @@ hipError_t launch_causal_attention(const uint16_t* q, const uint16_t* k, const u
                                    int kv_heads, int head_dim, int window, float scale,
                                    uint16_t* out, hipStream_t s);
 
-hipError_t launch_combine(const float* y_routed, const float* y_shared,
+hipError_t launch_combine(const uint16_t* y_routed, const uint16_t* y_shared,
                           const uint16_t* addend, int64_t tokens, int dim,
                           uint16_t* out, hipStream_t s);
 

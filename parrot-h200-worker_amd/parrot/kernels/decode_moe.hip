@@ -464,8 +464,11 @@ __global__ __launch_bounds__(256) void decode_down_kernel(
         for (int cc = 0; cc < 4; ++cc) v += part[q][wv][cc][tid];
       y[q] = v;
     }
-    // combine_kernel's order: shared, then the two weighted routed rows.
-    const float v = (y[2] + weights[2 * t] * y[0]) + weights[2 * t + 1] * y[1];
+    // combine_kernel's order and rounding points: the shared row and each
+    // weighted routed row rounded to bf16 (as the down projection writes
+    // them), then added in fp32, shared first.
+    const float v = (bf16_round(y[2]) + bf16_round(weights[2 * t] * y[0])) +
+                    bf16_round(weights[2 * t + 1] * y[1]);
     const int64_t o = static_cast<int64_t>(t) * dim + slice * 16 + tid;
     uint16_t r = f32_to_bf16(v);
     if (addend != nullptr) r = f32_to_bf16(bf16_to_f32(addend[o]) + bf16_to_f32(r));

@@ -41,8 +41,8 @@ struct GemmArgs {
   const uint16_t* w_routed;   // phase 1: [E, 2H, dim]; phase 2: [E, dim, H]
   const uint16_t* w_shared;   // phase 1: [2Hs, dim];  phase 2: [dim, Hs]
   uint16_t* hidden_out;       // phase 1 output
-  float* y_routed;            // phase 2 output [2T, dim]
-  float* y_shared;            // phase 2 output [T, dim]
+  uint16_t* y_routed;         // phase 2 output bf16 [2T, dim]
+  uint16_t* y_shared;         // phase 2 output bf16 [T, dim]
   // Grouping inside phase 1 (group_find, group_rows): top-2 ids in; counts,
   // offsets and the hidden rows' assignment ids out.  Phase 2 with `sorted`
   // reads a row's assignment id there instead of perm / overflow.
@@ -686,16 +686,15 @@ void grouped_gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < kTilesN; ++j) {
       const int n = n0 + wn0 + j * 16 + (lane & 15);
-      if (n >= N) continue;
 #pragma unroll
       for (int i = 0; i < kTilesM; ++i) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = wm0 + i * 16 + 4 * (lane >> 4) + r;
           const int dst = row_dst[row];
-          if (dst < 0) continue;
-          if (shared) p.y_shared[static_cast<int64_t>(dst) * p.dim + n] = acc[i][j][r];
-          else p.y_routed[static_cast<int64_t>(dst) * p.dim + n] = p.weights[dst] * acc[i][j][r];
+          const int64_t at = static_cast<int64_t>(max(dst, 0)) * p.dim + n;
+          const float v = shared ? acc[i][j][r] : p.weights[max(dst, 0)] * acc[i][j][r];
+          if (dst >= 0 && n < N) (shared ? p.y_shared : p.y_routed)[at] = f32_to_bf16(v);
         }
       }
     }
@@ -949,18 +948,17 @@ void grouped_gemm_wide_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < kTilesN; ++j) {
       const int n = n0 + wn * kWaveN + 32 * j + (lane & 31);
-      if (n >= N) continue;
 #pragma unroll
       for (int i = 0; i < kTilesM; ++i) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int row = wm0 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
           const int dst = row_dst[row];
-          if (dst < 0) continue;
-          if (shared) p.y_shared[static_cast<int64_t>(dst) * p.dim + n] = acc[i][j][e];
-          else
-            p.y_routed[static_cast<int64_t>(dst) * p.dim + n] =
-                (kRouteInLds ? row_w[row] : route_w[kRouteInLds ? 0 : i][e]) * acc[i][j][e];
+          const int64_t at = static_cast<int64_t>(max(dst, 0)) * p.dim + n;
+          const float w = shared ? 1.0f
+                                 : (kRouteInLds ? row_w[row] : route_w[kRouteInLds ? 0 : i][e]);
+          const float v = shared ? acc[i][j][e] : w * acc[i][j][e];
+          if (dst >= 0 && n < N) (shared ? p.y_shared : p.y_routed)[at] = f32_to_bf16(v);
         }
       }
     }
@@ -1206,15 +1204,14 @@ void grouped_gemm_stream_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < kTilesN; ++j) {
       const int n = n0 + wave * WN + j * 16 + (lane & 15);
-      if (n >= N) continue;
 #pragma unroll
       for (int mi = 0; mi < kTilesM; ++mi) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int dst = dst_row[mi][r];
-          if (dst < 0) continue;
-          if (shared) p.y_shared[static_cast<int64_t>(dst) * p.dim + n] = acc[mi][j][r];
-          else p.y_routed[static_cast<int64_t>(dst) * p.dim + n] = route_w[mi][r] * acc[mi][j][r];
+          const int64_t at = static_cast<int64_t>(max(dst, 0)) * p.dim + n;
+          const float v = shared ? acc[mi][j][r] : route_w[mi][r] * acc[mi][j][r];
+          if (dst >= 0 && n < N) (shared ? p.y_shared : p.y_routed)[at] = f32_to_bf16(v);
         }
       }
     }
@@ -1389,7 +1386,7 @@ GroupInKernel experts_group_in_kernel(int64_t tokens, int dim, int experts, int 
 hipError_t launch_expert_gemm(int phase, const uint16_t* x, int64_t tokens, int dim,
                               int experts, int hidden_dim, int shared_dim, int capacity,
                               const GroupMap& map, const ExpertWeights& w, uint16_t* hidden,
-                              float* y_routed, float* y_shared, hipStream_t s) {
+                              uint16_t* y_routed, uint16_t* y_shared, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
   GemmArgs args{};
   args.a_src = x;

@@ -130,12 +130,12 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   uint2 v[kMaxDepthSources];
 #pragma unroll
   for (int s = 0; s < NS; ++s) v[s] = reinterpret_cast<const uint2*>(sp[s])[base + ic];
-  float4 sh = {0.f, 0.f, 0.f, 0.f}, y0 = sh, y1 = sh;
+  uint2 sh = make_uint2(0u, 0u), y0 = sh, y1 = sh;
   uint2 pa = make_uint2(0u, 0u);
   if (combine) {
-    sh = reinterpret_cast<const float4*>(comb.y_shared)[base + ic];
-    y0 = reinterpret_cast<const float4*>(comb.y_routed)[(2 * tok) * chunks + ic];
-    y1 = reinterpret_cast<const float4*>(comb.y_routed)[(2 * tok + 1) * chunks + ic];
+    sh = reinterpret_cast<const uint2*>(comb.y_shared)[base + ic];
+    y0 = reinterpret_cast<const uint2*>(comb.y_routed)[(2 * tok) * chunks + ic];
+    y1 = reinterpret_cast<const uint2*>(comb.y_routed)[(2 * tok + 1) * chunks + ic];
     if (comb.addend != nullptr) pa = reinterpret_cast<const uint2*>(comb.addend)[base + ic];
   }
   const uint2 q = reinterpret_cast<const uint2*>(query)[ic];
@@ -173,8 +173,10 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     // bf16(addend + that), exactly as the combine kernel; it is the new
     // residual source and the last depth source.
     uint2 o;
-    o.x = pack_bf16x2(sh.x + y0.x + y1.x, sh.y + y0.y + y1.y);
-    o.y = pack_bf16x2(sh.z + y0.z + y1.z, sh.w + y0.w + y1.w);
+    o.x = pack_bf16x2(lo_bf16(sh.x) + lo_bf16(y0.x) + lo_bf16(y1.x),
+                      hi_bf16(sh.x) + hi_bf16(y0.x) + hi_bf16(y1.x));
+    o.y = pack_bf16x2(lo_bf16(sh.y) + lo_bf16(y0.y) + lo_bf16(y1.y),
+                      hi_bf16(sh.y) + hi_bf16(y0.y) + hi_bf16(y1.y));
     if (comb.addend != nullptr) {
       o.x = pack_bf16x2(lo_bf16(pa.x) + lo_bf16(o.x), hi_bf16(pa.x) + hi_bf16(o.x));
       o.y = pack_bf16x2(lo_bf16(pa.y) + lo_bf16(o.y), hi_bf16(pa.y) + hi_bf16(o.y));

@@ -184,8 +184,8 @@ def test_default_forward_512(monkeypatch):
 
 def test_default_forward_bf16_noise_floor(monkeypatch):
     """C4's argmax disagreement with fp32 is bf16 arithmetic, not a kernel
-    error: pooled over four seeded inputs of the default model (seed 2 is
-    C4; 2,048 positions), the HIP forward is as close to the fp32 oracle and
+    error: pooled over twelve seeded inputs of the default model (seed 2 is
+    C4; 6,144 positions), the HIP forward is as close to the fp32 oracle and
     to the bf16 emulation of the same rounding points
     (oracle/rounding_emulation.py), both forced to the HIP top-2 choices, as
     that emulation is to itself with another accumulation order (every
@@ -195,6 +195,9 @@ def test_default_forward_bf16_noise_floor(monkeypatch):
     differences at fp32 reassociation grow over sixteen layers to the size of
     the bf16 error itself, so two bf16 forwards agree on ~99 % of argmax
     positions (tests/test_error_budget_cpu.py::test_bf16_noise_floor).
+    Twelve inputs, not four: per input the HIP-vs-emulation agreement
+    scatters by about a point (97.1-99.6 % over seeds 2-13), so four inputs
+    pool to within ~0.3 point of the twelve-input value only by luck.
     Bars, each from the pooled counts:
       * argmax(HIP) vs argmax(emulation) agree at least as often as the two
         emulations do, less 0.5 point;
@@ -208,7 +211,7 @@ def test_default_forward_bf16_noise_floor(monkeypatch):
     cfg = ModelConfig(moe_backend="grouped_hip", depth_backend="hip", collect_router_stats=False)
     got_all, emu_all, emu64_all, ref_all = [], [], [], []
     rec = RouteRecorder(monkeypatch)
-    for seed in (2, 3, 4, 5):
+    for seed in range(2, 14):
         model = _hip_model(cfg, seed)
         ids = torch.randint(0, 32768, (1, 512), generator=torch.Generator().manual_seed(seed))
         with torch.no_grad():
