@@ -238,7 +238,7 @@ class StageBench:
 
     def bytes_down(self):
         T, d, H, Hs = self.T, self.dim, self.H, self.Hs
-        return (self.hit * d * H + d * Hs + 2 * T * H + T * Hs) * 2 + 3 * T * d * 4 + 2 * T * 4
+        return (self.hit * d * H + d * Hs + 2 * T * H + T * Hs + 3 * T * d) * 2 + 2 * T * 4
 
     def bytes_grouping(self):
         """Extra bytes of the in-kernel grouping: ids (or the route block
@@ -247,7 +247,7 @@ class StageBench:
         return ids + (3 * self.E + 2 + 2 * self.T) * 4
 
     def bytes_combine(self):
-        return 3 * self.T * self.dim * 4 + self.T * self.dim * 2
+        return 3 * self.T * self.dim * 2 + self.T * self.dim * 2
 
     def flops_gate_up(self):
         return 2 * (2 * self.T) * 2 * self.H * self.dim + 2 * self.T * 2 * self.Hs * self.dim

@@ -566,13 +566,14 @@ size_t parrot_experts_workspace_bytes(int64_t tokens, int32_t dim, int32_t hidde
 /* The three stages of parrot_grouped_experts_bf16, for callers that schedule
  * them separately.  They share one workspace of
  * parrot_experts_workspace_bytes() bytes that carries the intermediate
- * results from stage to stage (hidden rows, then fp32 expert outputs), so
+ * results from stage to stage (hidden rows, then bf16 expert outputs), so
  * the same workspace must be passed to all three, in order, on one stream.
  *   gate_up: h = bf16(silu(x Wg^T) * (x Wu^T)) for every routed assignment
  *            (in-capacity slots and overflow list alike) and every token of
  *            the shared expert, one grouped MFMA launch;
- *   down:    y = w[a] * (h Wd^T) per routed assignment, h Ws^T per token;
- *   combine: out[t] = bf16(y_shared[t] + y[2t] + y[2t+1]) (+ addend).
+ *   down:    y = bf16(w[a] * (h Wd^T)) per routed assignment, bf16(h Ws^T)
+ *            per token (fp32 products and sums, one rounding each);
+ *   combine: out[t] = bf16(y_shared[t] + y[2t] + y[2t+1]) in fp32 (+ addend).
  * Replace the torch.bmm / swiglu_from_gate_up_bf16 / moe_overflow_hidden_bf16
  * (gate_up), torch.bmm + overflow dot (down) and moe_gather_grouped_bf16
  * (combine) steps of grouped_mps_experts, parrot/metal_moe.py:400-415. */
