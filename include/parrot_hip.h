@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 12
+#define PARROT_ABI_VERSION 13
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -76,6 +76,24 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
                           const void* score_norm_weight, float score_eps,
                           const void* out_norm_weight, float out_eps, int64_t tokens,
                           int32_t dim, void* out_mix, void* out_norm, void* stream);
+
+/* The forward's first launch: rows_out[t] = table[ids[t]] (bf16 [tokens,
+ * dim], the embedding rows that become the residual stream's first source)
+ * and out_norm = rmsnorm(parrot_depth_mix_bf16 of that single source;
+ * out_norm_weight, out_eps), the first module's input, with the same bits as
+ * the separate gather and depth mix; also zero-fills n_zeros floats at zeros
+ * (the forward's router-stat outputs when they are not collected; zeros may
+ * be NULL when n_zeros is 0).  Ids outside [0, vocab) read the nearest row:
+ * the caller validates them (nn.Embedding raises).  tokens may be 0 (only the
+ * zero fill runs).  dim % 4 == 0, dim <= 2048; bf16 pointers 8-byte aligned.
+ * Replaces self.embedding(input_ids) and the first depth_mix of
+ * Parrot.forward (parrot/model.py:679, 685-687) and the router-stat zeros
+ * (parrot/model.py:719-723) when bag_size is 1. */
+int parrot_embed_depth_mix_bf16(const int64_t* ids, int64_t tokens, const void* table,
+                                int64_t vocab, int32_t dim, const void* query,
+                                const void* score_norm_weight, float score_eps,
+                                const void* out_norm_weight, float out_eps, void* rows_out,
+                                void* out_norm, float* zeros, int32_t n_zeros, void* stream);
 
 /* parrot_depth_mix_bf16 (out_norm required) followed by the router of
  * parrot_route_bf16 on the normalised rows, in one launch: writes

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (maps PyTorch's HIP runtime before the library)
 
 LIBRARY = Path(__file__).resolve().parent / "_lib" / "libparrot_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -29,6 +29,9 @@ SIGNATURES: dict[str, tuple] = {
     "parrot_rms_norm_bf16": (ctypes.c_int, [_p, _p, _p, _i64, _i32, _f32, _p]),
     "parrot_depth_mix_bf16": (
         ctypes.c_int, [_p, _i32, _p, _p, _f32, _p, _f32, _i64, _i32, _p, _p, _p]),
+    "parrot_embed_depth_mix_bf16": (
+        ctypes.c_int,
+        [_p, _i64, _p, _i64, _i32, _p, _p, _f32, _p, _f32, _p, _p, _p, _i32, _p]),
     "parrot_rope_qkv_bf16": (
         ctypes.c_int,
         [_p, _p, _p, _i64, _i32, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),

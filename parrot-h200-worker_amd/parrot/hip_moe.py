@@ -1272,6 +1272,34 @@ def _depth(module, sources: list[Tensor], output_norm, router=None, logit_bias=N
     return out, RouteResult(None, weights, indices, None)
 
 
+def embed_depth_mix_norm(ids: Tensor, table: Tensor, module, output_norm,
+                         zeros: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """The forward's first launch: the embedding rows of ``ids`` [batch, T]
+    (as ``table[ids]``, parrot/model.py:679) and ``depth_mix_norm(module,
+    [rows], output_norm)`` (parrot/model.py:685-687), the same bits as the
+    two steps; ``zeros`` (an fp32 tensor) is zero-filled by the same launch.
+    Ids outside the table read its nearest row: the caller validates them."""
+    _require(table, "The HIP depth backend")
+    if ids.dtype != torch.int64 or ids.device != table.device or table.ndim != 2:
+        raise RuntimeError("ids must be int64 on the table's device; table [vocab, dim]")
+    if not table.is_contiguous():
+        raise RuntimeError("embedding table must be contiguous")
+    if zeros is not None and (zeros.dtype != torch.float32 or zeros.device != table.device or
+                              not zeros.is_contiguous()):
+        raise RuntimeError("zeros must be a contiguous fp32 tensor on the table's device")
+    flat = ids.contiguous()
+    vocab, dim = table.shape
+    rows = torch.empty((*ids.shape, dim), dtype=table.dtype, device=table.device)
+    out = torch.empty_like(rows)
+    _abi.check(_abi.load().parrot_embed_depth_mix_bf16(
+        ptr(flat), flat.numel(), ptr(table), vocab, dim, ptr(module.query),
+        ptr(module.norm.weight), float(module.norm.eps), ptr(output_norm.weight),
+        float(output_norm.eps), ptr(rows), ptr(out), ptr(zeros),
+        0 if zeros is None else zeros.numel(), _stream(table.device)),
+        "parrot_embed_depth_mix_bf16")
+    return rows, out
+
+
 def depth_mix(module, sources: list[Tensor]) -> Tensor:
     """Block AttnRes mix of 1..9 sources (cf. metal_depth_mix)."""
     return _depth(module, sources, None)

@@ -162,6 +162,32 @@ int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const v
                          stream);
 }
 
+int parrot_embed_depth_mix_bf16(const int64_t* ids, int64_t tokens, const void* table,
+                                int64_t vocab, int32_t dim, const void* query,
+                                const void* score_norm_weight, float score_eps,
+                                const void* out_norm_weight, float out_eps, void* rows_out,
+                                void* out_norm, float* zeros, int32_t n_zeros, void* stream) {
+  if (!table || !query || !score_norm_weight || !out_norm_weight) return PARROT_ERR_NULL_POINTER;
+  if (tokens > 0 && (!ids || !rows_out || !out_norm)) return PARROT_ERR_NULL_POINTER;
+  if (n_zeros > 0 && !zeros) return PARROT_ERR_NULL_POINTER;
+  if (tokens < 0 || tokens > (int64_t{1} << 31) - 1 || vocab < 1 || n_zeros < 0 || dim <= 0 ||
+      dim % 4)
+    return PARROT_ERR_BAD_SHAPE;
+  if (dim > 2048) return PARROT_ERR_UNSUPPORTED;
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(query) |
+                         reinterpret_cast<uintptr_t>(score_norm_weight) |
+                         reinterpret_cast<uintptr_t>(out_norm_weight) |
+                         reinterpret_cast<uintptr_t>(rows_out) |
+                         reinterpret_cast<uintptr_t>(out_norm);
+  if (bits & 7u) return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_embed_mix(
+      ids, static_cast<const uint16_t*>(table), vocab, static_cast<const uint16_t*>(query),
+      static_cast<const uint16_t*>(score_norm_weight), score_eps,
+      static_cast<const uint16_t*>(out_norm_weight), out_eps, tokens, dim,
+      static_cast<uint16_t*>(rows_out), static_cast<uint16_t*>(out_norm), zeros, n_zeros,
+      as_stream(stream)));
+}
+
 int parrot_depth_mix_route_bf16(const void* const* sources, int32_t n_sources,
                                 const void* query, const void* score_norm_weight,
                                 float score_eps, const void* out_norm_weight, float out_eps,

@@ -288,6 +288,15 @@ struct RouteOut {
 
 // comb: optional (nullptr: every source is read from srcs).  route:
 // optional; needs out_norm.
+// The forward's first launch: embedding rows by id (written to rows_out) and
+// their single-source depth mix + RMSNorm (out_norm); zero-fills n_zeros
+// floats at zeros (see norm.hip).
+hipError_t launch_embed_mix(const int64_t* ids, const uint16_t* table, int64_t vocab,
+                            const uint16_t* query, const uint16_t* score_w, float score_eps,
+                            const uint16_t* out_norm_w, float out_eps, int64_t tokens, int dim,
+                            uint16_t* rows_out, uint16_t* out_norm, float* zeros, int n_zeros,
+                            hipStream_t s);
+
 hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
                             const uint16_t* query, const uint16_t* score_w,
                             float score_eps, const uint16_t* out_norm_w,

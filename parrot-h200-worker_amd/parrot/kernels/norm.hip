@@ -253,6 +253,49 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   }
 }
 
+// The forward's first launch (parrot/model.py:679, 685-687): the tokens'
+// embedding rows gathered by id and written out (the residual stream's first
+// source, as nn.Embedding does), and the first module's input, the depth mix
+// of that single source and its RMSNorm, with depth_mix_kernel<0, 1>'s
+// arithmetic (the same bits for every token; a single source's softmax
+// weight is exactly 1, so the mix is the row).  Workgroup 0 also zero-fills
+// `zeros` (the forward's router-stat outputs when they are not collected,
+// parrot/model.py:719-723).  Ids outside [0, vocab) read the nearest row;
+// the host rejects them before an eager launch.
+__global__ __launch_bounds__(64 * kDepthMaxWaves) void embed_mix_kernel(
+    const int64_t* __restrict__ ids, const uint16_t* __restrict__ table, int64_t vocab,
+    const uint16_t* __restrict__ query, const uint16_t* __restrict__ score_w, float score_eps,
+    const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
+    uint16_t* __restrict__ rows_out, uint16_t* __restrict__ out_norm,
+    float* __restrict__ zeros, int n_zeros) {
+  __shared__ DepthMixLds mix_lds;
+  asm volatile("" ::"s"(ids), "s"(table), "s"(vocab), "s"(query), "s"(score_w), "s"(out_w),
+               "s"(dim), "s"(rows_out), "s"(out_norm), "s"(zeros), "s"(n_zeros), "s"(tokens));
+  if (blockIdx.x == 0)
+    for (int z = threadIdx.x; z < n_zeros; z += blockDim.x) zeros[z] = 0.0f;
+  if (static_cast<int64_t>(blockIdx.x) >= tokens) return;  // uniform: the zero-fill-only launch
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int waves = blockDim.x >> 6;
+  const int64_t tok = blockIdx.x;
+  const int chunks = dim >> 2;
+  const int i = wave * kWave + lane;
+  const bool has = i < chunks;
+  const int ic = has ? i : 0;
+  const int64_t id = min(max(ids[tok], int64_t{0}), vocab - 1);
+  const uint2 q = reinterpret_cast<const uint2*>(query)[ic];
+  const uint2 g = reinterpret_cast<const uint2*>(score_w)[ic];
+  const uint2 g_out = reinterpret_cast<const uint2*>(out_w)[ic];
+  uint2 v[kMaxDepthSources];
+  v[0] = reinterpret_cast<const uint2*>(table)[id * chunks + ic];
+  if (!has) v[0] = make_uint2(0u, 0u);
+  if (has) reinterpret_cast<uint2*>(rows_out)[tok * chunks + i] = v[0];
+  const uint2 mixed = depth_mix_chunk<1>(v, q, g, has, waves, wave, lane, dim, score_eps, mix_lds);
+  const uint2 o = depth_mix_norm_chunk(mixed, g_out, has, waves, wave, lane, dim, out_eps,
+                                       mix_lds);
+  if (has) reinterpret_cast<uint2*>(out_norm)[tok * chunks + i] = o;
+}
+
 // The depth mix at large token counts: one wavefront per token, two
 // tokens per workgroup, no barrier.  The wavefront does, slice by slice, what
 // the wavefronts of depth_mix_kernel do side by side: lane l owns the 4-dim
@@ -433,6 +476,22 @@ hipError_t launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out,
     case 8: rms_norm_kernel<8><<<grid, 64, 0, s>>>(x, w, out, rows, dim, eps); break;
     default: rms_norm_kernel<16><<<grid, 64, 0, s>>>(x, w, out, rows, dim, eps); break;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_mix(const int64_t* ids, const uint16_t* table, int64_t vocab,
+                            const uint16_t* query, const uint16_t* score_w, float score_eps,
+                            const uint16_t* out_norm_w, float out_eps, int64_t tokens, int dim,
+                            uint16_t* rows_out, uint16_t* out_norm, float* zeros, int n_zeros,
+                            hipStream_t s) {
+  if (tokens == 0 && n_zeros == 0) return hipSuccess;
+  const int waves = (dim + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
+  if (waves > kDepthMaxWaves) return hipErrorInvalidValue;
+  // With no tokens, one workgroup that only zero-fills.
+  const unsigned grid = static_cast<unsigned>(tokens > 0 ? tokens : 1);
+  embed_mix_kernel<<<grid, kWave * waves, 0, s>>>(ids, table, vocab, query, score_w, score_eps,
+                                                  out_norm_w, out_eps, tokens, dim, rows_out,
+                                                  out_norm, zeros, n_zeros);
   return hipGetLastError();
 }
 

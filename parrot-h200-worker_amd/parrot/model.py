@@ -850,6 +850,36 @@ class Parrot(nn.Module):
 
     # -- helpers -------------------------------------------------------------
 
+    def _embedded(self, input_ids: Tensor, bag_size: int = 1,
+                  stat_zeros: Tensor | None = None) -> tuple[Tensor, Tensor | None]:
+        """The embedding rows (parrot/model.py:679) and, where the HIP path
+        makes it in the same launch, the first module's input (else None);
+        ``stat_zeros`` is zero-filled by that launch."""
+        if not self._embeds_first_mix(input_ids, bag_size):
+            x = self.embedding(input_ids)
+            if bag_size > 1:
+                b, source_len = input_ids.shape
+                x = x.reshape(b, source_len // bag_size, bag_size, -1).mean(2)
+            return x, None
+        from . import hip_moe
+        weight = self.embedding.weight
+        if not torch.cuda.is_current_stream_capturing():
+            # The launch clamps ids outside the table (a graph replay has no
+            # error channel); an eager call raises as nn.Embedding does.
+            if bool(((input_ids < 0) | (input_ids >= weight.shape[0])).any()):
+                raise IndexError(f"token id out of range of the {weight.shape[0]}-row embedding")
+        return hip_moe.embed_depth_mix_norm(input_ids, weight, self.depth_mix[0],
+                                            self.blocks[0].attention_norm, stat_zeros)
+
+    def _embeds_first_mix(self, input_ids: Tensor, bag_size: int) -> bool:
+        """The HIP forward's first launch gathers the embedding rows and makes
+        the first module's input (AttnRes, one token per position)."""
+        cfg = self.config
+        return (bag_size == 1 and cfg.residual == "attnres" and cfg.depth_backend == "hip" and
+                len(self.blocks) > 0 and input_ids.dtype == torch.int64 and
+                input_ids.device == self.embedding.weight.device and
+                _hip_inference(self.embedding.weight))
+
     def _head(self, normed: Tensor) -> Tensor:
         """Tied vocabulary head (reference parrot/model.py:714-715).  On the
         HIP backend the logits come out in fp32, never rounded to bf16: a
@@ -988,14 +1018,17 @@ class Parrot(nn.Module):
         if supervised_logits_only and labels is None:
             raise ValueError("supervised_logits_only requires labels")
 
-        x = self.embedding(input_ids)
-        if bag_size > 1:
-            x = x.reshape(b, t, bag_size, -1).mean(2)
+        stat_zeros = None
+        if self._embeds_first_mix(input_ids, bag_size) and not cfg.collect_router_stats:
+            stat_zeros = torch.empty((1 + cfg.n_layers * cfg.n_experts,), dtype=torch.float32,
+                                     device=self.embedding.weight.device)
+        # pending: the next module's input (the first module's from the
+        # embedding launch, then each made by the previous MoE's combine)
+        x, pending = self._embedded(input_ids, bag_size, stat_zeros)
         stream = _AttnRes(x, cfg.depth_block_size) if cfg.residual == "attnres" else None
         aux_losses, utilization = [], []
         remat = cfg.checkpoint_modules and self.training and torch.is_grad_enabled()
         index = 0
-        pending = None  # the next module's input, made by the previous MoE's combine
         for bi, block in enumerate(self.blocks):
             h = pending if pending is not None else \
                 self._mixed_input(stream, x, index, block.attention_norm)
@@ -1042,8 +1075,10 @@ class Parrot(nn.Module):
             aux_loss = torch.stack(aux_losses).mean()
             expert_utilization = torch.stack(utilization)
         else:
-            # one zero fill for both (views of one buffer)
-            zeros = x.new_zeros((1 + cfg.n_layers * cfg.n_experts,), dtype=torch.float32)
+            # one zero fill for both (views of one buffer; on the HIP path the
+            # first launch filled it)
+            zeros = stat_zeros if stat_zeros is not None else \
+                x.new_zeros((1 + cfg.n_layers * cfg.n_experts,), dtype=torch.float32)
             aux_loss = zeros[0]
             expert_utilization = zeros[1:].view(cfg.n_layers, cfg.n_experts)
         lm_loss = loss = None
@@ -1071,11 +1106,12 @@ class Parrot(nn.Module):
         b, t = input_ids.shape
         if t > cfg.max_seq_len:
             raise ValueError("Prompt exceeds max_seq_len")
-        x = self.embedding(input_ids)
+        # pending: the next module's input (the first module's from the
+        # embedding launch, then each made by the previous MoE's combine)
+        x, pending = self._embedded(input_ids)
         stream = _AttnRes(x, cfg.depth_block_size) if cfg.residual == "attnres" else None
         caches: list[LocalKVCache | MLALatentCache] = []
         index = 0
-        pending = None  # the next module's input, made by the previous MoE's combine
         for bi, block in enumerate(self.blocks):
             h = pending if pending is not None else \
                 self._mixed_input(stream, x, index, block.attention_norm)

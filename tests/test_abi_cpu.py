@@ -114,6 +114,19 @@ def test_argument_validation_without_gpu(lib):
                                      fake, 1e-6, 4, 64, fake, null, null) == -3
     assert lib.parrot_depth_mix_bf16(ctypes.cast(srcs, ctypes.c_void_p), 2, fake, fake, 1e-6,
                                      null, 1e-6, 4, 64, null, null, null) == -1
+    # the forward's first launch: shapes, pointers and alignment
+    assert lib.parrot_embed_depth_mix_bf16(fake, 4, fake, 100, 66, fake, fake, 1e-6, fake,
+                                           1e-6, fake, fake, null, 0, null) == -2
+    assert lib.parrot_embed_depth_mix_bf16(fake, 4, fake, 100, 4096, fake, fake, 1e-6, fake,
+                                           1e-6, fake, fake, null, 0, null) == -3
+    assert lib.parrot_embed_depth_mix_bf16(fake, 4, null, 100, 64, fake, fake, 1e-6, fake,
+                                           1e-6, fake, fake, null, 0, null) == -1
+    assert lib.parrot_embed_depth_mix_bf16(fake, 4, fake, 100, 64, fake, fake, 1e-6, fake,
+                                           1e-6, fake, fake, null, 8, null) == -1
+    assert lib.parrot_embed_depth_mix_bf16(fake, 4, fake, 0, 64, fake, fake, 1e-6, fake,
+                                           1e-6, fake, fake, null, 0, null) == -2
+    assert lib.parrot_embed_depth_mix_bf16(fake, 4, fake + 2, 100, 64, fake, fake, 1e-6, fake,
+                                           1e-6, fake, fake, null, 0, null) == -5
     ws = lib.parrot_route_workspace_bytes(64, 8)
     args = [fake] * 9  # out_logits .. out_overflow
     # experts outside 2..32

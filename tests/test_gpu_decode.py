@@ -596,3 +596,12 @@ def test_eager_decode_step_rejects_out_of_range_ids():
     assert state.position == 8
     logits, state = model.decode_step(torch.tensor([[5], [7]], device="cuda"), state)
     assert state.position == 9 and torch.isfinite(logits.float()).all()
+    # The forward and prefill gather their rows in the first launch, which
+    # clamps too: eager calls raise before it.
+    for bad in (32768, -1):
+        ids = prompt.clone()
+        ids[1, 3] = bad
+        with torch.no_grad(), pytest.raises(IndexError):
+            model(ids)
+        with pytest.raises(IndexError):
+            model.prefill(ids)

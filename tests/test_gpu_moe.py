@@ -123,6 +123,42 @@ MOE_CASES = [
 ]
 
 
+@pytest.mark.parametrize("tokens,dim", [(1, 768), (17, 768), (512, 768), (5000, 768), (40, 448)])
+def test_embed_depth_mix_equals_gather_and_mix(tokens, dim):
+    """The forward's first launch (parrot_embed_depth_mix_bf16): the gathered
+    embedding rows equal table[ids] and the first module's input equals the
+    separate depth_mix_norm of that one source, bit for bit (from 4096 tokens
+    the separate mix runs the one-wavefront kernel); ids outside the table
+    read its nearest row; the stat buffer is zero-filled, also with no
+    tokens."""
+    from parrot import hip_moe
+    _say(f"embed + first depth mix T={tokens} dim={dim}")
+    torch.manual_seed(tokens + dim)
+    vocab = 1000
+    depth = _Depth(dim).cuda().bfloat16()
+    with torch.no_grad():
+        depth.query.normal_()
+    out_norm = _Norm(dim).cuda().bfloat16()
+    table = (torch.randn(vocab, dim) * 2).cuda().bfloat16()
+    ids = torch.randint(0, vocab, (1, tokens)).cuda()
+    ids[0, 0] = -5
+    ids[0, -1] = vocab + 3
+    zeros = torch.full((257,), float("nan"), device="cuda")
+    with torch.no_grad():
+        rows, first = hip_moe.embed_depth_mix_norm(ids, table, depth, out_norm, zeros)
+        clamped = ids.clamp(0, vocab - 1)
+        ref_rows = table[clamped]
+        ref_first = hip_moe.depth_mix_norm(depth, [ref_rows], out_norm)
+    assert torch.equal(rows, ref_rows)
+    assert torch.equal(first, ref_first)
+    assert torch.equal(zeros, torch.zeros_like(zeros))
+    empty = torch.full((5,), float("nan"), device="cuda")
+    with torch.no_grad():
+        hip_moe.embed_depth_mix_norm(ids[:, :0], table, depth, out_norm, empty)
+    torch.cuda.synchronize()
+    assert torch.equal(empty, torch.zeros_like(empty))
+
+
 @pytest.mark.parametrize("name,tokens,experts,skewed", MOE_CASES)
 def test_moe_layer(name, tokens, experts, skewed):
     from parrot import hip_moe
