@@ -50,11 +50,19 @@ constexpr int kRouteStepSlots = 6;
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
 
+// Dot product of 8 bf16 pairs in fp32: four v_dot2c_f32_bf16, each adding two
+// exact bf16 products to the running sum (4 instructions where unpacking the
+// halves and fusing multiply-adds takes 24; decode steps 1-2 % faster on
+// MI355X).  Its rounding is neither the exactly rounded sum nor two chained
+// FMAs: on 67M random finite inputs it matched the first in 88.7 % and the
+// second in 87.3 % of cases, within one fp32 rounding of both.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
 __device__ __forceinline__ float dot8(uint4 a, uint4 b) {
-  return lo_bf16(a.x) * lo_bf16(b.x) + hi_bf16(a.x) * hi_bf16(b.x) +
-         lo_bf16(a.y) * lo_bf16(b.y) + hi_bf16(a.y) * hi_bf16(b.y) +
-         lo_bf16(a.z) * lo_bf16(b.z) + hi_bf16(a.z) * hi_bf16(b.z) +
-         lo_bf16(a.w) * lo_bf16(b.w) + hi_bf16(a.w) * hi_bf16(b.w);
+  return dot2(a.w, b.w, dot2(a.z, b.z, dot2(a.y, b.y, dot2(a.x, b.x, 0.0f))));
 }
 
 // One 16-byte chunk of an LDS array, read as LDS (ds_read_b128) rather
