@@ -24,16 +24,16 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// Dot product of 8 bf16 pairs in fp32 on four v_dot2c_f32_bf16 (each adds two
+// exact bf16 products to the running sum; within one fp32 rounding of the
+// exactly rounded sum, as the decode MoE's dot8).
+typedef __bf16 gemv_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float gemv_dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(gemv_bf16x2, a),
+                                         __builtin_bit_cast(gemv_bf16x2, b), c, false);
+}
 __device__ __forceinline__ float dot_bf16x8(uint4 w, uint4 x) {
-  float s = lo_bf16(w.x) * lo_bf16(x.x);
-  s += hi_bf16(w.x) * hi_bf16(x.x);
-  s += lo_bf16(w.y) * lo_bf16(x.y);
-  s += hi_bf16(w.y) * hi_bf16(x.y);
-  s += lo_bf16(w.z) * lo_bf16(x.z);
-  s += hi_bf16(w.z) * hi_bf16(x.z);
-  s += lo_bf16(w.w) * lo_bf16(x.w);
-  s += hi_bf16(w.w) * hi_bf16(x.w);
-  return s;
+  return gemv_dot2(w.w, x.w, gemv_dot2(w.z, x.z, gemv_dot2(w.y, x.y, gemv_dot2(w.x, x.x, 0.0f))));
 }
 
 __device__ __forceinline__ float dot_f32x8(uint4 w, float4 x0, float4 x1) {
