@@ -1023,10 +1023,11 @@ def summarize_steps(directory: str, out_dir: Path | None = None) -> str:
                "python3 bench.py --summarize-steps gpurun_out/prof_steps")
     bench = load_json(BENCH_FILE) or {}
     out_dir = ROOT / "profiles" if out_dir is None else Path(out_dir)
-    # Forwards: from one bs1 x 512 embedding gather to the next; the timed
-    # graph replays are the last `steps` of the most common launch count.
+    # Forwards: from one bs1 x 512 first launch (the embedding gather with
+    # the first module's input, one workgroup per token) to the next; the
+    # timed graph replays are the last `steps` of the most common launch count.
     starts = [i for i, r in enumerate(rows)
-              if "gather" in r["name"] and r["gx"] == TOKENS * 128]
+              if "embed_mix_kernel" in r["name"] and r["gx"] // r["wg"] == TOKENS]
     segs = [rows[a:b] for a, b in zip(starts, starts[1:] + [len(rows)])]
     counts = [len(sg) for sg in segs]
     mode = max(set(counts), key=counts.count) if counts else 0
@@ -1037,7 +1038,7 @@ def summarize_steps(directory: str, out_dir: Path | None = None) -> str:
         "# Kernel trace: Parrot bf16 forward, batch 1 x 512 (HIP-graph replay)\n\n"
         "Command (GPU box, repo root):\n\n```\n" + command + "\n```\n\n"
         f"The last {len(fwd)} forwards of the trace (the timed graph replays), split at each "
-        f"forward's embedding gather.  Per forward: {launches:g} launches, {busy:.1f} us of "
+        f"forward's first launch (embedding rows and first module input).  Per forward: {launches:g} launches, {busy:.1f} us of "
         f"kernel time, {span:.1f} us from the first launch's start to the last one's end"
         + (f" (the committed bench line: {ms * 1e3:.1f} us per step)" if ms else "")
         + ".  Durations in us (End - Start), under the profiler.\n\n" + table + "\n")
