@@ -27,13 +27,15 @@ def _trace(path: Path, rows):
 
 def test_step_summaries_split_forwards_and_decode_steps(tmp_path):
     import bench
-    gather = "void at::native::vectorized_gather_kernel<16, long>(int, char*)"
+    embed = ("parrot::(anonymous namespace)::embed_mix_kernel(long const*, unsigned short const*, "
+             "long, unsigned short const*, unsigned short const*, float, unsigned short const*, "
+             "float, int, int, unsigned short*, unsigned short*, float*, int)")
     mix = "void parrot::(anonymous namespace)::depth_mix_kernel<0, 3>(parrot::DepthSources)"
     att = "void parrot::(anonymous namespace)::decode_attention_kernel<float, float, 16, 0>(int)"
     red = "parrot::(anonymous namespace)::vocab_argmax_reduce_kernel(float const*)"
     rows = []
-    for _ in range(3):  # three forwards of three launches
-        rows += [(gather, 400, bench.TOKENS * 128, 1), (mix, 700, 98304, 1), (mix, 900, 98304, 1)]
+    for _ in range(3):  # three forwards of three launches, each opened by the fused first one
+        rows += [(embed, 400, bench.TOKENS * 256, 1), (mix, 700, 98304, 1), (mix, 900, 98304, 1)]
     for b in (1, 2):    # two decode steps per batch
         for _ in range(2):
             rows += [(att, 600, 2048, b), (red, 300, 256 * b, 1)]
