@@ -82,6 +82,25 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// 16 bytes per lane from a buffer straight into LDS: lane l's bytes land at
+// lds + 16 l (buffer_load_dwordx4 ... lds).  Reads past the buffer end
+// return zero.  (The global_load_lds form is a FLAT-family instruction that
+// touches two address spaces, after which the compiler turns every
+// vector-memory wait it places into vmcnt(0); the buffer form is not.)
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* lds,
+                                                uint32_t voffset, uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voffset, soffset, 0, 0);
+}
+
+// Waits until at most N vector-memory operations of this wavefront are
+// outstanding, then joins the workgroup barrier.  Written out because
+// __syncthreads() would also wait for every in-flight direct-to-LDS load
+// (vmcnt(0)), which drains a ring of stages on every step.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(N) : "memory");
+}
+
 // One RoPE rotation pair (x[2i], x[2i+1]) by angle (c, s), in fp32 with the
 // products contracted the same way wherever it is applied, so the fused and
 // the stand-alone RoPE paths round identically.

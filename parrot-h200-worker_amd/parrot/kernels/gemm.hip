@@ -439,23 +439,6 @@ struct WaveLayout {
   static constexpr int kWavesN = 4 / kWavesM;
 };
 
-// Waits until at most N vector-memory loads of this wavefront are
-// outstanding, then joins the workgroup barrier.  Written out because
-// __syncthreads() would also wait for every in-flight direct-to-LDS load
-// (vmcnt(0)), which drains the stage ring on every k step.
-template <int N>
-__device__ __forceinline__ void wait_vm_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(N) : "memory");
-}
-
-// 16 bytes per lane from a buffer straight into LDS: lane l's bytes land at
-// lds + 16 l (buffer_load_dwordx4 ... lds).  Reads past the buffer end
-// return zero.
-__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* lds,
-                                                uint32_t voffset, uint32_t soffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voffset, soffset, 0, 0);
-}
-
 // One 16-byte MFMA fragment from LDS, read with inline asm so the compiler
 // does not treat it as an LDS access: otherwise it cannot tell the ring slot
 // being read from the slots the in-flight direct-to-LDS loads fill, and

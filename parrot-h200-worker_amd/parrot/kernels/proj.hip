@@ -216,16 +216,25 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
       }
   }
 
-  // ---- A: the whole tile, direct to LDS (rows past the end read the last row)
+  // ---- A: the whole tile, direct to LDS (rows past the end read the last
+  // row).  Buffer loads, not global_load_lds: after a global_load_lds the
+  // compiler cannot see that the wait below covered it and turns its own
+  // wait for the first weight fragment into vmcnt(0), so no MFMA would start
+  // before every weight load of the ring had landed.
   {
+    const int tile_rows = min(BM, p.rows - m0);
+    const __amdgpu_buffer_rsrc_t x_rsrc =
+        make_rsrc(p.x + static_cast<int64_t>(m0) * p.lda,
+                  static_cast<uint32_t>(static_cast<int64_t>(tile_rows) * p.lda * 2));
     const int slots = BM * chunks;  // multiple of 64
     for (int i = wave; i < slots / kWave; i += 4) {
       const int s = i * kWave + lane;
       const int r = s / chunks;
       const int pc = s - r * chunks;
       const int c = (pc & ~swz) | ((pc ^ r) & swz);
-      const uint16_t* g = p.x + static_cast<int64_t>(min(m0 + r, p.rows - 1)) * p.lda + c * 8;
-      __builtin_amdgcn_global_load_lds(g, (lds_void_t*)(a_lds + i * kWave * 8), 16, 0, 0);
+      const uint32_t off =
+          static_cast<uint32_t>((static_cast<int64_t>(min(r, tile_rows - 1)) * p.lda + c * 8) * 2);
+      buffer_to_lds16(x_rsrc, a_lds + i * kWave * 8, off, 0);
     }
   }
 
