@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PARROT_ABI_VERSION 13
+#define PARROT_ABI_VERSION 14
 
 #define PARROT_OK 0
 #define PARROT_ERR_NULL_POINTER (-1)
@@ -114,6 +114,23 @@ int parrot_depth_mix_route_bf16(const void* const* sources, int32_t n_sources,
                                 const void* router_weight, const float* logit_bias,
                                 int32_t experts, float* out_weights, int64_t* out_indices,
                                 void* stream);
+
+/* parrot_depth_mix_route_bf16 (no out_mix) whose last source is a pending
+ * attention output: resolved = bf16(base + bf16(sum over the heads of
+ * contributions[t, h, :])) (heads == 8, summed in head order; base optional,
+ * else the rounded sum alone), written to `resolved` and mixed as source
+ * n_sources - 1 (whose pointer in `sources` must still be a readable
+ * [tokens, dim] row block; it is not used).  contributions fp32 [tokens,
+ * heads, dim] as parrot_causal_attention_frag_out_bf16 writes them.
+ * Replaces resolving the reference's PendingResidual inside the consumer's
+ * mix (parrot/model.py:103-106, 832-860; metal_depth_mix_norm_pending,
+ * parrot/metal_moe.py:480-500) for a MoE module's routed input. */
+int parrot_depth_mix_route_pending_bf16(
+    const void* const* sources, int32_t n_sources, const void* query,
+    const void* score_norm_weight, float score_eps, const void* out_norm_weight, float out_eps,
+    int64_t tokens, int32_t dim, void* out_norm, const void* router_weight,
+    const float* logit_bias, int32_t experts, float* out_weights, int64_t* out_indices,
+    const float* contributions, int32_t heads, const void* base, void* resolved, void* stream);
 
 /* parrot_experts_combine_bf16 folded into the next module's depth mix: the
  * combined MoE row out (bf16(addend + bf16(shared + routed rows)), exactly
@@ -431,6 +448,25 @@ int parrot_causal_attention_frag_bf16(const void* q, const int64_t* q_strides, c
                                       const void* v_frag, int64_t batch, int32_t seq,
                                       int32_t heads, int32_t kv_heads, int32_t head_dim,
                                       int32_t window, float scale, void* out, void* stream);
+
+/* parrot_causal_attention_frag_bf16 with the output projection deferred per
+ * head, for whole sequences: instead of the output y it writes each head's
+ * share of out(y), contributions[b, t, h, :] = y[b, t, h, :] (rounded to
+ * bf16 as the output would be) times the head's head_dim columns of the
+ * output weight, fp32 [batch, seq, heads, dim].  out_weight_packed is the
+ * [dim, heads * head_dim] output weight packed as parrot_proj_bf16 takes it;
+ * dim in {512, 768, 1024}.  bf16 of the sum over heads is
+ * parrot_proj_bf16(y, out_weight) up to fp32 summation order.  Replaces the
+ * attention + out projection of LocalGQA.prefill and GlobalMLA.prefill
+ * (parrot/model.py:264-295, 350-360) where the next module's depth mix
+ * takes the sum (parrot_depth_mix_route_pending_bf16), as the reference's
+ * decode defers it (PendingResidual, parrot/model.py:103-106, 301-316). */
+int parrot_causal_attention_frag_out_bf16(const void* q, const int64_t* q_strides,
+                                          const void* k_frag, const void* v_frag, int64_t batch,
+                                          int32_t seq, int32_t heads, int32_t kv_heads,
+                                          int32_t head_dim, int32_t window, float scale,
+                                          const void* out_weight_packed, int32_t dim,
+                                          float* contributions, void* stream);
 
 /* Dense projection y = x . W^T (bf16 in and out, fp32 accumulation) for the
  * attention layers' linear maps, with the weight pre-packed in MFMA fragment

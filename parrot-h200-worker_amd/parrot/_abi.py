@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (maps PyTorch's HIP runtime before the library)
 
 LIBRARY = Path(__file__).resolve().parent / "_lib" / "libparrot_hip.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -65,6 +65,11 @@ SIGNATURES: dict[str, tuple] = {
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p]),
     "parrot_vocab_argmax_bf16": (ctypes.c_int, [_p, _i64, _i32, _p, _i32, _p, _p, _p, _sz, _p]),
+    "parrot_causal_attention_frag_out_bf16": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                                                              _i32, _i32, _f32, _p, _i32, _p, _p]),
+    "parrot_depth_mix_route_pending_bf16": (ctypes.c_int, [_p, _i32, _p, _p, _f32, _p, _f32, _i64,
+                                                            _i32, _p, _p, _p, _i32, _p, _p, _p,
+                                                            _i32, _p, _p, _p]),
     "parrot_decode_moe_bf16": (
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),

@@ -910,6 +910,48 @@ def causal_attention_frag(q: Tensor, k_frag: Tensor, v_frag: Tensor, *, kv_heads
     return out
 
 
+# Output widths and head count for which an attention output's projection
+# can be deferred per head to the next depth mix (the kernels' instances).
+ATTENTION_OUT_WIDTHS = (512, 768, 1024)
+PENDING_HEADS = 8
+
+
+def attention_heads_out_supported(heads: int, head_dim: int, dim: int) -> bool:
+    """Whether causal_attention_frag_out takes these shapes and the depth
+    mix can sum its contributions (parrot_depth_mix_route_pending_bf16)."""
+    return (heads == PENDING_HEADS and head_dim in ATTENTION_HEAD_DIMS and
+            dim in ATTENTION_OUT_WIDTHS and dim % 32 == 0)
+
+
+def causal_attention_frag_out(q: Tensor, k_frag: Tensor, v_frag: Tensor, out_packed: Tensor,
+                              dim: int, *, kv_heads: int, scale: float,
+                              window: int | None = None) -> Tensor:
+    """``causal_attention_frag`` with the output projection deferred per
+    head: returns fp32 contributions [b, t, H, dim], head h's share
+    bf16(y_h) W[:, h d : h d + d]^T of the projection by ``out_packed`` (the
+    output weight packed by ``pack_linear``).  bf16 of their sum over heads
+    is ``proj(y, out_packed, dim)`` up to fp32 summation order (cf. the
+    reference's defer_sum, parrot/model.py:301-316)."""
+    _require(q, "HIP causal attention")
+    b, heads, t, d = q.shape
+    if not attention_heads_out_supported(heads, d, dim):
+        raise RuntimeError(f"no deferred output projection for {heads} heads of {d}, width {dim}")
+    need = b * kv_heads * key_blocks(t) * 32 * d
+    if k_frag.numel() != need or v_frag.numel() != need:
+        raise RuntimeError("fragment-order K / V do not match the query shape")
+    if out_packed.numel() != dim * heads * d:
+        raise RuntimeError("packed output weight does not match [dim, heads * head_dim]")
+    if q.stride(-1) != 1 or any(st % 8 for st in q.stride()[:3]) or q.data_ptr() % 16:
+        q = q.contiguous()
+    out = torch.empty((b, t, heads, dim), dtype=torch.float32, device=q.device)
+    st = (ctypes.c_int64 * 3)(*q.stride()[:3])
+    _abi.check(_abi.load().parrot_causal_attention_frag_out_bf16(
+        ptr(q), ctypes.cast(st, ctypes.c_void_p), ptr(k_frag), ptr(v_frag), b, t, heads, kv_heads,
+        d, t if window is None else window, scale, ptr(out_packed), dim, ptr(out),
+        _stream(q.device)), "parrot_causal_attention_frag_out_bf16")
+    return out
+
+
 def _check_position(position: Tensor, device: torch.device) -> None:
     if position.dtype != torch.int32 or position.device != device or position.numel() != 1:
         raise RuntimeError("position must be a one-element int32 tensor on the cache's device")
@@ -1230,7 +1272,8 @@ def rms_norm(module, x: Tensor) -> Tensor:
 _SourceArray = ctypes.c_void_p * MAX_DEPTH_SOURCES
 
 
-def _depth(module, sources: list[Tensor], output_norm, router=None, logit_bias=None):
+def _depth(module, sources: list[Tensor], output_norm, router=None, logit_bias=None,
+           pending=None):
     if not 1 <= len(sources) <= MAX_DEPTH_SOURCES:
         raise RuntimeError(f"HIP depth mixing supports one to {MAX_DEPTH_SOURCES} sources")
     first = sources[0]
@@ -1265,9 +1308,24 @@ def _depth(module, sources: list[Tensor], output_norm, router=None, logit_bias=N
     indices = torch.empty((tokens, 2), dtype=torch.int64, device=first.device)
     if logit_bias is not None:
         logit_bias = logit_bias.to(device=first.device, dtype=torch.float32).contiguous()
-    _abi.check(lib.parrot_depth_mix_route_bf16(
-        *mix_args, ptr(router_w), ptr(logit_bias), cfg.n_experts, ptr(weights), ptr(indices),
-        _stream(first.device)), "parrot_depth_mix_route_bf16")
+    if pending is None:
+        _abi.check(lib.parrot_depth_mix_route_bf16(
+            *mix_args, ptr(router_w), ptr(logit_bias), cfg.n_experts, ptr(weights), ptr(indices),
+            _stream(first.device)), "parrot_depth_mix_route_bf16")
+    else:
+        contributions, base, resolved = pending
+        if (contributions.dtype != torch.float32 or not contributions.is_contiguous() or
+                contributions.numel() != tokens * PENDING_HEADS * dim or
+                contributions.device != first.device):
+            raise RuntimeError("contributions must be contiguous fp32 [tokens, 8, dim]")
+        for t_ in (base, resolved):
+            if t_ is not None and (t_.shape != first.shape or t_.dtype != first.dtype or
+                                   not t_.is_contiguous() or t_.device != first.device):
+                raise RuntimeError("base and resolved must be contiguous rows like the sources")
+        _abi.check(lib.parrot_depth_mix_route_pending_bf16(
+            *mix_args[:9], mix_args[10], ptr(router_w), ptr(logit_bias), cfg.n_experts,
+            ptr(weights), ptr(indices), ptr(contributions), PENDING_HEADS, ptr(base),
+            ptr(resolved), _stream(first.device)), "parrot_depth_mix_route_pending_bf16")
     del flat
     return out, RouteResult(None, weights, indices, None)
 
@@ -1312,11 +1370,17 @@ def depth_mix_norm(module, sources: list[Tensor], output_norm) -> Tensor:
 
 
 def depth_mix_norm_route(module, sources: list[Tensor], output_norm, moe: "MoE",
-                         logit_bias: Tensor | None = None) -> tuple[Tensor, RouteResult]:
+                         logit_bias: Tensor | None = None,
+                         pending: tuple | None = None) -> tuple[Tensor, RouteResult]:
     """``depth_mix_norm`` of a MoE layer's input plus that layer's router
     top-2 on the result, in one kernel: at every token count the weights
     and indices equal ``route(moe, result)``'s bit for bit (no grouping, no
-    router stats)."""
+    router stats).  ``pending`` = (contributions fp32 [tokens, 8, dim], base
+    or None, resolved): the last source is the deferred attention output
+    bf16(base + bf16(sum of the contributions over heads)), made in the
+    kernel and written to ``resolved`` (``sources[-1]`` only holds its
+    place)."""
     if moe.cfg.top_k != 2 or moe.cfg.n_experts > MAX_EXPERTS:
         raise RuntimeError(f"HIP routing supports top-2 of at most {MAX_EXPERTS} experts")
-    return _depth(module, sources, output_norm, router=moe, logit_bias=logit_bias)
+    return _depth(module, sources, output_norm, router=moe, logit_bias=logit_bias,
+                  pending=pending)

@@ -126,7 +126,8 @@ static int depth_mix_entry(const void* const* sources, int32_t n_sources, const 
                            const void* score_norm_weight, float score_eps,
                            const void* out_norm_weight, float out_eps, int64_t tokens,
                            int32_t dim, void* out_mix, void* out_norm,
-                           const parrot::RouteOut* route, void* stream) {
+                           const parrot::RouteOut* route, void* stream,
+                           const parrot::PendingSum* pend = nullptr) {
   if (!sources || !query || !score_norm_weight) return PARROT_ERR_NULL_POINTER;
   if (!out_mix && !out_norm) return PARROT_ERR_NULL_POINTER;
   if (out_norm && !out_norm_weight) return PARROT_ERR_NULL_POINTER;
@@ -150,7 +151,7 @@ static int depth_mix_entry(const void* const* sources, int32_t n_sources, const 
       static_cast<const uint16_t*>(score_norm_weight), score_eps,
       static_cast<const uint16_t*>(out_norm_weight), out_eps, tokens, dim,
       static_cast<uint16_t*>(out_mix), static_cast<uint16_t*>(out_norm), nullptr, route,
-      as_stream(stream)));
+      as_stream(stream), pend));
 }
 
 int parrot_depth_mix_bf16(const void* const* sources, int32_t n_sources, const void* query,
@@ -204,6 +205,29 @@ int parrot_depth_mix_route_bf16(const void* const* sources, int32_t n_sources,
   return depth_mix_entry(sources, n_sources, query, score_norm_weight, score_eps,
                          out_norm_weight, out_eps, tokens, dim, out_mix, out_norm, &route,
                          stream);
+}
+
+int parrot_depth_mix_route_pending_bf16(
+    const void* const* sources, int32_t n_sources, const void* query,
+    const void* score_norm_weight, float score_eps, const void* out_norm_weight, float out_eps,
+    int64_t tokens, int32_t dim, void* out_norm, const void* router_weight,
+    const float* logit_bias, int32_t experts, float* out_weights, int64_t* out_indices,
+    const float* contributions, int32_t heads, const void* base, void* resolved, void* stream) {
+  if (!out_norm || !router_weight || !out_weights || !out_indices || !contributions || !resolved)
+    return PARROT_ERR_NULL_POINTER;
+  if (experts < 2 || experts > kMaxExperts) return PARROT_ERR_UNSUPPORTED;
+  if (dim % 32) return PARROT_ERR_UNSUPPORTED;
+  if (heads != parrot::kPendingHeads || n_sources < 2) return PARROT_ERR_UNSUPPORTED;
+  if (!aligned16(router_weight) || !aligned16(contributions)) return PARROT_ERR_ALIGNMENT;
+  if ((reinterpret_cast<uintptr_t>(base) | reinterpret_cast<uintptr_t>(resolved)) & 7u)
+    return PARROT_ERR_ALIGNMENT;
+  const parrot::RouteOut route{static_cast<const uint16_t*>(router_weight), logit_bias, experts,
+                               out_weights, out_indices};
+  const parrot::PendingSum pend{contributions, static_cast<const uint16_t*>(base),
+                                static_cast<uint16_t*>(resolved)};
+  return depth_mix_entry(sources, n_sources, query, score_norm_weight, score_eps,
+                         out_norm_weight, out_eps, tokens, dim, nullptr, out_norm, &route, stream,
+                         &pend);
 }
 
 int parrot_rope_qkv_bf16(const void* qkv, const float* cos_table, const float* sin_table,
@@ -1028,6 +1052,36 @@ int parrot_causal_attention_frag_bf16(const void* q, const int64_t* q_strides, c
       static_cast<const uint16_t*>(v_frag), q_strides, nullptr, nullptr,
       static_cast<int>(batch), seq, heads, kv_heads, head_dim, window, scale,
       static_cast<uint16_t*>(out), as_stream(stream)));
+}
+
+int parrot_causal_attention_frag_out_bf16(const void* q, const int64_t* q_strides,
+                                          const void* k_frag, const void* v_frag, int64_t batch,
+                                          int32_t seq, int32_t heads, int32_t kv_heads,
+                                          int32_t head_dim, int32_t window, float scale,
+                                          const void* out_weight_packed, int32_t dim,
+                                          float* contributions, void* stream) {
+  if (!q || !q_strides || !k_frag || !v_frag || !out_weight_packed || !contributions)
+    return PARROT_ERR_NULL_POINTER;
+  if (batch < 0 || seq < 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 || window <= 0 ||
+      dim <= 0)
+    return PARROT_ERR_BAD_SHAPE;
+  if (heads % kv_heads || !parrot::attention_head_dim_supported(head_dim) ||
+      !parrot::attention_out_width_supported(dim) || batch > 65535 || heads > 65535)
+    return PARROT_ERR_UNSUPPORTED;
+  const int64_t padded = (static_cast<int64_t>(seq) + 31) / 32 * 32;
+  if (padded * head_dim * 2 >= (int64_t{1} << 31) ||
+      static_cast<int64_t>(heads) * head_dim * dim * 2 >= (int64_t{1} << 31))
+    return PARROT_ERR_UNSUPPORTED;
+  for (int i = 0; i < 3; ++i)
+    if (q_strides[i] % 8 || q_strides[i] < 0) return PARROT_ERR_ALIGNMENT;
+  if (!aligned16(q) || !aligned16(k_frag) || !aligned16(v_frag) ||
+      !aligned16(out_weight_packed) || !aligned16(contributions))
+    return PARROT_ERR_ALIGNMENT;
+  return status(parrot::launch_causal_attention_out(
+      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_frag),
+      static_cast<const uint16_t*>(v_frag), q_strides, static_cast<int>(batch), seq, heads,
+      kv_heads, head_dim, window, scale, static_cast<const uint16_t*>(out_weight_packed), dim,
+      contributions, as_stream(stream)));
 }
 
 int parrot_proj_bf16(const void* x, int64_t rows, int32_t k, int64_t lda, const void* w_packed,

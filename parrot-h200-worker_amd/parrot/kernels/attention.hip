@@ -31,6 +31,16 @@
 // blocks w, w + 8, ... (next block's loads in flight during the current
 // one), and the partial states (max, sum, O) are merged in wavefront order
 // through LDS at the end.
+//
+// PROJ: the output projection's share of this head instead of the output
+// itself (the deferred output sum of the reference's decode,
+// parrot/model.py:301-316, applied to whole sequences): the head's rows
+// y_h [16, D] (rounded to bf16 exactly as the output would be) times the
+// head's D columns of the packed output weight, written as fp32
+// contributions [batch, seq, heads, n_out].  Their sum over heads, rounded
+// to bf16, is the output projection of y; the next depth mix sums them.
+// The weight fragments are loaded once the key loop is done (the block
+// registers are free then), while the wavefronts' states are merged.
 #include "common.h"
 
 namespace parrot {
@@ -49,6 +59,11 @@ struct AttnArgs {
   int seq, heads, kv_heads, window;
   float scale_log2;             // scale * log2(e)
   uint16_t* out;                // [batch, seq, heads, head_dim]
+  // PROJ: packed output weight [n_out / 16][heads * head_dim / 32][64][8]
+  // (parrot_proj_bf16's layout) and the fp32 contributions
+  const uint16_t* w_out;
+  int n_out;
+  float* contrib;               // [batch, seq, heads, n_out]
 };
 
 __device__ __forceinline__ bf16x8 load8(const uint16_t* p) {
@@ -70,8 +85,9 @@ __device__ __forceinline__ float query_sum(float v) {
 // every fragment of a key block is one 1 KB contiguous wavefront load (a
 // row-major K or V^T load touches 16 rows per instruction, and at prefill
 // sizes the per-CU memory pipeline, not the MFMAs, then sets the time).
-template <int D, bool FRAG>
+template <int D, bool FRAG, int OT = 0>  // OT > 0: PROJ with OT output tiles per wavefront
 __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnArgs a) {
+  constexpr bool PROJ = OT > 0;
   constexpr int KS = D / 32;   // k steps of the score product
   constexpr int NT = D / 16;   // output dim tiles
   __shared__ float m_s[kAttnWaves][kAttnRows];
@@ -85,6 +101,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
                "s"(a.ks[0]), "s"(a.ks[1]), "s"(a.ks[2]), "s"(a.vs[0]), "s"(a.vs[1]),
                "s"(a.vs[2]), "s"(a.seq), "s"(a.heads), "s"(a.kv_heads), "s"(a.window),
                "s"(a.scale_log2), "s"(a.out));
+  if constexpr (PROJ) asm volatile("" ::"s"(a.w_out), "s"(a.n_out), "s"(a.contrib));
   __builtin_amdgcn_sched_barrier(0);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -268,6 +285,23 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
   }
   l = query_sum(l);
 
+  // PROJ: this wavefront's output-weight fragments (tiles wave, wave + 8,
+  // ... of the n_out columns; k steps h KS .. h KS + KS - 1 of the packed
+  // weight), in flight during the merge.
+  bf16x8 wq[PROJ ? OT : 1][KS];
+  if constexpr (PROJ) {
+    const int ksw = a.heads * D / 32;  // k steps of the packed weight
+    const __amdgpu_buffer_rsrc_t w_rsrc =
+        make_rsrc(a.w_out, static_cast<uint32_t>(a.n_out) * static_cast<uint32_t>(ksw) * 64u);
+#pragma unroll
+    for (int j = 0; j < OT; ++j)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const uint32_t frag = static_cast<uint32_t>((wave + 8 * j) * ksw + h * KS + s);
+        wq[j][s] = __builtin_bit_cast(bf16x8, buffer_load16(w_rsrc, frag * 1024u + lane * 16u, 0));
+      }
+  }
+
   // Merge the wavefronts' states in wavefront order: one scale factor
   // exp2(m_w - max_w m_w) / sum_w (l_w ...) per (wavefront, query), then
   // each output element is a D-independent weighted sum over wavefronts.
@@ -297,14 +331,46 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
     for (int w = 0; w < kAttnWaves; ++w) f_s[w][qq] = f[w] * inv;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < kAttnRows * D; i += 64 * kAttnWaves) {
-    const int qq = i / D, d = i - qq * D;
-    const int row = q0 + qq;
-    if (row >= T) continue;
-    float ot = 0.0f;
+  if constexpr (!PROJ) {
+    for (int i = threadIdx.x; i < kAttnRows * D; i += 64 * kAttnWaves) {
+      const int qq = i / D, d = i - qq * D;
+      const int row = q0 + qq;
+      if (row >= T) continue;
+      float ot = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) ot += o_s[w][d][qq] * f_s[w][qq];
-    a.out[((static_cast<int64_t>(b) * T + row) * a.heads + h) * D + d] = f32_to_bf16(ot);
+      for (int w = 0; w < kAttnWaves; ++w) ot += o_s[w][d][qq] * f_s[w][qq];
+      a.out[((static_cast<int64_t>(b) * T + row) * a.heads + h) * D + d] = f32_to_bf16(ot);
+    }
+  } else {
+    // y_h in LDS (bf16, rows padded to D + 8: the 16 rows of a fragment
+    // read land in distinct banks), rows past the sequence zero.
+    __shared__ __attribute__((aligned(16))) uint16_t y_s[kAttnRows][D + 8];
+    for (int i = threadIdx.x; i < kAttnRows * D; i += 64 * kAttnWaves) {
+      const int qq = i / D, d = i - qq * D;
+      float ot = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w) ot += o_s[w][d][qq] * f_s[w][qq];
+      y_s[qq][d] = q0 + qq < T ? f32_to_bf16(ot) : static_cast<uint16_t>(0);
+    }
+    __syncthreads();
+    // contributions[row, n] = sum_d y_h[row, d] W[n, h D + d]: lane l of the
+    // C fragment holds column 16 tile + l % 16, rows 4 (l / 16) + r.
+    bf16x8 af[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      af[s] = *reinterpret_cast<const bf16x8*>(&y_s[c][32 * s + 8 * g]);
+    float* crow = a.contrib + ((static_cast<int64_t>(b) * T + q0 + 4 * g) * a.heads + h) * a.n_out;
+    const int64_t row_stride = static_cast<int64_t>(a.heads) * a.n_out;
+#pragma unroll
+    for (int j = 0; j < OT; ++j) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[s], wq[j][s], acc, 0, 0, 0);
+      const int col = 16 * (wave + 8 * j) + c;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (q0 + 4 * g + r < T) crow[r * row_stride + col] = acc[r];
+    }
   }
 }
 
@@ -312,6 +378,49 @@ __global__ __launch_bounds__(64 * kAttnWaves) void causal_attention_kernel(AttnA
 
 bool attention_head_dim_supported(int head_dim) {
   return head_dim == 64 || head_dim == 96 || head_dim == 128;
+}
+
+hipError_t launch_causal_attention_out(const uint16_t* q, const uint16_t* k_frag,
+                                       const uint16_t* v_frag, const int64_t* q_strides, int batch,
+                                       int seq, int heads, int kv_heads, int head_dim, int window,
+                                       float scale, const uint16_t* w_out, int n_out,
+                                       float* contrib, hipStream_t s) {
+  if (batch == 0 || seq == 0) return hipSuccess;
+  AttnArgs a{};
+  a.q = q;
+  a.k = k_frag;
+  a.vt = v_frag;
+  for (int i = 0; i < 3; ++i) a.qs[i] = q_strides[i];
+  a.seq = seq;
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.window = window;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.w_out = w_out;
+  a.n_out = n_out;
+  a.contrib = contrib;
+  const dim3 grid((seq + kAttnRows - 1) / kAttnRows, heads, batch);
+#define PARROT_ATTN_OUT(D, OT) causal_attention_kernel<D, true, OT><<<grid, 64 * kAttnWaves, 0, s>>>(a)
+#define PARROT_ATTN_OUT_D(D)                      \
+  switch (n_out) {                                \
+    case 512: PARROT_ATTN_OUT(D, 4); break;       \
+    case 768: PARROT_ATTN_OUT(D, 6); break;       \
+    case 1024: PARROT_ATTN_OUT(D, 8); break;      \
+    default: return hipErrorInvalidValue;         \
+  }
+  switch (head_dim) {
+    case 64: PARROT_ATTN_OUT_D(64); break;
+    case 96: PARROT_ATTN_OUT_D(96); break;
+    case 128: PARROT_ATTN_OUT_D(128); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef PARROT_ATTN_OUT_D
+#undef PARROT_ATTN_OUT
+  return hipGetLastError();
+}
+
+bool attention_out_width_supported(int n_out) {
+  return n_out == 512 || n_out == 768 || n_out == 1024;
 }
 
 hipError_t launch_causal_attention(const uint16_t* q, const uint16_t* k, const uint16_t* vt,

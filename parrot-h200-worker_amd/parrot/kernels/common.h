@@ -295,6 +295,18 @@ struct CombineSource {
   uint16_t* out;           // [T, dim]
 };
 
+// An attention output whose sum over heads is deferred to the depth mix
+// that reads it (the output projection's per-head contributions of
+// launch_causal_attention_out): the mix's last source is made in the kernel
+// as bf16(base + bf16(sum over the kPendingHeads heads of contrib)), summed
+// in head order, written to `out`.
+constexpr int kPendingHeads = 8;
+struct PendingSum {
+  const float* contrib;    // fp32 [T, kPendingHeads, dim]
+  const uint16_t* base;    // optional [T, dim]
+  uint16_t* out;           // [T, dim]
+};
+
 // Router top-2 computed inside the depth mix whose normalised output is the
 // MoE input (route_kernel's results, bit for bit).
 struct RouteOut {
@@ -321,7 +333,8 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
                             float score_eps, const uint16_t* out_norm_w,
                             float out_eps, int64_t tokens, int dim,
                             uint16_t* out_mix, uint16_t* out_norm, const CombineSource* comb,
-                            const RouteOut* route, hipStream_t s);
+                            const RouteOut* route, hipStream_t s,
+                            const PendingSum* pend = nullptr);
 
 // Routing: router projection (or given fp32 logits) + top-2 + per-block
 // stable ranks.  Writes block-local ranks into `positions` and per-block
@@ -531,6 +544,16 @@ hipError_t launch_causal_attention(const uint16_t* q, const uint16_t* k, const u
                                    const int64_t* vt_strides, int batch, int seq, int heads,
                                    int kv_heads, int head_dim, int window, float scale,
                                    uint16_t* out, hipStream_t s);
+// Fragment-order K and V; instead of the output, each head's share of the
+// output projection: contrib [batch, seq, heads, n_out] fp32 = y_h W_h^T
+// with w_out packed as parrot_proj_bf16's weights (n_out rows, heads *
+// head_dim columns).  n_out from attention_out_width_supported.
+bool attention_out_width_supported(int n_out);  // 512, 768, 1024
+hipError_t launch_causal_attention_out(const uint16_t* q, const uint16_t* k_frag,
+                                       const uint16_t* v_frag, const int64_t* q_strides, int batch,
+                                       int seq, int heads, int kv_heads, int head_dim, int window,
+                                       float scale, const uint16_t* w_out, int n_out,
+                                       float* contrib, hipStream_t s);
 
 hipError_t launch_combine(const uint16_t* y_routed, const uint16_t* y_shared,
                           const uint16_t* addend, int64_t tokens, int dim,

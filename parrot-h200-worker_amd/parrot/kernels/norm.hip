@@ -88,13 +88,17 @@ __global__ __launch_bounds__(64) void rms_norm_kernel(
 constexpr int kRouteChainSlots = 2;
 constexpr int kRouteStepSlots = 6;
 
-template <int ROUTE, int NS>
+// PL > 0 (PL == kPendingHeads): the last source is a pending attention
+// output, bf16(base + bf16(sum over heads of pend.contrib)), made here and
+// written to pend.out (the depth mix of the MoE module that follows the
+// attention).
+template <int ROUTE, int NS, int PL = 0>
 __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     DepthSources srcs, const uint16_t* __restrict__ query,
     const uint16_t* __restrict__ score_w, float score_eps,
     const uint16_t* __restrict__ out_w, float out_eps, int64_t tokens, int dim,
     uint16_t* __restrict__ out_mix, uint16_t* __restrict__ out_norm, CombineSource comb,
-    RouteOut route) {
+    RouteOut route, PendingSum pend) {
   __shared__ DepthMixLds mix_lds;
   // The kernel arguments of the load phase in one batch of scalar loads,
   // before anything uses one: a field first read inside a branch, or after
@@ -110,6 +114,7 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   if constexpr (ROUTE > 0)
     asm volatile("" ::"s"(route.router_w), "s"(route.bias), "s"(route.experts),
                  "s"(route.weights), "s"(route.indices));
+  if constexpr (PL > 0) asm volatile("" ::"s"(pend.contrib), "s"(pend.base), "s"(pend.out));
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int waves = blockDim.x >> 6;
@@ -137,6 +142,15 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     y0 = reinterpret_cast<const uint2*>(comb.y_routed)[(2 * tok) * chunks + ic];
     y1 = reinterpret_cast<const uint2*>(comb.y_routed)[(2 * tok + 1) * chunks + ic];
     if (comb.addend != nullptr) pa = reinterpret_cast<const uint2*>(comb.addend)[base + ic];
+  }
+  // The pending attention output's per-head contributions (4 fp32 each).
+  float4 pc[PL > 0 ? PL : 1];
+  uint2 pbase = make_uint2(0u, 0u);
+  if constexpr (PL > 0) {
+#pragma unroll
+    for (int h = 0; h < PL; ++h)
+      pc[h] = reinterpret_cast<const float4*>(pend.contrib)[(tok * PL + h) * chunks + ic];
+    if (pend.base != nullptr) pbase = reinterpret_cast<const uint2*>(pend.base)[base + ic];
   }
   const uint2 q = reinterpret_cast<const uint2*>(query)[ic];
   const uint2 g = reinterpret_cast<const uint2*>(score_w)[ic];
@@ -182,6 +196,29 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
       o.y = pack_bf16x2(lo_bf16(pa.y) + lo_bf16(o.y), hi_bf16(pa.y) + hi_bf16(o.y));
     }
     if (has) reinterpret_cast<uint2*>(comb.out)[base + i] = o;
+    else o = make_uint2(0u, 0u);
+    v[NS - 1] = o;
+  }
+  if constexpr (PL > 0) {
+    // The attention output: the heads' fp32 sum in head order, rounded to
+    // bf16, then bf16(base + that) -- the output projection's rounding with
+    // its residual addend (parrot_proj_bf16's kStore).
+    float4 t = pc[0];
+#pragma unroll
+    for (int h = 1; h < PL; ++h) {
+      t.x += pc[h].x;
+      t.y += pc[h].y;
+      t.z += pc[h].z;
+      t.w += pc[h].w;
+    }
+    uint2 o;
+    o.x = pack_bf16x2(t.x, t.y);
+    o.y = pack_bf16x2(t.z, t.w);
+    if (pend.base != nullptr) {
+      o.x = pack_bf16x2(lo_bf16(pbase.x) + lo_bf16(o.x), hi_bf16(pbase.x) + hi_bf16(o.x));
+      o.y = pack_bf16x2(lo_bf16(pbase.y) + lo_bf16(o.y), hi_bf16(pbase.y) + hi_bf16(o.y));
+    }
+    if (has) reinterpret_cast<uint2*>(pend.out)[base + i] = o;
     else o = make_uint2(0u, 0u);
     v[NS - 1] = o;
   }
@@ -500,7 +537,7 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
                             float score_eps, const uint16_t* out_norm_w,
                             float out_eps, int64_t tokens, int dim,
                             uint16_t* out_mix, uint16_t* out_norm, const CombineSource* comb,
-                            const RouteOut* route, hipStream_t s) {
+                            const RouteOut* route, hipStream_t s, const PendingSum* pend) {
   if (tokens == 0) return hipSuccess;
   const int waves = (dim + kDepthDimsPerWave - 1) / kDepthDimsPerWave;
   if (waves > kDepthMaxWaves) return hipErrorInvalidValue;
@@ -508,6 +545,24 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
   const RouteOut no_route{};
   const CombineSource c = comb != nullptr ? *comb : none;
   const unsigned grid = static_cast<unsigned>(tokens);
+  if (pend != nullptr) {  // with a route, never with a combine (both make the last source)
+    if (route == nullptr || comb != nullptr || n_sources < 2) return hipErrorInvalidValue;
+    return with_sources(n_sources, [&](auto ns) {
+      if constexpr (decltype(ns)::value >= 2) {
+        if (route->experts > 16)
+          depth_mix_kernel<2, ns, kPendingHeads><<<grid, kWave * waves, 0, s>>>(
+              srcs, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
+              out_norm, none, *route, *pend);
+        else
+          depth_mix_kernel<1, ns, kPendingHeads><<<grid, kWave * waves, 0, s>>>(
+              srcs, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix,
+              out_norm, none, *route, *pend);
+        return hipGetLastError();
+      }
+      return hipErrorInvalidValue;
+    });
+  }
+  const PendingSum no_pend{};
   return with_sources(n_sources, [&](auto ns) {
     if (route == nullptr && comb == nullptr && tokens >= kDepthWaveMinTokens && waves <= 4) {
       const unsigned groups = static_cast<unsigned>(
@@ -528,15 +583,15 @@ hipError_t launch_depth_mix(const DepthSources& srcs, int n_sources,
     if (route != nullptr && route->experts > 16)
       depth_mix_kernel<2, ns><<<grid, kWave * waves, 0, s>>>(
           srcs, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix, out_norm,
-          c, *route);
+          c, *route, no_pend);
     else if (route != nullptr)
       depth_mix_kernel<1, ns><<<grid, kWave * waves, 0, s>>>(
           srcs, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix, out_norm,
-          c, *route);
+          c, *route, no_pend);
     else
       depth_mix_kernel<0, ns><<<grid, kWave * waves, 0, s>>>(
           srcs, query, score_w, score_eps, out_norm_w, out_eps, tokens, dim, out_mix, out_norm,
-          c, no_route);
+          c, no_route, no_pend);
     return hipGetLastError();
   });
 }

@@ -300,6 +300,29 @@ class LocalGQA(nn.Module):
                 hip_moe.proj_supported(c.dim, width + 2 * c.n_kv_heads * c.head_dim) and
                 hip_moe.proj_supported(width, c.dim))
 
+    def defers_heads(self, x: Tensor) -> bool:
+        """True when ``prefill_heads(x)`` applies: the HIP path with the
+        fused projections and a deferrable output projection."""
+        from . import hip_moe
+        c = self.cfg
+        return (self.fuses_addend(x) and
+                hip_moe.attention_heads_out_supported(c.n_heads, c.head_dim, c.dim))
+
+    def prefill_heads(self, x: Tensor) -> Tensor:
+        """The whole-sequence attention output with its projection deferred
+        per head (no KV cache): fp32 contributions [b, t, H, dim] whose sum
+        over heads, rounded to bf16, is ``prefill(x)[0]`` up to fp32
+        summation order (the reference's defer_sum, parrot/model.py:301-316)."""
+        from . import hip_moe
+        c = self.cfg
+        cos, sin = _rope_tables(c, x.new_empty(0, dtype=torch.float32))
+        q, kf, vf, _, _ = hip_moe.proj_rope_qkv_frag(
+            x, self._qkv_fragments(), cos, sin, c.n_heads, c.n_kv_heads, c.head_dim,
+            cache_kv=False)
+        packed = hip_moe.pack_linear(self, "out", (self.out.weight,))
+        return hip_moe.causal_attention_frag_out(q, kf, vf, packed, c.dim, kv_heads=c.n_kv_heads,
+                                                 scale=c.head_dim ** -0.5, window=c.window_size)
+
     def _project_out(self, y: Tensor, addend: Tensor | None) -> Tensor:
         """out(y) (+ addend, rounded as bf16(addend + bf16(out(y))))."""
         if self._hip(y) and self._fused_projections():
@@ -511,6 +534,27 @@ class GlobalMLA(nn.Module):
         return (c.head_dim in hip_moe.ATTENTION_HEAD_DIMS and r % 8 == 0 and
                 hip_moe.proj_supported(c.dim, width + r) and
                 hip_moe.proj_supported(r, 2 * width) and hip_moe.proj_supported(width, c.dim))
+
+    def defers_heads(self, x: Tensor) -> bool:
+        """True when ``prefill_heads(x)`` applies (see LocalGQA)."""
+        from . import hip_moe
+        c = self.cfg
+        return (self.fuses_addend(x) and
+                hip_moe.attention_heads_out_supported(c.n_heads, c.head_dim, c.dim))
+
+    def prefill_heads(self, x: Tensor) -> Tensor:
+        """``prefill(x)[0]`` with the output projection deferred per head:
+        fp32 contributions [b, t, H, dim] (see LocalGQA.prefill_heads)."""
+        from . import hip_moe
+        b, t, _ = x.shape
+        c = self.cfg
+        width = c.n_heads * c.head_dim
+        qkv = hip_moe.proj(x, self._fragments("q", "kv_down"), width + c.kv_latent_dim)
+        q, latent = qkv[..., :width], qkv[..., width:]
+        kf, vf = hip_moe.proj_kv_frag(latent, self._fragments("k_up", "v_up"), width, c.head_dim)
+        q = q.view(b, t, c.n_heads, c.head_dim).transpose(1, 2)
+        return hip_moe.causal_attention_frag_out(q, kf, vf, self._fragments("out"), c.dim,
+                                                 kv_heads=c.n_heads, scale=c.head_dim ** -0.5)
 
     def _fragments(self, *names: str) -> Tensor:
         """The named linears' weights, row-concatenated and packed."""
@@ -906,10 +950,25 @@ class Parrot(nn.Module):
         if (stream is not None and stream.partial is not None and
                 not self.config.collect_router_stats):
             sources = stream.sources()
-            if block.moe.routes_in_depth_mix(sources[0]):
+            first = sources[0]
+            pending = stream.partial if isinstance(stream.partial, PendingResidual) else None
+            if block.moe.routes_in_depth_mix(first):
                 from . import hip_moe
-                return hip_moe.depth_mix_norm_route(self.depth_mix[index], sources,
-                                                    block.moe_norm, block.moe)
+                if pending is None:
+                    return hip_moe.depth_mix_norm_route(self.depth_mix[index], sources,
+                                                        block.moe_norm, block.moe)
+                # The deferred attention output is summed and written inside
+                # the mix; it is then the open partial sum the MoE closes.
+                resolved = torch.empty_like(first)
+                placeholder = pending.base if pending.base is not None else first
+                contributions = pending.contributions.view(-1, *pending.contributions.shape[-2:])
+                h, routed = hip_moe.depth_mix_norm_route(
+                    self.depth_mix[index], sources[:-1] + [placeholder], block.moe_norm,
+                    block.moe, pending=(contributions, pending.base, resolved))
+                stream.partial = resolved
+                return h, routed
+            if pending is not None:  # _defers_attention_heads checked the same predicate
+                raise RuntimeError("a deferred attention output needs the fused MoE input mix")
         return self._mixed_input(stream, x, index, block.moe_norm), None
 
     def _fuses_decode_moe(self, block: Block, first: Tensor) -> bool:
@@ -985,6 +1044,19 @@ class Parrot(nn.Module):
         stream.close(result)
         return mixed
 
+    def _defers_attention_heads(self, block: Block, h: Tensor, stream: _AttnRes | None,
+                                index: int) -> bool:
+        """Whether attention module ``index`` of a whole-sequence forward
+        leaves its output projection's sum over heads to the MoE's input mix
+        (hip_moe.depth_mix_norm_route with ``pending``): that mix must be the
+        fused route mix, and the module must not close a depth block (its
+        output is then read by that mix alone before the MoE adds to it)."""
+        cfg = self.config
+        return (stream is not None and not cfg.collect_router_stats and
+                (index + 1) % cfg.depth_block_size != 0 and
+                block.attention.defers_heads(h) and
+                block.moe.routes_in_depth_mix(stream.sources()[0]))
+
     @staticmethod
     def _fuse_attention_addend(block: Block, h: Tensor, stream: _AttnRes | None) -> bool:
         """Fold ``partial + delta`` into the attention output projection (HIP only)."""
@@ -1033,7 +1105,10 @@ class Parrot(nn.Module):
             h = pending if pending is not None else \
                 self._mixed_input(stream, x, index, block.attention_norm)
             pending = None
-            if not remat and self._fuse_attention_addend(block, h, stream):
+            if not remat and self._defers_attention_heads(block, h, stream, index):
+                # the MoE's input mix sums the heads (and adds the partial sum)
+                stream.close(PendingResidual(stream.partial, block.attention.prefill_heads(h)))
+            elif not remat and self._fuse_attention_addend(block, h, stream):
                 stream.close(block.attention(h, addend=stream.partial))
             else:
                 delta = (checkpoint(block.attention, h, use_reentrant=False) if remat

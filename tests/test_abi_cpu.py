@@ -127,6 +127,26 @@ def test_argument_validation_without_gpu(lib):
                                            1e-6, fake, fake, null, 0, null) == -2
     assert lib.parrot_embed_depth_mix_bf16(fake, 4, fake + 2, 100, 64, fake, fake, 1e-6, fake,
                                            1e-6, fake, fake, null, 0, null) == -5
+    # attention with the output projection deferred per head: widths, shapes
+    ost = (ctypes.c_int64 * 3)(8 * 512 * 96, 512 * 96, 96)
+    attn_out = lambda **kw: lib.parrot_causal_attention_frag_out_bf16(*[kw.get(k, v) for k, v in (
+        ("q", fake), ("st", ctypes.cast(ost, ctypes.c_void_p)), ("kf", fake), ("vf", fake),
+        ("b", 1), ("t", 512), ("h", 8), ("hk", 2), ("d", 96), ("win", 2048), ("sc", 0.1),
+        ("w", fake), ("dim", 768), ("out", fake), ("stream", null))])
+    assert attn_out(w=null) == -1 and attn_out(out=null) == -1
+    assert attn_out(dim=0) == -2 and attn_out(win=0) == -2
+    assert attn_out(dim=640) == -3 and attn_out(d=80) == -3 and attn_out(h=6, hk=4) == -3
+    assert attn_out(w=fake + 8) == -5 and attn_out(out=fake + 4) == -5
+    # the MoE input mix with a pending attention output: 8 heads, 2+ sources
+    srcs2 = (ctypes.c_void_p * 9)(*([fake] * 9))
+    pend = lambda **kw: lib.parrot_depth_mix_route_pending_bf16(*[kw.get(k, v) for k, v in (
+        ("src", ctypes.cast(srcs2, ctypes.c_void_p)), ("n", 3), ("q", fake), ("sw", fake),
+        ("se", 1e-6), ("nw", fake), ("ne", 1e-6), ("tokens", 4), ("dim", 768), ("out", fake),
+        ("rw", fake), ("bias", null), ("e", 16), ("wts", fake), ("idx", fake), ("c", fake),
+        ("heads", 8), ("base", null), ("res", fake), ("stream", null))])
+    assert pend(c=null) == -1 and pend(res=null) == -1 and pend(out=null) == -1
+    assert pend(heads=4) == -3 and pend(n=1) == -3 and pend(e=33) == -3 and pend(dim=776) == -3
+    assert pend(c=fake + 8) == -5 and pend(res=fake + 2) == -5
     ws = lib.parrot_route_workspace_bytes(64, 8)
     args = [fake] * 9  # out_logits .. out_overflow
     # experts outside 2..32

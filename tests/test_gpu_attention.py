@@ -108,3 +108,53 @@ def test_causal_attention_fragments(b, H, Hk, t, d, window):
         err = (frag.float().cpu() - ref).abs()
         _say(f"  max-abs {err.max():.3e} mean-abs {err.mean():.3e}")
         assert err.max() <= 1e-2 and err.mean() <= 1e-3
+
+
+@pytest.mark.parametrize("b,H,Hk,t,d,dim,window", [
+    (1, 8, 2, 512, 96, 768, 2048),   # local layer of the bs1x512 forward
+    (1, 8, 8, 512, 96, 768, 4096),   # MLA layer (one kv head per head)
+    (2, 8, 2, 77, 64, 512, 40),      # ragged rows, band narrower than the sequence
+    (1, 8, 4, 33, 128, 1024, 33),
+    (3, 8, 2, 1, 96, 768, 2048),
+])
+def test_causal_attention_out_heads(b, H, Hk, t, d, dim, window):
+    """The attention kernel with the output projection deferred per head:
+    contributions[.., h, :] equal float64 products of the attention output
+    (the same kernel's bf16 y) with the head's columns of the output weight
+    within fp32 accumulation error; bf16 of their sum is the projection."""
+    from parrot import hip_moe
+    _say(f"attention out heads b={b} H={H} Hk={Hk} t={t} d={d} dim={dim} window={window}")
+    g = torch.Generator().manual_seed(t * 3 + d + dim)
+    q = torch.randn(b, H, t, d, generator=g).bfloat16()
+    k = torch.randn(b, Hk, t, d, generator=g).bfloat16()
+    v = torch.randn(b, Hk, t, d, generator=g).bfloat16()
+    w = (torch.randn(dim, H * d, generator=g) * 0.02).bfloat16()
+    kf, vf = hip_moe.pack_kv_fragments(_padded_nan(k, t).cuda(), _padded_nan(v, t).cuda())
+    holder = torch.nn.Module()
+    holder.out = torch.nn.Linear(H * d, dim, bias=False).cuda().bfloat16()
+    with torch.no_grad():
+        holder.out.weight.copy_(w)
+        packed = hip_moe.pack_linear(holder, "out", (holder.out.weight,))
+        y = hip_moe.causal_attention_frag(q.cuda(), kf, vf, kv_heads=Hk, scale=d ** -0.5,
+                                          window=window)
+        got = hip_moe.causal_attention_frag_out(q.cuda(), kf, vf, packed, dim, kv_heads=Hk,
+                                                scale=d ** -0.5, window=window)
+        proj = hip_moe.proj(y, packed, dim)
+    assert got.shape == (b, t, H, dim) and got.dtype == torch.float32
+    yh = y.double().cpu().view(b, t, H, d)
+    wh = w.double().view(dim, H, d)
+    exact = torch.einsum("bthd,nhd->bthn", yh, wh)
+    scale = torch.einsum("bthd,nhd->bthn", yh.abs(), wh.abs())
+    err = (got.double().cpu() - exact).abs()
+    _say(f"  max err / scale {float((err / scale.clamp_min(1e-30)).max()):.3e}")
+    assert bool((err <= 2e-6 * scale + 1e-30).all())
+    # bf16(sum over heads) against the one-GEMM projection: the same value
+    # up to fp32 reassociation, which moves a rounding boundary now and then
+    # (one bf16 ulp of the result, or more where the heads cancel: then by
+    # at most fp32 error of the terms' scale)
+    summed = got.sum(2).bfloat16().cpu().double()
+    ref = proj.cpu().double()
+    diff = (summed - ref).abs()
+    ulp = torch.maximum(summed.abs(), ref.abs()) * 2 ** -7
+    assert bool((diff <= ulp + 1e-5 * scale.sum(2)).all())
+    assert float((summed != ref).double().mean()) < 0.02

@@ -439,3 +439,40 @@ def test_experts_group_from_route_blocks(tokens, experts, skewed):
     assert torch.equal(counts.cpu(), g.counts.cpu())
     assert torch.equal(offsets.cpu(), g.offsets.cpu())
     assert torch.equal(sorted_ids.cpu(), _sorted_from_grouping(g, experts))
+
+
+@pytest.mark.parametrize("tokens,experts,older,with_base", [
+    (512, 16, 2, True), (512, 16, 1, False), (17, 32, 8, True), (1000, 16, 4, True)])
+def test_depth_mix_route_pending(tokens, experts, older, with_base):
+    """The MoE input mix with a deferred attention output as its last
+    source: `resolved` is bf16(base + bf16(sum of the 8 heads' fp32
+    contributions in head order)) bit for bit (restated on the host), and
+    the normalised rows, weights and indices equal depth_mix_norm_route's on
+    the explicit sources older + [resolved]."""
+    from parrot import hip_moe
+    _say(f"depth mix + route, pending T={tokens} E={experts} older={older} base={with_base}")
+    module = moe_module(experts, seed=6)
+    depth = _Depth(768).cuda().bfloat16()
+    norm = _Norm(768).cuda().bfloat16()
+    src = [inputs(tokens, seed=40 + s) * (1 + s) for s in range(older)]
+    g = torch.Generator().manual_seed(tokens + older)
+    contrib = (torch.randn(tokens, 8, 768, generator=g) * 0.05).float()
+    base = inputs(tokens, seed=60) if with_base else None
+    # host restatement: fp32 sum in head order, bf16, then bf16(base + that)
+    acc = contrib[:, 0].clone()
+    for h in range(1, 8):
+        acc = acc + contrib[:, h]
+    want = acc.bfloat16()
+    if base is not None:
+        want = (base.cpu().float() + want.float()).bfloat16()
+    with torch.no_grad():
+        resolved = torch.empty_like(src[0])
+        placeholder = base if base is not None else src[0]
+        normed, top2 = hip_moe.depth_mix_norm_route(
+            depth, src + [placeholder], norm, module,
+            pending=(contrib.cuda(), base, resolved))
+        ref, ref_top2 = hip_moe.depth_mix_norm_route(depth, src + [want.cuda()], norm, module)
+    assert torch.equal(resolved.cpu(), want)
+    assert torch.equal(normed, ref)
+    assert torch.equal(top2.indices, ref_top2.indices)
+    assert torch.equal(top2.weights, ref_top2.weights)
