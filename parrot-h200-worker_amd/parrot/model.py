@@ -308,20 +308,25 @@ class LocalGQA(nn.Module):
         return (self.fuses_addend(x) and
                 hip_moe.attention_heads_out_supported(c.n_heads, c.head_dim, c.dim))
 
-    def prefill_heads(self, x: Tensor) -> Tensor:
+    def prefill_heads(self, x: Tensor,
+                      need_kv: bool = False) -> tuple[Tensor, Tensor | None, Tensor | None]:
         """The whole-sequence attention output with its projection deferred
-        per head (no KV cache): fp32 contributions [b, t, H, dim] whose sum
-        over heads, rounded to bf16, is ``prefill(x)[0]`` up to fp32
-        summation order (the reference's defer_sum, parrot/model.py:301-316)."""
+        per head: (fp32 contributions [b, t, H, dim], keys, values), the
+        contributions' sum over heads, rounded to bf16, being ``prefill(x)[0]``
+        up to fp32 summation order (the reference's defer_sum,
+        parrot/model.py:301-316); keys and values as ``prefill`` returns them
+        when ``need_kv`` (a KV cache is being filled), else None."""
         from . import hip_moe
         c = self.cfg
         cos, sin = _rope_tables(c, x.new_empty(0, dtype=torch.float32))
-        q, kf, vf, _, _ = hip_moe.proj_rope_qkv_frag(
+        q, kf, vf, k, v = hip_moe.proj_rope_qkv_frag(
             x, self._qkv_fragments(), cos, sin, c.n_heads, c.n_kv_heads, c.head_dim,
-            cache_kv=False)
+            cache_kv=need_kv)
         packed = hip_moe.pack_linear(self, "out", (self.out.weight,))
-        return hip_moe.causal_attention_frag_out(q, kf, vf, packed, c.dim, kv_heads=c.n_kv_heads,
-                                                 scale=c.head_dim ** -0.5, window=c.window_size)
+        contributions = hip_moe.causal_attention_frag_out(
+            q, kf, vf, packed, c.dim, kv_heads=c.n_kv_heads, scale=c.head_dim ** -0.5,
+            window=c.window_size)
+        return contributions, k, v
 
     def _project_out(self, y: Tensor, addend: Tensor | None) -> Tensor:
         """out(y) (+ addend, rounded as bf16(addend + bf16(out(y))))."""
@@ -542,9 +547,9 @@ class GlobalMLA(nn.Module):
         return (self.fuses_addend(x) and
                 hip_moe.attention_heads_out_supported(c.n_heads, c.head_dim, c.dim))
 
-    def prefill_heads(self, x: Tensor) -> Tensor:
-        """``prefill(x)[0]`` with the output projection deferred per head:
-        fp32 contributions [b, t, H, dim] (see LocalGQA.prefill_heads)."""
+    def prefill_heads(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        """``prefill(x)`` with the output projection deferred per head: (fp32
+        contributions [b, t, H, dim], latent) (see LocalGQA.prefill_heads)."""
         from . import hip_moe
         b, t, _ = x.shape
         c = self.cfg
@@ -554,7 +559,8 @@ class GlobalMLA(nn.Module):
         kf, vf = hip_moe.proj_kv_frag(latent, self._fragments("k_up", "v_up"), width, c.head_dim)
         q = q.view(b, t, c.n_heads, c.head_dim).transpose(1, 2)
         return hip_moe.causal_attention_frag_out(q, kf, vf, self._fragments("out"), c.dim,
-                                                 kv_heads=c.n_heads, scale=c.head_dim ** -0.5)
+                                                 kv_heads=c.n_heads,
+                                                 scale=c.head_dim ** -0.5), latent
 
     def _fragments(self, *names: str) -> Tensor:
         """The named linears' weights, row-concatenated and packed."""
@@ -1107,7 +1113,7 @@ class Parrot(nn.Module):
             pending = None
             if not remat and self._defers_attention_heads(block, h, stream, index):
                 # the MoE's input mix sums the heads (and adds the partial sum)
-                stream.close(PendingResidual(stream.partial, block.attention.prefill_heads(h)))
+                stream.close(PendingResidual(stream.partial, block.attention.prefill_heads(h)[0]))
             elif not remat and self._fuse_attention_addend(block, h, stream):
                 stream.close(block.attention(h, addend=stream.partial))
             else:
@@ -1191,20 +1197,31 @@ class Parrot(nn.Module):
             h = pending if pending is not None else \
                 self._mixed_input(stream, x, index, block.attention_norm)
             pending = None
-            fuse = self._fuse_attention_addend(block, h, stream)
+            defer = self._defers_attention_heads(block, h, stream, index)
+            fuse = not defer and self._fuse_attention_addend(block, h, stream)
             addend = stream.partial if fuse else None
-            if isinstance(block.attention, LocalGQA):
+            local = isinstance(block.attention, LocalGQA)
+            if defer:
+                # as in forward: the MoE's input mix sums the heads
+                if local:
+                    delta, key, value = block.attention.prefill_heads(h, need_kv=True)
+                else:
+                    delta, latent = block.attention.prefill_heads(h)
+                delta = PendingResidual(stream.partial, delta)
+            elif local:
                 delta, key, value = block.attention.prefill(h, addend)
+            else:
+                delta, latent = block.attention.prefill(h, addend)
+            if local:
                 shape = (b, cfg.n_kv_heads, cfg.max_seq_len, cfg.head_dim)
                 cache = LocalKVCache(key.new_empty(shape), value.new_empty(shape))
                 cache.key[:, :, :t].copy_(key)
                 cache.value[:, :, :t].copy_(value)
             else:
-                delta, latent = block.attention.prefill(h, addend)
                 cache = MLALatentCache(latent.new_empty((b, cfg.max_seq_len, cfg.kv_latent_dim)))
                 cache.latent[:, :t].copy_(latent)
             caches.append(cache)
-            if fuse:
+            if fuse or defer:
                 stream.close(delta)
             elif stream is None:
                 x = x + delta

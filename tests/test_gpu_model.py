@@ -385,9 +385,20 @@ def test_deferred_attention_sums_match_projection_launches(monkeypatch):
     with torch.no_grad():
         monkeypatch.setattr(Parrot, "_defers_attention_heads", spy)
         deferred = model(ids).logits.float()
-        assert calls and all(calls)  # every attention module deferred
+        assert len(calls) == 16 and all(calls)  # every attention module deferred
+        prefill_deferred, state = model.prefill(ids)
+        assert len(calls) == 32 and all(calls)  # prefill too, filling the caches
+        token_deferred = model.decode_next(prefill_deferred.argmax(-1), state)[0]
         monkeypatch.setattr(Parrot, "_defers_attention_heads", lambda self, *a: False)
         launched = model(ids).logits.float()
+        prefill_launched, state = model.prefill(ids)
+        token_launched = model.decode_next(prefill_launched.argmax(-1), state)[0]
+    # the prefill's logits are the forward's last position (the vocabulary
+    # head runs on one row there: another library kernel, fp32 sums in
+    # another order)
+    assert float((prefill_deferred.float() - deferred[:, -1:]).abs().max()) <= 1e-4
+    assert float((prefill_launched.float() - launched[:, -1:]).abs().max()) <= 1e-4
+    say(f"  next tokens deferred {token_deferred.tolist()} launched {token_launched.tolist()}")
     diff = (deferred - launched).abs()
     agree = float((deferred.argmax(-1) == launched.argmax(-1)).float().mean())
     say(f"  logits max-abs {float(diff.max()):.3e} mean-abs {float(diff.mean()):.3e} "
