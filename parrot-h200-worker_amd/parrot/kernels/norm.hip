@@ -130,7 +130,7 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
   // zero it afterwards, and only uniform conditions (combine, addend, output
   // norm) guard a load: a load behind a branch on a kernel argument, or
   // inside a per-lane branch, costs a serial round trip each.
-  const bool combine = comb.y_shared != nullptr;
+  const bool combine = PL == 0 && comb.y_shared != nullptr;  // never with a pending source
   const int ic = has ? i : 0;
   uint2 v[kMaxDepthSources];
 #pragma unroll
@@ -150,12 +150,15 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
 #pragma unroll
     for (int h = 0; h < PL; ++h)
       pc[h] = reinterpret_cast<const float4*>(pend.contrib)[(tok * PL + h) * chunks + ic];
-    if (pend.base != nullptr) pbase = reinterpret_cast<const uint2*>(pend.base)[base + ic];
+    // (the query row stands in for a missing base: an unconditional load
+    // keeps the waits below exact; a load behind a branch makes the first
+    // use of any earlier load wait for every load, vmcnt(0))
+    pbase = (pend.base != nullptr ? reinterpret_cast<const uint2*>(pend.base) + base
+                                  : reinterpret_cast<const uint2*>(query))[ic];
   }
   const uint2 q = reinterpret_cast<const uint2*>(query)[ic];
   const uint2 g = reinterpret_cast<const uint2*>(score_w)[ic];
-  uint2 g_out = make_uint2(0u, 0u);
-  if (out_norm != nullptr) g_out = reinterpret_cast<const uint2*>(out_w)[ic];
+  const uint2 g_out = reinterpret_cast<const uint2*>(out_norm != nullptr ? out_w : score_w)[ic];
   // Router weights of this wavefront's first chains (ROUTE > 0).
   const int steps = dim / 32;
   const int koff = (lane >> 4) * 8;
@@ -166,15 +169,17 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     for (int h = 0; h < ROUTE; ++h)
       pb[h] = route.router_w +
               static_cast<int64_t>(min(16 * h + (lane & 15), route.experts - 1)) * dim + koff;
+    // Every wavefront loads every slot (chains and steps past the last are
+    // clamped to it and go unused), with no branch, so that the waits for
+    // the loads before these count them exactly.
 #pragma unroll
     for (int j = 0; j < kRouteChainSlots; ++j)
 #pragma unroll
       for (int i = 0; i < kRouteStepSlots; ++i) {
-        const int c = wave + j * waves, st = c + 4 * i;
-        if (c < 4 && st < steps)
+        const int c = min(wave + j * waves, 3), st = min(c + 4 * i, steps - 1);
 #pragma unroll
-          for (int h = 0; h < ROUTE; ++h)
-            rb[j][i][h] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(pb[h] + st * 32));
+        for (int h = 0; h < ROUTE; ++h)
+          rb[j][i][h] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(pb[h] + st * 32));
       }
   }
 
@@ -214,10 +219,12 @@ __global__ __launch_bounds__(64 * kDepthMaxWaves) void depth_mix_kernel(
     uint2 o;
     o.x = pack_bf16x2(t.x, t.y);
     o.y = pack_bf16x2(t.z, t.w);
-    if (pend.base != nullptr) {
-      o.x = pack_bf16x2(lo_bf16(pbase.x) + lo_bf16(o.x), hi_bf16(pbase.x) + hi_bf16(o.x));
-      o.y = pack_bf16x2(lo_bf16(pbase.y) + lo_bf16(o.y), hi_bf16(pbase.y) + hi_bf16(o.y));
-    }
+    // Without a base, -0 is added: the exact identity for every bf16 value
+    // (signed zeros included), so the add sits behind no branch (a branch
+    // would take the base's load with it and wait for every load there).
+    const uint2 bz = pend.base != nullptr ? pbase : make_uint2(0x80008000u, 0x80008000u);
+    o.x = pack_bf16x2(lo_bf16(bz.x) + lo_bf16(o.x), hi_bf16(bz.x) + hi_bf16(o.x));
+    o.y = pack_bf16x2(lo_bf16(bz.y) + lo_bf16(o.y), hi_bf16(bz.y) + hi_bf16(o.y));
     if (has) reinterpret_cast<uint2*>(pend.out)[base + i] = o;
     else o = make_uint2(0u, 0u);
     v[NS - 1] = o;
