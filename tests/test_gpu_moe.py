@@ -457,6 +457,9 @@ def test_depth_mix_route_pending(tokens, experts, older, with_base):
     src = [inputs(tokens, seed=40 + s) * (1 + s) for s in range(older)]
     g = torch.Generator().manual_seed(tokens + older)
     contrib = (torch.randn(tokens, 8, 768, generator=g) * 0.05).float()
+    # head sums of exactly -0 and +0 (a missing base must keep their signs)
+    contrib[0] = -0.0
+    contrib[1, :, :384] = 0.0
     base = inputs(tokens, seed=60) if with_base else None
     # host restatement: fp32 sum in head order, bf16, then bf16(base + that)
     acc = contrib[:, 0].clone()
@@ -472,7 +475,7 @@ def test_depth_mix_route_pending(tokens, experts, older, with_base):
             depth, src + [placeholder], norm, module,
             pending=(contrib.cuda(), base, resolved))
         ref, ref_top2 = hip_moe.depth_mix_norm_route(depth, src + [want.cuda()], norm, module)
-    assert torch.equal(resolved.cpu(), want)
+    assert torch.equal(resolved.cpu().view(torch.int16), want.view(torch.int16))  # bits
     assert torch.equal(normed, ref)
     assert torch.equal(top2.indices, ref_top2.indices)
     assert torch.equal(top2.weights, ref_top2.weights)
