@@ -95,6 +95,12 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   asm volatile("" ::"s"(q), "s"(k_new), "s"(v_new), "s"(k_cache), "s"(v_cache), "s"(position),
                "s"(heads), "s"(kv_heads), "s"(max_pos), "s"(window), "s"(scale));
   if constexpr (Q > 0) asm volatile("" ::"s"(ho.weight), "s"(ho.dim), "s"(ho.contributions));
+  // The device position first, read through the constant address space (it
+  // does not change during the launch) so that it is a scalar load: the
+  // cache rows' addresses wait for it alone, not for the element loads below
+  // (a vector load's wait would cover those too).
+  using const_i32 = const __attribute__((address_space(4))) int32_t;
+  const int pos = *(const_i32*)(reinterpret_cast<uintptr_t>(position));
   __builtin_amdgcn_sched_barrier(0);
   const int h = Q > 0 ? static_cast<int>(blockIdx.x) / Q : static_cast<int>(blockIdx.x);
   const int part_n = Q > 0 ? static_cast<int>(blockIdx.x) % Q : 0;
@@ -124,7 +130,6 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(
   const uint16_t kne = kn[ie], vne = vn[ie];
   const float qv = to_f32(q[(static_cast<int64_t>(b) * heads + h) * D + ie]);
   asm volatile("" ::: "memory");
-  const int pos = *position;
   if (pos < 0 || pos >= max_pos) return;  // uniform: nothing to attend to
   const int lo = max(0, pos - window + 1);
   const int L = pos - lo + 1;

@@ -447,11 +447,16 @@ __global__ __launch_bounds__(256) void decode_down_kernel(
       for (int i = 0; i < 4; ++i) wv[q][i] = wb[min(s0 + 4 * i, ks[q] - 1) * 64];
     }
     asm volatile("" ::: "memory");
+    // The shared expert's products first: its weights were loaded before the
+    // routed ones, so they are computed while those arrive (each sum keeps
+    // its own order).
 #pragma unroll
-    for (int q = 0; q < 3; ++q)
+    for (int qq = 0; qq < 3; ++qq) {
+      const int q = (qq + 2) % 3;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (s0 + 4 * i < ks[q]) acc[q] += dot8(wv[q][i], hv[q][i]);
+    }
   };
   // The first batch straight-line (its loads are clamped, so it is safe for
   // a wavefront past the k range), so that no address computation is
